@@ -1,0 +1,107 @@
+"""Oracle: the GPT language model around the segment-tree attention (CPU, float32 or bf16).
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Restates model.py:12-93 (pre-LN blocks, bias-free
+linears, GELU MLP, learned positions, tied output layer, N(0, 0.02) init with the residual projections
+rescaled) with the attention module of fastseg.py:318-405 (fixed budget) computed by the oracle.
+Parameter names match the reference's state_dict so weights move between this model, the product's
+model and both decoders.
+"""
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .attn_ref import seg_sparse_attend
+
+
+class LayerNorm(nn.Module):
+    def __init__(self, n):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(n))
+
+    def forward(self, x):
+        return F.layer_norm(x, self.weight.shape, self.weight, None, 1e-5)
+
+
+class SegAttentionRef(nn.Module):
+    """c_attn -> heads -> oracle selection + sparse attention -> c_proj (fastseg.py:338-343)."""
+
+    def __init__(self, cfg, mode='faithful'):
+        super().__init__()
+        self.cfg = cfg
+        C = cfg.n_embd
+        self.H = cfg.n_head
+        self.dh = C // cfg.n_head
+        self.mode = mode
+        self.c_attn = nn.Linear(C, 3 * C, bias=False)
+        self.c_proj = nn.Linear(C, C, bias=False)
+        self.aux = {}
+
+    def forward(self, x):
+        b, T, C = x.shape
+        q, k, v = self.c_attn(x).split(C, dim=2)
+        q, k, v = [a.view(b, T, self.H, self.dh).transpose(1, 2) for a in (q, k, v)]
+        out, self.aux, _, _ = seg_sparse_attend(q, k, v, self.cfg, mode=self.mode)
+        return self.c_proj(out.transpose(1, 2).reshape(b, T, C))
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        C = cfg.n_embd
+        self.c_fc = nn.Linear(C, 4 * C, bias=False)
+        self.c_proj = nn.Linear(4 * C, C, bias=False)
+
+    def forward(self, x):
+        return self.c_proj(F.gelu(self.c_fc(x)))
+
+
+class Block(nn.Module):
+    def __init__(self, cfg, mode):
+        super().__init__()
+        self.ln1 = LayerNorm(cfg.n_embd)
+        self.attn = SegAttentionRef(cfg, mode)
+        self.ln2 = LayerNorm(cfg.n_embd)
+        self.mlp = MLP(cfg)
+
+    def forward(self, x):
+        x = x + self.attn(self.ln1(x))
+        return x + self.mlp(self.ln2(x))
+
+
+class GPTRef(nn.Module):
+    """GPT-2 style model (model.py:51-93); forward returns (logits, None, stats)."""
+
+    def __init__(self, cfg, mode='faithful'):
+        super().__init__()
+        self.cfg = cfg
+        self.wte = nn.Embedding(cfg.vocab_size, cfg.n_embd)
+        self.wpe = nn.Embedding(cfg.seq_len, cfg.n_embd)
+        self.blocks = nn.ModuleList([Block(cfg, mode) for _ in range(cfg.n_layer)])
+        self.ln_f = LayerNorm(cfg.n_embd)
+        self.lm_head = nn.Linear(cfg.n_embd, cfg.vocab_size, bias=False)
+        self.lm_head.weight = self.wte.weight
+        self.apply(self._init)
+        for n, p in self.named_parameters():
+            if n.endswith('c_proj.weight'):
+                nn.init.normal_(p, mean=0.0, std=0.02 / math.sqrt(2 * cfg.n_layer))
+
+    @staticmethod
+    def _init(m):
+        if isinstance(m, (nn.Linear, nn.Embedding)):
+            nn.init.normal_(m.weight, mean=0.0, std=0.02)
+            if getattr(m, 'bias', None) is not None:
+                nn.init.zeros_(m.bias)
+
+    def forward(self, idx):
+        b, T = idx.shape
+        x = self.wte(idx) + self.wpe(torch.arange(T))
+        acc = {}
+        for blk in self.blocks:
+            x = blk(x)
+            for name, val in blk.attn.aux.items():
+                acc[name] = acc.get(name, 0.0) + val
+        logits = self.lm_head(self.ln_f(x))
+        n = len(self.blocks)
+        return logits, None, {name: float(val) / n for name, val in acc.items()}
