@@ -1,0 +1,167 @@
+/*
+ * treeattn.h -- C ABI of the MI355X (gfx950) segment-tree sparse attention library (libtreeattn.so).
+ *
+ * The reference (Dex8123/treeattn) has no native code: its hot path is PyTorch ops plus three Triton
+ * kernels reached from Python.  Each entry point below replaces one reference function or op chain,
+ * cited as file:line of the reference.  The Python package treeattn_amd binds these through ctypes and
+ * keeps the reference's Python signatures on top.
+ *
+ * Conventions (all entry points):
+ *   - Device pointers, explicit sizes and element strides, a hipStream_t passed as void*.  Work is
+ *     enqueued on that stream; nothing is synchronised and nothing is allocated.  Scratch memory, where
+ *     needed, is a caller-provided workspace whose size a *_workspace_size() function reports.
+ *   - Tensors of rows are addressed as base + b*sb + h*sh + n*sn with the last (feature) dimension
+ *     contiguous; strides are in elements.
+ *   - Element types: TA_F32, TA_F16, TA_BF16.  Index tensors are int32, -1 meaning "no entry".
+ *   - Return 0 on success, a TA_ERR_* code otherwise; ta_last_error() gives a message (per thread).
+ *   - Node sums ("pyramid") are float32.  Tree level j (j = 0 is the leaf-block level) holds nodes of
+ *     leaf * arity^j positions; node m covers [m*size, (m+1)*size).  Level j is passed as a device base
+ *     pointer plus its batch and head strides; node rows are contiguous with stride D.
+ */
+#ifndef TREEATTN_H_
+#define TREEATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TA_ABI_VERSION 1
+
+enum ta_dtype { TA_F32 = 0, TA_F16 = 1, TA_BF16 = 2 };
+
+enum ta_status {
+  TA_OK = 0,
+  TA_ERR_ARG = 1,       /* bad size, stride, alignment or dtype */
+  TA_ERR_UNSUPPORTED = 2, /* shape outside what the kernels are built for */
+  TA_ERR_LAUNCH = 3,    /* the HIP runtime refused the launch */
+  TA_ERR_WORKSPACE = 4  /* workspace too small */
+};
+
+int ta_abi_version(void);
+const char* ta_last_error(void);
+
+/* 1 when the current HIP device is a gfx950 the library has code for, 0 otherwise. */
+int ta_device_supported(void);
+
+/*
+ * Level-sum pyramid of a key tensor (replaces seg.py:26-41 level_sums, fastseg.py:238-251 level_sums_min
+ * without the gate, and the index-key preparation seg.py:128-130 / fastseg.py:306-308).
+ *
+ * k: (B, H, T, D) of k_dtype.  Index keys are k as float32, with position 0 zeroed when zero_sink is 1
+ * (seg.py:130; level_sums itself sums whatever it is given, seg.py:31-35).  Every node of the
+ * binary levels 1.. is the sum of its two children (children added left + right, in float32), and the
+ * levels listed in lv_* are written: lv_blevel[j] is the binary level (log2 of the node size) of output
+ * level j, strictly increasing.  Only nodes lying completely inside [0, t_end) are written.
+ * ws: float32 workspace of ta_level_sums_workspace_size(...) bytes.
+ */
+int64_t ta_level_sums_workspace_size(int B, int H, int t_end, int D);
+int ta_level_sums(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_t kst,
+                  int B, int H, int t_end, int D, int zero_sink,
+                  int n_levels, float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh,
+                  const int32_t* lv_blevel,
+                  float* ws, int64_t ws_bytes, void* stream);
+
+/*
+ * Beam descent with per-query top-k leaf-block selection (replaces seg.py:44-70 tree_pass and
+ * fastseg.py:254-271 tree_pass_fast, including the per-level gather_dot of fastseg.py:267 and topk).
+ *
+ * q: (B, H, Nq, D) of q_dtype (scored in float32).  tq: query positions, tq[b*tq_sb + n] (tq_sb = 0 to
+ * share one position list across the batch).  The tree spans [0, T) (T a power of two) with leaf blocks
+ * of 2^leaf_log2 keys and 2^arity_log2 children per node; the n_levels pyramid levels are tree levels
+ * 0..n_levels-1 in ta_level_sums layout.
+ * Semantics: at every level, top first, the candidates are the children of the kept nodes plus the
+ * complete left siblings of the node containing t; a node's score is q . sum / size in the canonical
+ * float32 order (per-dimension products without fused multiply-add, 16 groups of D/16 consecutive
+ * dimensions each reduced by the halving tree, then the halving tree over the 16 group sums, times the
+ * exact power of two 1/size); the best wmax by (score desc, node id asc) are kept.
+ * Outputs (B, H, Nq, wl) contiguous: ids (leaf-block ids, best first; -1 past the valid ones), vld (0/1),
+ * sct (scores; -inf past the valid ones).  wl is the reference's leaf beam width for this geometry.
+ * A query whose position lies outside [0, T) selects nothing.
+ */
+int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn,
+                    int B, int H, int Nq, int D,
+                    const int32_t* tq, int64_t tq_sb,
+                    int n_levels, const float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh,
+                    int T, int leaf_log2, int arity_log2, int wmax, int wl,
+                    int32_t* ids, uint8_t* vld, float* sct, void* stream);
+
+/*
+ * Scores of queries against gathered rows (replaces fastseg.py:118-130 gather_dot and its kernel
+ * fastseg.py:34-47).  out[b,h,n,c] = scale * q[b,h,n] . S[b,h,clamp(cand[b,h,n,c], 0, M-1)], float32,
+ * canonical order.  q: (B,H,N,D) q_dtype; S: (B,H,M,D) s_dtype; cand: (B,H,N,C) int32 contiguous;
+ * out: (B,H,N,C) float32 contiguous.
+ */
+int ta_gather_dot(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn,
+                  const void* S, int s_dtype, int64_t ssb, int64_t ssh, int64_t ssn,
+                  const int32_t* cand, int B, int H, int N, int M, int C, int D, float scale,
+                  float* out, void* stream);
+
+/*
+ * Leaf-block gather-dot: the candidates of a query are whole blocks of `block` consecutive rows,
+ * out[b,h,n, c*block + j] = scale * q[b,h,n] . K[b,h, blk[b,h,n,c]*block + j] (fastseg.py:118-130 with
+ * cand = blk*block + arange(block)).  blk: (B,H,N,NB) int32 contiguous, ids in [0, M/block).
+ * Same dtype for q and K; out (B,H,N,NB*block) float32 contiguous.
+ */
+int ta_gather_dot_blocks(const void* q, const void* K, int dtype,
+                         int64_t qsb, int64_t qsh, int64_t qsn, int64_t ksb, int64_t ksh, int64_t ksn,
+                         const int32_t* blk, int B, int H, int N, int M, int NB, int block, int D,
+                         float scale, float* out, void* stream);
+
+/*
+ * Softmax attention of each query over an explicit candidate list (replaces fastseg.py:173-177
+ * sparse_attn forward, its kernel fastseg.py:50-78 and the fallback fastseg.py:134-141).
+ * q, k, v: (B,H,T,D) same dtype; cand: (B,H,T,KC) int32 contiguous, -1 = unused, duplicates counted as
+ * given; positions >= T are treated as unused.  out: (B,H,T,D) contiguous in the input dtype; lse: (B,H,T)
+ * float32 (may be NULL).  Softmax in float32; a row with no valid candidate gives out = 0, lse = -1e30.
+ */
+int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype,
+                       int64_t qsb, int64_t qsh, int64_t qst, int64_t ksb, int64_t ksh, int64_t kst,
+                       int64_t vsb, int64_t vsh, int64_t vst,
+                       const int32_t* cand, int B, int H, int T, int KC, int D, float scale,
+                       void* out, float* lse, void* stream);
+
+/*
+ * Attention over the keys a descent selected (replaces fastseg.py:367-383 candidate assembly +
+ * dedupe_fast + sparse_attn, and engine.py:107-119 for one decode position), neighbours off.
+ * The key set of query n (position t = tq[b*tq_sb + n]) is the union of
+ *   - the first min(n_tree[b,h,n], #valid) leaf blocks of ids/vld (n_tree NULL: all valid ones),
+ *   - the query's own partial leaf block [leaf*floor(t/leaf), t],
+ *   - the static keys {0, t, t-1, ..., t-Lw+1} (>= 0), Lw = max(local, 3),
+ * each position once.  q: (B,H,Nq,D) with strides; k, v: (B,H,Tk,D) with strides (the whole sequence or a
+ * KV cache); positions outside [0, Tk) are never read (a query with t >= Tk attends nothing).  ids/vld: (B,H,Nq,wl) contiguous.  out: (B,H,Nq,D) in the input dtype with strides; lse:
+ * (B,H,Nq) float32 or NULL; keys: (B,H,Nq) float32 number of keys attended, or NULL.
+ * nsplit > 1 splits every query's keys over nsplit wavefronts and merges them (for few queries with
+ * many keys, as in decode); ws must then hold ta_seg_attn_workspace_size(...) bytes.
+ */
+int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int nsplit);
+int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype,
+                    int64_t qsb, int64_t qsh, int64_t qsn, int64_t ksb, int64_t ksh, int64_t kst,
+                    int64_t vsb, int64_t vsh, int64_t vst,
+                    int B, int H, int Nq, int D, int Tk,
+                    const int32_t* tq, int64_t tq_sb,
+                    const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl,
+                    int leaf, int local, float scale,
+                    void* out, int64_t osb, int64_t osh, int64_t osn, float* lse, float* keys,
+                    int nsplit, float* ws, int64_t ws_bytes, void* stream);
+
+/*
+ * Decode-cache append with incremental node formation (replaces engine.py:41-55 SegState.add and the
+ * state writes of engine.py:102-106).  For every sequence b at position t = t_pos[b]: row t of the K and
+ * V caches (B,H,Tcap,D, cache dtype) takes k_new, v_new (B,H,D with strides, same dtype as the cache);
+ * then every pyramid node whose last position is t is formed: a leaf block as the adjacent-pair sum of
+ * its keys (position 0 counted as 0), a higher node as the adjacent-pair sum of its children.
+ */
+int ta_kv_append(const void* k_new, const void* v_new, int dtype,
+                 int64_t nsb, int64_t nsh, int64_t vnsb, int64_t vnsh,
+                 void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst,
+                 int B, int H, int D, int Tcap, const int32_t* t_pos,
+                 int n_levels, float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh,
+                 int leaf_log2, int arity_log2, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TREEATTN_H_ */

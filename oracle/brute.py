@@ -21,13 +21,20 @@ def pairwise_node_sum(rows, lo, size):
     return (a + b).astype(f32)
 
 
-def halving_dot(q, u):
-    """Canonical score: fp32 products, halving-tree sum."""
-    p = [f32(f32(x) * f32(y)) for x, y in zip(q, u)]
+def _halve(p):
     while len(p) > 1:
         h = len(p) // 2
         p = [f32(p[i] + p[i + h]) for i in range(h)]
     return p[0]
+
+
+def halving_dot(q, u):
+    """Canonical score: fp32 products; groups of D/16 consecutive products (D/min(16,D)) each reduced by the
+    halving tree, then the group sums reduced by the halving tree."""
+    p = [f32(f32(x) * f32(y)) for x, y in zip(q, u)]
+    G = min(16, len(p))
+    R = len(p) // G
+    return _halve([_halve(p[g * R:(g + 1) * R]) for g in range(G)])
 
 
 def node_vec(kidx, l, m):

@@ -10,9 +10,10 @@ Two scoring/ranking modes:
   in torch's CPU reduction order and ``torch.topk`` (seg.py:64-69).
 * ``canonical``: the order the HIP kernels implement and the one they are
   compared with bit-exactly.  A score is ``fl(q_d * U_d)`` per dimension (no
-  fused multiply-add), summed by the halving tree ``x[i] += x[i + D/2]``
-  repeated until one value remains, then multiplied by the exact power of two
-  ``2**-l``.  Candidates are ranked by score (descending) and, on equal
+  fused multiply-add), summed in ``canonical_sum`` order (16 groups of D/16
+  consecutive dimensions, halving tree ``x[i] += x[i + n/2]`` inside each
+  group, then the same halving tree over the 16 group sums), then multiplied
+  by the exact power of two ``2**-l``.  Candidates are ranked by score (descending) and, on equal
   scores, by node id (ascending); invalid candidates rank after every valid
   one.
 """
@@ -134,9 +135,22 @@ def halving_sum(p):
     return p[..., 0]
 
 
+def canonical_sum(p):
+    """Canonical reduction of the last axis (length D, a power of two): split it into G = min(16, D) groups of
+    R = D/G consecutive elements, reduce each group by the halving tree, then reduce the G group sums by the
+    halving tree.  This is the order of the kernels (16 lanes per node, lane g holding elements
+    [R*g, R*g+R), in-lane halving, then an xor butterfly over the 16 lanes)."""
+    D = p.shape[-1]
+    ilog2(D)
+    G = min(16, D)
+    grouped = p.reshape(*p.shape[:-1], G, D // G)
+    return halving_sum(halving_sum(grouped))
+
+
 def dot_canonical(q, U):
-    """q (b,H,N,d) fp32, U (b,H,N,C,d) fp32 -> (b,H,N,C): per-dim products rounded to fp32, halving-tree sum."""
-    return halving_sum(q.unsqueeze(3) * U)
+    """q (b,H,N,d) fp32, U (b,H,N,C,d) fp32 -> (b,H,N,C): per-dim products rounded to fp32 (no fused
+    multiply-add), canonical_sum order."""
+    return canonical_sum(q.unsqueeze(3) * U)
 
 
 def dot_faithful(q, U):

@@ -1,0 +1,201 @@
+"""Kernel-level parity of the HIP library against the CPU oracle (GPU only).
+
+Bit-exact: pyramid node sums, descent leaf ids / validity / scores (canonical order), gather-dot scores.
+Tolerance: attention outputs, 1e-5 (fp32) and 2e-2 (bf16) max-abs.  Inputs are generated on the CPU with
+seeded generators, so the GPU and the oracle see identical values."""
+import math
+
+import pytest
+import torch
+
+from oracle import seg_ref as S
+from oracle.attn_ref import assemble, gather_dot as o_gather_dot, gather_dot_blocks as o_gather_blocks
+from oracle.attn_ref import sparse_attn_ref
+from oracle.engine_ref import SegStateRef
+from treeattn_amd import kernels as K
+from treeattn_amd.config import Config
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-3}
+
+
+def rnd(*shape, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype)
+
+
+@pytest.mark.parametrize('T,D,leaf,arity,dtype', [(1024, 64, 2, 2, torch.float32), (4096, 64, 64, 2, torch.bfloat16),
+                                                  (2048, 128, 64, 2, torch.bfloat16), (4096, 16, 4, 4, torch.float32),
+                                                  (8192, 32, 128, 4, torch.float16)])
+def test_level_sums_bit_exact(T, D, leaf, arity, dtype):
+    print('case', T, D, leaf, arity, dtype, flush=True)
+    k = rnd(2, 3, T, D, seed=T + D, dtype=dtype)
+    shape = K.TreeShape(T, leaf, arity)
+    got = K.level_sums(k.to(DEV), shape.blevels)
+    want = S.pyramid(S.index_keys(k), S.Geometry(T, leaf, arity))
+    for j in range(shape.n_levels):
+        assert torch.equal(got[j].cpu(), want[j]), j
+
+
+def test_level_sums_partial_and_no_sink():
+    T, D = 1000, 64
+    k = rnd(1, 2, 1024, D, seed=3)
+    blevels = list(range(1, 9))
+    got = K.level_sums(k.to(DEV), blevels, t_end=T, zero_sink=False)
+    want = S.level_sums(k, 9)
+    for l, g in zip(blevels, got):
+        n = T >> l
+        assert torch.equal(g.cpu()[:, :, :n], want[l][:, :, :n]), l
+
+
+def _descent_case(T, D, leaf, arity, wmax, dtype, B=2, H=2, seed=0, tq=None):
+    q = rnd(B, H, T if tq is None else tq.shape[-1], D, seed=seed, dtype=dtype)
+    k = rnd(B, H, T, D, seed=seed + 1, dtype=dtype)
+    geom = S.Geometry(T, leaf, arity)
+    pyr = S.pyramid(S.index_keys(k), geom)
+    tq_cpu = torch.arange(T) if tq is None else tq
+    want = S.tree_pass_general(q.float(), pyr, tq_cpu, geom, wmax, 'canonical')
+    shape = K.TreeShape(T, leaf, arity)
+    levels = [pyr[j].to(DEV) for j in range(geom.J + 1)]
+    got = K.tree_descend(q.to(DEV), levels, tq_cpu.to(DEV), shape, wmax)
+    return want, [g.cpu() for g in got], (q, k, pyr)
+
+
+@pytest.mark.parametrize('T,D,leaf,arity,wmax,dtype', [
+    (256, 64, 2, 2, 8, torch.float32),       # reference tree
+    (1024, 64, 2, 2, 4, torch.float32),
+    (2048, 64, 64, 2, 32, torch.bfloat16),   # decode/prefill configuration shape
+    (4096, 128, 64, 2, 32, torch.bfloat16),
+    (4096, 64, 128, 4, 16, torch.bfloat16),  # 4-ary
+    (512, 16, 4, 4, 3, torch.float32),
+    (1024, 32, 8, 2, 5, torch.float16)])
+def test_descend_bit_exact(T, D, leaf, arity, wmax, dtype):
+    print('case', T, D, leaf, arity, wmax, dtype, flush=True)
+    (ids, vld, sct), (gi, gv, gs), _ = _descent_case(T, D, leaf, arity, wmax, dtype)
+    assert gi.shape == ids.shape
+    assert torch.equal(gv.bool(), vld)
+    assert torch.equal(gi.long()[vld], ids[vld])
+    assert torch.equal(gs[vld], sct[vld])
+    assert (gi[~vld] == -1).all()
+
+
+def test_descend_per_sequence_positions():
+    """Decode form: one query per sequence at its own position over a larger cache (Tcap)."""
+    Tcap, D = 4096, 64
+    tq = torch.tensor([[3000], [4095], [64], [0]])
+    (ids, vld, sct), (gi, gv, gs), _ = _descent_case(Tcap, D, 64, 2, 8, torch.bfloat16, B=4, H=3, tq=tq)
+    assert torch.equal(gv.bool(), vld)
+    assert torch.equal(gi.long()[vld], ids[vld])
+    assert torch.equal(gs[vld], sct[vld])
+
+
+def test_descend_near_ties_vs_faithful():
+    """Against the torch-faithful oracle (reference op order) differences may only be near-ties: report them."""
+    T, D, wmax = 2048, 64, 8
+    q = rnd(2, 4, T, D, seed=11)
+    k = rnd(2, 4, T, D, seed=12)
+    geom = S.Geometry(T, 2, 2)
+    pyr = S.pyramid(S.index_keys(k), geom)
+    ids_f, vld_f, sct_f = S.tree_pass_general(q, pyr, torch.arange(T), geom, wmax, 'faithful')
+    gi, gv, gs = [x.cpu() for x in K.tree_descend(q.to(DEV), [pyr[j].to(DEV) for j in range(geom.J + 1)],
+                                                  torch.arange(T).to(DEV), K.TreeShape(T), wmax)]
+    same = (torch.where(vld_f, ids_f, -1) == torch.where(gv.bool(), gi.long(), -1)).all(-1)
+    n_diff = int((~same).sum())
+    print('queries with a different leaf list vs faithful order: %d of %d' % (n_diff, same.numel()))
+    assert same.float().mean().item() > 0.995
+
+
+@pytest.mark.parametrize('dtype,D', [(torch.float32, 64), (torch.bfloat16, 128), (torch.float16, 16)])
+def test_gather_dot_bit_exact(dtype, D):
+    q = rnd(2, 3, 50, D, seed=1, dtype=dtype)
+    Sm = rnd(2, 3, 70, D, seed=2, dtype=torch.float32)
+    g = torch.Generator().manual_seed(3)
+    cand = torch.randint(-2, 75, (2, 3, 50, 17), generator=g)
+    got = K.gather_dot(q.to(DEV), Sm.to(DEV), cand.to(DEV), 0.125).cpu()
+    want = o_gather_dot(q, Sm, cand, 0.125, mode='canonical')
+    assert torch.equal(got, want)
+    faithful = o_gather_dot(q, Sm, cand, 0.125)
+    assert (got - faithful).abs().max().item() < 1e-5
+
+
+def test_gather_dot_blocks_bit_exact():
+    B, H, T, D, NB, blk = 2, 2, 512, 64, 4, 64
+    q = rnd(B, H, T, D, seed=4, dtype=torch.bfloat16)
+    Km = rnd(B, H, T, D, seed=5, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(6)
+    idx = torch.randint(0, T // blk, (B, H, T, NB), generator=g, dtype=torch.int32)
+    got = K.gather_dot_blocks(q.to(DEV), Km.to(DEV), idx.to(DEV), blk).cpu()
+    want = o_gather_blocks(q, Km, idx, blk)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize('dtype,D', [(torch.float32, 64), (torch.bfloat16, 64), (torch.bfloat16, 128),
+                                     (torch.float32, 16)])
+def test_sparse_attn_matches_oracle(dtype, D):
+    B, H, T, KC = 2, 2, 160, 52
+    q, k, v = [rnd(B, H, T, D, seed=s, dtype=dtype) for s in (7, 8, 9)]
+    g = torch.Generator().manual_seed(10)
+    cand = torch.randint(-1, T, (B, H, T, KC), generator=g)
+    cand[..., 0] = torch.arange(T)
+    cand[1, 1, 5] = -1  # a row with nothing valid
+    out, lse = K.sparse_attn_fwd(q.to(DEV), k.to(DEV), v.to(DEV), cand.to(DEV), 1 / math.sqrt(D))
+    want = sparse_attn_ref(q, k, v, cand, 1 / math.sqrt(D))
+    assert (out.cpu().float() - want.float()).abs().max().item() < TOL[dtype]
+    assert (out.cpu()[1, 1, 5] == 0).all()
+
+
+def _seg_case(T, D, leaf, arity, wmax, dtype, beam=None, nsplit=1, local=3, B=2, H=2):
+    cfg = Config(wmax=wmax, beam=beam or wmax, neighbors=False, leaf=leaf, arity=arity, local=local, n_head=H)
+    q, k, v = [rnd(B, H, T, D, seed=s, dtype=dtype) for s in (20, 21, 22)]
+    geom = S.Geometry(T, leaf, arity)
+    pyr = S.pyramid(S.index_keys(k), geom)
+    tq = torch.arange(T)
+    ids, vld, sct = S.tree_pass_general(q.float(), pyr, tq, geom, wmax, 'canonical')
+    lhat = torch.full((B, H, T), cfg.beam, dtype=torch.long)
+    nid = torch.zeros(B, H, T, cfg.nb_window * cfg.nb_store, dtype=torch.long)
+    sel = S.finish(ids, vld, nid, torch.zeros_like(nid, dtype=torch.bool), torch.zeros(B, H, T, dtype=torch.long),
+                   lhat, cfg, leaf)
+    cand, keep, used = assemble(sel, tq, cfg, B, H)
+    want = sparse_attn_ref(q, k, v, torch.where(keep, cand, -1), 1 / math.sqrt(D))
+    gi = torch.where(vld, ids, -1).to(torch.int32)
+    out, lse, keys = K.seg_attn(q.to(DEV), k.to(DEV), v.to(DEV), tq.to(DEV), gi.to(DEV), vld.to(torch.uint8).to(DEV),
+                                sel['n_tree'].to(DEV), leaf, local, 1 / math.sqrt(D),
+                                keys=torch.empty(B, H, T, device=DEV), nsplit=nsplit)
+    return want, out.cpu(), keys.cpu(), keep
+
+
+@pytest.mark.parametrize('T,D,leaf,arity,wmax,dtype,beam,nsplit', [
+    (256, 64, 2, 2, 8, torch.float32, 4, 1),
+    (1024, 64, 64, 2, 4, torch.bfloat16, None, 1),
+    (1024, 128, 64, 2, 4, torch.bfloat16, None, 3),
+    (512, 32, 32, 2, 8, torch.float32, None, 1),
+    (1024, 64, 16, 4, 6, torch.float32, 3, 2)])
+def test_seg_attn_matches_oracle(T, D, leaf, arity, wmax, dtype, beam, nsplit):
+    print('case', T, D, leaf, arity, wmax, dtype, beam, nsplit, flush=True)
+    want, got, keys, keep = _seg_case(T, D, leaf, arity, wmax, dtype, beam, nsplit)
+    assert (got.float() - want.float()).abs().max().item() < TOL[dtype]
+    assert torch.equal(keys, keep.sum(-1).float())
+
+
+def test_kv_append_matches_state_add():
+    """Appending positions one by one forms the same nodes as the oracle's SegState.add, bit for bit."""
+    Tcap, H, D, leaf, arity = 512, 3, 64, 8, 4
+    cfg = Config(leaf=leaf, arity=arity, nb_store=2)
+    ref = SegStateRef(cfg, Tcap, H, D)
+    shape = K.TreeShape(Tcap, leaf, arity)
+    Kc = torch.zeros(1, H, Tcap, D, device=DEV)
+    Vc = torch.zeros(1, H, Tcap, D, device=DEV)
+    levels = shape.alloc_levels(1, H, D, DEV)
+    for lv in levels:
+        lv.zero_()
+    kk = rnd(Tcap, 1, H, D, seed=30)
+    vv = rnd(Tcap, 1, H, D, seed=31)
+    tpos = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for t in range(Tcap):
+        ref.add(t, kk[t], vv[t])
+        tpos.fill_(t)
+        K.kv_append(kk[t].to(DEV), vv[t].to(DEV), Kc, Vc, tpos, levels, leaf, arity)
+    assert torch.equal(Kc.cpu(), ref.K) and torch.equal(Vc.cpu(), ref.V)
+    for j, l in enumerate(shape.blevels):
+        assert torch.equal(levels[j].cpu(), ref.raw[l]), j

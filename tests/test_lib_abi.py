@@ -1,0 +1,57 @@
+"""CPU-side checks of the C-ABI library: it is built, loads, and exports every entry point include/treeattn.h
+declares (no compute calls: there is no GPU here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'treeattn.h')
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(ta_[a-z_0-9]+)\s*\(', text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for n in ('ta_level_sums', 'ta_tree_descend', 'ta_gather_dot', 'ta_gather_dot_blocks', 'ta_sparse_attn_fwd',
+              'ta_seg_attn_fwd', 'ta_kv_append', 'ta_last_error', 'ta_abi_version'):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    import torch  # noqa: F401  (the library binds to the HIP runtime torch loads)
+    from treeattn_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail('libtreeattn.so is not built (python -m treeattn_amd.build)')
+    L = _lib.lib()
+    for n in declared_functions():
+        assert hasattr(L, n), n
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+    assert L.ta_abi_version() == 1
+
+
+def test_library_rejects_bad_arguments_without_gpu():
+    """Argument validation runs on the host: a bad size returns an error code and a message."""
+    import torch  # noqa: F401
+    from treeattn_amd import _lib
+    L = _lib.lib()
+    rc = L.ta_tree_descend(None, 0, 0, 0, 0, 1, 1, 4, 64, None, 0, 0, None, None, None, 100, 1, 1, 4, 4,
+                           None, None, None, None)
+    assert rc == 1
+    assert b'bad sizes' in L.ta_last_error()
+    rc = L.ta_seg_attn_fwd(None, None, None, 2, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 64, 64, None, 0, None, None, None, 4,
+                           64, 200, 0.1, None, 0, 0, 0, None, None, 1, None, 0, None)
+    assert rc == 2
+
+
+def test_product_refuses_cpu_tensors():
+    import torch
+    from treeattn_amd import kernels
+    q = torch.zeros(1, 1, 4, 64)
+    with pytest.raises(RuntimeError, match='GPU'):
+        kernels.gather_dot(q, q, torch.zeros(1, 1, 4, 2, dtype=torch.long), 1.0)

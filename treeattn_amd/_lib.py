@@ -1,0 +1,129 @@
+"""ctypes binding of libtreeattn.so (the C ABI declared in include/treeattn.h).
+
+The library is loaded after torch so it binds to the HIP runtime torch already loaded.  Every call passes
+device pointers, element strides and torch's current HIP stream; a non-zero status raises RuntimeError
+with the library's message.  There is no fallback: a missing library, a non-GPU tensor or an unsupported
+device raises.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, 'libtreeattn.so')
+
+F32, F16, BF16 = 0, 1, 2
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+c_i32, c_i64, c_f32, c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+_P = ctypes.POINTER
+
+# name -> (restype, argtypes); mirrors include/treeattn.h
+SIGNATURES = {
+    'ta_abi_version': (c_i32, []),
+    'ta_last_error': (ctypes.c_char_p, []),
+    'ta_device_supported': (c_i32, []),
+    'ta_level_sums_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32]),
+    'ta_level_sums': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                              _P(c_vp), _P(c_i64), _P(c_i64), _P(ctypes.c_int32), c_vp, c_i64, c_vp]),
+    'ta_tree_descend': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64,
+                                c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32,
+                                c_vp, c_vp, c_vp, c_vp]),
+    'ta_gather_dot': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i32, c_i64, c_i64, c_i64, c_vp,
+                              c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_vp]),
+    'ta_gather_dot_blocks': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp,
+                                     c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_vp]),
+    'ta_sparse_attn_fwd': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                   c_i64, c_i64, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_vp,
+                                   c_vp]),
+    'ta_seg_attn_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    'ta_seg_attn_fwd': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32,
+                                c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64,
+                                c_vp]),
+    'ta_kv_append': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
+                             c_i32, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32,
+                             c_i32, c_vp]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load (once) and return the library.  Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError('treeattn_amd: %s is missing; build it with `python -m treeattn_amd.build`'
+                               % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc, name):
+    if rc != 0:
+        msg = lib().ta_last_error().decode(errors='replace')
+        raise RuntimeError('treeattn_amd: %s failed (status %d): %s' % (name, rc, msg))
+
+
+def call(name, *args):
+    check(getattr(lib(), name)(*args), name)
+
+
+def dtype_code(t):
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError('treeattn_amd: unsupported dtype %s' % t.dtype) from None
+
+
+_checked_devices = set()
+
+
+def require_gpu(*tensors):
+    """Every tensor must live on a supported GPU; the first use of a device checks it is a gfx950."""
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError('treeattn_amd: tensors must be on the GPU (got %s); there is no CPU path'
+                               % t.device)
+        dev = t.device.index if t.device.index is not None else torch.cuda.current_device()
+        if dev not in _checked_devices:
+            with torch.cuda.device(dev):
+                if lib().ta_device_supported() != 1:
+                    raise RuntimeError('treeattn_amd: device %d is not a gfx950 (MI355X)' % dev)
+            _checked_devices.add(dev)
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def rows3(t):
+    """Strides (b, h, n) in elements of a (B, H, N, D) tensor whose last dimension is contiguous."""
+    if t.stride(-1) != 1:
+        raise ValueError('treeattn_amd: last dimension must be contiguous')
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def ptr_array(tensors):
+    return (c_vp * max(1, len(tensors)))(*[t.data_ptr() for t in tensors])
+
+
+def i64_array(vals):
+    return (c_i64 * max(1, len(vals)))(*vals)
+
+
+def i32_array(vals):
+    return (ctypes.c_int32 * max(1, len(vals)))(*vals)

@@ -1,0 +1,58 @@
+"""Build libtreeattn.so (gfx950) in-tree with hipcc.
+
+    python -m treeattn_amd.build            # compile every source, link the library
+
+Every HIP source is compiled for gfx950 only, with packed-fp32 instruction generation disabled.  The
+selection kernels (select.hip) are compiled with floating-point contraction off so their scores follow
+the canonical float32 order exactly.
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, 'csrc')
+OBJ = os.path.join(HERE, '_build')
+LIB = os.path.join(HERE, 'libtreeattn.so')
+HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
+
+SOURCES = {
+    'abi.hip': [],
+    'select.hip': ['-ffp-contract=off'],
+    'attend.hip': [],
+}
+
+COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',
+          '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+          '-I', os.path.join(HERE, '..', 'include')]
+
+
+def _compile(name):
+    src = os.path.join(CSRC, name)
+    obj = os.path.join(OBJ, name.replace('.hip', '.o'))
+    cmd = [HIPCC, '-c', src, '-o', obj] + COMMON + SOURCES[name]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError('hipcc failed for %s:\n%s\n%s' % (name, ' '.join(cmd), r.stderr[-6000:]))
+    return obj
+
+
+def build(verbose=True):
+    os.makedirs(OBJ, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+        objs = list(ex.map(_compile, sorted(SOURCES)))
+    tmp = LIB + '.tmp'
+    cmd = [HIPCC, '-shared', '-fPIC', '--offload-arch=gfx950', '-o', tmp] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError('link failed:\n%s' % r.stderr[-4000:])
+    os.replace(tmp, LIB)
+    if verbose:
+        print('built', LIB)
+    return LIB
+
+
+if __name__ == '__main__':
+    build()
+    sys.exit(0)

@@ -1,0 +1,515 @@
+// Segment-tree key selection on gfx950: level-sum pyramid builder, beam descent with per-query top-k,
+// and gather-dot scoring.  Every score that decides a selection is computed in the canonical float32
+// order (products rounded separately, grouped halving-tree sum), so results are bit-identical to the CPU
+// oracle's canonical mode.  This file is compiled with -ffp-contract=off.
+//
+// Reference functions replaced: seg.py:26-41 level_sums, fastseg.py:238-251 level_sums_min (no gate),
+// seg.py:44-70 tree_pass, fastseg.py:254-271 tree_pass_fast, fastseg.py:118-130 gather_dot.
+#pragma clang fp contract(off)
+
+#include "common.hpp"
+
+namespace ta {
+
+// ----------------------------------------------------------------------------------------- canonical dot
+// Lane j of a 16-lane group holds q and s elements [R*j, R*j + R).  In-lane halving tree, then an xor
+// butterfly over the 16 lanes (offsets 8, 4, 2, 1).  Every lane of the group returns the same value.
+template <int R>
+__device__ __forceinline__ float canon_dot(const float (&q)[R], const float (&s)[R]) {
+  float p[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) p[i] = __fmul_rn(q[i], s[i]);
+#pragma unroll
+  for (int n = R / 2; n >= 1; n /= 2) {
+#pragma unroll
+    for (int i = 0; i < n; ++i) p[i] = __fadd_rn(p[i], p[i + n]);
+  }
+  float x = p[0];
+  x = __fadd_rn(x, __shfl_xor(x, 8, kWave));
+  x = __fadd_rn(x, __shfl_xor(x, 4, kWave));
+  x = __fadd_rn(x, __shfl_xor(x, 2, kWave));
+  x = __fadd_rn(x, __shfl_xor(x, 1, kWave));
+  return x;
+}
+
+// 2^-l as an exact float (l < 127)
+__device__ __forceinline__ float pow2_neg(int l) { return __int_as_float((127 - l) << 23); }
+
+// ----------------------------------------------------------------------------------------- pyramid build
+struct LevelOut {
+  float* ptr[kMaxLevels];
+  int64_t sb[kMaxLevels];
+  int64_t sh[kMaxLevels];
+  int8_t slot_of_blevel[64];  // binary level -> output level index, -1 when not written
+};
+
+__device__ __forceinline__ void store_node(const LevelOut& lo, int blevel, int b, int h, int64_t node, int D,
+                                           int d, float x) {
+  if (blevel < 64) {
+    int j = lo.slot_of_blevel[blevel];
+    if (j >= 0) lo.ptr[j][b * lo.sb[j] + h * lo.sh[j] + node * D + d] = x;
+  }
+}
+
+// One pass over rows of granularity 2^base (base 0: the keys).  Thread (d, seg): dimension d of a segment
+// of 64 consecutive rows, reduced by adjacent pairs with a carry stack (left + right, float32); the
+// workgroup then combines its NSEG segment sums the same way.  Nodes are written when their binary level
+// is an output level; the workgroup's total (the node of size 64*NSEG rows) goes to `tot` when complete.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void level_pass_kernel(const T* __restrict__ in, int64_t isb, int64_t ish,
+                                                         int64_t isr, int H, int n_rows, int base,
+                                                         int zero_first, LevelOut lo, float* __restrict__ tot,
+                                                         int n_chunks) {
+  constexpr int NSEG = 256 / D;
+  constexpr int LOG_NSEG = NSEG == 1 ? 0 : NSEG == 2 ? 1 : NSEG == 4 ? 2 : NSEG == 8 ? 3 : 4;
+  __shared__ float seg_sum[NSEG][D];
+  const int d = threadIdx.x % D;
+  const int seg = threadIdx.x / D;
+  const int chunk = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / H, h = bh % H;
+  const int64_t row0 = (int64_t)chunk * 64 * NSEG + seg * 64;
+  const T* src = in + b * isb + h * ish + d;
+
+  float carry[7];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const int64_t r = row0 + i;
+    if (r < n_rows) {
+      float x = (zero_first && r == 0) ? 0.0f : to_f32(src[r * isr]);
+      int lv = 0;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        if (((i >> k) & 1) == 0) break;
+        x = __fadd_rn(carry[k], x);
+        lv = k + 1;
+        store_node(lo, base + lv, b, h, r >> lv, D, d, x);
+      }
+      carry[lv] = x;
+    }
+  }
+  const bool seg_full = row0 + 63 < n_rows;
+  if (seg_full) seg_sum[seg][d] = carry[6];
+  __syncthreads();
+  if (seg == 0) {
+    float c2[LOG_NSEG + 1];
+    const int64_t gseg0 = (int64_t)chunk * NSEG;
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+      if ((gseg0 + s) * 64 + 63 < n_rows) {
+        float x = seg_sum[s][d];
+        int lv = 0;
+#pragma unroll
+        for (int k = 0; k < LOG_NSEG; ++k) {
+          if (((s >> k) & 1) == 0) break;
+          x = __fadd_rn(c2[k], x);
+          lv = k + 1;
+          store_node(lo, base + 6 + lv, b, h, (gseg0 + s) >> lv, D, d, x);
+        }
+        c2[lv] = x;
+      }
+    }
+    if (tot != nullptr && (int64_t)(chunk + 1) * 64 * NSEG <= n_rows)
+      tot[((int64_t)bh * n_chunks + chunk) * D + d] = c2[LOG_NSEG];
+  }
+}
+
+// ----------------------------------------------------------------------------------------- descent
+struct LevelIn {
+  const float* ptr[kMaxLevels];
+  int64_t sb[kMaxLevels];
+  int64_t sh[kMaxLevels];
+  int blevel[kMaxLevels];
+};
+
+// One wavefront per query.  Levels whose number of complete nodes is <= wmax keep every node, so the
+// descent starts at the highest level with more complete nodes than wmax (all of them are candidates
+// there) -- the same kept sets as descending from the top.  Each level: score candidates (16 lanes per
+// node, 4 nodes per round), rank every candidate against all others (score desc, id asc), keep the best
+// wmax, expand them to their children and add the level's complete left siblings.
+template <typename TQ, int D>
+__global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, int64_t qsb, int64_t qsh,
+                                                      int64_t qsn, int H, int Nq, int T, const int32_t* __restrict__ tq,
+                                                      int64_t tq_sb, LevelIn lv, int n_levels, int arity_log2,
+                                                      int wmax, int wl, int cmax, int32_t* __restrict__ ids,
+                                                      uint8_t* __restrict__ vld, float* __restrict__ sct) {
+  constexpr int R = D / 16;
+  constexpr int NB = (64 / R) < 16 ? (64 / R) : 16;
+  extern __shared__ int32_t smem_i[];
+  const int lane = lane_id(), w = wave_id();
+  const int n = blockIdx.x * (blockDim.x / kWave) + w;
+  if (n >= Nq) return;
+  const int bh = blockIdx.y;
+  const int b = bh / H, h = bh % H;
+  int32_t* cid = smem_i + w * (2 * cmax + 2 * wmax);
+  float* csc = reinterpret_cast<float*>(cid + cmax);
+  int32_t* kid = cid + 2 * cmax;
+  float* ksc = reinterpret_cast<float*>(kid + wmax);
+
+  const int t = tq[b * tq_sb + n];
+  const int g = lane >> 4, j16 = lane & 15;
+  float qr[R];
+  load_row<TQ, R>(q + b * qsb + h * qsh + n * qsn + R * j16, qr);
+  const int64_t obase = ((int64_t)bh * Nq + n) * wl;
+  const int arity = 1 << arity_log2;
+
+  int nk = 0;
+  if (n_levels > 0 && t > 0 && t < T) {
+    int start = 0;
+    for (int j = n_levels - 1; j >= 0; --j) {
+      if ((t >> lv.blevel[j]) > wmax) { start = j; break; }
+    }
+    int C = t >> lv.blevel[start];
+    for (int c = lane; c < C; c += kWave) cid[c] = c;
+    wave_sync();
+    for (int j = start;; --j) {
+      const float* base = lv.ptr[j] + b * lv.sb[j] + h * lv.sh[j] + R * j16;
+      const float scale = pow2_neg(lv.blevel[j]);
+      for (int c0 = 0; c0 < C; c0 += 4 * NB) {
+        float rows[NB][R];
+#pragma unroll
+        for (int r = 0; r < NB; ++r) {
+          const int c = c0 + 4 * r + g;
+          if (c < C) {
+            load_row<float, R>(base + (int64_t)cid[c] * D, rows[r]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < R; ++i) rows[r][i] = 0.0f;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < NB; ++r) {
+          const int c = c0 + 4 * r + g;
+          const float s = __fmul_rn(canon_dot<R>(qr, rows[r]), scale);
+          if (c < C && j16 == 0) csc[c] = s;
+        }
+      }
+      wave_sync();
+      for (int c = lane; c < C; c += kWave) {
+        const float s = csc[c];
+        const int id = cid[c];
+        int rank = 0;
+        for (int o = 0; o < C; ++o) {
+          const float so = csc[o];
+          const int io = cid[o];
+          rank += (so > s) || (so == s && io < id);
+        }
+        if (rank < wmax) {
+          kid[rank] = id;
+          ksc[rank] = s;
+        }
+      }
+      nk = C < wmax ? C : wmax;
+      wave_sync();
+      if (j == 0) break;
+      const int m = t >> lv.blevel[j - 1];
+      const int digit = m & (arity - 1);
+      const int nch = nk << arity_log2;
+      C = nch + digit;
+      for (int c = lane; c < C; c += kWave) {
+        cid[c] = c < nch ? (kid[c >> arity_log2] << arity_log2) + (c & (arity - 1)) : m - 1 - (c - nch);
+      }
+      wave_sync();
+    }
+  }
+  for (int r = lane; r < wl; r += kWave) {
+    if (r < nk) {
+      ids[obase + r] = kid[r];
+      vld[obase + r] = 1;
+      sct[obase + r] = ksc[r];
+    } else {
+      ids[obase + r] = -1;
+      vld[obase + r] = 0;
+      sct[obase + r] = -INFINITY;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------------- gather-dot
+// One wavefront per query row; 4 candidates per round (16 lanes each).  blk != nullptr selects the
+// leaf-block form: candidate c is row blk[c >> block_log2] * block + (c & (block - 1)).
+template <typename TQ, typename TS, int D>
+__global__ __launch_bounds__(256) void gather_dot_kernel(const TQ* __restrict__ q, int64_t qsb, int64_t qsh,
+                                                         int64_t qsn, const TS* __restrict__ S, int64_t ssb,
+                                                         int64_t ssh, int64_t ssn, const int32_t* __restrict__ cand,
+                                                         const int32_t* __restrict__ blk, int block_log2, int NB_blk,
+                                                         int H, int N, int M, int C, float scale,
+                                                         float* __restrict__ out) {
+  constexpr int R = D / 16;
+  constexpr int NB = (64 / R) < 16 ? (64 / R) : 16;
+  const int lane = lane_id(), w = wave_id();
+  const int n = blockIdx.x * (blockDim.x / kWave) + w;
+  if (n >= N) return;
+  const int bh = blockIdx.y;
+  const int b = bh / H, h = bh % H;
+  const int g = lane >> 4, j16 = lane & 15;
+  float qr[R];
+  load_row<TQ, R>(q + b * qsb + h * qsh + n * qsn + R * j16, qr);
+  const TS* base = S + b * ssb + h * ssh + R * j16;
+  const int64_t row = (int64_t)bh * N + n;
+  for (int c0 = 0; c0 < C; c0 += 4 * NB) {
+    float rows[NB][R];
+#pragma unroll
+    for (int r = 0; r < NB; ++r) {
+      const int c = c0 + 4 * r + g;
+      if (c < C) {
+        int idx;
+        if (blk != nullptr) {
+          idx = (blk[row * NB_blk + (c >> block_log2)] << block_log2) + (c & ((1 << block_log2) - 1));
+        } else {
+          idx = cand[row * C + c];
+        }
+        idx = idx < 0 ? 0 : (idx > M - 1 ? M - 1 : idx);
+        load_row<TS, R>(base + (int64_t)idx * ssn, rows[r]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < R; ++i) rows[r][i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NB; ++r) {
+      const int c = c0 + 4 * r + g;
+      const float s = __fmul_rn(canon_dot<R>(qr, rows[r]), scale);
+      if (c < C && j16 == 0) out[row * C + c] = s;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------------- host side
+namespace {
+
+bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int log2i(int64_t x) {
+  int l = 0;
+  while ((int64_t(1) << l) < x) ++l;
+  return l;
+}
+
+template <template <typename, int> class F, typename... A>
+int dispatch_dt_d(int dt, int D, A&&... a) {
+#define TA_CASE_D(T)                                            \
+  switch (D) {                                                  \
+    case 16: return F<T, 16>::run(std::forward<A>(a)...);       \
+    case 32: return F<T, 32>::run(std::forward<A>(a)...);       \
+    case 64: return F<T, 64>::run(std::forward<A>(a)...);       \
+    case 128: return F<T, 128>::run(std::forward<A>(a)...);     \
+    default: set_error("head dim must be 16, 32, 64 or 128"); return TA_ERR_UNSUPPORTED; \
+  }
+  switch (dt) {
+    case TA_F32: TA_CASE_D(float)
+    case TA_F16: TA_CASE_D(f16_t)
+    case TA_BF16: TA_CASE_D(bf16_t)
+    default: set_error("unknown dtype"); return TA_ERR_ARG;
+  }
+#undef TA_CASE_D
+}
+
+int chunk_rows(int D) { return 64 * (256 / D); }
+
+template <typename T, int D>
+struct LevelSumsRun {
+  static int run(const void* k, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int t_end, int zero_sink,
+                 const LevelOut& lo, int top_blevel, float* ws, hipStream_t st) {
+    const int CH = chunk_rows(D);
+    const int LCH = log2i(CH);
+    int64_t nA = ((int64_t)t_end / CH + 1) * B * H * D;
+    float* bufs[2] = {ws, ws + nA};
+    int base = 0;
+    int n_rows = t_end;
+    int pass = 0;
+    // pass 0 reads the keys; later passes read the previous pass's chunk totals
+    const void* src = k;
+    int64_t sb = ksb, sh = ksh, sr = kst;
+    while (true) {
+      const int n_chunks = (n_rows + CH - 1) / CH;
+      if (n_chunks == 0) break;
+      const bool more = top_blevel > base + LCH;
+      float* tot = more ? bufs[pass & 1] : nullptr;
+      const int tot_chunks = n_rows / CH;
+      dim3 grid(n_chunks, B * H);
+      if (pass == 0) {
+        hipLaunchKernelGGL((level_pass_kernel<T, D>), grid, dim3(256), 0, st, (const T*)src, sb, sh, sr, H, n_rows,
+                           base, zero_sink, lo, tot, tot_chunks);
+      } else {
+        hipLaunchKernelGGL((level_pass_kernel<float, D>), grid, dim3(256), 0, st, (const float*)src, sb, sh, sr, H,
+                           n_rows, base, 0, lo, tot, tot_chunks);
+      }
+      int rc = check_launch("level_pass_kernel");
+      if (rc) return rc;
+      if (!more) break;
+      src = tot;
+      sr = D;
+      sh = (int64_t)tot_chunks * D;
+      sb = sh * H;
+      n_rows = tot_chunks;
+      base += LCH;
+      ++pass;
+    }
+    return TA_OK;
+  }
+};
+
+template <typename T, int D>
+struct DescendRun {
+  static int run(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H, int Nq, const int32_t* tq,
+                 int64_t tq_sb, const LevelIn& lv, int n_levels, int Tgeo, int arity_log2, int wmax, int wl,
+                 int32_t* ids, uint8_t* vld, float* sct, hipStream_t st) {
+    const int arity = 1 << arity_log2;
+    const int cmax = arity * wmax + arity - 1;
+    const int waves = Nq >= 4 ? 4 : 1;
+    const size_t lds = (size_t)waves * (2 * cmax + 2 * wmax) * sizeof(int32_t);
+    if (lds > 64 * 1024) {
+      set_error("descent beam too wide for LDS (arity * wmax too large)");
+      return TA_ERR_UNSUPPORTED;
+    }
+    dim3 grid((Nq + waves - 1) / waves, B * H);
+    hipLaunchKernelGGL((descend_kernel<T, D>), grid, dim3(waves * kWave), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq,
+                       Tgeo, tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax, ids, vld, sct);
+    return check_launch("descend_kernel");
+  }
+};
+
+template <typename TQ, int D>
+struct GatherDotRun {
+  template <typename TS>
+  static int go(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* S, int64_t ssb, int64_t ssh,
+                int64_t ssn, const int32_t* cand, const int32_t* blk, int block_log2, int NB_blk, int B, int H,
+                int N, int M, int C, float scale, float* out, hipStream_t st) {
+    dim3 grid((N + 3) / 4, B * H);
+    hipLaunchKernelGGL((gather_dot_kernel<TQ, TS, D>), grid, dim3(256), 0, st, (const TQ*)q, qsb, qsh, qsn,
+                       (const TS*)S, ssb, ssh, ssn, cand, blk, block_log2, NB_blk, H, N, M, C, scale, out);
+    return check_launch("gather_dot_kernel");
+  }
+  static int run(int s_dtype, const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* S, int64_t ssb,
+                 int64_t ssh, int64_t ssn, const int32_t* cand, const int32_t* blk, int block_log2, int NB_blk, int B,
+                 int H, int N, int M, int C, float scale, float* out, hipStream_t st) {
+    switch (s_dtype) {
+      case TA_F32: return go<float>(q, qsb, qsh, qsn, S, ssb, ssh, ssn, cand, blk, block_log2, NB_blk, B, H, N, M, C, scale, out, st);
+      case TA_F16: return go<f16_t>(q, qsb, qsh, qsn, S, ssb, ssh, ssn, cand, blk, block_log2, NB_blk, B, H, N, M, C, scale, out, st);
+      case TA_BF16: return go<bf16_t>(q, qsb, qsh, qsn, S, ssb, ssh, ssn, cand, blk, block_log2, NB_blk, B, H, N, M, C, scale, out, st);
+      default: set_error("unknown dtype"); return TA_ERR_ARG;
+    }
+  }
+};
+
+bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
+
+int elem_size(int dt) { return dt == TA_F32 ? 4 : 2; }
+
+// A row slice of R = D/16 elements per lane is read with loads of up to 16 bytes: the base and all row
+// strides must keep that slice aligned.
+bool rows_aligned(const void* p, int dt, int D, std::initializer_list<int64_t> strides) {
+  int slice = (D / 16) * elem_size(dt);
+  int a = slice >= 16 ? 16 : slice;
+  if (!aligned(p, a)) return false;
+  for (int64_t s : strides)
+    if ((s * elem_size(dt)) % a) return false;
+  return true;
+}
+
+}  // namespace
+}  // namespace ta
+
+using namespace ta;
+
+extern "C" int64_t ta_level_sums_workspace_size(int B, int H, int t_end, int D) {
+  if (D <= 0 || D > 256) return 0;
+  int CH = chunk_rows(D);
+  int64_t nA = ((int64_t)t_end / CH + 1) * B * H * D;
+  int64_t nB = ((int64_t)t_end / CH / CH + 1) * B * H * D;
+  return (nA + nB) * (int64_t)sizeof(float);
+}
+
+extern "C" int ta_level_sums(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H,
+                             int t_end, int D, int zero_sink, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                             const int64_t* lv_sh, const int32_t* lv_blevel, float* ws, int64_t ws_bytes,
+                             void* stream) {
+  if (B <= 0 || H <= 0 || t_end < 0 || n_levels < 0 || n_levels > kMaxLevels) {
+    set_error("ta_level_sums: bad sizes");
+    return TA_ERR_ARG;
+  }
+  if (t_end == 0 || n_levels == 0) return TA_OK;
+  LevelOut lo;
+  for (int i = 0; i < 64; ++i) lo.slot_of_blevel[i] = -1;
+  int prev = 0;
+  for (int j = 0; j < n_levels; ++j) {
+    if (lv_blevel[j] <= prev || lv_blevel[j] >= 63) {
+      set_error("ta_level_sums: output levels must be increasing binary levels >= 1");
+      return TA_ERR_ARG;
+    }
+    prev = lv_blevel[j];
+    lo.ptr[j] = lv_ptr[j];
+    lo.sb[j] = lv_sb[j];
+    lo.sh[j] = lv_sh[j];
+    lo.slot_of_blevel[lv_blevel[j]] = (int8_t)j;
+  }
+  if (ws_bytes < ta_level_sums_workspace_size(B, H, t_end, D)) {
+    set_error("ta_level_sums: workspace too small");
+    return TA_ERR_WORKSPACE;
+  }
+  return dispatch_dt_d<LevelSumsRun>(k_dtype, D, k, ksb, ksh, kst, B, H, t_end, zero_sink, lo, prev, ws,
+                                    (hipStream_t)stream);
+}
+
+extern "C" int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H,
+                               int Nq, int D, const int32_t* tq, int64_t tq_sb, int n_levels,
+                               const float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh, int T,
+                               int leaf_log2, int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld,
+                               float* sct, void* stream) {
+  if (B <= 0 || H <= 0 || Nq < 0 || wmax < 1 || wl < 0 || n_levels < 0 || n_levels > kMaxLevels || !pow2(T) ||
+      leaf_log2 < 1 || arity_log2 < 1) {
+    set_error("ta_tree_descend: bad sizes");
+    return TA_ERR_ARG;
+  }
+  if (Nq == 0) return TA_OK;
+  if (!rows_aligned(q, q_dtype, D, {qsb, qsh, qsn})) {
+    set_error("ta_tree_descend: q rows not aligned");
+    return TA_ERR_ARG;
+  }
+  LevelIn lv;
+  for (int j = 0; j < n_levels; ++j) {
+    lv.ptr[j] = lv_ptr[j];
+    lv.sb[j] = lv_sb[j];
+    lv.sh[j] = lv_sh[j];
+    lv.blevel[j] = leaf_log2 + j * arity_log2;
+    if (!aligned(lv_ptr[j], 16)) {
+      set_error("ta_tree_descend: level pointer not 16-byte aligned");
+      return TA_ERR_ARG;
+    }
+  }
+  return dispatch_dt_d<DescendRun>(q_dtype, D, q, qsb, qsh, qsn, B, H, Nq, tq, tq_sb, lv, n_levels, T, arity_log2,
+                                   wmax, wl, ids, vld, sct, (hipStream_t)stream);
+}
+
+extern "C" int ta_gather_dot(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const void* S,
+                             int s_dtype, int64_t ssb, int64_t ssh, int64_t ssn, const int32_t* cand, int B, int H,
+                             int N, int M, int C, int D, float scale, float* out, void* stream) {
+  if (B <= 0 || H <= 0 || N < 0 || M <= 0 || C < 0) {
+    set_error("ta_gather_dot: bad sizes");
+    return TA_ERR_ARG;
+  }
+  if (N == 0 || C == 0) return TA_OK;
+  if (!rows_aligned(q, q_dtype, D, {qsb, qsh, qsn}) || !rows_aligned(S, s_dtype, D, {ssb, ssh, ssn})) {
+    set_error("ta_gather_dot: rows not aligned");
+    return TA_ERR_ARG;
+  }
+  return dispatch_dt_d<GatherDotRun>(q_dtype, D, s_dtype, q, qsb, qsh, qsn, S, ssb, ssh, ssn, cand,
+                                     (const int32_t*)nullptr, 0, 0, B, H, N, M, C, scale, out, (hipStream_t)stream);
+}
+
+extern "C" int ta_gather_dot_blocks(const void* q, const void* K, int dtype, int64_t qsb, int64_t qsh, int64_t qsn,
+                                    int64_t ksb, int64_t ksh, int64_t ksn, const int32_t* blk, int B, int H, int N,
+                                    int M, int NB, int block, int D, float scale, float* out, void* stream) {
+  if (B <= 0 || H <= 0 || N < 0 || M <= 0 || NB < 0 || !pow2(block)) {
+    set_error("ta_gather_dot_blocks: bad sizes");
+    return TA_ERR_ARG;
+  }
+  if (N == 0 || NB == 0) return TA_OK;
+  if (!rows_aligned(q, dtype, D, {qsb, qsh, qsn}) || !rows_aligned(K, dtype, D, {ksb, ksh, ksn})) {
+    set_error("ta_gather_dot_blocks: rows not aligned");
+    return TA_ERR_ARG;
+  }
+  return dispatch_dt_d<GatherDotRun>(dtype, D, dtype, q, qsb, qsh, qsn, K, ksb, ksh, ksn, (const int32_t*)nullptr, blk,
+                                     log2i(block), NB, B, H, N, M, NB * block, scale, out, (hipStream_t)stream);
+}

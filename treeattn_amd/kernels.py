@@ -1,0 +1,191 @@
+"""Tensor-level wrappers of the HIP kernels (one function per C-ABI entry point).
+
+All tensors must be on a gfx950 GPU.  Outputs are allocated here with torch (the library never
+allocates) unless the caller passes them in.  Work goes on torch's current stream.
+"""
+import math
+
+import torch
+
+from . import _lib as L
+
+
+def _ilog2(x):
+    x = int(x)
+    if x <= 0 or x & (x - 1):
+        raise ValueError('%d is not a power of two' % x)
+    return x.bit_length() - 1
+
+
+class TreeShape:
+    """Geometry of the segment tree over [0, T): leaf blocks of `leaf` keys, `arity` children per node.
+
+    Tree level j has nodes of leaf * arity**j keys (binary level l0 + j*log2(arity)); the top level is the
+    last with two or more nodes.  (leaf, arity) = (2, 2) is the reference's tree: binary levels 1..Lm,
+    Lm = log2(T) - 1 (seg.py:7-13, seg.py:127)."""
+
+    def __init__(self, T, leaf=2, arity=2):
+        self.T, self.leaf, self.arity = int(T), int(leaf), int(arity)
+        self.LT, self.l0, self.s = _ilog2(T), _ilog2(leaf), _ilog2(arity)
+        if self.l0 < 1 or self.s < 1:
+            raise ValueError('leaf and arity must be powers of two >= 2')
+        self.blevels = []
+        l = self.l0
+        while self.LT - l >= 1:
+            self.blevels.append(l)
+            l += self.s
+        self.n_levels = len(self.blevels)
+
+    def leaf_width(self, wmax):
+        """Width of the leaf-level beam the reference returns: w = min(wmax, C) level by level from the top,
+        C = arity - 1 at the top and arity * w + arity - 1 below (seg.py:61-66)."""
+        if self.n_levels == 0:
+            return 0
+        a = self.arity
+        C = a - 1
+        w = 0
+        for _ in range(self.n_levels):
+            w = min(wmax, C)
+            C = a * w + a - 1
+        return w
+
+    def alloc_levels(self, B, H, D, device, Tn=None):
+        Tn = self.T if Tn is None else Tn
+        return [torch.empty(B, H, Tn >> l, D, device=device, dtype=torch.float32) for l in self.blevels]
+
+
+# ----------------------------------------------------------------------------------------------- builder
+def level_sums(k, blevels, out=None, t_end=None, zero_sink=True):
+    """Node sums of binary levels `blevels` of keys k (B,H,T,D): list of (B,H,T>>l,D) float32."""
+    L.require_gpu(k)
+    B, H, T, D = k.shape
+    t_end = T if t_end is None else int(t_end)
+    if out is None:
+        out = [torch.zeros(B, H, T >> l, D, device=k.device, dtype=torch.float32) for l in blevels]
+    for o in out:
+        if o.stride(-1) != 1 or o.stride(-2) != D:
+            raise ValueError('level tensors need contiguous node rows')
+    ws = torch.empty(max(1, L.lib().ta_level_sums_workspace_size(B, H, t_end, D)) // 4 + 1, device=k.device,
+                     dtype=torch.float32)
+    sb, sh, sn = L.rows3(k)
+    L.call('ta_level_sums', L.ptr(k), L.dtype_code(k), sb, sh, sn, B, H, t_end, D, int(bool(zero_sink)),
+           len(blevels), L.ptr_array(out), L.i64_array([o.stride(0) for o in out]),
+           L.i64_array([o.stride(1) for o in out]), L.i32_array(list(blevels)), L.ptr(ws), ws.numel() * 4,
+           L.stream())
+    return out
+
+
+# ----------------------------------------------------------------------------------------------- descent
+def tree_descend(q, levels, tq, shape, wmax, out=None):
+    """Beam descent of queries q (B,H,Nq,D) at positions tq ((Nq,) shared or (B,Nq)) over pyramid `levels`
+    (tree levels 0..J of `shape`).  Returns ids int32, vld uint8, sct float32, each (B,H,Nq,wl)."""
+    L.require_gpu(q, tq)
+    B, H, Nq, D = q.shape
+    wl = shape.leaf_width(wmax)
+    if tq.dtype != torch.int32:
+        tq = tq.to(torch.int32)
+    tq = tq.contiguous()
+    tq_sb = 0 if tq.dim() == 1 else tq.stride(0)
+    if out is None:
+        ids = torch.empty(B, H, Nq, wl, device=q.device, dtype=torch.int32)
+        vld = torch.empty(B, H, Nq, wl, device=q.device, dtype=torch.uint8)
+        sct = torch.empty(B, H, Nq, wl, device=q.device, dtype=torch.float32)
+    else:
+        ids, vld, sct = out
+    if wl == 0 or Nq == 0:
+        return ids, vld, sct
+    sb, sh, sn = L.rows3(q)
+    L.call('ta_tree_descend', L.ptr(q), L.dtype_code(q), sb, sh, sn, B, H, Nq, D, L.ptr(tq), tq_sb,
+           len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
+           L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl,
+           L.ptr(ids), L.ptr(vld), L.ptr(sct), L.stream())
+    return ids, vld, sct
+
+
+# ----------------------------------------------------------------------------------------------- gather-dot
+def gather_dot(q, S, cand, scale):
+    """scale * q . S[clamp(cand)] in float32, canonical order.  q (b,H,N,dh), S (b,H,M,dh), cand (b,H,N,C)."""
+    L.require_gpu(q, S, cand)
+    b, H, N, D = q.shape
+    M, C = S.shape[2], cand.shape[-1]
+    cc = cand.to(torch.int32).contiguous()
+    out = torch.empty(b, H, N, C, device=q.device, dtype=torch.float32)
+    if N == 0 or C == 0:
+        return out
+    qs, ss = L.rows3(q), L.rows3(S)
+    L.call('ta_gather_dot', L.ptr(q), L.dtype_code(q), *qs, L.ptr(S), L.dtype_code(S), *ss, L.ptr(cc), b, H, N, M, C,
+           D, float(scale), L.ptr(out), L.stream())
+    return out
+
+
+def gather_dot_blocks(q, K, blk, block, scale=1.0, out=None):
+    """Leaf-block gather-dot: out[..., c*block + j] = scale * q . K[blk[..., c]*block + j]."""
+    L.require_gpu(q, K, blk)
+    if q.dtype != K.dtype:
+        raise TypeError('q and K must have the same dtype')
+    b, H, N, D = q.shape
+    M = K.shape[2]
+    NB = blk.shape[-1]
+    bb = blk if (blk.dtype == torch.int32 and blk.is_contiguous()) else blk.to(torch.int32).contiguous()
+    if out is None:
+        out = torch.empty(b, H, N, NB * block, device=q.device, dtype=torch.float32)
+    L.call('ta_gather_dot_blocks', L.ptr(q), L.ptr(K), L.dtype_code(q), *L.rows3(q), *L.rows3(K), L.ptr(bb), b, H, N,
+           M, NB, int(block), D, float(scale), L.ptr(out), L.stream())
+    return out
+
+
+# ----------------------------------------------------------------------------------------------- attention
+def sparse_attn_fwd(q, k, v, cand, scale):
+    """Softmax attention over candidate positions (-1 unused).  Returns (out (b,H,T,dh) in v's dtype, lse)."""
+    L.require_gpu(q, k, v, cand)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError('q, k, v must share a dtype')
+    b, H, T, D = q.shape
+    KC = cand.shape[-1]
+    cc = cand.to(torch.int32).contiguous()
+    out = torch.empty(b, H, T, D, device=q.device, dtype=v.dtype)
+    lse = torch.empty(b, H, T, device=q.device, dtype=torch.float32)
+    L.call('ta_sparse_attn_fwd', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k), *L.rows3(v),
+           L.ptr(cc), b, H, T, KC, D, float(scale), L.ptr(out), L.ptr(lse), L.stream())
+    return out, lse
+
+
+def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=None, keys=None, nsplit=1, ws=None):
+    """Attention over selected leaf blocks + own leaf block + static keys (neighbours off).
+    q (B,H,Nq,D) strided; k, v (B,H,Tk,D) strided; tq (Nq,) or (B,Nq) int32; ids/vld (B,H,Nq,wl);
+    n_tree (B,H,Nq) int32 or None.  Returns (out, lse, keys)."""
+    L.require_gpu(q, k, v, tq, ids, vld)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError('q, k, v must share a dtype')
+    B, H, Nq, D = q.shape
+    wl = ids.shape[-1]
+    tq32 = tq if tq.dtype == torch.int32 else tq.to(torch.int32)
+    tq32 = tq32.contiguous()
+    tq_sb = 0 if tq32.dim() == 1 else tq32.stride(0)
+    if out is None:
+        out = torch.empty(B, H, Nq, D, device=q.device, dtype=v.dtype)
+    nt = None
+    if n_tree is not None:
+        nt = n_tree if (n_tree.dtype == torch.int32 and n_tree.is_contiguous()) else n_tree.to(torch.int32).contiguous()
+    if nsplit > 1 and ws is None:
+        ws = torch.empty(L.lib().ta_seg_attn_workspace_size(B, H, Nq, D, nsplit) // 4 + 1, device=q.device,
+                         dtype=torch.float32)
+    ws_bytes = ws.numel() * 4 if ws is not None else 0
+    L.call('ta_seg_attn_fwd', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k), *L.rows3(v),
+           B, H, Nq, D, k.shape[2], L.ptr(tq32), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(nt), wl, int(leaf), int(local),
+           float(scale), L.ptr(out), out.stride(0), out.stride(1), out.stride(2), L.ptr(lse), L.ptr(keys),
+           int(nsplit), L.ptr(ws), ws_bytes, L.stream())
+    return out, lse, keys
+
+
+# ----------------------------------------------------------------------------------------------- decode append
+def kv_append(k_new, v_new, Kc, Vc, t_pos, levels, leaf, arity):
+    """Write k_new, v_new (B,H,D) at row t_pos[b] of the caches (B,H,Tcap,D) and form the completed nodes."""
+    L.require_gpu(k_new, v_new, Kc, Vc, t_pos)
+    B, H, Tcap, D = Kc.shape
+    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or Kc.stride() != Vc.stride():
+        raise ValueError('kv_append: unsupported layout')
+    L.call('ta_kv_append', L.ptr(k_new), L.ptr(v_new), L.dtype_code(Kc), k_new.stride(0), k_new.stride(1),
+           v_new.stride(0), v_new.stride(1), L.ptr(Kc), L.ptr(Vc), Kc.stride(0), Kc.stride(1), Kc.stride(2), B, H, D,
+           Tcap, L.ptr(t_pos), len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
+           L.i64_array([t.stride(1) for t in levels]), _ilog2(leaf), _ilog2(arity), L.stream())
