@@ -1,0 +1,271 @@
+#!/usr/bin/env python
+"""Benchmark of the segment-tree sparse attention decode on one MI355X.
+
+Workload (the configuration the headline metric is quoted on): GPT 12 layers, d_model 768, 12 heads x 64,
+vocab 50304, random-init N(0, 0.02) (seed 3), bf16.  32 sequences, each prefilled with 32768 uniform random
+token ids (seed 3) through the model itself (sparse attention included; not timed), then greedy decode with
+the segment tree: leaf block 64, binary, top-k 32 leaves + own leaf block + static keys, neighbours off.
+Cache capacity Tcap = 65536.  A step decodes one token for every sequence; the whole step (12 layers: GEMMs,
+beam descent, cache append with node formation, sparse attention, logits, argmax) is one captured HIP graph.
+
+    python bench.py [--steps K] [--warmup W]
+
+Prints one JSON line: value = decoded tokens/s for the batch (32 tokens per step), the roofline of the
+dominant kernel (the decode attention, HBM-bound) measured live with HIP events, the CPU baseline (the
+oracle engine decoding one of the 32 sequences from the same state on the host), and the isolated
+gather-dot (8x12x4096x64 bf16, 16 blocks of 64 keys per query) as GB/s of 8 TB/s.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=64)
+    ap.add_argument('--warmup', type=int, default=8)
+    ap.add_argument('--batch', type=int, default=32)
+    ap.add_argument('--context', type=int, default=32768)
+    ap.add_argument('--tcap', type=int, default=65536)
+    ap.add_argument('--layers', type=int, default=12)
+    ap.add_argument('--embd', type=int, default=768)
+    ap.add_argument('--heads', type=int, default=12)
+    ap.add_argument('--vocab', type=int, default=50304)
+    ap.add_argument('--leaf', type=int, default=64)
+    ap.add_argument('--arity', type=int, default=2)
+    ap.add_argument('--topk', type=int, default=32)
+    ap.add_argument('--prefill-chunk', type=int, default=8)
+    ap.add_argument('--cpu-seconds', type=float, default=20.0, help='budget of the CPU baseline leg')
+    ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
+    ap.add_argument('--no-gather-dot', action='store_true', help='skip the isolated gather-dot leg')
+    ap.add_argument('--kernel-iters', type=int, default=50)
+    return ap.parse_args()
+
+
+def log(msg):
+    print('[bench] ' + msg, file=sys.stderr, flush=True)
+
+
+def descent_nodes(t, shape, wmax):
+    """Nodes the descent kernel scores for a query at position t (start level: all complete nodes; below:
+    arity * kept + complete left siblings)."""
+    a = shape.arity
+    start = 0
+    for j in range(shape.n_levels - 1, -1, -1):
+        if (t >> shape.blevels[j]) > wmax:
+            start = j
+            break
+    C = t >> shape.blevels[start]
+    total = C
+    nk = min(C, wmax)
+    for j in range(start - 1, -1, -1):
+        m = t >> shape.blevels[j]
+        C = a * nk + (m % a)
+        total += C
+        nk = min(C, wmax)
+    return total
+
+
+def time_launches(fn, iters):
+    """Average duration (us) of fn's GPU work, from HIP events recorded on the launching stream."""
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for a, b in evs:
+        a.record(st)
+        fn()
+        b.record(st)
+    torch.cuda.synchronize()
+    return 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / iters
+
+
+def gather_dot_leg(args):
+    from treeattn_amd import kernels as K
+    B, H, T, D, NB, blk = 8, 12, 4096, 64, 16, 64
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16)
+    nvalid = torch.clamp(torch.arange(T) // blk, min=1).view(1, 1, T, 1).float()
+    idx = (torch.rand(B, H, T, NB, generator=g) * nvalid).floor().to(torch.int32)
+    q, k, idx = q.cuda(), k.cuda(), idx.cuda()
+    out = torch.empty(B, H, T, NB * blk, device='cuda')
+    for _ in range(3):
+        K.gather_dot_blocks(q, k, idx, blk, 1.0, out=out)
+    us = time_launches(lambda: K.gather_dot_blocks(q, k, idx, blk, 1.0, out=out), 20)
+    nbytes = q.numel() * 2 + k.numel() * 2 + idx.numel() * 4 + out.numel() * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {'workload': 'gather_dot Q,K (8,12,4096,64) bf16, 16 blocks of 64 per query, out fp32 (8,12,4096,1024)',
+            'bytes_per_call': nbytes, 'avg_us': round(us, 1), 'GB/s': round(gbs, 1),
+            'frac_of_hbm': round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s):
+    """The oracle engine (CPU restatement of engine.py) decodes sequence 0 from the GPU's state."""
+    from oracle.engine_ref import DecoderRef, SegStateRef
+    from treeattn_amd import kernels as K
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    Wc = dict(wte=W['wte'].cpu(), wpe=W['wpe'].cpu(), ln_f=W['ln_f'].cpu(),
+              layers=[{k: v.cpu() for k, v in L.items()} for L in W['layers']])
+    ref = DecoderRef(Wc, args.layers, args.heads, args.embd, args.tcap, 'seg', cfg, act_dtype=torch.bfloat16,
+                     sel_mode='faithful')
+    for i, st in enumerate(dec.states):
+        ref.states[i].fill(st.K[0:1].float().cpu(), st.V[0:1].float().cpu())
+    tok = int(tok_now[0])
+    t = int(t_now)
+    # GPU: decode the same steps eagerly for the parity check of sequence 0
+    times, errs, toks_same = [], [], 0
+    tg = tok_now.clone()
+    n = 0
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        lc, _ = ref.step(tok, t)
+        dt = time.perf_counter() - t0
+        lg, _ = dec.step(tg, t)
+        lg0 = lg[0].float().cpu()
+        errs.append((lc - lg0).abs().max().item())
+        nc = int(lc.argmax())
+        ng = int(K.argmax_rows(lg)[0])
+        toks_same += int(nc == ng)
+        if n > 0:              # the first step is the warm-up
+            times.append(dt)
+        tok = nc
+        tg = K.argmax_rows(lg)
+        tg[0] = nc
+        t += 1
+        n += 1
+        if n >= 3 and (time.perf_counter() - t_start > budget_s or n >= 64):
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {'value': round(1.0 / med, 3), 'unit': 'tokens/s', 'cores': ncores, 'kind': 'port',
+            'sample': '%d greedy decode steps of 1 of the 32 sequences from the GPU state at position %d, '
+                      'oracle engine on the host (torch CPU, bf16 activations, fp32 selection/attention); '
+                      'median s/token; a 32-sequence batch takes 32x as long on the host' % (len(times), int(t_now)),
+            'parity_seq0': {'max_abs_logit_diff': round(max(errs), 5), 'steps': n,
+                            'same_greedy_token': toks_same}}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print('bench.py: this build measures one GPU; --gpus %d is not supported (run with --gpus 1)' % args.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from treeattn_amd import kernels as K
+    from treeattn_amd.config import Config
+    from treeattn_amd.engine import Decoder, weights_from_ours
+    from treeattn_amd.model import GPT
+
+    B, T0, Tcap = args.batch, args.context, args.tcap
+    H, C = args.heads, args.embd
+    dh = C // H
+    cfg = Config(vocab_size=args.vocab, seq_len=Tcap, n_layer=args.layers, n_head=H, n_embd=C, attn='seg',
+                 wmax=args.topk, beam=args.topk, beam_mode='fixed', neighbors=False, leaf=args.leaf,
+                 arity=args.arity, local=3)
+    log('init model (seed 3)')
+    torch.manual_seed(3)
+    model = GPT(cfg)
+    sd = {k: v.detach().to(torch.bfloat16).cuda() for k, v in model.state_dict().items()}
+    del model
+    W = weights_from_ours(sd, cfg)
+    g = torch.Generator().manual_seed(3)
+    idx = torch.randint(0, args.vocab, (B, T0), generator=g)
+    dec = Decoder(W, args.layers, H, C, Tcap, 'seg', cfg, 'cuda', batch=B, dtype=torch.bfloat16)
+    log('prefill %d x %d tokens' % (B, T0))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = dec.prefill(idx.cuda(), chunk=args.prefill_chunk)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    log('prefill %.1f s; capture decode step' % prefill_s)
+    tok = K.argmax_rows(logits)
+    dec.capture(tok, T0)
+    for _ in range(args.warmup):
+        dec.replay()
+    torch.cuda.synchronize()
+    log('timed decode: %d steps' % args.steps)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dec.replay()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_step = el / args.steps * 1000.0
+    value = B * args.steps / el
+    t_now = T0 + args.warmup + args.steps
+    log('%.3f ms/step, %.0f tokens/s' % (ms_step, value))
+
+    # ---- dominant kernel: the decode attention of one layer over the live state, HIP events on its stream
+    st = dec.states[0]
+    sh = st.shape
+    t_last = t_now - 1
+    gq = torch.Generator().manual_seed(11)
+    q = torch.randn(B, H, 1, dh, generator=gq).to(torch.bfloat16).cuda()
+    tpos = torch.full((B,), t_last, dtype=torch.int32, device='cuda')
+    sc = dec.scratch
+    ids, vld, sct = K.tree_descend(q, st.levels, tpos.view(B, 1), sh, cfg.wmax)
+    n_tree = torch.full((B, H, 1), min(max(cfg.beam, 2), cfg.wmax), dtype=torch.int32, device='cuda')
+    out = torch.empty(B, H, 1, dh, device='cuda', dtype=torch.bfloat16)
+    keys = torch.empty(B, H, 1, device='cuda')
+
+    def attn():
+        K.seg_attn(q, st.K, st.V, tpos.view(B, 1), ids, vld, n_tree, sh.leaf, cfg.local, 1.0 / math.sqrt(dh),
+                   out=out, keys=keys, nsplit=sc.nsplit, ws=sc.ws)
+
+    def descend():
+        K.tree_descend(q, st.levels, tpos.view(B, 1), sh, cfg.wmax, out=(sc.ids, sc.vld, sc.sct))
+
+    for _ in range(3):
+        attn()
+        descend()
+    attn_us = time_launches(attn, args.kernel_iters)
+    desc_us = time_launches(descend, args.kernel_iters)
+    keys_total = float(keys.sum())
+    elem = 2
+    wl = ids.shape[-1]
+    attn_bytes = keys_total * dh * elem * 2 + B * H * (2 * dh * elem + wl * 5 + 4)
+    attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
+    desc_bytes = B * H * (descent_nodes(t_last, sh, cfg.wmax) * dh * 4 + dh * elem + wl * 9)
+    desc_gbs = desc_bytes / (desc_us * 1e-6) / 1e9
+    log('attention %.1f us (%.0f GB/s), descent %.1f us' % (attn_us, attn_gbs, desc_us))
+
+    res = {
+        'metric': 'sparse-attn decode tokens/s @bs32x32k; gather-dot GB/s as % of 8 TB/s HBM',
+        'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
+        'ms_per_step': round(ms_step, 4), 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+        'dtype': 'bf16', 'data': 'synthetic (random-init weights seed 3, uniform random token ids seed 3)',
+        'config': {'workload': 'KV-cache decode engine (config 4): GPT 12L/768/12H, vocab 50304, bf16, batch %d x '
+                               '%d-token prefilled context, greedy decode, leaf %d, arity %d, top-k %d, Tcap %d'
+                               % (B, T0, args.leaf, args.arity, args.topk, Tcap),
+                   'batch': B, 'context': T0, 'leaf': args.leaf, 'arity': args.arity, 'topk': args.topk,
+                   'tcap': Tcap, 'prefill_s': round(prefill_s, 2)},
+        'roofline': {'bound': 'hbm', 'kernel': 'attn_kernel<bf16_t, 64, true> (split decode attention, one layer)',
+                     'achieved': round(attn_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                     'frac': round(attn_gbs / HBM_PEAK_GBS, 4), 'traffic': None,
+                     'bytes_per_launch': int(attn_bytes), 'avg_us': round(attn_us, 2),
+                     'keys_per_query': round(keys_total / (B * H), 1)},
+        'kernels': {'descend_us': round(desc_us, 2), 'descend_GB/s': round(desc_gbs, 1),
+                    'descend_bytes': int(desc_bytes)},
+    }
+    if not args.no_gather_dot:
+        log('gather-dot leg')
+        res['gather_dot'] = gather_dot_leg(args)
+    if not args.no_cpu:
+        log('cpu baseline leg (oracle engine, one sequence)')
+        res['cpu_baseline'] = cpu_baseline_leg(args, cfg, W, dec, int(dec.g_t[0]), dec.g_tok, args.cpu_seconds)
+    else:
+        res['cpu_baseline'] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == '__main__':
+    main()

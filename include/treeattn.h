@@ -112,14 +112,14 @@ int ta_gather_dot_blocks(const void* q, const void* K, int dtype,
 /*
  * Softmax attention of each query over an explicit candidate list (replaces fastseg.py:173-177
  * sparse_attn forward, its kernel fastseg.py:50-78 and the fallback fastseg.py:134-141).
- * q, k, v: (B,H,T,D) same dtype; cand: (B,H,T,KC) int32 contiguous, -1 = unused, duplicates counted as
- * given; positions >= T are treated as unused.  out: (B,H,T,D) contiguous in the input dtype; lse: (B,H,T)
+ * q: (B,H,T,D), k, v: (B,H,Tk,D), same dtype; cand: (B,H,T,KC) int32 contiguous, -1 = unused, duplicates
+ * counted as given; positions >= Tk are treated as unused.  out: (B,H,T,D) contiguous in the input dtype; lse: (B,H,T)
  * float32 (may be NULL).  Softmax in float32; a row with no valid candidate gives out = 0, lse = -1e30.
  */
 int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                        int64_t qsb, int64_t qsh, int64_t qst, int64_t ksb, int64_t ksh, int64_t kst,
                        int64_t vsb, int64_t vsh, int64_t vst,
-                       const int32_t* cand, int B, int H, int T, int KC, int D, float scale,
+                       const int32_t* cand, int B, int H, int T, int Tk, int KC, int D, float scale,
                        void* out, float* lse, void* stream);
 
 /*
@@ -132,8 +132,11 @@ int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype,
  * each position once.  q: (B,H,Nq,D) with strides; k, v: (B,H,Tk,D) with strides (the whole sequence or a
  * KV cache); positions outside [0, Tk) are never read (a query with t >= Tk attends nothing).  ids/vld: (B,H,Nq,wl) contiguous.  out: (B,H,Nq,D) in the input dtype with strides; lse:
  * (B,H,Nq) float32 or NULL; keys: (B,H,Nq) float32 number of keys attended, or NULL.
- * nsplit > 1 splits every query's keys over nsplit wavefronts and merges them (for few queries with
- * many keys, as in decode); ws must then hold ta_seg_attn_workspace_size(...) bytes.
+ * nsplit > 1 splits every query's keys over nsplit wavefronts (for few queries with many keys, as in
+ * decode); the last split to finish for a query merges the partials.  ws must then hold
+ * ta_seg_attn_workspace_size(...) bytes and be zero-filled before its first use; every call leaves its
+ * arrival counters at zero again, so one workspace serves any number of calls.  Calls that share a
+ * workspace must not run concurrently.
  */
 int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int nsplit);
 int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype,
@@ -159,6 +162,14 @@ int ta_kv_append(const void* k_new, const void* v_new, int dtype,
                  int B, int H, int D, int Tcap, const int32_t* t_pos,
                  int n_levels, float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh,
                  int leaf_log2, int arity_log2, void* stream);
+
+/*
+ * Row-wise argmax for greedy decoding (replaces logits.argmax(-1) of the reference's greedy loop,
+ * phase2.py:51-66): out[r] = the first index of the largest value of x[r, 0:n].  x: rows of n elements of
+ * dtype with row stride `stride`; out: int64.
+ */
+int ta_argmax_rows(const void* x, int dtype, int64_t rows, int64_t n, int64_t stride, int64_t* out,
+                   void* stream);
 
 #ifdef __cplusplus
 }

@@ -199,3 +199,16 @@ def test_kv_append_matches_state_add():
     assert torch.equal(Kc.cpu(), ref.K) and torch.equal(Vc.cpu(), ref.V)
     for j, l in enumerate(shape.blevels):
         assert torch.equal(levels[j].cpu(), ref.raw[l]), j
+
+
+def test_sparse_attn_decode_shape():
+    """One query row per (b, h) over a longer key cache (Tk > T), as in decode (regression: keys past the
+    number of query rows were once treated as unused)."""
+    B, H, Tk, KC, D = 2, 3, 300, 40, 64
+    q = rnd(B, H, 1, D, seed=40, dtype=torch.bfloat16)
+    k, v = rnd(B, H, Tk, D, seed=41, dtype=torch.bfloat16), rnd(B, H, Tk, D, seed=42, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(43)
+    cand = torch.randint(-1, Tk, (B, H, 1, KC), generator=g)
+    out, _ = K.sparse_attn_fwd(q.to(DEV), k.to(DEV), v.to(DEV), cand.to(DEV), 0.125)
+    want = sparse_attn_ref(q, k, v, cand, 0.125)
+    assert (out.cpu().float() - want.float()).abs().max().item() < 2e-2

@@ -35,8 +35,8 @@ SIGNATURES = {
     'ta_gather_dot_blocks': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp,
                                      c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_vp]),
     'ta_sparse_attn_fwd': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
-                                   c_i64, c_i64, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_vp,
-                                   c_vp]),
+                                   c_i64, c_i64, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp,
+                                   c_vp, c_vp]),
     'ta_seg_attn_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     'ta_seg_attn_fwd': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                 c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32,
@@ -45,6 +45,7 @@ SIGNATURES = {
     'ta_kv_append': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
                              c_i32, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32,
                              c_i32, c_vp]),
+    'ta_argmax_rows': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_vp]),
 }
 
 _lib = None

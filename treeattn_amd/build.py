@@ -21,6 +21,7 @@ SOURCES = {
     'abi.hip': [],
     'select.hip': ['-ffp-contract=off'],
     'attend.hip': [],
+    'sample.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

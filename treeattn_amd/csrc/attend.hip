@@ -6,7 +6,8 @@
 // K and V rows (a leaf block is a run of consecutive rows, so a chunk reads contiguous memory), keeps a
 // running max/sum (online softmax, float32) and its own weighted V accumulator; the wavefront reduces
 // the accumulators once at the end (reduce-scatter over lanes).  With nsplit > 1 the partial (max, sum,
-// accumulator) of every split goes to a workspace and a merge kernel combines them.
+// accumulator) of every split goes to a workspace; the split that finishes last for a query (a per-query
+// arrival counter, reset by that split) merges them, so one launch does the whole attention.
 //
 // Reference functions replaced: fastseg.py:50-78 (_attn_fwd), fastseg.py:134-177 (sparse_attn),
 // fastseg.py:367-383 (candidate assembly + dedupe_fast), engine.py:107-119 (decode attention),
@@ -39,7 +40,8 @@ struct AttnParams {
   int64_t osb, osh, osn;
   float* lse;
   float* keys;
-  float* ws;
+  float* ws;           // partials (query, split, D + 2)
+  unsigned* cnt;       // per-query arrival counters, zero between launches
 };
 
 constexpr float kNegBig = -1e30f;
@@ -88,7 +90,8 @@ struct LaneReduce {
   }
 };
 
-template <typename T, int D>
+// SPLIT: several wavefronts per query with the in-kernel merge (decode); otherwise one wavefront per query.
+template <typename T, int D, bool SPLIT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   constexpr int LPK = D > 64 ? D / 64 : 1;  // lanes per key
   constexpr int DPL = D / LPK;              // dims per lane
@@ -206,7 +209,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   const float L = wave_sum(l);
   const int dim0 = Red::run(acc, lane) + part * DPL;
   const bool writer = (lane & Red::dup_mask()) == 0;
-  if (p.nsplit == 1) {
+  if constexpr (!SPLIT) {
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     if (writer) {
       T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh + n * p.osn;
@@ -228,40 +231,39 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
       part_ws[1] = L;
       if (split == 0 && p.keys) p.keys[qi] = (float)N;
     }
-  }
-}
-
-// Combine the nsplit partials of every query: out = sum_s acc_s e^(m_s - M) / sum_s L_s e^(m_s - M).
-template <typename T, int D>
-__global__ __launch_bounds__(128) void merge_kernel(const float* __restrict__ ws, int nsplit, int H, int Nq,
-                                                    void* out, int64_t osb, int64_t osh, int64_t osn,
-                                                    float* __restrict__ lse) {
-  const int64_t qi = blockIdx.x;
-  const int n = (int)(qi % Nq);
-  const int bh = (int)(qi / Nq);
-  const int b = bh / H, h = bh % H;
-  const float* base = ws + qi * nsplit * (D + 2);
-  float M = kNegBig;
-  for (int s = 0; s < nsplit; ++s) {
-    const float* ps = base + s * (D + 2);
-    if (ps[1] > 0.0f) M = fmaxf(M, ps[0]);
-  }
-  float L = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float* ps = base + s * (D + 2);
-    if (ps[1] > 0.0f) L += ps[1] * __expf(ps[0] - M);
-  }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  T* orow = reinterpret_cast<T*>(out) + b * osb + h * osh + n * osn;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float a = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
+    // publish the partial, count arrivals; the last split of this query merges all of them
+    __threadfence();
+    int last = 0;
+    if (lane == 0) last = atomicAdd(p.cnt + qi, 1u) == (unsigned)(p.nsplit - 1);
+    last = __shfl(last, 0, kWave);
+    if (!last) return;
+    __threadfence();
+    const float* base = p.ws + qi * p.nsplit * (D + 2);
+    float M = kNegBig;
+    for (int s = 0; s < p.nsplit; ++s) {
       const float* ps = base + s * (D + 2);
-      if (ps[1] > 0.0f) a += ps[2 + d] * __expf(ps[0] - M);
+      if (ps[1] > 0.0f) M = fmaxf(M, ps[0]);
     }
-    orow[d] = from_f32<T>(a * inv);
+    float Lt = 0.0f;
+    for (int s = 0; s < p.nsplit; ++s) {
+      const float* ps = base + s * (D + 2);
+      if (ps[1] > 0.0f) Lt += ps[1] * __expf(ps[0] - M);
+    }
+    const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
+    T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh + n * p.osn;
+    for (int d = lane; d < D; d += kWave) {
+      float a = 0.0f;
+      for (int s = 0; s < p.nsplit; ++s) {
+        const float* ps = base + s * (D + 2);
+        if (ps[1] > 0.0f) a += ps[2 + d] * __expf(ps[0] - M);
+      }
+      orow[d] = from_f32<T>(a * inv);
+    }
+    if (lane == 0) {
+      if (p.lse) p.lse[qi] = Lt > 0.0f ? M + __logf(Lt) : kNegBig;
+      p.cnt[qi] = 0u;  // ready for the next launch
+    }
   }
-  if (threadIdx.x == 0 && lse) lse[qi] = L > 0.0f ? M + __logf(L) : kNegBig;
 }
 
 // ----------------------------------------------------------------------------------------- decode append
@@ -354,13 +356,12 @@ int launch_attn(const AttnParams& p, int B, hipStream_t st) {
   const size_t lds = (size_t)waves * (D + wl_pad + kWave) * sizeof(float);
   const int64_t nw = (int64_t)p.Nq * p.nsplit;
   dim3 grid((unsigned)((nw + waves - 1) / waves), B * p.H);
-  hipLaunchKernelGGL((attn_kernel<T, D>), grid, dim3(waves * kWave), lds, st, p);
-  int rc = check_launch("attn_kernel");
-  if (rc || p.nsplit == 1) return rc;
-  dim3 mg((unsigned)((int64_t)B * p.H * p.Nq));
-  hipLaunchKernelGGL((merge_kernel<T, D>), mg, dim3(D < 128 ? D : 128), 0, st, p.ws, p.nsplit, p.H, p.Nq, p.out,
-                     p.osb, p.osh, p.osn, p.lse);
-  return check_launch("merge_kernel");
+  if (p.nsplit > 1) {
+    hipLaunchKernelGGL((attn_kernel<T, D, true>), grid, dim3(waves * kWave), lds, st, p);
+  } else {
+    hipLaunchKernelGGL((attn_kernel<T, D, false>), grid, dim3(waves * kWave), lds, st, p);
+  }
+  return check_launch("attn_kernel");
 }
 
 int dispatch_attn(int dt, int D, const AttnParams& p, int B, hipStream_t st) {
@@ -388,9 +389,9 @@ using namespace ta;
 
 extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
                                   int64_t qst, int64_t ksb, int64_t ksh, int64_t kst, int64_t vsb, int64_t vsh,
-                                  int64_t vst, const int32_t* cand, int B, int H, int T, int KC, int D, float scale,
-                                  void* out, float* lse, void* stream) {
-  if (B <= 0 || H <= 0 || T < 0 || KC < 0) {
+                                  int64_t vst, const int32_t* cand, int B, int H, int T, int Tk, int KC, int D,
+                                  float scale, void* out, float* lse, void* stream) {
+  if (B <= 0 || H <= 0 || T < 0 || Tk < 0 || KC < 0) {
     set_error("ta_sparse_attn_fwd: bad sizes");
     return TA_ERR_ARG;
   }
@@ -403,7 +404,7 @@ extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, i
   p.q = q; p.qsb = qsb; p.qsh = qsh; p.qsn = qst;
   p.k = k; p.ksb = ksb; p.ksh = ksh; p.kst = kst;
   p.v = v; p.vsb = vsb; p.vsh = vsh; p.vst = vst;
-  p.H = H; p.Nq = T; p.Tk = T;
+  p.H = H; p.Nq = T; p.Tk = Tk;
   p.cand = cand; p.KC = KC;
   p.leaf_log2 = 1;
   p.scale = scale;
@@ -413,9 +414,11 @@ extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, i
   return dispatch_attn(dtype, D, p, B, (hipStream_t)stream);
 }
 
+static int64_t counter_bytes(int B, int H, int Nq) { return (((int64_t)B * H * Nq * 4) + 255) / 256 * 256; }
+
 extern "C" int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int nsplit) {
   if (nsplit <= 1) return 0;
-  return (int64_t)B * H * Nq * nsplit * (D + 2) * (int64_t)sizeof(float);
+  return counter_bytes(B, H, Nq) + (int64_t)B * H * Nq * nsplit * (D + 2) * (int64_t)sizeof(float);
 }
 
 extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
@@ -460,7 +463,11 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
   p.scale = scale;
   p.nsplit = nsplit;
   p.out = out; p.osb = osb; p.osh = osh; p.osn = osn;
-  p.lse = lse; p.keys = keys; p.ws = ws;
+  p.lse = lse; p.keys = keys;
+  if (nsplit > 1) {
+    p.cnt = reinterpret_cast<unsigned*>(ws);
+    p.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + counter_bytes(B, H, Nq));
+  }
   return dispatch_attn(dtype, D, p, B, (hipStream_t)stream);
 }
 

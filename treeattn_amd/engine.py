@@ -1,0 +1,364 @@
+"""Token-by-token decoding with a key cache (engine.py of the reference), on the GPU.
+
+Keeps the reference's API -- SegState(cfg, Tcap, H, dh, dev) with add/fill/getU, seg_attend(state, pw, q, k,
+v, t, update=True) -> (out, keys), Decoder(W, n_layer, n_head, n_embd, Tcap, mode, cfg, dev) with reset()
+and step(tok, t) -> (logits, keys), weights_from_ours / weights_from_nanogpt -- and extends it:
+
+* batch: SegState(..., batch=B) and Decoder(..., batch=B); step(tok: LongTensor(B), t) -> logits (B, V);
+* dtype: the caches take the weights' dtype (bf16 models keep bf16 K/V; node sums are always float32);
+* tree shape: cfg.leaf / cfg.arity (the reference is leaf=2, arity=2);
+* Decoder.prefill(idx) fills every layer's cache from a prompt in one pass (the forward of the model over
+  the prompt, sparse attention included) and returns the last position's logits;
+* Decoder.greedy(n) decodes n tokens with the whole step captured in a HIP graph (no host syncs).
+
+Per layer and token the HIP kernels are: beam descent over the node sums (positions < t), the cache
+append of position t with the formation of every node it completes, and the split-key attention over
+the selected leaf blocks + own leaf block + static keys with its merge.  With neighbours on (the
+reference's default) the candidate list of engine.py:107-114 is built on the device and attended by the
+candidate-list kernel.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels as K
+from . import selection as SEL
+from .forest import gather_nodes
+
+
+def _ln(x, w):
+    return F.layer_norm(x, (x.shape[-1],), w, None, 1e-5)
+
+
+class SegState:
+    """Per-layer cache (engine.py:18-71): K, V (B,H,Tcap,dh) in the model dtype, node sums of every tree
+    level (float32), the leaves each earlier query found (neighbour borrowing) and the running key sum."""
+
+    def __init__(self, cfg, Tcap, H, dh, dev, batch=1, dtype=torch.float32):
+        SEL.check_supported(cfg)
+        self.cfg, self.Tcap, self.H, self.dh, self.B = cfg, Tcap, H, dh, batch
+        self.dev = torch.device(dev)
+        self.shape = SEL.cfg_shape(cfg, Tcap)
+        self.Lm = self.shape.blevels[-1] if self.shape.n_levels else 0
+        self.K = torch.zeros(batch, H, Tcap, dh, device=dev, dtype=dtype)
+        self.V = torch.zeros(batch, H, Tcap, dh, device=dev, dtype=dtype)
+        self.levels = [torch.zeros(batch, H, Tcap >> l, dh, device=dev) for l in self.shape.blevels]
+        NS = cfg.nb_store
+        self.st_leaf = torch.zeros(batch, H, Tcap, NS, dtype=torch.int32, device=dev)
+        self.st_score = torch.zeros(batch, H, Tcap, NS, device=dev)
+        self.st_ok = torch.zeros(batch, H, Tcap, NS, dtype=torch.bool, device=dev)
+        self.ksum = torch.zeros(batch, H, dh, device=dev)
+
+    def level_of(self, l):
+        try:
+            return self.levels[self.shape.blevels.index(l)]
+        except ValueError:
+            raise KeyError('binary level %d is not a tree level of this cache' % l) from None
+
+    def getU(self, l, cand):
+        """Node vectors of `cand` at binary level l (engine.py:35-39)."""
+        return gather_nodes(self.level_of(l), cand)
+
+    def _tpos(self, t):
+        if torch.is_tensor(t):
+            return t.to(device=self.dev, dtype=torch.int32).reshape(self.B)
+        return torch.full((self.B,), int(t), dtype=torch.int32, device=self.dev)
+
+    def add(self, t, k, v):
+        """Store position t (k, v: (B,H,dh)) and form the nodes it completes (engine.py:41-55)."""
+        K.kv_append(k.to(self.K.dtype), v.to(self.V.dtype), self.K, self.V, self._tpos(t), self.levels,
+                    self.shape.leaf, self.shape.arity)
+        self.ksum += k.float()
+
+    def fill(self, K_, V_, t_end=None):
+        """Load a whole context (engine.py:57-71).  K_, V_: (B,H,T,dh) with T <= Tcap."""
+        T = K_.shape[2]
+        self.K[:, :, :T].copy_(K_)
+        self.V[:, :, :T].copy_(V_)
+        t_end = T if t_end is None else t_end
+        SEL.build_pyramid(self.K, self.shape, t_end=t_end, out=self.levels)
+        self.ksum = K_[:, :, :t_end].float().sum(2)
+
+
+class DenseState:
+    """Dense cached attention, the comparison baseline of the reference (engine.py:74-81)."""
+
+    def __init__(self, Tcap, H, dh, dev, batch=1, dtype=torch.float32):
+        self.K = torch.zeros(batch, H, Tcap, dh, device=dev, dtype=dtype)
+        self.V = torch.zeros(batch, H, Tcap, dh, device=dev, dtype=dtype)
+
+    def attend(self, q, k, v, t):
+        self.K[:, :, t], self.V[:, :, t] = k[:, :, 0], v[:, :, 0]
+        return F.scaled_dot_product_attention(q, self.K[:, :, :t + 1], self.V[:, :, :t + 1]), float(t + 1)
+
+
+class _Scratch:
+    """Per-decoder buffers reused by every layer of a step (fixed addresses, so a step can be captured)."""
+
+    def __init__(self, B, H, dh, wl, dev, nsplit, n_layer=1):
+        self.ids = torch.empty(B, H, 1, wl, dtype=torch.int32, device=dev)
+        self.vld = torch.empty(B, H, 1, wl, dtype=torch.uint8, device=dev)
+        self.sct = torch.empty(B, H, 1, wl, device=dev)
+        self.keys_all = torch.zeros(n_layer, B, H, 1, device=dev)
+        self.keys = self.keys_all[0]
+        self.nsplit = nsplit
+        nbytes = K.L.lib().ta_seg_attn_workspace_size(B, H, 1, dh, nsplit)
+        self.ws = torch.zeros(max(1, nbytes // 4 + 1), device=dev)  # arrival counters start at zero
+
+
+def decode_nsplit(B, H, wl, leaf):
+    """Split of each query's keys over wavefronts: aim for ~4 chunks of 64 keys per wavefront and at least
+    ~2048 wavefronts per launch (8 per CU)."""
+    chunks = max(1, (wl * leaf + leaf + 64) // 64)
+    ns = max(1, min(chunks // 4, 16))
+    while ns < 16 and B * H * ns < 2048 and ns * 2 <= chunks:
+        ns *= 2
+    return ns
+
+
+def _pw_budget(state, pw, q, t):
+    cfg, H = state.cfg, state.H
+    if cfg.beam_mode != 'pred':
+        return None
+    B = q.shape[0]
+    feats = [q.float(), torch.log(q.float().norm(dim=-1, keepdim=True) + 1e-6),
+             torch.eye(H, device=q.device).view(1, H, 1, H).expand(B, H, 1, H)]
+    if cfg.global_pool:
+        tt = state._tpos(t).float().clamp(min=1).view(B, 1, 1)
+        feats.append((state.ksum / tt).unsqueeze(2))
+    h = F.relu(F.linear(torch.cat(feats, -1), pw['w1'].float(), pw['b1'].float()))
+    return pw['classes'].to(q.device)[F.linear(h, pw['w2'].float(), pw['b2'].float()).argmax(-1)]
+
+
+@torch.no_grad()
+def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
+    """One decode step of one layer for every sequence, without host synchronisation.
+    q, k, v: (B,H,1,dh); t: int or (B,) positions.  Returns (out (B,H,1,dh), keys (B,H,1) float32)."""
+    cfg = state.cfg
+    B, H, _, dh = q.shape
+    leaf = state.shape.leaf
+    tpos = state._tpos(t)
+    scale = 1.0 / math.sqrt(dh)
+    lhat = _pw_budget(state, pw, q, t)
+    wl = state.shape.leaf_width(cfg.wmax)
+    if scratch is None:
+        scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
+    ids, vld, sct = K.tree_descend(q, state.levels, tpos.view(B, 1), state.shape, cfg.wmax,
+                                   out=(scratch.ids, scratch.vld, scratch.sct))
+    structural = (not cfg.neighbors) and lhat is None
+    if structural:
+        if update:
+            K.kv_append(k[:, :, 0], v[:, :, 0], state.K, state.V, tpos, state.levels, leaf, state.shape.arity)
+            if cfg.global_pool:
+                state.ksum += k[:, :, 0].float()
+        out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
+        n_tree = torch.full((B, H, 1), SEL.fixed_n_tree(cfg), dtype=torch.int32, device=q.device)
+        K.seg_attn(q, state.K, state.V, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out,
+                   keys=scratch.keys, nsplit=scratch.nsplit, ws=scratch.ws)
+        return out, scratch.keys
+    # reference-default mode: neighbour borrowing and/or the budget head -> candidate list
+    if lhat is None:
+        lhat = torch.full((B, H, 1), cfg.beam, dtype=torch.long, device=q.device)
+    idl, vb = ids.long(), vld.bool()
+    t64 = tpos.long().view(B, 1)
+    NS = cfg.nb_store
+    if state.shape.n_levels:
+        nid, match, nL = SEL.neighbor_pass(q.float(), state.levels[0], state.st_leaf, state.st_score, state.st_ok,
+                                           t64, cfg, leaf)
+    else:
+        Wn = cfg.nb_window
+        nid = torch.zeros(B, H, 1, Wn * NS, dtype=torch.long, device=q.device)
+        match = torch.zeros_like(nid, dtype=torch.bool)
+        nL = torch.zeros(B, H, 1, dtype=torch.long, device=q.device)
+    sel = SEL.finish(torch.where(vb, idl, torch.zeros_like(idl)), vb, nid, match, nL, lhat, cfg, leaf)
+    if update:
+        n = min(NS, wl)
+        bidx = torch.arange(B, device=q.device).view(B, 1)
+        hidx = torch.arange(H, device=q.device).view(1, H)
+        tt = t64.view(B, 1)
+        state.st_leaf[bidx, hidx, tt, :n] = ids[:, :, 0, :n].clamp(min=0)
+        state.st_score[bidx, hidx, tt, :n] = torch.where(vb[:, :, 0, :n], sct[:, :, 0, :n],
+                                                         torch.zeros_like(sct[:, :, 0, :n]))
+        state.st_ok[bidx, hidx, tt, :n] = vb[:, :, 0, :n]
+        K.kv_append(k[:, :, 0], v[:, :, 0], state.K, state.V, tpos, state.levels, leaf, state.shape.arity)
+        state.ksum += k[:, :, 0].float()
+    cand, keep, used = SEL.assemble(sel, t64, cfg, B, H)
+    out, _ = K.sparse_attn_fwd(q, state.K, state.V, torch.where(keep, cand, torch.full_like(cand, -1)), scale)
+    return out, keep.sum(-1).float()
+
+
+def seg_attend(state, pw, q, k, v, t, update=True):
+    """Reference signature (engine.py:84-120): returns (out, mean keys read per head) -- the mean is read
+    back to the host, as the reference does."""
+    out, keys = seg_attend_(state, pw, q, k, v, t, update)
+    return out, keys.float().mean().item()
+
+
+def weights_from_ours(sd, cfg):
+    """Engine weight dict from a model state_dict (engine.py:123-134)."""
+    W = dict(wte=sd['wte.weight'], wpe=sd['wpe.weight'], ln_f=sd['ln_f.weight'], layers=[])
+    for i in range(cfg.n_layer):
+        p = 'blocks.%d.' % i
+        L = dict(ln1=sd[p + 'ln1.weight'], c_attn=sd[p + 'attn.c_attn.weight'], c_proj=sd[p + 'attn.c_proj.weight'],
+                 ln2=sd[p + 'ln2.weight'], c_fc=sd[p + 'mlp.c_fc.weight'], c_mlp=sd[p + 'mlp.c_proj.weight'])
+        if cfg.beam_mode == 'pred':
+            L['pw'] = dict(w1=sd[p + 'attn.pred.0.weight'], b1=sd[p + 'attn.pred.0.bias'],
+                           w2=sd[p + 'attn.pred.2.weight'], b2=sd[p + 'attn.pred.2.bias'],
+                           classes=torch.tensor(list(cfg.beam_classes), device=sd['wte.weight'].device))
+        W['layers'].append(L)
+    return W
+
+
+def weights_from_nanogpt(sd, n_layer):
+    """Engine weight dict from a nanoGPT state_dict (engine.py:137-146)."""
+    sd = {k.replace('_orig_mod.', ''): v for k, v in sd.items()}
+    W = dict(wte=sd['transformer.wte.weight'], wpe=sd['transformer.wpe.weight'],
+             ln_f=sd['transformer.ln_f.weight'], layers=[])
+    for i in range(n_layer):
+        p = 'transformer.h.%d.' % i
+        W['layers'].append(dict(ln1=sd[p + 'ln_1.weight'], c_attn=sd[p + 'attn.c_attn.weight'],
+                                c_proj=sd[p + 'attn.c_proj.weight'], ln2=sd[p + 'ln_2.weight'],
+                                c_fc=sd[p + 'mlp.c_fc.weight'], c_mlp=sd[p + 'mlp.c_proj.weight']))
+    return W
+
+
+class Decoder:
+    """Layer loop around seg_attend (engine.py:149-177), batched and graph-capturable."""
+
+    def __init__(self, W, n_layer, n_head, n_embd, Tcap, mode, cfg=None, dev='cuda', batch=1, dtype=None):
+        self.W, self.nl, self.H, self.C, self.Tcap = W, n_layer, n_head, n_embd, Tcap
+        self.dh, self.mode, self.cfg, self.dev = n_embd // n_head, mode, cfg, torch.device(dev)
+        self.B = batch
+        self.dtype = dtype or W['wte'].dtype
+        self.graph = None
+        self.reset()
+
+    def reset(self):
+        B, H, dh = self.B, self.H, self.dh
+        if self.mode == 'seg':
+            self.states = [SegState(self.cfg, self.Tcap, H, dh, self.dev, B, self.dtype) for _ in range(self.nl)]
+            sh = self.states[0].shape
+            wl = sh.leaf_width(self.cfg.wmax)
+            self.scratch = _Scratch(B, H, dh, wl, self.dev, decode_nsplit(B, H, wl, sh.leaf), self.nl)
+        else:
+            self.states = [DenseState(self.Tcap, H, dh, self.dev, B, self.dtype) for _ in range(self.nl)]
+        self.graph = None
+
+    # ------------------------------------------------------------------------------------------ one step
+    def _forward_step(self, tok, tpos):
+        """tok (B,) long, tpos (B,) long on the device -> logits (B, V).  Keys attended per (layer, sequence,
+        head) are left in self.scratch.keys_all."""
+        W, H, C, dh, B = self.W, self.H, self.C, self.dh, self.B
+        x = (W['wte'][tok] + W['wpe'][tpos]).view(B, 1, C)
+        for i, L in enumerate(W['layers']):
+            q, k, v = F.linear(_ln(x, L['ln1']), L['c_attn']).split(C, -1)
+            q, k, v = [a.view(B, 1, H, dh).transpose(1, 2) for a in (q, k, v)]
+            if self.mode == 'seg':
+                self.scratch.keys = self.scratch.keys_all[i]
+                out, kr = seg_attend_(self.states[i], L.get('pw'), q, k, v, tpos, scratch=self.scratch)
+                if kr.data_ptr() != self.scratch.keys_all[i].data_ptr():
+                    self.scratch.keys_all[i].copy_(kr.view(B, H, 1))
+            else:
+                if B != 1:
+                    raise NotImplementedError('dense comparison mode is batch 1')
+                out, kr = self.states[i].attend(q, k, v, int(tpos[0]))
+                self.dense_keys = kr
+            x = x + F.linear(out.transpose(1, 2).reshape(B, 1, C), L['c_proj'])
+            x = x + F.linear(F.gelu(F.linear(_ln(x, L['ln2']), L['c_fc'])), L['c_mlp'])
+        return F.linear(_ln(x, W['ln_f']), W['wte'])[:, 0]
+
+    def keys_read(self):
+        """Mean keys attended per head and layer of the last step, per sequence (B,) float32."""
+        if self.mode != 'seg':
+            return torch.full((self.B,), float(self.dense_keys), device=self.dev)
+        return self.scratch.keys_all.mean(dim=(0, 2, 3))
+
+    @torch.no_grad()
+    def step(self, tok, t):
+        """Feed `tok` at position t.  tok int (batch 1, reference signature) -> (logits (V,), keys float);
+        tok LongTensor(B) -> (logits (B,V), keys (B,) tensor); t int or (B,) positions."""
+        scalar = not torch.is_tensor(tok)
+        tk = torch.as_tensor(tok, device=self.dev).long().reshape(-1).expand(self.B) if scalar else tok.to(self.dev).long()
+        tp = t.to(self.dev).long() if torch.is_tensor(t) else torch.full((self.B,), int(t), device=self.dev,
+                                                                        dtype=torch.long)
+        logits = self._forward_step(tk, tp)
+        keys = self.keys_read()
+        if scalar and self.B == 1:
+            return logits[0], float(keys[0])
+        return logits, keys
+
+    # ------------------------------------------------------------------------------------------ prefill
+    @torch.no_grad()
+    def prefill(self, idx, chunk=None):
+        """Run the model over prompts idx (B, T0) and fill every layer's cache (positions 0..T0-1).
+        Selection and attention are those of the forward pass (fastseg.py:345-405 semantics over the cache's
+        tree).  Returns the last position's logits (B, V)."""
+        if self.mode != 'seg':
+            raise NotImplementedError('prefill is for the seg cache')
+        W, H, C, dh = self.W, self.H, self.C, self.dh
+        B, T0 = idx.shape
+        if B != self.B or T0 > self.Tcap:
+            raise ValueError('prompt shape does not fit the decoder')
+        cfg = self.cfg
+        if cfg.neighbors or cfg.beam_mode == 'pred':
+            raise NotImplementedError('prefill with neighbour borrowing or the budget head is not built yet')
+        chunk = chunk or B
+        tq = torch.arange(T0, device=self.dev, dtype=torch.int32)
+        scale = 1.0 / math.sqrt(dh)
+        n_tree_val = SEL.fixed_n_tree(cfg)
+        last = []
+        for b0 in range(0, B, chunk):
+            b1 = min(B, b0 + chunk)
+            nb = b1 - b0
+            x = W['wte'][idx[b0:b1].to(self.dev)] + W['wpe'][:T0].unsqueeze(0)
+            for i, L in enumerate(W['layers']):
+                st = self.states[i]
+                qkv = F.linear(_ln(x, L['ln1']), L['c_attn'])
+                q, k, v = [a.view(nb, T0, H, dh).transpose(1, 2) for a in qkv.split(C, -1)]
+                Kb, Vb = st.K[b0:b1], st.V[b0:b1]
+                Kb[:, :, :T0].copy_(k)
+                Vb[:, :, :T0].copy_(v)
+                lv = [t[b0:b1] for t in st.levels]
+                K.level_sums(Kb, st.shape.blevels, out=lv, t_end=T0, zero_sink=True)
+                ids, vld, _ = K.tree_descend(q, lv, tq, st.shape, cfg.wmax)
+                n_tree = torch.full(ids.shape[:3], n_tree_val, dtype=torch.int32, device=self.dev)
+                out = torch.empty(nb, T0, H, dh, device=self.dev, dtype=v.dtype)
+                K.seg_attn(q, Kb, Vb, tq, ids, vld, n_tree, st.shape.leaf, cfg.local, scale,
+                           out=out.transpose(1, 2))
+                del ids, vld, n_tree
+                x = x + F.linear(out.view(nb, T0, C), L['c_proj'])
+                x = x + F.linear(F.gelu(F.linear(_ln(x, L['ln2']), L['c_fc'])), L['c_mlp'])
+                if cfg.global_pool:
+                    st.ksum[b0:b1] = k.float().sum(2)
+            last.append(F.linear(_ln(x[:, -1], W['ln_f']), W['wte']))
+        return torch.cat(last, 0)
+
+    # ------------------------------------------------------------------------------------------ graphs
+    @torch.no_grad()
+    def capture(self, tok, t):
+        """Capture one greedy decode step in a HIP graph.  Buffers: self.g_tok (B,) and self.g_t (B,) hold the
+        next token and position; a replay decodes them, writes the argmax token and advances the position."""
+        self.g_tok = tok.to(self.dev).long().clone()
+        self.g_t = (t.to(self.dev).long() if torch.is_tensor(t) else
+                    torch.full((self.B,), int(t), device=self.dev, dtype=torch.long)).clone()
+        # Warm up on a side stream (library handles, allocator).  The step at a fixed (token, position) is
+        # idempotent -- it rewrites the same cache row and recomputes the same nodes -- so running it here
+        # and again at the first replay leaves the cache as one step would.
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._forward_step(self.g_tok, self.g_t)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            logits = self._forward_step(self.g_tok, self.g_t)
+            self.g_logits = logits
+            K.argmax_rows(logits, out=self.g_tok)
+            self.g_t.add_(1)
+        self.graph = g
+        return g
+
+    def replay(self):
+        self.graph.replay()

@@ -136,7 +136,8 @@ def gather_dot_blocks(q, K, blk, block, scale=1.0, out=None):
 
 # ----------------------------------------------------------------------------------------------- attention
 def sparse_attn_fwd(q, k, v, cand, scale):
-    """Softmax attention over candidate positions (-1 unused).  Returns (out (b,H,T,dh) in v's dtype, lse)."""
+    """Softmax attention over candidate positions (-1 unused) into k, v (b,H,Tk,dh).  Returns (out (b,H,T,dh)
+    in v's dtype, lse (b,H,T))."""
     L.require_gpu(q, k, v, cand)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError('q, k, v must share a dtype')
@@ -146,7 +147,7 @@ def sparse_attn_fwd(q, k, v, cand, scale):
     out = torch.empty(b, H, T, D, device=q.device, dtype=v.dtype)
     lse = torch.empty(b, H, T, device=q.device, dtype=torch.float32)
     L.call('ta_sparse_attn_fwd', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k), *L.rows3(v),
-           L.ptr(cc), b, H, T, KC, D, float(scale), L.ptr(out), L.ptr(lse), L.stream())
+           L.ptr(cc), b, H, T, k.shape[2], KC, D, float(scale), L.ptr(out), L.ptr(lse), L.stream())
     return out, lse
 
 
@@ -168,7 +169,7 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
     if n_tree is not None:
         nt = n_tree if (n_tree.dtype == torch.int32 and n_tree.is_contiguous()) else n_tree.to(torch.int32).contiguous()
     if nsplit > 1 and ws is None:
-        ws = torch.empty(L.lib().ta_seg_attn_workspace_size(B, H, Nq, D, nsplit) // 4 + 1, device=q.device,
+        ws = torch.zeros(L.lib().ta_seg_attn_workspace_size(B, H, Nq, D, nsplit) // 4 + 1, device=q.device,
                          dtype=torch.float32)
     ws_bytes = ws.numel() * 4 if ws is not None else 0
     L.call('ta_seg_attn_fwd', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k), *L.rows3(v),
@@ -178,10 +179,25 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
     return out, lse, keys
 
 
+# ----------------------------------------------------------------------------------------------- sampling
+def argmax_rows(x, out=None):
+    """First index of the maximum of every row of x (R, n) -> (R,) int64."""
+    L.require_gpu(x)
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    R, n = x.shape
+    if out is None:
+        out = torch.empty(R, dtype=torch.long, device=x.device)
+    L.call('ta_argmax_rows', L.ptr(x), L.dtype_code(x), R, n, x.stride(0), L.ptr(out), L.stream())
+    return out
+
+
 # ----------------------------------------------------------------------------------------------- decode append
 def kv_append(k_new, v_new, Kc, Vc, t_pos, levels, leaf, arity):
     """Write k_new, v_new (B,H,D) at row t_pos[b] of the caches (B,H,Tcap,D) and form the completed nodes."""
     L.require_gpu(k_new, v_new, Kc, Vc, t_pos)
+    if not (k_new.dtype == v_new.dtype == Kc.dtype == Vc.dtype):
+        raise TypeError('kv_append: new rows and caches must share a dtype')
     B, H, Tcap, D = Kc.shape
     if k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or Kc.stride() != Vc.stride():
         raise ValueError('kv_append: unsupported layout')

@@ -1,0 +1,95 @@
+"""Segment-tree selection (seg.py of the reference) on the GPU.
+
+Same names and signatures: gate_apply, level_sums, tree_pass, neighbor_pass, leaves_to_pos, finish,
+select_seg.  The reference's tree_pass/neighbor_pass take a callable getU(l, cand) that gathers node
+vectors; the kernels read node sums in place, so here getU must be one that carries its levels: a
+SegState.getU (engine) or a LevelSource built from level sums.
+"""
+import torch
+
+from . import _lib
+from . import kernels as K
+from . import selection as SEL
+
+
+def gate_apply(raw, lgsum, size, gate_q):
+    raise NotImplementedError('treeattn_amd: the mean-log gate (seg.py:16-23) is not built yet')
+
+
+class LevelSource:
+    """getU(l, cand) over level sums {l: (b,H,T>>l,dh)} (binary levels) that the descent kernel can also
+    read in place."""
+
+    def __init__(self, S):
+        self.S = S
+
+    def __call__(self, l, cand):
+        from .forest import gather_nodes
+        return gather_nodes(self.S[l], cand)
+
+    def tree_levels(self, shape):
+        return [self.S[l] for l in shape.blevels]
+
+
+def _levels_of(getU, shape):
+    src = getattr(getU, '__self__', None)
+    if src is not None and hasattr(src, 'levels') and hasattr(src, 'shape'):   # SegState.getU
+        if src.shape.blevels[:shape.n_levels] != shape.blevels:
+            raise ValueError('the cache tree does not match the requested levels')
+        return src.levels[:shape.n_levels]
+    if isinstance(getU, LevelSource):
+        return getU.tree_levels(shape)
+    raise TypeError('treeattn_amd.seg: getU must be a SegState.getU or a LevelSource; the descent kernel '
+                    'reads node sums in place and cannot call back into Python')
+
+
+@torch.no_grad()
+def level_sums(kidx, Lm, gate, gate_q):
+    """{l: (b,H,T>>l,dh)} for l = 1..Lm (seg.py:26-41)."""
+    if gate:
+        raise NotImplementedError('treeattn_amd: the mean-log gate is not built yet')
+    _lib.require_gpu(kidx)
+    out = K.level_sums(kidx, list(range(1, Lm + 1)), zero_sink=False)
+    return {l: out[l - 1] for l in range(1, Lm + 1)}
+
+
+@torch.no_grad()
+def tree_pass(q, getU, tq, Lm, wmax):
+    """Beam descent (seg.py:44-70) over the reference's binary tree with leaf groups of 2 keys, levels
+    Lm..1.  Returns leaf ids (b,H,Nq,wl) long, validity, scores (best first)."""
+    _lib.require_gpu(q)
+    T = 1 << (Lm + 1)
+    src = getattr(getU, '__self__', None)
+    if src is not None and hasattr(src, 'shape'):
+        T = src.shape.T
+    shape = K.TreeShape(T, 2, 2)
+    ids, vld, sct = K.tree_descend(q, _levels_of(getU, shape), tq, shape, wmax)
+    return ids.long(), vld.bool(), sct
+
+
+@torch.no_grad()
+def neighbor_pass(q, getU1, st_leaf, st_score, st_ok, tq, cfg):
+    """seg.py:73-103; getU1 must expose the level-1 sums (LevelSource or a SegState-bound callable)."""
+    if isinstance(getU1, LevelSource):
+        S1 = getU1.S[1]
+    else:
+        src = getattr(getU1, '__self__', None)
+        if src is None or not hasattr(src, 'level_of'):
+            raise TypeError('neighbor_pass: getU1 must be a LevelSource or a SegState method')
+        S1 = src.level_of(1)
+    return SEL.neighbor_pass(q.float(), S1, st_leaf, st_score, st_ok, tq, cfg, 2)
+
+
+def leaves_to_pos(ids, ok):
+    return SEL.leaves_to_pos(ids, ok, 2)
+
+
+def finish(ids, vld, nid, match, nL, lhat, cfg):
+    return SEL.finish(ids, vld, nid, match, nL, lhat, cfg, getattr(cfg, 'leaf', 2))
+
+
+@torch.no_grad()
+def select_seg(q, k, lhat, cfg):
+    """seg.py:122-140: dict(tree_pos, leaf_ok, nb_pos, n_tree, nb_leaves)."""
+    _lib.require_gpu(q, k)
+    return SEL.select(q, k, lhat, cfg)[0]
