@@ -132,11 +132,10 @@ int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype,
  * each position once.  q: (B,H,Nq,D) with strides; k, v: (B,H,Tk,D) with strides (the whole sequence or a
  * KV cache); positions outside [0, Tk) are never read (a query with t >= Tk attends nothing).  ids/vld: (B,H,Nq,wl) contiguous.  out: (B,H,Nq,D) in the input dtype with strides; lse:
  * (B,H,Nq) float32 or NULL; keys: (B,H,Nq) float32 number of keys attended, or NULL.
- * nsplit > 1 splits every query's keys over nsplit wavefronts (for few queries with many keys, as in
- * decode); the last split to finish for a query merges the partials.  ws must then hold
- * ta_seg_attn_workspace_size(...) bytes and be zero-filled before its first use; every call leaves its
- * arrival counters at zero again, so one workspace serves any number of calls.  Calls that share a
- * workspace must not run concurrently.
+ * nsplit is 1 (one wavefront per query) or a multiple of 4: the keys of every query are split over nsplit
+ * wavefronts (for few queries with many keys, as in decode), 4 per workgroup merged in LDS; with more
+ * than 4, nsplit/4 workgroups per query write partials to ws (ta_seg_attn_workspace_size(...) bytes) and
+ * a second kernel merges them.  Calls that share a workspace must not run concurrently.
  */
 int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int nsplit);
 int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype,

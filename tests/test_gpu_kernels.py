@@ -168,9 +168,10 @@ def _seg_case(T, D, leaf, arity, wmax, dtype, beam=None, nsplit=1, local=3, B=2,
 @pytest.mark.parametrize('T,D,leaf,arity,wmax,dtype,beam,nsplit', [
     (256, 64, 2, 2, 8, torch.float32, 4, 1),
     (1024, 64, 64, 2, 4, torch.bfloat16, None, 1),
-    (1024, 128, 64, 2, 4, torch.bfloat16, None, 3),
+    (1024, 128, 64, 2, 4, torch.bfloat16, None, 4),
     (512, 32, 32, 2, 8, torch.float32, None, 1),
-    (1024, 64, 16, 4, 6, torch.float32, 3, 2)])
+    (1024, 64, 16, 4, 6, torch.float32, 3, 8),
+    (512, 64, 8, 2, 8, torch.bfloat16, None, 12)])
 def test_seg_attn_matches_oracle(T, D, leaf, arity, wmax, dtype, beam, nsplit):
     print('case', T, D, leaf, arity, wmax, dtype, beam, nsplit, flush=True)
     want, got, keys, keep = _seg_case(T, D, leaf, arity, wmax, dtype, beam, nsplit)

@@ -5,9 +5,9 @@
 // chunk of the list maps one key to each lane (two lanes per key when D = 128).  Each lane reads its key's
 // K and V rows (a leaf block is a run of consecutive rows, so a chunk reads contiguous memory), keeps a
 // running max/sum (online softmax, float32) and its own weighted V accumulator; the wavefront reduces
-// the accumulators once at the end (reduce-scatter over lanes).  With nsplit > 1 the partial (max, sum,
-// accumulator) of every split goes to a workspace; the split that finishes last for a query (a per-query
-// arrival counter, reset by that split) merges them, so one launch does the whole attention.
+// the accumulators once at the end.  In split mode (few queries with many keys, as in decode) the four
+// wavefronts of a workgroup share a query and merge in LDS; more workgroups per query write partials that a
+// small merge kernel combines.
 //
 // Reference functions replaced: fastseg.py:50-78 (_attn_fwd), fastseg.py:134-177 (sparse_attn),
 // fastseg.py:367-383 (candidate assembly + dedupe_fast), engine.py:107-119 (decode attention),
@@ -35,89 +35,86 @@ struct AttnParams {
   const int32_t* n_tree;
   int wl, leaf_log2, Lw;
   float scale;
-  int nsplit;
+  int gsplit;           // workgroups per query (split mode)
   void* out;
   int64_t osb, osh, osn;
   float* lse;
   float* keys;
-  float* ws;           // partials (query, split, D + 2)
-  unsigned* cnt;       // per-query arrival counters, zero between launches
+  float* ws;            // per-workgroup partials (query, gsplit, D + 2) when gsplit > 1
 };
 
 constexpr float kNegBig = -1e30f;
+constexpr int kWavesPerBlock = 4;
 
-// Sum acc[DPL] over the lanes that share (lane % LPK); afterwards lane holds E = result length values of
-// dims [dim0, dim0 + E) of its LPK-slice.  Lanes whose `dup` bits are set hold duplicate results.
-template <int DPL, int LPK>
-struct LaneReduce {
-  static constexpr int steps_halve() {
-    int len = DPL, n = 0;
-    for (int o = 32; o >= LPK; o >>= 1)
-      if (len > 1) { len >>= 1; ++n; }
-    return n;
+template <typename T> struct Raw16;  // 16 bytes of T -> EPL floats
+template <> struct Raw16<float> {
+  static constexpr int EPL = 4;
+  __device__ static void cvt(const uint4& u, float (&f)[4]) {
+    f[0] = __uint_as_float(u.x); f[1] = __uint_as_float(u.y); f[2] = __uint_as_float(u.z); f[3] = __uint_as_float(u.w);
   }
-  static constexpr int E = DPL >> steps_halve();
-  static constexpr int dup_mask() {
-    int len = DPL, m = 0;
-    for (int o = 32; o >= LPK; o >>= 1) {
-      if (len > 1) len >>= 1; else m |= o;
+};
+template <> struct Raw16<bf16_t> {
+  static constexpr int EPL = 8;
+  __device__ static void cvt(const uint4& u, float (&f)[8]) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
-    return m;
   }
-  __device__ static int run(float (&acc)[DPL], int lane) {
-    int dim0 = 0;
-    int len = DPL;
+};
+template <> struct Raw16<f16_t> {
+  static constexpr int EPL = 8;
+  __device__ static void cvt(const uint4& u, float (&f)[8]) {
+    const f16_t* h = reinterpret_cast<const f16_t*>(&u);
 #pragma unroll
-    for (int o = 32; o >= LPK; o >>= 1) {
-      if (len > 1) {
-        const int half = len >> 1;
-        const bool up = (lane & o) != 0;
-#pragma unroll
-        for (int i = 0; i < DPL / 2; ++i) {
-          if (i < half) {
-            const float mine = up ? acc[i + half] : acc[i];
-            const float other = up ? acc[i] : acc[i + half];
-            acc[i] = mine + __shfl_xor(other, o, kWave);
-          }
-        }
-        if (up) dim0 += half;
-        len = half;
-      } else {
-        acc[0] += __shfl_xor(acc[0], o, kWave);
-      }
-    }
-    return dim0;
+    for (int i = 0; i < 8; ++i) f[i] = (float)h[i];
   }
 };
 
-// SPLIT: several wavefronts per query with the in-kernel merge (decode); otherwise one wavefront per query.
+// Attention of queries over their key lists.  Rows of K and V are read as 16-byte slices: LPR = D / EPL
+// lanes share a row (EPL elements each) and one load instruction covers RPI = 64 / LPR consecutive keys,
+// so a leaf block is read in contiguous 1 KB pieces.  A chunk is NL load instructions = KPC keys; the next
+// chunk's loads are issued before the current one is consumed.  Scores are reduced over the LPR lanes of
+// a row; every lane keeps a weighted-V accumulator for its EPL dimensions, reduced over the RPI row groups
+// at the end.
+//   SPLIT = false: one wavefront per query (many queries: prefill).
+//   SPLIT = true: the 4 wavefronts of a workgroup share one query and interleave its chunks; their partial
+//   (max, sum, accumulator) are merged in LDS.  With gsplit > 1 workgroups per query each writes its merged
+//   partial to ws and merge_kernel combines them.
 template <typename T, int D, bool SPLIT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
-  constexpr int LPK = D > 64 ? D / 64 : 1;  // lanes per key
-  constexpr int DPL = D / LPK;              // dims per lane
-  constexpr int KPC = kWave / LPK;          // keys per chunk
-  using Red = LaneReduce<DPL, LPK>;
+  constexpr int EPL = Raw16<T>::EPL;
+  constexpr int LPR = D / EPL;              // lanes per key row
+  static_assert(LPR >= 1 && LPR <= kWave, "row slice layout");
+  constexpr int RPI = kWave / LPR;          // key rows per load instruction
+  constexpr int NL = 8;                     // load instructions per chunk
+  constexpr int KPC = NL * RPI;             // keys per chunk
   extern __shared__ float smem_f[];
   const int lane = lane_id(), w = wave_id();
-  const int wi = blockIdx.x * (blockDim.x / kWave) + w;
-  const int n = wi / p.nsplit, split = wi % p.nsplit;
+  int n, g = 0;
+  if constexpr (SPLIT) {
+    n = blockIdx.x / p.gsplit;
+    g = blockIdx.x % p.gsplit;
+  } else {
+    n = blockIdx.x * kWavesPerBlock + w;
+  }
   if (n >= p.Nq) return;
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
   const int64_t qi = (int64_t)bh * p.Nq + n;
   const int wl_pad = p.cand ? 0 : ((p.wl + 3) & ~3);
-  float* qf = smem_f + w * (D + wl_pad + kWave);
-  int32_t* s_ids = reinterpret_cast<int32_t*>(qf + D);
+  int32_t* s_ids = reinterpret_cast<int32_t*>(smem_f + w * (wl_pad + kWave));
   int32_t* s_ext = s_ids + wl_pad;
+  const int rg = lane / LPR;               // key row of this lane inside a load instruction
+  const int ds = (lane % LPR) * EPL;       // first dimension of this lane's slice
 
-  // query row -> LDS (float32)
-  {
-    const T* qr = reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh + n * p.qsn;
-    for (int d = lane; d < D; d += kWave) qf[d] = to_f32(qr[d]);
-  }
+  float qv[EPL];
+  load_row<T, EPL>(reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh + n * p.qsn + ds, qv);
 
   // key list of this query
-  int N, nused = 0, lb = 0, nloc = 0, nseg = 0;
+  int N, nused = 0, lb = 0, nloc = 0, next = 0;
   const int leaf = 1 << p.leaf_log2;
   if (p.cand) {
     N = p.KC;
@@ -150,120 +147,215 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
     }
     const uint64_t bal = __ballot(keep);
     if (keep) s_ext[__popcll(bal & ((1ull << lane) - 1))] = pe;
-    nseg = __popcll(bal);
-    N = nused * leaf + nloc + nseg;
+    next = __popcll(bal);
+    N = nused * leaf + nloc + next;
   }
   wave_sync();
 
-  const T* kb = reinterpret_cast<const T*>(p.k) + b * p.ksb + h * p.ksh;
-  const T* vb = reinterpret_cast<const T*>(p.v) + b * p.vsb + h * p.vsh;
-  const int kl = lane / LPK;        // key slot of this lane inside a chunk
-  const int part = lane % LPK;      // dim slice of this lane
+  const char* kb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.k) + b * p.ksb + h * p.ksh + ds);
+  const char* vb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.v) + b * p.vsb + h * p.vsh + ds);
+  const int64_t kst_b = p.kst * (int64_t)sizeof(T), vst_b = p.vst * (int64_t)sizeof(T);
   const int nchunks = (N + KPC - 1) / KPC;
   const int nl = nused * leaf;
+  const int stride = SPLIT ? p.gsplit * kWavesPerBlock : 1;
+  const int first = SPLIT ? g * kWavesPerBlock + w : 0;
+
+  auto fetch = [&](int c, uint4 (&kr)[NL], uint4 (&vr)[NL], bool (&ok)[NL]) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int key = c * KPC + i * RPI + rg;
+      int pos = -1;
+      if (key < N) {
+        if (p.cand) {
+          pos = p.cand[qi * p.KC + key];
+        } else if (key < nl) {
+          pos = (s_ids[key >> p.leaf_log2] << p.leaf_log2) + (key & (leaf - 1));
+        } else if (key < nl + nloc) {
+          pos = lb + (key - nl);
+        } else {
+          pos = s_ext[key - nl - nloc];
+        }
+      }
+      ok[i] = pos >= 0 && pos < p.Tk;
+      const int64_t row = ok[i] ? pos : 0;
+      kr[i] = *reinterpret_cast<const uint4*>(kb + row * kst_b);
+      vr[i] = *reinterpret_cast<const uint4*>(vb + row * vst_b);
+    }
+  };
 
   float m = kNegBig, l = 0.0f;
-  float acc[DPL];
+  float acc[EPL];
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) acc[d] = 0.0f;
+  for (int d = 0; d < EPL; ++d) acc[d] = 0.0f;
 
-  for (int c = split; c < nchunks; c += p.nsplit) {
-    const int key = c * KPC + kl;
-    int pos = -1;
-    if (key < N) {
-      if (p.cand) {
-        pos = p.cand[qi * p.KC + key];
-      } else if (key < nl) {
-        pos = (s_ids[key >> p.leaf_log2] << p.leaf_log2) + (key & (leaf - 1));
-      } else if (key < nl + nloc) {
-        pos = lb + (key - nl);
-      } else {
-        pos = s_ext[key - nl - nloc];
-      }
-    }
-    const bool valid = pos >= 0 && pos < p.Tk;
-    const int64_t row = valid ? pos : 0;
-    float kv[DPL];
-    load_row<T, DPL>(kb + row * p.kst + part * DPL, kv);
-    float vv[DPL];
-    load_row<T, DPL>(vb + row * p.vst + part * DPL, vv);
-    float dot = 0.0f;
+  auto consume = [&](const uint4 (&kr)[NL], const uint4 (&vr)[NL], const bool (&ok)[NL]) {
+    float sc[NL];
 #pragma unroll
-    for (int d = 0; d < DPL; ++d) dot = fmaf(qf[part * DPL + d], kv[d], dot);
-    if constexpr (LPK == 2) dot += __shfl_xor(dot, 1, kWave);
-    const float sc = valid ? dot * p.scale : kNegBig;
-    const float mn = fmaxf(m, wave_max(sc));
-    const float pw = valid ? __expf(sc - mn) : 0.0f;
+    for (int i = 0; i < NL; ++i) {
+      float kv[EPL];
+      Raw16<T>::cvt(kr[i], kv);
+      float d0 = 0.0f;
+#pragma unroll
+      for (int d = 0; d < EPL; ++d) d0 = fmaf(qv[d], kv[d], d0);
+      sc[i] = d0;
+    }
+#pragma unroll
+    for (int o = LPR / 2; o >= 1; o >>= 1) {
+#pragma unroll
+      for (int i = 0; i < NL; ++i) sc[i] += __shfl_xor(sc[i], o, kWave);
+    }
+    float cm = kNegBig;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      sc[i] = ok[i] ? sc[i] * p.scale : kNegBig;
+      cm = fmaxf(cm, sc[i]);
+    }
+    const float mn = fmaxf(m, wave_max(cm));
     if (mn != m) {
       const float alpha = __expf(m - mn);
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) acc[d] *= alpha;
+      for (int d = 0; d < EPL; ++d) acc[d] *= alpha;
       l *= alpha;
     }
+    float lsum = 0.0f;
 #pragma unroll
-    for (int d = 0; d < DPL; ++d) acc[d] = fmaf(pw, vv[d], acc[d]);
-    if (part == 0) l += pw;
+    for (int i = 0; i < NL; ++i) {
+      const float pw = ok[i] ? __expf(sc[i] - mn) : 0.0f;
+      lsum += pw;
+      float vv[EPL];
+      Raw16<T>::cvt(vr[i], vv);
+#pragma unroll
+      for (int d = 0; d < EPL; ++d) acc[d] = fmaf(pw, vv[d], acc[d]);
+    }
+    if (lane % LPR == 0) l += lsum;
     m = mn;
+  };
+
+  {
+    uint4 kA[NL], vA[NL];
+    bool okA[NL];
+    int c = first;
+    if (c < nchunks) fetch(c, kA, vA, okA);
+    while (c < nchunks) {
+      const int cn = c + stride;
+      uint4 kB[NL], vB[NL];
+      bool okB[NL];
+      if (cn < nchunks) fetch(cn, kB, vB, okB);
+      consume(kA, vA, okA);
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        kA[i] = kB[i];
+        vA[i] = vB[i];
+        okA[i] = okB[i];
+      }
+      c = cn;
+    }
   }
 
-  const float L = wave_sum(l);
-  const int dim0 = Red::run(acc, lane) + part * DPL;
-  const bool writer = (lane & Red::dup_mask()) == 0;
-  if constexpr (!SPLIT) {
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    if (writer) {
-      T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh + n * p.osn;
+  float L = wave_sum(l);
+  // sum the accumulators of the RPI row groups: afterwards lanes 0..LPR-1 hold the full dims
 #pragma unroll
-      for (int e = 0; e < Red::E; ++e) orow[dim0 + e] = from_f32<T>(acc[e] * inv);
+  for (int o = LPR; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int d = 0; d < EPL; ++d) acc[d] += __shfl_xor(acc[d], o, kWave);
+  }
+  if constexpr (SPLIT) {
+    // merge the 4 wavefronts of the workgroup through LDS
+    float* red = smem_f + kWavesPerBlock * (wl_pad + kWave);   // [4][D + 2]
+    if (rg == 0) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) red[w * (D + 2) + 2 + ds + e] = acc[e];
     }
     if (lane == 0) {
-      if (p.lse) p.lse[qi] = L > 0.0f ? m + __logf(L) : kNegBig;
-      if (p.keys) p.keys[qi] = (float)N;
+      red[w * (D + 2)] = m;
+      red[w * (D + 2) + 1] = L;
     }
-  } else {
-    float* part_ws = p.ws + (qi * p.nsplit + split) * (D + 2);
-    if (writer) {
-#pragma unroll
-      for (int e = 0; e < Red::E; ++e) part_ws[2 + dim0 + e] = acc[e];
-    }
-    if (lane == 0) {
-      part_ws[0] = m;
-      part_ws[1] = L;
-      if (split == 0 && p.keys) p.keys[qi] = (float)N;
-    }
-    // publish the partial, count arrivals; the last split of this query merges all of them
-    __threadfence();
-    int last = 0;
-    if (lane == 0) last = atomicAdd(p.cnt + qi, 1u) == (unsigned)(p.nsplit - 1);
-    last = __shfl(last, 0, kWave);
-    if (!last) return;
-    __threadfence();
-    const float* base = p.ws + qi * p.nsplit * (D + 2);
+    __syncthreads();
+    if (w != 0) return;
     float M = kNegBig;
-    for (int s = 0; s < p.nsplit; ++s) {
-      const float* ps = base + s * (D + 2);
-      if (ps[1] > 0.0f) M = fmaxf(M, ps[0]);
-    }
+#pragma unroll
+    for (int s = 0; s < kWavesPerBlock; ++s)
+      if (red[s * (D + 2) + 1] > 0.0f) M = fmaxf(M, red[s * (D + 2)]);
     float Lt = 0.0f;
-    for (int s = 0; s < p.nsplit; ++s) {
-      const float* ps = base + s * (D + 2);
-      if (ps[1] > 0.0f) Lt += ps[1] * __expf(ps[0] - M);
+    float sc[kWavesPerBlock];
+#pragma unroll
+    for (int s = 0; s < kWavesPerBlock; ++s) {
+      const float Ls = red[s * (D + 2) + 1];
+      sc[s] = Ls > 0.0f ? __expf(red[s * (D + 2)] - M) : 0.0f;
+      Lt += Ls * sc[s];
+    }
+    if (p.gsplit > 1) {
+      float* part = p.ws + (qi * p.gsplit + g) * (D + 2);
+      for (int d = lane; d < D; d += kWave) {
+        float a = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kWavesPerBlock; ++s) a += red[s * (D + 2) + 2 + d] * sc[s];
+        part[2 + d] = a;
+      }
+      if (lane == 0) {
+        part[0] = M;
+        part[1] = Lt;
+        if (g == 0 && p.keys) p.keys[qi] = (float)N;
+      }
+      return;
     }
     const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
     T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh + n * p.osn;
     for (int d = lane; d < D; d += kWave) {
       float a = 0.0f;
-      for (int s = 0; s < p.nsplit; ++s) {
-        const float* ps = base + s * (D + 2);
-        if (ps[1] > 0.0f) a += ps[2 + d] * __expf(ps[0] - M);
-      }
+#pragma unroll
+      for (int s = 0; s < kWavesPerBlock; ++s) a += red[s * (D + 2) + 2 + d] * sc[s];
       orow[d] = from_f32<T>(a * inv);
     }
     if (lane == 0) {
       if (p.lse) p.lse[qi] = Lt > 0.0f ? M + __logf(Lt) : kNegBig;
-      p.cnt[qi] = 0u;  // ready for the next launch
+      if (p.keys) p.keys[qi] = (float)N;
+    }
+  } else {
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    if (rg == 0) {
+      T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh + n * p.osn + ds;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) orow[e] = from_f32<T>(acc[e] * inv);
+    }
+    if (lane == 0) {
+      if (p.lse) p.lse[qi] = L > 0.0f ? m + __logf(L) : kNegBig;
+      if (p.keys) p.keys[qi] = (float)N;
     }
   }
+}
+
+// Combine the gsplit workgroup partials of every query: out = sum_g acc_g e^(m_g - M) / sum_g L_g e^(m_g - M).
+template <typename T, int D>
+__global__ __launch_bounds__(128) void merge_kernel(const float* __restrict__ ws, int gsplit, int H, int Nq,
+                                                    void* out, int64_t osb, int64_t osh, int64_t osn,
+                                                    float* __restrict__ lse) {
+  const int64_t qi = blockIdx.x;
+  const int n = (int)(qi % Nq);
+  const int bh = (int)(qi / Nq);
+  const int b = bh / H, h = bh % H;
+  const float* base = ws + qi * gsplit * (D + 2);
+  float M = kNegBig;
+  for (int s = 0; s < gsplit; ++s) {
+    const float* ps = base + s * (D + 2);
+    if (ps[1] > 0.0f) M = fmaxf(M, ps[0]);
+  }
+  float L = 0.0f;
+  for (int s = 0; s < gsplit; ++s) {
+    const float* ps = base + s * (D + 2);
+    if (ps[1] > 0.0f) L += ps[1] * __expf(ps[0] - M);
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  T* orow = reinterpret_cast<T*>(out) + b * osb + h * osh + n * osn;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float a = 0.0f;
+    for (int s = 0; s < gsplit; ++s) {
+      const float* ps = base + s * (D + 2);
+      if (ps[1] > 0.0f) a += ps[2 + d] * __expf(ps[0] - M);
+    }
+    orow[d] = from_f32<T>(a * inv);
+  }
+  if (threadIdx.x == 0 && lse) lse[qi] = L > 0.0f ? M + __logf(L) : kNegBig;
 }
 
 // ----------------------------------------------------------------------------------------- decode append
@@ -338,11 +430,10 @@ namespace {
 int elem_size(int dt) { return dt == TA_F32 ? 4 : 2; }
 bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
 
-// K/V rows are read D/LPK elements per lane with loads of up to 16 bytes.
+// K/V/q rows are read in 16-byte slices.
 bool kv_aligned(const void* p, int dt, int D, std::initializer_list<int64_t> strides) {
-  const int LPK = D > 64 ? D / 64 : 1;
-  int slice = (D / LPK) * elem_size(dt);
-  int a = slice >= 16 ? 16 : slice;
+  const int a = 16;
+  if (D * elem_size(dt) < 16 || (D * elem_size(dt)) % 16) return false;
   if (!aligned(p, a)) return false;
   for (int64_t s : strides)
     if ((s * elem_size(dt)) % a) return false;
@@ -350,27 +441,32 @@ bool kv_aligned(const void* p, int dt, int D, std::initializer_list<int64_t> str
 }
 
 template <typename T, int D>
-int launch_attn(const AttnParams& p, int B, hipStream_t st) {
-  const int waves = 4;
+int launch_attn(const AttnParams& p, int B, bool split, hipStream_t st) {
   const int wl_pad = p.cand ? 0 : ((p.wl + 3) & ~3);
-  const size_t lds = (size_t)waves * (D + wl_pad + kWave) * sizeof(float);
-  const int64_t nw = (int64_t)p.Nq * p.nsplit;
-  dim3 grid((unsigned)((nw + waves - 1) / waves), B * p.H);
-  if (p.nsplit > 1) {
-    hipLaunchKernelGGL((attn_kernel<T, D, true>), grid, dim3(waves * kWave), lds, st, p);
-  } else {
-    hipLaunchKernelGGL((attn_kernel<T, D, false>), grid, dim3(waves * kWave), lds, st, p);
+  size_t lds = (size_t)kWavesPerBlock * (wl_pad + kWave) * sizeof(float);
+  if (split) {
+    lds += (size_t)kWavesPerBlock * (D + 2) * sizeof(float);
+    dim3 grid((unsigned)((int64_t)p.Nq * p.gsplit), B * p.H);
+    hipLaunchKernelGGL((attn_kernel<T, D, true>), grid, dim3(kWavesPerBlock * kWave), lds, st, p);
+    int rc = check_launch("attn_kernel");
+    if (rc || p.gsplit == 1) return rc;
+    dim3 mg((unsigned)((int64_t)B * p.H * p.Nq));
+    hipLaunchKernelGGL((merge_kernel<T, D>), mg, dim3(D < 128 ? D : 128), 0, st, p.ws, p.gsplit, p.H, p.Nq, p.out,
+                       p.osb, p.osh, p.osn, p.lse);
+    return check_launch("merge_kernel");
   }
+  dim3 grid((unsigned)((p.Nq + kWavesPerBlock - 1) / kWavesPerBlock), B * p.H);
+  hipLaunchKernelGGL((attn_kernel<T, D, false>), grid, dim3(kWavesPerBlock * kWave), lds, st, p);
   return check_launch("attn_kernel");
 }
 
-int dispatch_attn(int dt, int D, const AttnParams& p, int B, hipStream_t st) {
-#define TA_CASE_D(T)                                      \
-  switch (D) {                                            \
-    case 16: return launch_attn<T, 16>(p, B, st);         \
-    case 32: return launch_attn<T, 32>(p, B, st);         \
-    case 64: return launch_attn<T, 64>(p, B, st);         \
-    case 128: return launch_attn<T, 128>(p, B, st);       \
+int dispatch_attn(int dt, int D, const AttnParams& p, int B, bool split, hipStream_t st) {
+#define TA_CASE_D(T)                                             \
+  switch (D) {                                                   \
+    case 16: return launch_attn<T, 16>(p, B, split, st);         \
+    case 32: return launch_attn<T, 32>(p, B, split, st);         \
+    case 64: return launch_attn<T, 64>(p, B, split, st);         \
+    case 128: return launch_attn<T, 128>(p, B, split, st);       \
     default: set_error("head dim must be 16, 32, 64 or 128"); return TA_ERR_UNSUPPORTED; \
   }
   switch (dt) {
@@ -396,8 +492,9 @@ extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, i
     return TA_ERR_ARG;
   }
   if (T == 0) return TA_OK;
-  if (!kv_aligned(k, dtype, D, {ksb, ksh, kst}) || !kv_aligned(v, dtype, D, {vsb, vsh, vst})) {
-    set_error("ta_sparse_attn_fwd: k/v rows not aligned");
+  if (!kv_aligned(q, dtype, D, {qsb, qsh, qst}) || !kv_aligned(k, dtype, D, {ksb, ksh, kst}) ||
+      !kv_aligned(v, dtype, D, {vsb, vsh, vst})) {
+    set_error("ta_sparse_attn_fwd: q/k/v rows not 16-byte aligned");
     return TA_ERR_ARG;
   }
   AttnParams p{};
@@ -408,17 +505,16 @@ extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, i
   p.cand = cand; p.KC = KC;
   p.leaf_log2 = 1;
   p.scale = scale;
-  p.nsplit = 1;
+  p.gsplit = 1;
   p.out = out; p.osb = (int64_t)H * T * D; p.osh = (int64_t)T * D; p.osn = D;
   p.lse = lse;
-  return dispatch_attn(dtype, D, p, B, (hipStream_t)stream);
+  return dispatch_attn(dtype, D, p, B, false, (hipStream_t)stream);
 }
 
-static int64_t counter_bytes(int B, int H, int Nq) { return (((int64_t)B * H * Nq * 4) + 255) / 256 * 256; }
-
 extern "C" int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int nsplit) {
-  if (nsplit <= 1) return 0;
-  return counter_bytes(B, H, Nq) + (int64_t)B * H * Nq * nsplit * (D + 2) * (int64_t)sizeof(float);
+  const int gsplit = nsplit / kWavesPerBlock;
+  if (gsplit <= 1) return 0;
+  return (int64_t)B * H * Nq * gsplit * (D + 2) * (int64_t)sizeof(float);
 }
 
 extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
@@ -427,8 +523,9 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
                                const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl, int leaf,
                                int local, float scale, void* out, int64_t osb, int64_t osh, int64_t osn, float* lse,
                                float* keys, int nsplit, float* ws, int64_t ws_bytes, void* stream) {
-  if (B <= 0 || H <= 0 || Nq < 0 || wl < 0 || nsplit < 1 || leaf < 2 || (leaf & (leaf - 1))) {
-    set_error("ta_seg_attn_fwd: bad sizes");
+  if (B <= 0 || H <= 0 || Nq < 0 || wl < 0 || nsplit < 1 || leaf < 2 || (leaf & (leaf - 1)) ||
+      (nsplit > 1 && nsplit % kWavesPerBlock)) {
+    set_error("ta_seg_attn_fwd: bad sizes (nsplit must be 1 or a multiple of 4)");
     return TA_ERR_ARG;
   }
   const int Lw = local > 3 ? local : 3;
@@ -441,12 +538,13 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
     return TA_ERR_UNSUPPORTED;
   }
   if (Nq == 0) return TA_OK;
-  if (nsplit > 1 && ws_bytes < ta_seg_attn_workspace_size(B, H, Nq, D, nsplit)) {
+  if (ws_bytes < ta_seg_attn_workspace_size(B, H, Nq, D, nsplit)) {
     set_error("ta_seg_attn_fwd: workspace too small");
     return TA_ERR_WORKSPACE;
   }
-  if (!kv_aligned(k, dtype, D, {ksb, ksh, kst}) || !kv_aligned(v, dtype, D, {vsb, vsh, vst})) {
-    set_error("ta_seg_attn_fwd: k/v rows not aligned");
+  if (!kv_aligned(q, dtype, D, {qsb, qsh, qsn}) || !kv_aligned(k, dtype, D, {ksb, ksh, kst}) ||
+      !kv_aligned(v, dtype, D, {vsb, vsh, vst})) {
+    set_error("ta_seg_attn_fwd: q/k/v rows not 16-byte aligned");
     return TA_ERR_ARG;
   }
   AttnParams p{};
@@ -461,14 +559,10 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
   p.leaf_log2 = ll;
   p.Lw = Lw;
   p.scale = scale;
-  p.nsplit = nsplit;
+  p.gsplit = nsplit > 1 ? nsplit / kWavesPerBlock : 1;
   p.out = out; p.osb = osb; p.osh = osh; p.osn = osn;
-  p.lse = lse; p.keys = keys;
-  if (nsplit > 1) {
-    p.cnt = reinterpret_cast<unsigned*>(ws);
-    p.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + counter_bytes(B, H, Nq));
-  }
-  return dispatch_attn(dtype, D, p, B, (hipStream_t)stream);
+  p.lse = lse; p.keys = keys; p.ws = ws;
+  return dispatch_attn(dtype, D, p, B, nsplit > 1, (hipStream_t)stream);
 }
 
 extern "C" int ta_kv_append(const void* k_new, const void* v_new, int dtype, int64_t nsb, int64_t nsh, int64_t vnsb,

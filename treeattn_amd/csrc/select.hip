@@ -122,32 +122,44 @@ struct LevelIn {
   int blevel[kMaxLevels];
 };
 
-// One wavefront per query.  Levels whose number of complete nodes is <= wmax keep every node, so the
-// descent starts at the highest level with more complete nodes than wmax (all of them are candidates
-// there) -- the same kept sets as descending from the top.  Each level: score candidates (16 lanes per
-// node, 4 nodes per round), rank every candidate against all others (score desc, id asc), keep the best
-// wmax, expand them to their children and add the level's complete left siblings.
-template <typename TQ, int D>
+// WPQ wavefronts per query (1: many queries, prefill; 4: few queries, decode).  Levels whose number of
+// complete nodes is <= wmax keep every node, so the descent starts at the highest level with more complete
+// nodes than wmax (all of them are candidates there) -- the same kept sets as descending from the top.
+// Each level: score the candidates (16 lanes per node, 4 nodes per wavefront and round), rank every
+// candidate against all others (score desc, id asc; candidate lists padded to a multiple of 4 with entries
+// that never rank first so LDS is read 16 bytes at a time), keep the best wmax, expand them to their
+// children and add the level's complete left siblings.
+template <int WPQ>
+__device__ __forceinline__ void query_sync() {
+  if constexpr (WPQ == 1) wave_sync(); else __syncthreads();
+}
+
+template <typename TQ, int D, int WPQ>
 __global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, int64_t qsb, int64_t qsh,
                                                       int64_t qsn, int H, int Nq, int T, const int32_t* __restrict__ tq,
                                                       int64_t tq_sb, LevelIn lv, int n_levels, int arity_log2,
-                                                      int wmax, int wl, int cmax, int32_t* __restrict__ ids,
+                                                      int wmax, int wl, int cmax4, int32_t* __restrict__ ids,
                                                       uint8_t* __restrict__ vld, float* __restrict__ sct) {
   constexpr int R = D / 16;
   constexpr int NB = (64 / R) < 16 ? (64 / R) : 16;
+  constexpr int NG = 4 * WPQ;          // 16-lane groups per query
+  constexpr int NT = kWave * WPQ;      // threads per query
   extern __shared__ int32_t smem_i[];
   const int lane = lane_id(), w = wave_id();
-  const int n = blockIdx.x * (blockDim.x / kWave) + w;
+  const int qw = w / WPQ;              // query slot in the block
+  const int tid = (w % WPQ) * kWave + lane;
+  const int n = blockIdx.x * ((int)blockDim.x / NT) + qw;
   if (n >= Nq) return;
   const int bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
-  int32_t* cid = smem_i + w * (2 * cmax + 2 * wmax);
-  float* csc = reinterpret_cast<float*>(cid + cmax);
-  int32_t* kid = cid + 2 * cmax;
-  float* ksc = reinterpret_cast<float*>(kid + wmax);
+  const int wmax4 = (wmax + 3) & ~3;
+  int32_t* cid = smem_i + qw * (2 * cmax4 + 2 * wmax4);
+  float* csc = reinterpret_cast<float*>(cid + cmax4);
+  int32_t* kid = cid + 2 * cmax4;
+  float* ksc = reinterpret_cast<float*>(kid + wmax4);
 
   const int t = tq[b * tq_sb + n];
-  const int g = lane >> 4, j16 = lane & 15;
+  const int gg = (w % WPQ) * 4 + (lane >> 4), j16 = lane & 15;
   float qr[R];
   load_row<TQ, R>(q + b * qsb + h * qsh + n * qsn + R * j16, qr);
   const int64_t obase = ((int64_t)bh * Nq + n) * wl;
@@ -160,16 +172,19 @@ __global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, 
       if ((t >> lv.blevel[j]) > wmax) { start = j; break; }
     }
     int C = t >> lv.blevel[start];
-    for (int c = lane; c < C; c += kWave) cid[c] = c;
-    wave_sync();
+    for (int c = tid; c < ((C + 3) & ~3); c += NT) {
+      cid[c] = c < C ? c : INT32_MAX;
+      if (c >= C) csc[c] = -INFINITY;
+    }
+    query_sync<WPQ>();
     for (int j = start;; --j) {
       const float* base = lv.ptr[j] + b * lv.sb[j] + h * lv.sh[j] + R * j16;
       const float scale = pow2_neg(lv.blevel[j]);
-      for (int c0 = 0; c0 < C; c0 += 4 * NB) {
+      for (int c0 = 0; c0 < C; c0 += NG * NB) {
         float rows[NB][R];
 #pragma unroll
         for (int r = 0; r < NB; ++r) {
-          const int c = c0 + 4 * r + g;
+          const int c = c0 + NG * r + gg;
           if (c < C) {
             load_row<float, R>(base + (int64_t)cid[c] * D, rows[r]);
           } else {
@@ -179,20 +194,26 @@ __global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, 
         }
 #pragma unroll
         for (int r = 0; r < NB; ++r) {
-          const int c = c0 + 4 * r + g;
+          const int c = c0 + NG * r + gg;
           const float s = __fmul_rn(canon_dot<R>(qr, rows[r]), scale);
           if (c < C && j16 == 0) csc[c] = s;
         }
       }
-      wave_sync();
-      for (int c = lane; c < C; c += kWave) {
+      query_sync<WPQ>();
+      const int C4 = (C + 3) >> 2;
+      const float4* sc4 = reinterpret_cast<const float4*>(csc);
+      const int4* id4 = reinterpret_cast<const int4*>(cid);
+      for (int c = tid; c < C; c += NT) {
         const float s = csc[c];
         const int id = cid[c];
         int rank = 0;
-        for (int o = 0; o < C; ++o) {
-          const float so = csc[o];
-          const int io = cid[o];
-          rank += (so > s) || (so == s && io < id);
+        for (int o = 0; o < C4; ++o) {
+          const float4 so = sc4[o];
+          const int4 io = id4[o];
+          rank += (so.x > s) | ((so.x == s) & (io.x < id));
+          rank += (so.y > s) | ((so.y == s) & (io.y < id));
+          rank += (so.z > s) | ((so.z == s) & (io.z < id));
+          rank += (so.w > s) | ((so.w == s) & (io.w < id));
         }
         if (rank < wmax) {
           kid[rank] = id;
@@ -200,19 +221,24 @@ __global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, 
         }
       }
       nk = C < wmax ? C : wmax;
-      wave_sync();
+      query_sync<WPQ>();
       if (j == 0) break;
       const int m = t >> lv.blevel[j - 1];
       const int digit = m & (arity - 1);
       const int nch = nk << arity_log2;
       C = nch + digit;
-      for (int c = lane; c < C; c += kWave) {
-        cid[c] = c < nch ? (kid[c >> arity_log2] << arity_log2) + (c & (arity - 1)) : m - 1 - (c - nch);
+      for (int c = tid; c < ((C + 3) & ~3); c += NT) {
+        if (c < C) {
+          cid[c] = c < nch ? (kid[c >> arity_log2] << arity_log2) + (c & (arity - 1)) : m - 1 - (c - nch);
+        } else {
+          cid[c] = INT32_MAX;
+          csc[c] = -INFINITY;
+        }
       }
-      wave_sync();
+      query_sync<WPQ>();
     }
   }
-  for (int r = lane; r < wl; r += kWave) {
+  for (int r = tid; r < wl; r += NT) {
     if (r < nk) {
       ids[obase + r] = kid[r];
       vld[obase + r] = 1;
@@ -356,16 +382,24 @@ struct DescendRun {
                  int64_t tq_sb, const LevelIn& lv, int n_levels, int Tgeo, int arity_log2, int wmax, int wl,
                  int32_t* ids, uint8_t* vld, float* sct, hipStream_t st) {
     const int arity = 1 << arity_log2;
-    const int cmax = arity * wmax + arity - 1;
-    const int waves = Nq >= 4 ? 4 : 1;
-    const size_t lds = (size_t)waves * (2 * cmax + 2 * wmax) * sizeof(int32_t);
+    const int cmax4 = (arity * wmax + arity - 1 + 3) & ~3;
+    const int wmax4 = (wmax + 3) & ~3;
+    // few queries (decode): four wavefronts per query; many (prefill): one wavefront per query, 4 per block
+    const bool wide = (int64_t)B * H * Nq < 4096;
+    const int qpb = wide ? 1 : 4;
+    const size_t lds = (size_t)qpb * (2 * cmax4 + 2 * wmax4) * sizeof(int32_t);
     if (lds > 64 * 1024) {
       set_error("descent beam too wide for LDS (arity * wmax too large)");
       return TA_ERR_UNSUPPORTED;
     }
-    dim3 grid((Nq + waves - 1) / waves, B * H);
-    hipLaunchKernelGGL((descend_kernel<T, D>), grid, dim3(waves * kWave), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq,
-                       Tgeo, tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax, ids, vld, sct);
+    dim3 grid((Nq + qpb - 1) / qpb, B * H);
+    if (wide) {
+      hipLaunchKernelGGL((descend_kernel<T, D, 4>), grid, dim3(256), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq, Tgeo,
+                         tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct);
+    } else {
+      hipLaunchKernelGGL((descend_kernel<T, D, 1>), grid, dim3(256), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq, Tgeo,
+                         tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct);
+    }
     return check_launch("descend_kernel");
   }
 };

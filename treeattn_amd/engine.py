@@ -102,19 +102,19 @@ class _Scratch:
         self.sct = torch.empty(B, H, 1, wl, device=dev)
         self.keys_all = torch.zeros(n_layer, B, H, 1, device=dev)
         self.keys = self.keys_all[0]
+        self.n_tree = None
         self.nsplit = nsplit
         nbytes = K.L.lib().ta_seg_attn_workspace_size(B, H, 1, dh, nsplit)
-        self.ws = torch.zeros(max(1, nbytes // 4 + 1), device=dev)  # arrival counters start at zero
+        self.ws = torch.empty(max(1, nbytes // 4 + 1), device=dev)
 
 
 def decode_nsplit(B, H, wl, leaf):
-    """Split of each query's keys over wavefronts: aim for ~4 chunks of 64 keys per wavefront and at least
-    ~2048 wavefronts per launch (8 per CU)."""
+    """Wavefronts per query for the decode attention: one 4-wavefront workgroup per query, or several
+    workgroups per query (merged by a second kernel) when there are too few queries to fill the GPU
+    (~512 workgroups), keeping at least one 64-key chunk per wavefront."""
     chunks = max(1, (wl * leaf + leaf + 64) // 64)
-    ns = max(1, min(chunks // 4, 16))
-    while ns < 16 and B * H * ns < 2048 and ns * 2 <= chunks:
-        ns *= 2
-    return ns
+    g = max(1, min(512 // max(1, B * H), chunks // 4, 64))
+    return 4 * g
 
 
 def _pw_budget(state, pw, q, t):
@@ -153,7 +153,9 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
             if cfg.global_pool:
                 state.ksum += k[:, :, 0].float()
         out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
-        n_tree = torch.full((B, H, 1), SEL.fixed_n_tree(cfg), dtype=torch.int32, device=q.device)
+        if scratch.n_tree is None:
+            scratch.n_tree = torch.full((B, H, 1), SEL.fixed_n_tree(cfg), dtype=torch.int32, device=q.device)
+        n_tree = scratch.n_tree
         K.seg_attn(q, state.K, state.V, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out,
                    keys=scratch.keys, nsplit=scratch.nsplit, ws=scratch.ws)
         return out, scratch.keys
@@ -251,12 +253,13 @@ class Decoder:
         head) are left in self.scratch.keys_all."""
         W, H, C, dh, B = self.W, self.H, self.C, self.dh, self.B
         x = (W['wte'][tok] + W['wpe'][tpos]).view(B, 1, C)
+        tpos32 = tpos.to(torch.int32)
         for i, L in enumerate(W['layers']):
             q, k, v = F.linear(_ln(x, L['ln1']), L['c_attn']).split(C, -1)
             q, k, v = [a.view(B, 1, H, dh).transpose(1, 2) for a in (q, k, v)]
             if self.mode == 'seg':
                 self.scratch.keys = self.scratch.keys_all[i]
-                out, kr = seg_attend_(self.states[i], L.get('pw'), q, k, v, tpos, scratch=self.scratch)
+                out, kr = seg_attend_(self.states[i], L.get('pw'), q, k, v, tpos32, scratch=self.scratch)
                 if kr.data_ptr() != self.scratch.keys_all[i].data_ptr():
                     self.scratch.keys_all[i].copy_(kr.view(B, H, 1))
             else:

@@ -168,9 +168,10 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
     nt = None
     if n_tree is not None:
         nt = n_tree if (n_tree.dtype == torch.int32 and n_tree.is_contiguous()) else n_tree.to(torch.int32).contiguous()
-    if nsplit > 1 and ws is None:
-        ws = torch.zeros(L.lib().ta_seg_attn_workspace_size(B, H, Nq, D, nsplit) // 4 + 1, device=q.device,
-                         dtype=torch.float32)
+    if ws is None:
+        nbytes = L.lib().ta_seg_attn_workspace_size(B, H, Nq, D, nsplit)
+        if nbytes > 0:
+            ws = torch.empty(nbytes // 4 + 1, device=q.device, dtype=torch.float32)
     ws_bytes = ws.numel() * 4 if ws is not None else 0
     L.call('ta_seg_attn_fwd', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k), *L.rows3(v),
            B, H, Nq, D, k.shape[2], L.ptr(tq32), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(nt), wl, int(leaf), int(local),
