@@ -163,6 +163,18 @@ int ta_kv_append(const void* k_new, const void* v_new, int dtype,
                  int leaf_log2, int arity_log2, void* stream);
 
 /*
+ * Row-block matrix product of the decode step (the model around the attention: model.py:21-44,
+ * engine.py:168-177 -- F.linear with the LayerNorm before it and GELU / residual add after it), bf16:
+ *   Y[M,N] = epilogue( LN(X)[M,K] . W[N,K]^T ),  LN applied when ln_w != NULL (no bias, eps ln_eps),
+ *   epilogue 0: none, 1: GELU (erf), 2: residual add R + (.).  Each op's result is rounded to bf16 as in
+ * the unfused chain.  Row strides ldx, ldw, ldy, ldr in elements; K a multiple of 64; X, W, ln_w 16-byte
+ * aligned.  Y may be the same buffer as R.
+ */
+int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy,
+             const void* R, int64_t ldr, const void* ln_w, float ln_eps, int M, int N, int K,
+             int epilogue, void* stream);
+
+/*
  * Row-wise argmax for greedy decoding (replaces logits.argmax(-1) of the reference's greedy loop,
  * phase2.py:51-66): out[r] = the first index of the largest value of x[r, 0:n].  x: rows of n elements of
  * dtype with row stride `stride`; out: int64.

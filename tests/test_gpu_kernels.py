@@ -213,3 +213,43 @@ def test_sparse_attn_decode_shape():
     out, _ = K.sparse_attn_fwd(q.to(DEV), k.to(DEV), v.to(DEV), cand.to(DEV), 0.125)
     want = sparse_attn_ref(q, k, v, cand, 0.125)
     assert (out.cpu().float() - want.float()).abs().max().item() < 2e-2
+
+
+def _chain(x, w, ln_w, epi, res):
+    """The unfused op chain in bf16 (torch on the GPU, products in fp32 then rounded)."""
+    import torch.nn.functional as F
+    h = F.layer_norm(x.float(), (x.shape[-1],), ln_w.float(), None, 1e-5).to(torch.bfloat16) if ln_w is not None else x
+    y = (h.float() @ w.float().t()).to(torch.bfloat16)
+    if epi == 'gelu':
+        y = F.gelu(y.float()).to(torch.bfloat16)
+    if epi == 'residual':
+        y = (res.float() + y.float()).to(torch.bfloat16)
+    return y
+
+
+@pytest.mark.parametrize('M,N,KD,ln,epi', [(32, 2304, 768, True, None), (32, 768, 768, False, 'residual'),
+                                          (32, 3072, 768, True, 'gelu'), (32, 768, 3072, False, 'residual'),
+                                          (5, 40, 64, True, None), (33, 100, 128, False, None),
+                                          (1, 50304, 768, True, None)])
+def test_rowmm_matches_op_chain(M, N, KD, ln, epi):
+    print('case', M, N, KD, ln, epi, flush=True)
+    g = torch.Generator().manual_seed(M + N + KD)
+    x = torch.randn(M, KD, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, KD, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    lw = (1 + 0.1 * torch.randn(KD, generator=g)).to(torch.bfloat16).to(DEV) if ln else None
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV) if epi == 'residual' else None
+    want = _chain(x, w, lw, epi, res).float()
+    got = K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, out=None).float()
+    err = (got - want).abs()
+    # one bf16 rounding step of the result (2^-8 relative) where a rounding flip occurs upstream
+    assert (err <= want.abs() * 2 ** -7 + 2e-3).float().mean().item() > 0.999, err.max().item()
+    assert err.max().item() < 0.05 * max(1.0, want.abs().max().item())
+
+
+def test_argmax_rows_first_maximum():
+    x = torch.zeros(3, 50304, dtype=torch.bfloat16)
+    x[0, 7] = 1; x[0, 900] = 1
+    x[1, 50303] = 2
+    x[2] = -1; x[2, 12345] = 0.5
+    got = K.argmax_rows(x.to(DEV)).cpu().tolist()
+    assert got == [7, 50303, 12345]

@@ -202,3 +202,58 @@ def test_graph_replays_match_eager():
         tb = K.argmax_rows(lg)
         assert torch.equal(a.g_tok, tb), r
         assert int(a.g_t[0]) == 49 + r
+
+
+def test_fused_bf16_decode_matches_oracle_engine():
+    """The bf16 decode step built from the row-block kernels (LN+QKV, projection+residual, LN+FC+GELU,
+    MLP+residual, LN+logits) against the oracle engine running the reference op chain in bf16 on the CPU."""
+    cfg = tiny(seq_len=256, n_embd=128, n_head=2, leaf=8, neighbors=False, wmax=4, beam=4, vocab_size=96)
+    torch.manual_seed(10)
+    model = GPT(cfg).eval()
+    sd = {k: v.to(torch.bfloat16) for k, v in model.state_dict().items()}
+    Wc = weights_from_ours(sd, cfg)
+    Wg = weights_from_ours({k: v.to(DEV) for k, v in sd.items()}, cfg)
+    dec = Decoder(Wg, 2, 2, 128, 256, 'seg', cfg, DEV, batch=2)
+    assert dec.fused
+    refs = [DecoderRef(Wc, 2, 2, 128, 256, 'seg', cfg, act_dtype=torch.bfloat16, sel_mode='canonical') for _ in range(2)]
+    g = torch.Generator().manual_seed(11)
+    toks = torch.randint(0, 96, (2, 40), generator=g)
+    worst = 0.0
+    for t in range(40):
+        lg, _ = dec.step(toks[:, t].to(DEV), t)
+        for s in range(2):
+            lr, _ = refs[s].step(int(toks[s, t]), t)
+            worst = max(worst, (lg[s].float().cpu() - lr).abs().max().item())
+    print('max |dlogit| fused bf16 decode vs oracle: %.3e' % worst)
+    assert worst < 3e-2
+
+
+def test_fused_groups_are_bit_identical_and_capture():
+    """Splitting the batch into sequence groups on parallel streams changes nothing: logits equal the
+    single-group step bit for bit, eagerly and as replays of a captured step."""
+    cfg = tiny(seq_len=256, n_embd=128, n_head=2, leaf=8, neighbors=False, wmax=4, beam=4, vocab_size=96)
+    torch.manual_seed(12)
+    model = GPT(cfg).eval()
+    sd = {k: v.to(torch.bfloat16).to(DEV) for k, v in model.state_dict().items()}
+    W = weights_from_ours(sd, cfg)
+    g = torch.Generator().manual_seed(13)
+    idx = torch.randint(0, 96, (6, 40), generator=g).to(DEV)
+    one = Decoder(W, 2, 2, 128, 256, 'seg', cfg, DEV, batch=6, groups=1)
+    three = Decoder(W, 2, 2, 128, 256, 'seg', cfg, DEV, batch=6, groups=3)
+    cap = Decoder(W, 2, 2, 128, 256, 'seg', cfg, DEV, batch=6, groups=3)
+    assert len(three.groups) == 3 and three.fused
+    for t in range(24):
+        a, _ = one.step(idx[:, t], t)
+        b, _ = three.step(idx[:, t], t)
+        c, _ = cap.step(idx[:, t], t)
+        assert torch.equal(a, b), t
+    tok = K.argmax_rows(a)
+    cap.capture(tok, 24)
+    tb = tok.clone()
+    for r in range(5):
+        cap.replay()
+        torch.cuda.synchronize()
+        lb, _ = one.step(tb, 24 + r)
+        assert torch.equal(cap.g_logits, lb), r
+        tb = K.argmax_rows(lb)
+        assert torch.equal(cap.g_tok, tb), r

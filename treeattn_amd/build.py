@@ -22,6 +22,7 @@ SOURCES = {
     'select.hip': ['-ffp-contract=off'],
     'attend.hip': [],
     'sample.hip': [],
+    'gemm.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

@@ -6,10 +6,10 @@
 namespace ta {
 
 template <typename T>
-__global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ x, int64_t n, int64_t stride,
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__ x, int64_t n, int64_t stride,
                                                           int64_t* __restrict__ out) {
-  __shared__ float s_val[256];
-  __shared__ int64_t s_idx[256];
+  __shared__ float s_val[1024];
+  __shared__ int64_t s_idx[1024];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * stride;
   float best = -INFINITY;
@@ -53,13 +53,13 @@ extern "C" int ta_argmax_rows(const void* x, int dtype, int64_t rows, int64_t n,
   dim3 grid((unsigned)rows);
   switch (dtype) {
     case TA_F32:
-      hipLaunchKernelGGL((argmax_rows_kernel<float>), grid, dim3(256), 0, st, (const float*)x, n, stride, out);
+      hipLaunchKernelGGL((argmax_rows_kernel<float>), grid, dim3(1024), 0, st, (const float*)x, n, stride, out);
       break;
     case TA_F16:
-      hipLaunchKernelGGL((argmax_rows_kernel<f16_t>), grid, dim3(256), 0, st, (const f16_t*)x, n, stride, out);
+      hipLaunchKernelGGL((argmax_rows_kernel<f16_t>), grid, dim3(1024), 0, st, (const f16_t*)x, n, stride, out);
       break;
     case TA_BF16:
-      hipLaunchKernelGGL((argmax_rows_kernel<bf16_t>), grid, dim3(256), 0, st, (const bf16_t*)x, n, stride, out);
+      hipLaunchKernelGGL((argmax_rows_kernel<bf16_t>), grid, dim3(1024), 0, st, (const bf16_t*)x, n, stride, out);
       break;
     default:
       set_error("unknown dtype");

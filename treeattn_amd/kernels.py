@@ -180,6 +180,30 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
     return out, lse, keys
 
 
+# ----------------------------------------------------------------------------------------------- row-block GEMM
+_EPI = {None: 0, 'gelu': 1, 'residual': 2}
+
+
+def rowmm_supported(x, w):
+    return x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.shape[-1] % 64 == 0
+
+
+def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None):
+    """epilogue(LN(x) @ w.T) for a few rows, bf16: x (M,K), w (N,K) -> (M,N).  epilogue None | 'gelu' |
+    'residual' (adds `residual`, (M,N)); `out` may be `residual`."""
+    L.require_gpu(x, w)
+    M, K = x.shape
+    N = w.shape[0]
+    if x.stride(1) != 1 or w.stride(1) != 1:
+        raise ValueError('rowmm: rows must be contiguous')
+    if out is None:
+        out = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    r = residual if epilogue == 'residual' else None
+    L.call('ta_rowmm', L.ptr(x), x.stride(0), L.ptr(w), w.stride(0), L.ptr(out), out.stride(0), L.ptr(r),
+           r.stride(0) if r is not None else 0, L.ptr(ln_w), float(eps), M, N, K, _EPI[epilogue], L.stream())
+    return out
+
+
 # ----------------------------------------------------------------------------------------------- sampling
 def argmax_rows(x, out=None):
     """First index of the maximum of every row of x (R, n) -> (R,) int64."""
