@@ -45,7 +45,6 @@ struct AttnParams {
 
 constexpr float kNegBig = -1e30f;
 constexpr int kWavesPerBlock = 4;
-
 template <typename T> struct Raw16;  // 16 bytes of T -> EPL floats
 template <> struct Raw16<float> {
   static constexpr int EPL = 4;
