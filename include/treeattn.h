@@ -101,8 +101,12 @@ int ta_gather_dot(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t 
 /*
  * Leaf-block gather-dot: the candidates of a query are whole blocks of `block` consecutive rows,
  * out[b,h,n, c*block + j] = scale * q[b,h,n] . K[b,h, blk[b,h,n,c]*block + j] (fastseg.py:118-130 with
- * cand = blk*block + arange(block)).  blk: (B,H,N,NB) int32 contiguous, ids in [0, M/block).
- * Same dtype for q and K; out (B,H,N,NB*block) float32 contiguous.
+ * cand = blk*block + arange(block)).  blk: (B,H,N,NB) int32 contiguous, ids in [0, M/block) (ids outside
+ * are clamped to that range).  Same dtype for q and K; out (B,H,N,NB*block) float32 contiguous.
+ * For bf16/f16 with D in {64, 128}, block in {32, 64, 128}, M a multiple of block, NB <= 64 and 16-byte
+ * aligned rows, the scores come from matrix-core products of the exact bf16/f16 values with float32
+ * accumulation (a few ulps from a sequential float32 sum); other shapes use the canonical order of
+ * ta_gather_dot.
  */
 int ta_gather_dot_blocks(const void* q, const void* K, int dtype,
                          int64_t qsb, int64_t qsh, int64_t qsn, int64_t ksb, int64_t ksh, int64_t ksn,

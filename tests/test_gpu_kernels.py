@@ -119,15 +119,23 @@ def test_gather_dot_bit_exact(dtype, D):
     assert (got - faithful).abs().max().item() < 1e-5
 
 
-def test_gather_dot_blocks_bit_exact():
-    B, H, T, D, NB, blk = 2, 2, 512, 64, 4, 64
-    q = rnd(B, H, T, D, seed=4, dtype=torch.bfloat16)
-    Km = rnd(B, H, T, D, seed=5, dtype=torch.bfloat16)
+@pytest.mark.parametrize('T,D,NB,blk,dtype,N', [(512, 64, 4, 64, torch.bfloat16, 512), (4096, 64, 16, 64, torch.bfloat16, 200),
+                                               (1024, 128, 8, 128, torch.bfloat16, 77), (512, 64, 5, 32, torch.float16, 96),
+                                               (512, 16, 4, 64, torch.bfloat16, 64)])
+def test_gather_dot_blocks(T, D, NB, blk, dtype, N):
+    """Block gather-dot against the oracle: matrix-core path within a few float32 ulps of the canonical sum
+    (exact bf16 products, different summation order); the canonical path (D=16) bit for bit."""
+    B, H = 2, 2
+    q = rnd(B, H, N, D, seed=4, dtype=dtype)
+    Km = rnd(B, H, T, D, seed=5, dtype=dtype)
     g = torch.Generator().manual_seed(6)
-    idx = torch.randint(0, T // blk, (B, H, T, NB), generator=g, dtype=torch.int32)
+    idx = torch.randint(0, T // blk, (B, H, N, NB), generator=g, dtype=torch.int32)
     got = K.gather_dot_blocks(q.to(DEV), Km.to(DEV), idx.to(DEV), blk).cpu()
     want = o_gather_blocks(q, Km, idx, blk)
-    assert torch.equal(got, want)
+    if D == 16:
+        assert torch.equal(got, want)
+    else:
+        assert (got - want).abs().max().item() <= 2e-5 * max(1.0, want.abs().max().item())
 
 
 @pytest.mark.parametrize('dtype,D', [(torch.float32, 64), (torch.bfloat16, 64), (torch.bfloat16, 128),

@@ -23,6 +23,7 @@ SOURCES = {
     'attend.hip': [],
     'sample.hip': [],
     'gemm.hip': [],
+    'gather_blocks.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

@@ -544,6 +544,9 @@ extern "C" int ta_gather_dot_blocks(const void* q, const void* K, int dtype, int
     set_error("ta_gather_dot_blocks: rows not aligned");
     return TA_ERR_ARG;
   }
+  const int rc = gather_blocks_mfma(q, K, dtype, qsb, qsh, qsn, ksb, ksh, ksn, blk, B, H, N, M, NB, block, D, scale,
+                                    out, stream);
+  if (rc != TA_ERR_UNSUPPORTED) return rc;
   return dispatch_dt_d<GatherDotRun>(dtype, D, dtype, q, qsb, qsh, qsn, K, ksb, ksh, ksn, (const int32_t*)nullptr, blk,
                                      log2i(block), NB, B, H, N, M, NB * block, scale, out, (hipStream_t)stream);
 }
