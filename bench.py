@@ -74,6 +74,19 @@ def descent_nodes(t, shape, wmax):
     return total
 
 
+def recorded_traffic(name):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter summary (FETCH_SIZE and
+    WRITE_SIZE passes scaled by a calibration copy), or None when not recorded."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'decode_attention_traffic.md')
+    try:
+        for line in open(path):
+            if line.startswith('traffic_bytes_per_launch ' + name + ':'):
+                return int(line.split(':')[1])
+    except OSError:
+        return None
+    return None
+
+
 def time_launches(fn, iters):
     """Average duration (us) of fn's GPU work, from HIP events recorded on the launching stream."""
     st = torch.cuda.current_stream()
@@ -250,7 +263,10 @@ def main():
                    'tcap': Tcap, 'prefill_s': round(prefill_s, 2)},
         'roofline': {'bound': 'hbm', 'kernel': 'attn_kernel<bf16_t, 64, true> (split decode attention, one layer)',
                      'achieved': round(attn_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': round(attn_gbs / HBM_PEAK_GBS, 4), 'traffic': None,
+                     'frac': round(attn_gbs / HBM_PEAK_GBS, 4),
+                     'traffic': recorded_traffic('attn_kernel_decode'),
+                     'traffic_source': 'profiles/decode_attention_traffic.md (rocprofv3 FETCH_SIZE x2.0 + '
+                                       'WRITE_SIZE x1.0, calibrated on a 256 MiB copy)',
                      'bytes_per_launch': int(attn_bytes), 'avg_us': round(attn_us, 2),
                      'keys_per_query': round(keys_total / (B * H), 1)},
         'kernels': {'descend_us': round(desc_us, 2), 'descend_GB/s': round(desc_gbs, 1),
