@@ -88,6 +88,21 @@ int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_
                     int32_t* ids, uint8_t* vld, float* sct, void* stream);
 
 /*
+ * One decode position per (sequence, head): ta_tree_descend of q (B,H,1,D) at t = t_pos[b], and, in the same
+ * launch, ta_kv_append of k_new / v_new at row t_pos[b] (the selection and cache update of one decode step,
+ * engine.py:96-105 then engine.py:41-55).  The descent reads only nodes that end before t and the append
+ * writes row t and the nodes ending at t, so the results equal the two calls made one after the other.
+ * q, k_new, v_new and the caches share dtype; B*H < 4096; the levels are written (the append's nodes).
+ */
+int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
+                           const int32_t* t_pos, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                           const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl,
+                           int32_t* ids, uint8_t* vld, float* sct,
+                           const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
+                           int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
+                           void* stream);
+
+/*
  * Scores of queries against gathered rows (replaces fastseg.py:118-130 gather_dot and its kernel
  * fastseg.py:34-47).  out[b,h,n,c] = scale * q[b,h,n] . S[b,h,clamp(cand[b,h,n,c], 0, M-1)], float32,
  * canonical order.  q: (B,H,N,D) q_dtype; S: (B,H,M,D) s_dtype; cand: (B,H,N,C) int32 contiguous;
@@ -136,10 +151,12 @@ int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype,
  * each position once.  q: (B,H,Nq,D) with strides; k, v: (B,H,Tk,D) with strides (the whole sequence or a
  * KV cache); positions outside [0, Tk) are never read (a query with t >= Tk attends nothing).  ids/vld: (B,H,Nq,wl) contiguous.  out: (B,H,Nq,D) in the input dtype with strides; lse:
  * (B,H,Nq) float32 or NULL; keys: (B,H,Nq) float32 number of keys attended, or NULL.
- * nsplit is 1 (one wavefront per query) or a multiple of 4: the keys of every query are split over nsplit
- * wavefronts (for few queries with many keys, as in decode), 4 per workgroup merged in LDS; with more
- * than 4, nsplit/4 workgroups per query write partials to ws (ta_seg_attn_workspace_size(...) bytes) and
- * a second kernel merges them.  Calls that share a workspace must not run concurrently.
+ * nsplit is 1 (one wavefront per query) or a multiple of 4 up to 256: the keys of every query are split
+ * over nsplit wavefronts (for few queries with many keys, as in decode), 4 per workgroup merged in LDS; with
+ * more than 4, nsplit/4 workgroups per query write partials to ws (ta_seg_attn_workspace_size(...) bytes,
+ * 256-byte aligned, zero-filled once when allocated: its head holds per-query counters that every call
+ * leaves at zero) and the last workgroup of each query merges them.  Calls that share a workspace must not
+ * run concurrently.
  */
 int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int nsplit);
 int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype,
@@ -173,10 +190,15 @@ int ta_kv_append(const void* k_new, const void* v_new, int dtype,
  *   epilogue 0: none, 1: GELU (erf), 2: residual add R + (.).  Each op's result is rounded to bf16 as in
  * the unfused chain.  Row strides ldx, ldw, ldy, ldr in elements; K a multiple of 64; X, W, ln_w 16-byte
  * aligned.  Y may be the same buffer as R.
+ * splits > 1 divides K among that many workgroups per 32 x 32 output tile (clamped to K/64); their float32
+ * partials go to the workspace `ws` (ta_rowmm_workspace_size bytes, 256-byte aligned, zero-filled once when
+ * allocated: its head holds per-tile counters that every call leaves at zero) and are summed in split order,
+ * so results are deterministic.  Calls that share a workspace must not overlap in time.
  */
+int64_t ta_rowmm_workspace_size(int M, int N, int K, int splits);
 int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy,
              const void* R, int64_t ldr, const void* ln_w, float ln_eps, int M, int N, int K,
-             int epilogue, void* stream);
+             int epilogue, int splits, void* ws, int64_t ws_bytes, void* stream);
 
 /*
  * Row-wise argmax for greedy decoding (replaces logits.argmax(-1) of the reference's greedy loop,

@@ -187,6 +187,34 @@ def test_seg_attn_matches_oracle(T, D, leaf, arity, wmax, dtype, beam, nsplit):
     assert torch.equal(keys, keep.sum(-1).float())
 
 
+def test_seg_attn_split_merge_reuses_workspace():
+    """Several workgroups per query, merged by the last to arrive: a workspace reused across calls (its
+    counters return to zero) gives identical results each time, and output and LSE agree with one workgroup
+    per query, up to the maximum split."""
+    B, H, T, D, leaf, wmax = 2, 3, 2048, 64, 16, 8
+    q, k, v = [rnd(B, H, T, D, seed=s) for s in (50, 51, 52)]
+    geom = S.Geometry(T, leaf, 2)
+    tq = torch.arange(T - 64, T)
+    qs = q[:, :, T - 64:].contiguous()
+    ids, vld, _ = S.tree_pass_general(qs, S.pyramid(S.index_keys(k), geom), tq, geom, wmax, 'canonical')
+    gi = torch.where(vld, ids, -1).to(torch.int32).to(DEV)
+    vl = vld.to(torch.uint8).to(DEV)
+    args = (qs.to(DEV), k.to(DEV), v.to(DEV), tq.to(DEV), gi, vl, None, leaf, 3, 1 / math.sqrt(D))
+    lse0 = torch.empty(B, H, 64, device=DEV)
+    base, _, _ = K.seg_attn(*args, lse=lse0, nsplit=4)
+    for nsplit in (8, 36, 256):
+        ws = K.seg_attn_workspace(B, H, 64, D, nsplit, DEV)
+        outs = []
+        for _ in range(3):
+            lse = torch.empty(B, H, 64, device=DEV)
+            o, _, _ = K.seg_attn(*args, lse=lse, nsplit=nsplit, ws=ws)
+            outs.append((o.clone(), lse.clone()))
+        for o, l in outs[1:]:
+            assert torch.equal(o, outs[0][0]) and torch.equal(l, outs[0][1]), nsplit
+        assert (outs[0][0] - base).abs().max().item() < 1e-5, nsplit
+        assert (outs[0][1] - lse0).abs().max().item() < 1e-5, nsplit
+
+
 def test_kv_append_matches_state_add():
     """Appending positions one by one forms the same nodes as the oracle's SegState.add, bit for bit."""
     Tcap, H, D, leaf, arity = 512, 3, 64, 8, 4
@@ -261,3 +289,93 @@ def test_argmax_rows_first_maximum():
     x[2] = -1; x[2, 12345] = 0.5
     got = K.argmax_rows(x.to(DEV)).cpu().tolist()
     assert got == [7, 50303, 12345]
+
+
+@pytest.mark.parametrize('M,N,KD,ln,epi', [(32, 2304, 768, True, None), (32, 768, 3072, False, 'residual'),
+                                          (7, 96, 640, True, 'gelu')])
+def test_rowmm_split_k(M, N, KD, ln, epi):
+    """K divided among workgroups: every split count agrees with the op chain, repeated calls sharing one
+    workspace give identical results (the tile counters return to zero), and graph replays match eager."""
+    print('case', M, N, KD, ln, epi, flush=True)
+    g = torch.Generator().manual_seed(7 * M + N + KD)
+    x = torch.randn(M, KD, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, KD, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    lw = (1 + 0.1 * torch.randn(KD, generator=g)).to(torch.bfloat16).to(DEV) if ln else None
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV) if epi == 'residual' else None
+    want = _chain(x, w, lw, epi, res).float()
+    for S in (2, 3, KD // 64, KD // 64 + 5):
+        ws = K.rowmm_workspace(M, N, KD, S, DEV)
+        a = K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, splits=S, ws=ws)
+        b = K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, splits=S, ws=ws)
+        assert torch.equal(a, b), S
+        err = (a.float() - want).abs()
+        assert (err <= want.abs() * 2 ** -7 + 2e-3).float().mean().item() > 0.999, (S, err.max().item())
+        assert err.max().item() < 0.05 * max(1.0, want.abs().max().item())
+    S = 4
+    ws = K.rowmm_workspace(M, N, KD, S, DEV)
+    eager = K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, splits=S, ws=ws)
+    out = torch.zeros_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, out=out, splits=S, ws=ws)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr, stream=s):
+            K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, out=out, splits=S, ws=ws)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.zero_()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, splits=S, ws=ws), eager)
+
+
+def test_rowmm_split_needs_workspace():
+    x = torch.zeros(32, 768, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(768, 768, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match='workspace'):
+        K.rowmm(x, w, splits=4, ws=None)
+
+
+@pytest.mark.parametrize('leaf,arity,B,H,dtype', [(8, 2, 2, 3, torch.float32), (16, 4, 1, 2, torch.bfloat16),
+                                                  (64, 2, 32, 12, torch.bfloat16)])
+def test_descend_append_equals_two_calls(leaf, arity, B, H, dtype):
+    """The fused decode launch (descent + cache append) gives the same selection, caches and nodes, bit for
+    bit, as the descent followed by the append, over positions that complete leaf blocks and higher nodes."""
+    print('case', leaf, arity, B, H, dtype, flush=True)
+    Tcap, D, wmax = 1024, 64, 4
+    shape = K.TreeShape(Tcap, leaf, arity)
+    t0 = 5 * leaf * arity - 3
+    kk = rnd(B, H, Tcap, D, seed=60, dtype=dtype).to(DEV)
+    vv = rnd(B, H, Tcap, D, seed=61, dtype=dtype).to(DEV)
+    qq = rnd(B, H, 8, D, seed=62, dtype=dtype).to(DEV)
+    state = []
+    for _ in range(2):
+        Kc = torch.zeros(B, H, Tcap, D, device=DEV, dtype=dtype)
+        Vc = torch.zeros_like(Kc)
+        Kc[:, :, :t0] = kk[:, :, :t0]
+        Vc[:, :, :t0] = vv[:, :, :t0]
+        levels = shape.alloc_levels(B, H, D, DEV)
+        for lv in levels:
+            lv.zero_()
+        K.level_sums(Kc, shape.blevels, out=levels, t_end=t0)
+        state.append((Kc, Vc, levels))
+    wl = shape.leaf_width(wmax)
+    for step in range(8):
+        t = t0 + step
+        tpos = torch.full((B,), t, dtype=torch.int32, device=DEV)
+        q = qq[:, :, step:step + 1]
+        Kc, Vc, levels = state[0]
+        a = K.tree_descend(q, levels, tpos.view(B, 1), shape, wmax)
+        K.kv_append(kk[:, :, t], vv[:, :, t], Kc, Vc, tpos, levels, leaf, arity)
+        Kc2, Vc2, levels2 = state[1]
+        outs = (torch.empty(B, H, 1, wl, dtype=torch.int32, device=DEV),
+                torch.empty(B, H, 1, wl, dtype=torch.uint8, device=DEV), torch.empty(B, H, 1, wl, device=DEV))
+        bb = K.tree_descend_append(q, levels2, tpos, shape, wmax, kk[:, :, t], vv[:, :, t], Kc2, Vc2, out=outs)
+        for x, y in zip(a, bb):
+            assert torch.equal(x, y), step
+    assert torch.equal(state[0][0], state[1][0]) and torch.equal(state[0][1], state[1][1])
+    for x, y in zip(state[0][2], state[1][2]):
+        assert torch.equal(x, y)

@@ -6,14 +6,16 @@
 // K and V rows (a leaf block is a run of consecutive rows, so a chunk reads contiguous memory), keeps a
 // running max/sum (online softmax, float32) and its own weighted V accumulator; the wavefront reduces
 // the accumulators once at the end.  In split mode (few queries with many keys, as in decode) the four
-// wavefronts of a workgroup share a query and merge in LDS; more workgroups per query write partials that a
-// small merge kernel combines.
+// wavefronts of a workgroup share a query and merge in LDS; with more workgroups per query each writes its
+// partial through to memory and the last of them to arrive (counted with a device-wide atomic) merges the
+// partials and writes the output.
 //
 // Reference functions replaced: fastseg.py:50-78 (_attn_fwd), fastseg.py:134-177 (sparse_attn),
 // fastseg.py:367-383 (candidate assembly + dedupe_fast), engine.py:107-119 (decode attention),
 // engine.py:41-55 (SegState.add).
 #include <utility>
 
+#include "append.hpp"
 #include "common.hpp"
 
 namespace ta {
@@ -41,6 +43,7 @@ struct AttnParams {
   float* lse;
   float* keys;
   float* ws;            // per-workgroup partials (query, gsplit, D + 2) when gsplit > 1
+  uint32_t* cnt;        // per-query arrival counters when gsplit > 1 (zero between calls)
 };
 
 constexpr float kNegBig = -1e30f;
@@ -81,7 +84,10 @@ template <> struct Raw16<f16_t> {
 //   SPLIT = false: one wavefront per query (many queries: prefill).
 //   SPLIT = true: the 4 wavefronts of a workgroup share one query and interleave its chunks; their partial
 //   (max, sum, accumulator) are merged in LDS.  With gsplit > 1 workgroups per query each writes its merged
-//   partial to ws and merge_kernel combines them.
+//   partial to ws with stores that write through to memory, waits for them to complete and counts itself in;
+//   the last to arrive reads the partials past the caches, combines them
+//   (out = sum_g acc_g e^(m_g - M) / sum_g L_g e^(m_g - M)) and resets the counter.  No workgroup waits for
+//   another.
 template <typename T, int D, bool SPLIT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   constexpr int EPL = Raw16<T>::EPL;
@@ -289,12 +295,52 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
         float a = 0.0f;
 #pragma unroll
         for (int s = 0; s < kWavesPerBlock; ++s) a += red[s * (D + 2) + 2 + d] * sc[s];
-        part[2 + d] = a;
+        __hip_atomic_store(part + 2 + d, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
       if (lane == 0) {
-        part[0] = M;
-        part[1] = Lt;
+        __hip_atomic_store(part, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(part + 1, Lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         if (g == 0 && p.keys) p.keys[qi] = (float)N;
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial has reached memory
+      int last = 0;
+      if (lane == 0)
+        last = __hip_atomic_fetch_add(p.cnt + qi, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+               (uint32_t)(p.gsplit - 1);
+      if (!__shfl(last, 0, kWave)) return;
+      // last workgroup of this query: lane s holds partial s's (max, sum); gsplit <= 64
+      const float* base = p.ws + qi * p.gsplit * (D + 2);
+      float ms = kNegBig, Ls = 0.0f;
+      if (lane < p.gsplit) {
+        ms = __hip_atomic_load(base + lane * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        Ls = __hip_atomic_load(base + lane * (D + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+      const float Mq = wave_max(Ls > 0.0f ? ms : kNegBig);
+      const float fac = Ls > 0.0f ? __expf(ms - Mq) : 0.0f;
+      const float Lq = wave_sum(Ls * fac);
+      const float inv = Lq > 0.0f ? 1.0f / Lq : 0.0f;
+      float* s_fac = reinterpret_cast<float*>(s_ext);   // the static-key list is no longer needed
+      s_fac[lane] = fac;
+      wave_sync();
+      T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh + n * p.osn;
+      for (int d = lane; d < D; d += kWave) {
+        float a = 0.0f;
+        for (int s0 = 0; s0 < p.gsplit; s0 += 8) {
+          float pv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            pv[i] = s0 + i < p.gsplit ? __hip_atomic_load(base + (s0 + i) * (D + 2) + 2 + d, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_SYSTEM)
+                                      : 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (s0 + i < p.gsplit) a += pv[i] * s_fac[s0 + i];
+        }
+        orow[d] = from_f32<T>(a * inv);
+      }
+      if (lane == 0) {
+        if (p.lse) p.lse[qi] = Lq > 0.0f ? Mq + __logf(Lq) : kNegBig;
+        __hip_atomic_store(p.cnt + qi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);   // ready for the next call
       }
       return;
     }
@@ -324,39 +370,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   }
 }
 
-// Combine the gsplit workgroup partials of every query: out = sum_g acc_g e^(m_g - M) / sum_g L_g e^(m_g - M).
-template <typename T, int D>
-__global__ __launch_bounds__(128) void merge_kernel(const float* __restrict__ ws, int gsplit, int H, int Nq,
-                                                    void* out, int64_t osb, int64_t osh, int64_t osn,
-                                                    float* __restrict__ lse) {
-  const int64_t qi = blockIdx.x;
-  const int n = (int)(qi % Nq);
-  const int bh = (int)(qi / Nq);
-  const int b = bh / H, h = bh % H;
-  const float* base = ws + qi * gsplit * (D + 2);
-  float M = kNegBig;
-  for (int s = 0; s < gsplit; ++s) {
-    const float* ps = base + s * (D + 2);
-    if (ps[1] > 0.0f) M = fmaxf(M, ps[0]);
-  }
-  float L = 0.0f;
-  for (int s = 0; s < gsplit; ++s) {
-    const float* ps = base + s * (D + 2);
-    if (ps[1] > 0.0f) L += ps[1] * __expf(ps[0] - M);
-  }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  T* orow = reinterpret_cast<T*>(out) + b * osb + h * osh + n * osn;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float a = 0.0f;
-    for (int s = 0; s < gsplit; ++s) {
-      const float* ps = base + s * (D + 2);
-      if (ps[1] > 0.0f) a += ps[2 + d] * __expf(ps[0] - M);
-    }
-    orow[d] = from_f32<T>(a * inv);
-  }
-  if (threadIdx.x == 0 && lse) lse[qi] = L > 0.0f ? M + __logf(L) : kNegBig;
-}
-
 // ----------------------------------------------------------------------------------------- decode append
 struct LevelRW {
   float* ptr[kMaxLevels];
@@ -364,9 +377,7 @@ struct LevelRW {
   int64_t sh[kMaxLevels];
 };
 
-// One thread per dimension of one (sequence, head).  Writes row t of K and V, then forms the nodes whose
-// last position is t: the leaf block from its keys, each higher node from its children, both as
-// adjacent-pair sums (carry stack in LDS, one column per thread).
+// One thread per dimension of one (sequence, head): append_dim.
 template <typename T>
 __global__ __launch_bounds__(256) void kv_append_kernel(const T* __restrict__ kn, const T* __restrict__ vn,
                                                         int64_t nsb, int64_t nsh, int64_t vnsb, int64_t vnsh,
@@ -381,46 +392,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const T* __restrict__ kn
   const int b = bh / H, h = bh % H;
   const int t = t_pos[b];
   if (t < 0 || t >= Tcap) return;
-  T* krow = Kc + b * csb + h * csh;
-  T* vrow = Vc + b * csb + h * csh;
-  const T kx = kn[b * nsb + h * nsh + d];
-  krow[(int64_t)t * cst + d] = kx;
-  vrow[(int64_t)t * cst + d] = vn[b * vnsb + h * vnsh + d];
-  if (n_levels == 0) return;
-  const int leaf = 1 << leaf_log2;
-  if (((t + 1) & (leaf - 1)) != 0) return;
-  // leaf block [t+1-leaf, t]
-  const int p0 = t + 1 - leaf;
-  float x = 0.0f;
-  for (int i = 0; i < leaf; ++i) {
-    const int pp = p0 + i;
-    x = pp == 0 ? 0.0f : (pp == t ? to_f32(kx) : to_f32(krow[(int64_t)pp * cst + d]));
-    int lvl = 0;
-    while ((i >> lvl) & 1) {
-      x = __fadd_rn(stk[lvl * D + d], x);
-      ++lvl;
-    }
-    stk[lvl * D + d] = x;
-  }
-  float* base0 = lv.ptr[0] + b * lv.sb[0] + h * lv.sh[0];
-  base0[(int64_t)(t >> leaf_log2) * D + d] = x;
-  const int arity = 1 << arity_log2;
-  for (int j = 1; j < n_levels; ++j) {
-    const int lj = leaf_log2 + j * arity_log2;
-    if (((t + 1) & ((1 << lj) - 1)) != 0) break;
-    const int64_t node = t >> lj;
-    const float* child = lv.ptr[j - 1] + b * lv.sb[j - 1] + h * lv.sh[j - 1] + node * arity * D + d;
-    for (int c = 0; c < arity; ++c) {
-      x = child[(int64_t)c * D];
-      int lvl = 0;
-      while ((c >> lvl) & 1) {
-        x = __fadd_rn(stk[lvl * D + d], x);
-        ++lvl;
-      }
-      stk[lvl * D + d] = x;
-    }
-    lv.ptr[j][b * lv.sb[j] + h * lv.sh[j] + node * D + d] = x;
-  }
+  append_dim<T>(d, D, t, kn + b * nsb + h * nsh, vn + b * vnsb + h * vnsh, Kc + b * csb + h * csh,
+                Vc + b * csb + h * csh, cst, n_levels, leaf_log2, arity_log2, stk,
+                [&](int j) { return lv.ptr[j] + b * lv.sb[j] + h * lv.sh[j]; });
 }
 
 // ----------------------------------------------------------------------------------------- host side
@@ -447,12 +421,7 @@ int launch_attn(const AttnParams& p, int B, bool split, hipStream_t st) {
     lds += (size_t)kWavesPerBlock * (D + 2) * sizeof(float);
     dim3 grid((unsigned)((int64_t)p.Nq * p.gsplit), B * p.H);
     hipLaunchKernelGGL((attn_kernel<T, D, true>), grid, dim3(kWavesPerBlock * kWave), lds, st, p);
-    int rc = check_launch("attn_kernel");
-    if (rc || p.gsplit == 1) return rc;
-    dim3 mg((unsigned)((int64_t)B * p.H * p.Nq));
-    hipLaunchKernelGGL((merge_kernel<T, D>), mg, dim3(D < 128 ? D : 128), 0, st, p.ws, p.gsplit, p.H, p.Nq, p.out,
-                       p.osb, p.osh, p.osn, p.lse);
-    return check_launch("merge_kernel");
+    return check_launch("attn_kernel");
   }
   dim3 grid((unsigned)((p.Nq + kWavesPerBlock - 1) / kWavesPerBlock), B * p.H);
   hipLaunchKernelGGL((attn_kernel<T, D, false>), grid, dim3(kWavesPerBlock * kWave), lds, st, p);
@@ -510,10 +479,15 @@ extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, i
   return dispatch_attn(dtype, D, p, B, false, (hipStream_t)stream);
 }
 
+namespace {
+// workspace: per-query counters (rounded up to 256 bytes), then the partials
+int64_t attn_counter_bytes(int B, int H, int Nq) { return ((int64_t)B * H * Nq * 4 + 255) / 256 * 256; }
+}  // namespace
+
 extern "C" int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int nsplit) {
   const int gsplit = nsplit / kWavesPerBlock;
-  if (gsplit <= 1) return 0;
-  return (int64_t)B * H * Nq * gsplit * (D + 2) * (int64_t)sizeof(float);
+  if (gsplit <= 1 || B <= 0 || H <= 0 || Nq <= 0) return 0;
+  return attn_counter_bytes(B, H, Nq) + (int64_t)B * H * Nq * gsplit * (D + 2) * (int64_t)sizeof(float);
 }
 
 extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
@@ -523,8 +497,8 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
                                int local, float scale, void* out, int64_t osb, int64_t osh, int64_t osn, float* lse,
                                float* keys, int nsplit, float* ws, int64_t ws_bytes, void* stream) {
   if (B <= 0 || H <= 0 || Nq < 0 || wl < 0 || nsplit < 1 || leaf < 2 || (leaf & (leaf - 1)) ||
-      (nsplit > 1 && nsplit % kWavesPerBlock)) {
-    set_error("ta_seg_attn_fwd: bad sizes (nsplit must be 1 or a multiple of 4)");
+      (nsplit > 1 && nsplit % kWavesPerBlock) || nsplit > kWavesPerBlock * kWave) {
+    set_error("ta_seg_attn_fwd: bad sizes (nsplit must be 1 or a multiple of 4, at most 256)");
     return TA_ERR_ARG;
   }
   const int Lw = local > 3 ? local : 3;
@@ -537,8 +511,9 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
     return TA_ERR_UNSUPPORTED;
   }
   if (Nq == 0) return TA_OK;
-  if (ws_bytes < ta_seg_attn_workspace_size(B, H, Nq, D, nsplit)) {
-    set_error("ta_seg_attn_fwd: workspace too small");
+  const int64_t need = ta_seg_attn_workspace_size(B, H, Nq, D, nsplit);
+  if (ws_bytes < need || (need > 0 && (ws == nullptr || (uintptr_t)ws % 256))) {
+    set_error("ta_seg_attn_fwd: workspace missing, too small or not 256-byte aligned");
     return TA_ERR_WORKSPACE;
   }
   if (!kv_aligned(q, dtype, D, {qsb, qsh, qsn}) || !kv_aligned(k, dtype, D, {ksb, ksh, kst}) ||
@@ -560,7 +535,11 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
   p.scale = scale;
   p.gsplit = nsplit > 1 ? nsplit / kWavesPerBlock : 1;
   p.out = out; p.osb = osb; p.osh = osh; p.osn = osn;
-  p.lse = lse; p.keys = keys; p.ws = ws;
+  p.lse = lse; p.keys = keys;
+  if (need > 0) {
+    p.cnt = reinterpret_cast<uint32_t*>(ws);
+    p.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + attn_counter_bytes(B, H, Nq));
+  }
   return dispatch_attn(dtype, D, p, B, nsplit > 1, (hipStream_t)stream);
 }
 

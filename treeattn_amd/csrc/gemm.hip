@@ -8,11 +8,15 @@
 // Rounding follows the unfused op chain in bf16: the LayerNorm output, the product and the GELU output are
 // each rounded to bf16, the residual sum is taken in float32 of the two bf16 values and rounded.
 //
-// One workgroup computes a 32 x 32 output tile; its eight wavefronts split K in blocks of 64, each issuing the
-// loads of up to four blocks before its first product, and their partial tiles are summed in LDS in a fixed
-// order.  A lane reads 64 contiguous bytes of one X row and one W
-// row per block: lanes 0-31 rows 0-31 at k0..k0+31, lanes 32-63 the same rows at k0+32..k0+63; MFMA j of the
-// block takes elements 8j..8j+7 of each lane's run, the same k positions for X and W.
+// One workgroup computes a 32 x 32 output tile over a range of K; its eight wavefronts split that range in
+// blocks of 64, each issuing the loads of up to four blocks before its first product, and their partial tiles
+// are summed in LDS in a fixed order.  With `splits` > 1 the K blocks are divided among that many workgroups
+// per tile (a few rows give too few tiles to occupy the chip): each writes its float32 partial tile to the
+// workspace and counts itself in with a device-scope atomic; the last to arrive sums the partials in split
+// order (so the result does not depend on arrival order), applies the epilogue and resets the counter.
+// A lane reads 64 contiguous bytes of one X row and one W row per block: lanes 0-31 rows 0-31 at k0..k0+31,
+// lanes 32-63 the same rows at k0+32..k0+63; MFMA j of the block takes elements 8j..8j+7 of each lane's run,
+// the same k positions for X and W.
 #include "common.hpp"
 
 namespace ta {
@@ -36,7 +40,8 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
                                                                 const bf16_t* __restrict__ W, int64_t ldw, bf16_t* Y,
                                                                 int64_t ldy, const bf16_t* R, int64_t ldr,
                                                                 const bf16_t* __restrict__ gam, float eps, int M, int N,
-                                                                int K) {
+                                                                int K, int splits, float* __restrict__ part,
+                                                                uint32_t* __restrict__ cnt) {
   constexpr int NT = kRowmmWaves * 64;
   __shared__ float s_mean[32], s_rstd[32];
   __shared__ float red[kRowmmWaves][32][33];
@@ -89,7 +94,15 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  const int nblk = K / 64;
+  // this workgroup's K blocks [blk0, blk1)
+  const int nblk_all = K / 64;
+  const int per = (nblk_all + splits - 1) / splits;
+  const int blk0 = blockIdx.z * per;
+  const int blk1 = blk0 + per < nblk_all ? blk0 + per : nblk_all;
+  const int nblk = blk1 - blk0;
+  xr += blk0 * 64;
+  wr += blk0 * 64;
+  const bf16_t* gk = LN ? gam + blk0 * 64 : gam;
   for (int base = 0; base < nblk; base += kRowmmWaves * kRowmmBlk) {
     uint4 xa[kRowmmBlk][4], wb[kRowmmBlk][4];
 #pragma unroll
@@ -113,7 +126,7 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
           const bf16_t* xe = reinterpret_cast<const bf16_t*>(&xa[i][j]);
 #pragma unroll
           for (int e = 0; e < 8; ++e) f[e] = to_f32(xe[e]);
-          load_row<bf16_t, 8>(gam + blk * 64 + kh + 8 * j, gg);
+          load_row<bf16_t, 8>(gk + blk * 64 + kh + 8 * j, gg);
           uint32_t o[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e)
@@ -134,28 +147,82 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
 #pragma unroll
   for (int i = 0; i < 16; ++i) red[w][8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)][lane & 31] = acc[i];
   __syncthreads();
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  if (splits > 1) {
+    // partial tile -> workspace; the last workgroup of the tile to arrive goes on to the epilogue
+    float* mine = part + ((int64_t)blockIdx.z * gridDim.x * gridDim.y + tile) * 1024;
+    for (int e = tid; e < 1024; e += NT) {
+      const int r = e >> 5, c = e & 31;
+      float v = red[0][r][c];
+#pragma unroll
+      for (int s = 1; s < kRowmmWaves; ++s) v += red[s][r][c];
+      __hip_atomic_store(&mine[e], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);   // written through
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wavefront's stores have completed
+    __syncthreads();
+    __shared__ uint32_t s_last;
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+               (uint32_t)(splits - 1);
+    __syncthreads();
+    if (!s_last) return;
+  }
   for (int e = tid; e < 1024; e += NT) {
     const int r = e >> 5, c = e & 31;
     const int gm = m0 + r, gn = n0 + c;
     if (gm < M && gn < N) {
-      float v = red[0][r][c];
+      float v;
+      if (splits > 1) {
+        const int64_t stride = (int64_t)gridDim.x * gridDim.y * 1024;
+        const float* p = part + (int64_t)tile * 1024 + e;
+        v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);   // bypassing the caches
+        for (int s = 1; s < splits; ++s)
+          v += __hip_atomic_load(p + s * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      } else {
+        v = red[0][r][c];
 #pragma unroll
-      for (int s = 1; s < kRowmmWaves; ++s) v += red[s][r][c];
+        for (int s = 1; s < kRowmmWaves; ++s) v += red[s][r][c];
+      }
       v = bf16_round(v);
       if constexpr (EPI == EPI_GELU) v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
       if constexpr (EPI == EPI_RESIDUAL) v = to_f32(R[(int64_t)gm * ldr + gn]) + v;
       Y[(int64_t)gm * ldy + gn] = bf16_from(v);
     }
   }
+  if (splits > 1 && tid == 0)   // ready for the next call
+    __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 }  // namespace ta
 
 using namespace ta;
 
+namespace {
+
+constexpr int64_t kRowmmCountBytes = 4096;   // tile counters at the head of the workspace
+
+int64_t rowmm_tiles(int M, int N) { return (int64_t)((N + 31) / 32) * ((M + 31) / 32); }
+
+int rowmm_splits(int K, int splits) {
+  const int nblk = K / 64;
+  if (splits < 1) splits = 1;
+  if (splits > nblk) splits = nblk;
+  const int per = (nblk + splits - 1) / splits;
+  return (nblk + per - 1) / per;   // no empty split
+}
+
+}  // namespace
+
+extern "C" int64_t ta_rowmm_workspace_size(int M, int N, int K, int splits) {
+  if (M <= 0 || N <= 0 || K < 64) return 0;
+  const int s = rowmm_splits(K, splits);
+  if (s <= 1) return 0;
+  return kRowmmCountBytes + (int64_t)s * rowmm_tiles(M, N) * 1024 * 4;
+}
+
 extern "C" int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy,
                         const void* R, int64_t ldr, const void* ln_w, float ln_eps, int M, int N, int K,
-                        int epilogue, void* stream) {
+                        int epilogue, int splits, void* ws, int64_t ws_bytes, void* stream) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64 || ldx < K || ldw < K || ldy < N ||
       (epilogue == EPI_RESIDUAL && (R == nullptr || ldr < N)) || epilogue < 0 || epilogue > 2) {
     set_error("ta_rowmm: bad sizes (K must be a multiple of 64)");
@@ -166,7 +233,22 @@ extern "C" int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, 
     set_error("ta_rowmm: X, W and the LayerNorm weight must be 16-byte aligned with 16-byte row strides");
     return TA_ERR_ARG;
   }
-  dim3 grid((N + 31) / 32, (M + 31) / 32);
+  const int S = rowmm_splits(K, splits);
+  float* part = nullptr;
+  uint32_t* cnt = nullptr;
+  if (S > 1) {
+    if (rowmm_tiles(M, N) * 4 > kRowmmCountBytes) {
+      set_error("ta_rowmm: too many output tiles for a split product (at most 1024)");
+      return TA_ERR_UNSUPPORTED;
+    }
+    if (ws == nullptr || ws_bytes < ta_rowmm_workspace_size(M, N, K, splits) || (uintptr_t)ws % 256) {
+      set_error("ta_rowmm: workspace missing, too small or not 256-byte aligned");
+      return TA_ERR_WORKSPACE;
+    }
+    cnt = (uint32_t*)ws;
+    part = (float*)((char*)ws + kRowmmCountBytes);
+  }
+  dim3 grid((N + 31) / 32, (M + 31) / 32, S);
   hipStream_t st = (hipStream_t)stream;
   const bf16_t* x = (const bf16_t*)X;
   const bf16_t* w = (const bf16_t*)W;
@@ -175,7 +257,7 @@ extern "C" int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, 
   const bf16_t* g = (const bf16_t*)ln_w;
 #define TA_LAUNCH(LNF, E)                                                                                   \
   hipLaunchKernelGGL((rowmm_kernel<LNF, E>), grid, dim3(kRowmmWaves * 64), 0, st, x, ldx, w, ldw, y, ldy, r, ldr, g, ln_eps, M, \
-                     N, K)
+                     N, K, S, part, cnt)
   if (ln_w) {
     if (epilogue == EPI_NONE) TA_LAUNCH(true, EPI_NONE);
     else if (epilogue == EPI_GELU) TA_LAUNCH(true, EPI_GELU);

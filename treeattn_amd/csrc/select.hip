@@ -7,13 +7,23 @@
 // seg.py:44-70 tree_pass, fastseg.py:254-271 tree_pass_fast, fastseg.py:118-130 gather_dot.
 #pragma clang fp contract(off)
 
+#include "append.hpp"
 #include "common.hpp"
 
 namespace ta {
 
 // ----------------------------------------------------------------------------------------- canonical dot
-// Lane j of a 16-lane group holds q and s elements [R*j, R*j + R).  In-lane halving tree, then an xor
-// butterfly over the 16 lanes (offsets 8, 4, 2, 1).  Every lane of the group returns the same value.
+// The value of lane (j -/+ n) mod 16 of this lane's 16-lane row (DPP row rotate by n).
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xF, 0xF, false));
+}
+
+// Lane j of a 16-lane group (a DPP row) holds q and s elements [R*j, R*j + R).  In-lane halving tree, then
+// the xor butterfly over the 16 lanes (partners j^8, j^4, j^2, j^1).  The partners are reached with row
+// rotates: rotating by 8 pairs j with j^8; after that step lanes j and j^8 hold the same value, so the value
+// at (j -/+ 4) mod 16 is the one at j^4, and likewise for 2 and 1.  Float addition being commutative, every
+// lane of the group returns the same value, bit for bit the butterfly's.
 template <int R>
 __device__ __forceinline__ float canon_dot(const float (&q)[R], const float (&s)[R]) {
   float p[R];
@@ -25,10 +35,10 @@ __device__ __forceinline__ float canon_dot(const float (&q)[R], const float (&s)
     for (int i = 0; i < n; ++i) p[i] = __fadd_rn(p[i], p[i + n]);
   }
   float x = p[0];
-  x = __fadd_rn(x, __shfl_xor(x, 8, kWave));
-  x = __fadd_rn(x, __shfl_xor(x, 4, kWave));
-  x = __fadd_rn(x, __shfl_xor(x, 2, kWave));
-  x = __fadd_rn(x, __shfl_xor(x, 1, kWave));
+  x = __fadd_rn(x, row_ror<8>(x));
+  x = __fadd_rn(x, row_ror<4>(x));
+  x = __fadd_rn(x, row_ror<2>(x));
+  x = __fadd_rn(x, row_ror<1>(x));
   return x;
 }
 
@@ -134,12 +144,38 @@ __device__ __forceinline__ void query_sync() {
   if constexpr (WPQ == 1) wave_sync(); else __syncthreads();
 }
 
-template <typename TQ, int D, int WPQ>
-__global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, int64_t qsb, int64_t qsh,
-                                                      int64_t qsn, int H, int Nq, int T, const int32_t* __restrict__ tq,
-                                                      int64_t tq_sb, LevelIn lv, int n_levels, int arity_log2,
-                                                      int wmax, int wl, int cmax4, int32_t* __restrict__ ids,
-                                                      uint8_t* __restrict__ vld, float* __restrict__ sct) {
+// Order-preserving 64-bit key of a candidate: larger key = ranked first (higher score, then lower node id).
+// The float score maps to an unsigned integer of the same order (-0 counted as +0, as float comparison does).
+__device__ __forceinline__ uint64_t rank_key(float s, int id) {
+  uint32_t u = __float_as_uint(s + 0.0f);
+  u ^= (u >> 31) ? 0xFFFFFFFFu : 0x80000000u;
+  return ((uint64_t)u << 32) | (uint32_t)(0x7FFFFFFF - id);
+}
+
+// The value of lane j ^ X (X = 1 or 2) of this lane's quad (DPP quad permute).
+template <int X>
+__device__ __forceinline__ int quad_xor(int x) {
+  constexpr int ctrl = X == 1 ? 0xB1 : 0x4E;   // quad_perm [1,0,3,2] / [2,3,0,1]
+  return __builtin_amdgcn_update_dpp(0, x, ctrl, 0xF, 0xF, false);
+}
+
+// The decode-cache append fused into the descent launch (one query per (sequence, head)): new rows and
+// the caches, of the query's element type.
+struct AppendIn {
+  const void* kn;
+  const void* vn;
+  int64_t nsb, nsh, vnsb, vnsh;
+  void* Kc;
+  void* Vc;
+  int64_t csb, csh, cst;
+  int Tcap;
+};
+
+template <typename TQ, int D, int WPQ, bool APPEND>
+__global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
+    const TQ* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qsn, int H, int Nq, int T,
+    const int32_t* __restrict__ tq, int64_t tq_sb, LevelIn lv, int n_levels, int arity_log2, int wmax, int wl,
+    int cmax4, int32_t* __restrict__ ids, uint8_t* __restrict__ vld, float* __restrict__ sct, AppendIn ap) {
   constexpr int R = D / 16;
   constexpr int NB = (64 / R) < 16 ? (64 / R) : 16;
   constexpr int NG = 4 * WPQ;          // 16-lane groups per query
@@ -153,12 +189,26 @@ __global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, 
   const int bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
   const int wmax4 = (wmax + 3) & ~3;
-  int32_t* cid = smem_i + qw * (2 * cmax4 + 2 * wmax4);
+  // per query: rank keys (uint64), candidate ids and scores, kept ids and scores
+  uint64_t* ckey = reinterpret_cast<uint64_t*>(smem_i + qw * (4 * cmax4 + 2 * wmax4));
+  int32_t* cid = reinterpret_cast<int32_t*>(ckey + cmax4);
   float* csc = reinterpret_cast<float*>(cid + cmax4);
   int32_t* kid = cid + 2 * cmax4;
   float* ksc = reinterpret_cast<float*>(kid + wmax4);
 
   const int t = tq[b * tq_sb + n];
+  if constexpr (APPEND) {
+    // row t and the nodes ending at t; the descent below reads only nodes that end before t
+    if (tid < D && t >= 0 && t < ap.Tcap) {
+      float* stk = reinterpret_cast<float*>(smem_i + 4 * cmax4 + 2 * wmax4);   // one query per block
+      append_dim<TQ>(tid, D, t, reinterpret_cast<const TQ*>(ap.kn) + b * ap.nsb + h * ap.nsh,
+                     reinterpret_cast<const TQ*>(ap.vn) + b * ap.vnsb + h * ap.vnsh,
+                     reinterpret_cast<TQ*>(ap.Kc) + b * ap.csb + h * ap.csh,
+                     reinterpret_cast<TQ*>(ap.Vc) + b * ap.csb + h * ap.csh, ap.cst, n_levels, lv.blevel[0],
+                     arity_log2, stk,
+                     [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
+    }
+  }
   const int gg = (w % WPQ) * 4 + (lane >> 4), j16 = lane & 15;
   float qr[R];
   load_row<TQ, R>(q + b * qsb + h * qsh + n * qsn + R * j16, qr);
@@ -174,19 +224,26 @@ __global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, 
     int C = t >> lv.blevel[start];
     for (int c = tid; c < ((C + 3) & ~3); c += NT) {
       cid[c] = c < C ? c : INT32_MAX;
-      if (c >= C) csc[c] = -INFINITY;
+      if (c >= C) ckey[c] = 0;
     }
     query_sync<WPQ>();
     for (int j = start;; --j) {
       const float* base = lv.ptr[j] + b * lv.sb[j] + h * lv.sh[j] + R * j16;
       const float scale = pow2_neg(lv.blevel[j]);
       for (int c0 = 0; c0 < C; c0 += NG * NB) {
-        float rows[NB][R];
+        // rows this round (uniform over the workgroup): all ids first, then all loads, then the dots
+        const int nr = (C - c0 + NG - 1) / NG;
+        int rid[NB];
 #pragma unroll
         for (int r = 0; r < NB; ++r) {
           const int c = c0 + NG * r + gg;
-          if (c < C) {
-            load_row<float, R>(base + (int64_t)cid[c] * D, rows[r]);
+          rid[r] = cid[(r < nr && c < C) ? c : 0];   // unconditional read: no wait per row
+        }
+        float rows[NB][R];
+#pragma unroll
+        for (int r = 0; r < NB; ++r) {
+          if (r < nr) {
+            load_row<float, R>(base + (int64_t)rid[r] * D, rows[r]);
           } else {
 #pragma unroll
             for (int i = 0; i < R; ++i) rows[r][i] = 0.0f;
@@ -194,30 +251,41 @@ __global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, 
         }
 #pragma unroll
         for (int r = 0; r < NB; ++r) {
-          const int c = c0 + NG * r + gg;
-          const float s = __fmul_rn(canon_dot<R>(qr, rows[r]), scale);
-          if (c < C && j16 == 0) csc[c] = s;
+          if (r < nr) {
+            const int c = c0 + NG * r + gg;
+            const float s = __fmul_rn(canon_dot<R>(qr, rows[r]), scale);
+            if (c < C && j16 == 0) {
+              csc[c] = s;
+              ckey[c] = rank_key(s, rid[r]);
+            }
+          }
         }
       }
       query_sync<WPQ>();
-      const int C4 = (C + 3) >> 2;
-      const float4* sc4 = reinterpret_cast<const float4*>(csc);
-      const int4* id4 = reinterpret_cast<const int4*>(cid);
-      for (int c = tid; c < C; c += NT) {
-        const float s = csc[c];
-        const int id = cid[c];
-        int rank = 0;
-        for (int o = 0; o < C4; ++o) {
-          const float4 so = sc4[o];
-          const int4 io = id4[o];
-          rank += (so.x > s) | ((so.x == s) & (io.x < id));
-          rank += (so.y > s) | ((so.y == s) & (io.y < id));
-          rank += (so.z > s) | ((so.z == s) & (io.z < id));
-          rank += (so.w > s) | ((so.w == s) & (io.w < id));
-        }
-        if (rank < wmax) {
-          kid[rank] = id;
-          ksc[rank] = s;
+      // rank = number of candidates with a larger key; P lanes (a quad's aligned part) share a candidate
+      {
+        const int C2 = (C + 1) >> 1;
+        const int P = 4 * C <= NT ? 4 : (2 * C <= NT ? 2 : 1);
+        const int lp = P == 4 ? 2 : P - 1;
+        const ulonglong2* key2 = reinterpret_cast<const ulonglong2*>(ckey);
+        for (int e0 = 0; e0 < C * P; e0 += NT) {
+          const int e = e0 + tid;
+          const int c = e >> lp, part = e & (P - 1);
+          int rank = 0;
+          if (c < C) {
+            const uint64_t mine = ckey[c];
+#pragma unroll 4
+            for (int o = part; o < C2; o += P) {
+              const ulonglong2 kk = key2[o];
+              rank += (int)(kk.x > mine) + (int)(kk.y > mine);
+            }
+          }
+          if (P >= 2) rank += quad_xor<1>(rank);
+          if (P >= 4) rank += quad_xor<2>(rank);
+          if (c < C && part == 0 && rank < wmax) {
+            kid[rank] = cid[c];
+            ksc[rank] = csc[c];
+          }
         }
       }
       nk = C < wmax ? C : wmax;
@@ -232,7 +300,7 @@ __global__ __launch_bounds__(256) void descend_kernel(const TQ* __restrict__ q, 
           cid[c] = c < nch ? (kid[c >> arity_log2] << arity_log2) + (c & (arity - 1)) : m - 1 - (c - nch);
         } else {
           cid[c] = INT32_MAX;
-          csc[c] = -INFINITY;
+          ckey[c] = 0;
         }
       }
       query_sync<WPQ>();
@@ -380,26 +448,42 @@ template <typename T, int D>
 struct DescendRun {
   static int run(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H, int Nq, const int32_t* tq,
                  int64_t tq_sb, const LevelIn& lv, int n_levels, int Tgeo, int arity_log2, int wmax, int wl,
-                 int32_t* ids, uint8_t* vld, float* sct, hipStream_t st) {
+                 int32_t* ids, uint8_t* vld, float* sct, const AppendIn* ap, hipStream_t st) {
     const int arity = 1 << arity_log2;
     const int cmax4 = (arity * wmax + arity - 1 + 3) & ~3;
     const int wmax4 = (wmax + 3) & ~3;
-    // few queries (decode): four wavefronts per query; many (prefill): one wavefront per query, 4 per block
-    const bool wide = (int64_t)B * H * Nq < 4096;
+    // many queries (prefill): one wavefront per query, 4 per block; few (decode): four wavefronts per query;
+    // very few (a single sequence): sixteen
+    const int64_t nq_all = (int64_t)B * H * Nq;
+    const int wpq = nq_all <= 256 ? 16 : (nq_all < 4096 ? 4 : 1);
+    const bool wide = wpq > 1;
     const int qpb = wide ? 1 : 4;
-    const size_t lds = (size_t)qpb * (2 * cmax4 + 2 * wmax4) * sizeof(int32_t);
+    size_t lds = (size_t)qpb * (4 * cmax4 + 2 * wmax4) * sizeof(int32_t);
+    if (ap) {
+      if (!wide || Nq != 1) {
+        set_error("descent with append: one query per (sequence, head) and fewer than 4096 of them");
+        return TA_ERR_UNSUPPORTED;
+      }
+      lds += (size_t)16 * D * sizeof(float);   // the append's carry stack
+    }
     if (lds > 64 * 1024) {
       set_error("descent beam too wide for LDS (arity * wmax too large)");
       return TA_ERR_UNSUPPORTED;
     }
     dim3 grid((Nq + qpb - 1) / qpb, B * H);
-    if (wide) {
-      hipLaunchKernelGGL((descend_kernel<T, D, 4>), grid, dim3(256), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq, Tgeo,
-                         tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct);
+    const AppendIn none{};
+#define TA_DESC(WPQ, NTH, APP)                                                                                   \
+  hipLaunchKernelGGL((descend_kernel<T, D, WPQ, APP>), grid, dim3(NTH), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq, \
+                     Tgeo, tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct, ap ? *ap : none)
+    if (ap) {
+      if (wpq == 16) TA_DESC(16, 1024, true);
+      else TA_DESC(4, 256, true);
     } else {
-      hipLaunchKernelGGL((descend_kernel<T, D, 1>), grid, dim3(256), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq, Tgeo,
-                         tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct);
+      if (wpq == 16) TA_DESC(16, 1024, false);
+      else if (wide) TA_DESC(4, 256, false);
+      else TA_DESC(1, 256, false);
     }
+#undef TA_DESC
     return check_launch("descend_kernel");
   }
 };
@@ -513,7 +597,40 @@ extern "C" int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t 
     }
   }
   return dispatch_dt_d<DescendRun>(q_dtype, D, q, qsb, qsh, qsn, B, H, Nq, tq, tq_sb, lv, n_levels, T, arity_log2,
-                                   wmax, wl, ids, vld, sct, (hipStream_t)stream);
+                                   wmax, wl, ids, vld, sct, (const AppendIn*)nullptr, (hipStream_t)stream);
+}
+
+extern "C" int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
+                                      const int32_t* t_pos, int n_levels, float* const* lv_ptr,
+                                      const int64_t* lv_sb, const int64_t* lv_sh, int T, int leaf_log2,
+                                      int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld, float* sct,
+                                      const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
+                                      int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst,
+                                      int Tcap, void* stream) {
+  if (B <= 0 || H <= 0 || wmax < 1 || wl < 0 || n_levels < 0 || n_levels > kMaxLevels || !pow2(T) ||
+      leaf_log2 < 1 || leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4 || Tcap <= 0 || D > 256) {
+    set_error("ta_tree_descend_append: bad sizes");
+    return TA_ERR_ARG;
+  }
+  if (!rows_aligned(q, dtype, D, {qsb, qsh})) {
+    set_error("ta_tree_descend_append: q rows not aligned");
+    return TA_ERR_ARG;
+  }
+  LevelIn lv;
+  for (int j = 0; j < n_levels; ++j) {
+    lv.ptr[j] = lv_ptr[j];
+    lv.sb[j] = lv_sb[j];
+    lv.sh[j] = lv_sh[j];
+    lv.blevel[j] = leaf_log2 + j * arity_log2;
+    if (!aligned(lv_ptr[j], 16)) {
+      set_error("ta_tree_descend_append: level pointer not 16-byte aligned");
+      return TA_ERR_ARG;
+    }
+  }
+  if (n_levels == 0) lv.blevel[0] = leaf_log2;
+  AppendIn ap{k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc, csb, csh, cst, Tcap};
+  return dispatch_dt_d<DescendRun>(dtype, D, q, qsb, qsh, (int64_t)0, B, H, 1, t_pos, (int64_t)1, lv, n_levels, T,
+                                   arity_log2, wmax, wl, ids, vld, sct, (const AppendIn*)&ap, (hipStream_t)stream);
 }
 
 extern "C" int ta_gather_dot(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const void* S,

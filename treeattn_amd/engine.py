@@ -114,8 +114,21 @@ class _Scratch:
         self.keys = self.keys_all[0]
         self.n_tree = None
         self.nsplit = nsplit
-        nbytes = K.L.lib().ta_seg_attn_workspace_size(B, H, 1, dh, nsplit)
-        self.ws = torch.empty(max(1, nbytes // 4 + 1), device=dev)
+        self.ws = K.seg_attn_workspace(B, H, 1, dh, nsplit, dev)
+        self.mm_ws = None
+
+    def mm(self, x, w, **kw):
+        """ta_rowmm with the split count of K.rowmm_splits; the split workspace is allocated (zero-filled)
+        on first use and shared by the group's products, which run one after another on its stream."""
+        M, Kd = x.shape
+        S = K.rowmm_splits(M, w.shape[0], Kd)
+        if S > 1:
+            need = K.L.lib().ta_rowmm_workspace_size(M, w.shape[0], Kd, S)
+            if self.mm_ws is None or self.mm_ws.numel() < need:
+                if torch.cuda.is_current_stream_capturing():
+                    raise RuntimeError('rowmm workspace must be allocated before graph capture')
+                self.mm_ws = torch.zeros(need, dtype=torch.uint8, device=x.device)
+        return K.rowmm(x, w, splits=S, ws=self.mm_ws if S > 1 else None, **kw)
 
 
 def decode_nsplit(B, H, wl, leaf):
@@ -154,12 +167,19 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     wl = state.shape.leaf_width(cfg.wmax)
     if scratch is None:
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
-    ids, vld, sct = K.tree_descend(q, state.levels, tpos.view(B, 1), state.shape, cfg.wmax,
-                                   out=(scratch.ids, scratch.vld, scratch.sct))
     structural = (not cfg.neighbors) and lhat is None
+    fused = structural and update and B * H < 4096 and q.dtype == k.dtype == state.K.dtype
+    if fused:
+        # descent and cache append in one launch (the append touches only row t and the nodes ending at t)
+        ids, vld, sct = K.tree_descend_append(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0],
+                                              state.K, state.V, out=(scratch.ids, scratch.vld, scratch.sct))
+    else:
+        ids, vld, sct = K.tree_descend(q, state.levels, tpos.view(B, 1), state.shape, cfg.wmax,
+                                       out=(scratch.ids, scratch.vld, scratch.sct))
     if structural:
         if update:
-            K.kv_append(k[:, :, 0], v[:, :, 0], state.K, state.V, tpos, state.levels, leaf, state.shape.arity)
+            if not fused:
+                K.kv_append(k[:, :, 0], v[:, :, 0], state.K, state.V, tpos, state.levels, leaf, state.shape.arity)
             if cfg.global_pool:
                 state.ksum += k[:, :, 0].float()
         out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
@@ -310,16 +330,16 @@ class Decoder:
         x = W['wte'][tok] + W['wpe'][tpos]
         tpos32 = tpos.to(torch.int32)
         for i, L in enumerate(W['layers']):
-            qkv = K.rowmm(x, L['c_attn'], ln_w=L['ln1'])
+            qkv = sc.mm(x, L['c_attn'], ln_w=L['ln1'])
             q, k, v = [a.view(B, 1, H, dh).transpose(1, 2) for a in qkv.split(C, -1)]
             sc.keys = sc.keys_all[i]
             out, kr = seg_attend_(grp['states'][i], L.get('pw'), q, k, v, tpos32, scratch=sc)
             if kr.data_ptr() != sc.keys_all[i].data_ptr():
                 sc.keys_all[i].copy_(kr.view(B, H, 1))
-            K.rowmm(out.view(B, C), L['c_proj'], epilogue='residual', residual=x, out=x)
-            hmid = K.rowmm(x, L['c_fc'], ln_w=L['ln2'], epilogue='gelu')
-            K.rowmm(hmid, L['c_mlp'], epilogue='residual', residual=x, out=x)
-        K.rowmm(x, W['wte'], ln_w=W['ln_f'], out=logits)
+            sc.mm(out.view(B, C), L['c_proj'], epilogue='residual', residual=x, out=x)
+            hmid = sc.mm(x, L['c_fc'], ln_w=L['ln2'], epilogue='gelu')
+            sc.mm(hmid, L['c_mlp'], epilogue='residual', residual=x, out=x)
+        sc.mm(x, W['wte'], ln_w=W['ln_f'], out=logits)
 
     def _forward_step_fused(self, tok, tpos):
         """The same step with the row-block kernels: LN1+QKV, attention, projection+residual, LN2+FC+GELU,

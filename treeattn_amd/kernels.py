@@ -102,6 +102,28 @@ def tree_descend(q, levels, tq, shape, wmax, out=None):
     return ids, vld, sct
 
 
+def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out):
+    """Decode step's descent of q (B,H,1,D) at t_pos (B,) int32 and, in the same launch, the cache append of
+    k_new, v_new (B,H,D) at row t_pos[b] of Kc, Vc (B,H,Tcap,D) with node formation.  out = (ids, vld, sct)
+    buffers (B,H,1,wl)."""
+    L.require_gpu(q, t_pos, k_new, v_new, Kc, Vc)
+    B, H, Nq, D = q.shape
+    if Nq != 1 or t_pos.dtype != torch.int32 or not t_pos.is_contiguous():
+        raise ValueError('tree_descend_append: one query per (sequence, head) and contiguous int32 positions')
+    if not (q.dtype == k_new.dtype == v_new.dtype == Kc.dtype == Vc.dtype):
+        raise TypeError('tree_descend_append: q, new rows and caches must share a dtype')
+    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or Kc.stride() != Vc.stride():
+        raise ValueError('tree_descend_append: unsupported layout')
+    ids, vld, sct = out
+    wl = shape.leaf_width(wmax)
+    L.call('ta_tree_descend_append', L.ptr(q), L.dtype_code(q), q.stride(0), q.stride(1), B, H, D, L.ptr(t_pos),
+           len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
+           L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, L.ptr(ids),
+           L.ptr(vld), L.ptr(sct), L.ptr(k_new), L.ptr(v_new), k_new.stride(0), k_new.stride(1), v_new.stride(0),
+           v_new.stride(1), L.ptr(Kc), L.ptr(Vc), Kc.stride(0), Kc.stride(1), Kc.stride(2), Kc.shape[2], L.stream())
+    return ids, vld, sct
+
+
 # ----------------------------------------------------------------------------------------------- gather-dot
 def gather_dot(q, S, cand, scale):
     """scale * q . S[clamp(cand)] in float32, canonical order.  q (b,H,N,dh), S (b,H,M,dh), cand (b,H,N,C)."""
@@ -151,6 +173,15 @@ def sparse_attn_fwd(q, k, v, cand, scale):
     return out, lse
 
 
+def seg_attn_workspace(B, H, Nq, D, nsplit, device):
+    """Zero-filled workspace for seg_attn with `nsplit` (None when none is needed).  The per-query counters
+    at its head are left at zero by every call, so one workspace serves calls that run one after another."""
+    nbytes = L.lib().ta_seg_attn_workspace_size(B, H, Nq, D, nsplit)
+    if nbytes <= 0:
+        return None
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+
 def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=None, keys=None, nsplit=1, ws=None):
     """Attention over selected leaf blocks + own leaf block + static keys (neighbours off).
     q (B,H,Nq,D) strided; k, v (B,H,Tk,D) strided; tq (Nq,) or (B,Nq) int32; ids/vld (B,H,Nq,wl);
@@ -169,10 +200,8 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
     if n_tree is not None:
         nt = n_tree if (n_tree.dtype == torch.int32 and n_tree.is_contiguous()) else n_tree.to(torch.int32).contiguous()
     if ws is None:
-        nbytes = L.lib().ta_seg_attn_workspace_size(B, H, Nq, D, nsplit)
-        if nbytes > 0:
-            ws = torch.empty(nbytes // 4 + 1, device=q.device, dtype=torch.float32)
-    ws_bytes = ws.numel() * 4 if ws is not None else 0
+        ws = seg_attn_workspace(B, H, Nq, D, nsplit, q.device)
+    ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
     L.call('ta_seg_attn_fwd', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k), *L.rows3(v),
            B, H, Nq, D, k.shape[2], L.ptr(tq32), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(nt), wl, int(leaf), int(local),
            float(scale), L.ptr(out), out.stride(0), out.stride(1), out.stride(2), L.ptr(lse), L.ptr(keys),
@@ -188,9 +217,31 @@ def rowmm_supported(x, w):
     return x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.shape[-1] % 64 == 0
 
 
-def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None):
+ROWMM_TARGET_WGS = 256
+
+
+def rowmm_splits(M, N, K):
+    """Split count for ta_rowmm.  Measured on MI355X at M=32: a workgroup's fixed cost outweighs the extra
+    parallelism unless each split keeps at least 768 of K (K=3072: 13.2 us unsplit, 8.6 us with 4 splits;
+    K=768: no gain), and products with >= ROWMM_TARGET_WGS tiles are left whole."""
+    tiles = ((M + 31) // 32) * ((N + 31) // 32)
+    if tiles >= ROWMM_TARGET_WGS or tiles > 1024:
+        return 1
+    return max(1, K // 768)
+
+
+def rowmm_workspace(M, N, K, splits, device):
+    """Zero-filled workspace for ta_rowmm with `splits` (None when the product needs none)."""
+    n = L.lib().ta_rowmm_workspace_size(M, N, K, splits)
+    if n <= 0:
+        return None
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None, splits=1, ws=None):
     """epilogue(LN(x) @ w.T) for a few rows, bf16: x (M,K), w (N,K) -> (M,N).  epilogue None | 'gelu' |
-    'residual' (adds `residual`, (M,N)); `out` may be `residual`."""
+    'residual' (adds `residual`, (M,N)); `out` may be `residual`.  splits > 1 divides K among workgroups and
+    needs `ws` from rowmm_workspace (one workspace serves calls that run one after another)."""
     L.require_gpu(x, w)
     M, K = x.shape
     N = w.shape[0]
@@ -200,7 +251,8 @@ def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None):
         out = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
     r = residual if epilogue == 'residual' else None
     L.call('ta_rowmm', L.ptr(x), x.stride(0), L.ptr(w), w.stride(0), L.ptr(out), out.stride(0), L.ptr(r),
-           r.stride(0) if r is not None else 0, L.ptr(ln_w), float(eps), M, N, K, _EPI[epilogue], L.stream())
+           r.stride(0) if r is not None else 0, L.ptr(ln_w), float(eps), M, N, K, _EPI[epilogue], int(splits),
+           L.ptr(ws), ws.numel() if ws is not None else 0, L.stream())
     return out
 
 
