@@ -291,6 +291,19 @@ def test_argmax_rows_first_maximum():
     assert got == [7, 50303, 12345]
 
 
+@pytest.mark.parametrize('rows,n,dtype,offset', [(32, 50304, torch.bfloat16, 0), (3, 131080, torch.float32, 0),
+                                                 (5, 150001, torch.float16, 0), (4, 70000, torch.bfloat16, 3)])
+def test_argmax_rows_random(rows, n, dtype, offset):
+    """Random rows with repeated values (coarse quantisation) in the 16-byte-run path and the scalar path
+    (odd lengths, unaligned views): the first index of the maximum, as numpy's argmax."""
+    g = torch.Generator().manual_seed(n + rows)
+    full = (torch.randn(rows, n + offset, generator=g) * 4).round().to(dtype)
+    x = full[:, offset:]
+    want = x.float().numpy().argmax(axis=1).tolist()
+    got = K.argmax_rows(full.to(DEV)[:, offset:]).cpu().tolist()
+    assert got == want
+
+
 @pytest.mark.parametrize('M,N,KD,ln,epi', [(32, 2304, 768, True, None), (32, 768, 3072, False, 'residual'),
                                           (7, 96, 640, True, 'gelu')])
 def test_rowmm_split_k(M, N, KD, ln, epi):

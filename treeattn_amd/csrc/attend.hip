@@ -47,6 +47,26 @@ struct AttnParams {
 };
 
 constexpr float kNegBig = -1e30f;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of G lanes (G a power of two up to 64); every lane of a group gets the sum.
+// Quad permutes pair lanes within quads; after them the value repeats every 4 lanes, so mirroring each
+// half-row (lane j <-> 7 - j) pairs the two quads of an 8-lane group, and mirroring the row (j <-> 15 - j)
+// the two halves of a 16-lane group.
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (G >= 2) x += dpp_f<0xB1>(x);    // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) x += dpp_f<0x4E>(x);    // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) x += dpp_f<0x141>(x);   // row_half_mirror
+  if constexpr (G >= 16) x += dpp_f<0x140>(x);  // row_mirror
+  if constexpr (G >= 32) x += __shfl_xor(x, 16, kWave);
+  if constexpr (G >= 64) x += __shfl_xor(x, 32, kWave);
+  return x;
+}
 constexpr int kWavesPerBlock = 4;
 template <typename T> struct Raw16;  // 16 bytes of T -> EPL floats
 template <> struct Raw16<float> {
@@ -88,7 +108,7 @@ template <> struct Raw16<f16_t> {
 //   the last to arrive reads the partials past the caches, combines them
 //   (out = sum_g acc_g e^(m_g - M) / sum_g L_g e^(m_g - M)) and resets the counter.  No workgroup waits for
 //   another.
-template <typename T, int D, bool SPLIT>
+template <typename T, int D, bool SPLIT, bool CAND>
 __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   constexpr int EPL = Raw16<T>::EPL;
   constexpr int LPR = D / EPL;              // lanes per key row
@@ -121,7 +141,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   // key list of this query
   int N, nused = 0, lb = 0, nloc = 0, next = 0;
   const int leaf = 1 << p.leaf_log2;
-  if (p.cand) {
+  if constexpr (CAND) {
     N = p.KC;
   } else {
     int t = p.tq[b * p.tq_sb + n];
@@ -165,24 +185,27 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   const int stride = SPLIT ? p.gsplit * kWavesPerBlock : 1;
   const int first = SPLIT ? g * kWavesPerBlock + w : 0;
 
+  // All positions of a chunk first (branch-free LDS reads in the structural mode, so no wait on memory
+  // sits between the K/V loads), then its K/V loads.
   auto fetch = [&](int c, uint4 (&kr)[NL], uint4 (&vr)[NL], bool (&ok)[NL]) {
+    int pos[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int key = c * KPC + i * RPI + rg;
-      int pos = -1;
-      if (key < N) {
-        if (p.cand) {
-          pos = p.cand[qi * p.KC + key];
-        } else if (key < nl) {
-          pos = (s_ids[key >> p.leaf_log2] << p.leaf_log2) + (key & (leaf - 1));
-        } else if (key < nl + nloc) {
-          pos = lb + (key - nl);
-        } else {
-          pos = s_ext[key - nl - nloc];
-        }
+      if constexpr (CAND) {
+        pos[i] = key < N ? p.cand[qi * p.KC + key] : -1;
+      } else {
+        const int kt = key < nl ? key : 0;
+        const int leafpos = (s_ids[kt >> p.leaf_log2] << p.leaf_log2) + (kt & (leaf - 1));
+        const int ke = key - nl - nloc;
+        const int extpos = s_ext[(ke >= 0 && ke < next) ? ke : 0];
+        pos[i] = key < nl ? leafpos : (key < nl + nloc ? lb + (key - nl) : (key < N ? extpos : -1));
       }
-      ok[i] = pos >= 0 && pos < p.Tk;
-      const int64_t row = ok[i] ? pos : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      ok[i] = pos[i] >= 0 && pos[i] < p.Tk;
+      const int64_t row = ok[i] ? pos[i] : 0;
       kr[i] = *reinterpret_cast<const uint4*>(kb + row * kst_b);
       vr[i] = *reinterpret_cast<const uint4*>(vb + row * vst_b);
     }
@@ -205,18 +228,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
       sc[i] = d0;
     }
 #pragma unroll
-    for (int o = LPR / 2; o >= 1; o >>= 1) {
-#pragma unroll
-      for (int i = 0; i < NL; ++i) sc[i] += __shfl_xor(sc[i], o, kWave);
-    }
+    for (int i = 0; i < NL; ++i) sc[i] = group_sum<LPR>(sc[i]);
+    // running max per row group (its LPR lanes see the same scores); the groups merge at the end
     float cm = kNegBig;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       sc[i] = ok[i] ? sc[i] * p.scale : kNegBig;
       cm = fmaxf(cm, sc[i]);
     }
-    const float mn = fmaxf(m, wave_max(cm));
-    if (mn != m) {
+    const float mn = fmaxf(m, cm);
+    {
       const float alpha = __expf(m - mn);
 #pragma unroll
       for (int d = 0; d < EPL; ++d) acc[d] *= alpha;
@@ -257,6 +278,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
     }
   }
 
+  // bring the row groups to the wavefront's max, then sum them
+  {
+    const float Mw = wave_max(m);
+    const float f = __expf(m - Mw);
+    l *= f;
+#pragma unroll
+    for (int d = 0; d < EPL; ++d) acc[d] *= f;
+    m = Mw;
+  }
   float L = wave_sum(l);
   // sum the accumulators of the RPI row groups: afterwards lanes 0..LPR-1 hold the full dims
 #pragma unroll
@@ -417,14 +447,17 @@ template <typename T, int D>
 int launch_attn(const AttnParams& p, int B, bool split, hipStream_t st) {
   const int wl_pad = p.cand ? 0 : ((p.wl + 3) & ~3);
   size_t lds = (size_t)kWavesPerBlock * (wl_pad + kWave) * sizeof(float);
+  const dim3 blk(kWavesPerBlock * kWave);
   if (split) {
     lds += (size_t)kWavesPerBlock * (D + 2) * sizeof(float);
     dim3 grid((unsigned)((int64_t)p.Nq * p.gsplit), B * p.H);
-    hipLaunchKernelGGL((attn_kernel<T, D, true>), grid, dim3(kWavesPerBlock * kWave), lds, st, p);
+    if (p.cand) hipLaunchKernelGGL((attn_kernel<T, D, true, true>), grid, blk, lds, st, p);
+    else hipLaunchKernelGGL((attn_kernel<T, D, true, false>), grid, blk, lds, st, p);
     return check_launch("attn_kernel");
   }
   dim3 grid((unsigned)((p.Nq + kWavesPerBlock - 1) / kWavesPerBlock), B * p.H);
-  hipLaunchKernelGGL((attn_kernel<T, D, false>), grid, dim3(kWavesPerBlock * kWave), lds, st, p);
+  if (p.cand) hipLaunchKernelGGL((attn_kernel<T, D, false, true>), grid, blk, lds, st, p);
+  else hipLaunchKernelGGL((attn_kernel<T, D, false, false>), grid, blk, lds, st, p);
   return check_launch("attn_kernel");
 }
 

@@ -48,8 +48,29 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
   const int tid = threadIdx.x;
   const int lane = lane_id(), w = wave_id();
   const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+  // this workgroup's K blocks [blk0, blk1)
+  const int nblk_all = K / 64;
+  const int per = (nblk_all + splits - 1) / splits;
+  const int blk0 = blockIdx.z * per;
+  const int blk1 = blk0 + per < nblk_all ? blk0 + per : nblk_all;
+  const int nblk = blk1 - blk0;
+  // LayerNorm statistics from the X blocks the wavefronts load for the product when one round of loads
+  // covers all of K; otherwise a separate pass over the rows first
+  const bool stats_from_blocks = splits == 1 && nblk <= kRowmmWaves * kRowmmBlk;
 
-  if constexpr (LN) {
+  // the residual tile of the epilogue, loaded up front
+  constexpr int EPT = 1024 / NT;   // epilogue elements per thread
+  float rres[EPT];
+  if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + k * NT;
+      const int gm = m0 + (e >> 5), gn = n0 + (e & 31);
+      rres[k] = (gm < M && gn < N) ? to_f32(R[(int64_t)gm * ldr + gn]) : 0.0f;
+    }
+  }
+
+  if (LN && !stats_from_blocks) {
     // row statistics in one pass (sum and sum of squares), TPR threads per row
     constexpr int TPR = NT / 32;
     const int r = tid / TPR, part = tid % TPR;
@@ -87,33 +108,63 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
   const bf16_t* xr = X + (int64_t)(m0 + (xok ? rl : 0)) * ldx + kh;
   const bf16_t* wr = W + (int64_t)(n0 + (wok ? rl : 0)) * ldw + kh;
   float mean = 0.0f, rstd = 0.0f;
-  if constexpr (LN) {
+  if (LN && !stats_from_blocks) {
     mean = s_mean[rl];
     rstd = s_rstd[rl];
   }
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  // this workgroup's K blocks [blk0, blk1)
-  const int nblk_all = K / 64;
-  const int per = (nblk_all + splits - 1) / splits;
-  const int blk0 = blockIdx.z * per;
-  const int blk1 = blk0 + per < nblk_all ? blk0 + per : nblk_all;
-  const int nblk = blk1 - blk0;
   xr += blk0 * 64;
   wr += blk0 * 64;
   const bf16_t* gk = LN ? gam + blk0 * 64 : gam;
   for (int base = 0; base < nblk; base += kRowmmWaves * kRowmmBlk) {
-    uint4 xa[kRowmmBlk][4], wb[kRowmmBlk][4];
+    uint4 xa[kRowmmBlk][4], wb[kRowmmBlk][4], ga[LN ? kRowmmBlk : 1][4];
 #pragma unroll
     for (int i = 0; i < kRowmmBlk; ++i) {
       const int blk = base + w + kRowmmWaves * i;
       const bool bok = blk < nblk;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        xa[i][j] = (bok && xok) ? *reinterpret_cast<const uint4*>(xr + blk * 64 + 8 * j) : make_uint4(0, 0, 0, 0);
         wb[i][j] = (bok && wok) ? *reinterpret_cast<const uint4*>(wr + blk * 64 + 8 * j) : make_uint4(0, 0, 0, 0);
+        xa[i][j] = (bok && xok) ? *reinterpret_cast<const uint4*>(xr + blk * 64 + 8 * j) : make_uint4(0, 0, 0, 0);
+        if constexpr (LN)
+          ga[i][j] = bok ? *reinterpret_cast<const uint4*>(gk + blk * 64 + kh + 8 * j) : make_uint4(0, 0, 0, 0);
       }
+    }
+    if (LN && stats_from_blocks) {
+      // lanes rl and rl + 32 hold the two halves of row rl of each of this wavefront's blocks
+      float sx = 0.0f, sxx = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kRowmmBlk; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float f[8];
+          const bf16_t* xe = reinterpret_cast<const bf16_t*>(&xa[i][j]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            f[e] = to_f32(xe[e]);
+            sx += f[e];
+            sxx = fmaf(f[e], f[e], sxx);
+          }
+        }
+      }
+      sx += __shfl_xor(sx, 32, kWave);
+      sxx += __shfl_xor(sxx, 32, kWave);
+      if (lane < 32) {
+        red[w][0][lane] = sx;
+        red[w][1][lane] = sxx;
+      }
+      __syncthreads();
+      float ts = 0.0f, tss = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kRowmmWaves; ++v) {
+        ts += red[v][0][rl];
+        tss += red[v][1][rl];
+      }
+      mean = ts / (float)K;
+      rstd = rsqrtf(fmaxf(tss / (float)K - mean * mean, 0.0f) + eps);
+      __syncthreads();   // red is reused for the output tile
     }
 #pragma unroll
     for (int i = 0; i < kRowmmBlk; ++i) {
@@ -124,9 +175,12 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
         for (int j = 0; j < 4; ++j) {
           float f[8], gg[8];
           const bf16_t* xe = reinterpret_cast<const bf16_t*>(&xa[i][j]);
+          const bf16_t* ge = reinterpret_cast<const bf16_t*>(&ga[i][j]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = to_f32(xe[e]);
-          load_row<bf16_t, 8>(gk + blk * 64 + kh + 8 * j, gg);
+          for (int e = 0; e < 8; ++e) {
+            f[e] = to_f32(xe[e]);
+            gg[e] = to_f32(ge[e]);
+          }
           uint32_t o[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e)
@@ -167,7 +221,9 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
     __syncthreads();
     if (!s_last) return;
   }
-  for (int e = tid; e < 1024; e += NT) {
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int e = tid + k * NT;
     const int r = e >> 5, c = e & 31;
     const int gm = m0 + r, gn = n0 + c;
     if (gm < M && gn < N) {
@@ -185,7 +241,7 @@ __global__ __launch_bounds__(kRowmmWaves * 64) void rowmm_kernel(const bf16_t* _
       }
       v = bf16_round(v);
       if constexpr (EPI == EPI_GELU) v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-      if constexpr (EPI == EPI_RESIDUAL) v = to_f32(R[(int64_t)gm * ldr + gn]) + v;
+      if constexpr (EPI == EPI_RESIDUAL) v = rres[k] + v;
       Y[(int64_t)gm * ldy + gn] = bf16_from(v);
     }
   }

@@ -5,37 +5,79 @@
 
 namespace ta {
 
+// (value, index) pairs: a is kept over b when larger, or equal with a smaller index
+__device__ __forceinline__ void better_of(float& v, int64_t& i, float v2, int64_t i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+// Every thread issues all its loads (16-byte runs of the row, up to kArgmaxRuns in flight) before comparing;
+// then the wavefronts reduce with shuffles and the workgroup through LDS.
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxRuns = 8;
+
 template <typename T>
-__global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__ x, int64_t n, int64_t stride,
-                                                          int64_t* __restrict__ out) {
-  __shared__ float s_val[1024];
-  __shared__ int64_t s_idx[1024];
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const T* __restrict__ x, int64_t n,
+                                                                    int64_t stride, int vec,
+                                                                    int64_t* __restrict__ out) {
+  constexpr int EPR = 16 / (int)sizeof(T);   // elements per 16-byte run
+  __shared__ float s_val[kArgmaxThreads / kWave];
+  __shared__ int64_t s_idx[kArgmaxThreads / kWave];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * stride;
   float best = -INFINITY;
   int64_t bi = n;  // sentinel: larger than any index
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-    const float v = to_f32(xr[i]);
-    if (v > best || (v == best && i < bi)) {
-      best = v;
-      bi = i;
-    }
-  }
-  s_val[threadIdx.x] = best;
-  s_idx[threadIdx.x] = bi;
-  __syncthreads();
-  for (int o = blockDim.x / 2; o >= 1; o >>= 1) {
-    if ((int)threadIdx.x < o) {
-      const float v = s_val[threadIdx.x + o];
-      const int64_t j = s_idx[threadIdx.x + o];
-      if (v > s_val[threadIdx.x] || (v == s_val[threadIdx.x] && j < s_idx[threadIdx.x])) {
-        s_val[threadIdx.x] = v;
-        s_idx[threadIdx.x] = j;
+  if (vec) {
+    const int64_t nruns = n / EPR;
+    for (int64_t r0 = 0; r0 < nruns; r0 += (int64_t)kArgmaxThreads * kArgmaxRuns) {
+      uint4 u[kArgmaxRuns];
+#pragma unroll
+      for (int k = 0; k < kArgmaxRuns; ++k) {
+        const int64_t r = r0 + threadIdx.x + (int64_t)k * kArgmaxThreads;
+        u[k] = r < nruns ? reinterpret_cast<const uint4*>(xr)[r] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < kArgmaxRuns; ++k) {
+        const int64_t r = r0 + threadIdx.x + (int64_t)k * kArgmaxThreads;
+        if (r < nruns) {
+          const T* e = reinterpret_cast<const T*>(&u[k]);
+#pragma unroll
+          for (int m = 0; m < EPR; ++m) better_of(best, bi, to_f32(e[m]), r * EPR + m);
+        }
       }
     }
-    __syncthreads();
+  } else {
+    for (int64_t i0 = 0; i0 < n; i0 += (int64_t)kArgmaxThreads * kArgmaxRuns) {
+      float v[kArgmaxRuns];
+#pragma unroll
+      for (int k = 0; k < kArgmaxRuns; ++k) {
+        const int64_t i = i0 + threadIdx.x + (int64_t)k * kArgmaxThreads;
+        v[k] = i < n ? to_f32(xr[i]) : -INFINITY;
+      }
+#pragma unroll
+      for (int k = 0; k < kArgmaxRuns; ++k) {
+        const int64_t i = i0 + threadIdx.x + (int64_t)k * kArgmaxThreads;
+        if (i < n) better_of(best, bi, v[k], i);
+      }
+    }
   }
-  if (threadIdx.x == 0) out[row] = s_idx[0] < n ? s_idx[0] : 0;
+#pragma unroll
+  for (int o = kWave / 2; o >= 1; o >>= 1) {
+    const float v2 = __shfl_xor(best, o, kWave);
+    const int64_t i2 = __shfl_xor(bi, o, kWave);
+    better_of(best, bi, v2, i2);
+  }
+  if (lane_id() == 0) {
+    s_val[wave_id()] = best;
+    s_idx[wave_id()] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w) better_of(best, bi, s_val[w], s_idx[w]);
+    out[row] = bi < n ? bi : 0;
+  }
 }
 
 }  // namespace ta
@@ -51,15 +93,19 @@ extern "C" int ta_argmax_rows(const void* x, int dtype, int64_t rows, int64_t n,
   if (rows == 0) return TA_OK;
   hipStream_t st = (hipStream_t)stream;
   dim3 grid((unsigned)rows);
+  const int esz = dtype == TA_F32 ? 4 : 2;
+  // 16-byte runs when every row starts 16-byte aligned and holds whole runs
+  const int vec = ((uintptr_t)x % 16 == 0 && (stride * esz) % 16 == 0 && (n * esz) % 16 == 0) ? 1 : 0;
+  const dim3 blk(kArgmaxThreads);
   switch (dtype) {
     case TA_F32:
-      hipLaunchKernelGGL((argmax_rows_kernel<float>), grid, dim3(1024), 0, st, (const float*)x, n, stride, out);
+      hipLaunchKernelGGL((argmax_rows_kernel<float>), grid, blk, 0, st, (const float*)x, n, stride, vec, out);
       break;
     case TA_F16:
-      hipLaunchKernelGGL((argmax_rows_kernel<f16_t>), grid, dim3(1024), 0, st, (const f16_t*)x, n, stride, out);
+      hipLaunchKernelGGL((argmax_rows_kernel<f16_t>), grid, blk, 0, st, (const f16_t*)x, n, stride, vec, out);
       break;
     case TA_BF16:
-      hipLaunchKernelGGL((argmax_rows_kernel<bf16_t>), grid, dim3(1024), 0, st, (const bf16_t*)x, n, stride, out);
+      hipLaunchKernelGGL((argmax_rows_kernel<bf16_t>), grid, blk, 0, st, (const bf16_t*)x, n, stride, vec, out);
       break;
     default:
       set_error("unknown dtype");
