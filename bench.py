@@ -1,19 +1,23 @@
 #!/usr/bin/env python
-"""Benchmark of the segment-tree sparse attention decode on one MI355X.
+"""Benchmark of the segment-tree sparse attention on one MI355X.
 
-Workload (the configuration the headline metric is quoted on): GPT 12 layers, d_model 768, 12 heads x 64,
-vocab 50304, random-init N(0, 0.02) (seed 3), bf16.  32 sequences, each prefilled with 32768 uniform random
-token ids (seed 3) through the model itself (sparse attention included; not timed), then greedy decode with
-the segment tree: leaf block 64, binary, top-k 32 leaves + own leaf block + static keys, neighbours off.
-Cache capacity Tcap = 65536.  A step decodes one token for every sequence; the whole step (12 layers: GEMMs,
-beam descent, cache append with node formation, sparse attention, logits, argmax) is one captured HIP graph.
+Default (the configuration the headline metric is quoted on, config 4): GPT 12 layers, d_model 768, 12
+heads x 64, vocab 50304, random-init N(0, 0.02) (seed 3), bf16.  32 sequences, each prefilled with 32768
+uniform random token ids (seed 3) through the model itself (sparse attention included; not timed), then
+greedy decode with the segment tree: leaf block 64, binary, top-k 32 leaves + own leaf block + static keys,
+neighbours off.  Cache capacity Tcap = 65536.  A step decodes one token for every sequence; the whole step
+(12 layers: GEMMs, beam descent with the cache append, sparse attention, logits, argmax) is one captured HIP
+graph.
 
-    python bench.py [--steps K] [--warmup W]
+    python bench.py [--steps K] [--warmup W]            config 4 (the headline line)
+    python bench.py --config 5                          same model, 1 sequence x 131072, leaf 128, 4-ary, top-64
+    python bench.py --config 1                          small fp32 GPT, 256 greedy steps, parity vs the oracle
+    python bench.py --config 3                          prefill sparse attention, (4,16,16384,128) bf16
 
-Prints one JSON line: value = decoded tokens/s for the batch (32 tokens per step), the roofline of the
-dominant kernel (the decode attention, HBM-bound) measured live with HIP events, the CPU baseline (the
-oracle engine decoding one of the 32 sequences from the same state on the host), and the isolated
-gather-dot (8x12x4096x64 bf16, 16 blocks of 64 keys per query) as GB/s of 8 TB/s.
+Each run prints one JSON line.  Config 4's: value = decoded tokens/s for the batch (32 tokens per step), the
+roofline of the dominant kernel (the decode attention, HBM-bound) measured live with HIP events, the CPU
+baseline (the oracle engine decoding one of the 32 sequences from the same state on the host), and the
+isolated gather-dot (8x12x4096x64 bf16, 16 blocks of 64 keys per query) as GB/s of 8 TB/s.
 """
 import argparse
 import json
@@ -25,29 +29,44 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=64)
-    ap.add_argument('--warmup', type=int, default=8)
-    ap.add_argument('--batch', type=int, default=32)
-    ap.add_argument('--context', type=int, default=32768)
-    ap.add_argument('--tcap', type=int, default=65536)
+    ap.add_argument('--config', type=int, default=4, choices=(1, 3, 4, 5))
+    ap.add_argument('--steps', type=int, default=None)
+    ap.add_argument('--warmup', type=int, default=None)
+    ap.add_argument('--batch', type=int, default=None)
+    ap.add_argument('--context', type=int, default=None)
+    ap.add_argument('--tcap', type=int, default=None)
     ap.add_argument('--layers', type=int, default=12)
     ap.add_argument('--embd', type=int, default=768)
     ap.add_argument('--heads', type=int, default=12)
     ap.add_argument('--vocab', type=int, default=50304)
-    ap.add_argument('--leaf', type=int, default=64)
-    ap.add_argument('--arity', type=int, default=2)
-    ap.add_argument('--topk', type=int, default=32)
-    ap.add_argument('--prefill-chunk', type=int, default=8)
+    ap.add_argument('--leaf', type=int, default=None)
+    ap.add_argument('--arity', type=int, default=None)
+    ap.add_argument('--topk', type=int, default=None)
+    ap.add_argument('--prefill-chunk', type=int, default=None)
     ap.add_argument('--cpu-seconds', type=float, default=20.0, help='budget of the CPU baseline leg')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--no-gather-dot', action='store_true', help='skip the isolated gather-dot leg')
     ap.add_argument('--kernel-iters', type=int, default=50)
-    return ap.parse_args()
+    args = ap.parse_args()
+    # per-config defaults: 4 (the headline) and 5 are decode engines; 1 the small fp32 model; 3 prefill attention
+    presets = {4: dict(steps=64, warmup=8, batch=32, context=32768, tcap=65536, leaf=64, arity=2, topk=32,
+                       prefill_chunk=8, ids_seed=3),
+               5: dict(steps=512, warmup=8, batch=1, context=131072, tcap=262144, leaf=128, arity=4, topk=64,
+                       prefill_chunk=1, ids_seed=4),
+               1: dict(steps=256, warmup=0, batch=1, context=512, tcap=1024, leaf=32, arity=2, topk=8,
+                       prefill_chunk=1, ids_seed=0),
+               3: dict(steps=5, warmup=2, batch=4, context=16384, tcap=16384, leaf=64, arity=2, topk=32,
+                       prefill_chunk=1, ids_seed=2)}
+    for k, v in presets[args.config].items():
+        if getattr(args, k, None) is None:
+            setattr(args, k, v)
+    return args
 
 
 def log(msg):
@@ -119,9 +138,9 @@ def gather_dot_leg(args):
             'frac_of_hbm': round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s):
+def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64):
     """The oracle engine (CPU restatement of engine.py) decodes sequence 0 from the GPU's state."""
-    from oracle.engine_ref import DecoderRef, SegStateRef
+    from oracle.engine_ref import DecoderRef
     from treeattn_amd import kernels as K
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
@@ -155,29 +174,35 @@ def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s):
         tg[0] = nc
         t += 1
         n += 1
-        if n >= 3 and (time.perf_counter() - t_start > budget_s or n >= 64):
+        if n >= 3 and (time.perf_counter() - t_start > budget_s or n >= max_steps):
             break
     times.sort()
     med = times[len(times) // 2]
     return {'value': round(1.0 / med, 3), 'unit': 'tokens/s', 'cores': ncores, 'kind': 'port',
-            'sample': '%d greedy decode steps of 1 of the 32 sequences from the GPU state at position %d, '
+            'sample': '%d greedy decode steps of 1 of the %d sequences from the GPU state at position %d, '
                       'oracle engine on the host (torch CPU, bf16 activations, fp32 selection/attention); '
-                      'median s/token; a 32-sequence batch takes 32x as long on the host' % (len(times), int(t_now)),
+                      'median s/token; a %d-sequence batch takes %dx as long on the host'
+                      % (len(times), args.batch, int(t_now), args.batch, args.batch),
             'parity_seq0': {'max_abs_logit_diff': round(max(errs), 5), 'steps': n,
                             'same_greedy_token': toks_same}}
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print('bench.py: this build measures one GPU; --gpus %d is not supported (run with --gpus 1)' % args.gpus,
-              file=sys.stderr)
-        sys.exit(2)
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+def build_model(cfg, seed, dtype):
+    from treeattn_amd.engine import weights_from_ours
+    from treeattn_amd.model import GPT
+    torch.manual_seed(seed)
+    model = GPT(cfg)
+    sd = {k: v.detach().to(dtype).cuda() for k, v in model.state_dict().items()}
+    del model
+    return weights_from_ours(sd, cfg)
+
+
+# ------------------------------------------------------------------------------------------ configs 4 and 5
+def decode_bench(args):
+    """KV-cache decode engine with graph-captured steps (config 4, the headline, and config 5)."""
     from treeattn_amd import kernels as K
     from treeattn_amd.config import Config
-    from treeattn_amd.engine import Decoder, weights_from_ours
-    from treeattn_amd.model import GPT
+    from treeattn_amd.engine import Decoder
 
     B, T0, Tcap = args.batch, args.context, args.tcap
     H, C = args.heads, args.embd
@@ -186,12 +211,8 @@ def main():
                  wmax=args.topk, beam=args.topk, beam_mode='fixed', neighbors=False, leaf=args.leaf,
                  arity=args.arity, local=3)
     log('init model (seed 3)')
-    torch.manual_seed(3)
-    model = GPT(cfg)
-    sd = {k: v.detach().to(torch.bfloat16).cuda() for k, v in model.state_dict().items()}
-    del model
-    W = weights_from_ours(sd, cfg)
-    g = torch.Generator().manual_seed(3)
+    W = build_model(cfg, 3, torch.bfloat16)
+    g = torch.Generator().manual_seed(args.ids_seed)
     idx = torch.randint(0, args.vocab, (B, T0), generator=g)
     dec = Decoder(W, args.layers, H, C, Tcap, 'seg', cfg, 'cuda', batch=B, dtype=torch.bfloat16)
     log('prefill %d x %d tokens' % (B, T0))
@@ -251,35 +272,256 @@ def main():
     desc_gbs = desc_bytes / (desc_us * 1e-6) / 1e9
     log('attention %.1f us (%.0f GB/s), descent %.1f us' % (attn_us, attn_gbs, desc_us))
 
+    headline = args.config == 4
     res = {
-        'metric': 'sparse-attn decode tokens/s @bs32x32k; gather-dot GB/s as % of 8 TB/s HBM',
+        'metric': ('sparse-attn decode tokens/s @bs32x32k; gather-dot GB/s as % of 8 TB/s HBM' if headline else
+                   'sparse-attn decode tokens/s @bs1x131k (config 5)'),
         'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
         'ms_per_step': round(ms_step, 4), 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
-        'dtype': 'bf16', 'data': 'synthetic (random-init weights seed 3, uniform random token ids seed 3)',
-        'config': {'workload': 'KV-cache decode engine (config 4): GPT 12L/768/12H, vocab 50304, bf16, batch %d x '
+        'dtype': 'bf16', 'data': 'synthetic (random-init weights seed 3, uniform random token ids seed %d)'
+                                 % args.ids_seed,
+        'config': {'workload': 'KV-cache decode engine (config %d): GPT 12L/768/12H, vocab 50304, bf16, batch %d x '
                                '%d-token prefilled context, greedy decode, leaf %d, arity %d, top-k %d, Tcap %d'
-                               % (B, T0, args.leaf, args.arity, args.topk, Tcap),
+                               % (args.config, B, T0, args.leaf, args.arity, args.topk, Tcap),
                    'batch': B, 'context': T0, 'leaf': args.leaf, 'arity': args.arity, 'topk': args.topk,
                    'tcap': Tcap, 'prefill_s': round(prefill_s, 2)},
-        'roofline': {'bound': 'hbm', 'kernel': 'attn_kernel<bf16_t, 64, true> (split decode attention, one layer)',
+        'roofline': {'bound': 'hbm', 'kernel': 'attn_kernel<bf16_t, 64, true, false> (split decode attention, '
+                                               'one layer)',
                      'achieved': round(attn_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(attn_gbs / HBM_PEAK_GBS, 4),
-                     'traffic': recorded_traffic('attn_kernel_decode'),
-                     'traffic_source': 'profiles/decode_attention_traffic.md (rocprofv3 FETCH_SIZE x2.0 + '
-                                       'WRITE_SIZE x1.0, calibrated on a 256 MiB copy)',
+                     'traffic': recorded_traffic('attn_kernel_decode') if headline else None,
                      'bytes_per_launch': int(attn_bytes), 'avg_us': round(attn_us, 2),
                      'keys_per_query': round(keys_total / (B * H), 1)},
         'kernels': {'descend_us': round(desc_us, 2), 'descend_GB/s': round(desc_gbs, 1),
-                    'descend_bytes': int(desc_bytes)},
+                    'descend_bytes': int(desc_bytes), 'attn_nsplit': sc.nsplit},
     }
-    if not args.no_gather_dot:
+    if headline:
+        res['roofline']['traffic_source'] = ('profiles/decode_attention_traffic.md (rocprofv3 FETCH_SIZE x2.0 + '
+                                             'WRITE_SIZE x1.0, calibrated on a 256 MiB copy)')
+    if headline and not args.no_gather_dot:
         log('gather-dot leg')
         res['gather_dot'] = gather_dot_leg(args)
     if not args.no_cpu:
         log('cpu baseline leg (oracle engine, one sequence)')
-        res['cpu_baseline'] = cpu_baseline_leg(args, cfg, W, dec, int(dec.g_t[0]), dec.g_tok, args.cpu_seconds)
+        res['cpu_baseline'] = cpu_baseline_leg(args, cfg, W, dec, int(dec.g_t[0]), dec.g_tok, args.cpu_seconds,
+                                               max_steps=64 if headline else 16)
     else:
         res['cpu_baseline'] = None
+    return res
+
+
+# ------------------------------------------------------------------------------------------ config 1
+def small_model_bench(args):
+    """Config 1: GPT 6L/384/6H, vocab 256, fp32, weights seed 0, a 512-token prompt (seed 0) and 256 greedy
+    steps at batch 1; the oracle engine (canonical selection order) decodes the same prompt token by token on
+    the host and every step's logits and token are compared.  Run for leaf 32 / top-8 and for leaf 2 (the
+    reference's binary geometry) / top-8."""
+    from oracle.engine_ref import DecoderRef
+    from treeattn_amd import kernels as K
+    from treeattn_amd.config import Config
+    from treeattn_amd.engine import Decoder, weights_from_ours
+    from treeattn_amd.model import GPT
+
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    runs = []
+    for leaf in (args.leaf, 2):
+        cfg = Config(vocab_size=256, seq_len=1024, n_layer=6, n_head=6, n_embd=384, attn='seg', wmax=args.topk,
+                     beam=args.topk, beam_mode='fixed', neighbors=False, leaf=leaf, arity=2, local=3)
+        torch.manual_seed(0)
+        model = GPT(cfg).eval()
+        sd = {k: v.detach() for k, v in model.state_dict().items()}
+        del model
+        Wc = weights_from_ours(sd, cfg)
+        W = weights_from_ours({k: v.cuda() for k, v in sd.items()}, cfg)
+        g = torch.Generator().manual_seed(0)
+        prompt = torch.randint(0, 256, (1, args.context), generator=g)
+        T0, steps = args.context, args.steps
+        # GPU: prefill + graph-captured greedy decode, logits of every step kept
+        dec = Decoder(W, 6, 6, 384, 1024, 'seg', cfg, 'cuda', batch=1, dtype=torch.float32)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        lg = dec.prefill(prompt.cuda())
+        tok = K.argmax_rows(lg)
+        dec.capture(tok, T0)
+        torch.cuda.synchronize()
+        setup_s = time.perf_counter() - t0
+        gl = torch.empty(steps, 256, device='cuda')
+        gt = torch.empty(steps, dtype=torch.long, device='cuda')
+        gl[0] = lg[0]
+        gt[0] = tok[0]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(1, steps):
+            dec.replay()
+            gl[s] = dec.g_logits[0]
+            gt[s] = dec.g_tok[0]
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        tok_s = (steps - 1) / el
+        # host: oracle engine over the prompt then greedy
+        ref = DecoderRef(Wc, 6, 6, 384, 1024, 'seg', cfg, sel_mode='canonical')
+        tc = time.perf_counter()
+        for t in range(T0 - 1):
+            ref.step(int(prompt[0, t]), t)
+        lc, _ = ref.step(int(prompt[0, T0 - 1]), T0 - 1)
+        errs, same, ctimes = [], 0, []
+        gl_c, gt_c = gl.cpu(), gt.cpu()
+        for s in range(steps):
+            errs.append((lc - gl_c[s]).abs().max().item())
+            nc = int(lc.argmax())
+            same += int(nc == int(gt_c[s]))
+            if s + 1 < steps:
+                t1 = time.perf_counter()
+                lc, _ = ref.step(nc, T0 + s)
+                ctimes.append(time.perf_counter() - t1)
+        cpu_total = time.perf_counter() - tc
+        ctimes.sort()
+        runs.append({'leaf': leaf, 'topk': args.topk, 'gpu_tokens_per_s': round(tok_s, 1),
+                     'gpu_ms_per_token': round(1000 / tok_s, 3), 'setup_s': round(setup_s, 2),
+                     'max_abs_logit_diff': float('%.3g' % max(errs)), 'same_greedy_token': same, 'steps': steps,
+                     'cpu_tokens_per_s': round(1.0 / ctimes[len(ctimes) // 2], 2),
+                     'cpu_total_s': round(cpu_total, 1)})
+        log('config 1 leaf %d: %.1f tok/s, max logit diff %.3g, %d/%d tokens same'
+            % (leaf, tok_s, max(errs), same, steps))
+    main_run = runs[0]
+    return {'metric': 'greedy decode tokens/s, small fp32 GPT (config 1)', 'value': main_run['gpu_tokens_per_s'],
+            'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': 0,
+            'ms_per_step': main_run['gpu_ms_per_token'], 'higher_is_better': True, 'scaling': 'weak',
+            'vs_baseline': None, 'dtype': 'f32',
+            'data': 'synthetic (random-init weights seed 0, uniform random prompt ids seed 0)',
+            'config': {'workload': 'GPT 6L/384/6H vocab 256 fp32, batch 1, 512-token prompt, 256 greedy steps, '
+                                   'top-k %d, leaf %d and leaf 2' % (args.topk, args.leaf)},
+            'runs': runs,
+            'cpu_baseline': {'value': main_run['cpu_tokens_per_s'], 'unit': 'tokens/s', 'cores': ncores,
+                             'kind': 'port',
+                             'sample': 'the oracle engine decoding the same 256 greedy steps (after the prompt) '
+                                       'on the host, median s/token'}}
+
+
+# ------------------------------------------------------------------------------------------ config 3
+def config3_inputs(B, H, T, D, seed):
+    """Q, V ~ N(0,1); K = 3 (Z W_h) + E with Z (B,H,T,8) ~ N(0,1), W_h (H,8,D) ~ N(0,1)/sqrt(8), E ~ N(0,1)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, T, D, generator=g)
+    v = torch.randn(B, H, T, D, generator=g)
+    z = torch.randn(B, H, T, 8, generator=g)
+    wh = torch.randn(H, 8, D, generator=g) / math.sqrt(8)
+    k = 3 * torch.matmul(z, wh.unsqueeze(0)) + torch.randn(B, H, T, D, generator=g)
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def prefill_attention_bench(args):
+    """Config 3: the forward pass's sparse attention (SegAttention.sparse_attend with neighbours off):
+    pyramid build, descent for every query, attention over the selected leaf blocks + own block + static
+    keys.  Parity: one (b, h) slice's selection bit for bit and output against the oracle."""
+    from oracle import attn_ref as A
+    from oracle import seg_ref as S
+    from treeattn_amd import kernels as K
+    from treeattn_amd.config import Config
+    from treeattn_amd.selection import cfg_shape, fixed_n_tree
+
+    B, H, T, D = args.batch, 16, args.context, 128
+    cfg = Config(n_head=H, n_embd=H * D, seq_len=T, attn='seg', wmax=args.topk, beam=args.topk, beam_mode='fixed',
+                 neighbors=False, leaf=args.leaf, arity=args.arity, local=3)
+    log('config 3 inputs (seed 2)')
+    qc, kc, vc = config3_inputs(B, H, T, D, 2)
+    q, k, v = qc.cuda(), kc.cuda(), vc.cuda()
+    shape = cfg_shape(cfg, T)
+    levels = shape.alloc_levels(B, H, D, 'cuda')
+    tq = torch.arange(T, dtype=torch.int32, device='cuda')
+    wl = shape.leaf_width(cfg.wmax)
+    ids = torch.empty(B, H, T, wl, dtype=torch.int32, device='cuda')
+    vld = torch.empty(B, H, T, wl, dtype=torch.uint8, device='cuda')
+    sct = torch.empty(B, H, T, wl, device='cuda')
+    n_tree = torch.full((B, H, T), fixed_n_tree(cfg), dtype=torch.int32, device='cuda')
+    out = torch.empty(B, H, T, D, device='cuda', dtype=torch.bfloat16)
+    keys = torch.empty(B, H, T, device='cuda')
+    scale = 1.0 / math.sqrt(D)
+
+    def build():
+        K.level_sums(k, shape.blevels, out=levels, t_end=T)
+
+    def descend():
+        K.tree_descend(q, levels, tq, shape, cfg.wmax, out=(ids, vld, sct))
+
+    def attend():
+        K.seg_attn(q, k, v, tq, ids, vld, n_tree, shape.leaf, cfg.local, scale, out=out, keys=keys)
+
+    for _ in range(args.warmup):
+        build()
+        descend()
+        attend()
+    torch.cuda.synchronize()
+    it = args.steps
+    b_us = time_launches(build, it)
+    d_us = time_launches(descend, it)
+    a_us = time_launches(attend, it)
+    total_us = b_us + d_us + a_us
+    keys_total = float(keys.double().sum())
+    flops = 4.0 * D * keys_total
+    tflops = flops / (a_us * 1e-6) / 1e12
+    attn_bytes = keys_total * D * 2 * 2 + B * H * T * (2 * D * 2 + wl * 5)
+    log('config 3: build %.1f us, descent %.1f us, attention %.1f us (%.1f TFLOP/s)' % (b_us, d_us, a_us, tflops))
+
+    # parity on slice (b, h) = (1, 5): selection bit for bit, output within the bf16 tolerance
+    bb, hh = 1, 5
+    geom = S.Geometry(T, cfg.leaf, cfg.arity)
+    pyr = S.pyramid(S.index_keys(kc[bb:bb + 1, hh:hh + 1]), geom)
+    t_sel = torch.arange(T)
+    rid, rvld, _ = S.tree_pass_general(qc[bb:bb + 1, hh:hh + 1].float(), pyr, t_sel, geom, cfg.wmax, 'canonical')
+    gid = ids[bb:bb + 1, hh:hh + 1].long().cpu()
+    gv = vld[bb:bb + 1, hh:hh + 1].bool().cpu()
+    sel_same = bool(torch.equal(gv, rvld) and torch.equal(torch.where(gv, gid, -1), torch.where(rvld, rid, -1)))
+    lhat = torch.full((1, 1, T), cfg.beam, dtype=torch.long)
+    nid = torch.zeros(1, 1, T, cfg.nb_window * cfg.nb_store, dtype=torch.long)
+    sel = S.finish(rid, rvld, nid, torch.zeros_like(nid, dtype=torch.bool), torch.zeros(1, 1, T, dtype=torch.long),
+                   lhat, cfg, cfg.leaf)
+    cand, keep, _ = A.assemble(sel, t_sel, cfg, 1, 1)
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    cm = torch.where(keep, cand, -1)
+    qs, ks, vs = qc[bb:bb + 1, hh:hh + 1], kc[bb:bb + 1, hh:hh + 1], vc[bb:bb + 1, hh:hh + 1]
+    c0 = time.perf_counter()
+    want = torch.cat([A.sparse_attn_ref(qs[:, :, t0:t0 + 256], ks, vs, cm[:, :, t0:t0 + 256], scale)
+                      for t0 in range(0, T, 256)], 2)     # chunks of 256 queries bound the gathered rows
+    cpu_attn_s = time.perf_counter() - c0
+    err = (out[bb:bb + 1, hh:hh + 1].float().cpu() - want.float()).abs().max().item()
+    log('config 3 parity: selection same %s, max |out - oracle| %.3g' % (sel_same, err))
+    return {'metric': 'prefill sparse attention tokens/s (config 3)', 'value': round(B * T / (total_us * 1e-6), 1),
+            'unit': 'tokens/s', 'n_gpus': 1, 'steps': it, 'warmup': args.warmup,
+            'ms_per_step': round(total_us / 1000, 4), 'higher_is_better': True, 'scaling': 'weak',
+            'vs_baseline': None, 'dtype': 'bf16',
+            'data': 'synthetic (seed 2: Q, V ~ N(0,1), K = 3 Z W_h + E low-rank plus noise)',
+            'config': {'workload': 'SegAttention.sparse_attend, neighbours off: (4,16,16384,128) bf16, leaf %d, '
+                                   'arity %d, top-k %d + own block + static keys' % (args.leaf, args.arity, args.topk)},
+            'phases_us': {'pyramid': round(b_us, 1), 'descent': round(d_us, 1), 'attention': round(a_us, 1)},
+            'roofline': {'bound': 'mfma', 'kernel': 'attn_kernel<bf16_t, 128, false, false> (prefill attention)',
+                         'achieved': round(tflops, 2), 'peak': MFMA_BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                         'frac': round(tflops / MFMA_BF16_PEAK_TFLOPS, 5), 'traffic': None,
+                         'flops_per_launch': flops, 'keys_per_query': round(keys_total / (B * H * T), 1),
+                         'gathered_bytes_per_launch': int(attn_bytes),
+                         'gathered_GB/s': round(attn_bytes / (a_us * 1e-6) / 1e9, 1)},
+            'parity': {'slice': [bb, hh], 'selection_bit_exact': sel_same, 'max_abs_out_diff': float('%.3g' % err)},
+            'cpu_baseline': {'value': round(T / cpu_attn_s, 1), 'unit': 'tokens/s (attention only, one (b,h))',
+                             'cores': ncores, 'kind': 'port',
+                             'sample': 'oracle sparse_attn_ref over the selected keys of one (b, h) slice '
+                                       '(16384 queries); the whole call has 64 such slices'}}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print('bench.py: this build measures one GPU; --gpus %d is not supported (run with --gpus 1)' % args.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    if args.config in (4, 5):
+        res = decode_bench(args)
+    elif args.config == 1:
+        res = small_model_bench(args)
+    else:
+        res = prefill_attention_bench(args)
     print(json.dumps(res), flush=True)
 
 
