@@ -187,6 +187,50 @@ def test_seg_attn_matches_oracle(T, D, leaf, arity, wmax, dtype, beam, nsplit):
     assert torch.equal(keys, keep.sum(-1).float())
 
 
+@pytest.mark.parametrize('T,D,leaf,wmax,dtype,beam,local,tk_extra', [
+    (1000, 64, 32, 8, torch.bfloat16, None, 3, 0),
+    (1024, 128, 64, 4, torch.bfloat16, 3, 3, 0),
+    (2048, 128, 128, 6, torch.float16, None, 3, 0),
+    (777, 64, 64, 5, torch.float16, None, 5, 300),
+    (4096, 128, 64, 16, torch.bfloat16, None, 3, 0)])
+def test_seg_attn_prefill_matrix_cores(T, D, leaf, wmax, dtype, beam, local, tk_extra):
+    """The matrix-core prefill path (one query per position, bf16/f16, leaf >= 32): output, LSE and key counts
+    against the oracle's assembled key lists, including ragged query tiles, a beam narrower than the valid
+    leaves and caches longer than the queries."""
+    print('case', T, D, leaf, wmax, dtype, beam, local, tk_extra, flush=True)
+    B, H = 2, 2
+    cfg = Config(wmax=wmax, beam=beam or wmax, neighbors=False, leaf=leaf, arity=2, local=local, n_head=H)
+    q = rnd(B, H, T, D, seed=70, dtype=dtype)
+    k = rnd(B, H, T + tk_extra, D, seed=71, dtype=dtype)
+    v = rnd(B, H, T + tk_extra, D, seed=72, dtype=dtype)
+    Tg = 1 << (T - 1).bit_length()   # the tree spans a power of two; positions past T hold zero keys
+    geom = S.Geometry(Tg, leaf, 2)
+    kpad = torch.zeros(B, H, Tg, D, dtype=dtype)
+    kpad[:, :, :T] = k[:, :, :T]
+    pyr = S.pyramid(S.index_keys(kpad), geom)
+    tq = torch.arange(T)
+    ids, vld, _ = S.tree_pass_general(q.float(), pyr, tq, geom, wmax, 'canonical')
+    lhat = torch.full((B, H, T), cfg.beam, dtype=torch.long)
+    nid = torch.zeros(B, H, T, cfg.nb_window * cfg.nb_store, dtype=torch.long)
+    sel = S.finish(ids, vld, nid, torch.zeros_like(nid, dtype=torch.bool), torch.zeros(B, H, T, dtype=torch.long),
+                   lhat, cfg, leaf)
+    cand, keep, _ = assemble(sel, tq, cfg, B, H)
+    cm = torch.where(keep, cand, -1)
+    want = torch.cat([sparse_attn_ref(q[:, :, t0:t0 + 256], k, v, cm[:, :, t0:t0 + 256], 1 / math.sqrt(D))
+                      for t0 in range(0, T, 256)], 2)
+    from oracle.attn_ref import sparse_attn_lse
+    want_lse = torch.cat([sparse_attn_lse(q[:, :, t0:t0 + 256], k, v, cm[:, :, t0:t0 + 256], 1 / math.sqrt(D))
+                          for t0 in range(0, T, 256)], 2)
+    gi = torch.where(vld, ids, -1).to(torch.int32)
+    lse = torch.empty(B, H, T, device=DEV)
+    keys = torch.empty(B, H, T, device=DEV)
+    out, _, _ = K.seg_attn(q.to(DEV), k.to(DEV), v.to(DEV), tq.to(DEV), gi.to(DEV), vld.to(torch.uint8).to(DEV),
+                           sel['n_tree'].to(DEV), leaf, local, 1 / math.sqrt(D), lse=lse, keys=keys, nsplit=1)
+    assert torch.equal(keys.cpu(), keep.sum(-1).float())
+    assert (out.cpu().float() - want.float()).abs().max().item() < TOL[dtype]
+    assert (lse.cpu() - want_lse).abs().max().item() < 1e-2
+
+
 def test_seg_attn_split_merge_reuses_workspace():
     """Several workgroups per query, merged by the last to arrive: a workspace reused across calls (its
     counters return to zero) gives identical results each time, and output and LSE agree with one workgroup

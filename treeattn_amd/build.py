@@ -24,6 +24,7 @@ SOURCES = {
     'sample.hip': [],
     'gemm.hip': [],
     'gather_blocks.hip': [],
+    'prefill_attn.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

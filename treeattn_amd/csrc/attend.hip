@@ -16,37 +16,12 @@
 #include <utility>
 
 #include "append.hpp"
+#include "attn.hpp"
 #include "common.hpp"
 
 namespace ta {
 
-struct AttnParams {
-  const void* q;
-  int64_t qsb, qsh, qsn;
-  const void* k;
-  int64_t ksb, ksh, kst;
-  const void* v;
-  int64_t vsb, vsh, vst;
-  int H, Nq, Tk;
-  const int32_t* tq;
-  int64_t tq_sb;
-  const int32_t* cand;  // explicit candidate list mode when non-null
-  int KC;
-  const int32_t* ids;
-  const uint8_t* vld;
-  const int32_t* n_tree;
-  int wl, leaf_log2, Lw;
-  float scale;
-  int gsplit;           // workgroups per query (split mode)
-  void* out;
-  int64_t osb, osh, osn;
-  float* lse;
-  float* keys;
-  float* ws;            // per-workgroup partials (query, gsplit, D + 2) when gsplit > 1
-  uint32_t* cnt;        // per-query arrival counters when gsplit > 1 (zero between calls)
-};
 
-constexpr float kNegBig = -1e30f;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
@@ -572,6 +547,11 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
   if (need > 0) {
     p.cnt = reinterpret_cast<uint32_t*>(ws);
     p.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + attn_counter_bytes(B, H, Nq));
+  }
+  if (nsplit == 1) {
+    // many queries (prefill): the matrix-core kernel when the shape fits it
+    const int rc = prefill_attn_mfma(p, B, dtype, D, (hipStream_t)stream);
+    if (rc != TA_ERR_UNSUPPORTED) return rc;
   }
   return dispatch_attn(dtype, D, p, B, nsplit > 1, (hipStream_t)stream);
 }
