@@ -106,11 +106,15 @@ def recorded_traffic(name):
     return None
 
 
-def time_launches(fn, iters):
-    """Average duration (us) of fn's GPU work, from HIP events recorded on the launching stream."""
+def time_launches(fn, iters, flush=None):
+    """Average duration (us) of fn's GPU work, from HIP events recorded on the launching stream.  With
+    `flush` (a large device tensor) it is overwritten before every launch, so the launch starts with cold
+    caches (the MI355X last-level cache holds 256 MB) as it does inside a decode step."""
     st = torch.cuda.current_stream()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
-    for a, b in evs:
+    for i, (a, b) in enumerate(evs):
+        if flush is not None:
+            flush.fill_(i & 1)
         a.record(st)
         fn()
         b.record(st)
@@ -261,8 +265,11 @@ def decode_bench(args):
     for _ in range(3):
         attn()
         descend()
-    attn_us = time_launches(attn, args.kernel_iters)
-    desc_us = time_launches(descend, args.kernel_iters)
+    flush = torch.empty(1 << 28, dtype=torch.float32, device='cuda')   # 1 GiB, overwritten before each launch
+    attn_us = time_launches(attn, args.kernel_iters, flush)
+    desc_us = time_launches(descend, args.kernel_iters, flush)
+    attn_warm_us = time_launches(attn, args.kernel_iters)
+    del flush
     keys_total = float(keys.sum())
     elem = 2
     wl = ids.shape[-1]
@@ -291,6 +298,8 @@ def decode_bench(args):
                      'frac': round(attn_gbs / HBM_PEAK_GBS, 4),
                      'traffic': recorded_traffic('attn_kernel_decode') if headline else None,
                      'bytes_per_launch': int(attn_bytes), 'avg_us': round(attn_us, 2),
+                     'timing': 'cold caches (1 GiB overwritten before each of %d launches)' % args.kernel_iters,
+                     'avg_us_warm_cache': round(attn_warm_us, 2),
                      'keys_per_query': round(keys_total / (B * H), 1)},
         'kernels': {'descend_us': round(desc_us, 2), 'descend_GB/s': round(desc_gbs, 1),
                     'descend_bytes': int(desc_bytes), 'attn_nsplit': sc.nsplit},
