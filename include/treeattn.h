@@ -208,6 +208,15 @@ int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, in
 int ta_argmax_rows(const void* x, int dtype, int64_t rows, int64_t n, int64_t stride, int64_t* out,
                    void* stream);
 
+/*
+ * First op of a decode step (engine.py:168, x = wte[tok] + wpe[t]): x[b, :] = wte[tok[b], :] + wpe[t[b], :]
+ * in dtype (the sum rounded once), pos32[b] = t[b]; with `advance`, t[b] += 1 afterwards (the next step's
+ * position, so a captured step can be replayed).  tok, t: int64 (B,); tables with row strides ldw, ldp.
+ */
+int ta_embed(const int64_t* tok, int64_t* tpos, int advance, const void* wte, int64_t ldw, const void* wpe,
+             int64_t ldp, int dtype, int B, int C, int64_t V, int64_t P, void* x, int64_t ldx, int32_t* pos32,
+             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -436,3 +436,20 @@ def test_descend_append_equals_two_calls(leaf, arity, B, H, dtype):
     assert torch.equal(state[0][0], state[1][0]) and torch.equal(state[0][1], state[1][1])
     for x, y in zip(state[0][2], state[1][2]):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+def test_embed_matches_table_sum(dtype):
+    """x = wte[tok] + wpe[t] (rounded once), int32 positions, and the in-place position advance."""
+    B, C, V, P = 5, 96, 300, 64
+    wte = rnd(V, C, seed=80, dtype=dtype).to(DEV)
+    wpe = rnd(P, C, seed=81, dtype=dtype).to(DEV)
+    tok = torch.tensor([0, 299, 17, 5, 128], device=DEV)
+    t = torch.tensor([0, 63, 7, 31, 40], device=DEV)
+    x = torch.empty(B, C, device=DEV, dtype=dtype)
+    pos32 = torch.empty(B, device=DEV, dtype=torch.int32)
+    K.embed(tok, t, wte, wpe, out=x, pos32=pos32)
+    assert torch.equal(x, wte[tok] + wpe[t])
+    assert pos32.tolist() == t.tolist()
+    K.embed(tok, t, wte, wpe, out=x, pos32=pos32, advance=True)
+    assert pos32.tolist() == [0, 63, 7, 31, 40] and t.tolist() == [1, 64, 8, 32, 41]

@@ -50,6 +50,8 @@ SIGNATURES = {
                              c_i32, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32,
                              c_i32, c_vp]),
     'ta_argmax_rows': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_vp]),
+    'ta_embed': (c_i32, [c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_i64, c_i32, c_i32, c_i32, c_i64, c_i64, c_vp,
+                         c_i64, c_vp, c_vp]),
     'ta_rowmm_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32]),
     'ta_rowmm': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32, c_i32,
                          c_i32, c_vp, c_i64, c_vp]),

@@ -80,9 +80,60 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const T* __
   }
 }
 
+// The decode step's first op: x[b] = wte[tok[b]] + wpe[t[b]] rounded to the element type (as the
+// reference's bf16 sum does), the positions as int32 for the later kernels, and optionally t[b] += 1 for
+// the next step.  One workgroup per sequence; token and position clamped to the tables.
+template <typename T>
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ tok, int64_t* tpos, int advance,
+                                                    const T* __restrict__ wte, int64_t ldw, const T* __restrict__ wpe,
+                                                    int64_t ldp, int C, int64_t V, int64_t P, T* __restrict__ x,
+                                                    int64_t ldx, int32_t* __restrict__ pos32) {
+  const int b = blockIdx.x;
+  int64_t tk = tok[b], t = tpos[b];
+  tk = tk < 0 ? 0 : (tk >= V ? V - 1 : tk);
+  const int64_t tc = t < 0 ? 0 : (t >= P ? P - 1 : t);
+  const T* er = wte + tk * ldw;
+  const T* pr = wpe + tc * ldp;
+  T* xr = x + (int64_t)b * ldx;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) xr[c] = from_f32<T>(to_f32(er[c]) + to_f32(pr[c]));
+  __syncthreads();   // every thread has read tpos[b] before it may change
+  if (threadIdx.x == 0) {
+    pos32[b] = (int32_t)t;
+    if (advance) tpos[b] = t + 1;
+  }
+}
+
 }  // namespace ta
 
 using namespace ta;
+
+extern "C" int ta_embed(const int64_t* tok, int64_t* tpos, int advance, const void* wte, int64_t ldw, const void* wpe,
+                        int64_t ldp, int dtype, int B, int C, int64_t V, int64_t P, void* x, int64_t ldx,
+                        int32_t* pos32, void* stream) {
+  if (B <= 0 || C <= 0 || V <= 0 || P <= 0 || ldw < C || ldp < C || ldx < C) {
+    set_error("ta_embed: bad sizes");
+    return TA_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case TA_F32:
+      hipLaunchKernelGGL((embed_kernel<float>), dim3(B), dim3(256), 0, st, tok, tpos, advance, (const float*)wte, ldw,
+                         (const float*)wpe, ldp, C, V, P, (float*)x, ldx, pos32);
+      break;
+    case TA_F16:
+      hipLaunchKernelGGL((embed_kernel<f16_t>), dim3(B), dim3(256), 0, st, tok, tpos, advance, (const f16_t*)wte, ldw,
+                         (const f16_t*)wpe, ldp, C, V, P, (f16_t*)x, ldx, pos32);
+      break;
+    case TA_BF16:
+      hipLaunchKernelGGL((embed_kernel<bf16_t>), dim3(B), dim3(256), 0, st, tok, tpos, advance, (const bf16_t*)wte,
+                         ldw, (const bf16_t*)wpe, ldp, C, V, P, (bf16_t*)x, ldx, pos32);
+      break;
+    default:
+      set_error("unknown dtype");
+      return TA_ERR_ARG;
+  }
+  return check_launch("embed_kernel");
+}
 
 extern "C" int ta_argmax_rows(const void* x, int dtype, int64_t rows, int64_t n, int64_t stride, int64_t* out,
                               void* stream) {

@@ -293,7 +293,9 @@ class Decoder:
                 self.groups.append(dict(
                     b0=b0, b1=b1, states=[st.rows(b0, b1) for st in self.states],
                     scratch=_Scratch(n, H, dh, wl, self.dev, decode_nsplit(n, H, wl, sh.leaf), self.nl),
-                    stream=torch.cuda.Stream(device=self.dev) if G > 1 else None))
+                    stream=torch.cuda.Stream(device=self.dev) if G > 1 else None,
+                    x=torch.empty(n, self.C, device=self.dev, dtype=self.dtype),
+                    pos32=torch.empty(n, device=self.dev, dtype=torch.int32)))
         else:
             self.states = [DenseState(self.Tcap, H, dh, self.dev, B, self.dtype) for _ in range(self.nl)]
         self.graph = None
@@ -324,13 +326,15 @@ class Decoder:
             x = x + F.linear(F.gelu(F.linear(_ln(x, L['ln2']), L['c_fc'])), L['c_mlp'])
         return F.linear(_ln(x, W['ln_f']), W['wte'])[:, 0]
 
-    def _group_step(self, grp, tok, tpos, logits):
-        """One decode step for the sequences of one group (rows b0..b1-1), logits into `logits` rows."""
+    def _group_step(self, grp, tok, tpos, logits, advance=False):
+        """One decode step for the sequences of one group (rows b0..b1-1), logits into `logits` rows.  With
+        `advance` the positions tpos are incremented (by the embedding kernel, after it has read them)."""
         W, H, C, dh = self.W, self.H, self.C, self.dh
         B = grp['b1'] - grp['b0']
         sc = grp['scratch']
-        x = W['wte'][tok] + W['wpe'][tpos]
-        tpos32 = tpos.to(torch.int32)
+        x = grp['x']
+        K.embed(tok, tpos, W['wte'], W['wpe'], out=x, pos32=grp['pos32'], advance=advance)
+        tpos32 = grp['pos32']
         for i, L in enumerate(W['layers']):
             qkv = sc.mm(x, L['c_attn'], ln_w=L['ln1'])
             q, k, v = [a.view(B, 1, H, dh).transpose(1, 2) for a in qkv.split(C, -1)]
@@ -376,9 +380,10 @@ class Decoder:
         """Feed `tok` at position t.  tok int (batch 1, reference signature) -> (logits (V,), keys float);
         tok LongTensor(B) -> (logits (B,V), keys (B,) tensor); t int or (B,) positions."""
         scalar = not torch.is_tensor(tok)
-        tk = torch.as_tensor(tok, device=self.dev).long().reshape(-1).expand(self.B) if scalar else tok.to(self.dev).long()
-        tp = t.to(self.dev).long() if torch.is_tensor(t) else torch.full((self.B,), int(t), device=self.dev,
-                                                                        dtype=torch.long)
+        tk = (torch.as_tensor(tok, device=self.dev).long().reshape(-1).expand(self.B) if scalar
+              else tok.to(self.dev).long()).contiguous()
+        tp = (t.to(self.dev).long().contiguous() if torch.is_tensor(t) else
+              torch.full((self.B,), int(t), device=self.dev, dtype=torch.long))
         logits = self._forward_step(tk, tp)
         keys = self.keys_read()
         if scalar and self.B == 1:
@@ -454,11 +459,14 @@ class Decoder:
 
             def body():
                 if grp is not None:
-                    self._group_step(grp, tok_g, t_g, lg_g)
+                    self._group_step(grp, tok_g, t_g, lg_g, advance=True)
+                elif self.fused:
+                    self._group_step(self.groups[0], tok_g, t_g, lg_g, advance=True)
                 else:
                     lg_g.copy_(self._forward_step(tok_g, t_g))
                 K.argmax_rows(lg_g, out=tok_g)
-                t_g.add_(1)
+                if not self.fused:
+                    t_g.add_(1)
 
             # Warm up on the capture stream (library handles, allocator).  The step at a fixed (token, position)
             # is idempotent -- it rewrites the same cache row and recomputes the same nodes -- so running it here

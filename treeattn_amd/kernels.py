@@ -269,6 +269,23 @@ def argmax_rows(x, out=None):
     return out
 
 
+def embed(tok, tpos, wte, wpe, out, pos32, advance=False):
+    """out[b] = wte[tok[b]] + wpe[tpos[b]] (B, C) in the tables' dtype; pos32[b] = tpos[b]; with `advance`
+    tpos is incremented in place afterwards.  tok, tpos: int64 (B,)."""
+    L.require_gpu(tok, tpos, wte, wpe, out, pos32)
+    if tok.dtype != torch.long or tpos.dtype != torch.long or pos32.dtype != torch.int32:
+        raise TypeError('embed: tok and tpos int64, pos32 int32')
+    if not (wte.dtype == wpe.dtype == out.dtype) or wte.stride(1) != 1 or wpe.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError('embed: tables and output must share a dtype with contiguous rows')
+    if not (tok.is_contiguous() and tpos.is_contiguous() and pos32.is_contiguous()):
+        raise ValueError('embed: token and position vectors must be contiguous')
+    B, C = out.shape
+    L.call('ta_embed', L.ptr(tok), L.ptr(tpos), int(bool(advance)), L.ptr(wte), wte.stride(0), L.ptr(wpe),
+           wpe.stride(0), L.dtype_code(wte), B, C, wte.shape[0], wpe.shape[0], L.ptr(out), out.stride(0), L.ptr(pos32),
+           L.stream())
+    return out
+
+
 # ----------------------------------------------------------------------------------------------- decode append
 def kv_append(k_new, v_new, Kc, Vc, t_pos, levels, leaf, arity):
     """Write k_new, v_new (B,H,D) at row t_pos[b] of the caches (B,H,Tcap,D) and form the completed nodes."""
