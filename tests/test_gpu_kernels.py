@@ -121,7 +121,9 @@ def test_gather_dot_bit_exact(dtype, D):
 
 @pytest.mark.parametrize('T,D,NB,blk,dtype,N', [(512, 64, 4, 64, torch.bfloat16, 512), (4096, 64, 16, 64, torch.bfloat16, 200),
                                                (1024, 128, 8, 128, torch.bfloat16, 77), (512, 64, 5, 32, torch.float16, 96),
-                                               (512, 16, 4, 64, torch.bfloat16, 64)])
+                                               (512, 16, 4, 64, torch.bfloat16, 64), (65536, 64, 16, 64, torch.bfloat16, 64),
+                                               (2048, 128, 16, 32, torch.float16, 45), (256, 64, 1, 128, torch.bfloat16, 33),
+                                               (128, 64, 16, 64, torch.bfloat16, 100)])
 def test_gather_dot_blocks(T, D, NB, blk, dtype, N):
     """Block gather-dot against the oracle: matrix-core path within a few float32 ulps of the canonical sum
     (exact bf16 products, different summation order); the canonical path (D=16) bit for bit."""
