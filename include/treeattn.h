@@ -217,6 +217,68 @@ int ta_embed(const int64_t* tok, int64_t* tpos, int advance, const void* wte, in
              int64_t ldp, int dtype, int B, int C, int64_t V, int64_t P, void* x, int64_t ldx, int32_t* pos32,
              void* stream);
 
+/*
+ * The whole decode step in one launch (replaces Decoder.step, engine.py:161-177, with seg_attend in the
+ * structural mode, engine.py:84-120, SegState.add, engine.py:41-55, and the greedy argmax of
+ * phase2.py:51-66): embedding, every layer (LN1 + c_attn, cache append + beam descent + attention per
+ * (sequence, head), c_proj + residual, LN2 + c_fc + GELU, c_mlp + residual), LN_f + logits and the greedy
+ * token, for a bf16 GPT with head_dim 64 and up to 32 sequences.  The results equal the per-op entry
+ * points above run in the same order (ta_rowmm with the same split of c_mlp, ta_tree_descend_append,
+ * ta_seg_attn_fwd with one workgroup per query, ta_argmax_rows), bit for bit.
+ *
+ * ta_decode_step_prepare writes the step's plan (task list, tensor addresses) into the workspace `ws`
+ * (ta_decode_step_workspace_size bytes, 256-byte aligned; it also holds the step's activations and
+ * counters), zeroes its counters, waits for the stream, and fills `out` with the launch shape.  The model's
+ * tensors must stay at the addresses given.  ta_decode_step then enqueues one step: tokens tok (B, int64)
+ * at positions tpos (B, int64) -> logits (B, vocab) bf16 with row stride ld_logits; tok_out (may alias
+ * tok, or NULL) receives the greedy tokens; with `advance` every tpos[b] is incremented; keys (n_layer,
+ * B, n_head) float32, or NULL, receives the keys attended; trace (launch->n_tasks, 16) int64, or NULL,
+ * receives per task the wall-clock ticks (hipDeviceAttributeWallClockRate) when a workgroup took it, when
+ * its input wait ended, at up to ten points inside it (0 where a task has none) and when it finished, then
+ * that workgroup's CU id and two zeros.  Steps that share a workspace must not overlap
+ * in time.  The step waits on its own counters with a bounded wait (two seconds); when one runs out the
+ * step completes with wrong results and ta_decode_step_error reports 1 (it reads the flag synchronously;
+ * the flag stays set until the next prepare).
+ */
+#define TA_MAX_TREE_LEVELS 32
+
+typedef struct ta_step_layer {
+  const void* ln1;       /* (n_embd) */
+  const void* c_attn;    /* (3 n_embd, n_embd) */
+  const void* c_proj;    /* (n_embd, n_embd) */
+  const void* ln2;       /* (n_embd) */
+  const void* c_fc;      /* (n_ff, n_embd) */
+  const void* c_mlp;     /* (n_embd, n_ff) */
+  void* k_cache;         /* (batch, n_head, tcap, head_dim) */
+  void* v_cache;         /* same shape and strides as k_cache */
+  int64_t c_sb, c_sh, c_st;
+  float* levels[TA_MAX_TREE_LEVELS];   /* node sums of tree level j (node rows of head_dim floats) */
+  int64_t lv_sb[TA_MAX_TREE_LEVELS], lv_sh[TA_MAX_TREE_LEVELS];
+} ta_step_layer;
+
+typedef struct ta_step_model {
+  int n_layer, n_head, head_dim, n_embd, n_ff, vocab, n_pos, batch, tcap;
+  int leaf, arity, n_levels, wmax, n_tree, local;
+  int mlp_splits;        /* workgroups per c_mlp output tile along K */
+  float ln_eps;
+  const void* wte;       /* (vocab, n_embd), row stride ld_wte; also the tied output head */
+  int64_t ld_wte;
+  const void* wpe;       /* (n_pos, n_embd), row stride ld_wpe */
+  int64_t ld_wpe;
+  const void* ln_f;      /* (n_embd) */
+  const ta_step_layer* layers;   /* n_layer entries (host memory) */
+} ta_step_model;
+
+typedef struct ta_step_launch {
+  int grid, lds_bytes, n_tasks, head_dim;
+} ta_step_launch;
+
+int64_t ta_decode_step_workspace_size(const ta_step_model* m);
+int ta_decode_step_prepare(const ta_step_model* m, void* ws, int64_t ws_bytes, ta_step_launch* out, void* stream);
+int ta_decode_step(const ta_step_launch* launch, void* ws, const int64_t* tok, int64_t* tok_out, int64_t* tpos,
+                   int advance, void* logits, int64_t ld_logits, float* keys, int64_t* trace, void* stream);
+int ta_decode_step_error(const void* ws, int* error, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,31 @@ _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 _P = ctypes.POINTER
 
+MAX_TREE_LEVELS = 32
+
+
+class StepLayer(ctypes.Structure):
+    """ta_step_layer"""
+    _fields_ = [('ln1', c_vp), ('c_attn', c_vp), ('c_proj', c_vp), ('ln2', c_vp), ('c_fc', c_vp), ('c_mlp', c_vp),
+                ('k_cache', c_vp), ('v_cache', c_vp), ('c_sb', c_i64), ('c_sh', c_i64), ('c_st', c_i64),
+                ('levels', c_vp * MAX_TREE_LEVELS), ('lv_sb', c_i64 * MAX_TREE_LEVELS),
+                ('lv_sh', c_i64 * MAX_TREE_LEVELS)]
+
+
+class StepModel(ctypes.Structure):
+    """ta_step_model"""
+    _fields_ = [('n_layer', c_i32), ('n_head', c_i32), ('head_dim', c_i32), ('n_embd', c_i32), ('n_ff', c_i32),
+                ('vocab', c_i32), ('n_pos', c_i32), ('batch', c_i32), ('tcap', c_i32), ('leaf', c_i32),
+                ('arity', c_i32), ('n_levels', c_i32), ('wmax', c_i32), ('n_tree', c_i32), ('local', c_i32),
+                ('mlp_splits', c_i32), ('ln_eps', c_f32), ('wte', c_vp), ('ld_wte', c_i64), ('wpe', c_vp),
+                ('ld_wpe', c_i64), ('ln_f', c_vp), ('layers', ctypes.POINTER(StepLayer))]
+
+
+class StepLaunch(ctypes.Structure):
+    """ta_step_launch"""
+    _fields_ = [('grid', c_i32), ('lds_bytes', c_i32), ('n_tasks', c_i32), ('head_dim', c_i32)]
+
+
 # name -> (restype, argtypes); mirrors include/treeattn.h
 SIGNATURES = {
     'ta_abi_version': (c_i32, []),
@@ -55,6 +80,10 @@ SIGNATURES = {
     'ta_rowmm_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32]),
     'ta_rowmm': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32, c_i32,
                          c_i32, c_vp, c_i64, c_vp]),
+    'ta_decode_step_workspace_size': (c_i64, [_P(StepModel)]),
+    'ta_decode_step_prepare': (c_i32, [_P(StepModel), c_vp, c_i64, _P(StepLaunch), c_vp]),
+    'ta_decode_step': (c_i32, [_P(StepLaunch), c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp]),
+    'ta_decode_step_error': (c_i32, [c_vp, _P(c_i32), c_vp]),
 }
 
 _lib = None

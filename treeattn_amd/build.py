@@ -25,6 +25,7 @@ SOURCES = {
     'gemm.hip': [],
     'gather_blocks.hip': [],
     'prefill_attn.hip': [],
+    'step.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

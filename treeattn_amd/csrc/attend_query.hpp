@@ -1,0 +1,369 @@
+// Sparse softmax attention of one query over the keys it selected, shared by the attention kernels
+// (attend.hip) and the persistent decode step (step.hip).
+//
+// Reference functions replaced: fastseg.py:50-78 (_attn_fwd), fastseg.py:134-177 (sparse_attn),
+// fastseg.py:367-383 (candidate assembly + dedupe_fast), engine.py:107-119 (decode attention).
+#pragma once
+
+#include "attn.hpp"
+#include "common.hpp"
+
+namespace ta {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of G lanes (G a power of two up to 64); every lane of a group gets the sum.
+// Quad permutes pair lanes within quads; after them the value repeats every 4 lanes, so mirroring each
+// half-row (lane j <-> 7 - j) pairs the two quads of an 8-lane group, and mirroring the row (j <-> 15 - j)
+// the two halves of a 16-lane group.
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (G >= 2) x += dpp_f<0xB1>(x);    // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) x += dpp_f<0x4E>(x);    // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) x += dpp_f<0x141>(x);   // row_half_mirror
+  if constexpr (G >= 16) x += dpp_f<0x140>(x);  // row_mirror
+  if constexpr (G >= 32) x += __shfl_xor(x, 16, kWave);
+  if constexpr (G >= 64) x += __shfl_xor(x, 32, kWave);
+  return x;
+}
+constexpr int kWavesPerBlock = 4;
+template <typename T> struct Raw16;  // 16 bytes of T -> EPL floats
+template <> struct Raw16<float> {
+  static constexpr int EPL = 4;
+  __device__ static void cvt(const uint4& u, float (&f)[4]) {
+    f[0] = __uint_as_float(u.x); f[1] = __uint_as_float(u.y); f[2] = __uint_as_float(u.z); f[3] = __uint_as_float(u.w);
+  }
+};
+template <> struct Raw16<bf16_t> {
+  static constexpr int EPL = 8;
+  __device__ static void cvt(const uint4& u, float (&f)[8]) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+template <> struct Raw16<f16_t> {
+  static constexpr int EPL = 8;
+  __device__ static void cvt(const uint4& u, float (&f)[8]) {
+    const f16_t* h = reinterpret_cast<const f16_t*>(&u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)h[i];
+  }
+};
+
+// Attention of queries over their key lists.  Rows of K and V are read as 16-byte slices: LPR = D / EPL
+// lanes share a row (EPL elements each) and one load instruction covers RPI = 64 / LPR consecutive keys,
+// so a leaf block is read in contiguous 1 KB pieces.  A chunk is NL load instructions = KPC keys; the loads
+// of the next PF chunks are in flight while one is consumed.  Scores are reduced over the LPR lanes of
+// a row; every lane keeps a weighted-V accumulator for its EPL dimensions, reduced over the RPI row groups
+// at the end.
+//   SPLIT = false: one wavefront per query (many queries: prefill).
+//   SPLIT = true: the 4 wavefronts of a workgroup share one query and interleave its chunks; their partial
+//   (max, sum, accumulator) are merged in LDS.  With gsplit > 1 workgroups per query each writes its merged
+//   partial to ws with stores that write through to memory, waits for them to complete and counts itself in;
+//   the last to arrive reads the partials past the caches, combines them
+//   (out = sum_g acc_g e^(m_g - M) / sum_g L_g e^(m_g - M)) and resets the counter.  No workgroup waits for
+//   another.
+// Per query: n (index in its (sequence, head) row), g (split index), b, h, qi (flat query index for the
+// per-query arrays of p), qrow (the query's D elements), t (position; structural mode), idr / vr (selected
+// leaf-block ids and their validity; structural mode), nv_given (number of valid ids when >= 0, else counted
+// from vr), nt (budget of tree leaves), orow_base (the output row), smem_f (LDS of the workgroup).
+template <typename T, int D, bool SPLIT, bool CAND>
+__device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, int b, int h, int64_t qi, const T* qrow,
+                                           int t, const int32_t* idr, const uint8_t* vr, int nv_given, int nt,
+                                           T* orow_base, float* smem_f) {
+  constexpr int EPL = Raw16<T>::EPL;
+  constexpr int LPR = D / EPL;              // lanes per key row
+  static_assert(LPR >= 1 && LPR <= kWave, "row slice layout");
+  constexpr int RPI = kWave / LPR;          // key rows per load instruction
+  constexpr int NL = 2;                     // load instructions per chunk (4 chunks in flight ahead)
+  constexpr int KPC = NL * RPI;             // keys per chunk
+  const int lane = lane_id(), w = wave_id();
+  (void)n;
+  (void)b;
+  (void)h;
+  const int wl_pad = p.cand ? 0 : ((p.wl + 3) & ~3);
+  int32_t* s_ids = reinterpret_cast<int32_t*>(smem_f + w * (wl_pad + kWave));
+  int32_t* s_ext = s_ids + wl_pad;
+  const int rg = lane / LPR;               // key row of this lane inside a load instruction
+  const int ds = (lane % LPR) * EPL;       // first dimension of this lane's slice
+
+  float qv[EPL];
+  load_row<T, EPL>(qrow + ds, qv);
+
+  // key list of this query
+  int N, nused = 0, lb = 0, nloc = 0, next = 0;
+  const int leaf = 1 << p.leaf_log2;
+  if constexpr (CAND) {
+    N = p.KC;
+  } else {
+    if (t >= p.Tk) t = -1;  // out of range: attend nothing
+    int nv = nv_given;
+    if (nv < 0) {
+      nv = 0;
+      for (int i0 = 0; i0 < p.wl; i0 += kWave) {
+        const int i = i0 + lane;
+        const bool v = i < p.wl && vr[i] != 0;
+        nv += __popcll(__ballot(v));
+      }
+    }
+    nused = t < 0 ? 0 : (nv < nt ? nv : (nt > 0 ? nt : 0));
+    for (int i = lane; i < nused; i += kWave) s_ids[i] = idr[i];
+    lb = t < 0 ? 0 : (t >> p.leaf_log2) << p.leaf_log2;
+    nloc = t < 0 ? 0 : t - lb + 1;
+    wave_sync();
+    // static keys [0, t, t-1, ..., t-Lw+1]: keep those >= 0, outside the own block, whose leaf block is
+    // not used, and not a repeat of the sink
+    int pe = -1;
+    if (lane <= p.Lw && t >= 0) pe = lane == 0 ? 0 : t - (lane - 1);
+    bool keep = pe >= 0 && pe < lb && !(lane > 0 && pe == 0);
+    if (keep) {
+      const int lf = pe >> p.leaf_log2;
+      for (int i = 0; i < nused; ++i)
+        if (s_ids[i] == lf) keep = false;
+    }
+    const uint64_t bal = __ballot(keep);
+    if (keep) s_ext[__popcll(bal & ((1ull << lane) - 1))] = pe;
+    next = __popcll(bal);
+    N = nused * leaf + nloc + next;
+  }
+  wave_sync();
+
+  const char* kb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.k) + b * p.ksb + h * p.ksh + ds);
+  const char* vb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.v) + b * p.vsb + h * p.vsh + ds);
+  const int64_t kst_b = p.kst * (int64_t)sizeof(T), vst_b = p.vst * (int64_t)sizeof(T);
+  const int nchunks = (N + KPC - 1) / KPC;
+  const int nl = nused * leaf;
+  const int stride = SPLIT ? p.gsplit * kWavesPerBlock : 1;
+  const int first = SPLIT ? g * kWavesPerBlock + w : 0;
+
+  // All positions of a chunk first (branch-free LDS reads in the structural mode, so no wait on memory
+  // sits between the K/V loads), then its K/V loads.
+  auto fetch = [&](int c, uint4 (&kr)[NL], uint4 (&vr)[NL], bool (&ok)[NL]) {
+    int pos[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int key = c * KPC + i * RPI + rg;
+      if constexpr (CAND) {
+        pos[i] = key < N ? p.cand[qi * p.KC + key] : -1;
+      } else {
+        const int kt = key < nl ? key : 0;
+        const int leafpos = (s_ids[kt >> p.leaf_log2] << p.leaf_log2) + (kt & (leaf - 1));
+        const int ke = key - nl - nloc;
+        const int extpos = s_ext[(ke >= 0 && ke < next) ? ke : 0];
+        pos[i] = key < nl ? leafpos : (key < nl + nloc ? lb + (key - nl) : (key < N ? extpos : -1));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      ok[i] = pos[i] >= 0 && pos[i] < p.Tk;
+      const int64_t row = ok[i] ? pos[i] : 0;
+      kr[i] = ldg16(kb + row * kst_b);
+      vr[i] = ldg16(vb + row * vst_b);
+    }
+  };
+
+  float m = kNegBig, l = 0.0f;
+  float acc[EPL];
+#pragma unroll
+  for (int d = 0; d < EPL; ++d) acc[d] = 0.0f;
+
+  auto consume = [&](const uint4 (&kr)[NL], const uint4 (&vr)[NL], const bool (&ok)[NL]) {
+    float sc[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      float kv[EPL];
+      Raw16<T>::cvt(kr[i], kv);
+      float d0 = 0.0f;
+#pragma unroll
+      for (int d = 0; d < EPL; ++d) d0 = fmaf(qv[d], kv[d], d0);
+      sc[i] = d0;
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) sc[i] = group_sum<LPR>(sc[i]);
+    // running max per row group (its LPR lanes see the same scores); the groups merge at the end
+    float cm = kNegBig;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      sc[i] = ok[i] ? sc[i] * p.scale : kNegBig;
+      cm = fmaxf(cm, sc[i]);
+    }
+    const float mn = fmaxf(m, cm);
+    {
+      const float alpha = __expf(m - mn);
+#pragma unroll
+      for (int d = 0; d < EPL; ++d) acc[d] *= alpha;
+      l *= alpha;
+    }
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const float pw = ok[i] ? __expf(sc[i] - mn) : 0.0f;
+      lsum += pw;
+      float vv[EPL];
+      Raw16<T>::cvt(vr[i], vv);
+#pragma unroll
+      for (int d = 0; d < EPL; ++d) acc[d] = fmaf(pw, vv[d], acc[d]);
+    }
+    if (lane % LPR == 0) l += lsum;
+    m = mn;
+  };
+
+  {
+    constexpr int PF = 4;   // measured with cold caches at config 4: 46.9 us (8 loads x 1 ahead: 49.9 us)
+    uint4 kq[PF][NL], vq[PF][NL];
+    bool okq[PF][NL];
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+      if (first + j * stride < nchunks) fetch(first + j * stride, kq[j], vq[j], okq[j]);
+    int c = first;
+    while (c < nchunks) {
+      const int cn = c + PF * stride;
+      uint4 kn[NL], vn[NL];
+      bool okn[NL];
+      if (cn < nchunks) fetch(cn, kn, vn, okn);
+      consume(kq[0], vq[0], okq[0]);
+#pragma unroll
+      for (int j = 0; j + 1 < PF; ++j)
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          kq[j][i] = kq[j + 1][i]; vq[j][i] = vq[j + 1][i]; okq[j][i] = okq[j + 1][i];
+        }
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        kq[PF - 1][i] = kn[i]; vq[PF - 1][i] = vn[i]; okq[PF - 1][i] = okn[i];
+      }
+      c += stride;
+    }
+  }
+
+  // bring the row groups to the wavefront's max, then sum them
+  {
+    const float Mw = wave_max(m);
+    const float f = __expf(m - Mw);
+    l *= f;
+#pragma unroll
+    for (int d = 0; d < EPL; ++d) acc[d] *= f;
+    m = Mw;
+  }
+  float L = wave_sum(l);
+  // sum the accumulators of the RPI row groups: afterwards lanes 0..LPR-1 hold the full dims
+#pragma unroll
+  for (int o = LPR; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int d = 0; d < EPL; ++d) acc[d] += __shfl_xor(acc[d], o, kWave);
+  }
+  if constexpr (SPLIT) {
+    // merge the 4 wavefronts of the workgroup through LDS
+    float* red = smem_f + kWavesPerBlock * (wl_pad + kWave);   // [4][D + 2]
+    if (rg == 0) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) red[w * (D + 2) + 2 + ds + e] = acc[e];
+    }
+    if (lane == 0) {
+      red[w * (D + 2)] = m;
+      red[w * (D + 2) + 1] = L;
+    }
+    __syncthreads();
+    if (w != 0) return;
+    float M = kNegBig;
+#pragma unroll
+    for (int s = 0; s < kWavesPerBlock; ++s)
+      if (red[s * (D + 2) + 1] > 0.0f) M = fmaxf(M, red[s * (D + 2)]);
+    float Lt = 0.0f;
+    float sc[kWavesPerBlock];
+#pragma unroll
+    for (int s = 0; s < kWavesPerBlock; ++s) {
+      const float Ls = red[s * (D + 2) + 1];
+      sc[s] = Ls > 0.0f ? __expf(red[s * (D + 2)] - M) : 0.0f;
+      Lt += Ls * sc[s];
+    }
+    if (p.gsplit > 1) {
+      float* part = p.ws + (qi * p.gsplit + g) * (D + 2);
+      for (int d = lane; d < D; d += kWave) {
+        float a = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kWavesPerBlock; ++s) a += red[s * (D + 2) + 2 + d] * sc[s];
+        __hip_atomic_store(part + 2 + d, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (lane == 0) {
+        __hip_atomic_store(part, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part + 1, Lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (g == 0 && p.keys) p.keys[qi] = (float)N;
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial has reached memory
+      int last = 0;
+      if (lane == 0)
+        last = __hip_atomic_fetch_add(p.cnt + qi, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(p.gsplit - 1);
+      if (!__shfl(last, 0, kWave)) return;
+      // last workgroup of this query: lane s holds partial s's (max, sum); gsplit <= 64
+      const float* base = p.ws + qi * p.gsplit * (D + 2);
+      float ms = kNegBig, Ls = 0.0f;
+      if (lane < p.gsplit) {
+        ms = __hip_atomic_load(base + lane * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        Ls = __hip_atomic_load(base + lane * (D + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      const float Mq = wave_max(Ls > 0.0f ? ms : kNegBig);
+      const float fac = Ls > 0.0f ? __expf(ms - Mq) : 0.0f;
+      const float Lq = wave_sum(Ls * fac);
+      const float inv = Lq > 0.0f ? 1.0f / Lq : 0.0f;
+      float* s_fac = reinterpret_cast<float*>(s_ext);   // the static-key list is no longer needed
+      s_fac[lane] = fac;
+      wave_sync();
+      T* orow = orow_base;
+      for (int d = lane; d < D; d += kWave) {
+        float a = 0.0f;
+        for (int s0 = 0; s0 < p.gsplit; s0 += 8) {
+          float pv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            pv[i] = s0 + i < p.gsplit ? __hip_atomic_load(base + (s0 + i) * (D + 2) + 2 + d, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                      : 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (s0 + i < p.gsplit) a += pv[i] * s_fac[s0 + i];
+        }
+        orow[d] = from_f32<T>(a * inv);
+      }
+      if (lane == 0) {
+        if (p.lse) p.lse[qi] = Lq > 0.0f ? Mq + __logf(Lq) : kNegBig;
+        __hip_atomic_store(p.cnt + qi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next call
+      }
+      return;
+    }
+    const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
+    T* orow = orow_base;
+    for (int d = lane; d < D; d += kWave) {
+      float a = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kWavesPerBlock; ++s) a += red[s * (D + 2) + 2 + d] * sc[s];
+      orow[d] = from_f32<T>(a * inv);
+    }
+    if (lane == 0) {
+      if (p.lse) p.lse[qi] = Lt > 0.0f ? M + __logf(Lt) : kNegBig;
+      if (p.keys) p.keys[qi] = (float)N;
+    }
+  } else {
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    if (rg == 0) {
+      T* orow = orow_base + ds;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) orow[e] = from_f32<T>(acc[e] * inv);
+    }
+    if (lane == 0) {
+      if (p.lse) p.lse[qi] = L > 0.0f ? m + __logf(L) : kNegBig;
+      if (p.keys) p.keys[qi] = (float)N;
+    }
+  }
+}
+
+
+}  // namespace ta

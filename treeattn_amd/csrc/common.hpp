@@ -81,6 +81,75 @@ __device__ __forceinline__ void load_row(const T* __restrict__ p, float (&out)[N
   }
 }
 
+// ----------------------------------------------------------------------------------------- address spaces
+// Pointers that reach a function through memory (a plan in device memory, a non-inlined call) are generic;
+// loads through them become flat instructions, which count against the LDS counter too and so make every
+// LDS access wait for them.  These helpers state that the address is device memory.
+#define TA_GLOBAL __attribute__((address_space(1)))
+typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+  const u32x4_t v = *(const TA_GLOBAL u32x4_t*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Device-coherent loads and stores ("dc": device scope, coherent across the XCDs' L2 caches), for data that
+// other workgroups of the running kernel write or read.
+__device__ __forceinline__ uint64_t ldg8_dc(const void* p) {
+  return __hip_atomic_load((TA_GLOBAL uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint4 ldg16_dc(const void* p) {
+  const uint64_t a = ldg8_dc(p), b = ldg8_dc((const char*)p + 8);
+  return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+}
+__device__ __forceinline__ uint32_t ldg4_dc(const void* p) {
+  return __hip_atomic_load((TA_GLOBAL uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint16_t ldg2_dc(const void* p) {
+  return __hip_atomic_load((TA_GLOBAL uint16_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ldgf_dc(const float* p) {
+  return __hip_atomic_load((TA_GLOBAL float*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stg8_dc(void* p, uint64_t v) {
+  __hip_atomic_store((TA_GLOBAL uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stg4_dc(void* p, uint32_t v) {
+  __hip_atomic_store((TA_GLOBAL uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stg2_dc(void* p, uint16_t v) {
+  __hip_atomic_store((TA_GLOBAL uint16_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stgf_dc(float* p, float v) {
+  __hip_atomic_store((TA_GLOBAL float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// load_row from device memory (see load_row)
+template <typename T, int N>
+__device__ __forceinline__ void load_row_g(const T* p, float (&out)[N]) {
+  constexpr int kBytes = N * (int)sizeof(T);
+  if constexpr (kBytes % 16 == 0) {
+    constexpr int kPer = 16 / (int)sizeof(T);
+#pragma unroll
+    for (int c = 0; c < N / kPer; ++c) {
+      const uint4 u = ldg16(p + c * kPer);
+      const T* e = reinterpret_cast<const T*>(&u);
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) out[c * kPer + i] = to_f32(e[i]);
+    }
+  } else {
+    load_row<T, N>(p, out);
+  }
+}
+
+// s_waitcnt vmcnt(N) with the LDS and export counters left alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_n() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // ----------------------------------------------------------------------------------------- wave helpers
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 __device__ __forceinline__ int wave_id() { return (int)(threadIdx.x / kWave); }

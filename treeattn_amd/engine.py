@@ -261,7 +261,7 @@ class Decoder:
     """Layer loop around seg_attend (engine.py:149-177), batched and graph-capturable."""
 
     def __init__(self, W, n_layer, n_head, n_embd, Tcap, mode, cfg=None, dev='cuda', batch=1, dtype=None,
-                 groups=None):
+                 groups=None, one_launch=None, attn_split=None):
         self.W, self.nl, self.H, self.C, self.Tcap = W, n_layer, n_head, n_embd, Tcap
         self.dh, self.mode, self.cfg, self.dev = n_embd // n_head, mode, cfg, torch.device(dev)
         self.B = batch
@@ -272,6 +272,17 @@ class Decoder:
         self.fused = (mode == 'seg' and self.dtype == torch.bfloat16 and n_embd % 64 == 0
                       and all(L['c_attn'].dtype == torch.bfloat16 for L in W['layers'])
                       and all(W['layers'][0][n].is_contiguous() for n in ('c_attn', 'c_proj', 'c_fc', 'c_mlp')))
+        # the whole step as one launch (ta_decode_step): bf16, head_dim 64, up to 32 sequences, the structural
+        # key set (no neighbour borrowing, fixed budget) and one sequence group
+        # attn_split: workgroups per query of the per-op decode attention (default: decode_nsplit's choice)
+        self.attn_split = attn_split
+        can = (self.fused and self.dh == 64 and batch <= 32 and not groups and not cfg.neighbors
+               and cfg.beam_mode != 'pred' and n_layer <= 64)
+        if one_launch and not can:
+            raise ValueError('one_launch: needs a bf16 model with head_dim 64, batch <= 32, neighbours off and a '
+                             'fixed budget')
+        # off unless asked for: on MI355X the per-op graph is faster at config 4 (1.40 vs 2.32 ms per step)
+        self.one_launch = bool(one_launch)
         self.reset()
 
     def reset(self):
@@ -280,7 +291,7 @@ class Decoder:
             self.states = [SegState(self.cfg, self.Tcap, H, dh, self.dev, B, self.dtype) for _ in range(self.nl)]
             sh = self.states[0].shape
             wl = sh.leaf_width(self.cfg.wmax)
-            self.scratch = _Scratch(B, H, dh, wl, self.dev, decode_nsplit(B, H, wl, sh.leaf), self.nl)
+            self.scratch = _Scratch(B, H, dh, wl, self.dev, self._nsplit(B, wl, sh.leaf), self.nl)
             # independent sequence groups, each with its own stream and captured graph (fused path only).
             # Default one group: on MI355X the dispatch cost of the extra, smaller launches outweighs the
             # overlap (measured: 4 groups of 8 sequences 3.08 ms/step vs 1.88 ms for one group of 32).
@@ -292,13 +303,27 @@ class Decoder:
                 n = b1 - b0
                 self.groups.append(dict(
                     b0=b0, b1=b1, states=[st.rows(b0, b1) for st in self.states],
-                    scratch=_Scratch(n, H, dh, wl, self.dev, decode_nsplit(n, H, wl, sh.leaf), self.nl),
+                    scratch=_Scratch(n, H, dh, wl, self.dev, self._nsplit(n, wl, sh.leaf), self.nl),
                     stream=torch.cuda.Stream(device=self.dev) if G > 1 else None,
                     x=torch.empty(n, self.C, device=self.dev, dtype=self.dtype),
                     pos32=torch.empty(n, device=self.dev, dtype=torch.int32)))
         else:
             self.states = [DenseState(self.Tcap, H, dh, self.dev, B, self.dtype) for _ in range(self.nl)]
         self.graph = None
+        self._step = None
+
+    def _nsplit(self, B, wl, leaf):
+        if self.attn_split:
+            return 4 * int(self.attn_split)
+        return decode_nsplit(B, self.H, wl, leaf)
+
+    def step_kernel(self):
+        """The one-launch step over this decoder's weights and caches (built on first use)."""
+        if self._step is None:
+            C, F = self.C, self.W['layers'][0]['c_fc'].shape[0]
+            self._step = K.DecodeStep(self.W, self.states, self.H, SEL.fixed_n_tree(self.cfg), self.cfg.local,
+                                      self.cfg.wmax, K.rowmm_splits(self.B, C, F))
+        return self._step
 
     # ------------------------------------------------------------------------------------------ one step
     def _forward_step(self, tok, tpos):
@@ -353,6 +378,10 @@ class Decoder:
         run on their own streams (parallel branches of a captured step) and join before returning."""
         V = self.W['wte'].shape[0]
         logits = torch.empty(self.B, V, device=self.dev, dtype=torch.bfloat16)
+        if self.one_launch:
+            sc = self.groups[0]['scratch']
+            self.step_kernel()(tok, tpos, logits, keys=sc.keys_all)
+            return logits
         if len(self.groups) == 1:
             self._group_step(self.groups[0], tok, tpos, logits)
             return logits
@@ -458,6 +487,10 @@ class Decoder:
             tok_g, t_g, lg_g = self.g_tok[b0:b1], self.g_t[b0:b1], self.g_logits[b0:b1]
 
             def body():
+                if self.one_launch:
+                    self.step_kernel()(tok_g, t_g, lg_g, tok_out=tok_g, advance=True,
+                                       keys=self.groups[0]['scratch'].keys_all)
+                    return
                 if grp is not None:
                     self._group_step(grp, tok_g, t_g, lg_g, advance=True)
                 elif self.fused:

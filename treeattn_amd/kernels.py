@@ -3,6 +3,7 @@
 All tensors must be on a gfx950 GPU.  Outputs are allocated here with torch (the library never
 allocates) unless the caller passes them in.  Work goes on torch's current stream.
 """
+import ctypes
 import math
 
 import torch
@@ -299,3 +300,98 @@ def kv_append(k_new, v_new, Kc, Vc, t_pos, levels, leaf, arity):
            v_new.stride(0), v_new.stride(1), L.ptr(Kc), L.ptr(Vc), Kc.stride(0), Kc.stride(1), Kc.stride(2), B, H, D,
            Tcap, L.ptr(t_pos), len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
            L.i64_array([t.stride(1) for t in levels]), _ilog2(leaf), _ilog2(arity), L.stream())
+
+
+# ----------------------------------------------------------------------------------------------- decode step
+class DecodeStep:
+    """The whole decode step in one launch (ta_decode_step): embedding, every layer (LN1 + c_attn, cache
+    append + beam descent + attention per (sequence, head), c_proj + residual, LN2 + c_fc + GELU, c_mlp +
+    residual), LN_f + logits and the greedy token.
+
+    W: engine weight dict (bf16); states: one SegState per layer (bf16 caches, tree levels); n_tree: leaf
+    budget; mlp_splits: split of c_mlp along K (the same as rowmm_splits gives the per-op path, so both paths
+    agree bit for bit).  The workspace holds the step's plan, activations and counters; the weights and caches
+    must stay where they are."""
+
+    def __init__(self, W, states, n_head, n_tree, local, wmax, mlp_splits, eps=1e-5):
+        Ls = W['layers']
+        st0 = states[0]
+        B, H, Tcap, dh = st0.K.shape
+        C = W['wte'].shape[1]
+        F = Ls[0]['c_fc'].shape[0]
+        tensors = [W['wte'], W['wpe'], W['ln_f']] + [L_[n] for L_ in Ls for n in
+                                                     ('ln1', 'c_attn', 'c_proj', 'ln2', 'c_fc', 'c_mlp')]
+        L.require_gpu(*tensors)
+        if any(t.dtype != torch.bfloat16 for t in tensors) or any(s.K.dtype != torch.bfloat16 for s in states):
+            raise TypeError('DecodeStep: bf16 weights and caches')
+        if any(not t.is_contiguous() for t in tensors[3:]) or W['wte'].stride(1) != 1 or W['wpe'].stride(1) != 1:
+            raise ValueError('DecodeStep: weight matrices must be contiguous')
+        layers = (L.StepLayer * len(Ls))()
+        self._keep = tensors + [s.K for s in states] + [s.V for s in states] + [t for s in states for t in s.levels]
+        for i, (Lw, s) in enumerate(zip(Ls, states)):
+            d = layers[i]
+            for n in ('ln1', 'c_attn', 'c_proj', 'ln2', 'c_fc', 'c_mlp'):
+                setattr(d, n, Lw[n].data_ptr())
+            if s.K.stride() != s.V.stride() or s.K.stride(-1) != 1:
+                raise ValueError('DecodeStep: K and V caches must share a row-contiguous layout')
+            d.k_cache, d.v_cache = s.K.data_ptr(), s.V.data_ptr()
+            d.c_sb, d.c_sh, d.c_st = s.K.stride(0), s.K.stride(1), s.K.stride(2)
+            for j, t in enumerate(s.levels):
+                d.levels[j] = t.data_ptr()
+                d.lv_sb[j], d.lv_sh[j] = t.stride(0), t.stride(1)
+        m = L.StepModel()
+        m.n_layer, m.n_head, m.head_dim, m.n_embd, m.n_ff = len(Ls), n_head, dh, C, F
+        m.vocab, m.n_pos, m.batch, m.tcap = W['wte'].shape[0], W['wpe'].shape[0], B, Tcap
+        m.leaf, m.arity, m.n_levels = st0.shape.leaf, st0.shape.arity, st0.shape.n_levels
+        m.wmax, m.n_tree, m.local, m.mlp_splits, m.ln_eps = int(wmax), int(n_tree), int(local), int(mlp_splits), eps
+        m.wte, m.ld_wte = W['wte'].data_ptr(), W['wte'].stride(0)
+        m.wpe, m.ld_wpe = W['wpe'].data_ptr(), W['wpe'].stride(0)
+        m.ln_f = W['ln_f'].data_ptr()
+        m.layers = layers
+        self._layers, self._model = layers, m
+        nbytes = L.lib().ta_decode_step_workspace_size(ctypes.byref(m))
+        if nbytes <= 0:
+            raise RuntimeError('DecodeStep: shape not supported by the one-launch step')
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=W['wte'].device)
+        self.launch = L.StepLaunch()
+        L.call('ta_decode_step_prepare', ctypes.byref(m), L.ptr(self.ws), nbytes, ctypes.byref(self.launch),
+               L.stream())
+        self.B, self.V = B, W['wte'].shape[0]
+
+    def __call__(self, tok, tpos, logits, tok_out=None, advance=False, keys=None, trace=None):
+        """tok, tpos: int64 (B,); logits: bf16 (B, V) (row-contiguous); tok_out: int64 (B,) for the greedy tokens
+        (may be tok); advance: increment tpos; keys: float32 (n_layer, B, n_head) contiguous, or None; trace: int64
+        (n_tasks, 16) for the per-task timeline (wall-clock ticks: taken, wait end, ten points inside (0 where
+        unused), end; CU id), or None."""
+        if trace is not None and (trace.dtype != torch.long or not trace.is_contiguous()
+                                  or trace.numel() < 16 * self.launch.n_tasks):
+            raise ValueError('DecodeStep: trace must be contiguous int64 (n_tasks, 16)')
+        for t in (tok, tpos) + ((tok_out,) if tok_out is not None else ()):
+            if t.dtype != torch.long or not t.is_contiguous() or t.numel() != self.B:
+                raise ValueError('DecodeStep: tokens and positions must be contiguous int64 (B,)')
+        if logits.dtype != torch.bfloat16 or logits.stride(1) != 1 or tuple(logits.shape) != (self.B, self.V):
+            raise ValueError('DecodeStep: logits must be bf16 (B, V) with contiguous rows')
+        if keys is not None and (keys.dtype != torch.float32 or not keys.is_contiguous()):
+            raise ValueError('DecodeStep: keys must be contiguous float32')
+        L.call('ta_decode_step', ctypes.byref(self.launch), L.ptr(self.ws), L.ptr(tok), L.ptr(tok_out), L.ptr(tpos),
+               int(bool(advance)), L.ptr(logits), logits.stride(0), L.ptr(keys), L.ptr(trace), L.stream())
+        return logits
+
+    def task_kinds(self):
+        """Kind and layer of every task, in ticket order: [('embed', -1), ('qkv', 0), ..., ('final', -1)]."""
+        m = self._model
+        per = [('qkv', (3 * m.n_embd + 31) // 32), ('seq_head', m.batch * m.n_head), ('c_proj', (m.n_embd + 31) // 32),
+               ('c_fc', (m.n_ff + 31) // 32), ('c_mlp', (m.n_embd + 31) // 32 * m.mlp_splits)]
+        kinds = [('embed', -1)] * m.batch
+        for l in range(m.n_layer):
+            for name, n in per:
+                kinds += [(name, l)] * n
+        kinds += [('lm_head', -1)] * ((m.vocab + 31) // 32) + [('final', -1)]
+        assert len(kinds) == self.launch.n_tasks
+        return kinds
+
+    def error(self):
+        """1 when a wait of an earlier step ran out of time (its results are wrong), else 0.  Synchronises."""
+        e = ctypes.c_int(0)
+        L.call('ta_decode_step_error', L.ptr(self.ws), ctypes.byref(e), L.stream())
+        return e.value
