@@ -191,14 +191,22 @@ int ta_kv_append(const void* k_new, const void* v_new, int dtype,
  * the unfused chain.  Row strides ldx, ldw, ldy, ldr in elements; K a multiple of 64; X, W, ln_w 16-byte
  * aligned.  Y may be the same buffer as R.
  * splits > 1 divides K among that many workgroups per 32 x 32 output tile (clamped to K/64); their float32
- * partials go to the workspace `ws` (ta_rowmm_workspace_size bytes, 256-byte aligned, zero-filled once when
- * allocated: its head holds per-tile counters that every call leaves at zero) and are summed in split order,
- * so results are deterministic.  Calls that share a workspace must not overlap in time.
+ * partials are summed in split order, so results are deterministic.
+ * Tails, done once by the last output tile to finish (at most one per call):
+ *   ln_next != NULL: y_ln[M, N] = LN(Y) with weight ln_next (eps ln_eps) -- the LayerNorm the next product
+ *     of the residual stream applies (model.py:42-44, LN1 / LN2 / LN_f), bit for bit the prologue's
+ *     arithmetic; N a multiple of 64, Y, y_ln and ln_next 16-byte aligned (row stride ld_yln);
+ *   tok_out != NULL: tok_out[m] = the first column of the largest bf16 value of row m of Y (the greedy
+ *     token of the reference's loop, phase2.py:51-66; NaN never chosen, 0 for a row of NaN); no epilogue.
+ * ws: ta_rowmm_workspace_size bytes, 256-byte aligned, zero-filled once when allocated (its counters and
+ * keys return to zero after every call), needed when splits > 1 or a tail is asked for.  Calls that share a
+ * workspace must not overlap in time.
  */
 int64_t ta_rowmm_workspace_size(int M, int N, int K, int splits);
 int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy,
              const void* R, int64_t ldr, const void* ln_w, float ln_eps, int M, int N, int K,
-             int epilogue, int splits, void* ws, int64_t ws_bytes, void* stream);
+             int epilogue, int splits, const void* ln_next, void* y_ln, int64_t ld_yln, int64_t* tok_out,
+             void* ws, int64_t ws_bytes, void* stream);
 
 /*
  * Row-wise argmax for greedy decoding (replaces logits.argmax(-1) of the reference's greedy loop,
@@ -212,10 +220,19 @@ int ta_argmax_rows(const void* x, int dtype, int64_t rows, int64_t n, int64_t st
  * First op of a decode step (engine.py:168, x = wte[tok] + wpe[t]): x[b, :] = wte[tok[b], :] + wpe[t[b], :]
  * in dtype (the sum rounded once), pos32[b] = t[b]; with `advance`, t[b] += 1 afterwards (the next step's
  * position, so a captured step can be replayed).  tok, t: int64 (B,); tables with row strides ldw, ldp.
+ * ln_w != NULL (bf16, C a multiple of 64, at most 4096): also x_ln[b, :] = LN(x[b, :]) with weight ln_w and
+ * eps ln_eps, the first layer's LN1 (model.py:43), bit for bit as ta_rowmm computes it.
  */
 int ta_embed(const int64_t* tok, int64_t* tpos, int advance, const void* wte, int64_t ldw, const void* wpe,
              int64_t ldp, int dtype, int B, int C, int64_t V, int64_t P, void* x, int64_t ldx, int32_t* pos32,
-             void* stream);
+             const void* ln_w, float ln_eps, void* x_ln, int64_t ld_xln, void* stream);
+
+/*
+ * float32 -> bf16 with the rounding every kernel of the library uses (round to nearest even; NaN stays NaN):
+ * out[i] = bf16(in[i]), bit patterns.  in 16-byte and out 8-byte aligned.  (Lets a test hold the kernels'
+ * rounding against the reference framework's.)
+ */
+int ta_bf16_from_f32(const float* in, uint16_t* out, int64_t n, void* stream);
 
 /*
  * The whole decode step in one launch (replaces Decoder.step, engine.py:161-177, with seg_attend in the

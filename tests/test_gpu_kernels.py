@@ -391,6 +391,77 @@ def test_rowmm_split_k(M, N, KD, ln, epi):
         assert torch.equal(K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, splits=S, ws=ws), eager)
 
 
+@pytest.mark.parametrize('M,N,KD,S', [(32, 768, 768, 1), (32, 768, 3072, 4), (7, 128, 256, 2)])
+def test_rowmm_layernorm_tail_equals_prologue(M, N, KD, S):
+    """The LayerNorm tail (computed once by the last tile) gives, bit for bit, the rows the next product's
+    own LayerNorm prologue would compute: product(LN-tail output) == product with the LN prologue; and the
+    tail output is LN of the result within the bf16 bar.  Repeated calls reuse the workspace (its counter
+    returns to zero)."""
+    import torch.nn.functional as F
+    print('case', M, N, KD, S, flush=True)
+    g = torch.Generator().manual_seed(M * N + KD)
+    x = torch.randn(M, KD, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, KD, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    g2 = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.bfloat16).to(DEV)
+    w2 = (torch.randn(96, N, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    ws = K.rowmm_workspace(M, N, KD, S, DEV)
+    for _ in range(3):
+        y, yn = K.rowmm(x, w, epilogue='residual', residual=res, splits=S, ws=ws, ln_next=g2)
+        assert torch.equal(y, K.rowmm(x, w, epilogue='residual', residual=res, splits=S, ws=ws))
+        assert torch.equal(K.rowmm(yn, w2), K.rowmm(y, w2, ln_w=g2))
+        want = F.layer_norm(y.float(), (N,), g2.float(), None, 1e-5)
+        assert (yn.float() - want).abs().max().item() < 2e-2 * max(1.0, want.abs().max().item())
+
+
+@pytest.mark.parametrize('M,N', [(32, 50304), (5, 1000), (3, 96)])
+def test_rowmm_argmax_tail_equals_argmax_rows(M, N):
+    """The greedy-token tail equals ta_argmax_rows of the same logits (first index of the largest bf16 value),
+    call after call and as graph replays; ties are made common by coarse weights."""
+    print('case', M, N, flush=True)
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, 768, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, 768, generator=g) * 4).round().mul(0.01).to(torch.bfloat16).to(DEV)
+    lw = (1 + 0.1 * torch.randn(768, generator=g)).to(torch.bfloat16).to(DEV)
+    ws = K.rowmm_workspace(M, N, 768, 1, DEV)
+    tok = torch.full((M,), -1, dtype=torch.long, device=DEV)
+    for _ in range(3):
+        lg = K.rowmm(x, w, ln_w=lw, ws=ws, tok_out=tok)
+        assert torch.equal(tok, K.argmax_rows(lg))
+    lg = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        K.rowmm(x, w, ln_w=lw, ws=ws, tok_out=tok, out=lg)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr, stream=s):
+            K.rowmm(x, w, ln_w=lw, ws=ws, tok_out=tok, out=lg)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        tok.fill_(-1)
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(tok, K.argmax_rows(lg))
+
+
+def test_embed_layernorm_equals_prologue():
+    """The embedding's LayerNorm output is, bit for bit, what the next product's LN prologue computes."""
+    g = torch.Generator().manual_seed(77)
+    wte = (torch.randn(500, 768, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wpe = (torch.randn(300, 768, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    lw = (1 + 0.1 * torch.randn(768, generator=g)).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(256, 768, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    tok = torch.randint(0, 500, (9,), generator=g).to(DEV)
+    tpos = torch.randint(0, 300, (9,), generator=g).to(DEV)
+    x = torch.empty(9, 768, dtype=torch.bfloat16, device=DEV)
+    xn = torch.empty_like(x)
+    pos32 = torch.empty(9, dtype=torch.int32, device=DEV)
+    K.embed(tok, tpos, wte, wpe, out=x, pos32=pos32, ln_w=lw, out_ln=xn)
+    assert torch.equal(x, (wte[tok].float() + wpe[tpos].float()).to(torch.bfloat16))
+    assert torch.equal(K.rowmm(xn, w), K.rowmm(x, w, ln_w=lw))
+
+
 def test_rowmm_split_needs_workspace():
     x = torch.zeros(32, 768, dtype=torch.bfloat16, device=DEV)
     w = torch.zeros(768, 768, dtype=torch.bfloat16, device=DEV)
@@ -455,3 +526,20 @@ def test_embed_matches_table_sum(dtype):
     assert pos32.tolist() == t.tolist()
     K.embed(tok, t, wte, wpe, out=x, pos32=pos32, advance=True)
     assert pos32.tolist() == [0, 63, 7, 31, 40] and t.tolist() == [1, 64, 8, 32, 41]
+
+
+def test_bf16_rounding_matches_torch_all_floats():
+    """The kernels' float32 -> bf16 rounding (gfx950's conversion instruction) equals torch's round-to-nearest-
+    even for every one of the 2^32 float bit patterns (NaN only has to stay NaN)."""
+    n = 1 << 28
+    for c in range(16):
+        bits = torch.arange(c * n, (c + 1) * n, dtype=torch.int64, device=DEV).to(torch.int32)
+        f = bits.view(torch.float32)
+        got = K.bf16_round(f)
+        want = f.to(torch.bfloat16).view(torch.int16)
+        nan = torch.isnan(f)
+        same = (got == want) | nan
+        assert bool(same.all()), 'chunk %d: %d differ' % (c, int((~same).sum()))
+        gf = got.view(torch.bfloat16)
+        assert bool(torch.isnan(gf[nan]).all()), 'chunk %d: NaN lost' % c
+        del bits, f, got, want, nan, same, gf

@@ -29,17 +29,19 @@ __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
 __device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float(((uint32_t)x.bits) << 16); }
 
-// float -> bf16, round to nearest even (NaN kept quiet)
+// float -> bf16, round to nearest even (gfx950's v_cvt_pk_bf16_f32; NaN stays NaN)
 __device__ __forceinline__ bf16_t bf16_from(float f) {
-  uint32_t u = __float_as_uint(f);
   bf16_t r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    r.bits = (uint16_t)((u >> 16) | 0x40u);
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);
-    r.bits = (uint16_t)(u >> 16);
-  }
+  r.bits = __builtin_bit_cast(uint16_t, (__bf16)f);
   return r;
+}
+
+// two floats -> two bf16 (a in the low half), one conversion instruction
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16_pack2(float a, float b) {
+  const bf16x2_t v = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <typename T> __device__ __forceinline__ T from_f32(float x);

@@ -94,9 +94,7 @@ __device__ __forceinline__ uint4 mm_ld16(const void* p) {
 
 __device__ __forceinline__ float mm_bf16_round(float x) { return to_f32(bf16_from(x)); }
 
-__device__ __forceinline__ uint32_t mm_pack2(float a, float b) {
-  return (uint32_t)bf16_from(a).bits | ((uint32_t)bf16_from(b).bits << 16);
-}
+__device__ __forceinline__ uint32_t mm_pack2(float a, float b) { return bf16_pack2(a, b); }
 
 // Blocks [blk0, blk0 + nblk) of split s.
 __host__ __device__ __forceinline__ void mm_split_range(int K, int splits, int s, int& blk0, int& nblk) {
@@ -158,6 +156,52 @@ __device__ __forceinline__ void mm_add8(uint4 u, float& s, float& s2) {
     s2 = fmaf(f0, f0, s2);
     s += f1;
     s2 = fmaf(f1, f1, s2);
+  }
+}
+
+// Yn[r] = LN(Y[r]) (weight gam, no bias) for rows r < M of N columns, the arithmetic of mm_tile's prologue:
+// 8 threads per row, thread `part` sums piece `part` (8 elements) of every 64-column block in block order,
+// then the xor tree over the 8 threads; each element (y - mean) * rstd * g rounded to bf16.  256 threads.
+// FRESH: Y was written by other workgroups of the running kernel.
+template <bool FRESH>
+__device__ __forceinline__ void mm_rows_ln(const bf16_t* Y, int64_t ldy, int M, int N, const bf16_t* gam, float eps,
+                                           bf16_t* Yn, int64_t ldyn) {
+  const int tid = threadIdx.x;
+  for (int r0 = 0; r0 < M; r0 += kMmThreads / 8) {
+    const int r = r0 + (tid >> 3), part = tid & 7;
+    const bool ok = r < M;
+    const bf16_t* yr = Y + (int64_t)(ok ? r : 0) * ldy + 8 * part;
+    float s = 0.0f, s2 = 0.0f;
+    for (int k0 = 0; k0 < N; k0 += 64 * 8) {
+      uint4 u[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) u[i] = k0 + 64 * i < N ? mm_ld16<FRESH>(yr + k0 + 64 * i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (k0 + 64 * i < N) mm_add8(u[i], s, s2);
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+      s += __shfl_xor(s, o, kWave);
+      s2 += __shfl_xor(s2, o, kWave);
+    }
+    const float mean = s / (float)N;
+    const float rstd = rsqrtf(fmaxf(s2 / (float)N - mean * mean, 0.0f) + eps);
+    if (!ok) continue;
+    bf16_t* yn = Yn + (int64_t)r * ldyn + 8 * part;
+    for (int k = 0; k < N; k += 64) {
+      const uint4 xu = mm_ld16<FRESH>(yr + k);
+      const uint4 gu = ldg16(gam + k + 8 * part);
+      const uint32_t xw[4] = {xu.x, xu.y, xu.z, xu.w}, gw[4] = {gu.x, gu.y, gu.z, gu.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float f0 = __uint_as_float(xw[e] << 16), f1 = __uint_as_float(xw[e] & 0xffff0000u);
+        const float g0 = __uint_as_float(gw[e] << 16), g1 = __uint_as_float(gw[e] & 0xffff0000u);
+        o[e] = mm_pack2((f0 - mean) * rstd * g0, (f1 - mean) * rstd * g1);
+      }
+      *(TA_GLOBAL u32x4_t*)(yn + k) = u32x4_t{o[0], o[1], o[2], o[3]};
+    }
   }
 }
 
@@ -270,6 +314,7 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
       // statistics from the staged rows: thread (r, part) sums piece `part` of every block of row r
       const int r = tid >> 3, part = tid & 7;
       float s = 0.0f, s2 = 0.0f;
+#pragma unroll 4
       for (int blk = 0; blk < rn; ++blk) {
         const uint4 u = *reinterpret_cast<const uint4*>(xs + (size_t)(blk * 32 + r) * 64 + 8 * (part ^ (r & 7)));
         mm_add8(u, s, s2);
@@ -288,13 +333,16 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
     }
     if (round == 0) TA_MARK(1);
     if constexpr (LN) {
-      // the LayerNorm of the staged rows, in place: thread tid takes pieces tid, tid + 256, ...
-      for (int q = tid; q < rn * 256; q += kMmThreads) {
-        const int blk = q >> 8, row = (q >> 3) & 31, pos = q & 7;
+      // the LayerNorm of the staged rows, in place: thread tid takes position tid % 8 of row tid / 8 in every
+      // block of the round
+      const int row = tid >> 3, pos = tid & 7;
+      const float mean = s_mean[row], rstd = s_rstd[row];
+      const bf16_t* gp = gs + 8 * (pos ^ (row & 7));
+#pragma unroll 4
+      for (int blk = 0; blk < rn; ++blk) {
         uint4* xp = reinterpret_cast<uint4*>(xs + (size_t)(blk * 32 + row) * 64 + 8 * pos);
         const uint4 xu = *xp;
-        const uint4 gu = *reinterpret_cast<const uint4*>(gs + blk * 64 + 8 * (pos ^ (row & 7)));
-        const float mean = s_mean[row], rstd = s_rstd[row];
+        const uint4 gu = *reinterpret_cast<const uint4*>(gp + blk * 64);
         const uint32_t gw[4] = {gu.x, gu.y, gu.z, gu.w};
         const uint32_t xw[4] = {xu.x, xu.y, xu.z, xu.w};
         uint32_t o[4];

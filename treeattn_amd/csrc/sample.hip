@@ -1,7 +1,10 @@
 // Greedy token choice for the decode loop: row-wise argmax (first index among equal maxima), one
 // workgroup per row.  Replaces logits.argmax(-1) of the reference's greedy loop (phase2.py:51-66) so a
 // captured decode step holds no library reduction.
+#include <type_traits>
+
 #include "common.hpp"
+#include "rowmm_tile.hpp"
 
 namespace ta {
 
@@ -82,12 +85,17 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const T* __
 
 // The decode step's first op: x[b] = wte[tok[b]] + wpe[t[b]] rounded to the element type (as the
 // reference's bf16 sum does), the positions as int32 for the later kernels, and optionally t[b] += 1 for
-// the next step.  One workgroup per sequence; token and position clamped to the tables.
+// the next step.  One workgroup per sequence; token and position clamped to the tables.  With ln_w (bf16,
+// C a multiple of 64 and at most kEmbedLnMax): x_ln[b] = LN(x[b]) for the first layer's product, the
+// arithmetic of the row products' LayerNorm (mm_rows_ln).
+constexpr int kEmbedLnMax = 4096;
+
 template <typename T>
 __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ tok, int64_t* tpos, int advance,
                                                     const T* __restrict__ wte, int64_t ldw, const T* __restrict__ wpe,
                                                     int64_t ldp, int C, int64_t V, int64_t P, T* __restrict__ x,
-                                                    int64_t ldx, int32_t* __restrict__ pos32) {
+                                                    int64_t ldx, int32_t* __restrict__ pos32, const T* ln_w,
+                                                    float eps, T* x_ln, int64_t ldxl) {
   const int b = blockIdx.x;
   int64_t tk = tok[b], t = tpos[b];
   tk = tk < 0 ? 0 : (tk >= V ? V - 1 : tk);
@@ -96,6 +104,44 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
   const T* pr = wpe + tc * ldp;
   T* xr = x + (int64_t)b * ldx;
   for (int c = threadIdx.x; c < C; c += blockDim.x) xr[c] = from_f32<T>(to_f32(er[c]) + to_f32(pr[c]));
+  if constexpr (sizeof(T) == 2 && !std::is_same<T, f16_t>::value) {
+    if (ln_w) {
+      // the row as stored, then its LayerNorm: threads 0-7 take pieces 0-7 of every 64-column block
+      __shared__ __align__(16) bf16_t srow[kEmbedLnMax];
+      __shared__ float s_stat[2];
+      for (int c = threadIdx.x; c < C; c += blockDim.x) srow[c] = xr[c];
+      __syncthreads();
+      if (threadIdx.x < 8) {
+        float s = 0.0f, s2 = 0.0f;
+        for (int k = 0; k < C; k += 64) mm_add8(*reinterpret_cast<const uint4*>(srow + k + 8 * threadIdx.x), s, s2);
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+          s += __shfl_xor(s, o, kWave);
+          s2 += __shfl_xor(s2, o, kWave);
+        }
+        if (threadIdx.x == 0) {
+          const float mean = s / (float)C;
+          s_stat[0] = mean;
+          s_stat[1] = rsqrtf(fmaxf(s2 / (float)C - mean * mean, 0.0f) + eps);
+        }
+      }
+      __syncthreads();
+      const float mean = s_stat[0], rstd = s_stat[1];
+      for (int k = 8 * threadIdx.x; k < C; k += 8 * blockDim.x) {
+        const uint4 xu = *reinterpret_cast<const uint4*>(srow + k);
+        const uint4 gu = *reinterpret_cast<const uint4*>(ln_w + k);
+        const uint32_t xw[4] = {xu.x, xu.y, xu.z, xu.w}, gw[4] = {gu.x, gu.y, gu.z, gu.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float f0 = __uint_as_float(xw[e] << 16), f1 = __uint_as_float(xw[e] & 0xffff0000u);
+          const float g0 = __uint_as_float(gw[e] << 16), g1 = __uint_as_float(gw[e] & 0xffff0000u);
+          o[e] = mm_pack2((f0 - mean) * rstd * g0, (f1 - mean) * rstd * g1);
+        }
+        *reinterpret_cast<uint4*>(x_ln + (int64_t)b * ldxl + k) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
   __syncthreads();   // every thread has read tpos[b] before it may change
   if (threadIdx.x == 0) {
     pos32[b] = (int32_t)t;
@@ -103,30 +149,61 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
   }
 }
 
+// out[i] = bf16(in[i]) with the library's rounding (bf16_from), 4 per thread.
+__global__ __launch_bounds__(256) void bf16_round_kernel(const float* __restrict__ in, uint16_t* __restrict__ out,
+                                                         int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i + 4 <= n) {
+    const float4 v = *reinterpret_cast<const float4*>(in + i);
+    *reinterpret_cast<uint2*>(out + i) = make_uint2(bf16_pack2(v.x, v.y), bf16_pack2(v.z, v.w));
+  } else {
+    for (int64_t j = i; j < n; ++j) out[j] = bf16_from(in[j]).bits;
+  }
+}
+
 }  // namespace ta
 
 using namespace ta;
 
+extern "C" int ta_bf16_from_f32(const float* in, uint16_t* out, int64_t n, void* stream) {
+  if (n < 0 || (n > 0 && (in == nullptr || out == nullptr || (uintptr_t)in % 16 || (uintptr_t)out % 8))) {
+    set_error("ta_bf16_from_f32: bad arguments (in 16-byte and out 8-byte aligned)");
+    return TA_ERR_ARG;
+  }
+  if (n == 0) return TA_OK;
+  const int64_t blocks = (n + 1023) / 1024;
+  hipLaunchKernelGGL(bf16_round_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, in, out, n);
+  return check_launch("bf16_round_kernel");
+}
+
 extern "C" int ta_embed(const int64_t* tok, int64_t* tpos, int advance, const void* wte, int64_t ldw, const void* wpe,
                         int64_t ldp, int dtype, int B, int C, int64_t V, int64_t P, void* x, int64_t ldx,
-                        int32_t* pos32, void* stream) {
+                        int32_t* pos32, const void* ln_w, float ln_eps, void* x_ln, int64_t ld_xln, void* stream) {
   if (B <= 0 || C <= 0 || V <= 0 || P <= 0 || ldw < C || ldp < C || ldx < C) {
     set_error("ta_embed: bad sizes");
+    return TA_ERR_ARG;
+  }
+  if (ln_w && (dtype != TA_BF16 || C % 64 || C > kEmbedLnMax || x_ln == nullptr || ld_xln < C ||
+               (uintptr_t)ln_w % 16 || (uintptr_t)x_ln % 16 || (ld_xln * 2) % 16)) {
+    set_error("ta_embed: the LayerNorm output needs bf16, C a multiple of 64 up to 4096 and 16-byte alignment");
     return TA_ERR_ARG;
   }
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
     case TA_F32:
       hipLaunchKernelGGL((embed_kernel<float>), dim3(B), dim3(256), 0, st, tok, tpos, advance, (const float*)wte, ldw,
-                         (const float*)wpe, ldp, C, V, P, (float*)x, ldx, pos32);
+                         (const float*)wpe, ldp, C, V, P, (float*)x, ldx, pos32, (const float*)nullptr, ln_eps,
+                         (float*)nullptr, ld_xln);
       break;
     case TA_F16:
       hipLaunchKernelGGL((embed_kernel<f16_t>), dim3(B), dim3(256), 0, st, tok, tpos, advance, (const f16_t*)wte, ldw,
-                         (const f16_t*)wpe, ldp, C, V, P, (f16_t*)x, ldx, pos32);
+                         (const f16_t*)wpe, ldp, C, V, P, (f16_t*)x, ldx, pos32, (const f16_t*)nullptr, ln_eps,
+                         (f16_t*)nullptr, ld_xln);
       break;
     case TA_BF16:
       hipLaunchKernelGGL((embed_kernel<bf16_t>), dim3(B), dim3(256), 0, st, tok, tpos, advance, (const bf16_t*)wte,
-                         ldw, (const bf16_t*)wpe, ldp, C, V, P, (bf16_t*)x, ldx, pos32);
+                         ldw, (const bf16_t*)wpe, ldp, C, V, P, (bf16_t*)x, ldx, pos32, (const bf16_t*)ln_w, ln_eps,
+                         (bf16_t*)x_ln, ld_xln);
       break;
     default:
       set_error("unknown dtype");

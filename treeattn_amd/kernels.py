@@ -232,17 +232,18 @@ def rowmm_splits(M, N, K):
 
 
 def rowmm_workspace(M, N, K, splits, device):
-    """Zero-filled workspace for ta_rowmm with `splits` (None when the product needs none)."""
+    """Zero-filled workspace for ta_rowmm (split partials, tail counter, argmax keys)."""
     n = L.lib().ta_rowmm_workspace_size(M, N, K, splits)
-    if n <= 0:
-        return None
-    return torch.zeros(n, dtype=torch.uint8, device=device)
+    return torch.zeros(max(n, 256), dtype=torch.uint8, device=device)
 
 
-def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None, splits=1, ws=None):
+def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None, splits=1, ws=None, ln_next=None,
+          out_ln=None, tok_out=None):
     """epilogue(LN(x) @ w.T) for a few rows, bf16: x (M,K), w (N,K) -> (M,N).  epilogue None | 'gelu' |
-    'residual' (adds `residual`, (M,N)); `out` may be `residual`.  splits > 1 divides K among workgroups and
-    needs `ws` from rowmm_workspace (one workspace serves calls that run one after another)."""
+    'residual' (adds `residual`, (M,N)); `out` may be `residual`.  splits > 1 divides K among workgroups.
+    ln_next: also out_ln = LN(result) with that weight (for the next product); tok_out: also the greedy token of
+    every row (int64 (M,)).  splits > 1 and the tails need `ws` from rowmm_workspace (one workspace serves calls
+    that run one after another)."""
     L.require_gpu(x, w)
     M, K = x.shape
     N = w.shape[0]
@@ -250,10 +251,26 @@ def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None, spl
         raise ValueError('rowmm: rows must be contiguous')
     if out is None:
         out = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    if ln_next is not None and out_ln is None:
+        out_ln = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    if tok_out is not None and (tok_out.dtype != torch.long or not tok_out.is_contiguous() or tok_out.numel() != M):
+        raise ValueError('rowmm: tok_out must be contiguous int64 (M,)')
     r = residual if epilogue == 'residual' else None
     L.call('ta_rowmm', L.ptr(x), x.stride(0), L.ptr(w), w.stride(0), L.ptr(out), out.stride(0), L.ptr(r),
            r.stride(0) if r is not None else 0, L.ptr(ln_w), float(eps), M, N, K, _EPI[epilogue], int(splits),
-           L.ptr(ws), ws.numel() if ws is not None else 0, L.stream())
+           L.ptr(ln_next), L.ptr(out_ln if ln_next is not None else None),
+           out_ln.stride(0) if ln_next is not None else 0, L.ptr(tok_out), L.ptr(ws),
+           ws.numel() if ws is not None else 0, L.stream())
+    return (out, out_ln) if ln_next is not None else out
+
+
+def bf16_round(x):
+    """bf16 bit patterns (int16) of float32 x with the kernels' rounding (ta_bf16_from_f32)."""
+    L.require_gpu(x)
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError('bf16_round: contiguous float32 input')
+    out = torch.empty(x.shape, dtype=torch.int16, device=x.device)
+    L.call('ta_bf16_from_f32', L.ptr(x), L.ptr(out), x.numel(), L.stream())
     return out
 
 
@@ -270,9 +287,9 @@ def argmax_rows(x, out=None):
     return out
 
 
-def embed(tok, tpos, wte, wpe, out, pos32, advance=False):
+def embed(tok, tpos, wte, wpe, out, pos32, advance=False, ln_w=None, out_ln=None, eps=1e-5):
     """out[b] = wte[tok[b]] + wpe[tpos[b]] (B, C) in the tables' dtype; pos32[b] = tpos[b]; with `advance`
-    tpos is incremented in place afterwards.  tok, tpos: int64 (B,)."""
+    tpos is incremented in place afterwards; with ln_w, also out_ln = LN(out) (bf16).  tok, tpos: int64 (B,)."""
     L.require_gpu(tok, tpos, wte, wpe, out, pos32)
     if tok.dtype != torch.long or tpos.dtype != torch.long or pos32.dtype != torch.int32:
         raise TypeError('embed: tok and tpos int64, pos32 int32')
@@ -281,9 +298,11 @@ def embed(tok, tpos, wte, wpe, out, pos32, advance=False):
     if not (tok.is_contiguous() and tpos.is_contiguous() and pos32.is_contiguous()):
         raise ValueError('embed: token and position vectors must be contiguous')
     B, C = out.shape
+    if ln_w is not None and (out_ln is None or out_ln.stride(1) != 1):
+        raise ValueError('embed: the LayerNorm output needs a row-contiguous out_ln')
     L.call('ta_embed', L.ptr(tok), L.ptr(tpos), int(bool(advance)), L.ptr(wte), wte.stride(0), L.ptr(wpe),
            wpe.stride(0), L.dtype_code(wte), B, C, wte.shape[0], wpe.shape[0], L.ptr(out), out.stride(0), L.ptr(pos32),
-           L.stream())
+           L.ptr(ln_w), float(eps), L.ptr(out_ln), out_ln.stride(0) if out_ln is not None else 0, L.stream())
     return out
 
 
