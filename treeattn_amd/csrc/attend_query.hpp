@@ -216,30 +216,23 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
   };
 
   {
-    constexpr int PF = 4;   // measured with cold caches at config 4: 46.9 us (8 loads x 1 ahead: 49.9 us)
+    // A ring of PF chunk slots, unrolled so that every slot is a fixed set of registers: slot j is consumed
+    // and then refilled with the chunk PF strides ahead, so PF - 1 chunks stay in flight while one is
+    // consumed.  (Moving loaded registers down a shift register instead would make every iteration wait for
+    // the loads it has just issued, leaving one chunk in flight.)  Refills are unconditional so that a slot
+    // is always the same registers: a chunk past the end has no valid key and reads row 0, one cache line.
+    constexpr int PF = 4;
     uint4 kq[PF][NL], vq[PF][NL];
     bool okq[PF][NL];
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-      if (first + j * stride < nchunks) fetch(first + j * stride, kq[j], vq[j], okq[j]);
-    int c = first;
-    while (c < nchunks) {
-      const int cn = c + PF * stride;
-      uint4 kn[NL], vn[NL];
-      bool okn[NL];
-      if (cn < nchunks) fetch(cn, kn, vn, okn);
-      consume(kq[0], vq[0], okq[0]);
+    for (int j = 0; j < PF; ++j) fetch(first + j * stride, kq[j], vq[j], okq[j]);
+    for (int c = first; c < nchunks; c += PF * stride) {
 #pragma unroll
-      for (int j = 0; j + 1 < PF; ++j)
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-          kq[j][i] = kq[j + 1][i]; vq[j][i] = vq[j + 1][i]; okq[j][i] = okq[j + 1][i];
-        }
-#pragma unroll
-      for (int i = 0; i < NL; ++i) {
-        kq[PF - 1][i] = kn[i]; vq[PF - 1][i] = vn[i]; okq[PF - 1][i] = okn[i];
+      for (int j = 0; j < PF; ++j) {
+        const int cj = c + j * stride;
+        if (cj < nchunks) consume(kq[j], vq[j], okq[j]);
+        fetch(cj + PF * stride, kq[j], vq[j], okq[j]);
       }
-      c += stride;
     }
   }
 

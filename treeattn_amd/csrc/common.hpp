@@ -152,6 +152,12 @@ __device__ __forceinline__ void wait_vmcnt_n() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Workgroup barrier for LDS traffic only: this wavefront's LDS operations complete, then s_barrier.  Unlike
+// __syncthreads() (whose workgroup-scope release fence waits for every outstanding memory load as well) it
+// leaves global loads in flight, so they can overlap the LDS work that follows; data copied into LDS by
+// global_load_lds must be waited for with wait_vmcnt_n before it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ----------------------------------------------------------------------------------------- wave helpers
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 __device__ __forceinline__ int wave_id() { return (int)(threadIdx.x / kWave); }

@@ -27,9 +27,8 @@ template <bool LN, int EPI, int TAIL>
 __global__ __launch_bounds__(kMmThreads) void rowmm_kernel(MmArgs a, RowmmTail t) {
   extern __shared__ __align__(16) char rowmm_lds[];
   __shared__ uint32_t s_last;
-  MmPre pre;
-  mm_load_w(a, blockIdx.x, blockIdx.z, pre);
-  const bool wrote = mm_tile<LN, EPI, false, TAIL == TAIL_ARGMAX, TAIL == TAIL_LN>(
+  MmPre pre;   // unused: the tile loads W itself, after X (WLATE)
+  const bool wrote = mm_tile<LN, EPI, false, TAIL == TAIL_ARGMAX, TAIL == TAIL_LN, true>(
       a, blockIdx.x, blockIdx.y, blockIdx.z, blockIdx.y * gridDim.x + blockIdx.x, pre, rowmm_lds, t.amax);
   if constexpr (TAIL != TAIL_NONE) {
     if (!wrote) return;

@@ -122,6 +122,25 @@ __device__ __forceinline__ void mm_load_w_stream(const MmArgs& a, int n0, int bl
   }
 }
 
+// W of the first round for this wavefront's two streams as exactly kMmWLoads load instructions per lane,
+// whatever the shape: a block past the split reads block 0 again and a column past N reads column n0 (neither
+// feeds an output that is kept), so that a wait on the memory counter can count them.
+constexpr int kMmWLoads = 2 * kMmSlots * 4;
+__device__ __forceinline__ void mm_load_w_all(const MmArgs& a, int n0, int nblk0, int blk0, MmPre& pre) {
+  const int lane = lane_id(), w = wave_id();
+  const int rl = lane & 31, kh = (lane >> 5) * 32;
+  const bf16_t* wr = a.W + (int64_t)(n0 + (n0 + rl < a.N ? rl : 0)) * a.ldw + (int64_t)blk0 * 64 + kh;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < kMmSlots; ++i) {
+      const int blk = w + 4 * s + kMmStreams * i;
+      const int b = blk < nblk0 ? blk : 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pre.w[s][i][j] = ldg16(wr + (int64_t)b * 64 + 8 * j);
+    }
+}
+
 // Issue the loads of W's first round for this wavefront's two streams.
 __device__ __forceinline__ void mm_load_w(const MmArgs& a, int tn, int split, MmPre& pre) {
   int blk0, nblk;
@@ -210,7 +229,10 @@ __device__ __forceinline__ void mm_rows_ln(const bf16_t* Y, int64_t ldy, int M, 
 // row's best (value, column) over the tile's columns -- of the bf16 outputs -- into amax[row] with an atomic
 // maximum of mm_argmax_key.  Returns true when this workgroup wrote the tile's output (always without
 // splits; the last to arrive with splits).
-template <bool LN, int EPI, bool FRESH, bool ARGMAX = false, bool WT = FRESH>
+// WLATE: pre is not used; W's first round is loaded here, right after the copies of X's first round are
+// issued, and only the copies are waited for before the LayerNorm, so the statistics and the transform of
+// the staged rows run while W is still arriving.
+template <bool LN, int EPI, bool FRESH, bool ARGMAX = false, bool WT = FRESH, bool WLATE = false>
 __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int split, int tile, const MmPre& pre,
                                         char* lds, uint64_t* amax = nullptr) {
   const int tid = threadIdx.x;
@@ -281,37 +303,40 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[s][i] = 0.0f;
 
-  for (int round = 0; round < nround; ++round) {
-    const int rb0 = round * kMmRound;
-    const int rn = nblk - rb0 < kMmRound ? nblk - rb0 : kMmRound;
-    if (round > 0) __syncthreads();   // the previous round's rows have been read
-    // X rows m0..m0+31 of this round's blocks -> LDS; one copy = 8 rows of one block, lane -> (row, piece)
-    {
-      const int prow = lane >> 3, pc = (lane & 7) ^ prow;
-      for (int c = w; c < rn * 4; c += 4) {
-        const int blk = c >> 2, row = (c & 3) * 8 + prow;
-        const int gm = m0 + row < a.M ? m0 + row : a.M - 1;
-        const bf16_t* src = a.X + (int64_t)gm * a.ldx + (int64_t)(blk0 + rb0 + blk) * 64 + 8 * pc;
-        // FRESH: cache policy sc1 (device scope, as the device-coherent loads)
-        if constexpr (FRESH)
-          __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(xs + (size_t)c * 512), 16, 0, 16);
-        else
-          __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(xs + (size_t)c * 512), 16, 0, 0);
-      }
-      if constexpr (LN) {
-        // the LayerNorm weight of the round: rn * 8 pieces of 16 bytes (a copy's surplus lanes read piece 0)
-        for (int c = w; c * 64 < rn * 8; c += 4) {
-          const int piece = c * 64 + lane;
-          const bf16_t* src = a.gam + (int64_t)(blk0 + rb0) * 64 + 8 * (piece < rn * 8 ? piece : 0);
-          __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(gs + (size_t)c * 512), 16, 0, 0);
-        }
+  // X rows m0..m0+31 of blocks [rb0, rb0 + rn) of the split -> LDS, and the LayerNorm weight of those blocks;
+  // one copy = 8 rows of one block, lane -> (row, piece).  Unrolled, so that no copy waits for another.
+  auto stage = [&](int rb0, int rn) {
+    const int prow = lane >> 3, pc = (lane & 7) ^ prow;
+#pragma unroll
+    for (int i = 0; i < kMmRound; ++i) {
+      const int c = w + 4 * i;
+      if (c >= rn * 4) break;
+      const int blk = c >> 2, row = (c & 3) * 8 + prow;
+      const int gm = m0 + row < a.M ? m0 + row : a.M - 1;
+      const bf16_t* src = a.X + (int64_t)gm * a.ldx + (int64_t)(blk0 + rb0 + blk) * 64 + 8 * pc;
+      // FRESH: cache policy sc1 (device scope, as the device-coherent loads)
+      if constexpr (FRESH)
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(xs + (size_t)c * 512), 16, 0, 16);
+      else
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(xs + (size_t)c * 512), 16, 0, 0);
+    }
+    if constexpr (LN) {
+      // rn * 8 pieces of 16 bytes (a copy's surplus lanes read piece 0)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = w + 4 * i;
+        if (c * 64 >= rn * 8) break;
+        const int piece = c * 64 + lane;
+        const bf16_t* src = a.gam + (int64_t)(blk0 + rb0) * 64 + 8 * (piece < rn * 8 ? piece : 0);
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(gs + (size_t)c * 512), 16, 0, 0);
       }
     }
-    wait_vmcnt_n<0>();
-    __syncthreads();
-    if (round == 0) TA_MARK(0);
+  };
+
+  // statistics (when they come from the staged rows) and the LayerNorm of the staged rows, in place
+  auto normalise = [&](int rn) {
     if (LN && stats_staged) {
-      // statistics from the staged rows: thread (r, part) sums piece `part` of every block of row r
+      // thread (r, part) sums piece `part` of every block of row r
       const int r = tid >> 3, part = tid & 7;
       float s = 0.0f, s2 = 0.0f;
 #pragma unroll 4
@@ -329,12 +354,11 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
         s_mean[r] = mean;
         s_rstd[r] = rsqrtf(fmaxf(s2 / (float)a.K - mean * mean, 0.0f) + a.eps);
       }
-      __syncthreads();
+      lds_barrier();
     }
-    if (round == 0) TA_MARK(1);
+    TA_MARK(1);
     if constexpr (LN) {
-      // the LayerNorm of the staged rows, in place: thread tid takes position tid % 8 of row tid / 8 in every
-      // block of the round
+      // thread tid takes position tid % 8 of row tid / 8 in every block of the round
       const int row = tid >> 3, pos = tid & 7;
       const float mean = s_mean[row], rstd = s_rstd[row];
       const bf16_t* gp = gs + 8 * (pos ^ (row & 7));
@@ -354,21 +378,16 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
         }
         *xp = make_uint4(o[0], o[1], o[2], o[3]);
       }
-      __syncthreads();
+      lds_barrier();
     }
-    if (round == 0) TA_MARK(2);
+    TA_MARK(2);
+  };
+
+  // the products of the staged blocks with W (wb: this wavefront's two streams)
+  auto products = [&](int rn, const MmPre& wb) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int v = w + 4 * s;
-      uint4 wb[kMmSlots][4];
-      if (round == 0) {
-#pragma unroll
-        for (int i = 0; i < kMmSlots; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) wb[i][j] = pre.w[s][i][j];
-      } else {
-        mm_load_w_stream(a, n0, blk0, nblk, round, v, wb);
-      }
 #pragma unroll
       for (int i = 0; i < kMmSlots; ++i) {
         const int lb = v + kMmStreams * i;   // block within the round
@@ -379,11 +398,46 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
           const uint4 xa = *reinterpret_cast<const uint4*>(xrow + 8 * ((ph + j) ^ (rl & 7)));
           bf16x8 av, bv;
           __builtin_memcpy(&av, &xa, 16);
-          __builtin_memcpy(&bv, &wb[i][j], 16);
+          __builtin_memcpy(&bv, &wb.w[s][i][j], 16);
           acc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[s], 0, 0, 0);
         }
       }
     }
+  };
+
+  // round 0; its W registers are used where they were loaded (no copies, which would wait for the loads)
+  {
+    const int rn = nblk < kMmRound ? nblk : kMmRound;
+    stage(0, rn);
+    if constexpr (WLATE) {
+      MmPre wl;
+      asm volatile("" ::: "memory");   // W's loads are issued after the copies, so they are counted last
+      mm_load_w_all(a, n0, rn, blk0, wl);
+      wait_vmcnt_n<kMmWLoads>();       // the copies (and the residual loads before them) have landed
+      lds_barrier();                   // (W stays in flight through the LayerNorm)
+      TA_MARK(0);
+      normalise(rn);
+      products(rn, wl);
+    } else {
+      wait_vmcnt_n<0>();
+      __syncthreads();
+      TA_MARK(0);
+      normalise(rn);
+      products(rn, pre);
+    }
+  }
+  for (int round = 1; round < nround; ++round) {
+    const int rb0 = round * kMmRound;
+    const int rn = nblk - rb0 < kMmRound ? nblk - rb0 : kMmRound;
+    __syncthreads();   // the previous round's rows have been read
+    stage(rb0, rn);
+    wait_vmcnt_n<0>();
+    __syncthreads();
+    normalise(rn);
+    MmPre wb;
+    mm_load_w_stream(a, n0, blk0, nblk, round, w, wb.w[0]);
+    mm_load_w_stream(a, n0, blk0, nblk, round, w + 4, wb.w[1]);
+    products(rn, wb);
   }
   __syncthreads();   // every wavefront is done with the staged rows; the partial tiles take their place
   // 32x32 MFMA output layout: lane -> column lane % 32; register i -> row 8(i/4) + 4(lane/32) + i%4
