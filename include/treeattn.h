@@ -170,6 +170,25 @@ int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                     int nsplit, float* ws, int64_t ws_bytes, void* stream);
 
 /*
+ * One decode step of one layer's attention in one launch (replaces seg_attend in the structural mode,
+ * engine.py:84-120, with SegState.add, engine.py:41-55): per (sequence, head), the cache append of
+ * k_new / v_new at row t = t_pos[b] (and the nodes it completes), the beam descent of q (B,H,1,D) at t, and the
+ * attention over the kept leaf blocks (the first min(n_tree[b,h], kept) of them), the own block and the static
+ * keys, one workgroup per (sequence, head).  The selection is written to ids / vld / sct (B,H,1,wl) as
+ * ta_tree_descend writes it; out (B,H,1,D) strides osb, osh; keys (B,H,1) float32 or NULL.  Equals
+ * ta_tree_descend_append followed by ta_seg_attn_fwd with nsplit 4, bit for bit.  D is 64 or 128, wl <= 64;
+ * q, new rows, caches and output share dtype; the levels are written (the append's nodes).
+ */
+int ta_seg_attend(const void* q, const void* k_new, const void* v_new, int dtype, int64_t qsb, int64_t qsh,
+                  int64_t nsb, int64_t nsh, int64_t vnsb, int64_t vnsh, int B, int H, int D,
+                  const int32_t* t_pos, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                  const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl,
+                  void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
+                  const int32_t* n_tree, int local, float scale,
+                  int32_t* ids, uint8_t* vld, float* sct, void* out, int64_t osb, int64_t osh, float* keys,
+                  void* stream);
+
+/*
  * Decode-cache append with incremental node formation (replaces engine.py:41-55 SegState.add and the
  * state writes of engine.py:102-106).  For every sequence b at position t = t_pos[b]: row t of the K and
  * V caches (B,H,Tcap,D, cache dtype) takes k_new, v_new (B,H,D with strides, same dtype as the cache);

@@ -511,6 +511,65 @@ def test_descend_append_equals_two_calls(leaf, arity, B, H, dtype):
         assert torch.equal(x, y)
 
 
+@pytest.mark.parametrize('leaf,arity,B,H,D,dtype,wmax', [(8, 2, 2, 3, 64, torch.float32, 4),
+                                                         (16, 4, 1, 2, 128, torch.bfloat16, 6),
+                                                         (64, 2, 32, 12, 64, torch.bfloat16, 8),
+                                                         (32, 2, 3, 4, 64, torch.float16, 32)])
+def test_seg_attend_equals_descend_append_then_attention(leaf, arity, B, H, D, dtype, wmax):
+    """The one-launch decode attention (append + descent + attention per (sequence, head)) gives the same
+    selection, output, key counts, caches and nodes, bit for bit, as the descent with the append followed by
+    the attention kernel with one workgroup per query, over positions that complete leaf blocks and higher
+    nodes."""
+    print('case', leaf, arity, B, H, D, dtype, wmax, flush=True)
+    Tcap = 2048
+    shape = K.TreeShape(Tcap, leaf, arity)
+    t0 = 5 * leaf * arity - 3
+    kk = rnd(B, H, Tcap, D, seed=63, dtype=dtype).to(DEV)
+    vv = rnd(B, H, Tcap, D, seed=64, dtype=dtype).to(DEV)
+    qq = rnd(B, H, 8, D, seed=65, dtype=dtype).to(DEV)
+    state = []
+    for _ in range(2):
+        Kc = torch.zeros(B, H, Tcap, D, device=DEV, dtype=dtype)
+        Vc = torch.zeros_like(Kc)
+        Kc[:, :, :t0] = kk[:, :, :t0]
+        Vc[:, :, :t0] = vv[:, :, :t0]
+        levels = shape.alloc_levels(B, H, D, DEV)
+        for lv in levels:
+            lv.zero_()
+        K.level_sums(Kc, shape.blevels, out=levels, t_end=t0)
+        state.append((Kc, Vc, levels))
+    wl = shape.leaf_width(wmax)
+    n_tree = torch.full((B, H, 1), max(wl - 1, 1), dtype=torch.int32, device=DEV)
+    scale = 1.0 / math.sqrt(D)
+    ws = K.seg_attn_workspace(B, H, 1, D, 4, DEV)
+
+    def sel():
+        return (torch.empty(B, H, 1, wl, dtype=torch.int32, device=DEV),
+                torch.empty(B, H, 1, wl, dtype=torch.uint8, device=DEV), torch.empty(B, H, 1, wl, device=DEV))
+    for step in range(8):
+        t = t0 + step
+        tpos = torch.full((B,), t, dtype=torch.int32, device=DEV)
+        q = qq[:, :, step:step + 1]
+        Kc, Vc, levels = state[0]
+        a = K.tree_descend_append(q, levels, tpos, shape, wmax, kk[:, :, t], vv[:, :, t], Kc, Vc, out=sel())
+        oa = torch.empty(B, H, 1, D, device=DEV, dtype=dtype)
+        ka = torch.empty(B, H, 1, device=DEV)
+        K.seg_attn(q, Kc, Vc, tpos.view(B, 1), a[0], a[1], n_tree, leaf, 3, scale, out=oa, keys=ka, nsplit=4, ws=ws)
+        Kc2, Vc2, levels2 = state[1]
+        bsel = sel()
+        ob = torch.empty(B, H, 1, D, device=DEV, dtype=dtype)
+        kb = torch.empty(B, H, 1, device=DEV)
+        K.seg_attend(q, levels2, tpos, shape, wmax, kk[:, :, t], vv[:, :, t], Kc2, Vc2, n_tree, 3, scale, bsel, ob,
+                     keys=kb)
+        for x, y in zip(a, bsel):
+            assert torch.equal(x, y), step
+        assert torch.equal(oa, ob), (step, (oa.float() - ob.float()).abs().max().item())
+        assert torch.equal(ka, kb), step
+    assert torch.equal(state[0][0], state[1][0]) and torch.equal(state[0][1], state[1][1])
+    for x, y in zip(state[0][2], state[1][2]):
+        assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
 def test_embed_matches_table_sum(dtype):
     """x = wte[tok] + wpe[t] (rounded once), int32 positions, and the in-place position advance."""

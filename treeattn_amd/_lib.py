@@ -59,6 +59,10 @@ SIGNATURES = {
                                        _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp,
                                        c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
                                        c_i32, c_vp]),
+    'ta_seg_attend': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32,
+                              c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32,
+                              c_vp, c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_i32, c_f32, c_vp, c_vp, c_vp, c_vp,
+                              c_i64, c_i64, c_vp, c_vp]),
     'ta_gather_dot': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i32, c_i64, c_i64, c_i64, c_vp,
                               c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_vp]),
     'ta_gather_dot_blocks': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp,

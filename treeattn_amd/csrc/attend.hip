@@ -19,6 +19,7 @@
 #include "attend_query.hpp"
 #include "attn.hpp"
 #include "common.hpp"
+#include "descend.hpp"
 
 namespace ta {
 
@@ -51,6 +52,57 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
     nt = p.n_tree ? p.n_tree[qi] : p.wl;
   }
   attn_query<T, D, SPLIT, CAND>(p, n, g, b, h, qi, qrow, t, idr, vr, -1, nt, orow, smem_f);
+}
+
+// ----------------------------------------------------------------------------------------- decode attend
+// One decode position per (sequence, head), everything in one workgroup of four wavefronts: the cache
+// append of row t (and the nodes it completes), the beam descent (which reads only nodes ending before t),
+// then the attention over the kept leaf blocks, the own block and the static keys.  The kept leaves stay in
+// LDS; the selection is also written to ids / vld / sct as the descent kernel writes it.  Same device
+// functions as the separate kernels, so the results equal ta_tree_descend_append followed by
+// ta_seg_attn_fwd with one workgroup per query, bit for bit.
+template <typename T, int D>
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void seg_attend_kernel(AttnParams p, LevelIn lv, int n_levels,
+                                                                           int arity_log2, int Tgeo, int wmax,
+                                                                           int cmax4, int32_t* __restrict__ ids,
+                                                                           uint8_t* __restrict__ vld,
+                                                                           float* __restrict__ sct, AppendIn ap) {
+  extern __shared__ __align__(16) char sa_lds[];
+  constexpr int NT = kWavesPerBlock * kWave;
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, h = bh % p.H;
+  const int wmax4 = (wmax + 3) & ~3;
+  uint64_t* ckey = reinterpret_cast<uint64_t*>(sa_lds);
+  int32_t* cid = reinterpret_cast<int32_t*>(ckey + cmax4);
+  float* csc = reinterpret_cast<float*>(cid + cmax4);
+  int32_t* kid = cid + 2 * cmax4;
+  float* ksc = reinterpret_cast<float*>(kid + wmax4);
+  float* stk = ksc + wmax4;           // the append's carry stack, 16 * D
+  float* att = stk + 16 * D;          // the attention's LDS
+
+  const int t = p.tq[b];
+  if (tid < D && t >= 0 && t < ap.Tcap)
+    append_dim<T>(tid, D, t, reinterpret_cast<const T*>(ap.kn) + b * ap.nsb + h * ap.nsh,
+                  reinterpret_cast<const T*>(ap.vn) + b * ap.vnsb + h * ap.vnsh,
+                  reinterpret_cast<T*>(ap.Kc) + b * ap.csb + h * ap.csh,
+                  reinterpret_cast<T*>(ap.Vc) + b * ap.csb + h * ap.csh, ap.cst, n_levels, lv.blevel[0], arity_log2,
+                  stk, [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
+  const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh;
+  int nk = descend_query<T, D, kWavesPerBlock>(qrow, t, Tgeo, b, h, lv, n_levels, arity_log2, wmax, tid, ckey, cid,
+                                               csc, kid, ksc);
+  const int64_t obase = (int64_t)bh * p.wl;
+  for (int r = tid; r < p.wl; r += NT) {
+    const bool ok = r < nk;
+    ids[obase + r] = ok ? kid[r] : -1;
+    vld[obase + r] = ok ? 1 : 0;
+    sct[obase + r] = ok ? ksc[r] : -INFINITY;
+  }
+  nk = nk < p.wl ? nk : p.wl;   // the attention of the separate kernels sees the first wl of them
+  __syncthreads();              // the appended row is visible to every wavefront
+  const int nt = p.n_tree ? p.n_tree[bh] : p.wl;
+  T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh;
+  attn_query<T, D, true, false>(p, 0, 0, b, h, bh, qrow, t, kid, nullptr, nk, nt, orow, att);
 }
 
 // ----------------------------------------------------------------------------------------- decode append
@@ -232,6 +284,84 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
     if (rc != TA_ERR_UNSUPPORTED) return rc;
   }
   return dispatch_attn(dtype, D, p, B, nsplit > 1, (hipStream_t)stream);
+}
+
+extern "C" int ta_seg_attend(const void* q, const void* k_new, const void* v_new, int dtype, int64_t qsb, int64_t qsh,
+                             int64_t nsb, int64_t nsh, int64_t vnsb, int64_t vnsh, int B, int H, int D,
+                             const int32_t* t_pos, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                             const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl, void* Kc,
+                             void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap, const int32_t* n_tree,
+                             int local, float scale, int32_t* ids, uint8_t* vld, float* sct, void* out, int64_t osb,
+                             int64_t osh, float* keys, void* stream) {
+  if (B <= 0 || H <= 0 || wmax < 1 || wl < 0 || wl > kWave || n_levels < 0 || n_levels > kMaxLevels || T <= 0 ||
+      (T & (T - 1)) || leaf_log2 < 1 || leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4 || Tcap <= 0) {
+    set_error("ta_seg_attend: bad sizes (at most 64 kept leaves)");
+    return TA_ERR_ARG;
+  }
+  if (D != 64 && D != 128) {
+    set_error("ta_seg_attend: head dim must be 64 or 128");
+    return TA_ERR_UNSUPPORTED;
+  }
+  const int Lw = local > 3 ? local : 3;
+  if (Lw + 1 > kWave) {
+    set_error("ta_seg_attend: local window must be < 64");
+    return TA_ERR_UNSUPPORTED;
+  }
+  if (!kv_aligned(q, dtype, D, {qsb, qsh}) || !kv_aligned(Kc, dtype, D, {csb, csh, cst}) ||
+      !kv_aligned(k_new, dtype, D, {nsb, nsh}) || !kv_aligned(v_new, dtype, D, {vnsb, vnsh})) {
+    set_error("ta_seg_attend: q/k/v rows not 16-byte aligned");
+    return TA_ERR_ARG;
+  }
+  LevelIn lv;
+  for (int j = 0; j < n_levels; ++j) {
+    lv.ptr[j] = lv_ptr[j];
+    lv.sb[j] = lv_sb[j];
+    lv.sh[j] = lv_sh[j];
+    lv.blevel[j] = leaf_log2 + j * arity_log2;
+    if (!aligned(lv_ptr[j], 16)) {
+      set_error("ta_seg_attend: level pointer not 16-byte aligned");
+      return TA_ERR_ARG;
+    }
+  }
+  if (n_levels == 0) lv.blevel[0] = leaf_log2;
+  const int arity = 1 << arity_log2;
+  const int cmax4 = (arity * wmax + arity - 1 + 3) & ~3;
+  const int wmax4 = (wmax + 3) & ~3;
+  const int wl_pad = (wl + 3) & ~3;
+  const size_t lds = (size_t)(4 * cmax4 + 2 * wmax4 + 16 * D) * sizeof(float) +
+                     (size_t)kWavesPerBlock * (wl_pad + kWave) * sizeof(float) +
+                     (size_t)kWavesPerBlock * (D + 2) * sizeof(float);
+  if (lds > 64 * 1024) {
+    set_error("ta_seg_attend: beam too wide for LDS (arity * wmax too large)");
+    return TA_ERR_UNSUPPORTED;
+  }
+  AttnParams p{};
+  p.q = q; p.qsb = qsb; p.qsh = qsh; p.qsn = 0;
+  p.k = Kc; p.ksb = csb; p.ksh = csh; p.kst = cst;
+  p.v = Vc; p.vsb = csb; p.vsh = csh; p.vst = cst;
+  p.H = H; p.Nq = 1; p.Tk = Tcap;
+  p.tq = t_pos; p.tq_sb = 1;
+  p.n_tree = n_tree; p.wl = wl;
+  p.leaf_log2 = leaf_log2;
+  p.Lw = Lw;
+  p.scale = scale;
+  p.gsplit = 1;
+  p.out = out; p.osb = osb; p.osh = osh; p.osn = 0;
+  p.keys = keys;
+  AppendIn ap{k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc, csb, csh, cst, Tcap};
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(B * H), blk(kWavesPerBlock * kWave);
+#define TA_SA(TT, DD) \
+  hipLaunchKernelGGL((seg_attend_kernel<TT, DD>), grid, blk, lds, st, p, lv, n_levels, arity_log2, T, wmax, cmax4, ids, \
+                     vld, sct, ap)
+  switch (dtype) {
+    case TA_F32: if (D == 64) TA_SA(float, 64); else TA_SA(float, 128); break;
+    case TA_F16: if (D == 64) TA_SA(f16_t, 64); else TA_SA(f16_t, 128); break;
+    case TA_BF16: if (D == 64) TA_SA(bf16_t, 64); else TA_SA(bf16_t, 128); break;
+    default: set_error("unknown dtype"); return TA_ERR_ARG;
+  }
+#undef TA_SA
+  return check_launch("seg_attend_kernel");
 }
 
 extern "C" int ta_kv_append(const void* k_new, const void* v_new, int dtype, int64_t nsb, int64_t nsh, int64_t vnsb,

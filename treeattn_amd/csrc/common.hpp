@@ -169,6 +169,25 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of G lanes (G a power of two up to 64); every lane of a group gets the sum.
+// Quad permutes pair lanes within quads; after them the value repeats every 4 lanes, so mirroring each
+// half-row (lane j <-> 7 - j) pairs the two quads of an 8-lane group, and mirroring the row (j <-> 15 - j)
+// the two halves of a 16-lane group.
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (G >= 2) x += dpp_f<0xB1>(x);    // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) x += dpp_f<0x4E>(x);    // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) x += dpp_f<0x141>(x);   // row_half_mirror
+  if constexpr (G >= 16) x += dpp_f<0x140>(x);  // row_mirror
+  if constexpr (G >= 32) x += __shfl_xor(x, 16, kWave);
+  if constexpr (G >= 64) x += __shfl_xor(x, 32, kWave);
+  return x;
+}
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));

@@ -1,13 +1,19 @@
 // Beam descent over the segment-tree node sums for one query, shared by the descent kernels (select.hip)
 // and the persistent decode step (step.hip).  Every score that decides a selection is computed in the
-// canonical float32 order (products rounded separately, grouped halving-tree sum, written with explicit
-// round-to-nearest operations so no contraction can change it), so results are bit-identical to the CPU
-// oracle's canonical mode.
+// canonical float32 order (products rounded separately, grouped halving-tree sum, with floating-point
+// contraction turned off in canon_dot so no product is fused into a sum whatever the compile flags), so
+// results are bit-identical to the CPU oracle's canonical mode.
 //
 // Reference functions replaced: seg.py:44-70 tree_pass, fastseg.py:254-271 tree_pass_fast.
 #pragma once
 
 #include "common.hpp"
+
+#ifndef TA_DMARK
+#define TA_DMARK(i) \
+  do {              \
+  } while (0)
+#endif
 
 namespace ta {
 
@@ -25,19 +31,22 @@ __device__ __forceinline__ float row_ror(float x) {
 // lane of the group returns the same value, bit for bit the butterfly's.
 template <int R>
 __device__ __forceinline__ float canon_dot(const float (&q)[R], const float (&s)[R]) {
+  // The operators are written here, under the pragma, so that no product is fused into a sum whatever the
+  // file's -ffp-contract (the bodies of __fmul_rn / __fadd_rn are outside the pragma's reach).
+#pragma clang fp contract(off)
   float p[R];
 #pragma unroll
-  for (int i = 0; i < R; ++i) p[i] = __fmul_rn(q[i], s[i]);
+  for (int i = 0; i < R; ++i) p[i] = q[i] * s[i];
 #pragma unroll
   for (int n = R / 2; n >= 1; n /= 2) {
 #pragma unroll
-    for (int i = 0; i < n; ++i) p[i] = __fadd_rn(p[i], p[i + n]);
+    for (int i = 0; i < n; ++i) p[i] = p[i] + p[i + n];
   }
   float x = p[0];
-  x = __fadd_rn(x, row_ror<8>(x));
-  x = __fadd_rn(x, row_ror<4>(x));
-  x = __fadd_rn(x, row_ror<2>(x));
-  x = __fadd_rn(x, row_ror<1>(x));
+  x = x + row_ror<8>(x);
+  x = x + row_ror<4>(x);
+  x = x + row_ror<2>(x);
+  x = x + row_ror<1>(x);
   return x;
 }
 
@@ -108,6 +117,8 @@ __device__ __forceinline__ int descend_query(const TQ* qrow, int t, int T, int b
       if (c >= C) ckey[c] = 0;
     }
     query_sync<WPQ>();
+    TA_DMARK(0);
+    int lvl_done = 0;
     for (int j = start;; --j) {
       const float* base = lv.ptr[j] + b * lv.sb[j] + h * lv.sh[j] + R * j16;
       const float scale = pow2_neg(lv.blevel[j]);
@@ -143,6 +154,7 @@ __device__ __forceinline__ int descend_query(const TQ* qrow, int t, int T, int b
         }
       }
       query_sync<WPQ>();
+      TA_DMARK(1 + 2 * lvl_done);
       // rank = number of candidates with a larger key; P lanes (a quad's aligned part) share a candidate
       {
         const int C2 = (C + 1) >> 1;
@@ -171,6 +183,9 @@ __device__ __forceinline__ int descend_query(const TQ* qrow, int t, int T, int b
       }
       nk = C < wmax ? C : wmax;
       query_sync<WPQ>();
+      TA_DMARK(2 + 2 * lvl_done);
+      ++lvl_done;
+      (void)lvl_done;
       if (j == 0) break;
       const int m = t >> lv.blevel[j - 1];
       const int digit = m & (arity - 1);

@@ -199,11 +199,8 @@ __device__ __forceinline__ void mm_rows_ln(const bf16_t* Y, int64_t ldy, int M, 
       for (int i = 0; i < 8; ++i)
         if (k0 + 64 * i < N) mm_add8(u[i], s, s2);
     }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-      s += __shfl_xor(s, o, kWave);
-      s2 += __shfl_xor(s2, o, kWave);
-    }
+    s = group_sum<8>(s);
+    s2 = group_sum<8>(s2);
     const float mean = s / (float)N;
     const float rstd = rsqrtf(fmaxf(s2 / (float)N - mean * mean, 0.0f) + eps);
     if (!ok) continue;
@@ -283,11 +280,8 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
 #pragma unroll
       for (int i = 0; i < 8; ++i) mm_add8(u[i], s, s2);
     }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-      s += __shfl_xor(s, o, kWave);
-      s2 += __shfl_xor(s2, o, kWave);
-    }
+    s = group_sum<8>(s);
+    s2 = group_sum<8>(s2);
     if (part == 0) {
       const float mean = s / (float)a.K;
       s_mean[r] = mean;
@@ -334,49 +328,62 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
   };
 
   // statistics (when they come from the staged rows) and the LayerNorm of the staged rows, in place
-  auto normalise = [&](int rn) {
-    if (LN && stats_staged) {
-      // thread (r, part) sums piece `part` of every block of row r
-      const int r = tid >> 3, part = tid & 7;
-      float s = 0.0f, s2 = 0.0f;
-#pragma unroll 4
-      for (int blk = 0; blk < rn; ++blk) {
-        const uint4 u = *reinterpret_cast<const uint4*>(xs + (size_t)(blk * 32 + r) * 64 + 8 * (part ^ (r & 7)));
-        mm_add8(u, s, s2);
-      }
+  // statistics (when they come from the staged rows) and the LayerNorm of the staged rows, in place.  Thread
+  // (r, part) owns piece `part` of row r in every block of the round: it sums them for the statistics (the
+  // row's 8 threads then combine their sums), keeps them in registers and writes them back normalised.
+  auto ln_piece = [&](uint4 xu, uint4 gu, float mean, float rstd) {
+    const uint32_t gw[4] = {gu.x, gu.y, gu.z, gu.w};
+    const uint32_t xw[4] = {xu.x, xu.y, xu.z, xu.w};
+    uint32_t o[4];
 #pragma unroll
-      for (int o = 1; o < 8; o <<= 1) {
-        s += __shfl_xor(s, o, kWave);
-        s2 += __shfl_xor(s2, o, kWave);
-      }
-      if (part == 0) {
-        const float mean = s / (float)a.K;
-        s_mean[r] = mean;
-        s_rstd[r] = rsqrtf(fmaxf(s2 / (float)a.K - mean * mean, 0.0f) + a.eps);
-      }
-      lds_barrier();
+    for (int e = 0; e < 4; ++e) {
+      const float f0 = __uint_as_float(xw[e] << 16), f1 = __uint_as_float(xw[e] & 0xffff0000u);
+      const float g0 = __uint_as_float(gw[e] << 16), g1 = __uint_as_float(gw[e] & 0xffff0000u);
+      o[e] = mm_pack2((f0 - mean) * rstd * g0, (f1 - mean) * rstd * g1);
     }
-    TA_MARK(1);
+    return make_uint4(o[0], o[1], o[2], o[3]);
+  };
+  auto normalise = [&](int rn) {
     if constexpr (LN) {
-      // thread tid takes position tid % 8 of row tid / 8 in every block of the round
-      const int row = tid >> 3, pos = tid & 7;
-      const float mean = s_mean[row], rstd = s_rstd[row];
-      const bf16_t* gp = gs + 8 * (pos ^ (row & 7));
-#pragma unroll 4
-      for (int blk = 0; blk < rn; ++blk) {
-        uint4* xp = reinterpret_cast<uint4*>(xs + (size_t)(blk * 32 + row) * 64 + 8 * pos);
-        const uint4 xu = *xp;
-        const uint4 gu = *reinterpret_cast<const uint4*>(gp + blk * 64);
-        const uint32_t gw[4] = {gu.x, gu.y, gu.z, gu.w};
-        const uint32_t xw[4] = {xu.x, xu.y, xu.z, xu.w};
-        uint32_t o[4];
+      const int r = tid >> 3, part = tid & 7;
+      const int phys = 8 * (part ^ (r & 7));   // where piece `part` of row r sits in a staged block
+      const bf16_t* gp = gs + 8 * part;
+      if (stats_staged) {
+        uint4 xv[kMmRound];   // every read issued before the first sum (a block past the round reads block 0)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float f0 = __uint_as_float(xw[e] << 16), f1 = __uint_as_float(xw[e] & 0xffff0000u);
-          const float g0 = __uint_as_float(gw[e] << 16), g1 = __uint_as_float(gw[e] & 0xffff0000u);
-          o[e] = mm_pack2((f0 - mean) * rstd * g0, (f1 - mean) * rstd * g1);
+        for (int blk = 0; blk < kMmRound; ++blk)
+          xv[blk] = *reinterpret_cast<const uint4*>(xs + (size_t)((blk < rn ? blk : 0) * 32 + r) * 64 + phys);
+        float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int blk = 0; blk < kMmRound; ++blk)
+          if (blk < rn) mm_add8(xv[blk], s, s2);
+        s = group_sum<8>(s);
+        s2 = group_sum<8>(s2);
+        const float mean = s / (float)a.K;
+        const float rstd = rsqrtf(fmaxf(s2 / (float)a.K - mean * mean, 0.0f) + a.eps);
+        TA_MARK(1);
+        // four blocks at a time: their weight pieces read together, then the transforms, then the stores
+#pragma unroll
+        for (int b4 = 0; b4 < kMmRound; b4 += 4) {
+          if (b4 >= rn) break;
+          uint4 gv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            gv[i] = *reinterpret_cast<const uint4*>(gp + (b4 + i < rn ? b4 + i : 0) * 64);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (b4 + i < rn)
+              *reinterpret_cast<uint4*>(xs + (size_t)((b4 + i) * 32 + r) * 64 + phys) =
+                  ln_piece(xv[b4 + i], gv[i], mean, rstd);
         }
-        *xp = make_uint4(o[0], o[1], o[2], o[3]);
+      } else {
+        // statistics from the pass over X
+        const float mean = s_mean[r], rstd = s_rstd[r];
+#pragma unroll 4
+        for (int blk = 0; blk < rn; ++blk) {
+          uint4* xp = reinterpret_cast<uint4*>(xs + (size_t)(blk * 32 + r) * 64 + phys);
+          *xp = ln_piece(*xp, *reinterpret_cast<const uint4*>(gp + blk * 64), mean, rstd);
+        }
       }
       lds_barrier();
     }

@@ -114,11 +114,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
       if (threadIdx.x < 8) {
         float s = 0.0f, s2 = 0.0f;
         for (int k = 0; k < C; k += 64) mm_add8(*reinterpret_cast<const uint4*>(srow + k + 8 * threadIdx.x), s, s2);
-#pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {
-          s += __shfl_xor(s, o, kWave);
-          s2 += __shfl_xor(s2, o, kWave);
-        }
+        s = group_sum<8>(s);
+        s2 = group_sum<8>(s2);
         if (threadIdx.x == 0) {
           const float mean = s / (float)C;
           s_stat[0] = mean;

@@ -93,18 +93,8 @@ __global__ __launch_bounds__(256) void level_pass_kernel(const T* __restrict__ i
 }
 
 // ----------------------------------------------------------------------------------------- descent
-// The decode-cache append fused into the descent launch (one query per (sequence, head)): new rows and
-// the caches, of the query's element type.
-struct AppendIn {
-  const void* kn;
-  const void* vn;
-  int64_t nsb, nsh, vnsb, vnsh;
-  void* Kc;
-  void* Vc;
-  int64_t csb, csh, cst;
-  int Tcap;
-};
-
+// Descent of one query per WPQ wavefronts; with APPEND (one query per (sequence, head)) the decode-cache
+// append of ap (rows of the query's element type) runs in the same launch.
 template <typename TQ, int D, int WPQ, bool APPEND>
 __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
     const TQ* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qsn, int H, int Nq, int T,

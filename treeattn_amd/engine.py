@@ -173,6 +173,14 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
     structural = (not cfg.neighbors) and lhat is None
     fused = structural and update and B * H < 4096 and q.dtype == k.dtype == state.K.dtype
+    if fused and scratch.nsplit == 4 and dh in (64, 128) and wl <= 64 and not cfg.global_pool:
+        # append, descent and attention in one launch (one workgroup per (sequence, head))
+        if scratch.n_tree is None:
+            scratch.n_tree = torch.full((B, H, 1), SEL.fixed_n_tree(cfg), dtype=torch.int32, device=q.device)
+        out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
+        K.seg_attend(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0], state.K, state.V,
+                     scratch.n_tree, cfg.local, scale, (scratch.ids, scratch.vld, scratch.sct), out, keys=scratch.keys)
+        return out, scratch.keys
     if fused:
         # descent and cache append in one launch (the append touches only row t and the nodes ending at t)
         ids, vld, sct = K.tree_descend_append(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0],

@@ -125,6 +125,34 @@ def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out
     return ids, vld, sct
 
 
+def seg_attend(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, n_tree, local, scale, sel, out, keys=None):
+    """One decode position per (sequence, head) in one launch: the cache append of k_new, v_new (B,H,D) at row
+    t_pos[b] of Kc, Vc (B,H,Tcap,D), the beam descent of q (B,H,1,D) and the attention over the kept leaf
+    blocks, the own block and the static keys.  sel = (ids, vld, sct) buffers (B,H,1,wl) receive the
+    selection; out (B,H,1,D) the attention output; keys (B,H,1) float32 the number of keys attended.  Equals
+    tree_descend_append followed by seg_attn with nsplit 4, bit for bit."""
+    L.require_gpu(q, t_pos, k_new, v_new, Kc, Vc, out)
+    B, H, Nq, D = q.shape
+    if Nq != 1 or t_pos.dtype != torch.int32 or not t_pos.is_contiguous():
+        raise ValueError('seg_attend: one query per (sequence, head) and contiguous int32 positions')
+    if not (q.dtype == k_new.dtype == v_new.dtype == Kc.dtype == Vc.dtype == out.dtype):
+        raise TypeError('seg_attend: q, new rows, caches and output must share a dtype')
+    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or Kc.stride() != Vc.stride() or out.stride(-1) != 1:
+        raise ValueError('seg_attend: unsupported layout')
+    ids, vld, sct = sel
+    wl = shape.leaf_width(wmax)
+    nt = None
+    if n_tree is not None:
+        nt = n_tree if (n_tree.dtype == torch.int32 and n_tree.is_contiguous()) else n_tree.to(torch.int32).contiguous()
+    L.call('ta_seg_attend', L.ptr(q), L.ptr(k_new), L.ptr(v_new), L.dtype_code(q), q.stride(0), q.stride(1),
+           k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1), B, H, D, L.ptr(t_pos),
+           len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
+           L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, L.ptr(Kc),
+           L.ptr(Vc), Kc.stride(0), Kc.stride(1), Kc.stride(2), Kc.shape[2], L.ptr(nt), int(local), float(scale),
+           L.ptr(ids), L.ptr(vld), L.ptr(sct), L.ptr(out), out.stride(0), out.stride(1), L.ptr(keys), L.stream())
+    return out, keys
+
+
 # ----------------------------------------------------------------------------------------------- gather-dot
 def gather_dot(q, S, cand, scale):
     """scale * q . S[clamp(cand)] in float32, canonical order.  q (b,H,N,dh), S (b,H,M,dh), cand (b,H,N,C)."""
