@@ -256,6 +256,14 @@ def decode_bench(args):
     out = torch.empty(B, H, 1, dh, device='cuda', dtype=torch.bfloat16)
     keys = torch.empty(B, H, 1, device='cuda')
 
+    # the one-launch layer attention re-appends row t_last with the values it already holds, so timing it
+    # repeatedly leaves the caches and node sums as they are
+    k_row = st.K[:, :, t_last].clone()
+    v_row = st.V[:, :, t_last].clone()
+    out2 = torch.empty_like(out)
+    keys2 = torch.empty_like(keys)
+    fused = sc.nsplit == 4   # the engine's choice (one workgroup per query)
+
     def attn():
         K.seg_attn(q, st.K, st.V, tpos.view(B, 1), ids, vld, n_tree, sh.leaf, cfg.local, 1.0 / math.sqrt(dh),
                    out=out, keys=keys, nsplit=sc.nsplit, ws=sc.ws)
@@ -263,13 +271,22 @@ def decode_bench(args):
     def descend():
         K.tree_descend(q, st.levels, tpos.view(B, 1), sh, cfg.wmax, out=(sc.ids, sc.vld, sc.sct))
 
+    def attend():
+        K.seg_attend(q, st.levels, tpos, sh, cfg.wmax, k_row, v_row, st.K, st.V, n_tree, cfg.local,
+                     1.0 / math.sqrt(dh), (sc.ids, sc.vld, sc.sct), out2, keys=keys2)
+
     for _ in range(3):
         attn()
         descend()
+        if fused:
+            attend()
     flush = torch.ones(1 << 28, dtype=torch.float32, device='cuda')   # 1 GiB, read before each launch
     attn_us = time_launches(attn, args.kernel_iters, flush)
     desc_us = time_launches(descend, args.kernel_iters, flush)
     attn_warm_us = time_launches(attn, args.kernel_iters)
+    if fused:
+        attend_us = time_launches(attend, args.kernel_iters, flush)
+        attend_warm_us = time_launches(attend, args.kernel_iters)
     del flush
     keys_total = float(keys.sum())
     elem = 2
@@ -279,6 +296,14 @@ def decode_bench(args):
     desc_bytes = B * H * (descent_nodes(t_last, sh, cfg.wmax) * dh * 4 + dh * elem + wl * 9)
     desc_gbs = desc_bytes / (desc_us * 1e-6) / 1e9
     log('attention %.1f us (%.0f GB/s), descent %.1f us' % (attn_us, attn_gbs, desc_us))
+    if fused:
+        # K/V rows of the selected blocks, the node sums the descent scores, q, out, the selection written
+        # (ids, vld, sct), n_tree, and the append (new k, v rows read and written)
+        attend_bytes = (keys_total * dh * elem * 2 + B * H * (descent_nodes(t_last, sh, cfg.wmax) * dh * 4 +
+                                                             2 * dh * elem + wl * 9 + 4 + 4 * dh * elem))
+        attend_gbs = attend_bytes / (attend_us * 1e-6) / 1e9
+        assert torch.equal(out2, out) and torch.equal(keys2, keys), 'one-launch attention differs from the kernels'
+        log('one-launch layer attention (append + descent + attention) %.1f us (%.0f GB/s)' % (attend_us, attend_gbs))
 
     headline = args.config == 4
     res = {
@@ -302,12 +327,21 @@ def decode_bench(args):
                      'timing': 'cold caches (1 GiB read before each of %d launches)' % args.kernel_iters,
                      'avg_us_warm_cache': round(attn_warm_us, 2),
                      'keys_per_query': round(keys_total / (B * H), 1)},
-        'kernels': {'descend_us': round(desc_us, 2), 'descend_GB/s': round(desc_gbs, 1),
+        'kernels': {'attn_kernel_us': round(attn_us, 2), 'attn_kernel_GB/s': round(attn_gbs, 1),
+                    'descend_us': round(desc_us, 2), 'descend_GB/s': round(desc_gbs, 1),
                     'descend_bytes': int(desc_bytes), 'attn_nsplit': sc.nsplit},
     }
     if headline:
         res['roofline']['traffic_source'] = ('profiles/decode_attention_traffic.md (rocprofv3 FETCH_SIZE x2.0 + '
                                              'WRITE_SIZE x1.0, calibrated on a 256 MiB copy)')
+    if fused:
+        # the decode step runs the one-launch layer attention: that is the dominant kernel
+        res['roofline'].update({
+            'kernel': 'seg_attend_kernel<bf16_t, 64> (cache append + beam descent + attention, one layer)',
+            'achieved': round(attend_gbs, 1), 'frac': round(attend_gbs / HBM_PEAK_GBS, 4),
+            'traffic': recorded_traffic('seg_attend_kernel_decode') if headline else None,
+            'bytes_per_launch': int(attend_bytes), 'avg_us': round(attend_us, 2),
+            'avg_us_warm_cache': round(attend_warm_us, 2)})
     if headline and not args.no_gather_dot:
         log('gather-dot leg')
         res['gather_dot'] = gather_dot_leg(args)
