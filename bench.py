@@ -53,6 +53,8 @@ def parse():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--no-gather-dot', action='store_true', help='skip the isolated gather-dot leg')
     ap.add_argument('--kernel-iters', type=int, default=50)
+    ap.add_argument('--groups', type=int, default=None,
+                    help='independent sequence groups, each captured and replayed on its own stream')
     args = ap.parse_args()
     # per-config defaults: 4 (the headline) and 5 are decode engines; 1 the small fp32 model; 3 prefill attention
     presets = {4: dict(steps=64, warmup=8, batch=32, context=32768, tcap=65536, leaf=64, arity=2, topk=32,
@@ -219,7 +221,8 @@ def decode_bench(args):
     W = build_model(cfg, 3, torch.bfloat16)
     g = torch.Generator().manual_seed(args.ids_seed)
     idx = torch.randint(0, args.vocab, (B, T0), generator=g)
-    dec = Decoder(W, args.layers, H, C, Tcap, 'seg', cfg, 'cuda', batch=B, dtype=torch.bfloat16)
+    dec = Decoder(W, args.layers, H, C, Tcap, 'seg', cfg, 'cuda', batch=B, dtype=torch.bfloat16,
+                  groups=args.groups)
     log('prefill %d x %d tokens' % (B, T0))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
