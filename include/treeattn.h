@@ -228,6 +228,22 @@ int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, in
              void* ws, int64_t ws_bytes, void* stream);
 
 /*
+ * Logits of a decode step and their greedy token (replaces engine.py:177, F.linear(ln_f(x), wte), and
+ * logits.argmax(-1) of the reference's greedy loop, phase2.py:51-66), bf16, for up to 32 rows:
+ *   Y[M,N] = LN(X)[M,K] . W[N,K]^T  (LN applied when ln_w != NULL, eps ln_eps), bit for bit ta_rowmm's
+ *   result with epilogue 0;  tok_out[m] (when tok_out != NULL) = the first column of the largest bf16 value
+ *   of row m of Y (NaN never chosen, 0 for a row of NaN), as ta_argmax_rows.
+ * 1 <= M <= 32, K a multiple of 64 up to 1024; X, W, ln_w 16-byte aligned with 16-byte row strides.  Each
+ * workgroup normalises the rows once and walks several 32-column tiles (the next tile's W in flight while one
+ * is multiplied); the last workgroup to finish reduces the per-workgroup row maxima.
+ * ws (needed with tok_out): ta_logits_workspace_size bytes, 256-byte aligned, zero-filled once when
+ * allocated (its counter returns to zero after every call); calls sharing a workspace must not overlap.
+ */
+int64_t ta_logits_workspace_size(int M, int N);
+int ta_logits(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy, const void* ln_w,
+              float ln_eps, int M, int N, int K, int64_t* tok_out, void* ws, int64_t ws_bytes, void* stream);
+
+/*
  * Row-wise argmax for greedy decoding (replaces logits.argmax(-1) of the reference's greedy loop,
  * phase2.py:51-66): out[r] = the first index of the largest value of x[r, 0:n].  x: rows of n elements of
  * dtype with row stride `stride`; out: int64.

@@ -391,6 +391,63 @@ def test_rowmm_split_k(M, N, KD, ln, epi):
         assert torch.equal(K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, splits=S, ws=ws), eager)
 
 
+@pytest.mark.parametrize('M,N,KD,ln,coarse', [(32, 50304, 768, True, False), (5, 1000, 128, True, True),
+                                               (1, 33, 64, False, False), (32, 70001, 1024, True, True),
+                                               (17, 4096, 512, False, True)])
+def test_logits_equal_rowmm_and_argmax(M, N, KD, ln, coarse):
+    """ta_logits (rows normalised once per workgroup, several column tiles each, row maxima reduced by the
+    last workgroup) equals ta_rowmm bit for bit and its tokens equal ta_argmax_rows of those logits (first
+    index among equal maxima: `coarse` weights make many ties), on two calls in a row sharing a workspace and
+    on graph replays."""
+    print('case', M, N, KD, ln, coarse, flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N + KD)
+    x = torch.randn(M, KD, generator=g).to(torch.bfloat16).to(DEV)
+    if coarse:
+        w = (torch.randint(-2, 3, (N, KD), generator=g).float() * 0.25).to(torch.bfloat16).to(DEV)
+    else:
+        w = (torch.randn(N, KD, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    lw = (1 + 0.1 * torch.randn(KD, generator=g)).to(torch.bfloat16).to(DEV) if ln else None
+    want = K.rowmm(x, w, ln_w=lw)
+    want_tok = K.argmax_rows(want)
+    ws = K.logits_workspace(M, N, DEV)
+    for rep in range(2):
+        tok = torch.full((M,), -1, dtype=torch.long, device=DEV)
+        got = K.logits(x, w, ln_w=lw, tok_out=tok, ws=ws)
+        assert torch.equal(got, want), rep
+        assert torch.equal(tok, want_tok), (rep, tok.tolist(), want_tok.tolist())
+    assert torch.equal(K.logits(x, w, ln_w=lw), want)   # logits only, no workspace
+    out = torch.zeros_like(want)
+    tok = torch.zeros(M, dtype=torch.long, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr, stream=s):
+            K.logits(x, w, ln_w=lw, out=out, tok_out=tok, ws=ws)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.zero_()
+        tok.fill_(-1)
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want) and torch.equal(tok, want_tok)
+
+
+def test_logits_rejects_bad_sizes():
+    bf = torch.bfloat16
+    x = torch.zeros(33, 128, dtype=bf, device=DEV)
+    w = torch.zeros(100, 128, dtype=bf, device=DEV)
+    with pytest.raises(RuntimeError):
+        K.logits(x, w)                                  # more than 32 rows
+    with pytest.raises(RuntimeError):
+        K.logits(x[:4], w, tok_out=torch.zeros(4, dtype=torch.long, device=DEV))   # no workspace
+    x2 = torch.zeros(4, 1088, dtype=bf, device=DEV)
+    with pytest.raises(RuntimeError):
+        K.logits(x2, torch.zeros(100, 1088, dtype=bf, device=DEV))   # K over 1024
+
+
 @pytest.mark.parametrize('M,N,KD,S', [(32, 768, 768, 1), (32, 768, 3072, 4), (7, 128, 256, 2)])
 def test_rowmm_layernorm_tail_equals_prologue(M, N, KD, S):
     """The LayerNorm tail (computed once by the last tile) gives, bit for bit, the rows the next product's

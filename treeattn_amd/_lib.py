@@ -84,6 +84,9 @@ SIGNATURES = {
     'ta_rowmm_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32]),
     'ta_rowmm': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32, c_i32,
                          c_i32, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
+    'ta_logits_workspace_size': (c_i64, [c_i32, c_i32]),
+    'ta_logits': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64,
+                          c_vp]),
     'ta_bf16_from_f32': (c_i32, [c_vp, c_vp, c_i64, c_vp]),
     'ta_decode_step_workspace_size': (c_i64, [_P(StepModel)]),
     'ta_decode_step_prepare': (c_i32, [_P(StepModel), c_vp, c_i64, _P(StepLaunch), c_vp]),

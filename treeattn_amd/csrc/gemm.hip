@@ -51,6 +51,186 @@ __global__ __launch_bounds__(kMmThreads) void rowmm_kernel(MmArgs a, RowmmTail t
   }
 }
 
+// ----------------------------------------------------------------------------------------- logits
+// LN_f + logits + greedy token of the decode step (engine.py:177, F.linear(ln_f(x), wte), and the argmax of
+// the greedy loop, phase2.py:51-66) for up to 32 rows.  Each workgroup stages and normalises the rows once,
+// then walks column tiles blockIdx.x, blockIdx.x + G, ... with the W of the next two tiles in flight while a
+// tile is multiplied.  Eight wavefronts: wavefront v computes K-block stream v of the tile (the blocks and
+// the order of mm_tile's stream v) and the partial tiles are summed in stream order, so the logits equal
+// ta_rowmm's bit for bit.  Every workgroup keeps each row's best (bf16 value, column) over its tiles and
+// writes it to ws; the last workgroup to finish takes the maximum per row (first column among equal maxima;
+// NaN never chosen; 0 for a row of NaN).
+constexpr int kLgThreads = 512;
+constexpr int kLgTriples = 3;   // a workgroup takes at most 3 * kLgTriples column tiles
+
+struct LogitsTail {
+  uint32_t* cnt;      // workgroups finished (zero between calls)
+  uint64_t* keys;     // [gridDim.x][M] best key of each workgroup and row
+  int64_t* tok_out;   // greedy token per row; NULL: logits only
+};
+
+// W of one tile for this wavefront's stream: kMmSlots blocks, unconditional loads (a block past K reads block
+// 0, a column past N reads column n0; neither feeds a kept output), so a wait can count them.
+struct LgW {
+  uint4 w[kMmSlots][4];
+};
+__device__ __forceinline__ void lg_load_w(const MmArgs& a, int n0, int rn, LgW& p) {
+  const int lane = lane_id(), v = wave_id();
+  const int rl = lane & 31, kh = (lane >> 5) * 32;
+  const bf16_t* wr = a.W + (int64_t)(n0 + (n0 + rl < a.N ? rl : 0)) * a.ldw + kh;
+#pragma unroll
+  for (int i = 0; i < kMmSlots; ++i) {
+    const int blk = v + kMmStreams * i;
+    const int b = blk < rn ? blk : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p.w[i][j] = ldg16(wr + (int64_t)b * 64 + 8 * j);
+  }
+}
+
+template <bool LN>
+__global__ __launch_bounds__(kLgThreads) void logits_kernel(MmArgs a, LogitsTail t) {
+  extern __shared__ __align__(16) char lg_lds[];
+  __shared__ uint32_t s_last;
+  __shared__ uint64_t s_key[kLgThreads];
+  constexpr int EPT = 1024 / kLgThreads;
+  constexpr int kLoads = kMmSlots * 4;   // W loads per lane and tile
+  const int tid = threadIdx.x, lane = lane_id(), v = wave_id();
+  const int rl = lane & 31, ph = (lane >> 5) * 4;
+  const int rn = a.K / 64;   // all of K is staged (the host checks K <= 1024)
+  bf16_t* xs = reinterpret_cast<bf16_t*>(lg_lds);
+  bf16_t* gs = xs + rn * 2048;
+  float* red = reinterpret_cast<float*>(lg_lds + mm_lds_main(rn));   // [8][32][33], not aliasing the rows
+  const int ntn = (a.N + 31) / 32, G = gridDim.x;
+  // the tiles of this workgroup: tn0 + G * i for i < ntile (the host launches at most ntn workgroups and
+  // enough that ntile <= 3 * kLgTriples)
+  const int tn0 = blockIdx.x;
+  const int ntile = (ntn - tn0 + G - 1) / G;
+  auto col = [&](int i) { return (tn0 + G * (i < ntile ? i : ntile - 1)) * 32; };
+
+  if (v < 4) mm_stage<LN, false>(a, xs, gs, 0, 0, rn);   // the staging is laid out for four wavefronts
+  LgW wa, wb, wc;
+  asm volatile("" ::: "memory");   // W's loads are issued after the copies, so they are counted last
+  lg_load_w(a, col(0), rn, wa);
+  lg_load_w(a, col(1), rn, wb);
+  wait_vmcnt_n<2 * kLoads>();      // the copies have landed (W stays in flight through the LayerNorm)
+  lds_barrier();
+  if constexpr (LN) {
+    if (tid < kMmThreads) mm_ln_staged(xs, gs, rn, a.K, a.eps);
+    lds_barrier();
+  }
+
+  float bv[EPT];
+  int bi[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    bv[k] = -INFINITY;
+    bi[k] = 0x7FFFFFFF;
+  }
+  auto tile = [&](int i, const LgW& wr) {
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kMmSlots; ++s) {
+      const int lb = v + kMmStreams * s;   // block of stream v
+      if (lb >= rn) break;
+      const bf16_t* xrow = xs + (size_t)(lb * 32 + rl) * 64;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 xa = *reinterpret_cast<const uint4*>(xrow + 8 * ((ph + j) ^ (rl & 7)));
+        bf16x8 av, bw;
+        __builtin_memcpy(&av, &xa, 16);
+        __builtin_memcpy(&bw, &wr.w[s][j], 16);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bw, acc, 0, 0, 0);
+      }
+    }
+    // 32x32 MFMA output layout: lane -> column lane % 32; register e -> row 8(e/4) + 4(lane/32) + e%4
+#pragma unroll
+    for (int e = 0; e < 16; ++e) red[(v * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * 33 + rl] = acc[e];
+    lds_barrier();
+    const int n0 = col(i);
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + k * kLgThreads;
+      const int r = e >> 5, c = e & 31;
+      float x = red[r * 33 + c];
+#pragma unroll
+      for (int s = 1; s < kMmStreams; ++s) x += red[(s * 32 + r) * 33 + c];
+      const int gn = n0 + c;
+      const bf16_t o = bf16_from(mm_bf16_round(x));
+      if (r < a.M && gn < a.N) {
+        *(TA_GLOBAL uint16_t*)(a.Y + (int64_t)r * a.ldy + gn) = o.bits;
+        const float f = to_f32(o);
+        if (f == f) mm_better(bv[k], bi[k], f, gn);
+      }
+    }
+    lds_barrier();   // the partial tiles have been read before the next tile writes them
+  };
+  // three W buffers in rotation, named, in straight-line code (a loop would copy buffers at its back edge,
+  // and a copy of registers with loads in flight waits for them); loads past this workgroup's last tile
+  // repeat that tile's (cached) rows, which keeps the count of loads fixed
+#pragma unroll
+  for (int q = 0; q < kLgTriples; ++q) {
+    const int i = 3 * q;
+    lg_load_w(a, col(i + 2), rn, wc);
+    tile(i, wa);
+    if (i + 1 >= ntile) break;
+    lg_load_w(a, col(i + 3), rn, wa);
+    tile(i + 1, wb);
+    if (i + 2 >= ntile) break;
+    lg_load_w(a, col(i + 4), rn, wb);
+    tile(i + 2, wc);
+    if (i + 3 >= ntile) break;
+  }
+  if (t.tok_out == nullptr) return;
+
+  // each row's best over this workgroup's tiles (lanes 0-31 or 32-63 of a wavefront hold one row)
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+#pragma unroll
+    for (int o2 = 1; o2 < 32; o2 <<= 1) {
+      const float v2 = __shfl_xor(bv[k], o2, kWave);
+      const int i2 = __shfl_xor(bi[k], o2, kWave);
+      mm_better(bv[k], bi[k], v2, i2);
+    }
+    const int r = (tid + k * kLgThreads) >> 5;
+    if (rl == 0 && r < a.M)
+      stg8_dc(t.keys + (int64_t)blockIdx.x * a.M + r, bi[k] != 0x7FFFFFFF ? mm_argmax_key(bv[k], bi[k]) : 0ull);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the keys have reached memory
+  __syncthreads();
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add((TA_GLOBAL uint32_t*)t.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (uint32_t)(G - 1);
+  __syncthreads();
+  if (!s_last) return;
+  // the last workgroup: thread (group q, row r) takes the maximum over workgroups q, q + 16, ...
+  constexpr int NQ = kLgThreads / 32;
+  {
+    const int r = tid & 31, q = tid >> 5;
+    uint64_t best = 0;
+    if (r < a.M) {
+      for (int g0 = q; g0 < G; g0 += NQ * 8) {
+        uint64_t kv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          kv[u] = g0 + NQ * u < G ? ldg8_dc(t.keys + (int64_t)(g0 + NQ * u) * a.M + r) : 0ull;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) best = kv[u] > best ? kv[u] : best;
+      }
+    }
+    s_key[tid] = best;
+  }
+  __syncthreads();
+  if (tid < a.M && tid < 32) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) best = s_key[q * 32 + tid] > best ? s_key[q * 32 + tid] : best;
+    t.tok_out[tid] = best ? (int64_t)(0x7FFFFFFF - (int)(uint32_t)(best & 0xFFFFFFFFu)) : 0;
+  }
+  if (tid == 0) stg4_dc(t.cnt, 0u);   // ready for the next call
+}
+
 }  // namespace ta
 
 using namespace ta;
@@ -174,4 +354,69 @@ extern "C" int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, 
   }
 #undef TA_LAUNCH
   return check_launch("rowmm_kernel");
+}
+
+namespace {
+
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+}  // namespace
+
+// workspace: [counter | 252 B | keys: one per workgroup and row (at most one workgroup per column tile)]
+extern "C" int64_t ta_logits_workspace_size(int M, int N) {
+  return M <= 0 || N <= 0 ? 0 : 256 + ((int64_t)((N + 31) / 32) * M * 8 + 255) / 256 * 256;
+}
+
+extern "C" int ta_logits(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy,
+                         const void* ln_w, float ln_eps, int M, int N, int K, int64_t* tok_out, void* ws,
+                         int64_t ws_bytes, void* stream) {
+  if (M <= 0 || M > 32 || N <= 0 || K < 64 || K > 1024 || K % 64 || ldx < K || ldw < K || ldy < N) {
+    set_error("ta_logits: bad sizes (1 <= M <= 32, K a multiple of 64 up to 1024)");
+    return TA_ERR_ARG;
+  }
+  if (((uintptr_t)X | (uintptr_t)W | (uintptr_t)ln_w) % 16 || (ldx * 2) % 16 || (ldw * 2) % 16) {
+    set_error("ta_logits: X, W and ln_w must be 16-byte aligned with 16-byte row strides");
+    return TA_ERR_ARG;
+  }
+  if (tok_out && (ws == nullptr || ws_bytes < ta_logits_workspace_size(M, N) || (uintptr_t)ws % 256)) {
+    set_error("ta_logits: workspace missing, too small or not 256-byte aligned");
+    return TA_ERR_WORKSPACE;
+  }
+  const int cus = device_cus();
+  if (cus <= 0) {
+    set_error("ta_logits: cannot query the device");
+    return TA_ERR_LAUNCH;
+  }
+  const int ntn = (N + 31) / 32;
+  // one workgroup per CU (its LDS allows one), more when a workgroup would otherwise take over 3 * kLgTriples
+  // tiles
+  const int grid = std::max(std::min(ntn, cus), (ntn + 3 * kLgTriples - 1) / (3 * kLgTriples));
+  MmArgs a{};
+  a.X = (const bf16_t*)X; a.ldx = ldx;
+  a.W = (const bf16_t*)W; a.ldw = ldw;
+  a.Y = (bf16_t*)Y; a.ldy = ldy;
+  a.gam = (const bf16_t*)ln_w; a.eps = ln_eps;
+  a.M = M; a.N = N; a.K = K;
+  a.splits = 1;
+  a.tiles = ntn;
+  LogitsTail t{};
+  t.cnt = (uint32_t*)ws;
+  t.keys = tok_out ? (uint64_t*)((char*)ws + 256) : nullptr;
+  t.tok_out = tok_out;
+  const size_t lds = (size_t)mm_lds_main(K / 64) + kMmRedBytes;
+  if (ln_w)
+    hipLaunchKernelGGL(logits_kernel<true>, dim3(grid), dim3(kLgThreads), lds, (hipStream_t)stream, a, t);
+  else
+    hipLaunchKernelGGL(logits_kernel<false>, dim3(grid), dim3(kLgThreads), lds, (hipStream_t)stream, a, t);
+  return check_launch("logits_kernel");
 }

@@ -221,6 +221,113 @@ __device__ __forceinline__ void mm_rows_ln(const bf16_t* Y, int64_t ldy, int M, 
   }
 }
 
+// X rows m0..m0+31 of blocks [blk0, blk0 + rn) -> LDS xs ([rn][32][64], 16-byte pieces of a row swizzled
+// by the row), and the LayerNorm weight of those blocks -> gs; one copy = 8 rows of one block, lane -> (row,
+// piece).  Unrolled, so that no copy waits for another.  FRESH: cache policy sc1 (device scope, as the
+// device-coherent loads).
+template <bool LN, bool FRESH>
+__device__ __forceinline__ void mm_stage(const MmArgs& a, bf16_t* xs, bf16_t* gs, int m0, int blk0, int rn) {
+  const int lane = lane_id(), w = wave_id();
+  const int prow = lane >> 3, pc = (lane & 7) ^ prow;
+#pragma unroll
+  for (int i = 0; i < kMmRound; ++i) {
+    const int c = w + 4 * i;
+    if (c >= rn * 4) break;
+    const int blk = c >> 2, row = (c & 3) * 8 + prow;
+    const int gm = m0 + row < a.M ? m0 + row : a.M - 1;
+    const bf16_t* src = a.X + (int64_t)gm * a.ldx + (int64_t)(blk0 + blk) * 64 + 8 * pc;
+    if constexpr (FRESH)
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(xs + (size_t)c * 512), 16, 0, 16);
+    else
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(xs + (size_t)c * 512), 16, 0, 0);
+  }
+  if constexpr (LN) {
+    // rn * 8 pieces of 16 bytes (a copy's surplus lanes read piece 0)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = w + 4 * i;
+      if (c * 64 >= rn * 8) break;
+      const int piece = c * 64 + lane;
+      const bf16_t* src = a.gam + (int64_t)blk0 * 64 + 8 * (piece < rn * 8 ? piece : 0);
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(gs + (size_t)c * 512), 16, 0, 0);
+    }
+  }
+}
+
+// One 16-byte piece of a row normalised: (x - mean) * rstd * g, rounded to bf16.
+__device__ __forceinline__ uint4 mm_ln_piece(uint4 xu, uint4 gu, float mean, float rstd) {
+  const uint32_t gw[4] = {gu.x, gu.y, gu.z, gu.w};
+  const uint32_t xw[4] = {xu.x, xu.y, xu.z, xu.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float f0 = __uint_as_float(xw[e] << 16), f1 = __uint_as_float(xw[e] & 0xffff0000u);
+    const float g0 = __uint_as_float(gw[e] << 16), g1 = __uint_as_float(gw[e] & 0xffff0000u);
+    o[e] = mm_pack2((f0 - mean) * rstd * g0, (f1 - mean) * rstd * g1);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// LayerNorm in place of the rn staged blocks that hold all of K (statistics from the staged rows).  Thread
+// (r, part) owns piece `part` of row r in every block: it sums them for the statistics (the row's 8 threads
+// then combine their sums), keeps them in registers and writes them back normalised.
+__device__ __forceinline__ void mm_ln_staged(bf16_t* xs, const bf16_t* gs, int rn, int K, float eps) {
+  const int tid = threadIdx.x;
+  const int r = tid >> 3, part = tid & 7;
+  const int phys = 8 * (part ^ (r & 7));   // where piece `part` of row r sits in a staged block
+  const bf16_t* gp = gs + 8 * part;
+  uint4 xv[kMmRound];   // every read issued before the first sum (a block past the round reads block 0)
+#pragma unroll
+  for (int blk = 0; blk < kMmRound; ++blk)
+    xv[blk] = *reinterpret_cast<const uint4*>(xs + (size_t)((blk < rn ? blk : 0) * 32 + r) * 64 + phys);
+  float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+  for (int blk = 0; blk < kMmRound; ++blk)
+    if (blk < rn) mm_add8(xv[blk], s, s2);
+  s = group_sum<8>(s);
+  s2 = group_sum<8>(s2);
+  const float mean = s / (float)K;
+  const float rstd = rsqrtf(fmaxf(s2 / (float)K - mean * mean, 0.0f) + eps);
+  // four blocks at a time: their weight pieces read together, then the transforms, then the stores
+#pragma unroll
+  for (int b4 = 0; b4 < kMmRound; b4 += 4) {
+    if (b4 >= rn) break;
+    uint4 gv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gv[i] = *reinterpret_cast<const uint4*>(gp + (b4 + i < rn ? b4 + i : 0) * 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (b4 + i < rn)
+        *reinterpret_cast<uint4*>(xs + (size_t)((b4 + i) * 32 + r) * 64 + phys) = mm_ln_piece(xv[b4 + i], gv[i], mean, rstd);
+  }
+}
+
+// The products of the rn staged blocks with W (wb: this wavefront's two streams of K blocks), accumulated
+// into acc in a fixed order.
+__device__ __forceinline__ void mm_products(const bf16_t* xs, int rn, const MmPre& wb, f32x16 (&acc)[2]) {
+  const int lane = lane_id(), w = wave_id();
+  const int rl = lane & 31;
+  const int ph = (lane >> 5) * 4;   // first 16-byte piece of this lane's half of a block row
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int v = w + 4 * s;
+#pragma unroll
+    for (int i = 0; i < kMmSlots; ++i) {
+      const int lb = v + kMmStreams * i;   // block within the round
+      if (lb >= rn) break;
+      const bf16_t* xrow = xs + (size_t)(lb * 32 + rl) * 64;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 xa = *reinterpret_cast<const uint4*>(xrow + 8 * ((ph + j) ^ (rl & 7)));
+        bf16x8 av, bv;
+        __builtin_memcpy(&av, &xa, 16);
+        __builtin_memcpy(&bv, &wb.w[s][i][j], 16);
+        acc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[s], 0, 0, 0);
+      }
+    }
+  }
+}
+
 // The tile (tn, tm) of split `split`, tile index `tile` among a.tiles.  pre holds W's first round (from
 // mm_load_w).  lds: mm_lds_bytes(blocks of the split) bytes of LDS, 16-byte aligned.  ARGMAX: also fold each
 // row's best (value, column) over the tile's columns -- of the bf16 outputs -- into amax[row] with an atomic
@@ -289,100 +396,29 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
     }
   }
 
-  const int rl = lane & 31;
-  const int ph = (lane >> 5) * 4;   // first 16-byte piece of this lane's half of a block row
   f32x16 acc[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[s][i] = 0.0f;
 
-  // X rows m0..m0+31 of blocks [rb0, rb0 + rn) of the split -> LDS, and the LayerNorm weight of those blocks;
-  // one copy = 8 rows of one block, lane -> (row, piece).  Unrolled, so that no copy waits for another.
-  auto stage = [&](int rb0, int rn) {
-    const int prow = lane >> 3, pc = (lane & 7) ^ prow;
-#pragma unroll
-    for (int i = 0; i < kMmRound; ++i) {
-      const int c = w + 4 * i;
-      if (c >= rn * 4) break;
-      const int blk = c >> 2, row = (c & 3) * 8 + prow;
-      const int gm = m0 + row < a.M ? m0 + row : a.M - 1;
-      const bf16_t* src = a.X + (int64_t)gm * a.ldx + (int64_t)(blk0 + rb0 + blk) * 64 + 8 * pc;
-      // FRESH: cache policy sc1 (device scope, as the device-coherent loads)
-      if constexpr (FRESH)
-        __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(xs + (size_t)c * 512), 16, 0, 16);
-      else
-        __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(xs + (size_t)c * 512), 16, 0, 0);
-    }
-    if constexpr (LN) {
-      // rn * 8 pieces of 16 bytes (a copy's surplus lanes read piece 0)
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int c = w + 4 * i;
-        if (c * 64 >= rn * 8) break;
-        const int piece = c * 64 + lane;
-        const bf16_t* src = a.gam + (int64_t)(blk0 + rb0) * 64 + 8 * (piece < rn * 8 ? piece : 0);
-        __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(gs + (size_t)c * 512), 16, 0, 0);
-      }
-    }
-  };
+  auto stage = [&](int rb0, int rn) { mm_stage<LN, FRESH>(a, xs, gs, m0, blk0 + rb0, rn); };
 
   // statistics (when they come from the staged rows) and the LayerNorm of the staged rows, in place
-  // statistics (when they come from the staged rows) and the LayerNorm of the staged rows, in place.  Thread
-  // (r, part) owns piece `part` of row r in every block of the round: it sums them for the statistics (the
-  // row's 8 threads then combine their sums), keeps them in registers and writes them back normalised.
-  auto ln_piece = [&](uint4 xu, uint4 gu, float mean, float rstd) {
-    const uint32_t gw[4] = {gu.x, gu.y, gu.z, gu.w};
-    const uint32_t xw[4] = {xu.x, xu.y, xu.z, xu.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float f0 = __uint_as_float(xw[e] << 16), f1 = __uint_as_float(xw[e] & 0xffff0000u);
-      const float g0 = __uint_as_float(gw[e] << 16), g1 = __uint_as_float(gw[e] & 0xffff0000u);
-      o[e] = mm_pack2((f0 - mean) * rstd * g0, (f1 - mean) * rstd * g1);
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
-  };
   auto normalise = [&](int rn) {
     if constexpr (LN) {
       const int r = tid >> 3, part = tid & 7;
       const int phys = 8 * (part ^ (r & 7));   // where piece `part` of row r sits in a staged block
       const bf16_t* gp = gs + 8 * part;
       if (stats_staged) {
-        uint4 xv[kMmRound];   // every read issued before the first sum (a block past the round reads block 0)
-#pragma unroll
-        for (int blk = 0; blk < kMmRound; ++blk)
-          xv[blk] = *reinterpret_cast<const uint4*>(xs + (size_t)((blk < rn ? blk : 0) * 32 + r) * 64 + phys);
-        float s = 0.0f, s2 = 0.0f;
-#pragma unroll
-        for (int blk = 0; blk < kMmRound; ++blk)
-          if (blk < rn) mm_add8(xv[blk], s, s2);
-        s = group_sum<8>(s);
-        s2 = group_sum<8>(s2);
-        const float mean = s / (float)a.K;
-        const float rstd = rsqrtf(fmaxf(s2 / (float)a.K - mean * mean, 0.0f) + a.eps);
-        TA_MARK(1);
-        // four blocks at a time: their weight pieces read together, then the transforms, then the stores
-#pragma unroll
-        for (int b4 = 0; b4 < kMmRound; b4 += 4) {
-          if (b4 >= rn) break;
-          uint4 gv[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            gv[i] = *reinterpret_cast<const uint4*>(gp + (b4 + i < rn ? b4 + i : 0) * 64);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (b4 + i < rn)
-              *reinterpret_cast<uint4*>(xs + (size_t)((b4 + i) * 32 + r) * 64 + phys) =
-                  ln_piece(xv[b4 + i], gv[i], mean, rstd);
-        }
+        mm_ln_staged(xs, gs, rn, a.K, a.eps);
       } else {
         // statistics from the pass over X
         const float mean = s_mean[r], rstd = s_rstd[r];
 #pragma unroll 4
         for (int blk = 0; blk < rn; ++blk) {
           uint4* xp = reinterpret_cast<uint4*>(xs + (size_t)(blk * 32 + r) * 64 + phys);
-          *xp = ln_piece(*xp, *reinterpret_cast<const uint4*>(gp + blk * 64), mean, rstd);
+          *xp = mm_ln_piece(*xp, *reinterpret_cast<const uint4*>(gp + blk * 64), mean, rstd);
         }
       }
       lds_barrier();
@@ -390,27 +426,7 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
     TA_MARK(2);
   };
 
-  // the products of the staged blocks with W (wb: this wavefront's two streams)
-  auto products = [&](int rn, const MmPre& wb) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int v = w + 4 * s;
-#pragma unroll
-      for (int i = 0; i < kMmSlots; ++i) {
-        const int lb = v + kMmStreams * i;   // block within the round
-        if (lb >= rn) break;
-        const bf16_t* xrow = xs + (size_t)(lb * 32 + rl) * 64;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint4 xa = *reinterpret_cast<const uint4*>(xrow + 8 * ((ph + j) ^ (rl & 7)));
-          bf16x8 av, bv;
-          __builtin_memcpy(&av, &xa, 16);
-          __builtin_memcpy(&bv, &wb.w[s][i][j], 16);
-          acc[s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[s], 0, 0, 0);
-        }
-      }
-    }
-  };
+  auto products = [&](int rn, const MmPre& wb) { mm_products(xs, rn, wb, acc); };
 
   // round 0; its W registers are used where they were loaded (no copies, which would wait for the loads)
   {

@@ -116,6 +116,7 @@ class _Scratch:
         self.nsplit = nsplit
         self.ws = K.seg_attn_workspace(B, H, 1, dh, nsplit, dev)
         self.mm_ws = None
+        self.lg_ws = None
 
     def mm(self, x, w, **kw):
         """ta_rowmm with the split count of K.rowmm_splits; the workspace (split partials, tail counter, argmax
@@ -131,6 +132,20 @@ class _Scratch:
                 self.mm_ws = torch.zeros(need, dtype=torch.uint8, device=x.device)
             return K.rowmm(x, w, splits=S, ws=self.mm_ws, **kw)
         return K.rowmm(x, w, splits=S, **kw)
+
+    def logits(self, x, w, ln_w, out, tok_out):
+        """LN_f + logits (+ greedy token) as one launch (ta_logits) when it serves the shapes, else ta_rowmm and
+        ta_argmax_rows."""
+        if not K.logits_supported(x, w):
+            self.mm(x, w, ln_w=ln_w, out=out)
+            if tok_out is not None:
+                K.argmax_rows(out, out=tok_out)
+            return
+        if self.lg_ws is None:   # allocated on the first (eager) step, so that a captured step finds it
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError('logits workspace must be allocated before graph capture')
+            self.lg_ws = K.logits_workspace(x.shape[0], w.shape[0], x.device)
+        K.logits(x, w, ln_w=ln_w, out=out, tok_out=tok_out, ws=self.lg_ws)
 
 
 def decode_nsplit(B, H, wl, leaf):
@@ -366,8 +381,10 @@ class Decoder:
         `advance` the positions tpos are incremented (by the embedding kernel, after it has read them); with
         tok_out the greedy tokens are written there.  Each product normalises its input rows itself (the
         LayerNorm prologue); measured on MI355X this is faster than normalising once in the producing kernel's
-        tail (1.37 vs 1.61 ms per config-4 step), and a separate argmax kernel is faster than the product's
-        argmax tail (whose per-row atomic maxima contend)."""
+        tail (1.37 vs 1.61 ms per config-4 step).  The logits and the greedy token come from ta_logits, whose
+        workgroups each normalise the rows once for several column tiles and reduce their row maxima before a
+        last workgroup combines them (the product's per-tile argmax tail, with per-row atomic maxima from every
+        tile, contends)."""
         W, H, C, dh = self.W, self.H, self.C, self.dh
         B = grp['b1'] - grp['b0']
         sc = grp['scratch']
@@ -384,9 +401,7 @@ class Decoder:
             sc.mm(out.view(B, C), L['c_proj'], epilogue='residual', residual=x, out=x)
             hmid = sc.mm(x, L['c_fc'], ln_w=L['ln2'], epilogue='gelu')
             sc.mm(hmid, L['c_mlp'], epilogue='residual', residual=x, out=x)
-        sc.mm(x, W['wte'], ln_w=W['ln_f'], out=logits)
-        if tok_out is not None:
-            K.argmax_rows(logits, out=tok_out)
+        sc.logits(x, W['wte'], W['ln_f'], logits, tok_out)
 
     def _forward_step_fused(self, tok, tpos):
         """The same step with the row-block kernels: LN1+QKV, attention, projection+residual, LN2+FC+GELU,

@@ -292,6 +292,36 @@ def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None, spl
     return (out, out_ln) if ln_next is not None else out
 
 
+def logits_supported(x, w):
+    """Whether ta_logits serves these rows and weights (bf16, at most 32 rows, K a multiple of 64 up to 1024)."""
+    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and 1 <= x.shape[0] <= 32
+            and x.shape[1] % 64 == 0 and 64 <= x.shape[1] <= 1024)
+
+
+def logits_workspace(M, N, device):
+    """Zero-filled workspace for logits with tok_out (arrival counter, per-workgroup row maxima)."""
+    n = L.lib().ta_logits_workspace_size(M, N)
+    return torch.zeros(max(n, 256), dtype=torch.uint8, device=device)
+
+
+def logits(x, w, ln_w=None, eps=1e-5, out=None, tok_out=None, ws=None):
+    """LN(x) @ w.T for up to 32 rows (bf16; x (M,K), w (N,K) -> (M,N)), bit for bit rowmm's result, and with
+    tok_out also the greedy token of every row (int64 (M,), the first index of the row's largest value), which
+    needs `ws` from logits_workspace."""
+    L.require_gpu(x, w)
+    M, K = x.shape
+    N = w.shape[0]
+    if x.stride(1) != 1 or w.stride(1) != 1:
+        raise ValueError('logits: rows must be contiguous')
+    if out is None:
+        out = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    if tok_out is not None and (tok_out.dtype != torch.long or not tok_out.is_contiguous() or tok_out.numel() != M):
+        raise ValueError('logits: tok_out must be contiguous int64 (M,)')
+    L.call('ta_logits', L.ptr(x), x.stride(0), L.ptr(w), w.stride(0), L.ptr(out), out.stride(0), L.ptr(ln_w),
+           float(eps), M, N, K, L.ptr(tok_out), L.ptr(ws), ws.numel() if ws is not None else 0, L.stream())
+    return out
+
+
 def bf16_round(x):
     """bf16 bit patterns (int16) of float32 x with the kernels' rounding (ta_bf16_from_f32)."""
     L.require_gpu(x)
