@@ -543,7 +543,7 @@ def prefill_attention_bench(args):
             'config': {'workload': 'SegAttention.sparse_attend, neighbours off: (4,16,16384,128) bf16, leaf %d, '
                                    'arity %d, top-k %d + own block + static keys' % (args.leaf, args.arity, args.topk)},
             'phases_us': {'pyramid': round(b_us, 1), 'descent': round(d_us, 1), 'attention': round(a_us, 1)},
-            'roofline': {'bound': 'mfma', 'kernel': 'attn_kernel<bf16_t, 128, false, false> (prefill attention)',
+            'roofline': {'bound': 'mfma', 'kernel': 'prefill_attn_kernel<bf16_t, 128, 6> (matrix-core prefill attention)',
                          'achieved': round(tflops, 2), 'peak': MFMA_BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                          'frac': round(tflops / MFMA_BF16_PEAK_TFLOPS, 5), 'traffic': None,
                          'flops_per_launch': flops, 'keys_per_query': round(keys_total / (B * H * T), 1),
