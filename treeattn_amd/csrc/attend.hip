@@ -91,18 +91,21 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void seg_attend_kernel(Attn
   const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh;
   int nk = descend_query<T, D, kWavesPerBlock>(qrow, t, Tgeo, b, h, lv, n_levels, arity_log2, wmax, tid, ckey, cid,
                                                csc, kid, ksc);
-  const int64_t obase = (int64_t)bh * p.wl;
+  const int nkw = nk < p.wl ? nk : p.wl;   // the attention of the separate kernels sees the first wl of them
+  // the appended row is visible to every wavefront: its stores (long since done) are waited for, then the
+  // barrier; the selection's outputs are written after the attention, so that no wait here covers them
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const int nt = p.n_tree ? p.n_tree[bh] : p.wl;
+  T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh;
+  attn_query<T, D, true, false>(p, 0, 0, b, h, bh, qrow, t, kid, nullptr, nkw, nt, orow, att);
+  const int64_t obase = (int64_t)bh * p.wl;   // kid and ksc are not written by the attention
   for (int r = tid; r < p.wl; r += NT) {
     const bool ok = r < nk;
     ids[obase + r] = ok ? kid[r] : -1;
     vld[obase + r] = ok ? 1 : 0;
     sct[obase + r] = ok ? ksc[r] : -INFINITY;
   }
-  nk = nk < p.wl ? nk : p.wl;   // the attention of the separate kernels sees the first wl of them
-  __syncthreads();              // the appended row is visible to every wavefront
-  const int nt = p.n_tree ? p.n_tree[bh] : p.wl;
-  T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh;
-  attn_query<T, D, true, false>(p, 0, 0, b, h, bh, qrow, t, kid, nullptr, nk, nt, orow, att);
 }
 
 // ----------------------------------------------------------------------------------------- decode append

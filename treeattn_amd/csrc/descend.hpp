@@ -68,9 +68,12 @@ struct LevelIn {
 // candidate against all others (score desc, id asc; candidate lists padded to a multiple of 4 with entries
 // that never rank first so LDS is read 16 bytes at a time), keep the best wmax, expand them to their
 // children and add the level's complete left siblings.
+// The query's threads exchange only LDS data (candidate ids, keys, scores, the kept set), so the workgroup
+// barrier waits for LDS operations only: a __syncthreads() would also wait for every global store and load
+// in flight (the decode step's cache append before the descent, say), which the descent does not read.
 template <int WPQ>
 __device__ __forceinline__ void query_sync() {
-  if constexpr (WPQ == 1) wave_sync(); else __syncthreads();
+  if constexpr (WPQ == 1) wave_sync(); else lds_barrier();
 }
 
 // Order-preserving 64-bit key of a candidate: larger key = ranked first (higher score, then lower node id).
