@@ -142,6 +142,25 @@ int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                        void* out, float* lse, void* stream);
 
 /*
+ * Backward of ta_sparse_attn_fwd (replaces fastseg.py:81-110 _attn_bwd and fastseg.py:158-170
+ * _SparseAttnFn.backward): given q, k, v, the forward's out o and lse, and dout = dL/do, with
+ * p_j = exp(scale q.k_j - lse) over the valid slots, Dq = dout . o and ds_j = p_j (dout . v_j - Dq):
+ *   dq = scale sum_j ds_j k_j  (written, input dtype, (B,H,T,D) contiguous),
+ *   dk[cand_j] += scale ds_j q,  dv[cand_j] += p_j dout  (float32 (B,H,Tk,D) contiguous, accumulated into:
+ *   zero them first).
+ * Slots as in the forward (-1 or >= Tk unused, duplicates counted).  q, o, dout: element strides (b, h, t)
+ * with the last dimension contiguous; k, v rows 16-byte aligned.  D a multiple of 8 up to 256, B*H <= 65535.
+ * dk and dv take float32 atomic adds, as the reference's kernel does: their summation order depends on
+ * scheduling (reproducible to float32 rounding); dq is deterministic.
+ */
+int ta_sparse_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, int dtype,
+                       int64_t qsb, int64_t qsh, int64_t qst, int64_t ksb, int64_t ksh, int64_t kst,
+                       int64_t vsb, int64_t vsh, int64_t vst, int64_t osb, int64_t osh, int64_t ost,
+                       int64_t dsb, int64_t dsh, int64_t dst, const int32_t* cand, const float* lse,
+                       int B, int H, int T, int Tk, int KC, int D, float scale, void* dq, float* dk, float* dv,
+                       void* stream);
+
+/*
  * Attention over the keys a descent selected (replaces fastseg.py:367-383 candidate assembly +
  * dedupe_fast + sparse_attn, and engine.py:107-119 for one decode position), neighbours off.
  * The key set of query n (position t = tq[b*tq_sb + n]) is the union of

@@ -51,6 +51,37 @@ def sparse_attn_lse(q, k, v, cand, scale):
     return torch.logsumexp(s, -1)
 
 
+def sparse_attn_bwd_ref(q, k, v, cand, scale, do):
+    """Gradients of sparse_attn_ref in closed form (the math of fastseg.py:81-110 _attn_bwd and
+    fastseg.py:158-170 _SparseAttnFn.backward), float32: with p_j = softmax over the valid slots of
+    scale * q . k_j, D = do . o, dp_j = do . v_j and ds_j = p_j (dp_j - D):
+        dq = scale * sum_j ds_j k_j,  dk[cand_j] += scale * ds_j q,  dv[cand_j] += p_j do.
+    Every valid slot counts (duplicates included); a row with no valid slot contributes nothing.
+    Returns (dq, dk, dv) float32 of the shapes of q, k, v."""
+    keep = cand >= 0
+    idx = cand.clamp(min=0).long()
+    qf, kf, vf, dof = q.float(), k.float(), v.float(), do.float()
+    kg = gather_nodes(kf, idx)
+    vg = gather_nodes(vf, idx)
+    s = (qf.unsqueeze(3) * kg).sum(-1) * scale
+    s = s.masked_fill(~keep, float('-inf'))
+    p = torch.nan_to_num(torch.softmax(s, -1), nan=0.0)
+    o = (p.unsqueeze(-1) * vg).sum(3)
+    Dt = (dof * o).sum(-1, keepdim=True)
+    dp = (dof.unsqueeze(3) * vg).sum(-1)
+    ds = torch.where(keep, p * (dp - Dt), torch.zeros_like(p))
+    dq = scale * (ds.unsqueeze(-1) * kg).sum(3)
+    b, H, T, KC = cand.shape
+    D = q.shape[-1]
+    dk = torch.zeros_like(kf)
+    dv = torch.zeros_like(vf)
+    flat = idx.reshape(b, H, T * KC, 1).expand(b, H, T * KC, D)
+    dk.scatter_add_(2, flat, (scale * ds.unsqueeze(-1) * qf.unsqueeze(3)).reshape(b, H, T * KC, D))
+    dv.scatter_add_(2, flat, (torch.where(keep, p, torch.zeros_like(p)).unsqueeze(-1) * dof.unsqueeze(3))
+                    .reshape(b, H, T * KC, D))
+    return dq, dk, dv
+
+
 def dedupe(cand, valid):
     """Keep the first valid copy of every position, by an all-pairs comparison (attention_dyn.py:12-17)."""
     n = cand.shape[-1]

@@ -155,6 +155,49 @@ def test_sparse_attn_matches_oracle(dtype, D):
     assert (out.cpu()[1, 1, 5] == 0).all()
 
 
+@pytest.mark.parametrize('dtype,D,KC', [(torch.float32, 64, 52), (torch.bfloat16, 64, 52), (torch.float16, 128, 70),
+                                        (torch.float32, 16, 9), (torch.bfloat16, 128, 200)])
+def test_sparse_attn_bwd_matches_oracle(dtype, D, KC):
+    """Backward of the candidate-list attention against the oracle's closed form (float32 from the same
+    inputs): dq, dk, dv within the dtype's bar; rows with nothing valid, duplicated and out-of-range slots."""
+    from oracle.attn_ref import sparse_attn_bwd_ref
+    print('case', dtype, D, KC, flush=True)
+    B, H, T = 2, 3, 150
+    q, k, v, do = [rnd(B, H, T, D, seed=s, dtype=dtype) for s in (30, 31, 32, 33)]
+    g = torch.Generator().manual_seed(34)
+    cand = torch.randint(-1, T, (B, H, T, KC), generator=g)
+    cand[..., 0] = torch.arange(T)
+    cand[1, 2, 7] = -1                       # nothing valid
+    cand[0, 1, 9, 1:4] = 3                   # a key three times
+    scale = 1 / math.sqrt(D)
+    qd, kd, vd, cd = q.to(DEV), k.to(DEV), v.to(DEV), cand.to(DEV)
+    out, lse = K.sparse_attn_fwd(qd, kd, vd, cd, scale)
+    dq, dk, dv = K.sparse_attn_bwd(qd, kd, vd, cd, scale, out, lse, do.to(DEV))
+    assert dq.dtype == dtype and dk.dtype == dtype and dv.dtype == dtype
+    wq, wk, wv = sparse_attn_bwd_ref(q, k, v, cand, scale, do)
+    tol = {torch.float32: 2e-4, torch.bfloat16: 6e-2, torch.float16: 1e-2}[dtype]
+    for got, want in ((dq, wq), (dk, wk), (dv, wv)):
+        err = (got.cpu().float() - want).abs().max().item()
+        assert err <= tol * max(1.0, want.abs().max().item()), err
+    assert (dq.cpu()[1, 2, 7] == 0).all()
+
+
+def test_fastseg_sparse_attn_is_differentiable():
+    """fastseg.sparse_attn through autograd: gradients equal the oracle's closed form (float32)."""
+    from oracle.attn_ref import sparse_attn_bwd_ref
+    from treeattn_amd import fastseg as FS
+    B, H, T, D, KC = 1, 2, 64, 64, 24
+    q, k, v, do = [rnd(B, H, T, D, seed=s, dtype=torch.float32) for s in (40, 41, 42, 43)]
+    g = torch.Generator().manual_seed(44)
+    cand = torch.randint(-1, T, (B, H, T, KC), generator=g)
+    qa, ka, va = [x.to(DEV).requires_grad_(True) for x in (q, k, v)]
+    out = FS.sparse_attn(qa, ka, va, cand.to(DEV), 0.125)
+    (out * do.to(DEV)).sum().backward()
+    wq, wk, wv = sparse_attn_bwd_ref(q, k, v, cand, 0.125, do)
+    for got, want in ((qa.grad, wq), (ka.grad, wk), (va.grad, wv)):
+        assert (got.cpu() - want).abs().max().item() < 2e-4 * max(1.0, want.abs().max().item())
+
+
 def _seg_case(T, D, leaf, arity, wmax, dtype, beam=None, nsplit=1, local=3, B=2, H=2):
     cfg = Config(wmax=wmax, beam=beam or wmax, neighbors=False, leaf=leaf, arity=arity, local=local, n_head=H)
     q, k, v = [rnd(B, H, T, D, seed=s, dtype=dtype) for s in (20, 21, 22)]

@@ -83,6 +83,41 @@ def test_all_keys_matches_dense(leaf, arity):
     assert (got - dense_causal(q, k, v)).abs().max().item() < 1e-5
 
 
+@pytest.mark.parametrize('kw', [dict(beam_mode='fixed'), dict(leaf=8, neighbors=False, wmax=3, beam=3)])
+def test_model_backward_matches_oracle(kw):
+    """Training step through the GPT (the reference's test_backward_and_losses, test_seg.py:97-108, made
+    exact): loss and every parameter gradient on the GPU equal the oracle model's (CPU autograd, float32)
+    within 1e-3 of the largest gradient; gradients are finite."""
+    import torch.nn.functional as F
+    cfg = tiny(**kw)
+    torch.manual_seed(5)
+    model = GPT(cfg).train()
+    ref = GPTRef(cfg, 'canonical').train()
+    sd = model.state_dict()
+    ref.load_state_dict({k: v for k, v in sd.items() if 'pred' not in k}, strict=False)
+    idx = torch.randint(0, 64, (2, 64))
+    tgt = torch.randint(0, 64, (2, 64))
+    want_logits = ref(idx)[0]
+    F.cross_entropy(want_logits.reshape(-1, 64), tgt.reshape(-1)).backward()
+    model = model.to(DEV)
+    got_logits = model(idx.to(DEV))[0]
+    loss = F.cross_entropy(got_logits.reshape(-1, 64), tgt.to(DEV).reshape(-1))
+    loss.backward()
+    assert torch.isfinite(loss).item()
+    rp = dict(ref.named_parameters())
+    n = 0
+    for name, prm in model.named_parameters():
+        if 'pred' in name or prm.grad is None:
+            continue
+        assert torch.isfinite(prm.grad).all(), name
+        want = rp[name].grad
+        assert want is not None, name
+        err = (prm.grad.cpu() - want).abs().max().item()
+        assert err <= 1e-3 * max(1e-3, want.abs().max().item()) + 1e-6, (name, err)
+        n += 1
+    assert n >= 8
+
+
 @pytest.mark.parametrize('kw', [dict(beam_mode='fixed'), dict(beam_mode='pred', global_pool=True),
                                 dict(leaf=8, neighbors=False, wmax=3, beam=3)])
 def test_causality(kw):

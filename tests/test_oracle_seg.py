@@ -256,3 +256,30 @@ def test_planted_wrong_operand_is_caught(monkeypatch):
     monkeypatch.setattr(S, 'dot_canonical', lambda q, U: orig(q, torch.cat([-U[..., :1], U[..., 1:]], -1)))
     with pytest.raises(AssertionError):
         test_descent_matches_brute_force(64, 2, 2, 3)
+
+
+@pytest.mark.parametrize('D,KC,seed', [(16, 7, 0), (64, 20, 1), (32, 40, 2)])
+def test_sparse_attn_bwd_closed_form_matches_autograd(D, KC, seed):
+    """The oracle's closed-form backward of the candidate-list attention equals torch autograd through the
+    oracle's forward (float64), including rows with no valid slot and duplicated slots."""
+    from oracle.attn_ref import sparse_attn_bwd_ref, sparse_attn_ref
+    g = torch.Generator().manual_seed(seed)
+    B, H, T = 2, 2, 24
+    q, k, v, do = [torch.randn(B, H, T, D, generator=g, dtype=torch.float64) for _ in range(4)]
+    cand = torch.randint(-1, T, (B, H, T, KC), generator=g)
+    cand[0, 1, 3] = -1                  # nothing valid
+    cand[1, 0, 5, :3] = 7               # a duplicated key
+    scale = 1 / D ** 0.5
+    qa, ka, va = [x.clone().requires_grad_(True) for x in (q, k, v)]
+    keep = cand >= 0
+    kg = S.gather_nodes(ka, cand.clamp(min=0).long())
+    vg = S.gather_nodes(va, cand.clamp(min=0).long())
+    s = ((qa.unsqueeze(3) * kg).sum(-1) * scale).masked_fill(~keep, float('-inf'))
+    p = torch.nan_to_num(torch.softmax(s, -1), nan=0.0)
+    o = (p.unsqueeze(-1) * vg).sum(3)
+    (o * do).sum().backward()
+    dq, dk, dv = sparse_attn_bwd_ref(q, k, v, cand, scale, do)
+    for got, want in ((dq, qa.grad), (dk, ka.grad), (dv, va.grad)):
+        assert (got.double() - want).abs().max().item() < 1e-4
+    # the forward the closed form differentiates is the oracle's own
+    assert (sparse_attn_ref(q.float(), k.float(), v.float(), cand, scale).double() - o.detach()).abs().max() < 1e-4

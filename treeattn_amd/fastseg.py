@@ -71,19 +71,24 @@ def gather_dot(q, S, cand, scale):
 
 # ------------------------------------------------------------------------------------------- attention
 class _SparseAttnFn(torch.autograd.Function):
+    """fastseg.py:144-170: the forward saves (q, k, v, cand, out, lse); the backward returns (dq, dk, dv)."""
+
     @staticmethod
     def forward(ctx, q, k, v, cand, scale):
-        out, _ = K.sparse_attn_fwd(q, k, v, cand, scale)
+        out, lse = K.sparse_attn_fwd(q, k, v, cand, scale)
+        ctx.save_for_backward(q, k, v, cand, out, lse)
+        ctx.scale = scale
         return out
 
     @staticmethod
     def backward(ctx, do):
-        raise NotImplementedError('treeattn_amd: the sparse-attention backward kernel (training) is not built yet')
+        q, k, v, cand, out, lse = ctx.saved_tensors
+        dq, dk, dv = K.sparse_attn_bwd(q, k, v, cand, ctx.scale, out, lse, do)
+        return dq, dk, dv, None, None
 
 
 def sparse_attn(q, k, v, cand, scale):
-    """cand: (b,H,T,K) int, -1 = unused slot (fastseg.py:173-177).  Forward on the GPU; the training
-    backward is not built yet."""
+    """cand: (b,H,T,K) int, -1 = unused slot (fastseg.py:173-177).  Differentiable in q, k, v."""
     _use_fast(q)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
         return _SparseAttnFn.apply(q, k, v, cand, scale)

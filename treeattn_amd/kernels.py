@@ -202,6 +202,27 @@ def sparse_attn_fwd(q, k, v, cand, scale):
     return out, lse
 
 
+def sparse_attn_bwd(q, k, v, cand, scale, out, lse, dout):
+    """Gradients of sparse_attn_fwd: (dq in q's dtype, dk, dv in k's / v's dtype).  dk and dv are summed in
+    float32 with atomic adds (their order depends on scheduling, as in the reference's kernel)."""
+    L.require_gpu(q, k, v, cand, out, lse, dout)
+    if not (q.dtype == k.dtype == v.dtype == out.dtype):
+        raise TypeError('q, k, v and out must share a dtype')
+    q, k, v, out, dout = [t.contiguous() for t in (q, k, v, out, dout.to(q.dtype))]
+    b, H, T, D = q.shape
+    Tk = k.shape[2]
+    KC = cand.shape[-1]
+    cc = cand.to(torch.int32).contiguous()
+    ls = lse.float().contiguous()
+    dq = torch.empty_like(q)
+    dk = torch.zeros(k.shape, device=q.device, dtype=torch.float32)
+    dv = torch.zeros(v.shape, device=q.device, dtype=torch.float32)
+    L.call('ta_sparse_attn_bwd', L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(out), L.ptr(dout), L.dtype_code(q),
+           *L.rows3(q), *L.rows3(k), *L.rows3(v), *L.rows3(out), *L.rows3(dout), L.ptr(cc), L.ptr(ls), b, H, T, Tk,
+           KC, D, float(scale), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.stream())
+    return dq, dk.to(k.dtype), dv.to(v.dtype)
+
+
 def seg_attn_workspace(B, H, Nq, D, nsplit, device):
     """Zero-filled workspace for seg_attn with `nsplit` (None when none is needed).  The per-query counters
     at its head are left at zero by every call, so one workspace serves calls that run one after another."""

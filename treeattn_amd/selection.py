@@ -172,7 +172,10 @@ def attend(q, k, v, lhat, cfg, scale=None):
     wl = ids32.shape[-1]
     NBK = sel['nb_pos'].shape[-1]
     tq = torch.arange(T, device=q.device)
-    if not cfg.neighbors:
+    # gradients wanted (training): the candidate-list kernels, whose backward is built (the structural kernel
+    # attends the same key set, forward only)
+    grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
+    if not cfg.neighbors and not grad:
         n_tree = sel['n_tree'].to(torch.int32)
         keys = torch.empty(b, H, T, device=q.device)
         out, _, keys = K.seg_attn(q, k, v, tq, ids32, vld8, n_tree, leaf, cfg.local, scale, keys=keys)
@@ -183,7 +186,12 @@ def attend(q, k, v, lhat, cfg, scale=None):
                    leaves_used=nused.mean())
         return out, aux, sel, None
     cand, keep, used = assemble(sel, tq, cfg, b, H)
-    out, _ = K.sparse_attn_fwd(q, k, v, torch.where(keep, cand, torch.full_like(cand, -1)), scale)
+    cm = torch.where(keep, cand, torch.full_like(cand, -1))
+    if grad:
+        from . import fastseg as FS
+        out = FS.sparse_attn(q, k, v, cm, scale)
+    else:
+        out, _ = K.sparse_attn_fwd(q, k, v, cm, scale)
     aux = dict(keys_total=keep.sum(-1).float().mean(), keys_tree=keep[..., :leaf * wl].sum(-1).float().mean(),
                keys_nb=keep[..., leaf * wl:leaf * wl + NBK].sum(-1).float().mean(),
                nb_leaves=sel['nb_leaves'].float().mean(), leaves_used=used.sum(-1).float().mean())
