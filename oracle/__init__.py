@@ -26,6 +26,9 @@ How each part is pinned (the reference ships no golden vectors):
   the identity ``dedupe == dedupe_fast``.
 * ``sparse_attn_ref`` / module logic: equality with dense causal softmax
   attention when every key is selected; causality.
+* ``sparse_attn_bwd_ref`` (closed-form gradients of ``sparse_attn_ref``): torch
+  autograd through the oracle's own forward in float64, with empty rows and
+  duplicated slots (tests/test_oracle_seg.py).
 * engine: the decode == prefill invariant (token-by-token logits equal the
   full-sequence forward logits).
 * Parity unpinned: ``torch.topk`` tie order and torch's CPU reduction order in

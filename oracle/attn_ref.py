@@ -1,6 +1,7 @@
 """Oracle: gather-dot, sparse softmax attention, candidate assembly and de-duplication.
 
-TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Restates fastseg.py:118-141 and 227-234,
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Restates fastseg.py:118-141 and 227-234, the backward
+of fastseg.py:81-110 / 158-170 in closed form,
 attention_dyn.py:12-17 and the module orchestration of fastseg.py:345-389 / attention_dyn.py:50-102.
 """
 import math
