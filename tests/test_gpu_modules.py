@@ -169,6 +169,28 @@ def test_engine_matches_forward(kw):
     assert (ref - got).abs().max().item() < 1e-4
 
 
+@pytest.mark.parametrize('kw', [dict(), dict(leaf=4, arity=4, wmax=3, beam=2)])
+def test_prefill_with_neighbours_then_decode_matches_decode_from_scratch(kw):
+    """Reference-default mode (neighbour borrowing on): a batched prefill of the first 40 positions, which
+    seeds the neighbour store, then token-by-token decoding gives the logits of decoding every position
+    from an empty cache (the decode == prefill invariant), and the prefill's last logits equal the forward's."""
+    torch.manual_seed(6)
+    cfg = tiny(**kw)
+    model = GPT(cfg).to(DEV).eval()
+    idx = torch.randint(0, 64, (1, 64)).to(DEV)
+    W = weights_from_ours(model.state_dict(), cfg)
+    T0 = 40
+    with torch.no_grad():
+        full = model(idx)[0][0]
+        a = Decoder(W, cfg.n_layer, cfg.n_head, cfg.n_embd, 64, 'seg', cfg, DEV)
+        last = a.prefill(idx[:, :T0])
+        got = torch.stack([a.step(int(idx[0, t]), t)[0] for t in range(T0, 64)])
+        b = Decoder(W, cfg.n_layer, cfg.n_head, cfg.n_embd, 64, 'seg', cfg, DEV)
+        want = torch.stack([b.step(int(idx[0, t]), t)[0] for t in range(64)])
+    assert (last[0] - full[T0 - 1]).abs().max().item() < 1e-4
+    assert (got - want[T0:]).abs().max().item() < 1e-4
+
+
 def test_engine_matches_oracle_engine():
     """Decoder.step logits vs the oracle decoder (fp32, leaf 8, neighbours off) over 96 positions."""
     cfg = tiny(seq_len=128, leaf=8, neighbors=False, wmax=4, beam=4, n_layer=2)

@@ -463,8 +463,8 @@ class Decoder:
         if B != self.B or T0 > self.Tcap:
             raise ValueError('prompt shape does not fit the decoder')
         cfg = self.cfg
-        if cfg.neighbors or cfg.beam_mode == 'pred':
-            raise NotImplementedError('prefill with neighbour borrowing or the budget head is not built yet')
+        if cfg.beam_mode == 'pred':
+            raise NotImplementedError('prefill with the budget head is not built yet')
         chunk = chunk or B
         tq = torch.arange(T0, device=self.dev, dtype=torch.int32)
         scale = 1.0 / math.sqrt(dh)
@@ -483,12 +483,29 @@ class Decoder:
                 Vb[:, :, :T0].copy_(v)
                 lv = [t[b0:b1] for t in st.levels]
                 K.level_sums(Kb, st.shape.blevels, out=lv, t_end=T0, zero_sink=True)
-                ids, vld, _ = K.tree_descend(q, lv, tq, st.shape, cfg.wmax)
-                n_tree = torch.full(ids.shape[:3], n_tree_val, dtype=torch.int32, device=self.dev)
                 out = torch.empty(nb, T0, H, dh, device=self.dev, dtype=v.dtype)
-                K.seg_attn(q, Kb, Vb, tq, ids, vld, n_tree, st.shape.leaf, cfg.local, scale,
-                           out=out.transpose(1, 2))
-                del ids, vld, n_tree
+                if cfg.neighbors:
+                    # the forward's selection with neighbour borrowing (fastseg.py:345-389), and the decode
+                    # store seeded with what decoding positions 0..T0-1 would have written (engine.py:103-105):
+                    # each position's top nb_store leaves of its own tree pass, which the selection's own
+                    # neighbour pass reads too
+                    lhat = torch.full((nb, H, T0), cfg.beam, dtype=torch.long, device=self.dev)
+                    sel, ids, vld, sct, _ = SEL.select(q, k, lhat, cfg, st.shape, lv)
+                    n = min(cfg.nb_store, ids.shape[-1])
+                    vb = vld[..., :n].bool()
+                    st.st_leaf[b0:b1, :, :T0, :n] = ids[..., :n].clamp(min=0)
+                    st.st_score[b0:b1, :, :T0, :n] = torch.where(vb, sct[..., :n], torch.zeros_like(sct[..., :n]))
+                    st.st_ok[b0:b1, :, :T0, :n] = vb
+                    cand, keep, _ = SEL.assemble(sel, tq.long(), cfg, nb, H)
+                    o, _ = K.sparse_attn_fwd(q, k, v, torch.where(keep, cand, torch.full_like(cand, -1)), scale)
+                    out.transpose(1, 2).copy_(o)
+                    del sel, ids, vld, sct, cand, keep, o
+                else:
+                    ids, vld, _ = K.tree_descend(q, lv, tq, st.shape, cfg.wmax)
+                    n_tree = torch.full(ids.shape[:3], n_tree_val, dtype=torch.int32, device=self.dev)
+                    K.seg_attn(q, Kb, Vb, tq, ids, vld, n_tree, st.shape.leaf, cfg.local, scale,
+                               out=out.transpose(1, 2))
+                    del ids, vld, n_tree
                 x = x + F.linear(out.view(nb, T0, C), L['c_proj'])
                 x = x + F.linear(F.gelu(F.linear(_ln(x, L['ln2']), L['c_fc'])), L['c_mlp'])
                 if cfg.global_pool:

@@ -130,13 +130,14 @@ def assemble(sel, tq, cfg, b, H):
     return cand, keep, used
 
 
-def select(q, k, lhat, cfg, shape=None):
-    """Whole-sequence selection (seg.py:122-140 / fastseg.py:302-314) on the device.
+def select(q, k, lhat, cfg, shape=None, levels=None):
+    """Whole-sequence selection (seg.py:122-140 / fastseg.py:302-314) on the device.  `levels`: node sums
+    already built for `shape` (a decode cache's), else they are built from k.
     Returns (sel dict, ids, vld, sct, levels)."""
     check_supported(cfg)
     b, H, T, dh = q.shape
     shape = shape or cfg_shape(cfg, T)
-    levels = build_pyramid(k, shape)
+    levels = build_pyramid(k, shape) if levels is None else levels
     tq = torch.arange(T, device=q.device)
     ids32, vld8, sct = K.tree_descend(q, levels, tq, shape, cfg.wmax)
     ids, vld = ids32.long(), vld8.bool()
