@@ -169,11 +169,13 @@ def test_engine_matches_forward(kw):
     assert (ref - got).abs().max().item() < 1e-4
 
 
-@pytest.mark.parametrize('kw', [dict(), dict(leaf=4, arity=4, wmax=3, beam=2)])
+@pytest.mark.parametrize('kw', [dict(), dict(leaf=4, arity=4, wmax=3, beam=2), dict(beam_mode='pred', global_pool=True),
+                                dict(beam_mode='pred', neighbors=False, leaf=8, wmax=4)])
 def test_prefill_with_neighbours_then_decode_matches_decode_from_scratch(kw):
-    """Reference-default mode (neighbour borrowing on): a batched prefill of the first 40 positions, which
-    seeds the neighbour store, then token-by-token decoding gives the logits of decoding every position
-    from an empty cache (the decode == prefill invariant), and the prefill's last logits equal the forward's."""
+    """Reference-default mode (neighbour borrowing on) and the budget head: a batched prefill of the first 40
+    positions, which seeds the neighbour store, then token-by-token decoding gives the logits of decoding
+    every position from an empty cache (the decode == prefill invariant), and the prefill's last logits equal
+    the forward's."""
     torch.manual_seed(6)
     cfg = tiny(**kw)
     model = GPT(cfg).to(DEV).eval()

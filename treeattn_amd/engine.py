@@ -173,6 +173,20 @@ def _pw_budget(state, pw, q, t):
     return pw['classes'].to(q.device)[F.linear(h, pw['w2'].float(), pw['b2'].float()).argmax(-1)]
 
 
+def _pw_budget_seq(cfg, H, pw, q, k):
+    """_pw_budget for every position of a prompt (q, k: (B,H,T,dh)): the same features, the global pool being
+    the mean of the keys before each position (what the decode cache's running sum holds at that step)."""
+    B, _, T, _ = q.shape
+    feats = [q.float(), torch.log(q.float().norm(dim=-1, keepdim=True) + 1e-6),
+             torch.eye(H, device=q.device).view(1, H, 1, H).expand(B, H, T, H)]
+    if cfg.global_pool:
+        kf = k.float()
+        tt = torch.arange(T, device=q.device).float().clamp(min=1).view(1, 1, T, 1)
+        feats.append((kf.cumsum(2) - kf) / tt)
+    h = F.relu(F.linear(torch.cat(feats, -1), pw['w1'].float(), pw['b1'].float()))
+    return pw['classes'].to(q.device)[F.linear(h, pw['w2'].float(), pw['b2'].float()).argmax(-1)]
+
+
 @torch.no_grad()
 def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     """One decode step of one layer for every sequence, without host synchronisation.
@@ -463,8 +477,6 @@ class Decoder:
         if B != self.B or T0 > self.Tcap:
             raise ValueError('prompt shape does not fit the decoder')
         cfg = self.cfg
-        if cfg.beam_mode == 'pred':
-            raise NotImplementedError('prefill with the budget head is not built yet')
         chunk = chunk or B
         tq = torch.arange(T0, device=self.dev, dtype=torch.int32)
         scale = 1.0 / math.sqrt(dh)
@@ -484,12 +496,15 @@ class Decoder:
                 lv = [t[b0:b1] for t in st.levels]
                 K.level_sums(Kb, st.shape.blevels, out=lv, t_end=T0, zero_sink=True)
                 out = torch.empty(nb, T0, H, dh, device=self.dev, dtype=v.dtype)
-                if cfg.neighbors:
-                    # the forward's selection with neighbour borrowing (fastseg.py:345-389), and the decode
-                    # store seeded with what decoding positions 0..T0-1 would have written (engine.py:103-105):
-                    # each position's top nb_store leaves of its own tree pass, which the selection's own
-                    # neighbour pass reads too
-                    lhat = torch.full((nb, H, T0), cfg.beam, dtype=torch.long, device=self.dev)
+                if cfg.neighbors or cfg.beam_mode == 'pred':
+                    # the forward's selection with neighbour borrowing and/or the budget head's per-query budget
+                    # (fastseg.py:345-389), and the decode store seeded with what decoding positions 0..T0-1
+                    # would have written (engine.py:103-105): each position's top nb_store leaves of its own tree
+                    # pass, which the selection's own neighbour pass reads too
+                    if cfg.beam_mode == 'pred':
+                        lhat = _pw_budget_seq(cfg, H, L['pw'], q, k)
+                    else:
+                        lhat = torch.full((nb, H, T0), cfg.beam, dtype=torch.long, device=self.dev)
                     sel, ids, vld, sct, _ = SEL.select(q, k, lhat, cfg, st.shape, lv)
                     n = min(cfg.nb_store, ids.shape[-1])
                     vb = vld[..., :n].bool()
