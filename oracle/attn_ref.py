@@ -140,9 +140,30 @@ def assemble(sel, tq, cfg, b, H):
     return cand, keep, used
 
 
+def budget_head(pw, q, k, cfg, classes):
+    """Per-query leaf budget of the module's budget head (fastseg.py:352-365): features [q, log(|q| + 1e-6),
+    one-hot head, (mean of the keys before the position when global_pool)] in q's dtype, the two-layer head
+    (Linear, ReLU, Linear) over them, argmax -> class.  pw: dict w1, b1, w2, b2 of the head's weights.
+    Returns (lhat (b,H,T) long, logits)."""
+    b, H, T, dh = q.shape
+    dt = q.dtype
+    qd = q.detach()
+    feats = [qd, torch.log(qd.float().norm(dim=-1, keepdim=True) + 1e-6).to(dt),
+             torch.eye(H, dtype=dt).view(1, H, 1, H).expand(b, H, T, H)]
+    if cfg.global_pool:
+        kd = k.detach().float()
+        before = kd.cumsum(2) - kd
+        feats.append((before / torch.arange(T).clamp(min=1).view(1, 1, T, 1).float()).to(dt))
+    x = torch.cat(feats, -1)
+    h = torch.relu(torch.nn.functional.linear(x, pw['w1'].to(dt), pw['b1'].to(dt)))
+    plog = torch.nn.functional.linear(h, pw['w2'].to(dt), pw['b2'].to(dt))
+    return torch.as_tensor(classes)[plog.argmax(-1)], plog
+
+
 def seg_sparse_attend(q, k, v, cfg, lhat=None, mode='faithful'):
-    """SegAttention.sparse_attend with a fixed budget (fastseg.py:345-389): selection, candidates,
-    de-duplication, exact attention over the kept keys, aux statistics.  Returns (out, aux, cand, keep)."""
+    """SegAttention.sparse_attend (fastseg.py:345-389) given the per-query budget lhat (b,H,T) (the fixed beam
+    when None; budget_head gives the learned one): selection, candidates, de-duplication, exact attention over
+    the kept keys, aux statistics.  Returns (out, aux, cand, keep)."""
     b, H, T, dh = q.shape
     scale = 1.0 / math.sqrt(dh)
     if lhat is None:

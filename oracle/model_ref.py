@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Restates model.py:12-93 (pre-LN blocks, bias-free
 linears, GELU MLP, learned positions, tied output layer, N(0, 0.02) init with the residual projections
-rescaled) with the attention module of fastseg.py:318-405 (fixed budget) computed by the oracle.
+rescaled) with the attention module of fastseg.py:318-405 (fixed budget, or the budget head of
+fastseg.py:330-335 / 352-365 when beam_mode='pred') computed by the oracle.
 Parameter names match the reference's state_dict so weights move between this model, the product's
 model and both decoders.
 """
@@ -12,7 +13,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .attn_ref import seg_sparse_attend
+from .attn_ref import budget_head, seg_sparse_attend
 
 
 class LayerNorm(nn.Module):
@@ -36,13 +37,21 @@ class SegAttentionRef(nn.Module):
         self.mode = mode
         self.c_attn = nn.Linear(C, 3 * C, bias=False)
         self.c_proj = nn.Linear(C, C, bias=False)
+        if cfg.beam_mode == 'pred':
+            # created after c_attn / c_proj, as fastseg.py:333-335, so the seeded init draws the same numbers
+            fin = self.dh + 1 + self.H + (self.dh if cfg.global_pool else 0)
+            self.pred = nn.Sequential(nn.Linear(fin, 64), nn.ReLU(), nn.Linear(64, len(cfg.beam_classes)))
         self.aux = {}
 
     def forward(self, x):
         b, T, C = x.shape
         q, k, v = self.c_attn(x).split(C, dim=2)
         q, k, v = [a.view(b, T, self.H, self.dh).transpose(1, 2) for a in (q, k, v)]
-        out, self.aux, _, _ = seg_sparse_attend(q, k, v, self.cfg, mode=self.mode)
+        lhat = None
+        if self.cfg.beam_mode == 'pred':
+            pw = dict(w1=self.pred[0].weight, b1=self.pred[0].bias, w2=self.pred[2].weight, b2=self.pred[2].bias)
+            lhat, _ = budget_head(pw, q, k, self.cfg, list(self.cfg.beam_classes))
+        out, self.aux, _, _ = seg_sparse_attend(q, k, v, self.cfg, lhat=lhat, mode=self.mode)
         return self.c_proj(out.transpose(1, 2).reshape(b, T, C))
 
 

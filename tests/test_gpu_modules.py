@@ -5,7 +5,7 @@ import math
 import pytest
 import torch
 
-from oracle.attn_ref import dense_causal, seg_sparse_attend
+from oracle.attn_ref import budget_head, dense_causal, seg_sparse_attend
 from oracle.engine_ref import DecoderRef
 from oracle.model_ref import GPTRef
 from treeattn_amd import fastseg, seg
@@ -44,8 +44,11 @@ def test_sparse_attend_matches_oracle(kw):
     q, k, v = [rnd(2, 2, 128, 64, seed=s) for s in (1, 2, 3)]
     lhat = None
     if cfg.beam_mode == 'pred':
-        lhat, _ = mod.budget(q.to(DEV), k.to(DEV))
-        lhat = lhat.cpu()
+        # the budget from the module's own head weights, computed by the oracle on the CPU (fastseg.py:352-365)
+        sd = {n: p.detach().cpu() for n, p in mod.state_dict().items()}
+        pw = dict(w1=sd['pred.0.weight'], b1=sd['pred.0.bias'], w2=sd['pred.2.weight'], b2=sd['pred.2.bias'])
+        lhat, _ = budget_head(pw, q, k, cfg, list(cfg.beam_classes))
+        assert len(set(lhat.reshape(-1).tolist())) > 1
     with torch.no_grad():
         got = mod.sparse_attend(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
     want, aux, _, _ = seg_sparse_attend(q, k, v, cfg, lhat=lhat, mode='canonical')
@@ -143,10 +146,8 @@ def test_model_matches_oracle(kw):
     model = GPT(cfg).eval()
     ref = GPTRef(cfg, 'canonical').eval()
     sd = model.state_dict()
-    ref.load_state_dict({k: v for k, v in sd.items() if 'pred' not in k}, strict=False)
+    ref.load_state_dict(sd)
     idx = torch.randint(0, 64, (2, 64))
-    if cfg.beam_mode == 'pred':
-        pytest.skip('the oracle model has the fixed budget only; the pred budget is covered by sparse_attend')
     with torch.no_grad():
         want = ref(idx)[0]
         got = model.to(DEV)(idx.to(DEV))[0].cpu()
@@ -261,6 +262,38 @@ def test_graph_replays_match_eager():
         tb = K.argmax_rows(lg)
         assert torch.equal(a.g_tok, tb), r
         assert int(a.g_t[0]) == 49 + r
+
+
+@pytest.mark.parametrize('kw', [dict(beam_mode='pred', global_pool=True),
+                                dict(beam_mode='pred', global_pool=True, neighbors=False, leaf=8, wmax=4)])
+def test_graph_replays_match_eager_budget_head(kw):
+    """The budget head with the global-pool feature (the running key sum over the cache) and neighbour
+    borrowing: replays of a captured step equal eager steps of a twin decoder, so the capture's warm-up
+    leaves the running key sum as it found it."""
+    cfg = tiny(seq_len=256, vocab_size=64, **kw)
+    torch.manual_seed(9)
+    model = GPT(cfg).to(DEV).eval()
+    W = weights_from_ours(model.state_dict(), cfg)
+    idx = torch.randint(0, 64, (2, 48)).to(DEV)
+    a = Decoder(W, 2, 2, 32, 256, 'seg', cfg, DEV, batch=2)
+    b = Decoder(W, 2, 2, 32, 256, 'seg', cfg, DEV, batch=2)
+    la, lb = a.prefill(idx), b.prefill(idx)
+    assert torch.equal(la, lb)
+    tok = la.float().argmax(-1)
+    a.capture(tok, 48)
+    for st_a, st_b in zip(a.states, b.states):
+        assert torch.equal(st_a.ksum, st_b.ksum)
+    tb = tok.clone()
+    for r in range(6):
+        a.replay()
+        torch.cuda.synchronize()
+        _ = torch.randn(1000, device=DEV).sum()   # unrelated eager work between replays
+        lg, _ = b.step(tb, 48 + r)
+        assert (a.g_logits.float() - lg.float()).abs().max().item() < 1e-5, r
+        tb = K.argmax_rows(lg)
+        assert torch.equal(a.g_tok, tb), r
+    for st_a, st_b in zip(a.states, b.states):
+        assert (st_a.ksum - st_b.ksum).abs().max().item() < 1e-5
 
 
 def test_fused_bf16_decode_matches_oracle_engine():

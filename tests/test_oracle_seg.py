@@ -283,3 +283,56 @@ def test_sparse_attn_bwd_closed_form_matches_autograd(D, KC, seed):
         assert (got.double() - want).abs().max().item() < 1e-4
     # the forward the closed form differentiates is the oracle's own
     assert (sparse_attn_ref(q.float(), k.float(), v.float(), cand, scale).double() - o.detach()).abs().max() < 1e-4
+
+
+# ------------------------------------------------------------------------------ leaf budget (seg.py:111-117)
+def n_tree_scalar(L, nL, wmax):
+    """The budget rule of seg.py:111-117, one query at a time in plain integers: neighbours that cover the
+    whole budget leave the tree nothing; otherwise the tree supplies what they do not cover, but at least two
+    leaves while the neighbours bring fewer than half the budget (2*nL < L, i.e. nL < ceil(L/2)) and at least
+    one otherwise; never more than wmax."""
+    if nL >= L:
+        return 0
+    least = 2 if 2 * nL < L else 1
+    return min(max(L - nL, least), wmax)
+
+
+def _finish_sweep(fn, wmax_list=(2, 4, 8), classes=(1, 2, 3, 4, 5, 6, 8)):
+    bad = []
+    for wmax in wmax_list:
+        for L in classes:
+            nLs = torch.arange(0, L + 3)
+            lhat = torch.full_like(nLs, L)
+            got = fn(nLs, lhat, wmax)
+            for nL, g in zip(nLs.tolist(), got.tolist()):
+                if g != n_tree_scalar(L, nL, wmax):
+                    bad.append((wmax, L, nL, g))
+    return bad
+
+
+def _oracle_n_tree(nL, lhat, wmax):
+    cfg = tiny(wmax=wmax)
+    z = torch.zeros(1, 1, nL.numel(), 1, dtype=torch.long)
+    sel = S.finish(z, z.bool(), z, z.bool(), nL.view(1, 1, -1), lhat.view(1, 1, -1), cfg, 2)
+    return sel['n_tree'].view(-1)
+
+
+def test_finish_budget_matches_scalar_rule():
+    """Oracle finish and the product's budget split against the scalar rule, nL in [0, L+2] for budgets
+    1..8 (the default beam_classes and beams) and wmax 2, 4, 8."""
+    from treeattn_amd.selection import budget_split
+    assert _finish_sweep(_oracle_n_tree) == []
+    assert _finish_sweep(lambda nL, L, w: budget_split(nL, L, w)) == []
+
+
+def test_planted_budget_mistake_is_caught(monkeypatch):
+    """nL <= ceil(L/2) in place of nL < ceil(L/2) (the floor of two leaves kept one step too long) must fail."""
+    def mutant(ids, vld, nid, match, nL, lhat, cfg, leaf=2):
+        L = lhat
+        half = (L + 1) // 2
+        need = (L - nL).clamp(min=0)
+        least = torch.where(nL <= half, torch.full_like(L, 2), torch.ones_like(L))
+        n_tree = torch.where(nL >= L, torch.zeros_like(L), torch.maximum(need, least)).clamp(max=cfg.wmax)
+        return dict(n_tree=n_tree)
+    monkeypatch.setattr(S, 'finish', mutant)
+    assert _finish_sweep(_oracle_n_tree) != []

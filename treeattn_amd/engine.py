@@ -9,7 +9,8 @@ and step(tok, t) -> (logits, keys), weights_from_ours / weights_from_nanogpt -- 
 * tree shape: cfg.leaf / cfg.arity (the reference is leaf=2, arity=2);
 * Decoder.prefill(idx) fills every layer's cache from a prompt in one pass (the forward of the model over
   the prompt, sparse attention included) and returns the last position's logits;
-* Decoder.greedy(n) decodes n tokens with the whole step captured in a HIP graph (no host syncs).
+* Decoder.capture(tok, t) captures one greedy step (logits, argmax token, position advance) in a HIP graph
+  and Decoder.replay() launches it: n replays decode n tokens with no host synchronisation.
 
 Per layer and token the HIP kernels are: beam descent over the node sums (positions < t), the cache
 append of position t with the formation of every node it completes, and the split-key attention over
@@ -563,17 +564,22 @@ class Decoder:
                     K.argmax_rows(lg_g, out=tok_g)
                     t_g.add_(1)
 
-            # Warm up on the capture stream (library handles, allocator).  The step at a fixed (token, position)
-            # is idempotent -- it rewrites the same cache row and recomputes the same nodes -- so running it here
-            # and again at the first replay leaves the cache as one step would.  The warm-up must not advance
-            # the token and position, so it runs the step without the argmax/advance tail.
+            # Warm up on the capture stream (library handles, allocator).  The cache writes of a step at a fixed
+            # (token, position) are idempotent -- it rewrites the same cache row, the same stored leaves and the
+            # same nodes -- so running it here and again at the first replay leaves them as one step would.  The
+            # running key sum (the budget head's global-pool feature) accumulates instead, so it is saved before
+            # the warm-up and put back after it.  The warm-up must not advance the token and position, so it
+            # runs the step without the argmax/advance tail.
             s.wait_stream(main)
             with torch.cuda.stream(s):
+                ksums = [st.ksum.clone() for st in self.states] if self.mode == 'seg' else []
                 for _ in range(2):
                     if grp is not None:
                         self._group_step(grp, tok_g, t_g, lg_g)
                     else:
                         self._forward_step(tok_g, t_g)
+                for st, ks in zip(self.states, ksums):
+                    st.ksum.copy_(ks)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s):
                 body()

@@ -85,7 +85,8 @@ def leaves_to_pos(ids, ok):
 
 
 def finish(ids, vld, nid, match, nL, lhat, cfg):
-    return SEL.finish(ids, vld, nid, match, nL, lhat, cfg, getattr(cfg, 'leaf', 2))
+    """seg.py:111-119 over the reference's leaf groups of 2 keys (the tree of every function here)."""
+    return SEL.finish(ids, vld, nid, match, nL, lhat, cfg, 2)
 
 
 @torch.no_grad()
