@@ -9,7 +9,7 @@ import math
 import torch
 import torch.nn.functional as F
 
-from .attn_ref import dedupe, local_block, static_keys
+from .attn_ref import dedupe, dedupe_fast, local_block, static_keys
 from .seg_ref import (Geometry, dot_canonical, finish, gate_apply, gather_nodes, injected, neighbor_pass,
                       rank_canonical, tree_pass)
 
@@ -128,7 +128,7 @@ def budget(state, pw, q, t):
 
 
 @torch.no_grad()
-def seg_attend_ref(state, pw, q, k, v, t, update=True, mode='faithful', want_sel=False):
+def seg_attend_ref(state, pw, q, k, v, t, update=True, mode='faithful', want_sel=False, sort_dedupe=False):
     """One decode step of one layer (engine.py:84-120): budget, descent over the cache (positions < t),
     neighbour pass over the stored leaves, budget split, store this query's leaves and add position t,
     candidate assembly with the static keys (and the own leaf block when leaf > 2), K x K de-duplication,
@@ -165,7 +165,8 @@ def seg_attend_ref(state, pw, q, k, v, t, update=True, mode='faithful', want_sel
     cand = torch.cat([sel['tree_pos'], sel['nb_pos'], extra], -1)
     used = sel['leaf_ok'] & (torch.arange(wl) < sel['n_tree'].unsqueeze(-1))
     tv = torch.cat([used] * leaf, -1) & (sel['tree_pos'] >= 0)
-    keep = dedupe(cand, torch.cat([tv, sel['nb_pos'] >= 0, extra >= 0], -1))
+    # the K x K comparison of engine.py:114, or the equal sort-based form (fastseg.py:227-234) for long lists
+    keep = (dedupe_fast if sort_dedupe else dedupe)(cand, torch.cat([tv, sel['nb_pos'] >= 0, extra >= 0], -1))
     idx = cand.clamp(min=0)
     kg, vg = gather_nodes(state.K, idx), gather_nodes(state.V, idx)
     s = (q.unsqueeze(3) * kg).sum(-1) * (1.0 / math.sqrt(dh))
@@ -197,34 +198,48 @@ class DecoderRef:
     bf16 activations and weights (the bf16 decode configurations); selection and attention stay fp32."""
 
     def __init__(self, W, n_layer, n_head, n_embd, Tcap, mode='seg', cfg=None, act_dtype=torch.float32,
-                 sel_mode='faithful'):
+                 sel_mode='faithful', linear=None, sort_dedupe=False):
         self.W, self.nl, self.H, self.C, self.Tcap = W, n_layer, n_head, n_embd, Tcap
         self.dh, self.mode, self.cfg = n_embd // n_head, mode, cfg
         self.dt = act_dtype
         self.sel_mode = sel_mode
+        # the matrix product of every linear layer (F.linear; another float32-accumulating product rounded to
+        # the activation dtype gives an equally valid bf16 result, which measures the rounding noise floor)
+        self.lin = linear or F.linear
+        self.sort_dedupe = sort_dedupe
         self.reset()
 
     def reset(self):
         self.states = [SegStateRef(self.cfg, self.Tcap, self.H, self.dh) for _ in range(self.nl)]
 
     @torch.no_grad()
-    def step(self, tok, t, want_sel=False):
-        """Feed token `tok` at position t -> (logits (V,) fp32, mean keys read per head and layer)."""
+    def step(self, tok, t, want_sel=False, probe=None):
+        """Feed token `tok` at position t -> (logits (V,) fp32, mean keys read per head and layer).
+        probe(i, values), when given, sees every layer's intermediate tensors (x_in, q, k, v, out, x_mid, h,
+        x_out) and finally probe('final', dict(x, logits)) -- for comparing another implementation op by op."""
         W, H, C, dh, dt = self.W, self.H, self.C, self.dh, self.dt
         x = (W['wte'][tok].to(dt) + W['wpe'][t].to(dt)).view(1, 1, C)
         keys = 0.0
         sels = []
         for i, L in enumerate(W['layers']):
-            q, k, v = F.linear(_ln(x, L['ln1'].to(dt)), L['c_attn'].to(dt)).split(C, -1)
+            x_in = x
+            q, k, v = self.lin(_ln(x, L['ln1'].to(dt)), L['c_attn'].to(dt)).split(C, -1)
             q, k, v = [a.view(1, 1, H, dh).transpose(1, 2) for a in (q, k, v)]
-            res = seg_attend_ref(self.states[i], L.get('pw'), q, k, v, t, mode=self.sel_mode, want_sel=want_sel)
+            res = seg_attend_ref(self.states[i], L.get('pw'), q, k, v, t, mode=self.sel_mode,
+                                 want_sel=want_sel or probe is not None, sort_dedupe=self.sort_dedupe)
             out, kr = res[0], res[1]
             if want_sel:
                 sels.append(res[2])
             keys += kr
-            x = x + F.linear(out.to(dt).transpose(1, 2).reshape(1, 1, C), L['c_proj'].to(dt))
-            x = x + F.linear(F.gelu(F.linear(_ln(x, L['ln2'].to(dt)), L['c_fc'].to(dt))), L['c_mlp'].to(dt))
-        logits = F.linear(_ln(x, W['ln_f'].to(dt)), W['wte'].to(dt))[0, 0].float()
+            x = x + self.lin(out.to(dt).transpose(1, 2).reshape(1, 1, C), L['c_proj'].to(dt))
+            x_mid = x
+            h = F.gelu(self.lin(_ln(x, L['ln2'].to(dt)), L['c_fc'].to(dt)))
+            x = x + self.lin(h, L['c_mlp'].to(dt))
+            if probe is not None:
+                probe(i, dict(x_in=x_in, q=q, k=k, v=v, out=out, x_mid=x_mid, h=h, x_out=x, sel=res[2]))
+        logits = self.lin(_ln(x, W['ln_f'].to(dt)), W['wte'].to(dt))[0, 0].float()
+        if probe is not None:
+            probe('final', dict(x=x, logits=logits))
         if want_sel:
             return logits, keys / self.nl, sels
         return logits, keys / self.nl

@@ -1,0 +1,310 @@
+"""Parity at the BASELINE configurations' own workloads (GPU).
+
+* config 1 -- 6L/384/6H GPT, vocab 256, fp32, seed 0, a 512-token prompt (seed 0) and 256 greedy steps:
+  at the reference's own tree (leaf groups of 2, binary, top-8) against the reference's logits and tokens
+  (tests/golden/decode_config1.npz, written by the reference engine itself), and at leaf 32 (the config)
+  against the oracle engine.  Bar: identical greedy tokens, logits within 1e-5.
+* config 3 -- one (1, 2, 16384, 128) bf16 slice with the config's low-rank keys, leaf 64, top-32: the
+  descent of every query bit-exact against the oracle's canonical order, every disagreement between the
+  canonical and the reference's torch order classified as a tie, and the matrix-core attention of the last
+  2048 queries of each head within 2e-2 of the oracle's.
+* config 4 -- the 12L/768/12H vocab-50304 bf16 model, leaf 64, top-32, 2 sequences with a 32768-token
+  context (Tcap 65536), 8 decode steps; config 5 -- the same model, leaf 128, 4-ary, top-64, 1 sequence with
+  a 65536-token context (Tcap 131072), 6 steps.  Against the oracle engine (engine.py:84-177, bf16
+  activations, canonical selection) from the same cache contents:
+    - teacher-forced, layer by layer (each GPU op fed the oracle's inputs): leaf ids bit-exact, every
+      intermediate (q/k/v, attention output, residual stream, MLP hidden) and the logits within 2e-2;
+    - free-running (each side feeding itself): the logit difference is compared with the noise floor of
+      the bf16 op chain itself -- the oracle against the same oracle whose linear layers accumulate in
+      another order -- and greedy tokens must agree wherever the oracle's top-two logits are further apart
+      than that difference.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attn_ref as A
+from oracle import seg_ref as S
+from oracle.engine_ref import DecoderRef, descend
+from oracle.ties import tie_report
+from treeattn_amd import engine as E
+from treeattn_amd import kernels as K
+from treeattn_amd.config import Config
+from treeattn_amd.engine import Decoder, weights_from_ours
+from treeattn_amd.model import GPT
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden')
+BF16_BAR = 2e-2
+FP32_BAR = 1e-5
+
+
+def _free():
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+# ------------------------------------------------------------------------------------------------ config 1
+def config1_cfg(leaf):
+    return Config(vocab_size=256, seq_len=1024, n_layer=6, n_head=6, n_embd=384, attn='seg', wmax=8, beam=8,
+                  beam_mode='fixed', local=3, neighbors=False, leaf=leaf, arity=2)
+
+
+def _config1_gpu(leaf, prompt, steps):
+    """Prefill + graph-captured greedy decode on the GPU; returns (logits (steps, 256), tokens (steps,))."""
+    cfg = config1_cfg(leaf)
+    torch.manual_seed(0)
+    model = GPT(cfg).eval()
+    sd = {k: v.detach() for k, v in model.state_dict().items()}
+    W = weights_from_ours({k: v.to(DEV) for k, v in sd.items()}, cfg)
+    dec = Decoder(W, 6, 6, 384, 1024, 'seg', cfg, DEV, batch=1, dtype=torch.float32)
+    T0 = prompt.shape[1]
+    lg = dec.prefill(prompt.to(DEV))
+    tok = K.argmax_rows(lg)
+    dec.capture(tok, T0)
+    logits = torch.empty(steps, 256, device=DEV)
+    toks = torch.empty(steps, dtype=torch.long, device=DEV)
+    logits[0], toks[0] = lg[0], tok[0]
+    for s in range(1, steps):
+        dec.replay()
+        logits[s], toks[s] = dec.g_logits[0], dec.g_tok[0]
+    return logits.cpu(), toks.cpu(), sd
+
+
+def test_config1_reference_tree_equals_reference():
+    """Config 1 at the reference's own tree (leaf groups of 2): the 256 greedy tokens and every step's logits
+    equal those of the reference engine (engine.py:149-177) run by the reference itself."""
+    g = np.load(os.path.join(GOLD, 'decode_config1.npz'), allow_pickle=False)
+    prompt = torch.from_numpy(g['prompt'].astype(np.int64))
+    want, want_tok = torch.from_numpy(g['logits']), torch.from_numpy(g['tokens'].astype(np.int64))
+    logits, toks, _ = _config1_gpu(2, prompt, want.shape[0])
+    err = (logits - want).abs().max().item()
+    print('config 1 leaf 2 vs the reference: max |dlogit| %.3g, tokens %d/%d' %
+          (err, int((toks == want_tok).sum()), toks.numel()), flush=True)
+    assert torch.equal(toks, want_tok)
+    assert err <= FP32_BAR
+    _free()
+
+
+def test_config1_matches_oracle_engine():
+    """Config 1 itself (leaf 32, top-8): 256 greedy tokens and logits against the oracle engine."""
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, 256, (1, 512), generator=g)
+    steps = 256
+    logits, toks, sd = _config1_gpu(32, prompt, steps)
+    cfg = config1_cfg(32)
+    from oracle.engine_ref import weights_from_ours as wref
+    ref = DecoderRef(wref(sd, cfg), 6, 6, 384, 1024, 'seg', cfg, sel_mode='canonical')
+    for t in range(511):
+        ref.step(int(prompt[0, t]), t)
+    lc, _ = ref.step(int(prompt[0, 511]), 511)
+    worst, same = 0.0, 0
+    for s in range(steps):
+        worst = max(worst, (lc - logits[s]).abs().max().item())
+        same += int(int(lc.argmax()) == int(toks[s]))
+        if s + 1 < steps:
+            lc, _ = ref.step(int(toks[s]), 512 + s)
+    print('config 1 leaf 32 vs the oracle: max |dlogit| %.3g, tokens %d/%d' % (worst, same, steps), flush=True)
+    assert same == steps
+    assert worst <= FP32_BAR
+    _free()
+
+
+# ------------------------------------------------------------------------------------------------ config 3
+def config3_slice(H, T, D, seed):
+    """Config 3's inputs (Q, V ~ N(0,1); K = 3 Z W_h + E, rank-8 component), for H heads of one sequence."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, H, T, D, generator=g)
+    v = torch.randn(1, H, T, D, generator=g)
+    z = torch.randn(1, H, T, 8, generator=g)
+    wh = torch.randn(H, 8, D, generator=g) / math.sqrt(8)
+    k = 3 * torch.matmul(z, wh.unsqueeze(0)) + torch.randn(1, H, T, D, generator=g)
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def test_config3_selection_and_attention():
+    H, T, D = 2, 16384, 128
+    cfg = Config(n_head=H, n_embd=H * D, seq_len=T, attn='seg', wmax=32, beam=32, beam_mode='fixed',
+                 neighbors=False, leaf=64, arity=2, local=3)
+    qc, kc, vc = config3_slice(H, T, D, 2)
+    q, k, v = qc.to(DEV), kc.to(DEV), vc.to(DEV)
+    shape = K.TreeShape(T, 64, 2)
+    levels = K.level_sums(k, shape.blevels)
+    tq = torch.arange(T, dtype=torch.int32, device=DEV)
+    ids, vld, _ = K.tree_descend(q, levels, tq, shape, cfg.wmax)
+    n_tree = torch.full((1, H, T), 32, dtype=torch.int32, device=DEV)
+    out, _, keys = K.seg_attn(q, k, v, tq, ids, vld, n_tree, 64, cfg.local, 1.0 / math.sqrt(D),
+                              keys=torch.empty(1, H, T, device=DEV))
+    gi, gv, out, keys = ids.long().cpu(), vld.bool().cpu(), out.float().cpu(), keys.cpu()
+    geom = S.Geometry(T, 64, 2)
+    pyr = S.pyramid(S.index_keys(kc), geom)
+    t_all = torch.arange(T)
+    ci, cv, _ = S.tree_pass_general(qc.float(), pyr, t_all, geom, cfg.wmax, 'canonical')
+    assert torch.equal(gv, cv)
+    assert torch.equal(torch.where(gv, gi, -1), torch.where(cv, ci, -1))
+    fi, fv, _ = S.tree_pass_general(qc.float(), pyr, t_all, geom, cfg.wmax, 'faithful')
+    for h in range(H):
+        r = tie_report(qc[0, h].float(), {j: pyr[j][0, h] for j in pyr}, t_all, geom, cfg.wmax,
+                       ci[0, h], cv[0, h], fi[0, h], fv[0, h])
+        print('config 3 head %d: %d of %d queries differ from the torch order, %d within 1 ulp, %d within the '
+              'rounding bound' % (h, r['diverged'], T, r['within_1ulp'], r['within_bound']), flush=True)
+        assert r['within_bound'] == r['diverged']
+    # attention of the last 2048 queries of each head against the oracle over the same kept keys
+    lhat = torch.full((1, H, T), 32, dtype=torch.long)
+    nid = torch.zeros(1, H, T, cfg.nb_window * cfg.nb_store, dtype=torch.long)
+    sel = S.finish(ci, cv, nid, torch.zeros_like(nid, dtype=torch.bool), torch.zeros(1, H, T, dtype=torch.long),
+                   lhat, cfg, 64)
+    cand, keep, _ = A.assemble(sel, t_all, cfg, 1, H)
+    assert torch.equal(keys, keep.sum(-1).float())
+    cm = torch.where(keep, cand, -1)
+    t0 = T - 2048
+    worst = 0.0
+    for a in range(t0, T, 256):
+        want = A.sparse_attn_ref(qc[:, :, a:a + 256], kc, vc, cm[:, :, a:a + 256], 1.0 / math.sqrt(D))
+        worst = max(worst, (out[:, :, a:a + 256] - want.float()).abs().max().item())
+    print('config 3 attention (last 2048 queries x %d heads) max |dout| %.3g' % (H, worst), flush=True)
+    assert worst <= BF16_BAR
+    _free()
+
+
+# ------------------------------------------------------------------------------------------------ configs 4, 5
+def _f32_then_round(x, w):
+    """A linear layer as a float32 product of the bf16 operands, rounded once to bf16 -- the same real
+    quantity as F.linear on bf16 tensors, accumulated in another order."""
+    return (x.float() @ w.float().t()).to(x.dtype)
+
+
+def _decode_parity(leaf, arity, topk, B, T0, Tcap, steps, ids_seed, sort_dedupe):
+    n_layer, H, C, V = 12, 12, 768, 50304
+    dh = C // H
+    cfg = Config(vocab_size=V, seq_len=Tcap, n_layer=n_layer, n_head=H, n_embd=C, attn='seg', wmax=topk,
+                 beam=topk, beam_mode='fixed', neighbors=False, leaf=leaf, arity=arity, local=3)
+    torch.manual_seed(3)
+    model = GPT(cfg)
+    sd = {k: v.detach().to(torch.bfloat16) for k, v in model.state_dict().items()}
+    del model
+    Wc = weights_from_ours(sd, cfg)
+    W = weights_from_ours({k: v.to(DEV) for k, v in sd.items()}, cfg)
+    g = torch.Generator().manual_seed(ids_seed)
+    idx = torch.randint(0, V, (B, T0), generator=g)
+    dec = Decoder(W, n_layer, H, C, Tcap, 'seg', cfg, DEV, batch=B, dtype=torch.bfloat16)
+    lg0 = dec.prefill(idx.to(DEV), chunk=1)
+    tok0 = K.argmax_rows(lg0).cpu()
+    refs = []
+    for b in range(B):
+        r = DecoderRef(Wc, n_layer, H, C, Tcap, 'seg', cfg, act_dtype=torch.bfloat16, sel_mode='canonical',
+                       sort_dedupe=sort_dedupe)
+        for i, st in enumerate(dec.states):
+            r.states[i].fill(st.K[b:b + 1].float().cpu(), st.V[b:b + 1].float().cpu())
+        refs.append(r)
+    sc = dec.groups[0]['scratch']
+    geom = refs[0].states[0].geom
+    to_dev = lambda ts: torch.cat(ts, 0).to(DEV)
+
+    # ---- teacher-forced: every GPU op is fed the oracle's inputs
+    err = dict(qkv=0.0, attn=0.0, x_mid=0.0, h=0.0, x_out=0.0, logits=0.0)
+    ties = dict(queries=0, diverged=0, within_1ulp=0, within_bound=0)
+    toks = [int(tok0[b]) for b in range(B)]
+    for s in range(steps):
+        t = T0 + s
+        probes = [dict() for _ in range(B)]
+        outs = []
+        for b in range(B):
+            lo, _ = refs[b].step(toks[b], t, probe=lambda i, d, pb=probes[b]: pb.__setitem__(i, d))
+            outs.append(lo)
+        tpos = torch.full((B,), t, dtype=torch.int32, device=DEV)
+        for i, L in enumerate(W['layers']):
+            P = [probes[b][i] for b in range(B)]
+            x_in = to_dev([p['x_in'].view(1, C) for p in P])
+            qkv = sc.mm(x_in, L['c_attn'], ln_w=L['ln1'])
+            want = torch.cat([torch.cat([p[n].transpose(1, 2).reshape(1, C) for n in ('q', 'k', 'v')], -1)
+                              for p in P], 0)
+            err['qkv'] = max(err['qkv'], (qkv.float().cpu() - want.float()).abs().max().item())
+            q, k_, v_ = (to_dev([p[n] for p in P]) for n in ('q', 'k', 'v'))
+            sc.keys = sc.keys_all[i]
+            out, _ = E.seg_attend_(dec.states[i], None, q, k_, v_, tpos, scratch=sc)
+            ids, vld = sc.ids.long().cpu(), sc.vld.bool().cpu()
+            for b, p in enumerate(P):
+                wi, wv = p['sel']['ids'], p['sel']['vld']
+                assert torch.equal(vld[b:b + 1], wv), (b, i, s)
+                assert torch.equal(torch.where(vld[b:b + 1], ids[b:b + 1], -1), torch.where(wv, wi, -1)), (b, i, s)
+                st = refs[b].states[i]
+                fi, fv, _ = descend(st, p['q'].float(), t, 'faithful')
+                for h in range(H):
+                    r = tie_report(p['q'][0, h].float(), {j: st.raw[l][0, h] for j, l in enumerate(geom.blevels)},
+                                   torch.tensor([t]), geom, topk, wi[0, h], wv[0, h], fi[0, h], fv[0, h])
+                    for key in ties:
+                        ties[key] += r[key]
+            out_o = to_dev([p['out'] for p in P])
+            err['attn'] = max(err['attn'], (out.float() - out_o).abs().max().item())
+            out_b = out_o.to(torch.bfloat16).view(B, C)
+            x_mid = sc.mm(out_b, L['c_proj'], epilogue='residual', residual=x_in.clone())
+            err['x_mid'] = max(err['x_mid'], (x_mid.float().cpu() - to_dev([p['x_mid'].view(1, C) for p in P]).float().cpu()).abs().max().item())
+            xm_o = to_dev([p['x_mid'].view(1, C) for p in P])
+            hmid = sc.mm(xm_o, L['c_fc'], ln_w=L['ln2'], epilogue='gelu')
+            h_o = to_dev([p['h'].view(1, -1) for p in P])
+            err['h'] = max(err['h'], (hmid.float() - h_o.float()).abs().max().item())
+            x_out = sc.mm(h_o, L['c_mlp'], epilogue='residual', residual=xm_o.clone())
+            err['x_out'] = max(err['x_out'], (x_out.float() - to_dev([p['x_out'].view(1, C) for p in P]).float()).abs().max().item())
+        x_f = to_dev([probes[b]['final']['x'].view(1, C) for b in range(B)])
+        lg = torch.empty(B, V, device=DEV, dtype=torch.bfloat16)
+        sc.logits(x_f, W['wte'], W['ln_f'], lg, None)
+        err['logits'] = max(err['logits'], (lg.float().cpu() - torch.stack(outs)).abs().max().item())
+        toks = [int(o.argmax()) for o in outs]
+    print('teacher-forced (leaf %d, arity %d, top-%d, %d x %d): %s' %
+          (leaf, arity, topk, B, T0, ', '.join('%s %.3g' % kv for kv in err.items())), flush=True)
+    print('selection vs the torch order: %s' % ties, flush=True)
+    assert ties['within_bound'] == ties['diverged']
+    for name, e in err.items():
+        assert e <= BF16_BAR, (name, e)
+
+    # ---- free-running from the same caches (positions T0.. are rewritten before they are read)
+    def run_oracles(lin, follow=None):
+        res = []
+        for b in range(B):
+            refs[b].lin = lin
+            tk, seq = int(tok0[b]), []
+            for s in range(steps):
+                lo, _ = refs[b].step(tk, T0 + s)
+                seq.append(lo)
+                tk = int((lo if follow is None else follow[s, b]).argmax())
+            res.append(torch.stack(seq))
+        refs[0].lin = F.linear
+        return torch.stack(res, 1)                                   # (steps, B, V)
+    want = run_oracles(F.linear)
+    floor_run = run_oracles(_f32_then_round, follow=want)
+    tk = tok0.to(DEV)
+    got = []
+    for s in range(steps):
+        lg, _ = dec.step(tk, T0 + s)
+        got.append(lg.float().cpu())
+        tk = K.argmax_rows(lg)
+        for b in range(B):    # follow the oracle's token so both sides see the same inputs
+            tk[b] = int(want[s, b].argmax())
+    got = torch.stack(got)
+    d_gpu = (got - want).abs().amax(-1)                               # (steps, B)
+    d_floor = (floor_run - want).abs().amax(-1)
+    top2 = want.topk(2, -1).values
+    gap = top2[..., 0] - top2[..., 1]
+    same = got.argmax(-1) == want.argmax(-1)
+    print('free-running max |dlogit| per step, GPU vs oracle: %s; oracle vs oracle (other accumulation order): %s'
+          % (['%.3g' % x for x in d_gpu.amax(1).tolist()], ['%.3g' % x for x in d_floor.amax(1).tolist()]),
+          flush=True)
+    bound = max(BF16_BAR, 2.0 * float(d_floor.max()))
+    assert float(d_gpu.max()) <= bound, (float(d_gpu.max()), bound)
+    assert bool((same | (gap <= 2 * d_gpu)).all())
+    del dec, refs
+    _free()
+
+
+def test_config4_decode_matches_oracle():
+    _decode_parity(leaf=64, arity=2, topk=32, B=2, T0=32768, Tcap=65536, steps=8, ids_seed=3, sort_dedupe=True)
+
+
+def test_config5_decode_matches_oracle():
+    _decode_parity(leaf=128, arity=4, topk=64, B=1, T0=65536, Tcap=131072, steps=6, ids_seed=4, sort_dedupe=True)
