@@ -189,6 +189,27 @@ int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                     int nsplit, float* ws, int64_t ws_bytes, void* stream);
 
 /*
+ * ta_seg_attn_fwd without a workspace argument: no counterpart in the reference (it has no workspaces).  For
+ * callers that cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  The split attention's scratch (ta_seg_attn_workspace_size(...) bytes: per-query
+ * counters and per-workgroup partials) lives in a fixed array of TA_SCRATCH_BYTES bytes that the library holds
+ * on every GPU it runs on until the process ends; a call needing more returns TA_ERR_WORKSPACE (use
+ * ta_seg_attn_fwd with a workspace then).  The call allocates nothing.  Every call on one GPU shares that GPU's
+ * array: calls that overlap in time on one GPU race and must be ordered (one stream).  Arguments and results as
+ * ta_seg_attn_fwd, bit for bit.
+ */
+#define TA_SCRATCH_BYTES (4 << 20)
+int ta_seg_attn_fwd_noalloc(const void* q, const void* k, const void* v, int dtype,
+                            int64_t qsb, int64_t qsh, int64_t qsn, int64_t ksb, int64_t ksh, int64_t kst,
+                            int64_t vsb, int64_t vsh, int64_t vst,
+                            int B, int H, int Nq, int D, int Tk,
+                            const int32_t* tq, int64_t tq_sb,
+                            const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl,
+                            int leaf, int local, float scale,
+                            void* out, int64_t osb, int64_t osh, int64_t osn, float* lse, float* keys,
+                            int nsplit, void* stream);
+
+/*
  * One decode step of one layer's attention in one launch (replaces seg_attend in the structural mode,
  * engine.py:84-120, with SegState.add, engine.py:41-55): per (sequence, head), the cache append of
  * k_new / v_new at row t = t_pos[b] (and the nodes it completes), the beam descent of q (B,H,1,D) at t, and the

@@ -77,6 +77,10 @@ SIGNATURES = {
                                 c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32,
                                 c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64,
                                 c_vp]),
+    'ta_seg_attn_fwd_noalloc': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                        c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp,
+                                        c_vp, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp,
+                                        c_i32, c_vp]),
     'ta_kv_append': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
                              c_i32, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32,
                              c_i32, c_vp]),

@@ -21,6 +21,7 @@ SOURCES = {
     'abi.hip': [],
     'select.hip': ['-ffp-contract=off'],
     'attend.hip': [],
+    'attend_static.hip': [],
     'attend_bwd.hip': [],
     'sample.hip': [],
     'gemm.hip': [],

@@ -220,10 +220,6 @@ extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, i
   return dispatch_attn(dtype, D, p, B, false, (hipStream_t)stream);
 }
 
-namespace {
-// workspace: per-query counters (rounded up to 256 bytes), then the partials
-int64_t attn_counter_bytes(int B, int H, int Nq) { return ((int64_t)B * H * Nq * 4 + 255) / 256 * 256; }
-}  // namespace
 
 extern "C" int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int nsplit) {
   const int gsplit = nsplit / kWavesPerBlock;

@@ -33,6 +33,10 @@ struct AttnParams {
 
 constexpr float kNegBig = -1e30f;
 
+// Split-attention workspace layout: per-query arrival counters (uint32, the region rounded up to 256 bytes),
+// then the per-workgroup partials.
+inline int64_t attn_counter_bytes(int B, int H, int Nq) { return ((int64_t)B * H * Nq * 4 + 255) / 256 * 256; }
+
 // Matrix-core prefill attention for the structural key lists (selected leaf blocks + own block + static
 // keys), one workgroup per 32 consecutive queries; TA_ERR_UNSUPPORTED when the shape does not fit it.
 int prefill_attn_mfma(const AttnParams& p, int B, int dtype, int D, hipStream_t st);

@@ -259,6 +259,26 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
     return out, lse, keys
 
 
+def seg_attn_noalloc(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out, lse=None, keys=None, nsplit=1):
+    """seg_attn through ta_seg_attn_fwd_noalloc: no workspace argument and nothing allocated by the call (the
+    split scratch is the library's fixed per-GPU array; `out` must be given).  Calls on one GPU must not
+    overlap in time.  Returns (out, lse, keys)."""
+    L.require_gpu(q, k, v, tq, ids, vld, out)
+    if not (q.dtype == k.dtype == v.dtype == out.dtype):
+        raise TypeError('q, k, v and out must share a dtype')
+    B, H, Nq, D = q.shape
+    if tq.dtype != torch.int32 or not tq.is_contiguous():
+        raise ValueError('seg_attn_noalloc: tq must be contiguous int32')
+    if n_tree is not None and (n_tree.dtype != torch.int32 or not n_tree.is_contiguous()):
+        raise ValueError('seg_attn_noalloc: n_tree must be contiguous int32')
+    tq_sb = 0 if tq.dim() == 1 else tq.stride(0)
+    L.call('ta_seg_attn_fwd_noalloc', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k),
+           *L.rows3(v), B, H, Nq, D, k.shape[2], L.ptr(tq), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(n_tree),
+           ids.shape[-1], int(leaf), int(local), float(scale), L.ptr(out), out.stride(0), out.stride(1),
+           out.stride(2), L.ptr(lse), L.ptr(keys), int(nsplit), L.stream())
+    return out, lse, keys
+
+
 # ----------------------------------------------------------------------------------------------- row-block GEMM
 _EPI = {None: 0, 'gelu': 1, 'residual': 2}
 
