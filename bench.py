@@ -53,6 +53,8 @@ def parse():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--no-gather-dot', action='store_true', help='skip the isolated gather-dot leg')
     ap.add_argument('--kernel-iters', type=int, default=50)
+    ap.add_argument('--kv-layout', choices=('paged', 'contiguous'), default='paged',
+                    help='decode cache in pages of one leaf block per (sequence, head), or contiguous per sequence')
     ap.add_argument('--groups', type=int, default=None,
                     help='independent sequence groups, each captured and replayed on its own stream')
     args = ap.parse_args()
@@ -156,7 +158,9 @@ def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64):
     ref = DecoderRef(Wc, args.layers, args.heads, args.embd, args.tcap, 'seg', cfg, act_dtype=torch.bfloat16,
                      sel_mode='faithful')
     for i, st in enumerate(dec.states):
-        ref.states[i].fill(st.K[0:1].float().cpu(), st.V[0:1].float().cpu())
+        k0, v0 = st.dense_kv(0)
+        ref.states[i].fill(k0.float().cpu(), v0.float().cpu())
+        del k0, v0
     tok = int(tok_now[0])
     t = int(t_now)
     # GPU: decode the same steps eagerly for the parity check of sequence 0
@@ -221,8 +225,16 @@ def decode_bench(args):
     W = build_model(cfg, 3, torch.bfloat16)
     g = torch.Generator().manual_seed(args.ids_seed)
     idx = torch.randint(0, args.vocab, (B, T0), generator=g)
+    # pages for the positions this run reaches: the context, the warm-up and timed steps, the CPU leg's steps
+    # (at most 64) and the capture's reserve (pages are handed out reserve_ahead positions at a time)
+    reserve_ahead = 64
+    max_tokens = T0 + args.warmup + args.steps + 64 + 2 * reserve_ahead
     dec = Decoder(W, args.layers, H, C, Tcap, 'seg', cfg, 'cuda', batch=B, dtype=torch.bfloat16,
-                  groups=args.groups)
+                  groups=args.groups, max_tokens=max_tokens, reserve_ahead=reserve_ahead,
+                  paged=args.kv_layout == 'paged')
+    kv_bytes = sum(p.numel() * p.element_size() for p in dec.pool.pools) if dec.pool is not None else \
+        sum(st.K.numel() * st.K.element_size() * 2 for st in dec.states)
+    log('KV cache: %.2f GB (%s)' % (kv_bytes / 1e9, 'pages' if dec.pool is not None else 'contiguous'))
     log('prefill %d x %d tokens' % (B, T0))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -261,21 +273,21 @@ def decode_bench(args):
 
     # the one-launch layer attention re-appends row t_last with the values it already holds, so timing it
     # repeatedly leaves the caches and node sums as they are
-    k_row = st.K[:, :, t_last].clone()
-    v_row = st.V[:, :, t_last].clone()
+    k_row, v_row = st.row(t_last)
+    Kc, Vc = st.kv()
     out2 = torch.empty_like(out)
     keys2 = torch.empty_like(keys)
     fused = sc.nsplit == 4   # the engine's choice (one workgroup per query)
 
     def attn():
-        K.seg_attn(q, st.K, st.V, tpos.view(B, 1), ids, vld, n_tree, sh.leaf, cfg.local, 1.0 / math.sqrt(dh),
+        K.seg_attn(q, Kc, Vc, tpos.view(B, 1), ids, vld, n_tree, sh.leaf, cfg.local, 1.0 / math.sqrt(dh),
                    out=out, keys=keys, nsplit=sc.nsplit, ws=sc.ws)
 
     def descend():
         K.tree_descend(q, st.levels, tpos.view(B, 1), sh, cfg.wmax, out=(sc.ids, sc.vld, sc.sct))
 
     def attend():
-        K.seg_attend(q, st.levels, tpos, sh, cfg.wmax, k_row, v_row, st.K, st.V, n_tree, cfg.local,
+        K.seg_attend(q, st.levels, tpos, sh, cfg.wmax, k_row, v_row, Kc, Vc, n_tree, cfg.local,
                      1.0 / math.sqrt(dh), (sc.ids, sc.vld, sc.sct), out2, keys=keys2)
 
     for _ in range(3):
@@ -320,7 +332,9 @@ def decode_bench(args):
                                '%d-token prefilled context, greedy decode, leaf %d, arity %d, top-k %d, Tcap %d'
                                % (args.config, B, T0, args.leaf, args.arity, args.topk, Tcap),
                    'batch': B, 'context': T0, 'leaf': args.leaf, 'arity': args.arity, 'topk': args.topk,
-                   'tcap': Tcap, 'prefill_s': round(prefill_s, 2)},
+                   'tcap': Tcap, 'prefill_s': round(prefill_s, 2), 'kv_cache_GB': round(kv_bytes / 1e9, 2),
+                   'kv_layout': 'pages of one leaf block per (sequence, head)' if dec.pool is not None else
+                                'contiguous'},
         'roofline': {'bound': 'hbm', 'kernel': 'attn_kernel<bf16_t, 64, true, false> (split decode attention, '
                                                'one layer)',
                      'achieved': round(attn_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TA_ABI_VERSION 1
+#define TA_ABI_VERSION 2
 
 enum ta_dtype { TA_F32 = 0, TA_F16 = 1, TA_BF16 = 2 };
 
@@ -44,6 +44,23 @@ const char* ta_last_error(void);
 
 /* 1 when the current HIP device is a gfx950 the library has code for, 0 otherwise. */
 int ta_device_supported(void);
+
+/*
+ * Paged decode cache (replaces the contiguous per-layer K/V of engine.py:26-27, SegState; no counterpart for
+ * the layout itself in the reference).  A page holds the rows of one leaf block of one (sequence, head): with
+ * pages, row r (r < 2^block_log2) of leaf block j of (b, h) lives at
+ *   K: Kc + table[b*sb + h*sh + j] * page_stride + r * cst,   V: Vc + (same page) * page_stride + r * cst,
+ * so Kc / Vc are the bases of page 0's K and V rows and the per-sequence and per-head cache strides are not
+ * used.  A page id outside [0, num_pages) means "no page": such rows are never read and never written.
+ * Entry points taking `const ta_kv_pages* pages` use the contiguous layout when it is NULL.
+ */
+typedef struct ta_kv_pages {
+  const int32_t* table;   /* device memory, int32 page ids */
+  int64_t sb, sh;         /* element strides of the table for sequence and head */
+  int64_t page_stride;    /* elements from one page to the next (K and V alike) */
+  int64_t num_pages;
+  int block_log2;         /* rows per page = 2^block_log2 = the leaf block of the tree */
+} ta_kv_pages;
 
 /*
  * Level-sum pyramid of a key tensor (replaces seg.py:26-41 level_sums, fastseg.py:238-251 level_sums_min
@@ -100,7 +117,7 @@ int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int64_t qsh, i
                            int32_t* ids, uint8_t* vld, float* sct,
                            const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
                            int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
-                           void* stream);
+                           const ta_kv_pages* pages, void* stream);
 
 /*
  * Scores of queries against gathered rows (replaces fastseg.py:118-130 gather_dot and its kernel
@@ -139,7 +156,7 @@ int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                        int64_t qsb, int64_t qsh, int64_t qst, int64_t ksb, int64_t ksh, int64_t kst,
                        int64_t vsb, int64_t vsh, int64_t vst,
                        const int32_t* cand, int B, int H, int T, int Tk, int KC, int D, float scale,
-                       void* out, float* lse, void* stream);
+                       void* out, float* lse, const ta_kv_pages* pages, void* stream);
 
 /*
  * Backward of ta_sparse_attn_fwd (replaces fastseg.py:81-110 _attn_bwd and fastseg.py:158-170
@@ -186,7 +203,7 @@ int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                     const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl,
                     int leaf, int local, float scale,
                     void* out, int64_t osb, int64_t osh, int64_t osn, float* lse, float* keys,
-                    int nsplit, float* ws, int64_t ws_bytes, void* stream);
+                    int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages, void* stream);
 
 /*
  * ta_seg_attn_fwd without a workspace argument: no counterpart in the reference (it has no workspaces).  For
@@ -207,7 +224,7 @@ int ta_seg_attn_fwd_noalloc(const void* q, const void* k, const void* v, int dty
                             const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl,
                             int leaf, int local, float scale,
                             void* out, int64_t osb, int64_t osh, int64_t osn, float* lse, float* keys,
-                            int nsplit, void* stream);
+                            int nsplit, const ta_kv_pages* pages, void* stream);
 
 /*
  * One decode step of one layer's attention in one launch (replaces seg_attend in the structural mode,
@@ -226,7 +243,7 @@ int ta_seg_attend(const void* q, const void* k_new, const void* v_new, int dtype
                   void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
                   const int32_t* n_tree, int local, float scale,
                   int32_t* ids, uint8_t* vld, float* sct, void* out, int64_t osb, int64_t osh, float* keys,
-                  void* stream);
+                  const ta_kv_pages* pages, void* stream);
 
 /*
  * Decode-cache append with incremental node formation (replaces engine.py:41-55 SegState.add and the
@@ -240,7 +257,7 @@ int ta_kv_append(const void* k_new, const void* v_new, int dtype,
                  void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst,
                  int B, int H, int D, int Tcap, const int32_t* t_pos,
                  int n_levels, float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh,
-                 int leaf_log2, int arity_log2, void* stream);
+                 int leaf_log2, int arity_log2, const ta_kv_pages* pages, void* stream);
 
 /*
  * Row-block matrix product of the decode step (the model around the attention: model.py:21-44,

@@ -200,7 +200,9 @@ def _decode_parity(leaf, arity, topk, B, T0, Tcap, steps, ids_seed, sort_dedupe)
         r = DecoderRef(Wc, n_layer, H, C, Tcap, 'seg', cfg, act_dtype=torch.bfloat16, sel_mode='canonical',
                        sort_dedupe=sort_dedupe)
         for i, st in enumerate(dec.states):
-            r.states[i].fill(st.K[b:b + 1].float().cpu(), st.V[b:b + 1].float().cpu())
+            kb, vb = st.dense_kv(b)
+            r.states[i].fill(kb.float().cpu(), vb.float().cpu())
+            del kb, vb
         refs.append(r)
     sc = dec.groups[0]['scratch']
     geom = refs[0].states[0].geom

@@ -35,7 +35,10 @@ def _pair(cfg, W, B, prompt):
 
 def _same_state(a, b):
     for sa, sb in zip(a.states, b.states):
-        assert torch.equal(sa.K, sb.K) and torch.equal(sa.V, sb.V)
+        for s in range(a.B):   # a keeps its cache in pages, b (the one-launch step) contiguous
+            ka, va = sa.dense_kv(s)
+            kb, vb = sb.dense_kv(s)
+            assert torch.equal(ka, kb) and torch.equal(va, vb)
         for la, lb in zip(sa.levels, sb.levels):
             assert torch.equal(la, lb)
 

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for n in declared_functions():
         assert hasattr(L, n), n
     assert set(_lib.SIGNATURES) == set(declared_functions())
-    assert L.ta_abi_version() == 1
+    assert L.ta_abi_version() == 2
 
 
 def test_library_rejects_bad_arguments_without_gpu():
@@ -45,8 +45,9 @@ def test_library_rejects_bad_arguments_without_gpu():
     assert rc == 1
     assert b'bad sizes' in L.ta_last_error()
     rc = L.ta_seg_attn_fwd(None, None, None, 2, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 64, 64, None, 0, None, None, None, 4,
-                           64, 200, 0.1, None, 0, 0, 0, None, None, 1, None, 0, None)
+                           64, 200, 0.1, None, 0, 0, 0, None, None, 1, None, 0, None, None)
     assert rc == 2
+    assert b'local window' in L.ta_last_error()
 
 
 def test_product_refuses_cpu_tensors():

@@ -22,6 +22,12 @@ _P = ctypes.POINTER
 MAX_TREE_LEVELS = 32
 
 
+class KvPages(ctypes.Structure):
+    """ta_kv_pages"""
+    _fields_ = [('table', c_vp), ('sb', c_i64), ('sh', c_i64), ('page_stride', c_i64), ('num_pages', c_i64),
+                ('block_log2', c_i32)]
+
+
 class StepLayer(ctypes.Structure):
     """ta_step_layer"""
     _fields_ = [('ln1', c_vp), ('c_attn', c_vp), ('c_proj', c_vp), ('ln2', c_vp), ('c_fc', c_vp), ('c_mlp', c_vp),
@@ -58,32 +64,32 @@ SIGNATURES = {
     'ta_tree_descend_append': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp),
                                        _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp,
                                        c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
-                                       c_i32, c_vp]),
+                                       c_i32, _P(KvPages), c_vp]),
     'ta_seg_attend': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32,
                               c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32,
                               c_vp, c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_i32, c_f32, c_vp, c_vp, c_vp, c_vp,
-                              c_i64, c_i64, c_vp, c_vp]),
+                              c_i64, c_i64, c_vp, _P(KvPages), c_vp]),
     'ta_gather_dot': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i32, c_i64, c_i64, c_i64, c_vp,
                               c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_vp]),
     'ta_gather_dot_blocks': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp,
                                      c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_vp]),
     'ta_sparse_attn_fwd': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                    c_i64, c_i64, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp,
-                                   c_vp, c_vp]),
+                                   c_vp, _P(KvPages), c_vp]),
     'ta_sparse_attn_bwd': (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i32] + [c_i64] * 15 + [c_vp, c_vp] + [c_i32] * 6
                            + [c_f32, c_vp, c_vp, c_vp, c_vp]),
     'ta_seg_attn_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     'ta_seg_attn_fwd': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                 c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32,
                                 c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64,
-                                c_vp]),
+                                _P(KvPages), c_vp]),
     'ta_seg_attn_fwd_noalloc': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                         c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp,
                                         c_vp, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp,
-                                        c_i32, c_vp]),
+                                        c_i32, _P(KvPages), c_vp]),
     'ta_kv_append': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
                              c_i32, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32,
-                             c_i32, c_vp]),
+                             c_i32, _P(KvPages), c_vp]),
     'ta_argmax_rows': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_vp]),
     'ta_embed': (c_i32, [c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_i64, c_i32, c_i32, c_i32, c_i64, c_i64, c_vp,
                          c_i64, c_vp, c_vp, c_f32, c_vp, c_i64, c_vp]),

@@ -78,19 +78,33 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void seg_attend_kernel(Attn
   float* csc = reinterpret_cast<float*>(cid + cmax4);
   int32_t* kid = cid + 2 * cmax4;
   float* ksc = reinterpret_cast<float*>(kid + wmax4);
-  float* stk = ksc + wmax4;           // the append's carry stack, 16 * D
-  float* att = stk + 16 * D;          // the attention's LDS
+  int32_t* kpg = reinterpret_cast<int32_t*>(ksc + wmax4);   // pages of the kept leaves (paged caches)
+  int32_t* cpg = kpg + wmax4;                                // pages of the leaf-level candidates
+  int32_t* s_pre = cpg + ((cmax4 + 63) & ~63);               // pages of the static keys' blocks [32]
+  float* stk = reinterpret_cast<float*>(s_pre + 32);         // the append's carry stack, 16 * D
+  float* att = stk + 16 * D;                                 // the attention's LDS
 
   const int t = p.tq[b];
-  if (tid < D && t >= 0 && t < ap.Tcap)
+  // paged caches: the pages of the static keys' blocks are requested now and stored after the descent, so
+  // neither they nor the kept leaves' pages (read by the descent with the node rows) cost a round trip later
+  const int32_t* ptrow = p.ptab ? p.ptab + b * p.pt_sb + h * p.pt_sh : nullptr;
+  int pre = -1;
+  if (ptrow != nullptr && tid <= p.Lw && t >= 0 && t < p.Tk) {
+    const int pos = tid == 0 ? 0 : t - (tid - 1);
+    if (pos >= 0) pre = ptrow[pos >> p.leaf_log2];
+  }
+  if (tid < D && t >= 0 && t < ap.Tcap) {
+    T *kbase, *vbase;
+    const KvRows rows = append_rows<T>(ap, b, h, lv.blevel[0], kbase, vbase);
     append_dim<T>(tid, D, t, reinterpret_cast<const T*>(ap.kn) + b * ap.nsb + h * ap.nsh,
-                  reinterpret_cast<const T*>(ap.vn) + b * ap.vnsb + h * ap.vnsh,
-                  reinterpret_cast<T*>(ap.Kc) + b * ap.csb + h * ap.csh,
-                  reinterpret_cast<T*>(ap.Vc) + b * ap.csb + h * ap.csh, ap.cst, n_levels, lv.blevel[0], arity_log2,
-                  stk, [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
+                  reinterpret_cast<const T*>(ap.vn) + b * ap.vnsb + h * ap.vnsh, kbase, vbase, rows, n_levels,
+                  lv.blevel[0], arity_log2, stk,
+                  [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
+  }
   const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh;
   int nk = descend_query<T, D, kWavesPerBlock>(qrow, t, Tgeo, b, h, lv, n_levels, arity_log2, wmax, tid, ckey, cid,
-                                               csc, kid, ksc);
+                                               csc, kid, ksc, ptrow, cpg, kpg);
+  if (ptrow != nullptr && tid < 32) s_pre[tid] = pre;
   const int nkw = nk < p.wl ? nk : p.wl;   // the attention of the separate kernels sees the first wl of them
   // the appended row is visible to every wavefront: its stores (long since done) are waited for, then the
   // barrier; the selection's outputs are written after the attention, so that no wait here covers them
@@ -98,7 +112,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void seg_attend_kernel(Attn
   __syncthreads();
   const int nt = p.n_tree ? p.n_tree[bh] : p.wl;
   T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh;
-  attn_query<T, D, true, false>(p, 0, 0, b, h, bh, qrow, t, kid, nullptr, nkw, nt, orow, att);
+  attn_query<T, D, true, false>(p, 0, 0, b, h, bh, qrow, t, kid, nullptr, nkw, nt, orow, att, kpg, s_pre);
   const int64_t obase = (int64_t)bh * p.wl;   // kid and ksc are not written by the attention
   for (int r = tid; r < p.wl; r += NT) {
     const bool ok = r < nk;
@@ -117,22 +131,20 @@ struct LevelRW {
 
 // One thread per dimension of one (sequence, head): append_dim.
 template <typename T>
-__global__ __launch_bounds__(256) void kv_append_kernel(const T* __restrict__ kn, const T* __restrict__ vn,
-                                                        int64_t nsb, int64_t nsh, int64_t vnsb, int64_t vnsh,
-                                                        T* __restrict__ Kc, T* __restrict__ Vc, int64_t csb,
-                                                        int64_t csh, int64_t cst, int H, int D, int Tcap,
-                                                        const int32_t* __restrict__ t_pos, LevelRW lv, int n_levels,
-                                                        int leaf_log2, int arity_log2) {
+__global__ __launch_bounds__(256) void kv_append_kernel(AppendIn ap, int H, int D, const int32_t* __restrict__ t_pos,
+                                                        LevelRW lv, int n_levels, int leaf_log2, int arity_log2) {
   extern __shared__ float stk[];  // [16][D]
   const int d = threadIdx.x;
   if (d >= D) return;
   const int bh = blockIdx.x;
   const int b = bh / H, h = bh % H;
   const int t = t_pos[b];
-  if (t < 0 || t >= Tcap) return;
-  append_dim<T>(d, D, t, kn + b * nsb + h * nsh, vn + b * vnsb + h * vnsh, Kc + b * csb + h * csh,
-                Vc + b * csb + h * csh, cst, n_levels, leaf_log2, arity_log2, stk,
-                [&](int j) { return lv.ptr[j] + b * lv.sb[j] + h * lv.sh[j]; });
+  if (t < 0 || t >= ap.Tcap) return;
+  T *kbase, *vbase;
+  const KvRows rows = append_rows<T>(ap, b, h, leaf_log2, kbase, vbase);
+  append_dim<T>(d, D, t, reinterpret_cast<const T*>(ap.kn) + b * ap.nsb + h * ap.nsh,
+                reinterpret_cast<const T*>(ap.vn) + b * ap.vnsb + h * ap.vnsh, kbase, vbase, rows, n_levels,
+                leaf_log2, arity_log2, stk, [&](int j) { return lv.ptr[j] + b * lv.sb[j] + h * lv.sh[j]; });
 }
 
 // ----------------------------------------------------------------------------------------- host side
@@ -154,7 +166,7 @@ bool kv_aligned(const void* p, int dt, int D, std::initializer_list<int64_t> str
 template <typename T, int D>
 int launch_attn(const AttnParams& p, int B, bool split, hipStream_t st) {
   const int wl_pad = p.cand ? 0 : ((p.wl + 3) & ~3);
-  size_t lds = (size_t)kWavesPerBlock * (wl_pad + kWave) * sizeof(float);
+  size_t lds = (size_t)kWavesPerBlock * attn_wave_ints(wl_pad) * sizeof(float);
   const dim3 blk(kWavesPerBlock * kWave);
   if (split) {
     lds += (size_t)kWavesPerBlock * (D + 2) * sizeof(float);
@@ -187,6 +199,38 @@ int dispatch_attn(int dt, int D, const AttnParams& p, int B, bool split, hipStre
 #undef TA_CASE_D
 }
 
+// Paged K/V for the attention: checks the description against the leaf block and the row layout, and sets
+// p (p.k / p.v stay the bases of page 0's rows; the per-sequence and per-head strides are zeroed).
+int set_attn_pages(AttnParams& p, const ta_kv_pages* pages, int dt, int D, int leaf_log2, const char* who) {
+  if (pages == nullptr) return TA_OK;
+  // rows of K and V share one row index (page * rows-per-page + row in the page), an int32
+  if (pages->table == nullptr || pages->num_pages <= 0 || pages->block_log2 != leaf_log2 || pages->page_stride <= 0 ||
+      (pages->page_stride * elem_size(dt)) % 16 || p.kst < D || p.kst != p.vst || pages->page_stride % p.kst ||
+      ((int64_t)p.kst << leaf_log2) > pages->page_stride ||
+      pages->num_pages * (pages->page_stride / p.kst) > 0x7fffffffLL) {
+    set_error(std::string(who) + ": bad page description (block must be the leaf block, pages 16-byte aligned, a "
+                                 "whole number of rows and large enough for a block of rows, K and V rows alike, "
+                                 "fewer than 2^31 rows in all)");
+    return TA_ERR_ARG;
+  }
+  p.ptab = pages->table;
+  p.pt_sb = pages->sb;
+  p.pt_sh = pages->sh;
+  p.kps = p.vps = pages->page_stride;
+  p.npages = pages->num_pages;
+  p.ksb = p.ksh = p.vsb = p.vsh = 0;
+  return TA_OK;
+}
+
+void set_append_pages(AppendIn& ap, const ta_kv_pages* pages) {
+  if (pages == nullptr) return;
+  ap.ptab = pages->table;
+  ap.pt_sb = pages->sb;
+  ap.pt_sh = pages->sh;
+  ap.pstride = pages->page_stride;
+  ap.npages = pages->num_pages;
+}
+
 }  // namespace
 }  // namespace ta
 
@@ -195,7 +239,7 @@ using namespace ta;
 extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
                                   int64_t qst, int64_t ksb, int64_t ksh, int64_t kst, int64_t vsb, int64_t vsh,
                                   int64_t vst, const int32_t* cand, int B, int H, int T, int Tk, int KC, int D,
-                                  float scale, void* out, float* lse, void* stream) {
+                                  float scale, void* out, float* lse, const ta_kv_pages* pages, void* stream) {
   if (B <= 0 || H <= 0 || T < 0 || Tk < 0 || KC < 0) {
     set_error("ta_sparse_attn_fwd: bad sizes");
     return TA_ERR_ARG;
@@ -212,11 +256,17 @@ extern "C" int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, i
   p.v = v; p.vsb = vsb; p.vsh = vsh; p.vst = vst;
   p.H = H; p.Nq = T; p.Tk = Tk;
   p.cand = cand; p.KC = KC;
-  p.leaf_log2 = 1;
+  p.leaf_log2 = pages ? pages->block_log2 : 1;   // dense: rows addressed as pairs of rows, row stride kst
   p.scale = scale;
   p.gsplit = 1;
   p.out = out; p.osb = (int64_t)H * T * D; p.osh = (int64_t)T * D; p.osn = D;
   p.lse = lse;
+  if (pages && (pages->block_log2 < 1 || pages->block_log2 > 14)) {
+    set_error("ta_sparse_attn_fwd: bad page block");
+    return TA_ERR_ARG;
+  }
+  const int prc = set_attn_pages(p, pages, dtype, D, p.leaf_log2, "ta_sparse_attn_fwd");
+  if (prc != TA_OK) return prc;
   return dispatch_attn(dtype, D, p, B, false, (hipStream_t)stream);
 }
 
@@ -232,15 +282,16 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
                                int64_t vst, int B, int H, int Nq, int D, int Tk, const int32_t* tq, int64_t tq_sb,
                                const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl, int leaf,
                                int local, float scale, void* out, int64_t osb, int64_t osh, int64_t osn, float* lse,
-                               float* keys, int nsplit, float* ws, int64_t ws_bytes, void* stream) {
+                               float* keys, int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages,
+                               void* stream) {
   if (B <= 0 || H <= 0 || Nq < 0 || wl < 0 || nsplit < 1 || leaf < 2 || (leaf & (leaf - 1)) ||
       (nsplit > 1 && nsplit % kWavesPerBlock) || nsplit > kWavesPerBlock * kWave) {
     set_error("ta_seg_attn_fwd: bad sizes (nsplit must be 1 or a multiple of 4, at most 256)");
     return TA_ERR_ARG;
   }
   const int Lw = local > 3 ? local : 3;
-  if (Lw + 1 > kWave) {
-    set_error("ta_seg_attn_fwd: local window must be < 64");
+  if (Lw + 1 > 32) {
+    set_error("ta_seg_attn_fwd: local window must be < 32");
     return TA_ERR_UNSUPPORTED;
   }
   if (wl > 1024) {
@@ -277,7 +328,9 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
     p.cnt = reinterpret_cast<uint32_t*>(ws);
     p.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + attn_counter_bytes(B, H, Nq));
   }
-  if (nsplit == 1) {
+  const int prc = set_attn_pages(p, pages, dtype, D, ll, "ta_seg_attn_fwd");
+  if (prc != TA_OK) return prc;
+  if (nsplit == 1 && pages == nullptr) {
     // many queries (prefill): the matrix-core kernel when the shape fits it
     const int rc = prefill_attn_mfma(p, B, dtype, D, (hipStream_t)stream);
     if (rc != TA_ERR_UNSUPPORTED) return rc;
@@ -291,7 +344,7 @@ extern "C" int ta_seg_attend(const void* q, const void* k_new, const void* v_new
                              const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl, void* Kc,
                              void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap, const int32_t* n_tree,
                              int local, float scale, int32_t* ids, uint8_t* vld, float* sct, void* out, int64_t osb,
-                             int64_t osh, float* keys, void* stream) {
+                             int64_t osh, float* keys, const ta_kv_pages* pages, void* stream) {
   if (B <= 0 || H <= 0 || wmax < 1 || wl < 0 || wl > kWave || n_levels < 0 || n_levels > kMaxLevels || T <= 0 ||
       (T & (T - 1)) || leaf_log2 < 1 || leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4 || Tcap <= 0) {
     set_error("ta_seg_attend: bad sizes (at most 64 kept leaves)");
@@ -302,8 +355,8 @@ extern "C" int ta_seg_attend(const void* q, const void* k_new, const void* v_new
     return TA_ERR_UNSUPPORTED;
   }
   const int Lw = local > 3 ? local : 3;
-  if (Lw + 1 > kWave) {
-    set_error("ta_seg_attend: local window must be < 64");
+  if (Lw + 1 > 32) {
+    set_error("ta_seg_attend: local window must be < 32");
     return TA_ERR_UNSUPPORTED;
   }
   if (!kv_aligned(q, dtype, D, {qsb, qsh}) || !kv_aligned(Kc, dtype, D, {csb, csh, cst}) ||
@@ -327,8 +380,8 @@ extern "C" int ta_seg_attend(const void* q, const void* k_new, const void* v_new
   const int cmax4 = (arity * wmax + arity - 1 + 3) & ~3;
   const int wmax4 = (wmax + 3) & ~3;
   const int wl_pad = (wl + 3) & ~3;
-  const size_t lds = (size_t)(4 * cmax4 + 2 * wmax4 + 16 * D) * sizeof(float) +
-                     (size_t)kWavesPerBlock * (wl_pad + kWave) * sizeof(float) +
+  const size_t lds = (size_t)(4 * cmax4 + 2 * wmax4 + (wmax4 + ((cmax4 + 63) & ~63) + 32) + 16 * D) * sizeof(float) +
+                     (size_t)kWavesPerBlock * attn_wave_ints(wl_pad) * sizeof(float) +
                      (size_t)kWavesPerBlock * (D + 2) * sizeof(float);
   if (lds > 64 * 1024) {
     set_error("ta_seg_attend: beam too wide for LDS (arity * wmax too large)");
@@ -347,7 +400,10 @@ extern "C" int ta_seg_attend(const void* q, const void* k_new, const void* v_new
   p.gsplit = 1;
   p.out = out; p.osb = osb; p.osh = osh; p.osn = 0;
   p.keys = keys;
+  const int prc = set_attn_pages(p, pages, dtype, D, leaf_log2, "ta_seg_attend");
+  if (prc != TA_OK) return prc;
   AppendIn ap{k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc, csb, csh, cst, Tcap};
+  set_append_pages(ap, pages);
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid(B * H), blk(kWavesPerBlock * kWave);
 #define TA_SA(TT, DD) \
@@ -367,7 +423,7 @@ extern "C" int ta_kv_append(const void* k_new, const void* v_new, int dtype, int
                             int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int B, int H,
                             int D, int Tcap, const int32_t* t_pos, int n_levels, float* const* lv_ptr,
                             const int64_t* lv_sb, const int64_t* lv_sh, int leaf_log2, int arity_log2,
-                            void* stream) {
+                            const ta_kv_pages* pages, void* stream) {
   if (B <= 0 || H <= 0 || D <= 0 || D > 256 || n_levels < 0 || n_levels > kMaxLevels || leaf_log2 < 1 ||
       leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4) {
     set_error("ta_kv_append: bad sizes");
@@ -379,24 +435,28 @@ extern "C" int ta_kv_append(const void* k_new, const void* v_new, int dtype, int
     lv.sb[j] = lv_sb[j];
     lv.sh[j] = lv_sh[j];
   }
+  if (pages && (pages->table == nullptr || pages->block_log2 != leaf_log2 || pages->num_pages <= 0 ||
+                pages->page_stride < ((int64_t)cst << leaf_log2))) {
+    set_error("ta_kv_append: bad page description (block must be the leaf block)");
+    return TA_ERR_ARG;
+  }
+  AppendIn ap{k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc, csb, csh, cst, Tcap};
+  set_append_pages(ap, pages);
   const size_t lds = (size_t)16 * D * sizeof(float);
   dim3 grid(B * H);
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
     case TA_F32:
-      hipLaunchKernelGGL((kv_append_kernel<float>), grid, dim3(D), lds, st, (const float*)k_new, (const float*)v_new,
-                         nsb, nsh, vnsb, vnsh, (float*)Kc, (float*)Vc, csb, csh, cst, H, D, Tcap, t_pos, lv, n_levels,
-                         leaf_log2, arity_log2);
+      hipLaunchKernelGGL((kv_append_kernel<float>), grid, dim3(D), lds, st, ap, H, D, t_pos, lv, n_levels, leaf_log2,
+                         arity_log2);
       break;
     case TA_F16:
-      hipLaunchKernelGGL((kv_append_kernel<f16_t>), grid, dim3(D), lds, st, (const f16_t*)k_new, (const f16_t*)v_new,
-                         nsb, nsh, vnsb, vnsh, (f16_t*)Kc, (f16_t*)Vc, csb, csh, cst, H, D, Tcap, t_pos, lv, n_levels,
-                         leaf_log2, arity_log2);
+      hipLaunchKernelGGL((kv_append_kernel<f16_t>), grid, dim3(D), lds, st, ap, H, D, t_pos, lv, n_levels, leaf_log2,
+                         arity_log2);
       break;
     case TA_BF16:
-      hipLaunchKernelGGL((kv_append_kernel<bf16_t>), grid, dim3(D), lds, st, (const bf16_t*)k_new,
-                         (const bf16_t*)v_new, nsb, nsh, vnsb, vnsh, (bf16_t*)Kc, (bf16_t*)Vc, csb, csh, cst, H, D,
-                         Tcap, t_pos, lv, n_levels, leaf_log2, arity_log2);
+      hipLaunchKernelGGL((kv_append_kernel<bf16_t>), grid, dim3(D), lds, st, ap, H, D, t_pos, lv, n_levels, leaf_log2,
+                         arity_log2);
       break;
     default:
       set_error("unknown dtype");

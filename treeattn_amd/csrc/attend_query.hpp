@@ -55,10 +55,14 @@ template <> struct Raw16<f16_t> {
 // per-query arrays of p), qrow (the query's D elements), t (position; structural mode), idr / vr (selected
 // leaf-block ids and their validity; structural mode), nv_given (number of valid ids when >= 0, else counted
 // from vr), nt (budget of tree leaves), orow_base (the output row), smem_f (LDS of the workgroup).
+// Paged caches: pre_leaf_pg (LDS, may be null) holds the pages of the leaf blocks idr lists and pre_static_pg
+// (LDS, may be null) the page of static slot i's block (slot 0: position 0, slot i >= 1: position t - i + 1),
+// read earlier by the caller; when null they are looked up in the page table here.
 template <typename T, int D, bool SPLIT, bool CAND>
 __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, int b, int h, int64_t qi, const T* qrow,
                                            int t, const int32_t* idr, const uint8_t* vr, int nv_given, int nt,
-                                           T* orow_base, float* smem_f) {
+                                           T* orow_base, float* smem_f, const int32_t* pre_leaf_pg = nullptr,
+                                           const int32_t* pre_static_pg = nullptr) {
   constexpr int EPL = Raw16<T>::EPL;
   constexpr int LPR = D / EPL;              // lanes per key row
   static_assert(LPR >= 1 && LPR <= kWave, "row slice layout");
@@ -70,8 +74,18 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
   (void)b;
   (void)h;
   const int wl_pad = p.cand ? 0 : ((p.wl + 3) & ~3);
-  int32_t* s_ids = reinterpret_cast<int32_t*>(smem_f + w * (wl_pad + kWave));
-  int32_t* s_ext = s_ids + wl_pad;
+  // per wavefront: used leaf ids [wl_pad], their pages [wl_pad], static keys [32] and their pages [32]
+  int32_t* s_ids = reinterpret_cast<int32_t*>(smem_f + w * attn_wave_ints(wl_pad));
+  int32_t* s_row0 = s_ids + wl_pad;
+  int32_t* s_ext = s_row0 + wl_pad;
+  // Keys are addressed by a row index r (K at kb + r * kst, V at vb + r * vst).  Contiguous caches: r is the
+  // position.  Paged caches: r = page * rpp + (position within the block), rpp = rows from one page to the next
+  // (the page stride in rows), so a key costs the same arithmetic in both layouts.  row0_of(j): the row of the
+  // first position of leaf block j, -1 when the block has no valid page (its keys are then skipped).
+  const int32_t* ptrow = p.ptab ? p.ptab + b * p.pt_sb + h * p.pt_sh : nullptr;
+  const int rpp = ptrow ? (int)(p.kps / p.kst) : 0;
+  auto row0_pg = [&](int pg) -> int { return (pg >= 0 && pg < p.npages) ? pg * rpp : -1; };
+  auto row0_of = [&](int j) -> int { return ptrow == nullptr ? (j << p.leaf_log2) : row0_pg(ptrow[j]); };
   const int rg = lane / LPR;               // key row of this lane inside a load instruction
   const int ds = (lane % LPR) * EPL;       // first dimension of this lane's slice
 
@@ -79,7 +93,7 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
   load_row<T, EPL>(qrow + ds, qv);
 
   // key list of this query
-  int N, nused = 0, lb = 0, nloc = 0, next = 0;
+  int N, nused = 0, lb = 0, nloc = 0, next = 0, own0 = -1;
   const int leaf = 1 << p.leaf_log2;
   if constexpr (CAND) {
     N = p.KC;
@@ -95,7 +109,11 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
       }
     }
     nused = t < 0 ? 0 : (nv < nt ? nv : (nt > 0 ? nt : 0));
-    for (int i = lane; i < nused; i += kWave) s_ids[i] = idr[i];
+    for (int i = lane; i < nused; i += kWave) {
+      const int id = idr[i];
+      s_ids[i] = id;
+      s_row0[i] = (pre_leaf_pg != nullptr && ptrow != nullptr) ? row0_pg(pre_leaf_pg[i]) : row0_of(id);
+    }
     lb = t < 0 ? 0 : (t >> p.leaf_log2) << p.leaf_log2;
     nloc = t < 0 ? 0 : t - lb + 1;
     wave_sync();
@@ -110,9 +128,16 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
         if (s_ids[i] == lf) keep = false;
     }
     const uint64_t bal = __ballot(keep);
-    if (keep) s_ext[__popcll(bal & ((1ull << lane) - 1))] = pe;
+    if (keep) {
+      const int slot = __popcll(bal & ((1ull << lane) - 1));
+      const int r0 = (pre_static_pg != nullptr && ptrow != nullptr) ? row0_pg(pre_static_pg[lane])
+                                                                    : row0_of(pe >> p.leaf_log2);
+      s_ext[slot] = r0 < 0 ? -1 : r0 + (pe & (leaf - 1));
+    }
     next = __popcll(bal);
     N = nused * leaf + nloc + next;
+    own0 = t < 0 ? -1 : ((pre_static_pg != nullptr && ptrow != nullptr) ? row0_pg(pre_static_pg[1])
+                                                                        : row0_of(t >> p.leaf_log2));
   }
   wave_sync();
 
@@ -126,27 +151,33 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
 
   // All positions of a chunk first (branch-free LDS reads in the structural mode, so no wait on memory
   // sits between the K/V loads), then its K/V loads.
+  // All rows of a chunk first (branch-free LDS reads in the structural mode, so no wait on memory sits
+  // between the K/V loads), then its K/V loads.
   auto fetch = [&](int c, uint4 (&kr)[NL], uint4 (&vr)[NL], bool (&ok)[NL]) {
-    int pos[NL];
+    int row[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int key = c * KPC + i * RPI + rg;
       if constexpr (CAND) {
-        pos[i] = key < N ? p.cand[qi * p.KC + key] : -1;
+        const int pos = key < N ? p.cand[qi * p.KC + key] : -1;
+        const int r0 = (pos >= 0 && pos < p.Tk) ? row0_of(pos >> p.leaf_log2) : -1;
+        row[i] = r0 < 0 ? -1 : r0 + (pos & (leaf - 1));
       } else {
         const int kt = key < nl ? key : 0;
-        const int leafpos = (s_ids[kt >> p.leaf_log2] << p.leaf_log2) + (kt & (leaf - 1));
+        const int r0 = s_row0[kt >> p.leaf_log2];
+        const int leafrow = r0 < 0 ? -1 : r0 + (kt & (leaf - 1));
         const int ke = key - nl - nloc;
-        const int extpos = s_ext[(ke >= 0 && ke < next) ? ke : 0];
-        pos[i] = key < nl ? leafpos : (key < nl + nloc ? lb + (key - nl) : (key < N ? extpos : -1));
+        const int extrow = s_ext[(ke >= 0 && ke < next) ? ke : 0];
+        const int ownrow = own0 < 0 ? -1 : own0 + (key - nl);
+        row[i] = key < nl ? leafrow : (key < nl + nloc ? ownrow : (key < N ? extrow : -1));
       }
     }
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      ok[i] = pos[i] >= 0 && pos[i] < p.Tk;
-      const int64_t row = ok[i] ? pos[i] : 0;
-      kr[i] = ldg16(kb + row * kst_b);
-      vr[i] = ldg16(vb + row * vst_b);
+      ok[i] = row[i] >= 0;
+      const int64_t r = ok[i] ? row[i] : 0;
+      kr[i] = ldg16(kb + r * kst_b);
+      vr[i] = ldg16(vb + r * vst_b);
     }
   };
 
@@ -242,7 +273,7 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
   }
   if constexpr (SPLIT) {
     // merge the 4 wavefronts of the workgroup through LDS
-    float* red = smem_f + kWavesPerBlock * (wl_pad + kWave);   // [4][D + 2]
+    float* red = smem_f + kWavesPerBlock * attn_wave_ints(wl_pad);   // [4][D + 2]
     if (rg == 0) {
 #pragma unroll
       for (int e = 0; e < EPL; ++e) red[w * (D + 2) + 2 + ds + e] = acc[e];

@@ -16,7 +16,8 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
                                int64_t vst, int B, int H, int Nq, int D, int Tk, const int32_t* tq, int64_t tq_sb,
                                const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl, int leaf,
                                int local, float scale, void* out, int64_t osb, int64_t osh, int64_t osn, float* lse,
-                               float* keys, int nsplit, float* ws, int64_t ws_bytes, void* stream);
+                               float* keys, int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages,
+                               void* stream);
 
 // The scratch array (one copy per GPU, held until the process ends).  In host code `scratch` names a
 // host-side stand-in, never the device memory: kernels and fills get the address from hipGetSymbolAddress.
@@ -62,7 +63,7 @@ extern "C" int ta_seg_attn_fwd_noalloc(const void* q, const void* k, const void*
                                        const int32_t* tq, int64_t tq_sb, const int32_t* ids, const uint8_t* vld,
                                        const int32_t* n_tree, int wl, int leaf, int local, float scale, void* out,
                                        int64_t osb, int64_t osh, int64_t osn, float* lse, float* keys, int nsplit,
-                                       void* stream) {
+                                       const ta_kv_pages* pages, void* stream) {
   const int64_t need = ta_seg_attn_workspace_size(B, H, Nq, D, nsplit);
   if (need > TA_SCRATCH_BYTES) {
     ta::set_error("ta_seg_attn_fwd_noalloc: this call needs " + std::to_string(need) +
@@ -83,5 +84,5 @@ extern "C" int ta_seg_attn_fwd_noalloc(const void* q, const void* k, const void*
   }
   return ta_seg_attn_fwd(q, k, v, dtype, qsb, qsh, qsn, ksb, ksh, kst, vsb, vsh, vst, B, H, Nq, D, Tk, tq, tq_sb,
                          ids, vld, n_tree, wl, leaf, local, scale, out, osb, osh, osn, lse, keys, nsplit,
-                         reinterpret_cast<float*>(base), need, stream);
+                         reinterpret_cast<float*>(base), need, pages, stream);
 }

@@ -29,9 +29,18 @@ struct AttnParams {
   float* keys;
   float* ws;            // per-workgroup partials (query, gsplit, D + 2) when gsplit > 1
   uint32_t* cnt;        // per-query arrival counters when gsplit > 1 (zero between calls)
+  // paged K/V (ptab != null): leaf block j of (b, h) is page ptab[b * pt_sb + h * pt_sh + j] (valid when in
+  // [0, npages)); its row r at k + page * kps + r * kst (v likewise with vps, vst); ksb/ksh/vsb/vsh are 0
+  const int32_t* ptab;
+  int64_t pt_sb, pt_sh, kps, vps;
+  int64_t npages;
 };
 
 constexpr float kNegBig = -1e30f;
+
+// LDS ints per wavefront of the attention's key lists: used leaf ids and their pages (wl_pad each), the
+// static keys and their pages (32 each).
+__host__ __device__ constexpr int attn_wave_ints(int wl_pad) { return 2 * wl_pad + 64; }
 
 // Split-attention workspace layout: per-query arrival counters (uint32, the region rounded up to 256 bytes),
 // then the per-workgroup partials.

@@ -95,10 +95,15 @@ __device__ __forceinline__ int quad_xor(int x) {
 // levels of lv for the tree of geometry T and leave the kept leaf-level nodes, best first, in kid / ksc
 // (LDS); returns how many there are (at most wmax).  qrow: the query's D elements (any address space).
 // LDS per query: ckey[cmax4] (uint64), cid[cmax4], csc[cmax4], kid[wmax4], ksc[wmax4].
+// ptrow (paged caches, else null): the query's page table row; the pages of the leaf-level candidates are
+// copied into LDS (cpg[cmax4 rounded up to 64]) while their node rows load, and the kept leaves' pages left in
+// kpg[wmax4], so an attention that follows needs no further round trip to the table.
 template <typename TQ, int D, int WPQ>
 __device__ __forceinline__ int descend_query(const TQ* qrow, int t, int T, int b, int h, const LevelIn& lv,
                                              int n_levels, int arity_log2, int wmax, int tid, uint64_t* ckey,
-                                             int32_t* cid, float* csc, int32_t* kid, float* ksc) {
+                                             int32_t* cid, float* csc, int32_t* kid, float* ksc,
+                                             const int32_t* ptrow = nullptr, int32_t* cpg = nullptr,
+                                             int32_t* kpg = nullptr) {
   constexpr int R = D / 16;
   constexpr int NB = (64 / R) < 16 ? (64 / R) : 16;
   constexpr int NG = 4 * WPQ;          // 16-lane groups per query
@@ -144,6 +149,15 @@ __device__ __forceinline__ int descend_query(const TQ* qrow, int t, int T, int b
             for (int i = 0; i < R; ++i) rows[r][i] = 0.0f;
           }
         }
+        if (ptrow != nullptr && j == 0 && c0 == 0 && tid < kWave) {
+          // the leaf-level candidates' pages, straight into LDS (no registers held through the descent); the
+          // first wavefront waits for them before the ranking barrier
+          for (int p0 = 0; p0 < C; p0 += kWave) {
+            const int c = p0 + tid;
+            __builtin_amdgcn_global_load_lds((const void*)(ptrow + (c < C ? cid[c] : 0)), (lds_void*)(cpg + p0), 4,
+                                             0, 0);
+          }
+        }
 #pragma unroll
         for (int r = 0; r < NB; ++r) {
           if (r < nr) {
@@ -156,6 +170,7 @@ __device__ __forceinline__ int descend_query(const TQ* qrow, int t, int T, int b
           }
         }
       }
+      if (ptrow != nullptr && j == 0 && tid < kWave) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       query_sync<WPQ>();
       TA_DMARK(1 + 2 * lvl_done);
       // rank = number of candidates with a larger key; P lanes (a quad's aligned part) share a candidate
@@ -181,6 +196,7 @@ __device__ __forceinline__ int descend_query(const TQ* qrow, int t, int T, int b
           if (c < C && part == 0 && rank < wmax) {
             kid[rank] = cid[c];
             ksc[rank] = csc[c];
+            if (kpg != nullptr && j == 0) kpg[rank] = cpg[c];
           }
         }
       }

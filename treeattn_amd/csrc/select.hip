@@ -122,11 +122,11 @@ __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
     // row t and the nodes ending at t; the descent below reads only nodes that end before t
     if (tid < D && t >= 0 && t < ap.Tcap) {
       float* stk = reinterpret_cast<float*>(smem_i + 4 * cmax4 + 2 * wmax4);   // one query per block
+      TQ *kbase, *vbase;
+      const KvRows rows = append_rows<TQ>(ap, b, h, lv.blevel[0], kbase, vbase);
       append_dim<TQ>(tid, D, t, reinterpret_cast<const TQ*>(ap.kn) + b * ap.nsb + h * ap.nsh,
-                     reinterpret_cast<const TQ*>(ap.vn) + b * ap.vnsb + h * ap.vnsh,
-                     reinterpret_cast<TQ*>(ap.Kc) + b * ap.csb + h * ap.csh,
-                     reinterpret_cast<TQ*>(ap.Vc) + b * ap.csb + h * ap.csh, ap.cst, n_levels, lv.blevel[0],
-                     arity_log2, stk,
+                     reinterpret_cast<const TQ*>(ap.vn) + b * ap.vnsb + h * ap.vnsh, kbase, vbase, rows, n_levels,
+                     lv.blevel[0], arity_log2, stk,
                      [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
     }
   }
@@ -433,7 +433,7 @@ extern "C" int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int
                                       int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld, float* sct,
                                       const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
                                       int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst,
-                                      int Tcap, void* stream) {
+                                      int Tcap, const ta_kv_pages* pages, void* stream) {
   if (B <= 0 || H <= 0 || wmax < 1 || wl < 0 || n_levels < 0 || n_levels > kMaxLevels || !pow2(T) ||
       leaf_log2 < 1 || leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4 || Tcap <= 0 || D > 256) {
     set_error("ta_tree_descend_append: bad sizes");
@@ -456,6 +456,18 @@ extern "C" int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int
   }
   if (n_levels == 0) lv.blevel[0] = leaf_log2;
   AppendIn ap{k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc, csb, csh, cst, Tcap};
+  if (pages) {
+    if (pages->table == nullptr || pages->block_log2 != leaf_log2 || pages->num_pages <= 0 ||
+        pages->page_stride < ((int64_t)cst << leaf_log2)) {
+      set_error("ta_tree_descend_append: bad page description (block must be the leaf block)");
+      return TA_ERR_ARG;
+    }
+    ap.ptab = pages->table;
+    ap.pt_sb = pages->sb;
+    ap.pt_sh = pages->sh;
+    ap.pstride = pages->page_stride;
+    ap.npages = pages->num_pages;
+  }
   return dispatch_dt_d<DescendRun>(dtype, D, q, qsb, qsh, (int64_t)0, B, H, 1, t_pos, (int64_t)1, lv, n_levels, T,
                                    arity_log2, wmax, wl, ids, vld, sct, (const AppendIn*)&ap, (hipStream_t)stream);
 }

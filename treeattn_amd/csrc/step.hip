@@ -212,8 +212,11 @@ __device__ __noinline__ void task_seq_head(const StepPlan& P, const StepRun& R, 
   // cache append of row t (and the nodes it completes); the descent reads only nodes ending before t
   bf16_t* Kc = Ly.K + b * Ly.csb + h * Ly.csh;
   bf16_t* Vc = Ly.V + b * Ly.csb + h * Ly.csh;
+  KvRows rows{};   // contiguous cache
+  rows.cst = Ly.cst;
+  rows.blog2 = P.leaf_log2;
   if (tid < D && t >= 0 && t < P.Tcap)
-    append_dim<bf16_t>(tid, D, t, S.k, S.v, Kc, Vc, Ly.cst, P.n_levels, P.leaf_log2, P.arity_log2, stk,
+    append_dim<bf16_t>(tid, D, t, S.k, S.v, Kc, Vc, rows, P.n_levels, P.leaf_log2, P.arity_log2, stk,
                        [&](int j) { return const_cast<float*>(S.lv.ptr[j]) + b * S.lv.sb[j] + h * S.lv.sh[j]; });
   TA_MARK(1);
   int nk = descend_query<bf16_t, D, 4>(S.q, t, P.Tcap, b, h, S.lv, P.n_levels, P.arity_log2, P.wmax, tid, ckey,
@@ -457,7 +460,7 @@ const char* step_check(const ta_step_model* m) {
   if (m->n_levels < 0 || m->n_levels > kMaxLevels) return "n_levels out of range";
   if (m->wmax < 1 || m->n_tree < 0) return "bad wmax or n_tree";
   const int Lw = m->local > 3 ? m->local : 3;
-  if (Lw + 1 > kWave) return "local window must be < 64";
+  if (Lw + 1 > 32) return "local window must be < 32";
   if (((int64_t)m->ld_wte * 2) % 16 || ((int64_t)m->ld_wpe * 2) % 16 || m->ld_wte < m->n_embd || m->ld_wpe < m->n_embd)
     return "embedding row strides must be >= n_embd and 16-byte multiples";
   return nullptr;
@@ -480,7 +483,7 @@ int step_lds_bytes(const ta_step_model* m, int cmax4, int wl) {
   const int D = m->head_dim;
   const int wl_pad = (wl + 3) & ~3;
   const int da = (int)sizeof(DaLds<64>) + (4 * cmax4 + 2 * wmax4) * 4 + 16 * D * 4 +
-                 (kWavesPerBlock * (wl_pad + kWave) + kWavesPerBlock * (D + 2)) * 4;
+                 (kWavesPerBlock * attn_wave_ints(wl_pad) + kWavesPerBlock * (D + 2)) * 4;
   int b0, nb_mlp, nb_c = m->n_embd / 64;
   mm_split_range(m->n_ff, m->mlp_splits, 0, b0, nb_mlp);
   const int mm = mm_lds_bytes(nb_c > nb_mlp ? nb_c : nb_mlp);

@@ -7,6 +7,8 @@ and step(tok, t) -> (logits, keys), weights_from_ours / weights_from_nanogpt -- 
 * batch: SegState(..., batch=B) and Decoder(..., batch=B); step(tok: LongTensor(B), t) -> logits (B, V);
 * dtype: the caches take the weights' dtype (bf16 models keep bf16 K/V; node sums are always float32);
 * tree shape: cfg.leaf / cfg.arity (the reference is leaf=2, arity=2);
+* paged caches: a Decoder keeps K and V in pages of one leaf block of one (sequence, head) (PagePool), handed
+  out as positions are reached (max_tokens bounds the pool, not Tcap); a stand-alone SegState is contiguous;
 * Decoder.prefill(idx) fills every layer's cache from a prompt in one pass (the forward of the model over
   the prompt, sparse attention included) and returns the last position's logits;
 * Decoder.capture(tok, t) captures one greedy step (logits, argmax token, position advance) in a HIP graph
@@ -32,24 +34,118 @@ def _ln(x, w):
     return F.layer_norm(x, (x.shape[-1],), w, None, 1e-5)
 
 
-class SegState:
-    """Per-layer cache (engine.py:18-71): K, V (B,H,Tcap,dh) in the model dtype, node sums of every tree
-    level (float32), the leaves each earlier query found (neighbour borrowing) and the running key sum."""
+class PagePool:
+    """The pages of a decoder's caches.  A page holds the K and V rows of one leaf block of one (sequence,
+    head); every layer has its own pool tensor (P, 2, leaf, dh), and one page table (B, H, Tcap / leaf) int32
+    serves all layers (leaf block j of (b, h) has the same page id in every layer's pool).  Pages are handed out
+    as positions are reached (ensure, on the host, outside captured steps) and returned per sequence (release);
+    the pool holds num_pages pages, so memory follows the tokens provisioned rather than Tcap."""
 
-    def __init__(self, cfg, Tcap, H, dh, dev, batch=1, dtype=torch.float32):
+    def __init__(self, B, H, dh, leaf, Tcap, num_pages, n_layers, dtype, dev):
+        self.B, self.H, self.leaf, self.Tcap, self.P = B, H, leaf, Tcap, int(num_pages)
+        nblk = Tcap // leaf
+        self.table = torch.full((B, H, nblk), -1, dtype=torch.int32, device=dev)
+        self.host = torch.full((B, H, nblk), -1, dtype=torch.int32)
+        self.nblk = [0] * B                        # leaf blocks of each sequence that have pages
+        self.free = list(range(self.P - 1, -1, -1))   # pages handed out in increasing order
+        self.pools = [torch.zeros(self.P, 2, leaf, dh, dtype=dtype, device=dev) for _ in range(n_layers)]
+
+    def ensure(self, t_end, seqs=None):
+        """Pages for positions < t_end (at most Tcap) of the given sequences (all by default): a sequence's
+        blocks get consecutive pages, head by head."""
+        need = (min(int(t_end), self.Tcap) + self.leaf - 1) // self.leaf
+        for b in (range(self.B) if seqs is None else seqs):
+            have = self.nblk[b]
+            if have >= need:
+                continue
+            n = (need - have) * self.H
+            if n > len(self.free):
+                raise RuntimeError('PagePool: out of pages (%d needed, %d free of %d): raise max_tokens'
+                                   % (n, len(self.free), self.P))
+            for h in range(self.H):
+                for j in range(have, need):
+                    self.host[b, h, j] = self.free.pop()
+            self.table[b, :, have:need].copy_(self.host[b, :, have:need])
+            self.nblk[b] = need
+
+    def release(self, b):
+        """Return sequence b's pages (its cache rows are forgotten)."""
+        n = self.nblk[b]
+        for h in range(self.H - 1, -1, -1):
+            self.free.extend(int(p) for p in self.host[b, h, :n].flip(0).tolist())
+        self.host[b, :, :n] = -1
+        self.table[b, :, :n].fill_(-1)
+        self.nblk[b] = 0
+
+    def cache(self, layer):
+        return K.PagedCache(self.pools[layer], self.table, self.Tcap)
+
+
+class SegState:
+    """Per-layer cache (engine.py:18-71): K, V in the model dtype -- contiguous (B,H,Tcap,dh), or the pages of a
+    PagePool -- node sums of every tree level (float32), the leaves each earlier query found (neighbour
+    borrowing; allocated for the candidate-list path only: neighbour borrowing or the budget head) and the running
+    key sum."""
+
+    def __init__(self, cfg, Tcap, H, dh, dev, batch=1, dtype=torch.float32, pages=None, layer=0):
         SEL.check_supported(cfg)
         self.cfg, self.Tcap, self.H, self.dh, self.B = cfg, Tcap, H, dh, batch
         self.dev = torch.device(dev)
         self.shape = SEL.cfg_shape(cfg, Tcap)
         self.Lm = self.shape.blevels[-1] if self.shape.n_levels else 0
-        self.K = torch.zeros(batch, H, Tcap, dh, device=dev, dtype=dtype)
-        self.V = torch.zeros(batch, H, Tcap, dh, device=dev, dtype=dtype)
+        self.pages = pages
+        if pages is None:
+            self.K = torch.zeros(batch, H, Tcap, dh, device=dev, dtype=dtype)
+            self.V = torch.zeros(batch, H, Tcap, dh, device=dev, dtype=dtype)
+            self.cache = None
+        else:
+            self.cache = pages.cache(layer)
+        self.dtype = dtype
         self.levels = [torch.zeros(batch, H, Tcap >> l, dh, device=dev) for l in self.shape.blevels]
         NS = cfg.nb_store
-        self.st_leaf = torch.zeros(batch, H, Tcap, NS, dtype=torch.int32, device=dev)
-        self.st_score = torch.zeros(batch, H, Tcap, NS, device=dev)
-        self.st_ok = torch.zeros(batch, H, Tcap, NS, dtype=torch.bool, device=dev)
+        Tst = Tcap if (cfg.neighbors or cfg.beam_mode == 'pred') else 0   # read and written by the list path
+        self.st_leaf = torch.zeros(batch, H, Tst, NS, dtype=torch.int32, device=dev)
+        self.st_score = torch.zeros(batch, H, Tst, NS, device=dev)
+        self.st_ok = torch.zeros(batch, H, Tst, NS, dtype=torch.bool, device=dev)
         self.ksum = torch.zeros(batch, H, dh, device=dev)
+
+    def kv(self):
+        """The cache as the kernels take it: (K, V) tensors, or (PagedCache, None)."""
+        return (self.K, self.V) if self.cache is None else (self.cache, None)
+
+    def dense_kv(self, b, t_end=None):
+        """Contiguous (1, H, t_end, dh) K and V of sequence b (a copy when paged)."""
+        t_end = self.Tcap if t_end is None else t_end
+        if self.cache is None:
+            return self.K[b:b + 1, :, :t_end], self.V[b:b + 1, :, :t_end]
+        return self.cache.dense(b, t_end)
+
+    def row(self, t):
+        """Row t of K and V for every sequence and head: (B, H, dh) copies."""
+        if self.cache is None:
+            return self.K[:, :, t].clone(), self.V[:, :, t].clone()
+        c = self.cache
+        pg = c.table[:, :, t // c.leaf].long()
+        ok = (pg >= 0).unsqueeze(-1)
+        rows = c.pool[pg.clamp(min=0), :, t % c.leaf]        # (B, H, 2, dh)
+        return rows[:, :, 0] * ok, rows[:, :, 1] * ok
+
+    def write_rows(self, b0, k, v):
+        """Store positions 0..T-1 of sequences b0.. from k, v (n, H, T, dh) (a prompt's keys and values)."""
+        n, H, T, dh = k.shape
+        if self.cache is None:
+            self.K[b0:b0 + n, :, :T].copy_(k)
+            self.V[b0:b0 + n, :, :T].copy_(v)
+            return
+        c = self.cache
+        nb = (T + c.leaf - 1) // c.leaf
+        pg = c.table[b0:b0 + n, :, :nb].long()
+        if bool((pg < 0).any()):
+            raise RuntimeError('SegState: positions without pages (PagePool.ensure first)')
+        pad = nb * c.leaf - T
+        kk, vv = (F.pad(x, (0, 0, 0, pad)) if pad else x for x in (k, v))
+        c.pool[pg.reshape(-1), 0] = kk.reshape(n, H, nb, c.leaf, dh).reshape(-1, c.leaf, dh).to(c.dtype)
+        c.pool[pg.reshape(-1), 1] = vv.reshape(n, H, nb, c.leaf, dh).reshape(-1, c.leaf, dh).to(c.dtype)
 
     def level_of(self, l):
         try:
@@ -68,8 +164,9 @@ class SegState:
 
     def add(self, t, k, v):
         """Store position t (k, v: (B,H,dh)) and form the nodes it completes (engine.py:41-55)."""
-        K.kv_append(k.to(self.K.dtype), v.to(self.V.dtype), self.K, self.V, self._tpos(t), self.levels,
-                    self.shape.leaf, self.shape.arity)
+        Kc, Vc = self.kv()
+        K.kv_append(k.to(self.dtype), v.to(self.dtype), Kc, Vc, self._tpos(t), self.levels, self.shape.leaf,
+                    self.shape.arity)
         self.ksum += k.float()
 
     def rows(self, b0, b1):
@@ -78,17 +175,21 @@ class SegState:
         v.__dict__.update(self.__dict__)
         v.B = b1 - b0
         for name in ('K', 'V', 'st_leaf', 'st_score', 'st_ok', 'ksum'):
-            setattr(v, name, getattr(self, name)[b0:b1])
+            if hasattr(self, name):
+                setattr(v, name, getattr(self, name)[b0:b1])
+        if self.cache is not None:
+            v.cache = self.cache.rows(b0, b1)
         v.levels = [t[b0:b1] for t in self.levels]
         return v
 
     def fill(self, K_, V_, t_end=None):
         """Load a whole context (engine.py:57-71).  K_, V_: (B,H,T,dh) with T <= Tcap."""
         T = K_.shape[2]
-        self.K[:, :, :T].copy_(K_)
-        self.V[:, :, :T].copy_(V_)
+        if self.pages is not None:
+            self.pages.ensure(T)
+        self.write_rows(0, K_, V_)
         t_end = T if t_end is None else t_end
-        SEL.build_pyramid(self.K, self.shape, t_end=t_end, out=self.levels)
+        SEL.build_pyramid(K_.to(self.dtype), self.shape, t_end=t_end, out=self.levels)
         self.ksum.copy_(K_[:, :, :t_end].float().sum(2))
 
 
@@ -202,33 +303,34 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     if scratch is None:
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
     structural = (not cfg.neighbors) and lhat is None
-    fused = structural and update and B * H < 4096 and q.dtype == k.dtype == state.K.dtype
+    fused = structural and update and B * H < 4096 and q.dtype == k.dtype == state.dtype
+    Kc, Vc = state.kv()
     if fused and scratch.nsplit == 4 and dh in (64, 128) and wl <= 64 and not cfg.global_pool:
         # append, descent and attention in one launch (one workgroup per (sequence, head))
         if scratch.n_tree is None:
             scratch.n_tree = torch.full((B, H, 1), SEL.fixed_n_tree(cfg), dtype=torch.int32, device=q.device)
         out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
-        K.seg_attend(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0], state.K, state.V,
+        K.seg_attend(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0], Kc, Vc,
                      scratch.n_tree, cfg.local, scale, (scratch.ids, scratch.vld, scratch.sct), out, keys=scratch.keys)
         return out, scratch.keys
     if fused:
         # descent and cache append in one launch (the append touches only row t and the nodes ending at t)
         ids, vld, sct = K.tree_descend_append(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0],
-                                              state.K, state.V, out=(scratch.ids, scratch.vld, scratch.sct))
+                                              Kc, Vc, out=(scratch.ids, scratch.vld, scratch.sct))
     else:
         ids, vld, sct = K.tree_descend(q, state.levels, tpos.view(B, 1), state.shape, cfg.wmax,
                                        out=(scratch.ids, scratch.vld, scratch.sct))
     if structural:
         if update:
             if not fused:
-                K.kv_append(k[:, :, 0], v[:, :, 0], state.K, state.V, tpos, state.levels, leaf, state.shape.arity)
+                K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
             if cfg.global_pool:
                 state.ksum += k[:, :, 0].float()
         out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
         if scratch.n_tree is None:
             scratch.n_tree = torch.full((B, H, 1), SEL.fixed_n_tree(cfg), dtype=torch.int32, device=q.device)
         n_tree = scratch.n_tree
-        K.seg_attn(q, state.K, state.V, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out,
+        K.seg_attn(q, Kc, Vc, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out,
                    keys=scratch.keys, nsplit=scratch.nsplit, ws=scratch.ws)
         return out, scratch.keys
     # reference-default mode: neighbour borrowing and/or the budget head -> candidate list
@@ -255,10 +357,10 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         state.st_score[bidx, hidx, tt, :n] = torch.where(vb[:, :, 0, :n], sct[:, :, 0, :n],
                                                          torch.zeros_like(sct[:, :, 0, :n]))
         state.st_ok[bidx, hidx, tt, :n] = vb[:, :, 0, :n]
-        K.kv_append(k[:, :, 0], v[:, :, 0], state.K, state.V, tpos, state.levels, leaf, state.shape.arity)
+        K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
         state.ksum += k[:, :, 0].float()
     cand, keep, used = SEL.assemble(sel, t64, cfg, B, H)
-    out, _ = K.sparse_attn_fwd(q, state.K, state.V, torch.where(keep, cand, torch.full_like(cand, -1)), scale)
+    out, _ = K.sparse_attn_fwd(q, Kc, Vc, torch.where(keep, cand, torch.full_like(cand, -1)), scale)
     return out, keep.sum(-1).float()
 
 
@@ -301,7 +403,10 @@ class Decoder:
     """Layer loop around seg_attend (engine.py:149-177), batched and graph-capturable."""
 
     def __init__(self, W, n_layer, n_head, n_embd, Tcap, mode, cfg=None, dev='cuda', batch=1, dtype=None,
-                 groups=None, one_launch=None, attn_split=None):
+                 groups=None, one_launch=None, attn_split=None, paged=None, max_tokens=None, reserve_ahead=256):
+        """paged (default: on, except for the one-launch step, which takes contiguous caches): K and V in pages
+        of a PagePool sized for max_tokens positions per sequence (default Tcap); pages are handed out as
+        positions are reached, reserve_ahead positions at a time for captured steps."""
         self.W, self.nl, self.H, self.C, self.Tcap = W, n_layer, n_head, n_embd, Tcap
         self.dh, self.mode, self.cfg, self.dev = n_embd // n_head, mode, cfg, torch.device(dev)
         self.B = batch
@@ -323,12 +428,24 @@ class Decoder:
                              'fixed budget')
         # off unless asked for: on MI355X the per-op graph is faster at config 4 (1.40 vs 2.32 ms per step)
         self.one_launch = bool(one_launch)
+        self.paged = (mode == 'seg' and not self.one_launch) if paged is None else bool(paged)
+        if self.paged and (self.one_launch or mode != 'seg'):
+            raise ValueError('paged caches serve the per-op seg decoder (not the one-launch step or dense mode)')
+        self.max_tokens = min(int(max_tokens), Tcap) if max_tokens else Tcap
+        self.reserve_ahead = int(reserve_ahead)
         self.reset()
 
     def reset(self):
         B, H, dh = self.B, self.H, self.dh
+        self.pool = None
+        self._t_host = None      # largest position a step has used (host copy; None when unknown)
         if self.mode == 'seg':
-            self.states = [SegState(self.cfg, self.Tcap, H, dh, self.dev, B, self.dtype) for _ in range(self.nl)]
+            if self.paged:
+                leaf = SEL.cfg_shape(self.cfg, self.Tcap).leaf
+                npages = B * H * ((self.max_tokens + leaf - 1) // leaf)
+                self.pool = PagePool(B, H, dh, leaf, self.Tcap, npages, self.nl, self.dtype, self.dev)
+            self.states = [SegState(self.cfg, self.Tcap, H, dh, self.dev, B, self.dtype, pages=self.pool, layer=i)
+                           for i in range(self.nl)]
             sh = self.states[0].shape
             wl = sh.leaf_width(self.cfg.wmax)
             self.scratch = _Scratch(B, H, dh, wl, self.dev, self._nsplit(B, wl, sh.leaf), self.nl)
@@ -459,11 +576,20 @@ class Decoder:
               else tok.to(self.dev).long()).contiguous()
         tp = (t.to(self.dev).long().contiguous() if torch.is_tensor(t) else
               torch.full((self.B,), int(t), device=self.dev, dtype=torch.long))
+        if self.pool is not None:
+            self.reserve(int(t.max()) + 1 if torch.is_tensor(t) else int(t) + 1)
         logits = self._forward_step(tk, tp)
         keys = self.keys_read()
         if scalar and self.B == 1:
             return logits[0], float(keys[0])
         return logits, keys
+
+    def reserve(self, t_end):
+        """Pages for positions < t_end of every sequence (paged caches; host side, not inside a captured step)."""
+        if self.pool is not None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError('Decoder.reserve: pages are handed out outside graph capture')
+            self.pool.ensure(t_end)
 
     # ------------------------------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -480,6 +606,8 @@ class Decoder:
         cfg = self.cfg
         chunk = chunk or B
         tq = torch.arange(T0, device=self.dev, dtype=torch.int32)
+        if self.pool is not None:
+            self.reserve(T0)
         scale = 1.0 / math.sqrt(dh)
         n_tree_val = SEL.fixed_n_tree(cfg)
         last = []
@@ -491,11 +619,9 @@ class Decoder:
                 st = self.states[i]
                 qkv = F.linear(_ln(x, L['ln1']), L['c_attn'])
                 q, k, v = [a.view(nb, T0, H, dh).transpose(1, 2) for a in qkv.split(C, -1)]
-                Kb, Vb = st.K[b0:b1], st.V[b0:b1]
-                Kb[:, :, :T0].copy_(k)
-                Vb[:, :, :T0].copy_(v)
+                st.write_rows(b0, k, v)
                 lv = [t[b0:b1] for t in st.levels]
-                K.level_sums(Kb, st.shape.blevels, out=lv, t_end=T0, zero_sink=True)
+                K.level_sums(k, st.shape.blevels, out=lv, t_end=T0, zero_sink=True)
                 out = torch.empty(nb, T0, H, dh, device=self.dev, dtype=v.dtype)
                 if cfg.neighbors or cfg.beam_mode == 'pred':
                     # the forward's selection with neighbour borrowing and/or the budget head's per-query budget
@@ -519,7 +645,7 @@ class Decoder:
                 else:
                     ids, vld, _ = K.tree_descend(q, lv, tq, st.shape, cfg.wmax)
                     n_tree = torch.full(ids.shape[:3], n_tree_val, dtype=torch.int32, device=self.dev)
-                    K.seg_attn(q, Kb, Vb, tq, ids, vld, n_tree, st.shape.leaf, cfg.local, scale,
+                    K.seg_attn(q, k, v, tq, ids, vld, n_tree, st.shape.leaf, cfg.local, scale,
                                out=out.transpose(1, 2))
                     del ids, vld, n_tree
                 x = x + F.linear(out.view(nb, T0, C), L['c_proj'])
@@ -541,6 +667,10 @@ class Decoder:
         self.g_tok = tok.to(self.dev).long().clone()
         self.g_t = (t.to(self.dev).long() if torch.is_tensor(t) else
                     torch.full((B,), int(t), device=self.dev, dtype=torch.long)).clone()
+        # the replays' positions, followed on the host so pages can be handed out ahead of them without a sync
+        self._t_host = int(self.g_t.max()) if torch.is_tensor(t) else int(t)
+        self._reserved = self._t_host + 1 + self.reserve_ahead
+        self.reserve(self._reserved)
         self.g_logits = torch.empty(B, V, device=self.dev, dtype=torch.bfloat16 if self.fused else torch.float32)
         main = torch.cuda.current_stream()
         groups = self.groups if (self.fused and len(self.groups) > 1) else [None]
@@ -591,7 +721,14 @@ class Decoder:
 
     def replay(self):
         """Launch one captured step for every group (each on its own stream).  Successive replays of a group
-        are ordered by its stream; torch.cuda.synchronize() waits for all of them."""
+        are ordered by its stream; torch.cuda.synchronize() waits for all of them.  With paged caches the pages
+        of the next reserve_ahead positions are handed out (outside the graph) whenever the replays reach the
+        end of the reserved range."""
+        if self.pool is not None and self._t_host is not None:
+            if self._t_host + 1 >= self._reserved:
+                self._reserved = self._t_host + 1 + self.reserve_ahead
+                self.reserve(self._reserved)
+            self._t_host += 1
         main = torch.cuda.current_stream()
         for g, s in self.graphs:
             s.wait_stream(main)

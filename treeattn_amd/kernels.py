@@ -55,6 +55,61 @@ class TreeShape:
         return [torch.empty(B, H, Tn >> l, D, device=device, dtype=torch.float32) for l in self.blevels]
 
 
+# ----------------------------------------------------------------------------------------------- paged cache
+class PagedCache:
+    """One layer's decode cache in pages: pool (P, 2, leaf, D) -- page p holds the K rows (pool[p, 0]) and the V
+    rows (pool[p, 1]) of one leaf block of one (sequence, head) -- and the page table (B, H, n_blocks) int32
+    (-1: no page) that maps leaf block j of (b, h) to its page; the table may be shared by several layers'
+    pools.  tcap: positions per sequence the table covers.  Kernel wrappers take a PagedCache wherever they
+    take a contiguous (B, H, Tcap, D) cache."""
+
+    def __init__(self, pool, table, tcap):
+        P, two, leaf, D = pool.shape
+        if two != 2 or not pool.is_contiguous() or table.dtype != torch.int32 or not table.is_contiguous():
+            raise ValueError('PagedCache: pool (P, 2, leaf, D) contiguous and an int32 contiguous table')
+        if table.shape[2] * leaf < tcap:
+            raise ValueError('PagedCache: the table does not cover tcap positions')
+        self.pool, self.table, self.tcap = pool, table, int(tcap)
+        self.leaf, self.D, self.dtype, self.device = leaf, D, pool.dtype, pool.device
+        self.B, self.H = table.shape[0], table.shape[1]
+        self.desc = L.KvPages(table.data_ptr(), table.stride(0), table.stride(1), 2 * leaf * D, P, _ilog2(leaf))
+        self.k = pool[:, 0]   # (P, leaf, D) views whose first element is page 0's first K / V row
+        self.v = pool[:, 1]
+
+    def rows(self, b0, b1):
+        """The same pages seen from sequences b0..b1-1 (the table rows of those sequences)."""
+        return PagedCache(self.pool, self.table[b0:b1], self.tcap)
+
+    def dense(self, b, t_end=None):
+        """Contiguous (1, H, t_end, D) copies of K and V of sequence b (rows without a page are zero)."""
+        t_end = self.tcap if t_end is None else int(t_end)
+        nb = (t_end + self.leaf - 1) // self.leaf
+        pg = self.table[b, :, :nb].long()
+        ok = (pg >= 0).view(self.H, nb, 1, 1)
+        kv = self.pool[pg.clamp(min=0)] * ok.unsqueeze(2).to(self.dtype)   # (H, nb, 2, leaf, D)
+        k = kv[:, :, 0].reshape(1, self.H, nb * self.leaf, self.D)[:, :, :t_end]
+        v = kv[:, :, 1].reshape(1, self.H, nb * self.leaf, self.D)[:, :, :t_end]
+        return k, v
+
+
+def _cache(Kc, Vc):
+    """(K base, V base, sequence stride, head stride, row stride, Tcap, pages) of a contiguous cache or a
+    PagedCache, as the C ABI takes them."""
+    if isinstance(Kc, PagedCache):
+        return L.ptr(Kc.k), L.ptr(Kc.v), 0, 0, Kc.D, Kc.tcap, ctypes.byref(Kc.desc)
+    if Kc.stride(-1) != 1 or Kc.stride() != Vc.stride():
+        raise ValueError('treeattn_amd: K and V caches need the same strides and contiguous rows')
+    return L.ptr(Kc), L.ptr(Vc), Kc.stride(0), Kc.stride(1), Kc.stride(2), Kc.shape[2], None
+
+
+def _cache_tensors(Kc, Vc):
+    return (Kc.pool,) if isinstance(Kc, PagedCache) else (Kc, Vc)
+
+
+def _cache_dtype(Kc):
+    return Kc.dtype
+
+
 # ----------------------------------------------------------------------------------------------- builder
 def level_sums(k, blevels, out=None, t_end=None, zero_sink=True):
     """Node sums of binary levels `blevels` of keys k (B,H,T,D): list of (B,H,T>>l,D) float32."""
@@ -105,23 +160,24 @@ def tree_descend(q, levels, tq, shape, wmax, out=None):
 
 def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out):
     """Decode step's descent of q (B,H,1,D) at t_pos (B,) int32 and, in the same launch, the cache append of
-    k_new, v_new (B,H,D) at row t_pos[b] of Kc, Vc (B,H,Tcap,D) with node formation.  out = (ids, vld, sct)
-    buffers (B,H,1,wl)."""
-    L.require_gpu(q, t_pos, k_new, v_new, Kc, Vc)
+    k_new, v_new (B,H,D) at row t_pos[b] of the cache (Kc, Vc (B,H,Tcap,D), or a PagedCache as Kc) with node
+    formation.  out = (ids, vld, sct) buffers (B,H,1,wl)."""
+    L.require_gpu(q, t_pos, k_new, v_new, *_cache_tensors(Kc, Vc))
     B, H, Nq, D = q.shape
     if Nq != 1 or t_pos.dtype != torch.int32 or not t_pos.is_contiguous():
         raise ValueError('tree_descend_append: one query per (sequence, head) and contiguous int32 positions')
-    if not (q.dtype == k_new.dtype == v_new.dtype == Kc.dtype == Vc.dtype):
+    if not (q.dtype == k_new.dtype == v_new.dtype == _cache_dtype(Kc)):
         raise TypeError('tree_descend_append: q, new rows and caches must share a dtype')
-    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or Kc.stride() != Vc.stride():
+    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1:
         raise ValueError('tree_descend_append: unsupported layout')
+    kp, vp, csb, csh, cst, tcap, pages = _cache(Kc, Vc)
     ids, vld, sct = out
     wl = shape.leaf_width(wmax)
     L.call('ta_tree_descend_append', L.ptr(q), L.dtype_code(q), q.stride(0), q.stride(1), B, H, D, L.ptr(t_pos),
            len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
            L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, L.ptr(ids),
            L.ptr(vld), L.ptr(sct), L.ptr(k_new), L.ptr(v_new), k_new.stride(0), k_new.stride(1), v_new.stride(0),
-           v_new.stride(1), L.ptr(Kc), L.ptr(Vc), Kc.stride(0), Kc.stride(1), Kc.stride(2), Kc.shape[2], L.stream())
+           v_new.stride(1), kp, vp, csb, csh, cst, tcap, pages, L.stream())
     return ids, vld, sct
 
 
@@ -131,14 +187,15 @@ def seg_attend(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, n_tree, loca
     blocks, the own block and the static keys.  sel = (ids, vld, sct) buffers (B,H,1,wl) receive the
     selection; out (B,H,1,D) the attention output; keys (B,H,1) float32 the number of keys attended.  Equals
     tree_descend_append followed by seg_attn with nsplit 4, bit for bit."""
-    L.require_gpu(q, t_pos, k_new, v_new, Kc, Vc, out)
+    L.require_gpu(q, t_pos, k_new, v_new, out, *_cache_tensors(Kc, Vc))
     B, H, Nq, D = q.shape
     if Nq != 1 or t_pos.dtype != torch.int32 or not t_pos.is_contiguous():
         raise ValueError('seg_attend: one query per (sequence, head) and contiguous int32 positions')
-    if not (q.dtype == k_new.dtype == v_new.dtype == Kc.dtype == Vc.dtype == out.dtype):
+    if not (q.dtype == k_new.dtype == v_new.dtype == _cache_dtype(Kc) == out.dtype):
         raise TypeError('seg_attend: q, new rows, caches and output must share a dtype')
-    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or Kc.stride() != Vc.stride() or out.stride(-1) != 1:
+    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or out.stride(-1) != 1:
         raise ValueError('seg_attend: unsupported layout')
+    kp, vp, csb, csh, cst, tcap, pages = _cache(Kc, Vc)
     ids, vld, sct = sel
     wl = shape.leaf_width(wmax)
     nt = None
@@ -147,9 +204,9 @@ def seg_attend(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, n_tree, loca
     L.call('ta_seg_attend', L.ptr(q), L.ptr(k_new), L.ptr(v_new), L.dtype_code(q), q.stride(0), q.stride(1),
            k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1), B, H, D, L.ptr(t_pos),
            len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
-           L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, L.ptr(Kc),
-           L.ptr(Vc), Kc.stride(0), Kc.stride(1), Kc.stride(2), Kc.shape[2], L.ptr(nt), int(local), float(scale),
-           L.ptr(ids), L.ptr(vld), L.ptr(sct), L.ptr(out), out.stride(0), out.stride(1), L.ptr(keys), L.stream())
+           L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, kp, vp, csb, csh,
+           cst, tcap, L.ptr(nt), int(local), float(scale), L.ptr(ids), L.ptr(vld), L.ptr(sct), L.ptr(out),
+           out.stride(0), out.stride(1), L.ptr(keys), pages, L.stream())
     return out, keys
 
 
@@ -186,19 +243,30 @@ def gather_dot_blocks(q, K, blk, block, scale=1.0, out=None):
 
 
 # ----------------------------------------------------------------------------------------------- attention
+def _kv_rows(k, v):
+    """(K base, V base, K strides (b, h, row), V strides, Tk, pages) of attention keys/values: (b,H,Tk,dh)
+    tensors or a PagedCache (as k; v unused)."""
+    if isinstance(k, PagedCache):
+        D = k.D
+        return L.ptr(k.k), L.ptr(k.v), (0, 0, D), (0, 0, D), k.tcap, ctypes.byref(k.desc)
+    return L.ptr(k), L.ptr(v), L.rows3(k), L.rows3(v), k.shape[2], None
+
+
 def sparse_attn_fwd(q, k, v, cand, scale):
-    """Softmax attention over candidate positions (-1 unused) into k, v (b,H,Tk,dh).  Returns (out (b,H,T,dh)
-    in v's dtype, lse (b,H,T))."""
-    L.require_gpu(q, k, v, cand)
-    if not (q.dtype == k.dtype == v.dtype):
+    """Softmax attention over candidate positions (-1 unused) into k, v (b,H,Tk,dh) or a PagedCache (as k).
+    Returns (out (b,H,T,dh) in the values' dtype, lse (b,H,T))."""
+    L.require_gpu(q, cand, *_cache_tensors(k, v))
+    vdt = _cache_dtype(k) if isinstance(k, PagedCache) else v.dtype
+    if not (q.dtype == _cache_dtype(k) == vdt):
         raise TypeError('q, k, v must share a dtype')
     b, H, T, D = q.shape
     KC = cand.shape[-1]
     cc = cand.to(torch.int32).contiguous()
-    out = torch.empty(b, H, T, D, device=q.device, dtype=v.dtype)
+    out = torch.empty(b, H, T, D, device=q.device, dtype=vdt)
     lse = torch.empty(b, H, T, device=q.device, dtype=torch.float32)
-    L.call('ta_sparse_attn_fwd', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k), *L.rows3(v),
-           L.ptr(cc), b, H, T, k.shape[2], KC, D, float(scale), L.ptr(out), L.ptr(lse), L.stream())
+    kp, vp, ks, vs, Tk, pages = _kv_rows(k, v)
+    L.call('ta_sparse_attn_fwd', L.ptr(q), kp, vp, L.dtype_code(q), *L.rows3(q), *ks, *vs,
+           L.ptr(cc), b, H, T, Tk, KC, D, float(scale), L.ptr(out), L.ptr(lse), pages, L.stream())
     return out, lse
 
 
@@ -236,8 +304,9 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
     """Attention over selected leaf blocks + own leaf block + static keys (neighbours off).
     q (B,H,Nq,D) strided; k, v (B,H,Tk,D) strided; tq (Nq,) or (B,Nq) int32; ids/vld (B,H,Nq,wl);
     n_tree (B,H,Nq) int32 or None.  Returns (out, lse, keys)."""
-    L.require_gpu(q, k, v, tq, ids, vld)
-    if not (q.dtype == k.dtype == v.dtype):
+    L.require_gpu(q, tq, ids, vld, *_cache_tensors(k, v))
+    vdt = _cache_dtype(k) if isinstance(k, PagedCache) else v.dtype
+    if not (q.dtype == _cache_dtype(k) == vdt):
         raise TypeError('q, k, v must share a dtype')
     B, H, Nq, D = q.shape
     wl = ids.shape[-1]
@@ -245,17 +314,18 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
     tq32 = tq32.contiguous()
     tq_sb = 0 if tq32.dim() == 1 else tq32.stride(0)
     if out is None:
-        out = torch.empty(B, H, Nq, D, device=q.device, dtype=v.dtype)
+        out = torch.empty(B, H, Nq, D, device=q.device, dtype=vdt)
     nt = None
     if n_tree is not None:
         nt = n_tree if (n_tree.dtype == torch.int32 and n_tree.is_contiguous()) else n_tree.to(torch.int32).contiguous()
     if ws is None:
         ws = seg_attn_workspace(B, H, Nq, D, nsplit, q.device)
     ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
-    L.call('ta_seg_attn_fwd', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k), *L.rows3(v),
-           B, H, Nq, D, k.shape[2], L.ptr(tq32), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(nt), wl, int(leaf), int(local),
+    kp, vp, ks, vs, Tk, pages = _kv_rows(k, v)
+    L.call('ta_seg_attn_fwd', L.ptr(q), kp, vp, L.dtype_code(q), *L.rows3(q), *ks, *vs,
+           B, H, Nq, D, Tk, L.ptr(tq32), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(nt), wl, int(leaf), int(local),
            float(scale), L.ptr(out), out.stride(0), out.stride(1), out.stride(2), L.ptr(lse), L.ptr(keys),
-           int(nsplit), L.ptr(ws), ws_bytes, L.stream())
+           int(nsplit), L.ptr(ws), ws_bytes, pages, L.stream())
     return out, lse, keys
 
 
@@ -263,8 +333,9 @@ def seg_attn_noalloc(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out, lse
     """seg_attn through ta_seg_attn_fwd_noalloc: no workspace argument and nothing allocated by the call (the
     split scratch is the library's fixed per-GPU array; `out` must be given).  Calls on one GPU must not
     overlap in time.  Returns (out, lse, keys)."""
-    L.require_gpu(q, k, v, tq, ids, vld, out)
-    if not (q.dtype == k.dtype == v.dtype == out.dtype):
+    L.require_gpu(q, tq, ids, vld, out, *_cache_tensors(k, v))
+    vdt = _cache_dtype(k) if isinstance(k, PagedCache) else v.dtype
+    if not (q.dtype == _cache_dtype(k) == vdt == out.dtype):
         raise TypeError('q, k, v and out must share a dtype')
     B, H, Nq, D = q.shape
     if tq.dtype != torch.int32 or not tq.is_contiguous():
@@ -272,10 +343,11 @@ def seg_attn_noalloc(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out, lse
     if n_tree is not None and (n_tree.dtype != torch.int32 or not n_tree.is_contiguous()):
         raise ValueError('seg_attn_noalloc: n_tree must be contiguous int32')
     tq_sb = 0 if tq.dim() == 1 else tq.stride(0)
-    L.call('ta_seg_attn_fwd_noalloc', L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(q), *L.rows3(q), *L.rows3(k),
-           *L.rows3(v), B, H, Nq, D, k.shape[2], L.ptr(tq), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(n_tree),
-           ids.shape[-1], int(leaf), int(local), float(scale), L.ptr(out), out.stride(0), out.stride(1),
-           out.stride(2), L.ptr(lse), L.ptr(keys), int(nsplit), L.stream())
+    kp, vp, ks, vs, Tk, pages = _kv_rows(k, v)
+    L.call('ta_seg_attn_fwd_noalloc', L.ptr(q), kp, vp, L.dtype_code(q), *L.rows3(q), *ks, *vs, B, H, Nq, D, Tk,
+           L.ptr(tq), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(n_tree), ids.shape[-1], int(leaf), int(local),
+           float(scale), L.ptr(out), out.stride(0), out.stride(1), out.stride(2), L.ptr(lse), L.ptr(keys),
+           int(nsplit), pages, L.stream())
     return out, lse, keys
 
 
@@ -407,17 +479,19 @@ def embed(tok, tpos, wte, wpe, out, pos32, advance=False, ln_w=None, out_ln=None
 
 # ----------------------------------------------------------------------------------------------- decode append
 def kv_append(k_new, v_new, Kc, Vc, t_pos, levels, leaf, arity):
-    """Write k_new, v_new (B,H,D) at row t_pos[b] of the caches (B,H,Tcap,D) and form the completed nodes."""
-    L.require_gpu(k_new, v_new, Kc, Vc, t_pos)
-    if not (k_new.dtype == v_new.dtype == Kc.dtype == Vc.dtype):
+    """Write k_new, v_new (B,H,D) at row t_pos[b] of the cache (Kc, Vc (B,H,Tcap,D), or a PagedCache as Kc) and
+    form the completed nodes."""
+    L.require_gpu(k_new, v_new, t_pos, *_cache_tensors(Kc, Vc))
+    if not (k_new.dtype == v_new.dtype == _cache_dtype(Kc)):
         raise TypeError('kv_append: new rows and caches must share a dtype')
-    B, H, Tcap, D = Kc.shape
-    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or Kc.stride() != Vc.stride():
+    B, H, D = k_new.shape
+    if k_new.stride(-1) != 1 or v_new.stride(-1) != 1:
         raise ValueError('kv_append: unsupported layout')
-    L.call('ta_kv_append', L.ptr(k_new), L.ptr(v_new), L.dtype_code(Kc), k_new.stride(0), k_new.stride(1),
-           v_new.stride(0), v_new.stride(1), L.ptr(Kc), L.ptr(Vc), Kc.stride(0), Kc.stride(1), Kc.stride(2), B, H, D,
-           Tcap, L.ptr(t_pos), len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
-           L.i64_array([t.stride(1) for t in levels]), _ilog2(leaf), _ilog2(arity), L.stream())
+    kp, vp, csb, csh, cst, tcap, pages = _cache(Kc, Vc)
+    L.call('ta_kv_append', L.ptr(k_new), L.ptr(v_new), L.dtype_code(k_new), k_new.stride(0), k_new.stride(1),
+           v_new.stride(0), v_new.stride(1), kp, vp, csb, csh, cst, B, H, D, tcap, L.ptr(t_pos), len(levels),
+           L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]), L.i64_array([t.stride(1) for t in levels]),
+           _ilog2(leaf), _ilog2(arity), pages, L.stream())
 
 
 # ----------------------------------------------------------------------------------------------- decode step
