@@ -349,3 +349,32 @@ def test_fused_groups_are_bit_identical_and_capture():
         assert torch.equal(cap.g_logits, lb), r
         tb = K.argmax_rows(lb)
         assert torch.equal(cap.g_tok, tb), r
+
+
+def test_tree_pass_with_a_plain_getU():
+    """seg.tree_pass given the reference's own kind of getU -- a Python callable gathering node vectors
+    (seg.py:133-134) -- selects what the level-sum source selects, and neighbor_pass likewise."""
+    cfg = tiny(seq_len=256, n_embd=128, wmax=6, local=3)
+    q, k = rnd(2, 2, 256, 64, seed=40).to(DEV), rnd(2, 2, 256, 64, seed=41).to(DEV)
+    kidx = k.float().clone()
+    kidx[:, :, 0] = 0
+    Lm = 7
+    S = seg.level_sums(kidx, Lm, False, 0.25)
+    src = seg.LevelSource(S)
+    tq = torch.arange(256, device=DEV)
+
+    def getU(l, c):      # the reference's closure over the level sums
+        b, H, N, C = c.shape
+        return torch.gather(S[l], 2, c.reshape(b, H, N * C, 1).expand(b, H, N * C, S[l].shape[-1])).view(b, H, N, C, -1)
+
+    a = seg.tree_pass(q, src, tq, Lm, cfg.wmax)
+    b = seg.tree_pass(q, getU, tq, Lm, cfg.wmax)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    NS = cfg.nb_store
+    ids, vld, sct = a
+    st = (ids[..., :NS].to(torch.int32), sct[..., :NS], vld[..., :NS])
+    n1 = seg.neighbor_pass(q, src, *st, tq, cfg)
+    n2 = seg.neighbor_pass(q, lambda c: getU(1, c), *st, tq, cfg, T=256)
+    for x, y in zip(n1, n2):
+        assert torch.equal(x, y)

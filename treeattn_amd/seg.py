@@ -2,8 +2,9 @@
 
 Same names and signatures: gate_apply, level_sums, tree_pass, neighbor_pass, leaves_to_pos, finish,
 select_seg.  The reference's tree_pass/neighbor_pass take a callable getU(l, cand) that gathers node
-vectors; the kernels read node sums in place, so here getU must be one that carries its levels: a
-SegState.getU (engine) or a LevelSource built from level sums.
+vectors.  The kernels read node sums in place: a SegState.getU (engine) or a LevelSource hands them its
+level tensors directly; any other callable is asked once per level for every node of that level
+(getU(l, all node ids)), and the kernel runs on the rows it returns.
 """
 import torch
 
@@ -31,16 +32,25 @@ class LevelSource:
         return [self.S[l] for l in shape.blevels]
 
 
-def _levels_of(getU, shape):
+def _levels_of(getU, shape, q):
     src = getattr(getU, '__self__', None)
-    if src is not None and hasattr(src, 'levels') and hasattr(src, 'shape'):   # SegState.getU
-        if src.shape.blevels[:shape.n_levels] != shape.blevels:
+    if src is not None and hasattr(src, 'levels') and hasattr(src, 'shape') and not getattr(src.cfg, 'gate', False):
+        if src.shape.blevels[:shape.n_levels] != shape.blevels:       # SegState.getU without the gate
             raise ValueError('the cache tree does not match the requested levels')
         return src.levels[:shape.n_levels]
     if isinstance(getU, LevelSource):
         return getU.tree_levels(shape)
-    raise TypeError('treeattn_amd.seg: getU must be a SegState.getU or a LevelSource; the descent kernel '
-                    'reads node sums in place and cannot call back into Python')
+    # any other getU(l, cand) (seg.py:133-134, engine.py:35-39): every node of each level, asked for once
+    b, H = q.shape[0], q.shape[1]
+    out = []
+    for l in shape.blevels:
+        M = shape.T >> l
+        cand = torch.arange(M, device=q.device).view(1, 1, 1, M).expand(b, H, 1, M)
+        U = getU(l, cand)
+        if tuple(U.shape[:4]) != (b, H, 1, M):
+            raise ValueError('getU(l, cand) must return (b, H, Nq, C, dh) node vectors')
+        out.append(U.reshape(b, H, M, U.shape[-1]).float().contiguous())
+    return out
 
 
 @torch.no_grad()
@@ -63,20 +73,27 @@ def tree_pass(q, getU, tq, Lm, wmax):
     if src is not None and hasattr(src, 'shape'):
         T = src.shape.T
     shape = K.TreeShape(T, 2, 2)
-    ids, vld, sct = K.tree_descend(q, _levels_of(getU, shape), tq, shape, wmax)
+    ids, vld, sct = K.tree_descend(q, _levels_of(getU, shape, q), tq, shape, wmax)
     return ids.long(), vld.bool(), sct
 
 
 @torch.no_grad()
-def neighbor_pass(q, getU1, st_leaf, st_score, st_ok, tq, cfg):
-    """seg.py:73-103; getU1 must expose the level-1 sums (LevelSource or a SegState-bound callable)."""
+def neighbor_pass(q, getU1, st_leaf, st_score, st_ok, tq, cfg, T=None):
+    """seg.py:73-103.  getU1(cand) gathers level-1 node vectors: a LevelSource or a SegState method are read in
+    place; another callable is asked once for every level-1 node (T: positions of the tree, default the store's
+    length)."""
     if isinstance(getU1, LevelSource):
         S1 = getU1.S[1]
     else:
         src = getattr(getU1, '__self__', None)
-        if src is None or not hasattr(src, 'level_of'):
-            raise TypeError('neighbor_pass: getU1 must be a LevelSource or a SegState method')
-        S1 = src.level_of(1)
+        if src is not None and hasattr(src, 'level_of') and not getattr(src.cfg, 'gate', False):
+            S1 = src.level_of(1)
+        else:
+            b, H = q.shape[0], q.shape[1]
+            M = (st_leaf.shape[2] if T is None else T) >> 1
+            cand = torch.arange(M, device=q.device).view(1, 1, 1, M).expand(b, H, 1, M)
+            U = getU1(cand)
+            S1 = U.reshape(b, H, M, U.shape[-1]).float().contiguous()
     return SEL.neighbor_pass(q.float(), S1, st_leaf, st_score, st_ok, tq, cfg, 2)
 
 
