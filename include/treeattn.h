@@ -285,6 +285,19 @@ int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, in
              void* ws, int64_t ws_bytes, void* stream);
 
 /*
+ * ta_rowmm with the output tile chosen by the caller: cols = 4, 8, 16 or 32 columns per workgroup of eight
+ * wavefronts (one per K-block stream, operands loaded straight into registers), -1 for the four-wavefront
+ * 32-column tile with X staged in LDS, 0 for the library's choice (what ta_rowmm does: the widest of 32/16/8
+ * columns that still gives every compute unit a workgroup).  Every choice computes the same bits: the same
+ * K-block streams, MFMA chains and stream-order sums (an MFMA output column depends only on its own column of
+ * W).  The tails (ln_next, tok_out) always run on the 32-column tile.
+ */
+int ta_rowmm_ex(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy,
+                const void* R, int64_t ldr, const void* ln_w, float ln_eps, int M, int N, int K,
+                int epilogue, int splits, int cols, const void* ln_next, void* y_ln, int64_t ld_yln,
+                int64_t* tok_out, void* ws, int64_t ws_bytes, void* stream);
+
+/*
  * Logits of a decode step and their greedy token (replaces engine.py:177, F.linear(ln_f(x), wte), and
  * logits.argmax(-1) of the reference's greedy loop, phase2.py:51-66), bf16, for up to 32 rows:
  *   Y[M,N] = LN(X)[M,K] . W[N,K]^T  (LN applied when ln_w != NULL, eps ln_eps), bit for bit ta_rowmm's

@@ -193,6 +193,13 @@ def weights_from_ours(sd, cfg):
     return W
 
 
+def linear_f32_round(x, w):
+    """A linear layer as a float32 product of the operands rounded once to x's dtype: for bf16 operands the
+    same real quantity as F.linear accumulated in another order.  A DecoderRef built with it measures the
+    rounding noise floor of a bf16 op chain against one built with F.linear."""
+    return (x.float() @ w.float().t()).to(x.dtype)
+
+
 class DecoderRef:
     """Token-by-token decoder (engine.py:149-177).  act_dtype=torch.bfloat16 runs the same op chain on
     bf16 activations and weights (the bf16 decode configurations); selection and attention stay fp32."""

@@ -27,6 +27,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from _bf16_floor import BF16_BAR, bf16_bound, f32_then_round
 from oracle import attn_ref as A
 from oracle import seg_ref as S
 from oracle.engine_ref import DecoderRef, descend
@@ -40,7 +41,6 @@ from treeattn_amd.model import GPT
 pytestmark = pytest.mark.gpu
 DEV = 'cuda'
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden')
-BF16_BAR = 2e-2
 FP32_BAR = 1e-5
 
 
@@ -173,12 +173,6 @@ def test_config3_selection_and_attention():
 
 
 # ------------------------------------------------------------------------------------------------ configs 4, 5
-def _f32_then_round(x, w):
-    """A linear layer as a float32 product of the bf16 operands, rounded once to bf16 -- the same real
-    quantity as F.linear on bf16 tensors, accumulated in another order."""
-    return (x.float() @ w.float().t()).to(x.dtype)
-
-
 def _decode_parity(leaf, arity, topk, B, T0, Tcap, steps, ids_seed, sort_dedupe):
     n_layer, H, C, V = 12, 12, 768, 50304
     dh = C // H
@@ -279,7 +273,7 @@ def _decode_parity(leaf, arity, topk, B, T0, Tcap, steps, ids_seed, sort_dedupe)
         refs[0].lin = F.linear
         return torch.stack(res, 1)                                   # (steps, B, V)
     want = run_oracles(F.linear)
-    floor_run = run_oracles(_f32_then_round, follow=want)
+    floor_run = run_oracles(f32_then_round, follow=want)
     tk = tok0.to(DEV)
     got = []
     for s in range(steps):
@@ -297,7 +291,7 @@ def _decode_parity(leaf, arity, topk, B, T0, Tcap, steps, ids_seed, sort_dedupe)
     print('free-running max |dlogit| per step, GPU vs oracle: %s; oracle vs oracle (other accumulation order): %s'
           % (['%.3g' % x for x in d_gpu.amax(1).tolist()], ['%.3g' % x for x in d_floor.amax(1).tolist()]),
           flush=True)
-    bound = max(BF16_BAR, 2.0 * float(d_floor.max()))
+    bound = bf16_bound(d_floor.max())
     assert float(d_gpu.max()) <= bound, (float(d_gpu.max()), bound)
     assert bool((same | (gap <= 2 * d_gpu)).all())
     del dec, refs

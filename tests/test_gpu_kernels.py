@@ -371,6 +371,34 @@ def test_rowmm_matches_op_chain(M, N, KD, ln, epi):
     assert err.max().item() < 0.05 * max(1.0, want.abs().max().item())
 
 
+@pytest.mark.parametrize('M,N,KD,ln,epi,S', [(32, 2304, 768, True, None, 1), (32, 768, 768, False, 'residual', 1),
+                                            (32, 3072, 768, True, 'gelu', 1), (32, 768, 3072, False, 'residual', 4),
+                                            (32, 768, 3072, False, 'residual', 1), (5, 40, 64, True, None, 1),
+                                            (33, 100, 128, False, 'gelu', 2), (17, 1000, 1088, True, 'residual', 1),
+                                            (32, 200, 2048, True, None, 3), (64, 96, 640, True, 'gelu', 1)])
+def test_rowmm_narrow_tiles_are_bit_identical(M, N, KD, ln, epi, S):
+    """Every output tile width of ta_rowmm_ex (eight-wavefront tiles of 4, 8, 16, 32 columns, and the library's
+    choice) computes the four-wavefront 32-column tile's result bit for bit: the same K-block streams, MFMA
+    chains, stream-order and split-order sums, LayerNorm statistics and epilogue."""
+    print('case', M, N, KD, ln, epi, S, flush=True)
+    g = torch.Generator().manual_seed(3 * M + N + KD + S)
+    x = torch.randn(M, KD, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, KD, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    lw = (1 + 0.1 * torch.randn(KD, generator=g)).to(torch.bfloat16).to(DEV) if ln else None
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV) if epi == 'residual' else None
+    ws = K.rowmm_workspace(M, N, KD, S, DEV)
+    want = K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, splits=S, ws=ws, cols=-1)
+    for cols in (32, 16, 8, 4, 0):
+        for _ in range(2):   # the split counters return to zero
+            got = K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=res, splits=S, ws=ws, cols=cols)
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), cols
+    # in place on the residual (out is residual), as the decode step calls it
+    if epi == 'residual':
+        r2 = res.clone()
+        K.rowmm(x, w, ln_w=lw, epilogue=epi, residual=r2, out=r2, splits=S, ws=ws, cols=8)
+        assert torch.equal(r2.view(torch.int16), want.view(torch.int16))
+
+
 def test_argmax_rows_first_maximum():
     x = torch.zeros(3, 50304, dtype=torch.bfloat16)
     x[0, 7] = 1; x[0, 900] = 1

@@ -96,6 +96,8 @@ SIGNATURES = {
     'ta_rowmm_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32]),
     'ta_rowmm': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32, c_i32,
                          c_i32, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
+    'ta_rowmm_ex': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32,
+                            c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'ta_logits_workspace_size': (c_i64, [c_i32, c_i32]),
     'ta_logits': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64,
                           c_vp]),

@@ -25,6 +25,7 @@ SOURCES = {
     'attend_bwd.hip': [],
     'sample.hip': [],
     'gemm.hip': [],
+    'rowmm_nt.hip': [],
     'gather_blocks.hip': [],
     'prefill_attn.hip': [],
     'step.hip': [],

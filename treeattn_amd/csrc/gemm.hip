@@ -262,10 +262,42 @@ extern "C" int64_t ta_rowmm_workspace_size(int M, int N, int K, int splits) {
          (s > 1 ? (int64_t)s * rowmm_tiles(M, N) * 1024 * 4 : 0);
 }
 
+namespace ta {
+int rowmm_narrow(MmArgs a, int nc, bool ln, int epilogue, hipStream_t st);
+}
+
+namespace {
+int device_cus();
+
+// Columns per output tile of the narrow-tile kernel: the narrowest tile (of 4, 8, 16, 32 columns) whose
+// workgroups all fit on the compute units at once (one per unit: a workgroup of the LayerNorm variant takes
+// half of a unit's registers).  Measured at M = 32 with cold weights (per product, launch included): 768 x 768
+// 4.2 us at 4 columns against 5.5 us for the 32-column four-wavefront tile, 768 x 3072 (4 splits) 6.3 against
+// 7.4 us at 16, LayerNorm + 768 x 2304 6.7 against 7.3 us at 16 (8 columns: 288 workgroups, 9.3 us).
+int rowmm_auto_cols(int M, int N, int S) {
+  const int cus = device_cus();
+  int nc = 4;
+  while (nc < 32 && (int64_t)((N + nc - 1) / nc) * ((M + 31) / 32) * S > cus) nc *= 2;
+  return nc;
+}
+}  // namespace
+
 extern "C" int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy,
                         const void* R, int64_t ldr, const void* ln_w, float ln_eps, int M, int N, int K,
                         int epilogue, int splits, const void* ln_next, void* y_ln, int64_t ld_yln,
                         int64_t* tok_out, void* ws, int64_t ws_bytes, void* stream) {
+  return ta_rowmm_ex(X, ldx, W, ldw, Y, ldy, R, ldr, ln_w, ln_eps, M, N, K, epilogue, splits, 0, ln_next, y_ln,
+                     ld_yln, tok_out, ws, ws_bytes, stream);
+}
+
+extern "C" int ta_rowmm_ex(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy,
+                           const void* R, int64_t ldr, const void* ln_w, float ln_eps, int M, int N, int K,
+                           int epilogue, int splits, int cols, const void* ln_next, void* y_ln, int64_t ld_yln,
+                           int64_t* tok_out, void* ws, int64_t ws_bytes, void* stream) {
+  if (cols != 0 && cols != -1 && cols != 4 && cols != 8 && cols != 16 && cols != 32) {
+    set_error("ta_rowmm_ex: cols must be 0 (automatic), -1 (four-wavefront 32-column tile), 4, 8, 16 or 32");
+    return TA_ERR_ARG;
+  }
   if (M <= 0 || N <= 0 || K <= 0 || K % 64 || ldx < K || ldw < K || ldy < N ||
       (epilogue == EPI_RESIDUAL && (R == nullptr || ldr < N)) || epilogue < 0 || epilogue > 2) {
     set_error("ta_rowmm: bad sizes (K must be a multiple of 64)");
@@ -316,6 +348,16 @@ extern "C" int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, 
   t.tok_out = tok_out;
   dim3 grid((N + 31) / 32, (M + 31) / 32, S);
   hipStream_t st = (hipStream_t)stream;
+  // the narrow-tile kernel computes the same bits; the tails run on the four-wavefront tile
+  // (the narrow tile stages the LayerNorm weight in LDS: K up to 2048 with the prologue)
+  int nc = tail != TAIL_NONE || cols == -1 || (ln_w != nullptr && K > 2048) ? 0
+                                                                          : (cols ? cols : rowmm_auto_cols(M, N, S));
+  while (S > 1 && nc > 0 && nc < 32 && (int64_t)((N + nc - 1) / nc) * ((M + 31) / 32) * 4 > kRowmmCountBytes)
+    nc *= 2;   // one arrival counter per output tile
+  if (nc > 0 && device_cus() <= 0) {
+    set_error("ta_rowmm: cannot query the device");
+    return TA_ERR_LAUNCH;
+  }
   MmArgs a{};
   a.X = (const bf16_t*)X; a.ldx = ldx;
   a.W = (const bf16_t*)W; a.ldw = ldw;
@@ -326,6 +368,7 @@ extern "C" int ta_rowmm(const void* X, int64_t ldx, const void* W, int64_t ldw, 
   a.splits = S;
   a.tiles = (int)rowmm_tiles(M, N);
   a.part = part; a.cnt = cnt;
+  if (nc > 0) return rowmm_narrow(a, nc, ln_w != nullptr, epilogue, st);
   int b0, nb0;
   mm_split_range(K, S, 0, b0, nb0);   // the first split has the most blocks
   const size_t lds = (size_t)mm_lds_bytes(nb0);

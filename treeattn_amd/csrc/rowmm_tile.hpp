@@ -166,6 +166,24 @@ __device__ __forceinline__ uint64_t mm_argmax_key(float v, int col) {
   return ((uint64_t)u << 32) | (uint32_t)(0x7FFFFFFF - col);
 }
 
+// LayerNorm row statistics from the sums of x and x^2 over n elements: written once, with contraction off, so
+// that every kernel normalising rows computes the same bits.
+__device__ __forceinline__ void mm_stats(float s, float s2, int n, float eps, float& mean, float& rstd) {
+#pragma clang fp contract(off)
+  mean = s / (float)n;
+  rstd = rsqrtf(fmaxf(s2 / (float)n - mean * mean, 0.0f) + eps);
+}
+
+// The epilogue of one output element: the float32 product rounded to bf16, then GELU (erf form, model.py:30)
+// of that value rounded again, or the residual (a bf16 value as float32) plus it rounded.
+template <int EPI>
+__device__ __forceinline__ bf16_t mm_epilogue(float acc, float res) {
+  float v = mm_bf16_round(acc);
+  if constexpr (EPI == EPI_GELU) v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+  if constexpr (EPI == EPI_RESIDUAL) v = res + v;
+  return bf16_from(v);
+}
+
 __device__ __forceinline__ void mm_add8(uint4 u, float& s, float& s2) {
   const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -201,8 +219,8 @@ __device__ __forceinline__ void mm_rows_ln(const bf16_t* Y, int64_t ldy, int M, 
     }
     s = group_sum<8>(s);
     s2 = group_sum<8>(s2);
-    const float mean = s / (float)N;
-    const float rstd = rsqrtf(fmaxf(s2 / (float)N - mean * mean, 0.0f) + eps);
+    float mean, rstd;
+    mm_stats(s, s2, N, eps, mean, rstd);
     if (!ok) continue;
     bf16_t* yn = Yn + (int64_t)r * ldyn + 8 * part;
     for (int k = 0; k < N; k += 64) {
@@ -286,8 +304,8 @@ __device__ __forceinline__ void mm_ln_staged(bf16_t* xs, const bf16_t* gs, int r
     if (blk < rn) mm_add8(xv[blk], s, s2);
   s = group_sum<8>(s);
   s2 = group_sum<8>(s2);
-  const float mean = s / (float)K;
-  const float rstd = rsqrtf(fmaxf(s2 / (float)K - mean * mean, 0.0f) + eps);
+  float mean, rstd;
+  mm_stats(s, s2, K, eps, mean, rstd);
   // four blocks at a time: their weight pieces read together, then the transforms, then the stores
 #pragma unroll
   for (int b4 = 0; b4 < kMmRound; b4 += 4) {
@@ -390,9 +408,10 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
     s = group_sum<8>(s);
     s2 = group_sum<8>(s2);
     if (part == 0) {
-      const float mean = s / (float)a.K;
+      float mean, rstd;
+      mm_stats(s, s2, a.K, a.eps, mean, rstd);
       s_mean[r] = mean;
-      s_rstd[r] = rsqrtf(fmaxf(s2 / (float)a.K - mean * mean, 0.0f) + a.eps);
+      s_rstd[r] = rstd;
     }
   }
 
@@ -529,10 +548,7 @@ __device__ __forceinline__ bool mm_tile(const MmArgs& a, int tn, int tm, int spl
     const int r = e >> 5, c = e & 31;
     const int gm = m0 + r, gn = n0 + c;
     const bool in = gm < a.M && gn < a.N;
-    float v = mm_bf16_round(vals[k]);
-    if constexpr (EPI == EPI_GELU) v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-    if constexpr (EPI == EPI_RESIDUAL) v = rres[k] + v;
-    const bf16_t o = bf16_from(v);
+    const bf16_t o = mm_epilogue<EPI>(vals[k], rres[k]);
     if (in) {
       bf16_t* y = a.Y + (int64_t)gm * a.ldy + gn;
       if constexpr (WT) stg2_dc(y, o.bits);

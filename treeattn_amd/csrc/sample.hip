@@ -116,11 +116,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
         for (int k = 0; k < C; k += 64) mm_add8(*reinterpret_cast<const uint4*>(srow + k + 8 * threadIdx.x), s, s2);
         s = group_sum<8>(s);
         s2 = group_sum<8>(s2);
-        if (threadIdx.x == 0) {
-          const float mean = s / (float)C;
-          s_stat[0] = mean;
-          s_stat[1] = rsqrtf(fmaxf(s2 / (float)C - mean * mean, 0.0f) + eps);
-        }
+        if (threadIdx.x == 0) mm_stats(s, s2, C, eps, s_stat[0], s_stat[1]);
       }
       __syncthreads();
       const float mean = s_stat[0], rstd = s_stat[1];

@@ -379,12 +379,13 @@ def rowmm_workspace(M, N, K, splits, device):
 
 
 def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None, splits=1, ws=None, ln_next=None,
-          out_ln=None, tok_out=None):
+          out_ln=None, tok_out=None, cols=0):
     """epilogue(LN(x) @ w.T) for a few rows, bf16: x (M,K), w (N,K) -> (M,N).  epilogue None | 'gelu' |
     'residual' (adds `residual`, (M,N)); `out` may be `residual`.  splits > 1 divides K among workgroups.
     ln_next: also out_ln = LN(result) with that weight (for the next product); tok_out: also the greedy token of
     every row (int64 (M,)).  splits > 1 and the tails need `ws` from rowmm_workspace (one workspace serves calls
-    that run one after another)."""
+    that run one after another).  cols: output columns per workgroup (ta_rowmm_ex: 0 the library's choice, -1
+    the 32-column four-wavefront tile, 4/8/16/32 the eight-wavefront tile); every choice gives the same bits."""
     L.require_gpu(x, w)
     M, K = x.shape
     N = w.shape[0]
@@ -397,9 +398,9 @@ def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None, spl
     if tok_out is not None and (tok_out.dtype != torch.long or not tok_out.is_contiguous() or tok_out.numel() != M):
         raise ValueError('rowmm: tok_out must be contiguous int64 (M,)')
     r = residual if epilogue == 'residual' else None
-    L.call('ta_rowmm', L.ptr(x), x.stride(0), L.ptr(w), w.stride(0), L.ptr(out), out.stride(0), L.ptr(r),
+    L.call('ta_rowmm_ex', L.ptr(x), x.stride(0), L.ptr(w), w.stride(0), L.ptr(out), out.stride(0), L.ptr(r),
            r.stride(0) if r is not None else 0, L.ptr(ln_w), float(eps), M, N, K, _EPI[epilogue], int(splits),
-           L.ptr(ln_next), L.ptr(out_ln if ln_next is not None else None),
+           int(cols), L.ptr(ln_next), L.ptr(out_ln if ln_next is not None else None),
            out_ln.stride(0) if ln_next is not None else 0, L.ptr(tok_out), L.ptr(ws),
            ws.numel() if ws is not None else 0, L.stream())
     return (out, out_ln) if ln_next is not None else out
