@@ -61,15 +61,28 @@ __device__ __forceinline__ KvRows append_rows(const AppendIn& ap, int b, int h, 
 // kbase/vbase and rows locate the rows of this (sequence, head) in the caches (rows.blog2 = leaf_log2); a
 // row without a page is not written.  level(j) returns tree level j's node rows (D floats each) for this
 // (sequence, head); tree level j has binary level leaf_log2 + j * arity_log2.
+// The loads append_dim starts with (dimension d of the new K and V rows, row t's offset in the caches), split
+// off so that a caller can issue them early and store later (append_dim_with).
+template <typename T>
+struct AppendPre {
+  T kx, vx;
+  int64_t ot;
+};
+template <typename T>
+__device__ __forceinline__ AppendPre<T> append_prefetch(int d, int t, const T* __restrict__ kn,
+                                                        const T* __restrict__ vn, const KvRows& rows) {
+  return AppendPre<T>{kn[d], vn[d], rows.off(t)};
+}
+
 template <typename T, typename LevelFn>
-__device__ __forceinline__ void append_dim(int d, int D, int t, const T* __restrict__ kn, const T* __restrict__ vn,
-                                           T* kbase, T* vbase, const KvRows& rows, int n_levels, int leaf_log2,
-                                           int arity_log2, float* stk, LevelFn level) {
-  const T kx = kn[d];
-  const int64_t ot = rows.off(t);
+__device__ __forceinline__ void append_dim_with(int d, int D, int t, const AppendPre<T>& pre, T* kbase, T* vbase,
+                                                const KvRows& rows, int n_levels, int leaf_log2, int arity_log2,
+                                                float* stk, LevelFn level) {
+  const T kx = pre.kx;
+  const int64_t ot = pre.ot;
   if (ot < 0) return;   // no page for row t: nothing stored, no node formed
   kbase[ot + d] = kx;
-  vbase[ot + d] = vn[d];
+  vbase[ot + d] = pre.vx;
   if (n_levels == 0) return;
   const int leaf = 1 << leaf_log2;
   if (((t + 1) & (leaf - 1)) != 0) return;
@@ -117,6 +130,14 @@ __device__ __forceinline__ void append_dim(int d, int D, int t, const T* __restr
     }
     level(j)[node * D + d] = x;
   }
+}
+
+template <typename T, typename LevelFn>
+__device__ __forceinline__ void append_dim(int d, int D, int t, const T* __restrict__ kn, const T* __restrict__ vn,
+                                           T* kbase, T* vbase, const KvRows& rows, int n_levels, int leaf_log2,
+                                           int arity_log2, float* stk, LevelFn level) {
+  append_dim_with<T>(d, D, t, append_prefetch<T>(d, t, kn, vn, rows), kbase, vbase, rows, n_levels, leaf_log2,
+                     arity_log2, stk, level);
 }
 
 }  // namespace ta

@@ -93,17 +93,24 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void seg_attend_kernel(Attn
     const int pos = tid == 0 ? 0 : t - (tid - 1);
     if (pos >= 0) pre = ptrow[pos >> p.leaf_log2];
   }
-  if (tid < D && t >= 0 && t < ap.Tcap) {
-    T *kbase, *vbase;
-    const KvRows rows = append_rows<T>(ap, b, h, lv.blevel[0], kbase, vbase);
-    append_dim<T>(tid, D, t, reinterpret_cast<const T*>(ap.kn) + b * ap.nsb + h * ap.nsh,
-                  reinterpret_cast<const T*>(ap.vn) + b * ap.vnsb + h * ap.vnsh, kbase, vbase, rows, n_levels,
-                  lv.blevel[0], arity_log2, stk,
-                  [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
+  // The descent reads only nodes that end before t and the cache append writes row t and the nodes ending at
+  // t, so the append's loads (the new rows, row t's page) are issued first and its stores follow the descent:
+  // the first level's node rows are requested at once and the append is off that chain.
+  const bool appends = tid < D && t >= 0 && t < ap.Tcap;
+  T *kbase = nullptr, *vbase = nullptr;
+  KvRows rows{};
+  AppendPre<T> apre{};
+  if (appends) {
+    rows = append_rows<T>(ap, b, h, lv.blevel[0], kbase, vbase);
+    apre = append_prefetch<T>(tid, t, reinterpret_cast<const T*>(ap.kn) + b * ap.nsb + h * ap.nsh,
+                              reinterpret_cast<const T*>(ap.vn) + b * ap.vnsb + h * ap.vnsh, rows);
   }
   const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh;
   int nk = descend_query<T, D, kWavesPerBlock>(qrow, t, Tgeo, b, h, lv, n_levels, arity_log2, wmax, tid, ckey, cid,
                                                csc, kid, ksc, ptrow, cpg, kpg);
+  if (appends)
+    append_dim_with<T>(tid, D, t, apre, kbase, vbase, rows, n_levels, lv.blevel[0], arity_log2, stk,
+                       [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
   if (ptrow != nullptr && tid < 32) s_pre[tid] = pre;
   const int nkw = nk < p.wl ? nk : p.wl;   // the attention of the separate kernels sees the first wl of them
   // the appended row is visible to every wavefront: its stores (long since done) are waited for, then the
