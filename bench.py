@@ -35,7 +35,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--config', type=int, default=4, choices=(1, 3, 4, 5))
+    ap.add_argument('--config', type=int, default=4, choices=(1, 2, 3, 4, 5))
     ap.add_argument('--steps', type=int, default=None)
     ap.add_argument('--warmup', type=int, default=None)
     ap.add_argument('--batch', type=int, default=None)
@@ -66,7 +66,9 @@ def parse():
                1: dict(steps=256, warmup=0, batch=1, context=512, tcap=1024, leaf=32, arity=2, topk=8,
                        prefill_chunk=1, ids_seed=0),
                3: dict(steps=5, warmup=2, batch=4, context=16384, tcap=16384, leaf=64, arity=2, topk=32,
-                       prefill_chunk=1, ids_seed=2)}
+                       prefill_chunk=1, ids_seed=2),
+               2: dict(steps=20, warmup=3, batch=8, context=4096, tcap=4096, leaf=64, arity=2, topk=16,
+                       prefill_chunk=1, ids_seed=1)}
     for k, v in presets[args.config].items():
         if getattr(args, k, None) is None:
             setattr(args, k, v)
@@ -100,13 +102,17 @@ def descent_nodes(t, shape, wmax):
 def recorded_traffic(name):
     """HBM bytes per launch of a kernel from the committed rocprofv3 counter summary (FETCH_SIZE and
     WRITE_SIZE passes scaled by a calibration copy), or None when not recorded."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'decode_attention_traffic.md')
+    pdir = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles')
     try:
-        for line in open(path):
-            if line.startswith('traffic_bytes_per_launch ' + name + ':'):
-                return int(line.split(':')[1])
+        names = sorted(os.listdir(pdir))
     except OSError:
         return None
+    for fn in names:
+        if not fn.endswith('.md'):
+            continue
+        for line in open(os.path.join(pdir, fn)):
+            if line.startswith('traffic_bytes_per_launch ' + name + ':'):
+                return int(line.split(':')[1])
     return None
 
 
@@ -127,14 +133,22 @@ def time_launches(fn, iters, flush=None):
     return 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / iters
 
 
-def gather_dot_leg(args):
-    from treeattn_amd import kernels as K
+def gather_dot_inputs():
+    """Config 2: Q, K (8,12,4096,64) bf16 ~ N(0,1); leaf-block ids (8,12,4096,16) int32 drawn uniformly over the
+    causally valid blocks of 64 (block 0 below position 64), seed 1; generated on the CPU."""
     B, H, T, D, NB, blk = 8, 12, 4096, 64, 16, 64
     g = torch.Generator().manual_seed(1)
     q = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16)
     k = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16)
     nvalid = torch.clamp(torch.arange(T) // blk, min=1).view(1, 1, T, 1).float()
     idx = (torch.rand(B, H, T, NB, generator=g) * nvalid).floor().to(torch.int32)
+    return q, k, idx, blk
+
+
+def gather_dot_leg(args, keep=False):
+    from treeattn_amd import kernels as K
+    q, k, idx, blk = gather_dot_inputs()
+    B, H, T, NB = idx.shape
     q, k, idx = q.cuda(), k.cuda(), idx.cuda()
     out = torch.empty(B, H, T, NB * blk, device='cuda')
     for _ in range(3):
@@ -142,9 +156,51 @@ def gather_dot_leg(args):
     us = time_launches(lambda: K.gather_dot_blocks(q, k, idx, blk, 1.0, out=out), 20)
     nbytes = q.numel() * 2 + k.numel() * 2 + idx.numel() * 4 + out.numel() * 4
     gbs = nbytes / (us * 1e-6) / 1e9
-    return {'workload': 'gather_dot Q,K (8,12,4096,64) bf16, 16 blocks of 64 per query, out fp32 (8,12,4096,1024)',
-            'bytes_per_call': nbytes, 'avg_us': round(us, 1), 'GB/s': round(gbs, 1),
-            'frac_of_hbm': round(gbs / HBM_PEAK_GBS, 4)}
+    res = {'workload': 'gather_dot Q,K (8,12,4096,64) bf16, 16 blocks of 64 per query, out fp32 (8,12,4096,1024)',
+           'bytes_per_call': nbytes, 'avg_us': round(us, 1), 'GB/s': round(gbs, 1),
+           'frac_of_hbm': round(gbs / HBM_PEAK_GBS, 4)}
+    return (res, (q, k, idx, blk, out)) if keep else res
+
+
+def gather_dot_bench(args):
+    """Config 2, the isolated gather-dot op: one JSON line of its own (GB/s of the compulsory bytes), the oracle's
+    gather-dot (reference op chain, torch CPU) timed on one (b, h) slice beside it, and that slice's parity."""
+    from oracle.attn_ref import gather_dot_blocks as gd_ref
+    leg, (q, k, idx, blk, out) = gather_dot_leg(args, keep=True)
+    B, H, T, NB = idx.shape
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    qc, kc, ic = q[0:1, 0:1].cpu(), k[0:1, 0:1].cpu(), idx[0:1, 0:1].cpu()
+    want = gd_ref(qc, kc, ic, blk)                                  # canonical order, float32
+    got = out[0:1, 0:1].cpu()
+    rel = ((got - want).abs().max() / want.abs().max().clamp(min=1e-30)).item()
+    # the reference's own op chain ((q * U).sum(-1), fastseg.py:120-122) over the slice in 512-query tiles
+    from oracle.attn_ref import gather_dot as gd_chain
+    cand = (ic.long().unsqueeze(-1) * blk + torch.arange(blk)).reshape(1, 1, T, NB * blk)
+    times = []
+    for rep in range(3):
+        t0 = time.perf_counter()
+        for n0 in range(0, T, 512):
+            gd_chain(qc[:, :, n0:n0 + 512], kc, cand[:, :, n0:n0 + 512], 1.0)
+        times.append(time.perf_counter() - t0)
+    slice_s = sorted(times)[1]
+    bytes_slice = leg['bytes_per_call'] / (B * H)
+    res = {'metric': 'gather-dot GB/s (config 2, isolated op) as % of 8 TB/s HBM', 'value': leg['GB/s'],
+           'unit': 'GB/s', 'n_gpus': 1, 'steps': 20, 'warmup': 3, 'ms_per_step': round(leg['avg_us'] / 1000, 4),
+           'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16 in, f32 out',
+           'data': 'synthetic (N(0,1) q and k, uniform causally valid block ids, seed 1)',
+           'config': {'workload': leg['workload'], 'bytes_per_call': leg['bytes_per_call']},
+           'roofline': {'bound': 'hbm', 'kernel': 'gather_blocks_kernel (matrix-core block gather-dot)',
+                        'achieved': leg['GB/s'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': leg['frac_of_hbm'],
+                        'traffic': recorded_traffic('gather_blocks_kernel'), 'bytes_per_launch': leg['bytes_per_call'],
+                        'avg_us': leg['avg_us'], 'timing': 'cold caches (1 GiB read before each of 20 launches)'},
+           'parity': {'slice': [0, 0], 'max_rel_err_vs_oracle': float('%.3g' % rel), 'bar': 2e-5},
+           'cpu_baseline': {'value': round(bytes_slice / slice_s / 1e9, 3), 'unit': 'GB/s', 'cores': ncores,
+                            'kind': 'port',
+                            'sample': 'oracle gather_dot (the reference op chain, torch CPU) over one of the %d '
+                                      '(b, h) slices (4096 queries in 512-query tiles), median of 3; GB/s of that '
+                                      'slice\'s compulsory bytes' % (B * H)}}
+    return res
 
 
 def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64):
@@ -537,6 +593,8 @@ def prefill_attention_bench(args):
     keys_total = float(keys.double().sum())
     flops = 4.0 * D * keys_total
     tflops = flops / (a_us * 1e-6) / 1e12
+    mfma_peak = K.mfma_peak()
+    log('attention %.1f TFLOP/s useful; matrix-core peak measured %.1f TFLOP/s' % (tflops, mfma_peak))
     attn_bytes = keys_total * D * 2 * 2 + B * H * T * (2 * D * 2 + wl * 5)
     log('config 3: build %.1f us, descent %.1f us, attention %.1f us (%.1f TFLOP/s)' % (b_us, d_us, a_us, tflops))
 
@@ -575,6 +633,9 @@ def prefill_attention_bench(args):
             'roofline': {'bound': 'mfma', 'kernel': 'prefill_attn_kernel<bf16_t, 128, 6> (matrix-core prefill attention)',
                          'achieved': round(tflops, 2), 'peak': MFMA_BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                          'frac': round(tflops / MFMA_BF16_PEAK_TFLOPS, 5), 'traffic': None,
+                         'peak_measured': round(mfma_peak, 1),
+                         'peak_measured_how': 'ta_mfma_peak: 4 workgroups per CU, four independent '
+                                              'v_mfma_f32_32x32x16_bf16 chains per wavefront on registers',
                          'flops_per_launch': flops, 'keys_per_query': round(keys_total / (B * H * T), 1),
                          'gathered_bytes_per_launch': int(attn_bytes),
                          'gathered_GB/s': round(attn_bytes / (a_us * 1e-6) / 1e9, 1)},
@@ -596,6 +657,8 @@ def main():
         res = decode_bench(args)
     elif args.config == 1:
         res = small_model_bench(args)
+    elif args.config == 2:
+        res = gather_dot_bench(args)
     else:
         res = prefill_attention_bench(args)
     print(json.dumps(res), flush=True)

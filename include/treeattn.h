@@ -401,6 +401,14 @@ int ta_decode_step(const ta_step_launch* launch, void* ws, const int64_t* tok, i
                    int advance, void* logits, int64_t ld_logits, float* keys, int64_t* trace, void* stream);
 int ta_decode_step_error(const void* ws, int* error, void* stream);
 
+/*
+ * Calibration (no counterpart in the reference): wgs workgroups of four wavefronts each run 4 * iters
+ * v_mfma_f32_32x32x16_bf16 instructions (32768 flops each) on register operands, no memory traffic; timing the
+ * launch gives the dense bf16 matrix-core throughput the GPU sustains, the peak a kernel's MFMA utilisation is
+ * set against.  out: wgs floats (written only in a case that does not occur; it keeps the work alive).
+ */
+int ta_mfma_peak(int wgs, int iters, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

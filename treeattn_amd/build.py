@@ -29,6 +29,7 @@ SOURCES = {
     'gather_blocks.hip': [],
     'prefill_attn.hip': [],
     'step.hip': [],
+    'calib.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

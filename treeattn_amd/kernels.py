@@ -588,3 +588,27 @@ class DecodeStep:
         e = ctypes.c_int(0)
         L.call('ta_decode_step_error', L.ptr(self.ws), ctypes.byref(e), L.stream())
         return e.value
+
+
+def mfma_peak(wgs=None, iters=20000, reps=5):
+    """Dense bf16 matrix-core throughput this GPU sustains (TFLOP/s), from ta_mfma_peak: wgs workgroups of four
+    wavefronts (default 4 per compute unit), each wavefront 4 * iters MFMA instructions of 32768 flops; the best
+    of `reps` launches timed with HIP events on the current stream."""
+    if not torch.cuda.is_available():
+        raise RuntimeError('mfma_peak: needs the GPU')
+    if wgs is None:
+        wgs = 4 * torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    out = torch.empty(wgs, device='cuda')
+    st = torch.cuda.current_stream()
+    best = None
+    for r in range(reps + 1):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        L.call('ta_mfma_peak', int(wgs), int(iters), L.ptr(out), L.stream())
+        b.record(st)
+        torch.cuda.synchronize()
+        if r > 0:
+            ms = a.elapsed_time(b)
+            best = ms if best is None else min(best, ms)
+    flops = wgs * 4 * 4 * iters * 32768.0
+    return flops / (best * 1e-3) / 1e12
