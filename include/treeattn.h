@@ -402,6 +402,29 @@ int ta_decode_step(const ta_step_launch* launch, void* ws, const int64_t* tok, i
 int ta_decode_step_error(const void* ws, int* error, void* stream);
 
 /*
+ * Neighbour borrowing (replaces seg.py:73-103 neighbor_pass and fastseg.py:274-299 neighbor_pass_fast, and with
+ * lhat the budget split of seg.py:111-117).  For every query n of (b, h) at position t = tq[b * tq_sb + n]: the
+ * S = nb_window * nb_store stored slots of positions t - 1 .. t - nb_window (slot s: position t - (s / nb_store
+ * + 1), entry s % nb_store of st_*), each stored leaf scored against q with the canonical float32 dot times
+ * scale (the gather-dot's order; ids clamped into [0, M)); match = valid and score >= base - nb_rho * |base|;
+ * rate = matches / max(valid, 1) over the first nb_probe * nb_store slots; a slot of neighbour back is kept
+ * when back <= nb_cap_min + round_half_even((nb_window - nb_cap_min) * rate); none when neighbors == 0.
+ * Outputs: nid (B, H, Nq, S) int32 the stored leaf ids (0 for an empty slot), match (uint8), nL (B, H, Nq)
+ * distinct matched leaves, and with lhat (budgets, int32 (B, H, Nq)) n_tree = 0 if nL >= L else max(L - nL,
+ * 2 if nL < ceil(L / 2) else 1), at most wmax.
+ * q: (B, H, Nq, D) of q_dtype, D 16, 32, 64, 128 or 256; S0: the leaf-level node sums (B, H, M, D) float32 (batch and head
+ * strides ssb, ssh); st_leaf int32 / st_score float32 / st_ok uint8 (B, H, Tst, nb_store) with element strides
+ * st_sb, st_sh, st_st; S <= 64.
+ */
+int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const float* S0,
+                     int64_t ssb, int64_t ssh, int M, const int32_t* st_leaf, const float* st_score,
+                     const uint8_t* st_ok, int64_t st_sb, int64_t st_sh, int64_t st_st, int Tst,
+                     const int32_t* tq, int64_t tq_sb, int B, int H, int Nq, int D, int nb_window,
+                     int nb_store, int nb_probe, int nb_cap_min, float nb_rho, int neighbors, float scale,
+                     const int32_t* lhat, int wmax, int32_t* nid, uint8_t* match, int32_t* nL,
+                     int32_t* n_tree, void* stream);
+
+/*
  * Calibration (no counterpart in the reference): wgs workgroups of four wavefronts each run 4 * iters
  * v_mfma_f32_32x32x16_bf16 instructions (32768 flops each) on register operands, no memory traffic; timing the
  * launch gives the dense bf16 matrix-core throughput the GPU sustains, the peak a kernel's MFMA utilisation is

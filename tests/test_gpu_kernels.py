@@ -730,3 +730,47 @@ def test_bf16_rounding_matches_torch_all_floats():
         gf = got.view(torch.bfloat16)
         assert bool(torch.isnan(gf[nan]).all()), 'chunk %d: NaN lost' % c
         del bits, f, got, want, nan, same, gf
+
+
+@pytest.mark.parametrize('D,dtype,Wn,NS,probe,cap_min,leaf,neighbors,with_lhat',
+                         [(64, torch.float32, 8, 2, 3, 2, 2, True, False),
+                          (128, torch.bfloat16, 4, 3, 5, 1, 8, True, True),
+                          (64, torch.float32, 8, 2, 3, 2, 2, False, True),
+                          (64, torch.float16, 16, 4, 2, 3, 4, True, True)])
+def test_neighbor_pass_kernel(D, dtype, Wn, NS, probe, cap_min, leaf, neighbors, with_lhat):
+    """ta_neighbor_pass against the oracle's neighbour pass (seg.py:73-103, canonical dot) and budget split
+    (seg.py:111-117): stored ids with many repeats (distinct counts), empty slots, queries near position 0
+    (fewer than Wn neighbours), stored scores near the current ones (matches and misses), neighbours off, S up
+    to 64 slots.  Ids, match masks, nL and n_tree exact."""
+    print('case', D, dtype, Wn, NS, probe, cap_min, leaf, neighbors, with_lhat, flush=True)
+    cfg = Config(nb_window=Wn, nb_store=NS, nb_probe=probe, nb_cap_min=cap_min, nb_rho=0.35, neighbors=neighbors,
+                 wmax=8)
+    g = torch.Generator().manual_seed(D + Wn + NS + probe)
+    b, H, Nq, M, Tst = 2, 3, 96, 40, 96
+    q = torch.randn(b, H, Nq, D, generator=g).to(dtype)
+    S0 = torch.randn(b, H, M, D, generator=g)
+    st_leaf = torch.randint(0, 12, (b, H, Tst, NS), generator=g, dtype=torch.int32)   # many repeats
+    st_ok = torch.rand(b, H, Tst, NS, generator=g) < 0.8
+    tq = torch.cat([torch.arange(0, 12), torch.randint(12, Tst, (Nq - 12,), generator=g)])
+    # stored scores: around the first query's scores of the stored leaves
+    U = S.gather_nodes(S0, st_leaf.long())                                       # (b,H,Tst,NS,D)
+    cur = S.dot_canonical(q.float()[:, :, :1].expand(b, H, Tst, D).contiguous(), U) / float(leaf)
+    st_score = cur * (1.0 + 0.6 * torch.randn(b, H, Tst, NS, generator=g))
+    lhat = torch.tensor(cfg.beam_classes)[torch.randint(0, len(cfg.beam_classes), (b, H, Nq), generator=g)]
+    getU1 = lambda ids: S.gather_nodes(S0, ids.long())
+    w_ids, w_match, w_nL = S.neighbor_pass(q.float(), getU1, st_leaf.long(), st_score, st_ok, tq, cfg, leaf,
+                                           dot=S.dot_canonical)
+    out = K.neighbor_pass(q.to(DEV), S0.to(DEV), st_leaf.to(DEV), st_score.to(DEV), st_ok.to(DEV), tq.to(DEV), cfg,
+                          leaf, lhat=lhat.to(DEV) if with_lhat else None)
+    nid, match, nL = out[:3]
+    assert torch.equal(match.cpu(), w_match)
+    assert torch.equal(nL.cpu().long(), w_nL)
+    # ids of the valid slots (the reference gathers slot 0's position for queries before position Wn)
+    back = torch.arange(1, Wn + 1).repeat_interleave(NS)
+    inside = (tq.view(Nq, 1) - back.view(1, -1)) >= 0
+    assert torch.equal(torch.where(inside, nid.cpu().long(), 0), torch.where(inside, w_ids, 0))
+    if with_lhat:
+        ids0 = torch.zeros(b, H, Nq, 1, dtype=torch.long)
+        want = S.finish(ids0, ids0 >= 0, w_ids, w_match, w_nL, lhat, cfg, leaf)['n_tree']
+        assert torch.equal(out[3].cpu().long(), want)
+    print('matched slots %d of %d, mean nL %.2f' % (int(w_match.sum()), w_match.numel(), w_nL.float().mean()))

@@ -99,6 +99,9 @@ SIGNATURES = {
     'ta_rowmm_ex': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32,
                             c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'ta_mfma_peak': (c_i32, [c_i32, c_i32, c_vp, c_vp]),
+    'ta_neighbor_pass': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp,
+                                 c_i64, c_i64, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                 c_i32, c_i32, c_f32, c_i32, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'ta_logits_workspace_size': (c_i64, [c_i32, c_i32]),
     'ta_logits': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64,
                           c_vp]),

@@ -30,6 +30,7 @@ SOURCES = {
     'prefill_attn.hip': [],
     'step.hip': [],
     'calib.hip': [],
+    'neighbor.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

@@ -1,0 +1,173 @@
+// Neighbour borrowing (reference-default selection mode): each query takes the leaf groups that the nearest
+// earlier queries stored and keeps those it also scores well on.
+//
+// Reference functions replaced: seg.py:73-103 neighbor_pass, fastseg.py:274-299 neighbor_pass_fast, and the
+// budget split of seg.py:111-117 (finish) when a budget is given.
+//
+// One wavefront per query.  Lane s < S = Wn * NS holds stored slot s: neighbour back = s / NS + 1 (position
+// t - back), entry e = s % NS of that position's stored leaves.  The slots' leaf rows are scored by 16-lane
+// groups with the canonical float32 dot (canon_dot: the same order as the descent and the gather-dot kernel),
+// times the scale.  Then, per lane and with ballots over the slots:
+//   ok0   = position >= 0 and the stored entry valid
+//   match = ok0 and score >= base - rho * |base|          (each product and difference rounded to float32)
+//   rate  = matches / max(valid, 1) over the first probe * NS slots (float32 division)
+//   cap   = cap_min + round_half_even((Wn - cap_min) * rate);  match &= back <= cap;  all off without neighbours
+//   nL    = distinct leaf ids among the matched slots
+//   n_tree (with a budget L) = 0 if nL >= L, else max(L - nL, 2 if nL < ceil(L / 2) else 1), at most wmax.
+#include "descend.hpp"
+
+namespace ta {
+
+struct NbParams {
+  const void* q;              // (B, H, Nq, D) rows, element strides qsb, qsh, qsn
+  int64_t qsb, qsh, qsn;
+  const float* S0;            // leaf-level node sums (B, H, M, D) float32, rows contiguous
+  int64_t ssb, ssh;
+  int M;
+  const int32_t* st_leaf;     // (B, H, Tst, NS) stored leaves, int32
+  const float* st_score;      // their scores
+  const uint8_t* st_ok;       // their validity (bytes)
+  int64_t st_sb, st_sh, st_st;   // element strides (the NS entries of a position contiguous)
+  int Tst;
+  const int32_t* tq;          // positions (B, Nq), row stride tq_sb (0: one row shared by every sequence)
+  int64_t tq_sb;
+  int B, H, Nq;
+  int Wn, NS, probe, cap_min, neighbors;
+  float rho, scale;
+  const int32_t* lhat;        // budgets per query (B, H, Nq) or null
+  int wmax;
+  int32_t* nid;               // out (B, H, Nq, Wn * NS): stored leaf ids (0 where the slot is empty)
+  uint8_t* match;             // out: matched slots
+  int32_t* nL;                // out (B, H, Nq): distinct matched leaves
+  int32_t* n_tree;            // out (B, H, Nq): tree leaves to use (with lhat)
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void neighbor_kernel(NbParams p) {
+  constexpr int R = D / 16;
+  const int lane = lane_id();
+  const int64_t qi = (int64_t)blockIdx.x * 4 + wave_id();   // flat (b, h, n)
+  if (qi >= (int64_t)p.B * p.H * p.Nq) return;
+  const int n = (int)(qi % p.Nq);
+  const int bh = (int)(qi / p.Nq);
+  const int b = bh / p.H, h = bh % p.H;
+  const int t = p.tq[b * p.tq_sb + n];
+  const int S = p.Wn * p.NS;
+
+  // this lane's slot
+  const int back = lane / p.NS + 1, e = lane % p.NS;
+  const int j = t - back;
+  bool ok0 = false;
+  int id = 0;
+  float base = 0.0f;
+  if (lane < S && j >= 0 && j < p.Tst) {
+    const int64_t o = b * p.st_sb + h * p.st_sh + (int64_t)j * p.st_st + e;
+    id = p.st_leaf[o];
+    base = p.st_score[o];
+    ok0 = p.st_ok[o] != 0;
+  }
+
+  // scores: group g (16 lanes) takes slots g, g + 4, ...; lane j16 of a group holds elements [R j16, R j16 + R)
+  const int g = lane >> 4, j16 = lane & 15;
+  float qr[R];
+  load_row<T, R>(reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn + R * j16, qr);
+  const float* srow = p.S0 + b * p.ssb + h * p.ssh + R * j16;
+  float sc = 0.0f;
+  for (int r0 = 0; r0 < S; r0 += 4) {
+    const int s = r0 + g;
+    int sid = __shfl(id, s < S ? s : 0, kWave);
+    sid = sid < 0 ? 0 : (sid >= p.M ? p.M - 1 : sid);   // gather-dot clamps the id into the level
+    float rows[R];
+    load_row_g<float, R>(srow + (int64_t)sid * D, rows);
+    const float v = __fmul_rn(canon_dot<R>(qr, rows), p.scale);   // every lane of the group holds it
+    const float mine = __shfl(v, (lane & 3) * 16, kWave);         // slot r0 + lane % 4 comes from group lane % 4
+    if ((lane >> 2) == (r0 >> 2)) sc = mine;
+  }
+
+  bool m;
+  {
+#pragma clang fp contract(off)
+    const float thr = base - p.rho * fabsf(base);
+    m = lane < S && ok0 && sc >= thr;
+  }
+  const uint64_t in_probe = p.probe * p.NS >= 64 ? ~0ull : ((1ull << (p.probe * p.NS)) - 1);
+  const uint64_t okb = __ballot(lane < S && ok0), mb = __ballot(m);
+  const int nok = __popcll(okb & in_probe), nm = __popcll(mb & in_probe);
+  const float rate = (float)nm / (float)(nok > 1 ? nok : 1);
+  const int cap = p.cap_min + (int)rintf((float)(p.Wn - p.cap_min) * rate);
+  m = m && back <= cap && p.neighbors != 0;
+  // distinct matched ids: a matched lane counts unless an earlier matched lane holds the same id
+  const uint64_t fin = __ballot(m);
+  bool first = m;
+  for (int s = 0; s < S; ++s) {
+    const int other = __shfl(id, s, kWave);
+    if (((fin >> s) & 1) && s < lane && other == id) first = false;
+  }
+  const int nl = __popcll(__ballot(first));
+
+  if (lane < S) {
+    p.nid[qi * S + lane] = id;
+    p.match[qi * S + lane] = m ? 1 : 0;
+  }
+  if (lane == 0) {
+    p.nL[qi] = nl;
+    if (p.lhat != nullptr && p.n_tree != nullptr) {
+      const int L = p.lhat[qi];
+      const int half = (L + 1) / 2;
+      const int need = L - nl > 0 ? L - nl : 0;
+      const int least = nl < half ? 2 : 1;
+      int nt = nl >= L ? 0 : (need > least ? need : least);
+      p.n_tree[qi] = nt < p.wmax ? nt : p.wmax;
+    }
+  }
+}
+
+}  // namespace ta
+
+using namespace ta;
+
+extern "C" int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const float* S0,
+                                int64_t ssb, int64_t ssh, int M, const int32_t* st_leaf, const float* st_score,
+                                const uint8_t* st_ok, int64_t st_sb, int64_t st_sh, int64_t st_st, int Tst,
+                                const int32_t* tq, int64_t tq_sb, int B, int H, int Nq, int D, int nb_window,
+                                int nb_store, int nb_probe, int nb_cap_min, float nb_rho, int neighbors, float scale,
+                                const int32_t* lhat, int wmax, int32_t* nid, uint8_t* match, int32_t* nL,
+                                int32_t* n_tree, void* stream) {
+  if (B <= 0 || H <= 0 || Nq <= 0 || M <= 0 || nb_window <= 0 || nb_store <= 0 || nb_window * nb_store > 64 ||
+      nb_probe < 0 || Tst <= 0 || (D != 16 && D != 32 && D != 64 && D != 128 && D != 256) || q == nullptr || S0 == nullptr || st_leaf == nullptr ||
+      st_score == nullptr || st_ok == nullptr || tq == nullptr || nid == nullptr || match == nullptr ||
+      nL == nullptr || (lhat != nullptr && n_tree == nullptr)) {
+    set_error("ta_neighbor_pass: bad arguments (D 16, 32, 64, 128 or 256; nb_window * nb_store <= 64)");
+    return TA_ERR_ARG;
+  }
+  const int R = D / 16, es = q_dtype == TA_F32 ? 4 : 2;
+  if (((uintptr_t)S0 % 16) || (ssb % 4) || (ssh % 4) || ((uintptr_t)q % (R * es)) || (qsb % R) || (qsh % R) ||
+      (qsn % R)) {
+    set_error("ta_neighbor_pass: node sums 16-byte aligned, query rows aligned to D / 16 elements");
+    return TA_ERR_ARG;
+  }
+  NbParams p{q, qsb, qsh, qsn, S0, ssb, ssh, M, st_leaf, st_score, st_ok, st_sb, st_sh, st_st, Tst, tq, tq_sb,
+             B, H, Nq, nb_window, nb_store, nb_probe, nb_cap_min, neighbors, nb_rho, scale, lhat, wmax, nid, match,
+             nL, n_tree};
+  const int64_t nqry = (int64_t)B * H * Nq;
+  const dim3 grid((unsigned)((nqry + 3) / 4));
+  hipStream_t st = (hipStream_t)stream;
+#define TA_NB(TT, DD) hipLaunchKernelGGL((neighbor_kernel<TT, DD>), grid, dim3(256), 0, st, p)
+#define TA_NB_D(TT)                          \
+  switch (D) {                               \
+    case 16: TA_NB(TT, 16); break;           \
+    case 32: TA_NB(TT, 32); break;           \
+    case 64: TA_NB(TT, 64); break;           \
+    case 128: TA_NB(TT, 128); break;         \
+    default: TA_NB(TT, 256); break;          \
+  }
+  switch (q_dtype) {
+    case TA_F32: TA_NB_D(float); break;
+    case TA_F16: TA_NB_D(f16_t); break;
+    case TA_BF16: TA_NB_D(bf16_t); break;
+    default: set_error("ta_neighbor_pass: unknown dtype"); return TA_ERR_ARG;
+  }
+#undef TA_NB_D
+#undef TA_NB
+  return check_launch("neighbor_kernel");
+}

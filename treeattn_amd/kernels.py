@@ -226,6 +226,40 @@ def gather_dot(q, S, cand, scale):
     return out
 
 
+def neighbor_pass(q, S0, st_leaf, st_score, st_ok, tq, cfg, leaf, lhat=None):
+    """Neighbour borrowing (ta_neighbor_pass; seg.py:73-103, with lhat also seg.py:111-117's budget split).
+    q (b,H,Nq,D); S0 leaf-level node sums (b,H,M,D) float32; st_leaf int32 / st_score float32 / st_ok bool
+    (b,H,Tst,NS); tq (Nq,) or (b,Nq) positions.  Returns (nid int32 (b,H,Nq,Wn*NS), match bool, nL int32
+    (b,H,Nq)) and with lhat (b,H,Nq) also n_tree int32."""
+    L.require_gpu(q, S0, st_leaf, st_score, st_ok, tq)
+    b, H, Nq, D = q.shape
+    Wn, NS = int(cfg.nb_window), int(cfg.nb_store)
+    if st_leaf.dtype != torch.int32 or st_score.dtype != torch.float32 or st_ok.dtype != torch.bool:
+        raise TypeError('neighbor_pass: st_leaf int32, st_score float32, st_ok bool')
+    if S0.dtype != torch.float32 or S0.stride(3) != 1 or S0.stride(2) != D:
+        raise ValueError('neighbor_pass: S0 float32 with contiguous rows')
+    if not (st_leaf.stride() == st_score.stride() == st_ok.stride()) or st_leaf.stride(3) != 1:
+        raise ValueError('neighbor_pass: st_* must share one layout with the entries of a position contiguous')
+    if q.stride(3) != 1:
+        raise ValueError('neighbor_pass: q rows must be contiguous')
+    t2 = tq.view(1, Nq) if tq.dim() == 1 else tq
+    t32 = t2.to(torch.int32).contiguous()
+    tq_sb = 0 if t32.shape[0] == 1 else t32.stride(0)
+    nid = torch.empty(b, H, Nq, Wn * NS, device=q.device, dtype=torch.int32)
+    match = torch.empty(b, H, Nq, Wn * NS, device=q.device, dtype=torch.bool)
+    nL = torch.empty(b, H, Nq, device=q.device, dtype=torch.int32)
+    n_tree = torch.empty(b, H, Nq, device=q.device, dtype=torch.int32) if lhat is not None else None
+    lh = lhat.to(torch.int32).contiguous().view(b, H, Nq) if lhat is not None else None
+    L.call('ta_neighbor_pass', L.ptr(q), L.dtype_code(q), q.stride(0), q.stride(1), q.stride(2), L.ptr(S0),
+           S0.stride(0), S0.stride(1), S0.shape[2], L.ptr(st_leaf), L.ptr(st_score), L.ptr(st_ok), st_leaf.stride(0),
+           st_leaf.stride(1), st_leaf.stride(2), st_leaf.shape[2], L.ptr(t32), tq_sb, b, H, Nq, D, Wn, NS,
+           int(cfg.nb_probe), int(cfg.nb_cap_min), float(cfg.nb_rho), 1 if cfg.neighbors else 0, 1.0 / float(leaf),
+           L.ptr(lh), int(cfg.wmax), L.ptr(nid), L.ptr(match), L.ptr(nL), L.ptr(n_tree), L.stream())
+    if lhat is not None:
+        return nid, match, nL, n_tree
+    return nid, match, nL
+
+
 def gather_dot_blocks(q, K, blk, block, scale=1.0, out=None):
     """Leaf-block gather-dot: out[..., c*block + j] = scale * q . K[blk[..., c]*block + j]."""
     L.require_gpu(q, K, blk)

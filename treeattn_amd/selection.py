@@ -26,38 +26,16 @@ def build_pyramid(k, shape, t_end=None, out=None):
 
 
 def neighbor_pass(q, S0, st_leaf, st_score, st_ok, tq, cfg, leaf):
-    """Neighbour borrowing (seg.py:73-103, fastseg.py:274-299) on the device.
-    q (b,H,Nq,dh) fp32; S0 leaf-level node sums (b,H,M,dh); st_* (b,H,Tst,NS); tq (Nq,) or (b,Nq) long.
-    Scores come from the gather-dot kernel (canonical order)."""
-    b, H, Nq, dh = q.shape
-    Wn, NS = cfg.nb_window, cfg.nb_store
-    dev = q.device
-    back = torch.arange(1, Wn + 1, device=dev)
-    tq2 = tq.view(1, Nq).expand(b, Nq) if tq.dim() == 1 else tq
-    jpos = tq2.unsqueeze(-1) - back                         # (b, Nq, Wn)
-    jok = jpos >= 0
-    jc = jpos.clamp(min=0)
-    bidx = torch.arange(b, device=dev).view(b, 1, 1, 1)
-    hidx = torch.arange(H, device=dev).view(1, H, 1, 1)
-    jcx = jc.view(b, 1, Nq * Wn).expand(b, H, Nq * Wn)
-    ids = st_leaf[bidx.view(b, 1, 1), hidx.view(1, H, 1), jcx].reshape(b, H, Nq, Wn * NS)
-    base = st_score[bidx.view(b, 1, 1), hidx.view(1, H, 1), jcx].reshape(b, H, Nq, Wn * NS)
-    ok0 = st_ok[bidx.view(b, 1, 1), hidx.view(1, H, 1), jcx].reshape(b, H, Nq, Wn, NS)
-    ok0 = (ok0 & jok.view(b, 1, Nq, Wn, 1)).reshape(b, H, Nq, Wn * NS)
-    sc_now = K.gather_dot(q, S0, ids, 1.0 / float(leaf))
-    match = ok0 & (sc_now >= base - cfg.nb_rho * base.abs())
-    probe = cfg.nb_probe * NS
-    rate = match[..., :probe].float().sum(-1) / ok0[..., :probe].float().sum(-1).clamp(min=1)
-    cap = cfg.nb_cap_min + torch.round((Wn - cfg.nb_cap_min) * rate).long()
-    rank = torch.arange(Wn * NS, device=dev) // NS + 1
-    match = match & (rank <= cap.unsqueeze(-1))
-    if not cfg.neighbors:
-        match = torch.zeros_like(match)
-    masked = torch.where(match, ids.long(), torch.full_like(ids, -1, dtype=torch.long))
-    srt, _ = masked.sort(-1)
-    present = srt >= 0
-    nL = present.sum(-1) - ((srt[..., 1:] == srt[..., :-1]) & present[..., 1:]).sum(-1)
-    return ids.long(), match, nL
+    """Neighbour borrowing (seg.py:73-103, fastseg.py:274-299): one launch of ta_neighbor_pass.
+    q (b,H,Nq,dh); S0 leaf-level node sums (b,H,M,dh); st_* (b,H,Tst,NS); tq (Nq,) or (b,Nq) long.
+    Returns (ids long, match bool, nL long) as the reference does."""
+    st_leaf = st_leaf if st_leaf.dtype == torch.int32 else st_leaf.to(torch.int32)
+    st_ok = st_ok if st_ok.dtype == torch.bool else st_ok.bool()
+    st_score = st_score if st_score.dtype == torch.float32 else st_score.float()
+    if not (st_leaf.stride() == st_score.stride() == st_ok.stride()):
+        st_leaf, st_score, st_ok = st_leaf.contiguous(), st_score.contiguous(), st_ok.contiguous()
+    nid, match, nL = K.neighbor_pass(q, S0, st_leaf, st_score, st_ok, tq, cfg, leaf)
+    return nid.long(), match, nL.long()
 
 
 def leaves_to_pos(ids, ok, leaf=2):
