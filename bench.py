@@ -51,6 +51,9 @@ def parse():
     ap.add_argument('--prefill-chunk', type=int, default=None)
     ap.add_argument('--cpu-seconds', type=float, default=20.0, help='budget of the CPU baseline leg')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
+    ap.add_argument('--neighbors', action='store_true',
+                    help='configs 4/5: decode in the reference-default selection mode (neighbour borrowing on); '
+                         'reports the step rate only')
     ap.add_argument('--no-gather-dot', action='store_true', help='skip the isolated gather-dot leg')
     ap.add_argument('--kernel-iters', type=int, default=50)
     ap.add_argument('--kv-layout', choices=('paged', 'contiguous'), default='paged',
@@ -290,7 +293,7 @@ def decode_bench(args):
     H, C = args.heads, args.embd
     dh = C // H
     cfg = Config(vocab_size=args.vocab, seq_len=Tcap, n_layer=args.layers, n_head=H, n_embd=C, attn='seg',
-                 wmax=args.topk, beam=args.topk, beam_mode='fixed', neighbors=False, leaf=args.leaf,
+                 wmax=args.topk, beam=args.topk, beam_mode='fixed', neighbors=bool(args.neighbors), leaf=args.leaf,
                  arity=args.arity, local=3)
     log('init model (seed 3)')
     W = build_model(cfg, 3, torch.bfloat16)
@@ -309,7 +312,14 @@ def decode_bench(args):
     log('prefill %d x %d tokens' % (B, T0))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    logits = dec.prefill(idx.cuda(), chunk=args.prefill_chunk)
+    if args.neighbors:
+        # the prompt is filled without neighbour borrowing (its candidate lists at 32k positions would take tens
+        # of GB per sequence); the neighbour store then fills from the decode steps (warm-up >= nb_window)
+        cfg.neighbors = False
+        logits = dec.prefill(idx.cuda(), chunk=args.prefill_chunk)
+        cfg.neighbors = True
+    else:
+        logits = dec.prefill(idx.cuda(), chunk=args.prefill_chunk)
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     log('prefill %.1f s; capture decode step' % prefill_s)
@@ -328,6 +338,18 @@ def decode_bench(args):
     value = B * args.steps / el
     t_now = T0 + args.warmup + args.steps
     log('%.3f ms/step, %.0f tokens/s' % (ms_step, value))
+    if args.neighbors:
+        return {'metric': 'sparse-attn decode tokens/s @bs%dx%d, reference-default selection (neighbour borrowing '
+                          'on)' % (B, T0), 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1,
+                'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(ms_step, 4),
+                'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16',
+                'data': 'synthetic (random-init weights seed 3, uniform random token ids seed %d)' % args.ids_seed,
+                'config': {'workload': 'config %d model and cache, neighbours on (nb_window %d, nb_store %d), leaf %d, '
+                                       'wmax = beam = %d; prompt filled without borrowing, the store from the %d '
+                                       'warm-up steps' % (args.config, cfg.nb_window, cfg.nb_store, args.leaf,
+                                                          args.topk, args.warmup),
+                           'batch': B, 'context': T0},
+                'roofline': None, 'cpu_baseline': None}
 
     # ---- dominant kernel: the decode attention of one layer over the live state, HIP events on its stream
     st = dec.states[0]

@@ -206,6 +206,26 @@ int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                     int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages, void* stream);
 
 /*
+ * ta_seg_attn_fwd in the reference-default selection mode (neighbour borrowing on; replaces the candidate
+ * assembly and first-copy dedupe of fastseg.py:367-383 / engine.py:107-114 and the attention over the
+ * result): besides the first n_tree valid tree leaves, each query attends the leaf blocks of its matched
+ * neighbour slots -- nb_id / nb_ok (B, H, Nq, nb_S) int32 / uint8, query qi's slots at qi * nb_S, as
+ * ta_neighbor_pass writes them -- each block once (a block already among the tree leaves, or held by an
+ * earlier matched slot, or not complete before the query's own block, is skipped), then the own block and the
+ * static keys outside every attended block.  nb_S <= 64.  keys[qi] counts the keys of that set.  Otherwise as
+ * ta_seg_attn_fwd (the vector kernels serve every shape here).
+ */
+int ta_seg_attn_nb_fwd(const void* q, const void* k, const void* v, int dtype,
+                       int64_t qsb, int64_t qsh, int64_t qsn, int64_t ksb, int64_t ksh, int64_t kst,
+                       int64_t vsb, int64_t vsh, int64_t vst,
+                       int B, int H, int Nq, int D, int Tk,
+                       const int32_t* tq, int64_t tq_sb,
+                       const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl,
+                       int leaf, int local, float scale, const int32_t* nb_id, const uint8_t* nb_ok, int nb_S,
+                       void* out, int64_t osb, int64_t osh, int64_t osn, float* lse, float* keys,
+                       int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages, void* stream);
+
+/*
  * ta_seg_attn_fwd without a workspace argument: no counterpart in the reference (it has no workspaces).  For
  * callers that cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  The split attention's scratch (ta_seg_attn_workspace_size(...) bytes: per-query

@@ -216,6 +216,65 @@ def test_engine_matches_oracle_engine():
     assert err < 1e-4, err
 
 
+@pytest.mark.parametrize('kw', [dict(), dict(leaf=8, wmax=3, beam=3), dict(leaf=4, arity=4, wmax=3, beam=2),
+                                dict(beam_mode='pred', global_pool=True)])
+def test_engine_reference_default_matches_oracle_engine(kw):
+    """Reference-default selection (neighbour borrowing on; the budget head in the last case): Decoder.step --
+    descent, ta_neighbor_pass, the store of this position's leaves, the attention over tree + neighbour leaves
+    each once -- against the oracle decoder (engine.py:84-177, canonical order, K x K dedupe), fp32, 96
+    positions from an empty cache: logits within 1e-4 and the same key counts."""
+    print('case', kw, flush=True)
+    cfg = tiny(seq_len=128, **kw)
+    torch.manual_seed(12)
+    model = GPT(cfg).eval()
+    W = weights_from_ours(model.state_dict(), cfg)
+    ref = DecoderRef(W, 2, 2, 32, 128, 'seg', cfg, sel_mode='canonical')
+    Wg = _to_dev(W)
+    dec = Decoder(Wg, 2, 2, 32, 128, 'seg', cfg, DEV)
+    g = torch.Generator().manual_seed(13)
+    toks = torch.randint(0, 64, (96,), generator=g)
+    err = 0.0
+    for t in range(96):
+        a, ka = ref.step(int(toks[t]), t)
+        b, kb = dec.step(int(toks[t]), t)
+        err = max(err, (a - b.cpu()).abs().max().item())
+        assert abs(ka - kb) < 1e-4, (t, ka, kb)
+    print('max |dlogit| %.2e' % err)
+    assert err < 1e-4, err
+
+
+@pytest.mark.parametrize('kw', [dict(), dict(beam_mode='pred', global_pool=True)])
+def test_prefill_then_decode_matches_oracle_engine(kw):
+    """Reference-default mode: a batched prefill of 40 positions (the forward's selection, seeding the neighbour
+    store as decoding the prompt would, engine.py:103-105) then 24 decode steps, against the oracle decoder
+    stepping through all 64 positions from an empty cache: logits within 1e-4 at the prompt's last position
+    and at every decoded one."""
+    print('case', kw, flush=True)
+    cfg = tiny(seq_len=64, **kw)
+    torch.manual_seed(14)
+    model = GPT(cfg).eval()
+    W = weights_from_ours(model.state_dict(), cfg)
+    ref = DecoderRef(W, 2, 2, 32, 64, 'seg', cfg, sel_mode='canonical')
+    g = torch.Generator().manual_seed(15)
+    idx = torch.randint(0, 64, (1, 64), generator=g)
+    want = torch.stack([ref.step(int(idx[0, t]), t)[0] for t in range(64)])
+    dec = Decoder(_to_dev(W), 2, 2, 32, 64, 'seg', cfg, DEV)
+    T0 = 40
+    last = dec.prefill(idx[:, :T0].to(DEV))
+    got = torch.stack([dec.step(int(idx[0, t]), t)[0] for t in range(T0, 64)]).cpu()
+    e0 = (last[0].cpu() - want[T0 - 1]).abs().max().item()
+    e1 = (got - want[T0:]).abs().max().item()
+    print('prefill last %.2e, decode %.2e' % (e0, e1))
+    assert e0 < 1e-4 and e1 < 1e-4, (e0, e1)
+
+
+def _to_dev(W):
+    Wg = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in W.items()}
+    Wg['layers'] = [{k: (v.to(DEV) if torch.is_tensor(v) else {a: b.to(DEV) for a, b in v.items()})
+                     for k, v in L.items()} for L in W['layers']]
+    return Wg
+
+
 def test_batched_prefill_and_decode_match_batch_one():
     """Batch of 3 sequences: prefill of 40 tokens then 24 decode steps equal three batch-1 decoders (bf16)."""
     cfg = tiny(seq_len=128, leaf=8, neighbors=False, wmax=4, beam=4)

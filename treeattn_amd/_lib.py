@@ -83,6 +83,10 @@ SIGNATURES = {
                                 c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32,
                                 c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64,
                                 _P(KvPages), c_vp]),
+    'ta_seg_attn_nb_fwd': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                   c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp,
+                                   c_i32, c_i32, c_i32, c_f32, c_vp, c_vp, c_i32, c_vp, c_i64, c_i64, c_i64, c_vp,
+                                   c_vp, c_i32, c_vp, c_i64, _P(KvPages), c_vp]),
     'ta_seg_attn_fwd_noalloc': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                         c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp,
                                         c_vp, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp,

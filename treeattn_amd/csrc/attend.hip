@@ -172,7 +172,7 @@ bool kv_aligned(const void* p, int dt, int D, std::initializer_list<int64_t> str
 
 template <typename T, int D>
 int launch_attn(const AttnParams& p, int B, bool split, hipStream_t st) {
-  const int wl_pad = p.cand ? 0 : ((p.wl + 3) & ~3);
+  const int wl_pad = p.cand ? 0 : attn_list_cap(p.wl, p.nb_S);
   size_t lds = (size_t)kWavesPerBlock * attn_wave_ints(wl_pad) * sizeof(float);
   const dim3 blk(kWavesPerBlock * kWave);
   if (split) {
@@ -284,16 +284,22 @@ extern "C" int64_t ta_seg_attn_workspace_size(int B, int H, int Nq, int D, int n
   return attn_counter_bytes(B, H, Nq) + (int64_t)B * H * Nq * gsplit * (D + 2) * (int64_t)sizeof(float);
 }
 
-extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
-                               int64_t qsn, int64_t ksb, int64_t ksh, int64_t kst, int64_t vsb, int64_t vsh,
-                               int64_t vst, int B, int H, int Nq, int D, int Tk, const int32_t* tq, int64_t tq_sb,
-                               const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl, int leaf,
-                               int local, float scale, void* out, int64_t osb, int64_t osh, int64_t osn, float* lse,
-                               float* keys, int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages,
-                               void* stream) {
+namespace {
+
+int seg_attn_fwd_impl(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
+                      int64_t qsn, int64_t ksb, int64_t ksh, int64_t kst, int64_t vsb, int64_t vsh,
+                      int64_t vst, int B, int H, int Nq, int D, int Tk, const int32_t* tq, int64_t tq_sb,
+                      const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl, int leaf,
+                      int local, float scale, void* out, int64_t osb, int64_t osh, int64_t osn, float* lse,
+                      float* keys, int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages,
+                      const int32_t* nb_id, const uint8_t* nb_ok, int nb_S, void* stream) {
   if (B <= 0 || H <= 0 || Nq < 0 || wl < 0 || nsplit < 1 || leaf < 2 || (leaf & (leaf - 1)) ||
       (nsplit > 1 && nsplit % kWavesPerBlock) || nsplit > kWavesPerBlock * kWave) {
     set_error("ta_seg_attn_fwd: bad sizes (nsplit must be 1 or a multiple of 4, at most 256)");
+    return TA_ERR_ARG;
+  }
+  if (nb_S < 0 || nb_S > kWave || (nb_S > 0 && (nb_id == nullptr || nb_ok == nullptr))) {
+    set_error("ta_seg_attn_nb_fwd: neighbour slots must number at most 64, with ids and flags");
     return TA_ERR_ARG;
   }
   const int Lw = local > 3 ? local : 3;
@@ -335,14 +341,41 @@ extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int 
     p.cnt = reinterpret_cast<uint32_t*>(ws);
     p.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + attn_counter_bytes(B, H, Nq));
   }
+  p.nb_id = nb_id; p.nb_ok = nb_ok; p.nb_S = nb_S;
   const int prc = set_attn_pages(p, pages, dtype, D, ll, "ta_seg_attn_fwd");
   if (prc != TA_OK) return prc;
-  if (nsplit == 1 && pages == nullptr) {
+  if (nsplit == 1 && pages == nullptr && nb_S == 0) {
     // many queries (prefill): the matrix-core kernel when the shape fits it
     const int rc = prefill_attn_mfma(p, B, dtype, D, (hipStream_t)stream);
     if (rc != TA_ERR_UNSUPPORTED) return rc;
   }
   return dispatch_attn(dtype, D, p, B, nsplit > 1, (hipStream_t)stream);
+}
+
+}  // namespace
+
+extern "C" int ta_seg_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
+                               int64_t qsn, int64_t ksb, int64_t ksh, int64_t kst, int64_t vsb, int64_t vsh,
+                               int64_t vst, int B, int H, int Nq, int D, int Tk, const int32_t* tq, int64_t tq_sb,
+                               const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl, int leaf,
+                               int local, float scale, void* out, int64_t osb, int64_t osh, int64_t osn, float* lse,
+                               float* keys, int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages,
+                               void* stream) {
+  return seg_attn_fwd_impl(q, k, v, dtype, qsb, qsh, qsn, ksb, ksh, kst, vsb, vsh, vst, B, H, Nq, D, Tk, tq, tq_sb,
+                           ids, vld, n_tree, wl, leaf, local, scale, out, osb, osh, osn, lse, keys, nsplit, ws,
+                           ws_bytes, pages, nullptr, nullptr, 0, stream);
+}
+
+extern "C" int ta_seg_attn_nb_fwd(const void* q, const void* k, const void* v, int dtype, int64_t qsb, int64_t qsh,
+                                  int64_t qsn, int64_t ksb, int64_t ksh, int64_t kst, int64_t vsb, int64_t vsh,
+                                  int64_t vst, int B, int H, int Nq, int D, int Tk, const int32_t* tq, int64_t tq_sb,
+                                  const int32_t* ids, const uint8_t* vld, const int32_t* n_tree, int wl, int leaf,
+                                  int local, float scale, const int32_t* nb_id, const uint8_t* nb_ok, int nb_S,
+                                  void* out, int64_t osb, int64_t osh, int64_t osn, float* lse, float* keys,
+                                  int nsplit, float* ws, int64_t ws_bytes, const ta_kv_pages* pages, void* stream) {
+  return seg_attn_fwd_impl(q, k, v, dtype, qsb, qsh, qsn, ksb, ksh, kst, vsb, vsh, vst, B, H, Nq, D, Tk, tq, tq_sb,
+                           ids, vld, n_tree, wl, leaf, local, scale, out, osb, osh, osn, lse, keys, nsplit, ws,
+                           ws_bytes, pages, nb_id, nb_ok, nb_S, stream);
 }
 
 extern "C" int ta_seg_attend(const void* q, const void* k_new, const void* v_new, int dtype, int64_t qsb, int64_t qsh,

@@ -73,7 +73,7 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
   (void)n;
   (void)b;
   (void)h;
-  const int wl_pad = p.cand ? 0 : ((p.wl + 3) & ~3);
+  const int wl_pad = p.cand ? 0 : attn_list_cap(p.wl, p.nb_S);
   // per wavefront: used leaf ids [wl_pad], their pages [wl_pad], static keys [32] and their pages [32]
   int32_t* s_ids = reinterpret_cast<int32_t*>(smem_f + w * attn_wave_ints(wl_pad));
   int32_t* s_row0 = s_ids + wl_pad;
@@ -117,6 +117,30 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
     lb = t < 0 ? 0 : (t >> p.leaf_log2) << p.leaf_log2;
     nloc = t < 0 ? 0 : t - lb + 1;
     wave_sync();
+    if (p.nb_S > 0 && t >= 0) {
+      // neighbour leaves: a matched slot joins when its block is complete before the own block, is not one of the
+      // tree leaves and no earlier matched slot holds the same leaf (the reference's first-copy dedupe of
+      // [tree | neighbour | static] positions, fastseg.py:376-381, as a set of leaf blocks)
+      const bool in = lane < p.nb_S;
+      const int id = in ? p.nb_id[qi * p.nb_S + lane] : -1;
+      const bool cand = in && p.nb_ok[qi * p.nb_S + lane] != 0 && id >= 0;
+      bool keepn = cand && id < (lb >> p.leaf_log2);
+      for (int i = 0; i < nused; ++i)
+        if (s_ids[i] == id) keepn = false;
+      const uint64_t cm = __ballot(cand);
+      for (int s2 = 0; s2 < p.nb_S; ++s2) {
+        const int o = __shfl(id, s2, kWave);
+        if (((cm >> s2) & 1) && s2 < lane && o == id) keepn = false;
+      }
+      const uint64_t km = __ballot(keepn);
+      if (keepn) {
+        const int slot = nused + __popcll(km & ((1ull << lane) - 1));
+        s_ids[slot] = id;
+        s_row0[slot] = row0_of(id);
+      }
+      nused += __popcll(km);
+      wave_sync();
+    }
     // static keys [0, t, t-1, ..., t-Lw+1]: keep those >= 0, outside the own block, whose leaf block is
     // not used, and not a repeat of the sink
     int pe = -1;

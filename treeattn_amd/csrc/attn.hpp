@@ -34,7 +34,16 @@ struct AttnParams {
   const int32_t* ptab;
   int64_t pt_sb, pt_sh, kps, vps;
   int64_t npages;
+  // neighbour leaves (structural mode, reference-default selection): per query nb_S slots of leaf ids and
+  // matched flags (query qi's at nb_id + qi * nb_S); the matched ones join the key set once each (nb_S = 0: none)
+  const int32_t* nb_id;
+  const uint8_t* nb_ok;
+  int nb_S;
 };
+
+// Capacity of a wavefront's leaf list: the tree leaves (wl) and the neighbour leaves (nb_S), each rounded up to
+// a multiple of 4.
+__host__ __device__ constexpr int attn_list_cap(int wl, int nb_S) { return ((wl + 3) & ~3) + ((nb_S + 3) & ~3); }
 
 constexpr float kNegBig = -1e30f;
 

@@ -303,7 +303,8 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     if scratch is None:
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
     structural = (not cfg.neighbors) and lhat is None
-    fused = structural and update and B * H < 4096 and q.dtype == k.dtype == state.dtype
+    appendable = update and B * H < 4096 and q.dtype == k.dtype == state.dtype
+    fused = structural and appendable
     Kc, Vc = state.kv()
     if fused and scratch.nsplit == 4 and dh in (64, 128) and wl <= 64 and not cfg.global_pool:
         # append, descent and attention in one launch (one workgroup per (sequence, head))
@@ -313,7 +314,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         K.seg_attend(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0], Kc, Vc,
                      scratch.n_tree, cfg.local, scale, (scratch.ids, scratch.vld, scratch.sct), out, keys=scratch.keys)
         return out, scratch.keys
-    if fused:
+    if appendable:
         # descent and cache append in one launch (the append touches only row t and the nodes ending at t)
         ids, vld, sct = K.tree_descend_append(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0],
                                               Kc, Vc, out=(scratch.ids, scratch.vld, scratch.sct))
@@ -322,7 +323,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
                                        out=(scratch.ids, scratch.vld, scratch.sct))
     if structural:
         if update:
-            if not fused:
+            if not appendable:
                 K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
             if cfg.global_pool:
                 state.ksum += k[:, :, 0].float()
@@ -333,35 +334,39 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         K.seg_attn(q, Kc, Vc, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out,
                    keys=scratch.keys, nsplit=scratch.nsplit, ws=scratch.ws)
         return out, scratch.keys
-    # reference-default mode: neighbour borrowing and/or the budget head -> candidate list
+    # reference-default mode: neighbour borrowing and/or the budget head.  The neighbour pass reads the store of
+    # positions t-1 .. t-Wn and gives the budget split (engine.py:100-102, seg.py:111-117); the top nb_store
+    # leaves of this descent are stored for position t (engine.py:103-105); the attention takes the first
+    # n_tree tree leaves and the matched neighbour leaves, each block once, with the own block and static keys
+    # (engine.py:107-119).
     if lhat is None:
         lhat = torch.full((B, H, 1), cfg.beam, dtype=torch.long, device=q.device)
-    idl, vb = ids.long(), vld.bool()
-    t64 = tpos.long().view(B, 1)
     NS = cfg.nb_store
     if state.shape.n_levels:
-        nid, match, nL = SEL.neighbor_pass(q.float(), state.levels[0], state.st_leaf, state.st_score, state.st_ok,
-                                           t64, cfg, leaf)
+        nid, match, nL, n_tree = K.neighbor_pass(q, state.levels[0], state.st_leaf, state.st_score, state.st_ok,
+                                                 tpos.view(B, 1), cfg, leaf, lhat=lhat.view(B, H, 1))
     else:
         Wn = cfg.nb_window
-        nid = torch.zeros(B, H, 1, Wn * NS, dtype=torch.long, device=q.device)
+        nid = torch.zeros(B, H, 1, Wn * NS, dtype=torch.int32, device=q.device)
         match = torch.zeros_like(nid, dtype=torch.bool)
-        nL = torch.zeros(B, H, 1, dtype=torch.long, device=q.device)
-    sel = SEL.finish(torch.where(vb, idl, torch.zeros_like(idl)), vb, nid, match, nL, lhat, cfg, leaf)
+        n_tree = SEL.budget_split(torch.zeros_like(lhat.view(B, H, 1)), lhat.view(B, H, 1), cfg.wmax).to(torch.int32)
     if update:
         n = min(NS, wl)
         bidx = torch.arange(B, device=q.device).view(B, 1)
         hidx = torch.arange(H, device=q.device).view(1, H)
-        tt = t64.view(B, 1)
+        tt = tpos.long().view(B, 1)
+        vb = vld.bool()
         state.st_leaf[bidx, hidx, tt, :n] = ids[:, :, 0, :n].clamp(min=0)
         state.st_score[bidx, hidx, tt, :n] = torch.where(vb[:, :, 0, :n], sct[:, :, 0, :n],
                                                          torch.zeros_like(sct[:, :, 0, :n]))
         state.st_ok[bidx, hidx, tt, :n] = vb[:, :, 0, :n]
-        K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
+        if not appendable:
+            K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
         state.ksum += k[:, :, 0].float()
-    cand, keep, used = SEL.assemble(sel, t64, cfg, B, H)
-    out, _ = K.sparse_attn_fwd(q, Kc, Vc, torch.where(keep, cand, torch.full_like(cand, -1)), scale)
-    return out, keep.sum(-1).float()
+    out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
+    K.seg_attn(q, Kc, Vc, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out, keys=scratch.keys,
+               nsplit=scratch.nsplit, ws=scratch.ws, nb=(nid, match))
+    return out, scratch.keys
 
 
 def seg_attend(state, pw, q, k, v, t, update=True):

@@ -334,10 +334,12 @@ def seg_attn_workspace(B, H, Nq, D, nsplit, device):
     return torch.zeros(nbytes, dtype=torch.uint8, device=device)
 
 
-def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=None, keys=None, nsplit=1, ws=None):
-    """Attention over selected leaf blocks + own leaf block + static keys (neighbours off).
+def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=None, keys=None, nsplit=1, ws=None,
+             nb=None):
+    """Attention over selected leaf blocks + own leaf block + static keys.
     q (B,H,Nq,D) strided; k, v (B,H,Tk,D) strided; tq (Nq,) or (B,Nq) int32; ids/vld (B,H,Nq,wl);
-    n_tree (B,H,Nq) int32 or None.  Returns (out, lse, keys)."""
+    n_tree (B,H,Nq) int32 or None.  nb: (nid int32, match bool) (B,H,Nq,S) from neighbor_pass -- the matched
+    neighbour leaves join the key set once each (ta_seg_attn_nb_fwd).  Returns (out, lse, keys)."""
     L.require_gpu(q, tq, ids, vld, *_cache_tensors(k, v))
     vdt = _cache_dtype(k) if isinstance(k, PagedCache) else v.dtype
     if not (q.dtype == _cache_dtype(k) == vdt):
@@ -356,6 +358,16 @@ def seg_attn(q, k, v, tq, ids, vld, n_tree, leaf, local, scale, out=None, lse=No
         ws = seg_attn_workspace(B, H, Nq, D, nsplit, q.device)
     ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
     kp, vp, ks, vs, Tk, pages = _kv_rows(k, v)
+    if nb is not None:
+        nid, nmatch = nb
+        if (nid.dtype != torch.int32 or nmatch.dtype != torch.bool or not nid.is_contiguous() or
+                not nmatch.is_contiguous() or nid.shape[:3] != (B, H, Nq) or nmatch.shape != nid.shape):
+            raise ValueError('seg_attn: nb must be contiguous (nid int32, match bool) of shape (B, H, Nq, S)')
+        L.call('ta_seg_attn_nb_fwd', L.ptr(q), kp, vp, L.dtype_code(q), *L.rows3(q), *ks, *vs,
+               B, H, Nq, D, Tk, L.ptr(tq32), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(nt), wl, int(leaf), int(local),
+               float(scale), L.ptr(nid), L.ptr(nmatch), nid.shape[-1], L.ptr(out), out.stride(0), out.stride(1),
+               out.stride(2), L.ptr(lse), L.ptr(keys), int(nsplit), L.ptr(ws), ws_bytes, pages, L.stream())
+        return out, lse, keys
     L.call('ta_seg_attn_fwd', L.ptr(q), kp, vp, L.dtype_code(q), *L.rows3(q), *ks, *vs,
            B, H, Nq, D, Tk, L.ptr(tq32), tq_sb, L.ptr(ids), L.ptr(vld), L.ptr(nt), wl, int(leaf), int(local),
            float(scale), L.ptr(out), out.stride(0), out.stride(1), out.stride(2), L.ptr(lse), L.ptr(keys),
