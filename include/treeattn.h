@@ -445,6 +445,43 @@ int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64
                      int32_t* n_tree, void* stream);
 
 /*
+ * Log-magnitude pyramid for the mean-log gate (seg.py:33, 39; engine.py:47, 53-54): ta_level_sums over the
+ * values log(|x| + 1e-6) of the index keys x (position 0 counted as 0 when zero_sink) instead of the keys --
+ * each log the float32 rounding of the double-precision log of the float32 |x| + 1e-6 -- with the same
+ * adjacent-pair float32 additions.  Arguments as ta_level_sums (same workspace size).
+ */
+int ta_level_log_sums(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_t kst,
+                      int B, int H, int t_end, int D, int zero_sink,
+                      int n_levels, float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh,
+                      const int32_t* lv_blevel, float* ws, int64_t ws_bytes, void* stream);
+
+/*
+ * Mean-log gate of node summaries (replaces seg.py:16-23 gate_apply as applied by seg.py:37-38, fastseg.py:
+ * 248-249 and SegState.getU, engine.py:35-39).  For level j (binary level blevel[j], nodes of 2^blevel
+ * positions) and every node n < n_nodes[j] of every (b, h): ml = lg / 2^blevel per dimension; thr = the gate_q
+ * quantile of ml over the D dimensions (order statistics at floor and ceil of r = gate_q * (D - 1) in float32,
+ * interpolated as torch.lerp: lo + w (hi - lo) for w < 0.5, else hi - (hi - lo)(1 - w), w = r - floor(r), each
+ * operation rounded); out = (raw * [ml >= thr]) * (D / max(#kept, 1)).  raw, lg, out: (B, H, M_j, D) float32
+ * with node rows contiguous and batch / head strides sb[j], sh[j]; out[j] == NULL skips level j.  D 16 to 128.
+ */
+int ta_gate_levels(int B, int H, int D, int n_levels, const float* const* raw, const float* const* lg,
+                   float* const* out, const int64_t* sb, const int64_t* sh, const int32_t* blevel,
+                   const int64_t* n_nodes, float gate_q, void* stream);
+
+/*
+ * The gate's share of a decode-cache append (engine.py:47, 53-54), after ta_kv_append has written row t_pos[b]
+ * and the raw nodes ending at it: forms the log-magnitude sums of the nodes ending at t (the leaf block's index
+ * keys read back from the K cache Kc -- contiguous (B, H, Tcap, D) with strides csb, csh, cst, or pages -- then
+ * every completed parent from its children, as the raw sums are formed) and the gated vectors of those nodes
+ * on levels whose out[j] is not NULL, as ta_gate_levels computes them.  Levels are tree levels 0.. with
+ * blevel[0] = log2(leaf) and arity 2^arity_log2; lg is written, raw read.
+ */
+int ta_gate_append(const void* Kc, int dtype, int64_t csb, int64_t csh, int64_t cst, int Tcap, int B, int H, int D,
+                   const int32_t* t_pos, int n_levels, const float* const* raw, float* const* lg,
+                   float* const* out, const int64_t* sb, const int64_t* sh, const int32_t* blevel,
+                   int arity_log2, float gate_q, const ta_kv_pages* pages, void* stream);
+
+/*
  * Calibration (no counterpart in the reference): wgs workgroups of four wavefronts each run 4 * iters
  * v_mfma_f32_32x32x16_bf16 instructions (32768 flops each) on register operands, no memory traffic; timing the
  * launch gives the dense bf16 matrix-core throughput the GPU sustains, the peak a kernel's MFMA utilisation is

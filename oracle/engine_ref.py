@@ -10,7 +10,7 @@ import torch
 import torch.nn.functional as F
 
 from .attn_ref import dedupe, dedupe_fast, local_block, static_keys
-from .seg_ref import (Geometry, dot_canonical, finish, gate_apply, gather_nodes, injected, neighbor_pass,
+from .seg_ref import (Geometry, dot_canonical, finish, gate_apply, gather_nodes, index_log, injected, neighbor_pass,
                       rank_canonical, tree_pass)
 
 
@@ -23,8 +23,9 @@ class SegStateRef:
     0..l_J (a node is formed, as the sum of its two children, when its last position arrives), the leaves
     each earlier query found (for neighbour borrowing) and the running key sum."""
 
-    def __init__(self, cfg, Tcap, H, dh):
+    def __init__(self, cfg, Tcap, H, dh, canon=False):
         self.cfg, self.Tcap, self.H, self.dh = cfg, Tcap, H, dh
+        self.canon = canon   # the gate's canonical log and quantile (seg_ref.index_log, quantile_canon)
         self.geom = Geometry(Tcap, getattr(cfg, 'leaf', 2), getattr(cfg, 'arity', 2))
         self.Ltop = self.geom.blevels[-1] if self.geom.J >= 0 else 0
         self.Lm = self.Ltop
@@ -42,7 +43,7 @@ class SegStateRef:
         """Node vectors of `cand` at binary level l, gated at l >= gate_min_level (engine.py:35-39)."""
         U = gather_nodes(self.raw[l], cand)
         if self.cfg.gate and l >= getattr(self.cfg, 'gate_min_level', 0):
-            U = gate_apply(U, gather_nodes(self.lg[l], cand), float(1 << l), self.cfg.gate_q)
+            U = gate_apply(U, gather_nodes(self.lg[l], cand), float(1 << l), self.cfg.gate_q, self.canon)
         return U
 
     def add(self, t, k, v):
@@ -52,7 +53,7 @@ class SegStateRef:
         kidx = torch.zeros_like(k.float()) if t == 0 else k.float()
         self.raw[0][:, :, t] = kidx
         if self.lg is not None:
-            self.lg[0][:, :, t] = torch.log(kidx.abs() + 1e-6)
+            self.lg[0][:, :, t] = index_log(kidx, self.canon)
         for l in range(1, self.Ltop + 1):
             if (t + 1) % (1 << l):
                 break
@@ -69,7 +70,7 @@ class SegStateRef:
         kidx = self.K.clone()
         kidx[:, :, 0] = 0
         self.raw[0] = kidx
-        lg = torch.log(kidx.abs() + 1e-6) if self.lg is not None else None
+        lg = index_log(kidx, self.canon) if self.lg is not None else None
         if lg is not None:
             self.lg[0] = lg
         for l in range(1, self.Ltop + 1):
@@ -217,7 +218,8 @@ class DecoderRef:
         self.reset()
 
     def reset(self):
-        self.states = [SegStateRef(self.cfg, self.Tcap, self.H, self.dh) for _ in range(self.nl)]
+        self.states = [SegStateRef(self.cfg, self.Tcap, self.H, self.dh, canon=self.sel_mode == 'canonical')
+                       for _ in range(self.nl)]
 
     @torch.no_grad()
     def step(self, tok, t, want_sel=False, probe=None):

@@ -80,28 +80,56 @@ def index_keys(k):
     return kidx
 
 
-def gate_apply(raw, lgsum, size, gate_q):
+def index_log(kidx, canon=False):
+    """log(|k| + 1e-6) of index keys (seg.py:33, engine.py:47): |k| + 1e-6 in float32, then torch.log in float32
+    (the reference's op); canon: the float64 log of that float32 value, rounded once to float32 -- the value the
+    HIP kernels compute (a float32 log's last bit depends on the library)."""
+    x = kidx.abs() + 1e-6
+    return torch.log(x.double()).float() if canon else torch.log(x)
+
+
+def quantile_canon(x, q):
+    """torch.quantile(x, q, dim=-1, keepdim=True) restated (linear interpolation): r = q (n - 1) in float32,
+    the order statistics at floor(r) and ceil(r), w = r - floor(r), and torch.lerp's two forms -- lo + w (hi - lo)
+    for w < 0.5, else hi - (hi - lo)(1 - w) -- each operation rounded to float32 (the HIP gate's threshold)."""
+    n = x.shape[-1]
+    srt, _ = x.sort(-1)
+    r = torch.tensor(q, dtype=torch.float32) * float(n - 1)
+    lo = int(torch.floor(r))
+    w = r - lo
+    hi = lo + 1 if float(w) > 0 else lo
+    vlo, vhi = srt[..., lo:lo + 1], srt[..., hi:hi + 1]
+    d = vhi - vlo
+    if float(w) < 0.5:
+        return vlo + w * d
+    return vhi - d * (1.0 - w)
+
+
+def gate_apply(raw, lgsum, size, gate_q, canon=False):
     """Mean-log dilution gate (seg.py:16-23): dimensions whose mean log-magnitude within the node is at or
-    above the gate_q quantile are kept and rescaled by dh / kept; the others are zeroed."""
+    above the gate_q quantile are kept and rescaled by dh / kept; the others are zeroed.  canon: the
+    quantile as quantile_canon (equal to torch.quantile whenever w (hi - lo) is exact, as at the reference's
+    gate_q = 0.25 with dh 16..128)."""
     mean_log = lgsum / size
-    thr = torch.quantile(mean_log, gate_q, dim=-1, keepdim=True)
+    thr = quantile_canon(mean_log, gate_q) if canon else torch.quantile(mean_log, gate_q, dim=-1, keepdim=True)
     keepdim = (mean_log >= thr).to(raw.dtype)
     n_kept = keepdim.sum(-1, keepdim=True).clamp(min=1.0)
     return raw * keepdim * (raw.shape[-1] / n_kept)
 
 
-def level_sums(kidx, Lm, gate=False, gate_q=0.25, gate_min=0):
+def level_sums(kidx, Lm, gate=False, gate_q=0.25, gate_min=0, canon=False):
     """Pyramid of node sums for binary levels 1..Lm: each level is the pairwise sum of adjacent nodes of
-    the level below (seg.py:26-41; with gate_min, fastseg.py:238-251).  Returns {l: (b,H,T>>l,dh)}."""
+    the level below (seg.py:26-41; with gate_min, fastseg.py:238-251).  Returns {l: (b,H,T>>l,dh)}.
+    canon: the canonical log and quantile (index_log, quantile_canon)."""
     b, H, T, dh = kidx.shape
     cur = kidx
-    lg = torch.log(kidx.abs() + 1e-6) if gate else None
+    lg = index_log(kidx, canon) if gate else None
     out = {}
     for l in range(1, Lm + 1):
         cur = cur.reshape(b, H, T >> l, 2, dh).sum(3)
         if gate:
             lg = lg.reshape(b, H, T >> l, 2, dh).sum(3)
-            out[l] = gate_apply(cur, lg, float(1 << l), gate_q) if l >= gate_min else cur
+            out[l] = gate_apply(cur, lg, float(1 << l), gate_q, canon) if l >= gate_min else cur
         else:
             out[l] = cur
     return out
@@ -306,10 +334,10 @@ def select_seg(q, k, lhat, cfg, mode='faithful'):
     tq = torch.arange(T)
     gate = getattr(cfg, 'gate', False)
     if gate:
-        if geom.leaf != 2 or geom.arity != 2:
-            raise NotImplementedError('gate with a generalised tree')
-        Lm = geom.blevels[-1]
-        S_l = level_sums(kidx, Lm, True, cfg.gate_q, getattr(cfg, 'gate_min_level', 0))
+        # every binary level up to the top one (adjacent pairs), gated at levels >= gate_min_level; the tree
+        # levels of (leaf, arity) are a subset of them
+        Lm = geom.blevels[-1] if geom.J >= 0 else 0
+        S_l = level_sums(kidx, Lm, True, cfg.gate_q, getattr(cfg, 'gate_min_level', 0), canon=mode == 'canonical')
         S = {j: S_l[l] for j, l in enumerate(geom.blevels)}
     else:
         S = pyramid(kidx, geom)

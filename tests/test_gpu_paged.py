@@ -153,7 +153,8 @@ def test_append_without_page_writes_nothing():
 
 
 @pytest.mark.parametrize('kw', [dict(neighbors=False, leaf=8, wmax=4, beam=4), dict(leaf=4, wmax=4, beam=3),
-                                dict(beam_mode='pred', global_pool=True, leaf=8, wmax=8)])
+                                dict(beam_mode='pred', global_pool=True, leaf=8, wmax=8),
+                                dict(gate=True, gate_min_level=4, leaf=8, wmax=4, beam=4)])
 def test_decoder_paged_equals_contiguous(kw):
     """Prefill, eager steps and replays of a captured step that cross page boundaries (pages handed out a few
     positions ahead): logits, tokens and node sums equal the contiguous decoder's bit for bit; the pool holds
@@ -189,6 +190,8 @@ def test_decoder_paged_equals_contiguous(kw):
             ka, va = sa.dense_kv(s, 82)
             kb, vb = sb.dense_kv(s, 82)
             assert torch.equal(ka, kb) and torch.equal(va, vb)
-        for x, y in zip(sa.levels, sb.levels):
+        for x, y in zip(sa.levels + (sa.lg or []), sb.levels + (sb.lg or [])):
+            assert torch.equal(x, y)
+        for x, y in zip(sa.score_levels, sb.score_levels):
             assert torch.equal(x, y)
     assert b.pool.nblk[0] * cfg.leaf < 82 + 16

@@ -336,3 +336,103 @@ def test_planted_budget_mistake_is_caught(monkeypatch):
         return dict(n_tree=n_tree)
     monkeypatch.setattr(S, 'finish', mutant)
     assert _finish_sweep(_oracle_n_tree) != []
+
+
+# ------------------------------------------------------------------------------------- mean-log gate (CPU)
+def _gate_brute(raw, lgsum, size, q):
+    """seg.py:16-23 for one node in plain Python: mean logs, the sorted order, the q-quantile by linear
+    interpolation (in float64), the kept dimensions and their D / kept rescale.  Returns (kept mask, thr)."""
+    ml = [float(x) / size for x in lgsum]
+    srt = sorted(ml)
+    r = q * (len(ml) - 1)
+    lo = int(np.floor(r))
+    hi = min(lo + 1, len(ml) - 1)
+    thr = srt[lo] + (r - lo) * (srt[hi] - srt[lo])
+    return [m >= thr for m in ml], thr
+
+
+@pytest.mark.parametrize('D', [16, 32, 64, 128])
+def test_quantile_canon_equals_torch_quantile_at_defaults(D):
+    """At the reference's gate_q = 0.25 (w = 0.75: the interpolation's product is exact) quantile_canon is
+    torch.quantile bit for bit; at other q within two float32 ulps of it."""
+    g = torch.Generator().manual_seed(D)
+    x = torch.randn(64, D, generator=g) * 3
+    assert torch.equal(S.quantile_canon(x, 0.25), torch.quantile(x, 0.25, dim=-1, keepdim=True))
+    for q in (0.0, 0.1, 0.3, 0.5, 0.9, 1.0):
+        a, b = S.quantile_canon(x, q), torch.quantile(x, q, dim=-1, keepdim=True)
+        assert ((a - b).abs() <= 2 * torch.finfo(torch.float32).eps * b.abs().clamp(min=1e-30)).all(), q
+
+
+def test_index_log_canon_within_one_ulp():
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(4, 1000, generator=g) * torch.logspace(-8, 3, 1000)
+    k[0, :10] = 0
+    a, b = S.index_log(k, True), S.index_log(k, False)
+    assert ((a - b).abs() <= torch.finfo(torch.float32).eps * b.abs().clamp(min=1e-30)).all()
+    want = torch.log((k.double().abs().float() + 1e-6).double())
+    assert (a.double() - want).abs().max() <= (torch.finfo(torch.float32).eps * want.abs()).max()
+
+
+@pytest.mark.parametrize('D,q', [(16, 0.25), (64, 0.25), (128, 0.25), (32, 0.5), (64, 0.1)])
+def test_gate_apply_matches_brute_force(D, q):
+    """gate_apply (both modes) keeps the dimensions the plain-Python quantile rule keeps, zeroes the rest,
+    scales the kept ones by D / kept; with distinct mean logs the kept count has the closed form
+    D - ceil(q (D - 1))."""
+    g = torch.Generator().manual_seed(D + int(q * 100))
+    n, size = 40, 8.0
+    raw = torch.randn(n, D, generator=g)
+    lgs = torch.randn(n, D, generator=g) * 5 - 20
+    for canon in (False, True):
+        out = S.gate_apply(raw, lgs, size, q, canon)
+        for i in range(n):
+            keep, thr = _gate_brute(raw[i].tolist(), lgs[i].tolist(), size, q)
+            ml = (lgs[i] / size).tolist()
+            if min(abs(m - thr) for m in ml) < 1e-5 * max(1.0, abs(thr)):
+                continue   # a dimension at the threshold: float32 and float64 may disagree
+            kept = sum(keep)
+            assert kept == D - int(np.ceil(q * (D - 1) - 1e-9)), (i, kept)
+            scale = D / kept
+            for d in range(D):
+                want = raw[i, d].item() * scale if keep[d] else 0.0
+                assert abs(out[i, d].item() - want) <= 1e-6 * max(1.0, abs(want)), (i, d)
+
+
+def test_gate_all_equal_keeps_everything():
+    """Equal mean logs (all-zero keys: log(1e-6) everywhere) tie at the threshold: every dimension is kept
+    and the scale is 1, so the gated vector is the raw one."""
+    raw = torch.randn(3, 32)
+    lgs = torch.full((3, 32), 8 * float(np.log(np.float32(1e-6))))
+    for canon in (False, True):
+        assert torch.equal(S.gate_apply(raw, lgs, 8.0, 0.25, canon), raw)
+
+
+@pytest.mark.parametrize('gate_min', [0, 3])
+def test_gated_levels_are_gate_of_closed_form_sums(gate_min):
+    """level_sums with the gate: level l is gate_apply of the closed-form segment sums of the keys and of their
+    log-magnitudes (within float32 rounding of the sums) at l >= gate_min, the plain sums below."""
+    g = torch.Generator().manual_seed(9)
+    k = torch.randn(1, 2, 64, 16, generator=g) * torch.linspace(0.01, 3, 16)
+    out = S.level_sums(k, 5, gate=True, gate_q=0.25, gate_min=gate_min, canon=True)
+    lg = S.index_log(k, True).double()
+    for l in range(1, 6):
+        raw = k.double().reshape(1, 2, 64 >> l, 1 << l, 16).sum(3)
+        if l < gate_min:
+            assert (out[l].double() - raw).abs().max() < 1e-5
+            continue
+        lgs = lg.reshape(1, 2, 64 >> l, 1 << l, 16).sum(3)
+        for h in range(2):
+            for m in range(64 >> l):
+                keep, thr = _gate_brute(raw[0, h, m].tolist(), lgs[0, h, m].tolist(), float(1 << l), 0.25)
+                ml = (lgs[0, h, m] / (1 << l)).tolist()
+                if min(abs(x - thr) for x in ml) < 1e-4:
+                    continue
+                want = raw[0, h, m] * torch.tensor(keep, dtype=torch.float64) * (16 / sum(keep))
+                assert (out[l][0, h, m].double() - want).abs().max() < 1e-4, (l, h, m)
+
+
+def test_planted_quantile_mistake_is_caught(monkeypatch):
+    """A quantile taken from the wrong end (1 - q) must fail the brute-force gate check."""
+    orig = S.quantile_canon
+    monkeypatch.setattr(S, 'quantile_canon', lambda x, q: orig(x, 1.0 - q))
+    with pytest.raises(AssertionError):
+        test_gate_apply_matches_brute_force(64, 0.1)

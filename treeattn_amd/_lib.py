@@ -103,6 +103,13 @@ SIGNATURES = {
     'ta_rowmm_ex': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32,
                             c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'ta_mfma_peak': (c_i32, [c_i32, c_i32, c_vp, c_vp]),
+    'ta_level_log_sums': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                  _P(c_vp), _P(c_i64), _P(c_i64), _P(c_i32), c_vp, c_i64, c_vp]),
+    'ta_gate_levels': (c_i32, [c_i32, c_i32, c_i32, c_i32, _P(c_vp), _P(c_vp), _P(c_vp), _P(c_i64), _P(c_i64),
+                               _P(c_i32), _P(c_i64), c_f32, c_vp]),
+    'ta_gate_append': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp),
+                               _P(c_vp), _P(c_vp), _P(c_i64), _P(c_i64), _P(c_i32), c_i32, c_f32, _P(KvPages),
+                               c_vp]),
     'ta_neighbor_pass': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp,
                                  c_i64, c_i64, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                  c_i32, c_i32, c_f32, c_i32, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),

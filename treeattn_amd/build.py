@@ -31,6 +31,7 @@ SOURCES = {
     'step.hip': [],
     'calib.hip': [],
     'neighbor.hip': [],
+    'gate.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

@@ -33,7 +33,11 @@ __device__ __forceinline__ void store_node(const LevelOut& lo, int blevel, int b
 // of 64 consecutive rows, reduced by adjacent pairs with a carry stack (left + right, float32); the
 // workgroup then combines its NSEG segment sums the same way.  Nodes are written when their binary level
 // is an output level; the workgroup's total (the node of size 64*NSEG rows) goes to `tot` when complete.
-template <typename T, int D>
+// LOGT: the rows are index keys whose log-magnitudes are summed instead (the gate's statistic): each key
+// value x (after the sink is zeroed) enters as the float32 rounding of the double log of |x| + 1e-6.
+__device__ __forceinline__ float index_log_key(float x) { return (float)log((double)(fabsf(x) + 1e-6f)); }
+
+template <typename T, int D, bool LOGT = false>
 __global__ __launch_bounds__(256) void level_pass_kernel(const T* __restrict__ in, int64_t isb, int64_t ish,
                                                          int64_t isr, int H, int n_rows, int base,
                                                          int zero_first, LevelOut lo, float* __restrict__ tot,
@@ -55,6 +59,7 @@ __global__ __launch_bounds__(256) void level_pass_kernel(const T* __restrict__ i
     const int64_t r = row0 + i;
     if (r < n_rows) {
       float x = (zero_first && r == 0) ? 0.0f : to_f32(src[r * isr]);
+      if constexpr (LOGT) x = index_log_key(x);
       int lv = 0;
 #pragma unroll
       for (int k = 0; k < 6; ++k) {
@@ -231,7 +236,7 @@ int chunk_rows(int D) { return 64 * (256 / D); }
 template <typename T, int D>
 struct LevelSumsRun {
   static int run(const void* k, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int t_end, int zero_sink,
-                 const LevelOut& lo, int top_blevel, float* ws, hipStream_t st) {
+                 const LevelOut& lo, int top_blevel, float* ws, hipStream_t st, bool logt = false) {
     const int CH = chunk_rows(D);
     const int LCH = log2i(CH);
     int64_t nA = ((int64_t)t_end / CH + 1) * B * H * D;
@@ -249,7 +254,10 @@ struct LevelSumsRun {
       float* tot = more ? bufs[pass & 1] : nullptr;
       const int tot_chunks = n_rows / CH;
       dim3 grid(n_chunks, B * H);
-      if (pass == 0) {
+      if (pass == 0 && logt) {
+        hipLaunchKernelGGL((level_pass_kernel<T, D, true>), grid, dim3(256), 0, st, (const T*)src, sb, sh, sr, H,
+                           n_rows, base, zero_sink, lo, tot, tot_chunks);
+      } else if (pass == 0) {
         hipLaunchKernelGGL((level_pass_kernel<T, D>), grid, dim3(256), 0, st, (const T*)src, sb, sh, sr, H, n_rows,
                            base, zero_sink, lo, tot, tot_chunks);
       } else {
@@ -366,10 +374,34 @@ extern "C" int64_t ta_level_sums_workspace_size(int B, int H, int t_end, int D) 
   return (nA + nB) * (int64_t)sizeof(float);
 }
 
+namespace {
+int level_sums_impl(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int t_end,
+                    int D, int zero_sink, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                    const int64_t* lv_sh, const int32_t* lv_blevel, float* ws, int64_t ws_bytes, void* stream,
+                    bool logt);
+}
+
 extern "C" int ta_level_sums(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H,
                              int t_end, int D, int zero_sink, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
                              const int64_t* lv_sh, const int32_t* lv_blevel, float* ws, int64_t ws_bytes,
                              void* stream) {
+  return level_sums_impl(k, k_dtype, ksb, ksh, kst, B, H, t_end, D, zero_sink, n_levels, lv_ptr, lv_sb, lv_sh,
+                         lv_blevel, ws, ws_bytes, stream, false);
+}
+
+extern "C" int ta_level_log_sums(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H,
+                                 int t_end, int D, int zero_sink, int n_levels, float* const* lv_ptr,
+                                 const int64_t* lv_sb, const int64_t* lv_sh, const int32_t* lv_blevel, float* ws,
+                                 int64_t ws_bytes, void* stream) {
+  return level_sums_impl(k, k_dtype, ksb, ksh, kst, B, H, t_end, D, zero_sink, n_levels, lv_ptr, lv_sb, lv_sh,
+                         lv_blevel, ws, ws_bytes, stream, true);
+}
+
+namespace {
+int level_sums_impl(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int t_end,
+                    int D, int zero_sink, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                    const int64_t* lv_sh, const int32_t* lv_blevel, float* ws, int64_t ws_bytes, void* stream,
+                    bool logt) {
   if (B <= 0 || H <= 0 || t_end < 0 || n_levels < 0 || n_levels > kMaxLevels) {
     set_error("ta_level_sums: bad sizes");
     return TA_ERR_ARG;
@@ -394,8 +426,9 @@ extern "C" int ta_level_sums(const void* k, int k_dtype, int64_t ksb, int64_t ks
     return TA_ERR_WORKSPACE;
   }
   return dispatch_dt_d<LevelSumsRun>(k_dtype, D, k, ksb, ksh, kst, B, H, t_end, zero_sink, lo, prev, ws,
-                                    (hipStream_t)stream);
+                                    (hipStream_t)stream, logt);
 }
+}  // namespace
 
 extern "C" int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H,
                                int Nq, int D, const int32_t* tq, int64_t tq_sb, int n_levels,

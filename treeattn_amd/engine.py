@@ -102,6 +102,14 @@ class SegState:
             self.cache = pages.cache(layer)
         self.dtype = dtype
         self.levels = [torch.zeros(batch, H, Tcap >> l, dh, device=dev) for l in self.shape.blevels]
+        # the mean-log gate (engine.py:27, 35-39): log-magnitude sums of every level, gated vectors of the levels
+        # at or above gate_min_level; the selection scores those (score_levels), the append forms all three
+        self.gated = SEL.gate_on(cfg)
+        if self.gated:
+            self.lg = [torch.zeros_like(t) for t in self.levels]
+            self.gl = [torch.zeros_like(t) if f else None for t, f in zip(self.levels, SEL.gated_flags(cfg, self.shape))]
+        else:
+            self.lg = self.gl = None
         NS = cfg.nb_store
         Tst = Tcap if (cfg.neighbors or cfg.beam_mode == 'pred') else 0   # read and written by the list path
         self.st_leaf = torch.zeros(batch, H, Tst, NS, dtype=torch.int32, device=dev)
@@ -147,15 +155,30 @@ class SegState:
         c.pool[pg.reshape(-1), 0] = kk.reshape(n, H, nb, c.leaf, dh).reshape(-1, c.leaf, dh).to(c.dtype)
         c.pool[pg.reshape(-1), 1] = vv.reshape(n, H, nb, c.leaf, dh).reshape(-1, c.leaf, dh).to(c.dtype)
 
+    @property
+    def score_levels(self):
+        """The node vectors the selection scores: the gated vectors where the gate applies, else the sums."""
+        if not self.gated:
+            return self.levels
+        return [g if g is not None else r for r, g in zip(self.levels, self.gl)]
+
     def level_of(self, l):
         try:
-            return self.levels[self.shape.blevels.index(l)]
+            return self.score_levels[self.shape.blevels.index(l)]
         except ValueError:
             raise KeyError('binary level %d is not a tree level of this cache' % l) from None
 
     def getU(self, l, cand):
-        """Node vectors of `cand` at binary level l (engine.py:35-39)."""
+        """Node vectors of `cand` at binary level l, gated where the gate applies (engine.py:35-39)."""
         return gather_nodes(self.level_of(l), cand)
+
+    def gate_append(self, tpos):
+        """The gate's part of appending positions tpos (after kv_append): log sums and gated vectors of the
+        nodes ending there (engine.py:47, 53-54)."""
+        if self.gated and self.shape.n_levels:
+            Kc, _ = self.kv()
+            K.gate_append(Kc, tpos, self.levels, self.lg, self.gl, self.shape.blevels, self.shape.arity,
+                          float(self.cfg.gate_q))
 
     def _tpos(self, t):
         if torch.is_tensor(t):
@@ -165,8 +188,10 @@ class SegState:
     def add(self, t, k, v):
         """Store position t (k, v: (B,H,dh)) and form the nodes it completes (engine.py:41-55)."""
         Kc, Vc = self.kv()
-        K.kv_append(k.to(self.dtype), v.to(self.dtype), Kc, Vc, self._tpos(t), self.levels, self.shape.leaf,
+        tpos = self._tpos(t)
+        K.kv_append(k.to(self.dtype), v.to(self.dtype), Kc, Vc, tpos, self.levels, self.shape.leaf,
                     self.shape.arity)
+        self.gate_append(tpos)
         self.ksum += k.float()
 
     def rows(self, b0, b1):
@@ -180,6 +205,9 @@ class SegState:
         if self.cache is not None:
             v.cache = self.cache.rows(b0, b1)
         v.levels = [t[b0:b1] for t in self.levels]
+        if self.gated:
+            v.lg = [t[b0:b1] for t in self.lg]
+            v.gl = [t[b0:b1] if t is not None else None for t in self.gl]
         return v
 
     def fill(self, K_, V_, t_end=None):
@@ -189,7 +217,10 @@ class SegState:
             self.pages.ensure(T)
         self.write_rows(0, K_, V_)
         t_end = T if t_end is None else t_end
-        SEL.build_pyramid(K_.to(self.dtype), self.shape, t_end=t_end, out=self.levels)
+        kd = K_.to(self.dtype)
+        SEL.build_pyramid(kd, self.shape, t_end=t_end, out=self.levels)
+        if self.gated:
+            SEL.build_gated(kd, self.shape, self.levels, self.cfg, t_end=t_end, lg=self.lg, gl=self.gl)
         self.ksum.copy_(K_[:, :, :t_end].float().sum(2))
 
 
@@ -303,7 +334,8 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     if scratch is None:
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
     structural = (not cfg.neighbors) and lhat is None
-    appendable = update and B * H < 4096 and q.dtype == k.dtype == state.dtype
+    # the fused append writes the levels the descent reads: not with the gate, whose descent reads gated vectors
+    appendable = update and B * H < 4096 and q.dtype == k.dtype == state.dtype and not state.gated
     fused = structural and appendable
     Kc, Vc = state.kv()
     if fused and scratch.nsplit == 4 and dh in (64, 128) and wl <= 64 and not cfg.global_pool:
@@ -319,12 +351,13 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         ids, vld, sct = K.tree_descend_append(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0],
                                               Kc, Vc, out=(scratch.ids, scratch.vld, scratch.sct))
     else:
-        ids, vld, sct = K.tree_descend(q, state.levels, tpos.view(B, 1), state.shape, cfg.wmax,
+        ids, vld, sct = K.tree_descend(q, state.score_levels, tpos.view(B, 1), state.shape, cfg.wmax,
                                        out=(scratch.ids, scratch.vld, scratch.sct))
     if structural:
         if update:
             if not appendable:
                 K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
+                state.gate_append(tpos)
             if cfg.global_pool:
                 state.ksum += k[:, :, 0].float()
         out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
@@ -343,7 +376,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         lhat = torch.full((B, H, 1), cfg.beam, dtype=torch.long, device=q.device)
     NS = cfg.nb_store
     if state.shape.n_levels:
-        nid, match, nL, n_tree = K.neighbor_pass(q, state.levels[0], state.st_leaf, state.st_score, state.st_ok,
+        nid, match, nL, n_tree = K.neighbor_pass(q, state.score_levels[0], state.st_leaf, state.st_score, state.st_ok,
                                                  tpos.view(B, 1), cfg, leaf, lhat=lhat.view(B, H, 1))
     else:
         Wn = cfg.nb_window
@@ -362,6 +395,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         state.st_ok[bidx, hidx, tt, :n] = vb[:, :, 0, :n]
         if not appendable:
             K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
+            state.gate_append(tpos)
         state.ksum += k[:, :, 0].float()
     out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
     K.seg_attn(q, Kc, Vc, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out, keys=scratch.keys,
@@ -427,7 +461,7 @@ class Decoder:
         # attn_split: workgroups per query of the per-op decode attention (default: decode_nsplit's choice)
         self.attn_split = attn_split
         can = (self.fused and self.dh == 64 and batch <= 32 and not groups and not cfg.neighbors
-               and cfg.beam_mode != 'pred' and n_layer <= 64)
+               and cfg.beam_mode != 'pred' and n_layer <= 64 and not SEL.gate_on(cfg))
         if one_launch and not can:
             raise ValueError('one_launch: needs a bf16 model with head_dim 64, batch <= 32, neighbours off and a '
                              'fixed budget')
@@ -627,6 +661,10 @@ class Decoder:
                 st.write_rows(b0, k, v)
                 lv = [t[b0:b1] for t in st.levels]
                 K.level_sums(k, st.shape.blevels, out=lv, t_end=T0, zero_sink=True)
+                if st.gated:
+                    # the gate's log sums and gated vectors of the prompt's nodes; the selection scores those
+                    lv = SEL.build_gated(k, st.shape, lv, cfg, t_end=T0, lg=[t[b0:b1] for t in st.lg],
+                                         gl=[t[b0:b1] if t is not None else None for t in st.gl])
                 out = torch.empty(nb, T0, H, dh, device=self.dev, dtype=v.dtype)
                 if cfg.neighbors or cfg.beam_mode == 'pred':
                     # the forward's selection with neighbour borrowing and/or the budget head's per-query budget

@@ -107,12 +107,9 @@ def _binary_levels_as_list(S, Lm):
 
 @torch.no_grad()
 def level_sums_min(kidx, Lm, gate, gate_q, gate_min):
-    """{l: (b,H,T>>l,dh)} float32 node sums for l = 1..Lm (fastseg.py:238-251); the gate is not built yet."""
-    if gate:
-        raise NotImplementedError('treeattn_amd: the mean-log gate is not built yet')
+    """{l: (b,H,T>>l,dh)} float32 node vectors for l = 1..Lm (fastseg.py:238-251): sums, gated at l >= gate_min."""
     _use_fast(kidx)
-    out = K.level_sums(kidx, list(range(1, Lm + 1)), zero_sink=False)
-    return {l: out[l - 1] for l in range(1, Lm + 1)}
+    return SEL.binary_level_sums(kidx, Lm, gate, gate_q, gate_min)
 
 
 @torch.no_grad()

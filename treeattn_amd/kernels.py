@@ -111,8 +111,9 @@ def _cache_dtype(Kc):
 
 
 # ----------------------------------------------------------------------------------------------- builder
-def level_sums(k, blevels, out=None, t_end=None, zero_sink=True):
-    """Node sums of binary levels `blevels` of keys k (B,H,T,D): list of (B,H,T>>l,D) float32."""
+def level_sums(k, blevels, out=None, t_end=None, zero_sink=True, log_magnitudes=False):
+    """Node sums of binary levels `blevels` of keys k (B,H,T,D): list of (B,H,T>>l,D) float32.  With
+    log_magnitudes: sums of log(|x| + 1e-6) of the index keys instead (the mean-log gate's statistic)."""
     L.require_gpu(k)
     B, H, T, D = k.shape
     t_end = T if t_end is None else int(t_end)
@@ -124,11 +125,69 @@ def level_sums(k, blevels, out=None, t_end=None, zero_sink=True):
     ws = torch.empty(max(1, L.lib().ta_level_sums_workspace_size(B, H, t_end, D)) // 4 + 1, device=k.device,
                      dtype=torch.float32)
     sb, sh, sn = L.rows3(k)
-    L.call('ta_level_sums', L.ptr(k), L.dtype_code(k), sb, sh, sn, B, H, t_end, D, int(bool(zero_sink)),
-           len(blevels), L.ptr_array(out), L.i64_array([o.stride(0) for o in out]),
+    L.call('ta_level_log_sums' if log_magnitudes else 'ta_level_sums', L.ptr(k), L.dtype_code(k), sb, sh, sn, B,
+           H, t_end, D, int(bool(zero_sink)), len(blevels), L.ptr_array(out), L.i64_array([o.stride(0) for o in out]),
            L.i64_array([o.stride(1) for o in out]), L.i32_array(list(blevels)), L.ptr(ws), ws.numel() * 4,
            L.stream())
     return out
+
+
+def _level_strides(levels, D):
+    for t in levels:
+        if t.dtype != torch.float32 or t.stride(-1) != 1 or t.stride(-2) != D:
+            raise ValueError('gate: float32 levels with contiguous node rows')
+    return L.i64_array([t.stride(0) for t in levels]), L.i64_array([t.stride(1) for t in levels])
+
+
+def gate_levels(raw, lg, out, blevels, gate_q, n_nodes=None):
+    """Mean-log gate (seg.py:16-23) of every node of the tree levels: out[j] = gate(raw[j], lg[j]) for the levels
+    whose out[j] is a tensor (None: level not gated); n_nodes[j] nodes per (b, h) (default all)."""
+    live = [j for j, o in enumerate(out) if o is not None]
+    if not live:
+        return out
+    L.require_gpu(*[raw[j] for j in live], *[lg[j] for j in live], *[out[j] for j in live])
+    B, H, _, D = raw[live[0]].shape
+    sb, sh = _level_strides(raw, D)
+    for j in live:
+        if raw[j].stride() != lg[j].stride() or raw[j].stride() != out[j].stride():
+            raise ValueError('gate_levels: raw, lg and out of a level must share a layout')
+    nn = [t.shape[2] for t in raw] if n_nodes is None else list(n_nodes)
+    outs = [o if o is not None else raw[j] for j, o in enumerate(out)]
+    optr = (ctypes.c_void_p * len(out))(*[o.data_ptr() if o is not None else None for o in out])
+    L.call('ta_gate_levels', B, H, D, len(raw), L.ptr_array(raw), L.ptr_array(lg), optr, sb, sh,
+           L.i32_array(list(blevels)), L.i64_array(nn), float(gate_q), L.stream())
+    del outs
+    return out
+
+
+def gate_apply(raw, lgsum, size, gate_q):
+    """seg.py:16-23 on any (..., dh) tensors of node sums and their log-magnitude sums over `size` positions
+    (a power of two): the gated vectors, float32, through ta_gate_levels."""
+    L.require_gpu(raw, lgsum)
+    D = raw.shape[-1]
+    bl = int(round(math.log2(size)))
+    if (1 << bl) != int(size):
+        raise ValueError('gate_apply: the node size must be a power of two')
+    r = raw.float().reshape(1, 1, -1, D).contiguous()
+    g = lgsum.float().reshape(1, 1, -1, D).contiguous()
+    out = torch.empty_like(r)
+    if r.shape[2]:
+        gate_levels([r], [g], [out], [bl], gate_q)
+    return out.view(raw.shape)
+
+
+def gate_append(Kc, t_pos, raw, lg, out, blevels, arity, gate_q):
+    """The gate's share of a decode append (engine.py:47, 53-54), after kv_append: log sums and gated vectors
+    of the nodes ending at t_pos[b].  Kc: contiguous (B,H,Tcap,D) K cache or a PagedCache; raw / lg / out the
+    tree levels (out[j] None: not gated)."""
+    L.require_gpu(t_pos, *raw, *lg, *_cache_tensors(Kc, Kc))
+    B, H, _, D = raw[0].shape
+    sb, sh = _level_strides(raw, D)
+    kp, _, csb, csh, cst, tcap, pages = _cache(Kc, Kc)
+    optr = (ctypes.c_void_p * len(out))(*[o.data_ptr() if o is not None else None for o in out])
+    L.call('ta_gate_append', kp, L.dtype_code(Kc), csb, csh, cst, tcap, B, H, D, L.ptr(t_pos), len(raw),
+           L.ptr_array(raw), L.ptr_array(lg), optr, sb, sh, L.i32_array(list(blevels)), _ilog2(arity),
+           float(gate_q), pages, L.stream())
 
 
 # ----------------------------------------------------------------------------------------------- descent

@@ -14,7 +14,10 @@ from . import selection as SEL
 
 
 def gate_apply(raw, lgsum, size, gate_q):
-    raise NotImplementedError('treeattn_amd: the mean-log gate (seg.py:16-23) is not built yet')
+    """Mean-log dilution gate (seg.py:16-23) of node sums raw given their log-magnitude sums over `size`
+    positions (ta_gate_levels)."""
+    _lib.require_gpu(raw, lgsum)
+    return K.gate_apply(raw, lgsum, size, gate_q)
 
 
 class LevelSource:
@@ -34,10 +37,10 @@ class LevelSource:
 
 def _levels_of(getU, shape, q):
     src = getattr(getU, '__self__', None)
-    if src is not None and hasattr(src, 'levels') and hasattr(src, 'shape') and not getattr(src.cfg, 'gate', False):
-        if src.shape.blevels[:shape.n_levels] != shape.blevels:       # SegState.getU without the gate
+    if src is not None and hasattr(src, 'score_levels') and hasattr(src, 'shape'):
+        if src.shape.blevels[:shape.n_levels] != shape.blevels:       # SegState.getU (gated where gated)
             raise ValueError('the cache tree does not match the requested levels')
-        return src.levels[:shape.n_levels]
+        return src.score_levels[:shape.n_levels]
     if isinstance(getU, LevelSource):
         return getU.tree_levels(shape)
     # any other getU(l, cand) (seg.py:133-134, engine.py:35-39): every node of each level, asked for once
@@ -55,12 +58,9 @@ def _levels_of(getU, shape, q):
 
 @torch.no_grad()
 def level_sums(kidx, Lm, gate, gate_q):
-    """{l: (b,H,T>>l,dh)} for l = 1..Lm (seg.py:26-41)."""
-    if gate:
-        raise NotImplementedError('treeattn_amd: the mean-log gate is not built yet')
+    """{l: (b,H,T>>l,dh)} for l = 1..Lm (seg.py:26-41); with the gate every level is gated."""
     _lib.require_gpu(kidx)
-    out = K.level_sums(kidx, list(range(1, Lm + 1)), zero_sink=False)
-    return {l: out[l - 1] for l in range(1, Lm + 1)}
+    return SEL.binary_level_sums(kidx, Lm, gate, gate_q, 0)
 
 
 @torch.no_grad()
@@ -86,7 +86,7 @@ def neighbor_pass(q, getU1, st_leaf, st_score, st_ok, tq, cfg, T=None):
         S1 = getU1.S[1]
     else:
         src = getattr(getU1, '__self__', None)
-        if src is not None and hasattr(src, 'level_of') and not getattr(src.cfg, 'gate', False):
+        if src is not None and hasattr(src, 'level_of'):
             S1 = src.level_of(1)
         else:
             b, H = q.shape[0], q.shape[1]

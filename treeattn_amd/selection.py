@@ -16,13 +16,54 @@ def cfg_shape(cfg, T):
 
 
 def check_supported(cfg):
-    if getattr(cfg, 'gate', False):
-        raise NotImplementedError('treeattn_amd: the mean-log gate (cfg.gate=True) is not built yet')
+    """Every Config option of the seg path is served (the gate included)."""
+    return True
 
 
 def build_pyramid(k, shape, t_end=None, out=None):
     """Node sums of every tree level from keys k (B,H,T,D), sink zeroed (seg.py:128-131)."""
     return K.level_sums(k, shape.blevels, out=out, t_end=t_end, zero_sink=True)
+
+
+def gate_on(cfg):
+    return bool(getattr(cfg, 'gate', False))
+
+
+def gated_flags(cfg, shape):
+    """Which tree levels the mean-log gate applies to: binary level >= gate_min_level (engine.py:37)."""
+    gmin = int(getattr(cfg, 'gate_min_level', 0))
+    return [gate_on(cfg) and l >= gmin for l in shape.blevels]
+
+
+def binary_level_sums(kidx, Lm, gate, gate_q, gate_min):
+    """{l: node vectors} for binary levels l = 1..Lm of index keys kidx (summed as given: seg.py:26-41,
+    fastseg.py:238-251): the sums, gated at l >= gate_min when `gate`."""
+    blevels = list(range(1, Lm + 1))
+    raw = K.level_sums(kidx, blevels, zero_sink=False)
+    if gate:
+        lg = K.level_sums(kidx, blevels, zero_sink=False, log_magnitudes=True)
+        gl = [torch.empty_like(r) if l >= gate_min else None for r, l in zip(raw, blevels)]
+        K.gate_levels(raw, lg, gl, blevels, float(gate_q))
+        raw = [g if g is not None else r for r, g in zip(raw, gl)]
+    return {l: raw[l - 1] for l in blevels}
+
+
+def build_gated(k, shape, raw, cfg, t_end=None, lg=None, gl=None):
+    """The gate's levels over raw node sums `raw` of keys k (B,H,T,D) (seg.py:26-41, fastseg.py:238-251): lg the
+    sums of log(|k| + 1e-6), gl the gated vectors of the levels the gate applies to.  Returns the levels the
+    selection scores: gl[j] where gated, raw[j] elsewhere (raw itself without the gate)."""
+    if not gate_on(cfg):
+        return raw
+    T = k.shape[2]
+    t_end = T if t_end is None else int(t_end)
+    flags = gated_flags(cfg, shape)
+    if lg is None:
+        lg = [torch.zeros_like(r) for r in raw]
+    K.level_sums(k, shape.blevels, out=lg, t_end=t_end, zero_sink=True, log_magnitudes=True)
+    if gl is None:
+        gl = [torch.zeros_like(r) if f else None for r, f in zip(raw, flags)]
+    K.gate_levels(raw, lg, gl, shape.blevels, float(cfg.gate_q), n_nodes=[t_end >> l for l in shape.blevels])
+    return [g if g is not None else r for r, g in zip(raw, gl)]
 
 
 def neighbor_pass(q, S0, st_leaf, st_score, st_ok, tq, cfg, leaf):
@@ -109,13 +150,14 @@ def assemble(sel, tq, cfg, b, H):
 
 
 def select(q, k, lhat, cfg, shape=None, levels=None):
-    """Whole-sequence selection (seg.py:122-140 / fastseg.py:302-314) on the device.  `levels`: node sums
-    already built for `shape` (a decode cache's), else they are built from k.
-    Returns (sel dict, ids, vld, sct, levels)."""
+    """Whole-sequence selection (seg.py:122-140 / fastseg.py:302-314) on the device.  `levels`: the levels the
+    selection scores, already built for `shape` (a decode cache's: gated where the gate applies), else they are
+    built from k (with the gate when cfg.gate).  Returns (sel dict, ids, vld, sct, levels)."""
     check_supported(cfg)
     b, H, T, dh = q.shape
     shape = shape or cfg_shape(cfg, T)
-    levels = build_pyramid(k, shape) if levels is None else levels
+    if levels is None:
+        levels = build_gated(k, shape, build_pyramid(k, shape), cfg)
     tq = torch.arange(T, device=q.device)
     ids32, vld8, sct = K.tree_descend(q, levels, tq, shape, cfg.wmax)
     ids, vld = ids32.long(), vld8.bool()
