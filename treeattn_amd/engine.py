@@ -54,19 +54,30 @@ class PagePool:
         """Pages for positions < t_end (at most Tcap) of the given sequences (all by default): a sequence's
         blocks get consecutive pages, head by head."""
         need = (min(int(t_end), self.Tcap) + self.leaf - 1) // self.leaf
-        for b in (range(self.B) if seqs is None else seqs):
+        todo = [b for b in (range(self.B) if seqs is None else seqs) if self.nblk[b] < need]
+        if not todo:
+            return
+        n_all = sum((need - self.nblk[b]) * self.H for b in todo)
+        if n_all > len(self.free):
+            raise RuntimeError('PagePool: out of pages (%d needed, %d free of %d): raise max_tokens'
+                               % (n_all, len(self.free), self.P))
+        lo = min(self.nblk[b] for b in todo)
+        for b in todo:
             have = self.nblk[b]
-            if have >= need:
-                continue
             n = (need - have) * self.H
-            if n > len(self.free):
-                raise RuntimeError('PagePool: out of pages (%d needed, %d free of %d): raise max_tokens'
-                                   % (n, len(self.free), self.P))
-            for h in range(self.H):
-                for j in range(have, need):
-                    self.host[b, h, j] = self.free.pop()
-            self.table[b, :, have:need].copy_(self.host[b, :, have:need])
+            ids = self.free[len(self.free) - n:]       # taken from the end of the free list, last entry first
+            del self.free[len(self.free) - n:]
+            ids.reverse()
+            self.host[b, :, have:need] = torch.tensor(ids, dtype=torch.int32).view(self.H, need - have)
             self.nblk[b] = need
+        # one copy of the changed columns, ordered on the current stream after the steps already queued (they
+        # read no entry that changes); staged in pinned memory so the host does not wait for those steps
+        rows = slice(min(todo), max(todo) + 1)
+        src = self.host[rows, :, lo:need].contiguous()
+        if self.table.is_cuda:
+            self.table[rows, :, lo:need].copy_(src.pin_memory(), non_blocking=True)
+        else:
+            self.table[rows, :, lo:need].copy_(src)
 
     def release(self, b):
         """Return sequence b's pages (its cache rows are forgotten)."""
