@@ -349,8 +349,8 @@ extern "C" int ta_rowmm_ex(const void* X, int64_t ldx, const void* W, int64_t ld
   dim3 grid((N + 31) / 32, (M + 31) / 32, S);
   hipStream_t st = (hipStream_t)stream;
   // the narrow-tile kernel computes the same bits; the tails run on the four-wavefront tile
-  // (the narrow tile stages the LayerNorm weight in LDS: K up to 2048 with the prologue)
-  int nc = tail != TAIL_NONE || cols == -1 || (ln_w != nullptr && K > 2048) ? 0
+  // (the narrow tile stages X's rows and the LayerNorm weight in LDS: K up to kNtLnMaxK with the prologue)
+  int nc = tail != TAIL_NONE || cols == -1 || (ln_w != nullptr && K > kNtLnMaxK) ? 0
                                                                           : (cols ? cols : rowmm_auto_cols(M, N, S));
   while (S > 1 && nc > 0 && nc < 32 && (int64_t)((N + nc - 1) / nc) * ((M + 31) / 32) * 4 > kRowmmCountBytes)
     nc *= 2;   // one arrival counter per output tile

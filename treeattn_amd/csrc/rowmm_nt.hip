@@ -9,13 +9,17 @@
 // v_mfma_f32_32x32x16_bf16 depends only on its own column of B, so a tile whose B operand holds NC real
 // columns (the other lanes feed zeros) computes those columns bit for bit as the 32-column tile does.
 //
-// Workgroup: eight wavefronts; wavefront v runs K-block stream v (blocks v, v + 8, v + 16, ... of the split)
-// with its operands loaded straight into registers in the MFMA layout (lane -> row lane % 32 of X and column
-// lane % 32 of W; lanes 32-63 take the second half of each 64-wide block).  With the LayerNorm prologue, the
-// first four wavefronts also read X's rows for the statistics (8 threads per row, mm_tile's order) and share
-// them through LDS; every wavefront normalises its own operand registers.  The eight partial tiles are summed
-// in stream order through LDS.  With splits > 1 the split protocol of mm_tile follows (write-through partials,
-// a device-scope arrival count, the last workgroup sums the partials in split order and applies the epilogue).
+// Workgroup: eight wavefronts; wavefront v runs K-block stream v (blocks v, v + 8, v + 16, ... of the split).
+// W is loaded straight into registers in the MFMA layout (lane -> column lane % 32 of W; lanes 32-63 take the
+// second half of each 64-wide block).  Without the LayerNorm, X's operand pieces are loaded into registers the
+// same way (lane -> row lane % 32).  With it, X's 32 rows and the LayerNorm weight go straight into LDS
+// (direct-to-LDS loads, issued before W); the first four wavefronts sum the statistics from there (8 threads
+// per row, mm_tile's order), every thread normalises its share of the staged pieces in place while W is still
+// arriving, and the products read the normalised pieces from LDS.  The staging, statistics and normalisation
+// are rolled loops: a dispatch starts with a cold instruction cache, and unrolled straight-line code there
+// costs more in instruction fetch than it saves.  The eight partial tiles are summed in stream order through
+// LDS.  With splits > 1 the split protocol of mm_tile follows (write-through partials, a device-scope arrival
+// count, the last workgroup sums the partials in split order and applies the epilogue).
 #include "rowmm_tile.hpp"
 
 namespace ta {
@@ -23,8 +27,8 @@ namespace ta {
 constexpr int kNtWaves = kMmStreams;           // one wavefront per K-block stream
 constexpr int kNtThreads = kNtWaves * kWave;   // 512
 constexpr int kNtRound = 2;                    // blocks of a stream held in registers at once
-constexpr int kNtStatPieces = 16;              // statistics loads in flight per thread (K <= 1024 in one go)
-constexpr int kNtLnMaxK = 2048;                // LayerNorm prologue: K up to this (the weight is staged in LDS)
+// LayerNorm prologue: K up to kNtLnMaxK, X's 32 rows staged in LDS with row stride K + 8 (kNtXsBytes)
+constexpr int kNtXsBytes = 32 * (kNtLnMaxK + 8) * 2;
 
 // s_waitcnt vmcnt(n) for a wave-uniform n of 0, 4, 8, 12 or 16 (anything else waits for every load).
 __device__ __forceinline__ void nt_wait_vm(int n) {
@@ -40,10 +44,15 @@ __device__ __forceinline__ void nt_wait_vm(int n) {
 template <bool LN, int EPI, int NC>
 __global__ __launch_bounds__(kNtThreads) void rowmm_nt_kernel(MmArgs a) {
   static_assert(NC == 4 || NC == 8 || NC == 16 || NC == 32, "NC divides 32");
+  constexpr int kRedBytes = kNtWaves * 32 * (NC + 1) * 4;
+  constexpr int kBufBytes = LN && kNtXsBytes > kRedBytes ? kNtXsBytes : kRedBytes;
+  // With the LayerNorm, X's 32 rows are staged here (row stride K + 8 elements) and the partial tiles of the
+  // eight streams reuse the space once every wavefront has read its operands.
+  __shared__ __align__(16) unsigned char s_buf[kBufBytes];
   __shared__ float s_mean[32], s_rstd[32];
-  __shared__ float red[kNtWaves][32][NC + 1];
   __shared__ __align__(16) bf16_t s_gam[LN ? kNtLnMaxK : 8];
   __shared__ uint32_t s_last;
+  auto red = reinterpret_cast<float (*)[32][NC + 1]>(s_buf);
   constexpr int NOUT = 32 * NC;   // outputs of a tile: output e is row e / NC, column e % NC
   constexpr int EPT = (NOUT + kNtThreads - 1) / kNtThreads;   // outputs per thread: e = tid + k * kNtThreads
   const int tid = threadIdx.x, lane = lane_id();
@@ -56,10 +65,8 @@ __global__ __launch_bounds__(kNtThreads) void rowmm_nt_kernel(MmArgs a) {
   auto out_e = [&](int k) { return tid + k * kNtThreads; };
 
   // Loads, per wavefront in issue order: the residual (EPT per lane, residual epilogue); with the LayerNorm,
-  // in wavefronts 0-3, one piece of the LayerNorm weight and the statistics pieces (kNtStatPieces); then X's
-  // operand pieces (4 per block of the stream's first round) and W's (4 per block, only the lanes of the
-  // tile's NC columns).  A wavefront loads only the blocks its stream has, so the waits below count
-  // 4 * nb0 operand loads of each kind.
+  // X's 32 rows and the LayerNorm weight straight into LDS (no registers); without it, X's operand pieces (4
+  // per block of the stream's first round); then W's (4 per block, only the lanes of the tile's NC columns).
   uint16_t rbits[EPT];
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
@@ -71,16 +78,24 @@ __global__ __launch_bounds__(kNtThreads) void rowmm_nt_kernel(MmArgs a) {
     }
   }
 
-  // LayerNorm statistics: thread (r, part) of the first four wavefronts sums piece `part` of every 64-wide
-  // block of row r in block order (mm_tile's order)
-  const bool stat_wave = LN && v < 4;
-  const int sr = tid >> 3, spart = tid & 7;
-  const bf16_t* sxr = a.X + (int64_t)(m0 + sr < a.M ? m0 + sr : a.M - 1) * a.ldx + 8 * spart;
-  uint4 sx[kNtStatPieces], gpiece;
-  if (stat_wave) {
-    gpiece = ldg16(a.gam + 8 * (tid % (a.K / 8)));   // thread t < K / 8 stages piece t of the weight
-#pragma unroll
-    for (int i = 0; i < kNtStatPieces; ++i) sx[i] = ldg16(sxr + (64 * i < a.K ? 64 * i : 0));
+  const int xs_ld = a.K + 8;   // LDS row stride of the staged X rows (elements)
+  bf16_t* s_x = reinterpret_cast<bf16_t*>(s_buf);
+  if constexpr (LN) {
+    // 1 KB per wavefront instruction: lane L of chunk c fills LDS elements [512 c + 8 L, + 8) of the staged
+    // rows; the 8 padding elements of a row and the elements past the last row are not loaded
+    const int total = 32 * xs_ld;
+#pragma unroll 1
+    for (int c = v; c * 512 < total; c += kNtWaves) {
+      const int e = c * 512 + 8 * lane, r = e / xs_ld, col = e - r * xs_ld;
+      if (e < total && col < a.K)
+        __builtin_amdgcn_global_load_lds((const void*)(a.X + (int64_t)(m0 + r < a.M ? m0 + r : a.M - 1) * a.ldx + col),
+                                         (lds_void*)(s_x + c * 512), 16, 0, 0);
+    }
+    if (v * 512 < a.K)   // the weight: K / 8 pieces of 16 bytes
+      if (64 * v + lane < a.K / 8)
+        __builtin_amdgcn_global_load_lds((const void*)(a.gam + 512 * v + 8 * lane), (lds_void*)(s_gam + 512 * v),
+                                         16, 0, 0);
+    asm volatile("" ::: "memory");   // issued before W (loads complete in issue order)
   }
 
   // operands of this wavefront's stream: X rows (lane -> row lane % 32), W columns (lane -> column lane % 32
@@ -95,12 +110,14 @@ __global__ __launch_bounds__(kNtThreads) void rowmm_nt_kernel(MmArgs a) {
     return n < kNtRound ? n : kNtRound;
   };
   auto load_round = [&](int round, int nb) {
+    if constexpr (!LN) {
 #pragma unroll
-    for (int i = 0; i < kNtRound; ++i) {
-      if (i >= nb) break;
-      const int64_t k = (int64_t)(blk0 + v + kNtWaves * (kNtRound * round + i)) * 64;
+      for (int i = 0; i < kNtRound; ++i) {
+        if (i >= nb) break;
+        const int64_t k = (int64_t)(blk0 + v + kNtWaves * (kNtRound * round + i)) * 64;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xa[i][j] = ldg16(xrow + k + 8 * j);
+        for (int j = 0; j < 4; ++j) xa[i][j] = ldg16(xrow + k + 8 * j);
+      }
     }
 #pragma unroll
     for (int i = 0; i < kNtRound; ++i) {
@@ -119,72 +136,85 @@ __global__ __launch_bounds__(kNtThreads) void rowmm_nt_kernel(MmArgs a) {
   load_round(0, nb0);
 
   if constexpr (LN) {
-    if (stat_wave) {
-      nt_wait_vm(8 * nb0);   // the weight piece and the statistics pieces have landed; the operands may not
-      if (tid < a.K / 8) *reinterpret_cast<uint4*>(s_gam + 8 * tid) = gpiece;
+    // W's 4 * nb0 loads are the only ones issued after the staging (lane 0 of every wavefront has a column, so
+    // each W load is issued): once this many are left, the staged rows and the weight have landed
+    nt_wait_vm(4 * nb0);
+    lds_barrier();
+    // statistics: thread (r, part) of the first four wavefronts sums piece `part` of every 64-wide block of row
+    // r in block order (mm_tile's order), then the row's 8 threads combine
+    if (v < 4) {
+      const int sr = tid >> 3, spart = tid & 7;
+      const bf16_t* xr = s_x + sr * xs_ld + 8 * spart;
       float s = 0.0f, s2 = 0.0f;
-#pragma unroll
-      for (int i = 0; i < kNtStatPieces; ++i)   // a piece past K adds zeros (s never holds -0)
-        mm_add8(64 * i < a.K ? sx[i] : make_uint4(0, 0, 0, 0), s, s2);
-      for (int k0 = 64 * kNtStatPieces; k0 < a.K; k0 += 64 * 8) {   // K > 1024: the rest, 8 pieces at a time
-        uint4 u[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) u[i] = k0 + 64 * i < a.K ? ldg16(sxr + k0 + 64 * i) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) mm_add8(u[i], s, s2);
-      }
+#pragma unroll 4
+      for (int k = 0; k < a.K; k += 64) mm_add8(*reinterpret_cast<const uint4*>(xr + k), s, s2);
       s = group_sum<8>(s);
       s2 = group_sum<8>(s2);
       if (spart == 0) mm_stats(s, s2, a.K, a.eps, s_mean[sr], s_rstd[sr]);
     }
-    lds_barrier();   // the statistics and the weight are in LDS; the operands may still be in flight
+    lds_barrier();
+    // every staged piece normalised in place (while W arrives)
+#pragma unroll 1
+    for (int pc = tid; pc < 4 * a.K; pc += kNtThreads) {   // 32 rows x K / 8 pieces
+      const int r = pc / (a.K / 8), col = 8 * (pc - r * (a.K / 8));
+      uint4* px = reinterpret_cast<uint4*>(s_x + r * xs_ld + col);
+      *px = mm_ln_piece(*px, *reinterpret_cast<const uint4*>(s_gam + col), s_mean[r], s_rstd[r]);
+    }
+    lds_barrier();
   }
 
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  // the products of the nb blocks held in xa / wb (round `round` of this stream), in block order
+  // the products of the nb blocks held in xa / wb (or, with the LayerNorm, staged normalised in LDS), in
+  // block order
   auto products = [&](int round, int nb, bool first) {
-    float mean = 0.0f, rstd = 0.0f;
     if constexpr (LN) {
-      mean = s_mean[rl];
-      rstd = s_rstd[rl];
-    }
-    if (first) nt_wait_vm(4 * nb);   // X has landed; W may be in flight while X is normalised
-    bf16x8 av[kNtRound][4];
+      if (first) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < kNtRound; ++i) {
-      if (i >= nb) break;
-      const int kb = (blk0 + v + kNtWaves * (kNtRound * round + i)) * 64;
+      for (int i = 0; i < kNtRound; ++i) {
+        if (i >= nb) break;
+        const int kb = (blk0 + v + kNtWaves * (kNtRound * round + i)) * 64;
+        const bf16_t* xp = s_x + rl * xs_ld + kb + 8 * ph;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint4 xu = xa[i][j];
-        if constexpr (LN)
-          xu = mm_ln_piece(xu, *reinterpret_cast<const uint4*>(s_gam + kb + 8 * (ph + j)), mean, rstd);
-        u32x4_t xr{xu.x, xu.y, xu.z, xu.w};
-        asm volatile("" : "+v"(xr));   // normalised before the wait for W below (not moved past it)
-        __builtin_memcpy(&av[i][j], &xr, 16);
+        for (int j = 0; j < 4; ++j) {
+          bf16x8 av, bv;
+          const uint4 xu = *reinterpret_cast<const uint4*>(xp + 8 * j);
+          __builtin_memcpy(&av, &xu, 16);
+          __builtin_memcpy(&bv, &wb[i][j], 16);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+        }
       }
-    }
-    if (first) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      if (first) nt_wait_vm(4 * nb);   // X has landed; W may be in flight
+      bf16x8 av[kNtRound][4];
 #pragma unroll
-    for (int i = 0; i < kNtRound; ++i) {
-      if (i >= nb) break;
+      for (int i = 0; i < kNtRound; ++i) {
+        if (i >= nb) break;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bf16x8 bv;
-        __builtin_memcpy(&bv, &wb[i][j], 16);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i][j], bv, acc, 0, 0, 0);
+        for (int j = 0; j < 4; ++j) __builtin_memcpy(&av[i][j], &xa[i][j], 16);
+      }
+      if (first) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < kNtRound; ++i) {
+        if (i >= nb) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          bf16x8 bv;
+          __builtin_memcpy(&bv, &wb[i][j], 16);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i][j], bv, acc, 0, 0, 0);
+        }
       }
     }
   };
   products(0, nb0, true);
   const int nround = (nblk + kNtWaves * kNtRound - 1) / (kNtWaves * kNtRound);
-  for (int round = 1; round < nround; ++round) {   // more than 16 blocks in the split
+  for (int round = 1; round < nround; ++round) {   // more than 16 blocks in the split (never with the LayerNorm)
     const int nb = blocks_of_round(round);
     load_round(round, nb);
     products(round, nb, false);
   }
+  if constexpr (LN) lds_barrier();   // every wavefront has read its operands: the space takes the partial tiles
   // 32x32 MFMA output layout: lane -> column lane % 32; register i -> row 8(i/4) + 4(lane/32) + i%4
   if (rl < NC) {
 #pragma unroll

@@ -51,6 +51,7 @@ constexpr int kMmSlots = 2;                        // blocks per stream and roun
 constexpr int kMmRound = kMmStreams * kMmSlots;    // 16 blocks (1024 of K) per round
 constexpr int kMmRedBytes = kMmStreams * 32 * 33 * 4;
 constexpr int kMmTailBytes = 64 * 4 + 16;          // mean, rstd, last
+constexpr int kNtLnMaxK = 896;                     // narrow tiles with the LayerNorm prologue: K up to this
 
 // LDS of a tile whose splits span at most `kblocks` K blocks: X (4 KB per block of a round) and the
 // LayerNorm weight of the round (128 B per block, plus the slack of a whole last copy), aliased by the
