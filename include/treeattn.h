@@ -489,6 +489,40 @@ int ta_gate_append(const void* Kc, int dtype, int64_t csb, int64_t csh, int64_t 
  */
 int ta_mfma_peak(int wgs, int iters, float* out, void* stream);
 
+/*
+ * Block forest (the reference's attn='block' attention), step 1 -- replaces forest.py:47-75 build_forest with
+ * forest.py:12-33 two_means_order and forest.py:36-44 soft_gate.  Keys k (B, H, T, D) (row 0, the sink, counted
+ * as zero), cut into blocks of `block` keys (a power of two in [4, 64] dividing T; depth = log2(block / 2)):
+ * every block's keys are ordered by depth rounds of 2-means splits of its groups (kmeans_iters iterations each),
+ * perm (B, H, T) int32 gets rank -> position inside the block, and sums[l] (B, H, (T / block) << l, D) float32
+ * (l = 0..depth; strides sb[l], sh[l], node rows contiguous) the node sums of every level (level 0 = the block,
+ * level depth = pairs of ranks; flat node id = block index * 2^l + m).  With gate, the soft gate (quantile
+ * gate_q, temperature gate_temp) is applied to every node sum in place; lg[l] (same layout) is its scratch.
+ */
+int ta_forest_build(const void* k, int dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int T, int D,
+                    int block, int kmeans_iters, int gate, float gate_q, float gate_temp, int32_t* perm,
+                    float* const* sums, float* const* lg, const int64_t* sb, const int64_t* sh, void* stream);
+
+/*
+ * Block forest, step 2 -- replaces attention.py:88-148 (the descent over the block trees, the budget's cut,
+ * leaves to key positions, static keys and their duplicates).  For every query t of q (B, H, T, D): the roots of
+ * all blocks are scored (q . node sum; valid: the blocks before t's own), the best min(wmax, C) kept (valid while
+ * their rank is below bq_desc), their two children scored, ... down to the pairs.  Writes leaf / leafv
+ * (B, H, T, wl) and cand (B, H, T, Kc) int32: [own block positions (the causal ones) | 0, t-1, t-2 (inside
+ * earlier blocks) | the two keys of every used leaf, all first keys then all second keys], -1 where unused; a
+ * leaf is used when valid and its rank is below bq_use[b, h, t] (bq_use NULL: every valid leaf); a key equal to
+ * a valid static key is dropped.  lv_cur / lv_cv (NULL or (depth + 1, B, H, T, lv_stride)): every level's
+ * candidates and their validity (-1 / 0 past the level's count), for the routing loss.  wl, Kc and the widest
+ * level: ta_forest_shape.
+ */
+int ta_forest_descend(const void* q, int dtype, int64_t qsb, int64_t qsh, int64_t qst, int B, int H, int T, int D,
+                      int block, const float* const* sums, const int64_t* sb, const int64_t* sh,
+                      const int32_t* perm, int wmax, int bq_desc, const int32_t* bq_use, int32_t* leaf,
+                      uint8_t* leafv, int32_t* cand, int32_t* lv_cur, uint8_t* lv_cv, int lv_stride, void* stream);
+
+/* Leaves per query (wl), candidate-list width (Kc = block + 3 + 2 wl) and widest level of ta_forest_descend. */
+int ta_forest_shape(int T, int block, int wmax, int* wl, int* kc, int* widest);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,7 +3,8 @@
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Restates model.py:12-93 (pre-LN blocks, bias-free
 linears, GELU MLP, learned positions, tied output layer, N(0, 0.02) init with the residual projections
 rescaled) with the attention module of fastseg.py:318-405 (fixed budget, or the budget head of
-fastseg.py:330-335 / 352-365 when beam_mode='pred') computed by the oracle.
+fastseg.py:330-335 / 352-365 when beam_mode='pred') computed by the oracle -- or, for attn='block', the block
+forest's module of attention.py:10-176 (forest_ref).
 Parameter names match the reference's state_dict so weights move between this model, the product's
 model and both decoders.
 """
@@ -14,6 +15,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .attn_ref import budget_head, seg_sparse_attend
+from .forest_ref import tree_sparse_attend
 
 
 class LayerNorm(nn.Module):
@@ -55,6 +57,34 @@ class SegAttentionRef(nn.Module):
         return self.c_proj(out.transpose(1, 2).reshape(b, T, C))
 
 
+class TreeAttentionRef(nn.Module):
+    """The block forest's module (attention.py:10-45) with the oracle's sparse_attend (forest_ref)."""
+
+    def __init__(self, cfg, mode='faithful'):
+        super().__init__()
+        self.cfg = cfg
+        C = cfg.n_embd
+        self.H = cfg.n_head
+        self.dh = C // cfg.n_head
+        self.mode = mode
+        self.c_attn = nn.Linear(C, 3 * C, bias=False)
+        self.c_proj = nn.Linear(C, C, bias=False)
+        if cfg.beam_mode == 'pred':
+            fin = self.dh + 1 + self.H + (self.dh if cfg.global_pool else 0)
+            self.pred = nn.Sequential(nn.Linear(fin, 64), nn.ReLU(), nn.Linear(64, len(cfg.beam_classes)))
+        self.aux = {}
+
+    def forward(self, x):
+        b, T, C = x.shape
+        q, k, v = self.c_attn(x).split(C, dim=2)
+        q, k, v = [a.view(b, T, self.H, self.dh).transpose(1, 2) for a in (q, k, v)]
+        pw = None
+        if self.cfg.beam_mode == 'pred':
+            pw = dict(w1=self.pred[0].weight, b1=self.pred[0].bias, w2=self.pred[2].weight, b2=self.pred[2].bias)
+        out, self.aux, _, _ = tree_sparse_attend(q, k, v, self.cfg, pw=pw, mode=self.mode)
+        return self.c_proj(out.transpose(1, 2).reshape(b, T, C))
+
+
 class MLP(nn.Module):
     def __init__(self, cfg):
         super().__init__()
@@ -70,7 +100,7 @@ class Block(nn.Module):
     def __init__(self, cfg, mode):
         super().__init__()
         self.ln1 = LayerNorm(cfg.n_embd)
-        self.attn = SegAttentionRef(cfg, mode)
+        self.attn = SegAttentionRef(cfg, mode) if cfg.attn == 'seg' else TreeAttentionRef(cfg, mode)
         self.ln2 = LayerNorm(cfg.n_embd)
         self.mlp = MLP(cfg)
 

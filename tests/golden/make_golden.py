@@ -21,6 +21,10 @@ closed form, brute force or invariant pins:
                         fp32, seed 0) at the reference's own tree (leaf groups of 2 keys, binary), wmax =
                         beam = 8, neighbours off: a 512-token prompt (seed 0) then 256 greedy tokens; the
                         greedy tokens and every greedy step's logits.
+* forest_block.npz      forest.build_forest (permutation and node sums, with and without the soft gate) on seeded
+                        (1,2,256,16) keys, and TreeAttention.sparse_attend (attention.py:47-176) on seeded
+                        (1,2,128,16) q, k, v: fixed budget, budget head + gate, train mode with the routing
+                        loss; the parameter summary of a block-attention GPT under a seed.
 * decode_small.npz      engine.Decoder on a 2-layer 64-wide model (vocab 64, Tcap 256) in reference-default
                         mode (neighbour borrowing on) and with the budget head (pred + global_pool): logits of
                         256 teacher-forced steps, plus GPT.forward logits over the same tokens.
@@ -182,6 +186,51 @@ def decode_small(ta, steps=256):
     np.savez_compressed(os.path.join(HERE, 'decode_small.npz'), **out)
 
 
+def forest_fixtures(ta):
+    """forest.build_forest and TreeAttention.sparse_attend (the block forest, attention.py / forest.py): the
+    permutation and node sums of seeded keys (with and without the soft gate), the module's output and aux for a
+    fixed budget and for the budget head with the gate (eval, and train with the routing loss on), and the
+    parameter summary of a block-attention GPT under a seed."""
+    from treeattn.attention import TreeAttention
+    from treeattn.config import Config
+    from treeattn.forest import build_forest
+    from treeattn.model import GPT
+    out = {}
+    k = seeded((1, 2, 256, 16), 301)
+    k_idx = k.clone()
+    k_idx[:, :, 0] = 0
+    out['k'] = k.numpy()
+    for name, gate in (('plain', False), ('gate', True)):
+        cfg = Config(tree_block=32, gate=gate)
+        perm, sums = build_forest(k_idx, 32, 4, cfg)
+        out[name + '_perm'] = perm.numpy().astype(np.int16)
+        for lvl, sm in enumerate(sums):
+            out['%s_sums%d' % (name, lvl)] = sm.numpy()
+    q, kk, v = seeded((1, 2, 128, 16), 311), seeded((1, 2, 128, 16), 312), seeded((1, 2, 128, 16), 313)
+    out.update(q=q.numpy(), kk=kk.numpy(), v=v.numpy())
+    base = dict(seq_len=128, n_head=2, n_embd=32, tree_block=32, wmax=4, beam=2, beam_classes=(2, 3, 4))
+    for name, kw in (('fixed', dict()), ('predgate', dict(beam_mode='pred', global_pool=True, gate=True)),
+                     ('route', dict(route_weight=1.0))):
+        cfg = Config(**base, **kw)
+        torch.manual_seed(9)
+        m = TreeAttention(cfg)
+        m.train(name != 'fixed')
+        with torch.no_grad():
+            o = m.sparse_attend(q, kk, v)
+        out[name + '_out'] = o.numpy()
+        out[name + '_aux_keys'] = np.array(sorted(m.aux))
+        out[name + '_aux'] = np.array([float(m.aux[a]) for a in sorted(m.aux)])
+        for pn, p in m.state_dict().items():
+            if pn.startswith('pred.'):
+                out[name + '_w_' + pn] = p.numpy()
+    cfg = Config(vocab_size=64, seq_len=128, n_layer=2, n_head=2, n_embd=32, tree_block=32, wmax=4, beam=2,
+                 beam_classes=(2, 3, 4), beam_mode='pred', global_pool=True, gate=True)
+    torch.manual_seed(1)
+    for n, sm in model_summary(GPT(cfg)).items():
+        out['init|' + n] = sm
+    np.savez_compressed(os.path.join(HERE, 'forest_block.npz'), **out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--reference', default='/root/reference')
@@ -190,7 +239,7 @@ def main():
     torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
     ta = load_reference(args.reference)
     jobs = dict(select=select_fixtures, attend=attend_fixtures, init=init_fixtures, config1=decode_config1,
-                small=decode_small)
+                small=decode_small, forest=forest_fixtures)
     for name, fn in jobs.items():
         if args.only and name not in args.only.split(','):
             continue

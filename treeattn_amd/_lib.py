@@ -103,6 +103,12 @@ SIGNATURES = {
     'ta_rowmm_ex': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32,
                             c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'ta_mfma_peak': (c_i32, [c_i32, c_i32, c_vp, c_vp]),
+    'ta_forest_build': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                c_f32, c_f32, c_vp, _P(c_vp), _P(c_vp), _P(c_i64), _P(c_i64), c_vp]),
+    'ta_forest_descend': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, _P(c_vp),
+                                  _P(c_i64), _P(c_i64), c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32,
+                                  c_vp]),
+    'ta_forest_shape': (c_i32, [c_i32, c_i32, c_i32, _P(c_i32), _P(c_i32), _P(c_i32)]),
     'ta_level_log_sums': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                   _P(c_vp), _P(c_i64), _P(c_i64), _P(c_i32), c_vp, c_i64, c_vp]),
     'ta_gate_levels': (c_i32, [c_i32, c_i32, c_i32, c_i32, _P(c_vp), _P(c_vp), _P(c_vp), _P(c_i64), _P(c_i64),

@@ -1,0 +1,195 @@
+"""Block-tree sparse attention, the reference's default attention (attention.py:10-176, attn='block').
+
+Same module interface as the reference's TreeAttention (constructor, parameter names, forward, sparse_attend,
+the aux statistics and training losses).  Every query attends exactly to its own block (causal), to three static
+keys (the sink and the two previous positions, inside earlier blocks) and to the keys it finds by a beam descent
+over one content-sorted binary tree per earlier block.  On the GPU:
+
+* ta_forest_build orders every block's keys by rounds of 2-means splits and forms the node sums of every level
+  (forest.py:12-75, soft gate included);
+* ta_forest_descend runs the descent for every query and writes its candidate list (attention.py:88-148);
+* the attention over the list is ta_sparse_attn_fwd, differentiable through ta_sparse_attn_bwd.
+
+The budget head's features and the training-only losses (routing and budget labels taken from the attention
+weights, attention.py:150-174) are host PyTorch over those results, as in the reference.
+"""
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from . import kernels as K
+from .fastseg import sparse_attn
+from .forest import gather_nodes
+
+
+class TreeAttention(nn.Module):
+    """Causal block-tree sparse attention (attention.py:10-45)."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        self.cfg = cfg
+        C = cfg.n_embd
+        self.H = cfg.n_head
+        self.dh = C // cfg.n_head
+        assert cfg.seq_len % cfg.tree_block == 0
+        assert cfg.tree_block >= 4 and (cfg.tree_block & (cfg.tree_block - 1)) == 0
+        self.c_attn = nn.Linear(C, 3 * C, bias=False)
+        self.c_proj = nn.Linear(C, C, bias=False)
+        if cfg.beam_mode == 'pred':
+            assert max(cfg.beam_classes) <= cfg.wmax
+            fin = self.dh + 1 + self.H + (self.dh if cfg.global_pool else 0)
+            self.pred = nn.Sequential(nn.Linear(fin, 64), nn.ReLU(), nn.Linear(64, len(cfg.beam_classes)))
+            self.register_buffer('classes', torch.tensor(list(cfg.beam_classes)), persistent=False)
+            self.register_buffer('head_eye', torch.eye(self.H), persistent=False)
+        self.aux = {}
+
+    def forward(self, x):
+        b, T, C = x.shape
+        q, k, v = self.c_attn(x).split(C, dim=2)
+        q, k, v = [t.view(b, T, self.H, self.dh).transpose(1, 2) for t in (q, k, v)]
+        out = self.sparse_attend(q, k, v)
+        return self.c_proj(out.transpose(1, 2).reshape(b, T, C))
+
+    def sparse_attend(self, q, k, v):
+        """attention.py:47-176 with the selection on the kernels.  q, k, v (b, H, T, dh) on the GPU."""
+        _lib.require_gpu(q, k, v)
+        cfg = self.cfg
+        b, H, T, dh = q.shape
+        B = cfg.tree_block
+        assert T % B == 0 and T <= cfg.seq_len
+        nb = T // B
+        dev = q.device
+        scale = 1.0 / math.sqrt(dh)
+        t = torch.arange(T, device=dev)
+        blk = t // B
+        self.aux = {}
+        if nb == 1:   # one block: exact causal attention inside it
+            own = torch.arange(B, device=dev).view(1, B).expand(T, B)
+            own = torch.where(own <= t.view(T, 1), own, torch.full_like(own, -1))
+            cand = own.to(torch.int32).view(1, 1, T, B).expand(b, H, T, B).contiguous()
+            return sparse_attn(q, k, v, cand, scale)
+
+        # (2) the forest of the blocks' keys (the sink left out of every index vector)
+        depth = K.forest_depth(B)
+        with torch.no_grad():
+            perm, sums = K.forest_build(k.detach(), B, cfg.kmeans_iters, cfg.gate, cfg.gate_q, cfg.gate_temp)
+        pred_mode = cfg.beam_mode == 'pred'
+        # (4) the budget head, from the query and the mean key of the earlier blocks
+        plog = None
+        if pred_mode:
+            qd = q.detach()
+            feats = [qd, torch.log(qd.float().norm(dim=-1, keepdim=True) + 1e-6).to(qd.dtype),
+                     self.head_eye.to(qd.dtype)[None, :, None, :].expand(b, H, T, H)]
+            if cfg.global_pool:
+                cum = sums[0].cumsum(2)
+                prev = torch.cat([torch.zeros_like(cum[:, :, :1]), cum[:, :, :-1]], 2)
+                denom = (torch.arange(nb, device=dev).clamp(min=1) * B).to(prev.dtype).view(1, 1, nb, 1)
+                feats.append((prev / denom)[:, :, blk, :].to(qd.dtype))
+            plog = self.pred(torch.cat(feats, -1))
+        # (3) + (5) the descent and the candidate list with every found leaf; the budget cuts the tree keys
+        want_levels = self.training and cfg.route_weight > 0
+        bq_desc = cfg.wmax if pred_mode else cfg.beam
+        with torch.no_grad():
+            leaf, leafv, cand_full, lv = K.forest_descend(q.detach(), sums, perm, B, cfg.wmax, bq_desc,
+                                                          levels=want_levels)
+        wl = leaf.shape[-1]
+        tree_full = cand_full[..., B + 3:]
+        if pred_mode:
+            bq_pred = self.classes[plog.argmax(-1).detach()]
+            slot = torch.arange(2 * wl, device=dev) % wl
+            keep = slot.view(1, 1, 1, -1) < bq_pred.unsqueeze(-1)
+            cand = torch.cat([cand_full[..., :B + 3], torch.where(keep, tree_full, torch.full_like(tree_full, -1))],
+                             -1)
+        else:
+            cand = cand_full
+        # (6) exact attention over own block + static keys + tree keys
+        out = sparse_attn(q, k, v, cand, scale)
+
+        tvalid = cand[..., B + 3:] >= 0
+        tcount = tvalid.sum(-1).float()
+        sv = cand[..., B:B + 3] >= 0
+        self.aux['keys_tree'] = tcount[:, :, B:].mean().detach()
+        self.aux['keys_total'] = ((t % B + 1).float().mean() + sv.float().sum(-1).mean() + tcount.mean()).detach()
+        if self.training:
+            self._training_signals(q, k, v, cand, cand_full, leaf, lv, perm, plog, depth)
+        return out
+
+    # ------------------------------------------------------------------------------------------ training
+    def _training_signals(self, q, k, v, cand, cand_full, leaf, lv, perm, plog, depth):
+        """attention.py:150-174: the routing loss (route_weight > 0: at every level, cross-entropy of the
+        query's scores against the ancestor of the tree leaf it attends to most) and the budget head's loss
+        (the label: how many of the found leaves hold 90 % of their attention mass)."""
+        cfg = self.cfg
+        b, H, T, dh = q.shape
+        B = cfg.tree_block
+        wl = leaf.shape[-1]
+        dev = q.device
+        scale = 1.0 / math.sqrt(dh)
+        blk = torch.arange(T, device=dev) // B
+        pred_mode = cfg.beam_mode == 'pred'
+        with torch.no_grad():
+            lab_cand = cand_full if pred_mode else cand
+            _, lse = K.sparse_attn_fwd(q.detach(), k.detach(), v.detach(), lab_cand, scale)
+            tkey = lab_cand[..., B + 3:]
+            tv_lab = tkey >= 0
+            kg = gather_nodes(k.detach().float(), tkey.long().clamp(min=0))
+            s = torch.einsum('bhtd,bhtkd->bhtk', q.detach().float(), kg) * scale
+            wt = torch.where(tv_lab, torch.exp(s - lse.unsqueeze(-1)), torch.zeros_like(s))
+            best = wt.argmax(-1)
+            ok = tv_lab.gather(-1, best.unsqueeze(-1)).squeeze(-1) & (wt.max(-1).values > 0) & \
+                (blk >= 1).view(1, 1, T)
+            leafnode = leaf.long().gather(-1, (best % wl).unsqueeze(-1)).squeeze(-1)
+            if pred_mode:
+                leaf_mass = wt[..., :wl] + wt[..., wl:]
+                total = leaf_mass.sum(-1, keepdim=True)
+                need = (leaf_mass.cumsum(-1) < 0.9 * total).sum(-1) + 1
+                label = (need.unsqueeze(-1) > self.classes).sum(-1).clamp(max=len(self.classes) - 1)
+        route = q.new_zeros(()).float()
+        if cfg.route_weight > 0 and bool(ok.any()):
+            sums_t = _torch_forest_sums(k, perm, B, depth, cfg)   # differentiable in k
+            terms = []
+            for lvl in range(depth + 1):
+                cur_l, cv_l = lv[0][lvl], lv[1][lvl]   # slots past the level's width: -1, invalid
+                sc = torch.einsum('bhtd,bhtwd->bhtw', q, gather_nodes(sums_t[lvl], cur_l.long().clamp(min=0)))
+                sc = sc.masked_fill(~cv_l, float('-inf'))
+                anc = leafnode >> (depth - lvl)
+                match = (cur_l.long() == anc.unsqueeze(-1)) & cv_l
+                rows = ok & match.any(-1)
+                if bool(rows.any()):
+                    size = B // (2 ** lvl)
+                    lg = (sc / (size * math.sqrt(dh))).float()
+                    terms.append(F.cross_entropy(lg[rows], match.float().argmax(-1)[rows]))
+            if terms:
+                route = torch.stack(terms).mean()
+        self.aux['route'] = route
+        if pred_mode:
+            prow = (blk >= 1).view(1, 1, T).expand(b, H, T)
+            self.aux['pred'] = F.cross_entropy(plog.float()[prow], label[prow])
+
+
+def _torch_forest_sums(k, perm, B, depth, cfg):
+    """Node sums of every level as differentiable functions of k (the routing loss's gradient path,
+    forest.py:65-75): the keys in the forest's order (perm from the kernel, the sink zeroed), summed per node,
+    soft-gated as forest.py:36-44 when the gate is on."""
+    b, H, T, d = k.shape
+    nb = T // B
+    mask = torch.ones(1, 1, T, 1, device=k.device, dtype=k.dtype)
+    mask[:, :, 0] = 0
+    kb = (k * mask).reshape(b * H * nb, B, d)
+    kp = kb.gather(1, perm.long().reshape(b * H * nb, B, 1).expand(-1, -1, d))
+    out = []
+    for lvl in range(depth + 1):
+        n = 2 ** lvl
+        grp = kp.reshape(b * H * nb, n, B // n, d)
+        sm = grp.sum(2)
+        if cfg.gate:
+            ml = torch.log(grp.float().abs() + 1e-6).mean(2)
+            thr = torch.quantile(ml, cfg.gate_q, dim=-1, keepdim=True)
+            g = torch.sigmoid((ml - thr) / cfg.gate_temp)
+            kept = g.sum(-1, keepdim=True).clamp(min=1.0)
+            sm = (sm.float() * g * (sm.shape[-1] / kept)).to(sm.dtype)
+        out.append(sm.reshape(b, H, nb * n, d))
+    return out

@@ -32,6 +32,7 @@ SOURCES = {
     'calib.hip': [],
     'neighbor.hip': [],
     'gate.hip': [],
+    'forest.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

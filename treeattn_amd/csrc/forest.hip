@@ -1,0 +1,504 @@
+// Block forest: one content-sorted binary tree per block of `block` keys, and a beam descent over the trees of
+// the blocks before the query's own (the reference's default attention, attn='block').
+//
+// Reference functions replaced: forest.py:12-33 two_means_order, forest.py:36-44 soft_gate, forest.py:47-75
+// build_forest, and attention.py:88-148 (the descent over the block trees, the budget's cut, leaves to key
+// positions, the static keys and their duplicates).  The attention over the candidate list this produces is
+// ta_sparse_attn_fwd / ta_sparse_attn_bwd.
+//
+// Arithmetic order (the CPU oracle's canonical mode computes the same, bit for bit):
+//  * a 2-means mean or centroid over the S members of a group: the halving tree over the members in group order
+//    (member i + member i + S/2, then + S/4, ...), then the division by the member count;
+//  * node sums and the gate's log-magnitude sums: adjacent pairs, ((x0 + x1) + (x2 + x3)) + ...;
+//  * dot products and squared distances: per-dimension float32 products in canon_dot's order;
+//    dist = (|x|^2 - 2 x.c) + |c|^2;
+//  * argmax / argmin: the first index; the member order: stable ascending sort of the projections;
+//  * soft gate: the float32 rounding of the double-precision log and logistic, the threshold as
+//    torch.quantile's linear interpolation in float32, the kept mass by the halving tree over dimensions;
+//  * descent ranking: valid first, score descending, node id ascending (invalid candidates by slot).
+// Node sums are float32 whatever the key type.
+#pragma clang fp contract(off)
+
+#include "descend.hpp"
+
+namespace ta {
+
+constexpr int kForestMaxRoots = 1024;   // blocks per sequence the descent ranks at its first level
+constexpr int kForestMaxW = 64;         // wmax
+
+// canon_dot's value for two D-vectors held by one lane (fa(i), fb(i) give element i): groups of D/16 (at least
+// 1) consecutive products reduced by the halving tree, then the halving tree over the (at most 16) groups.
+template <int D, typename FA, typename FB>
+__device__ __forceinline__ float lane_dot(FA fa, FB fb) {
+  constexpr int G = D < 16 ? D : 16, R = D / G;
+  float g[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    float p[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) p[i] = fa(R * j + i) * fb(R * j + i);
+#pragma unroll
+    for (int n = R / 2; n >= 1; n /= 2)
+#pragma unroll
+      for (int i = 0; i < n; ++i) p[i] = p[i] + p[i + n];
+    g[j] = p[0];
+  }
+#pragma unroll
+  for (int n = G / 2; n >= 1; n /= 2)
+#pragma unroll
+    for (int i = 0; i < n; ++i) g[i] = g[i] + g[i + n];
+  return g[0];
+}
+
+// Sum over the aligned S-lane segment holding this lane, by the halving tree over the segment's lanes in order
+// (every lane returns the same value: each step adds the lane at distance h, and float addition commutes).
+__device__ __forceinline__ float seg_sum(float v, int S) {
+  for (int h = S >> 1; h >= 1; h >>= 1) v = v + __shfl_xor(v, h, kWave);
+  return v;
+}
+__device__ __forceinline__ float seg_max(float v, int S) {
+  for (int h = S >> 1; h >= 1; h >>= 1) v = fmaxf(v, __shfl_xor(v, h, kWave));
+  return v;
+}
+// The first lane of the segment [gb, gb + S) whose v equals the segment's maximum.
+__device__ __forceinline__ int seg_argmax_first(float v, int gb, int S) {
+  const float mx = seg_max(v, S);
+  const uint64_t seg = S >= 64 ? ~0ull : (((1ull << S) - 1) << gb);
+  return __ffsll((unsigned long long)(__ballot(v == mx) & seg)) - 1;
+}
+
+__device__ __forceinline__ float forest_log(float x) { return (float)log((double)(fabsf(x) + 1e-6f)); }
+
+struct ForestLevels {
+  float* sums[kMaxLevels];   // level l: (B, H, nb << l, D) float32, node rows contiguous
+  float* lg[kMaxLevels];     // the gate's log-magnitude sums (null without the gate)
+  int64_t sb[kMaxLevels];
+  int64_t sh[kMaxLevels];
+};
+
+// One wavefront per (sequence, head, block); lane i holds the key at rank i of the block's current order.
+// Every level splits each group of S = block >> lvl consecutive ranks by a 2-means projection (forest.py:12-33):
+// the members are re-ranked inside the group, so the next level's groups are the halves.  Then the node sums
+// of every level by adjacent pairs (and, with the gate, the log-magnitude sums the same way).
+template <typename T, int D>
+__global__ __launch_bounds__(kWave) void forest_build_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
+                                                             int64_t kst, int H, int nb, int Bk, int depth,
+                                                             int iters, int gate, int32_t* __restrict__ perm,
+                                                             ForestLevels lv) {
+  constexpr int DP = D + 1;   // LDS row stride of the reorder buffer
+  __shared__ float s_x[kWave * DP];
+  __shared__ int s_p[kWave];
+  const int lane = lane_id();
+  const int pb = blockIdx.x, blk = pb % nb, bh = pb / nb, b = bh / H, h = bh % H;
+  const bool live = lane < Bk;
+  const int64_t pos = (int64_t)blk * Bk + (live ? lane : 0);
+  float x[D];
+  load_row_g<T, D>(k + b * ksb + h * ksh + pos * kst, x);
+#pragma unroll
+  for (int d = 0; d < D; ++d) x[d] = live ? (pos == 0 ? x[d] * 0.0f : x[d]) : 0.0f;   // the sink: k * 0
+  int p = lane;
+
+  float c0[D], c1[D];
+  for (int lvl = 0; lvl < depth; ++lvl) {
+    const int S = Bk >> lvl, gb = lane & ~(S - 1), li = lane - gb;
+    // the group mean, then the member farthest from it (a) and the member farthest from a (b)
+#pragma unroll
+    for (int d = 0; d < D; ++d) c0[d] = seg_sum(x[d], S) / (float)S;
+    const float d2 = lane_dot<D>([&](int i) { return x[i] - c0[i]; }, [&](int i) { return x[i] - c0[i]; });
+    const int la = seg_argmax_first(d2, gb, S);
+#pragma unroll
+    for (int d = 0; d < D; ++d) c0[d] = __shfl(x[d], la, kWave);
+    const float d2b = lane_dot<D>([&](int i) { return x[i] - c0[i]; }, [&](int i) { return x[i] - c0[i]; });
+    const int lb = seg_argmax_first(d2b, gb, S);
+#pragma unroll
+    for (int d = 0; d < D; ++d) c1[d] = __shfl(x[d], lb, kWave);
+    const float xx = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return x[i]; });
+    for (int it = 0; it < iters; ++it) {
+      const float cc0 = lane_dot<D>([&](int i) { return c0[i]; }, [&](int i) { return c0[i]; });
+      const float cc1 = lane_dot<D>([&](int i) { return c1[i]; }, [&](int i) { return c1[i]; });
+      const float xc0 = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return c0[i]; });
+      const float xc1 = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return c1[i]; });
+      const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
+      const bool lab1 = dist1 < dist0;   // argmin over the two centroids, the first on ties
+      const float m0 = lab1 ? 0.0f : 1.0f, m1 = lab1 ? 1.0f : 0.0f;
+      const float cnt0 = seg_sum(m0, S), cnt1 = seg_sum(m1, S);
+      const float den0 = fmaxf(cnt0, 1.0f), den1 = fmaxf(cnt1, 1.0f);
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const float n0 = seg_sum(x[d] * m0, S) / den0;
+        c0[d] = cnt0 > 0.0f ? n0 : c0[d];
+      }
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const float n1 = seg_sum(x[d] * m1, S) / den1;
+        c1[d] = cnt1 > 0.0f ? n1 : c1[d];
+      }
+    }
+    const float proj = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return c0[i] - c1[i]; });
+    // stable ascending rank of the projection inside the group, then the member moves to that rank
+    int rank = 0;
+    for (int j = 0; j < S; ++j) {
+      const float pj = __shfl(proj, gb + j, kWave);
+      rank += (pj < proj || (pj == proj && j < li)) ? 1 : 0;
+    }
+    const int slot = gb + rank;
+#pragma unroll
+    for (int d = 0; d < D; ++d) s_x[slot * DP + d] = x[d];
+    s_p[slot] = p;
+    wave_sync();
+#pragma unroll
+    for (int d = 0; d < D; ++d) x[d] = s_x[lane * DP + d];
+    p = s_p[lane];
+    wave_sync();
+  }
+  if (live) perm[(int64_t)bh * nb * Bk + (int64_t)blk * Bk + lane] = p;
+
+  // node sums by adjacent pairs: level depth holds pairs of ranks, level 0 the whole block
+  auto pyramid = [&](float (&y)[D], float* const* out) {
+    for (int l = depth; l >= 0; --l) {
+      const int sz = Bk >> l;   // keys per node at level l
+#pragma unroll
+      for (int d = 0; d < D; ++d) y[d] = y[d] + __shfl_xor(y[d], sz >> 1, kWave);
+      if (live && (lane & (sz - 1)) == 0) {
+        float* row = out[l] + b * lv.sb[l] + h * lv.sh[l] + ((int64_t)blk * (Bk / sz) + lane / sz) * D;
+#pragma unroll
+        for (int d = 0; d < D; ++d) row[d] = y[d];
+      }
+    }
+  };
+  float y[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) y[d] = x[d];
+  pyramid(y, lv.sums);
+  if (gate) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) y[d] = forest_log(x[d]);
+    pyramid(y, lv.lg);
+  }
+}
+
+// The soft gate of every node (forest.py:36-44), one wavefront per node, lane = dimension: mean log-magnitude
+// ml = lg / keys, thr = the gate_q quantile of ml over the dimensions, g = logistic((ml - thr) / temp), the node
+// sum becomes (sum * g) * (D / max(sum of g, 1)).  In place.
+template <int D>
+__global__ __launch_bounds__(256) void forest_gate_kernel(ForestLevels lv, int H, int nb, int Bk, int depth, int lo,
+                                                          float w, float temp) {
+  const int lane = lane_id();
+  const int64_t idx = (int64_t)blockIdx.x * 4 + wave_id();   // node index over all levels of one (b, h)
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  // level l holds nb << l nodes; they follow each other in level order
+  int l = 0;
+  int64_t n = idx, cnt = nb;
+  while (l <= depth && n >= cnt) {
+    n -= cnt;
+    cnt <<= 1;
+    ++l;
+  }
+  if (l > depth) return;
+  const bool in = lane < D;
+  float* row = lv.sums[l] + b * lv.sb[l] + h * lv.sh[l] + n * D;
+  const float* lrow = lv.lg[l] + b * lv.sb[l] + h * lv.sh[l] + n * D;
+  const float raw = in ? row[lane] : 0.0f;
+  const float ml = (in ? lrow[lane] : 0.0f) / (float)(Bk >> l);
+  int rank = 0;
+  for (int e = 0; e < D; ++e) {
+    const float o = __shfl(ml, e, kWave);
+    rank += (o < ml || (o == ml && e < lane)) ? 1 : 0;
+  }
+  const int hi = w > 0.0f ? lo + 1 : lo;
+  const uint64_t blo = __ballot(in && rank == lo), bhi = __ballot(in && rank == hi);
+  const float vlo = __shfl(ml, __ffsll((unsigned long long)blo) - 1, kWave);
+  const float vhi = __shfl(ml, __ffsll((unsigned long long)bhi) - 1, kWave);
+  const float dd = vhi - vlo;
+  const float thr = w < 0.5f ? vlo + w * dd : vhi - dd * (1.0f - w);
+  const float z = (ml - thr) / temp;
+  const float g = in ? (float)(1.0 / (1.0 + exp(-(double)z))) : 0.0f;
+  const float kept = fmaxf(seg_sum(g, D), 1.0f);
+  const float scale = (float)D / kept;
+  if (in) row[lane] = (raw * g) * scale;
+}
+
+struct ForestDesc {
+  const void* q;
+  int64_t qsb, qsh, qst;
+  int H, T, nb, Bk, depth, wmax, bq_desc, wl, Kc;
+  const float* sums[kMaxLevels];
+  int64_t sb[kMaxLevels], sh[kMaxLevels];
+  const int32_t* perm;      // (B, H, nb * Bk)
+  const int32_t* bq_use;    // (B, H, T) leaves the attention uses, or null (all the valid ones)
+  int32_t* leaf;            // (B, H, T, wl)
+  uint8_t* leafv;
+  int32_t* cand;            // (B, H, T, Kc): own block, static keys, tree keys; -1 where unused
+  int32_t* lv_cur;          // (depth + 1, B, H, T, lv_stride) candidates of every level, or null
+  uint8_t* lv_cv;
+  int lv_stride;
+};
+
+// One wavefront per query (attention.py:93-148): score the roots of all blocks (valid: the blocks before the
+// query's own), keep the best min(wmax, C) (valid while their rank is below bq_desc), expand every kept node to
+// its two children (all left children, then all right ones), ... down to the pairs; then the candidate list.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void forest_descend_kernel(ForestDesc p) {
+  constexpr int R = D / 16;
+  __shared__ float s_sc[4][kForestMaxRoots];
+  __shared__ int32_t s_id[4][kForestMaxRoots];
+  __shared__ uint8_t s_v[4][kForestMaxRoots];
+  __shared__ int32_t s_kid[4][kForestMaxW];
+  __shared__ uint8_t s_kv[4][kForestMaxW];
+  const int wv = wave_id(), lane = lane_id();
+  const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;   // grid: (positions / 4, B * H)
+  const int t = blockIdx.x * 4 + wv;
+  if (t >= p.T) return;
+  const int blk = t / p.Bk;
+  float* sc = s_sc[wv];
+  int32_t* id = s_id[wv];
+  uint8_t* vv = s_v[wv];
+  const int g = lane >> 4, j16 = lane & 15;
+  float qr[R];
+  load_row<T, R>(reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh + (int64_t)t * p.qst + R * j16, qr);
+  const int64_t qflat = (int64_t)bh * p.T + t;
+
+  int C = p.nb;
+  for (int c = lane; c < C; c += kWave) {
+    id[c] = c;
+    vv[c] = c < blk ? 1 : 0;
+  }
+  wave_sync();
+  int w = 0;
+  for (int l = 0; l <= p.depth; ++l) {
+    const float* base = p.sums[l] + b * p.sb[l] + h * p.sh[l] + R * j16;
+    for (int c0 = 0; c0 < C; c0 += 4) {
+      const int c = c0 + g;
+      const int cid = id[c < C ? c : 0];
+      float rows[R];
+      load_row_g<float, R>(base + (int64_t)cid * D, rows);
+      const float s = canon_dot<R>(qr, rows);
+      if (c < C && j16 == 0) sc[c] = vv[c] ? s : -INFINITY;
+    }
+    if (p.lv_cur != nullptr) {
+      const int64_t o = ((int64_t)l * gridDim.y * p.T + qflat) * p.lv_stride;
+      for (int c = lane; c < p.lv_stride; c += kWave) {
+        p.lv_cur[o + c] = c < C ? id[c] : -1;
+        p.lv_cv[o + c] = c < C ? vv[c] : 0;
+      }
+    }
+    wave_sync();
+    w = C < p.wmax ? C : p.wmax;
+    for (int c = lane; c < C; c += kWave) {
+      const float si = sc[c];
+      const int ii = id[c];
+      const bool vi = vv[c] != 0;
+      int rank = 0;
+      for (int e = 0; e < C; ++e) {
+        const bool ve = vv[e] != 0;
+        bool better;
+        if (ve != vi) better = ve;
+        else if (vi) better = sc[e] > si || (sc[e] == si && id[e] < ii);
+        else better = e < c;
+        rank += better ? 1 : 0;
+      }
+      if (rank < w) {
+        s_kid[wv][rank] = ii;
+        s_kv[wv][rank] = (vi && rank < p.bq_desc) ? 1 : 0;
+      }
+    }
+    wave_sync();
+    if (l == p.depth) break;
+    C = 2 * w;
+    for (int c = lane; c < C; c += kWave) {
+      const int k0 = c < w ? c : c - w;
+      id[c] = 2 * s_kid[wv][k0] + (c < w ? 0 : 1);
+      vv[c] = s_kv[wv][k0];
+    }
+    wave_sync();
+  }
+
+  // outputs: the leaves, and the candidate list [own block | 0, t-1, t-2 | left keys | right keys]
+  const int wl = p.wl;
+  for (int i = lane; i < wl; i += kWave) {
+    p.leaf[qflat * wl + i] = i < w ? s_kid[wv][i] : -1;
+    p.leafv[qflat * wl + i] = i < w ? s_kv[wv][i] : 0;
+  }
+  int32_t* cr = p.cand + qflat * p.Kc;
+  const int own0 = blk * p.Bk;
+  for (int j = lane; j < p.Bk; j += kWave) cr[j] = own0 + j <= t ? own0 + j : -1;
+  const int s0 = 0, s1 = t - 1, s2 = t - 2;
+  const bool v0 = s0 < own0, v1 = s1 >= 0 && s1 < own0, v2 = s2 >= 0 && s2 < own0;
+  if (lane == 0) {
+    cr[p.Bk] = v0 ? s0 : -1;
+    cr[p.Bk + 1] = v1 ? s1 : -1;
+    cr[p.Bk + 2] = v2 ? s2 : -1;
+  }
+  const int use = p.bq_use != nullptr ? p.bq_use[qflat] : wl;
+  const int32_t* pr = p.perm + (int64_t)bh * p.nb * p.Bk;
+  for (int c = lane; c < 2 * wl; c += kWave) {
+    const int i = c < wl ? c : c - wl;
+    int key = -1;
+    if (i < w && s_kv[wv][i] && i < use) {
+      const int pf = 2 * s_kid[wv][i] + (c < wl ? 0 : 1);
+      const int kk = (pf / p.Bk) * p.Bk + pr[pf];
+      const bool dup = (v0 && kk == s0) || (v1 && kk == s1) || (v2 && kk == s2);
+      key = dup ? -1 : kk;
+    }
+    cr[p.Bk + 3 + c] = key;
+  }
+}
+
+}  // namespace ta
+
+using namespace ta;
+
+namespace {
+bool forest_dim_ok(int D) { return D == 16 || D == 32 || D == 64; }
+}  // namespace
+
+extern "C" int ta_forest_build(const void* k, int dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int T,
+                               int D, int block, int kmeans_iters, int gate, float gate_q, float gate_temp,
+                               int32_t* perm, float* const* sums, float* const* lg, const int64_t* sb,
+                               const int64_t* sh, void* stream) {
+  if (B <= 0 || H <= 0 || T <= 0 || block < 4 || block > kWave || (block & (block - 1)) || T % block ||
+      !forest_dim_ok(D) || kmeans_iters < 0 || perm == nullptr || sums == nullptr || sb == nullptr ||
+      sh == nullptr || (gate && (lg == nullptr || !(gate_q >= 0.0f && gate_q <= 1.0f) || !(gate_temp > 0.0f)))) {
+    set_error("ta_forest_build: bad arguments (block a power of two in [4, 64] dividing T; D 16, 32 or 64)");
+    return TA_ERR_ARG;
+  }
+  const int es = dtype == TA_F32 ? 4 : 2;
+  if (((uintptr_t)k % 16) || (ksb * es) % 16 || (ksh * es) % 16 || (kst * es) % 16) {
+    set_error("ta_forest_build: key rows 16-byte aligned");
+    return TA_ERR_ARG;
+  }
+  const int nb = T / block;
+  int depth = 0;
+  while ((2 << depth) < block) ++depth;   // block / 2 = 2^depth
+  ForestLevels lv{};
+  for (int l = 0; l <= depth; ++l) {
+    if (sums[l] == nullptr || (gate && lg[l] == nullptr)) {
+      set_error("ta_forest_build: a level pointer is null");
+      return TA_ERR_ARG;
+    }
+    lv.sums[l] = sums[l];
+    lv.lg[l] = gate ? lg[l] : nullptr;
+    lv.sb[l] = sb[l];
+    lv.sh[l] = sh[l];
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)((int64_t)B * H * nb));
+#define TA_FB(TT, DD)                                                                                           \
+  hipLaunchKernelGGL((forest_build_kernel<TT, DD>), grid, dim3(kWave), 0, st, (const TT*)k, ksb, ksh, kst, H, \
+                     nb, block, depth, kmeans_iters, gate, perm, lv)
+#define TA_FB_D(TT)                  \
+  switch (D) {                       \
+    case 16: TA_FB(TT, 16); break;   \
+    case 32: TA_FB(TT, 32); break;   \
+    default: TA_FB(TT, 64); break;   \
+  }
+  switch (dtype) {
+    case TA_F32: TA_FB_D(float); break;
+    case TA_F16: TA_FB_D(f16_t); break;
+    case TA_BF16: TA_FB_D(bf16_t); break;
+    default: set_error("ta_forest_build: unknown dtype"); return TA_ERR_ARG;
+  }
+#undef TA_FB_D
+#undef TA_FB
+  int rc = check_launch("forest_build_kernel");
+  if (rc != TA_OK || !gate) return rc;
+  const float r = gate_q * (float)(D - 1);
+  const int lo = (int)floorf(r);
+  const float w = r - (float)lo;
+  // nodes per (b, h): nb * (1 + 2 + ... + 2^depth) = nb * (block - 1), four per workgroup
+  const dim3 ggrid((unsigned)((nb * (int64_t)(block - 1) + 3) / 4), B * H);
+  switch (D) {
+    case 16: hipLaunchKernelGGL((forest_gate_kernel<16>), ggrid, dim3(256), 0, st, lv, H, nb, block, depth, lo, w, gate_temp); break;
+    case 32: hipLaunchKernelGGL((forest_gate_kernel<32>), ggrid, dim3(256), 0, st, lv, H, nb, block, depth, lo, w, gate_temp); break;
+    default: hipLaunchKernelGGL((forest_gate_kernel<64>), ggrid, dim3(256), 0, st, lv, H, nb, block, depth, lo, w, gate_temp); break;
+  }
+  return check_launch("forest_gate_kernel");
+}
+
+extern "C" int ta_forest_descend(const void* q, int dtype, int64_t qsb, int64_t qsh, int64_t qst, int B, int H, int T,
+                                 int D, int block, const float* const* sums, const int64_t* sb, const int64_t* sh,
+                                 const int32_t* perm, int wmax, int bq_desc, const int32_t* bq_use, int32_t* leaf,
+                                 uint8_t* leafv, int32_t* cand, int32_t* lv_cur, uint8_t* lv_cv, int lv_stride,
+                                 void* stream) {
+  if (B <= 0 || H <= 0 || T <= 0 || block < 4 || block > kWave || (block & (block - 1)) || T % block ||
+      !forest_dim_ok(D) || wmax < 1 || wmax > kForestMaxW || T / block > kForestMaxRoots || q == nullptr ||
+      sums == nullptr || perm == nullptr || leaf == nullptr || leafv == nullptr || cand == nullptr ||
+      (lv_cur != nullptr && lv_cv == nullptr)) {
+    set_error("ta_forest_descend: bad arguments (block a power of two in [4, 64] dividing T, at most 1024 blocks; "
+              "D 16, 32 or 64; 1 <= wmax <= 64)");
+    return TA_ERR_ARG;
+  }
+  const int R = D / 16, es = dtype == TA_F32 ? 4 : 2;
+  if (((uintptr_t)q % (R * es)) || (qsb % R) || (qsh % R) || (qst % R)) {
+    set_error("ta_forest_descend: query rows aligned to D / 16 elements");
+    return TA_ERR_ARG;
+  }
+  ForestDesc p{};
+  p.q = q; p.qsb = qsb; p.qsh = qsh; p.qst = qst;
+  p.H = H; p.T = T; p.nb = T / block; p.Bk = block;
+  int depth = 0;
+  while ((2 << depth) < block) ++depth;
+  p.depth = depth;
+  p.wmax = wmax;
+  p.bq_desc = bq_desc;
+  int w = p.nb < wmax ? p.nb : wmax, wide = p.nb;
+  for (int l = 1; l <= depth; ++l) {
+    wide = wide > 2 * w ? wide : 2 * w;
+    w = 2 * w < wmax ? 2 * w : wmax;
+  }
+  p.wl = w;
+  p.Kc = block + 3 + 2 * w;
+  if (lv_cur != nullptr && lv_stride < wide) {
+    set_error("ta_forest_descend: lv_stride below the widest level");
+    return TA_ERR_ARG;
+  }
+  for (int l = 0; l <= depth; ++l) {
+    if (sums[l] == nullptr) {
+      set_error("ta_forest_descend: a level pointer is null");
+      return TA_ERR_ARG;
+    }
+    p.sums[l] = sums[l];
+    p.sb[l] = sb[l];
+    p.sh[l] = sh[l];
+  }
+  p.perm = perm; p.bq_use = bq_use; p.leaf = leaf; p.leafv = leafv; p.cand = cand;
+  p.lv_cur = lv_cur; p.lv_cv = lv_cv; p.lv_stride = lv_stride;
+  const dim3 grid((unsigned)((T + 3) / 4), B * H);
+  hipStream_t st = (hipStream_t)stream;
+#define TA_FD(TT, DD) hipLaunchKernelGGL((forest_descend_kernel<TT, DD>), grid, dim3(256), 0, st, p)
+#define TA_FD_D(TT)                  \
+  switch (D) {                       \
+    case 16: TA_FD(TT, 16); break;   \
+    case 32: TA_FD(TT, 32); break;   \
+    default: TA_FD(TT, 64); break;   \
+  }
+  switch (dtype) {
+    case TA_F32: TA_FD_D(float); break;
+    case TA_F16: TA_FD_D(f16_t); break;
+    case TA_BF16: TA_FD_D(bf16_t); break;
+    default: set_error("ta_forest_descend: unknown dtype"); return TA_ERR_ARG;
+  }
+#undef TA_FD_D
+#undef TA_FD
+  return check_launch("forest_descend_kernel");
+}
+
+// Candidate-list width and leaf count of ta_forest_descend for T positions (for the caller's allocations).
+extern "C" int ta_forest_shape(int T, int block, int wmax, int* wl, int* kc, int* widest) {
+  if (T <= 0 || block < 4 || (block & (block - 1)) || T % block || wmax < 1) {
+    set_error("ta_forest_shape: bad arguments");
+    return TA_ERR_ARG;
+  }
+  const int nb = T / block;
+  int depth = 0;
+  while ((2 << depth) < block) ++depth;
+  int w = nb < wmax ? nb : wmax, wide = nb;
+  for (int l = 1; l <= depth; ++l) {
+    wide = wide > 2 * w ? wide : 2 * w;
+    w = 2 * w < wmax ? 2 * w : wmax;
+  }
+  *wl = w;
+  *kc = block + 3 + 2 * w;
+  *widest = wide;
+  return TA_OK;
+}

@@ -345,6 +345,66 @@ def _kv_rows(k, v):
     return L.ptr(k), L.ptr(v), L.rows3(k), L.rows3(v), k.shape[2], None
 
 
+def forest_depth(block):
+    """Levels below the root of a block tree: block / 2 = 2^depth keys pairs."""
+    return _ilog2(block) - 1
+
+
+def forest_shape(T, block, wmax):
+    """(wl, Kc, widest level) of forest_descend for T positions."""
+    wl, kc, wide = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    L.call('ta_forest_shape', int(T), int(block), int(wmax), ctypes.byref(wl), ctypes.byref(kc), ctypes.byref(wide))
+    return wl.value, kc.value, wide.value
+
+
+def forest_build(k, block, kmeans_iters, gate=False, gate_q=0.25, gate_temp=0.3):
+    """Block forest of index keys k (B, H, T, D) (forest.py:47-75; row 0 counted as zero): returns perm (B, H, T)
+    int32 (rank -> position inside the block) and the node sums of levels 0..depth, float32
+    (B, H, (T / block) << l, D), soft-gated when gate."""
+    L.require_gpu(k)
+    B, H, T, D = k.shape
+    depth = forest_depth(block)
+    nb = T // block
+    perm = torch.empty(B, H, T, device=k.device, dtype=torch.int32)
+    sums = [torch.empty(B, H, nb << l, D, device=k.device, dtype=torch.float32) for l in range(depth + 1)]
+    lg = [torch.empty_like(t) for t in sums] if gate else sums
+    L.call('ta_forest_build', L.ptr(k), L.dtype_code(k), *L.rows3(k), B, H, T, D, int(block), int(kmeans_iters),
+           1 if gate else 0, float(gate_q), float(gate_temp), L.ptr(perm), L.ptr_array(sums), L.ptr_array(lg),
+           L.i64_array([t.stride(0) for t in sums]), L.i64_array([t.stride(1) for t in sums]), L.stream())
+    return perm, sums
+
+
+def forest_descend(q, sums, perm, block, wmax, bq_desc, bq_use=None, levels=False):
+    """Beam descent over the block trees and the attention's candidate list (attention.py:88-148).  q (B,H,T,D);
+    sums / perm from forest_build; bq_desc: leaves kept valid per level (an int); bq_use (B,H,T) the leaves used
+    per query, or None.  Returns (leaf (B,H,T,wl) int32, leafv bool, cand (B,H,T,Kc) int32, per-level
+    (candidates, validity) or None)."""
+    L.require_gpu(q, perm, *sums)
+    B, H, T, D = q.shape
+    wl, kc, wide = forest_shape(T, block, wmax)
+    dev = q.device
+    leaf = torch.empty(B, H, T, wl, device=dev, dtype=torch.int32)
+    leafv = torch.empty(B, H, T, wl, device=dev, dtype=torch.bool)
+    cand = torch.empty(B, H, T, kc, device=dev, dtype=torch.int32)
+    lv = None
+    if levels:
+        n = len(sums)
+        lv = (torch.empty(n, B, H, T, wide, device=dev, dtype=torch.int32),
+              torch.empty(n, B, H, T, wide, device=dev, dtype=torch.bool))
+    use = None
+    if bq_use is not None:
+        use = bq_use.to(device=dev, dtype=torch.int32).contiguous()
+    for t in sums:
+        if t.stride(-1) != 1 or t.stride(-2) != D:
+            raise ValueError('forest levels need contiguous node rows')
+    L.call('ta_forest_descend', L.ptr(q), L.dtype_code(q), *L.rows3(q), B, H, T, D, int(block), L.ptr_array(sums),
+           L.i64_array([t.stride(0) for t in sums]), L.i64_array([t.stride(1) for t in sums]),
+           L.ptr(perm.contiguous()), int(wmax), int(bq_desc), L.ptr(use), L.ptr(leaf), L.ptr(leafv), L.ptr(cand),
+           L.ptr(lv[0]) if lv else ctypes.c_void_p(0), L.ptr(lv[1]) if lv else ctypes.c_void_p(0),
+           wide if lv else 0, L.stream())
+    return leaf, leafv, cand, lv
+
+
 def sparse_attn_fwd(q, k, v, cand, scale):
     """Softmax attention over candidate positions (-1 unused) into k, v (b,H,Tk,dh) or a PagedCache (as k).
     Returns (out (b,H,T,dh) in the values' dtype, lse (b,H,T))."""

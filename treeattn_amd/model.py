@@ -1,7 +1,7 @@
 """GPT-2 style language model around the segment-tree attention (model.py:12-93 of the reference).
 
-Host PyTorch (embeddings, LayerNorm, linears, GELU); attention is SegAttention / DynAttention('seg'), whose
-selection and attention run in the HIP kernels.  Same module names, parameter names, initialisation and
+Host PyTorch (embeddings, LayerNorm, linears, GELU); attention is SegAttention, DynAttention('seg') or the
+block forest's TreeAttention, whose selection and attention run in the HIP kernels.  Same module names, parameter names, initialisation and
 forward signature as the reference, so its checkpoints and tests carry over.
 """
 import math
@@ -10,6 +10,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .attention import TreeAttention
 from .attention_dyn import DynAttention
 from .fastseg import SegAttention
 
@@ -35,12 +36,12 @@ class MLP(nn.Module):
 
 
 def make_attention(cfg):
+    """model.py:37: 'seg' the segment tree, 'dyn' the dynamic-tree module, anything else the block forest."""
     if cfg.attn == 'seg':
         return SegAttention(cfg)
     if cfg.attn == 'dyn':
         return DynAttention(cfg)
-    raise NotImplementedError("treeattn_amd implements the segment-tree attention ('seg'); "
-                              "attn=%r is another tree variant" % cfg.attn)
+    return TreeAttention(cfg)
 
 
 class Block(nn.Module):
