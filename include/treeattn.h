@@ -163,19 +163,26 @@ int ta_sparse_attn_fwd(const void* q, const void* k, const void* v, int dtype,
  * _SparseAttnFn.backward): given q, k, v, the forward's out o and lse, and dout = dL/do, with
  * p_j = exp(scale q.k_j - lse) over the valid slots, Dq = dout . o and ds_j = p_j (dout . v_j - Dq):
  *   dq = scale sum_j ds_j k_j  (written, input dtype, (B,H,T,D) contiguous),
- *   dk[cand_j] += scale ds_j q,  dv[cand_j] += p_j dout  (float32 (B,H,Tk,D) contiguous, accumulated into:
- *   zero them first).
+ *   dk[cand_j] += scale ds_j q,  dv[cand_j] += p_j dout  (float32 (B,H,Tk,D) contiguous).
  * Slots as in the forward (-1 or >= Tk unused, duplicates counted).  q, o, dout: element strides (b, h, t)
  * with the last dimension contiguous; k, v rows 16-byte aligned.  D a multiple of 8 up to 256, B*H <= 65535.
- * dk and dv take float32 atomic adds, as the reference's kernel does: their summation order depends on
- * scheduling (reproducible to float32 rounding); dq is deterministic.
+ * dq is deterministic.  dk and dv:
+ *   ws non-NULL (ta_sparse_attn_bwd_workspace_size bytes): written (every key row, zeros where no slot names
+ *     it), each key's contributions added in a fixed order (queries ascending, slots ascending) -- bit for bit
+ *     reproducible.  causal: every candidate position is at most its query's position (T == Tk), which lets a
+ *     key skip the queries before it.
+ *   ws NULL: accumulated into with float32 atomic adds, as the reference's kernel does (zero them first); the
+ *     summation order then depends on scheduling (reproducible to float32 rounding).
  */
 int ta_sparse_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, int dtype,
                        int64_t qsb, int64_t qsh, int64_t qst, int64_t ksb, int64_t ksh, int64_t kst,
                        int64_t vsb, int64_t vsh, int64_t vst, int64_t osb, int64_t osh, int64_t ost,
                        int64_t dsb, int64_t dsh, int64_t dst, const int32_t* cand, const float* lse,
                        int B, int H, int T, int Tk, int KC, int D, float scale, void* dq, float* dk, float* dv,
-                       void* stream);
+                       float* ws, int causal, void* stream);
+
+/* Bytes of the deterministic route's workspace of ta_sparse_attn_bwd (per-slot ds and p, float32). */
+int64_t ta_sparse_attn_bwd_workspace_size(int B, int H, int T, int KC);
 
 /*
  * Attention over the keys a descent selected (replaces fastseg.py:367-383 candidate assembly +

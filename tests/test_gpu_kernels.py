@@ -155,13 +155,15 @@ def test_sparse_attn_matches_oracle(dtype, D):
     assert (out.cpu()[1, 1, 5] == 0).all()
 
 
+@pytest.mark.parametrize('det', [True, False])
 @pytest.mark.parametrize('dtype,D,KC', [(torch.float32, 64, 52), (torch.bfloat16, 64, 52), (torch.float16, 128, 70),
                                         (torch.float32, 16, 9), (torch.bfloat16, 128, 200)])
-def test_sparse_attn_bwd_matches_oracle(dtype, D, KC):
+def test_sparse_attn_bwd_matches_oracle(dtype, D, KC, det):
     """Backward of the candidate-list attention against the oracle's closed form (float32 from the same
-    inputs): dq, dk, dv within the dtype's bar; rows with nothing valid, duplicated and out-of-range slots."""
+    inputs): dq, dk, dv within the dtype's bar; rows with nothing valid, duplicated and out-of-range slots; dk
+    and dv by the fixed-order route (det) and by atomic adds."""
     from oracle.attn_ref import sparse_attn_bwd_ref
-    print('case', dtype, D, KC, flush=True)
+    print('case', dtype, D, KC, det, flush=True)
     B, H, T = 2, 3, 150
     q, k, v, do = [rnd(B, H, T, D, seed=s, dtype=dtype) for s in (30, 31, 32, 33)]
     g = torch.Generator().manual_seed(34)
@@ -172,7 +174,7 @@ def test_sparse_attn_bwd_matches_oracle(dtype, D, KC):
     scale = 1 / math.sqrt(D)
     qd, kd, vd, cd = q.to(DEV), k.to(DEV), v.to(DEV), cand.to(DEV)
     out, lse = K.sparse_attn_fwd(qd, kd, vd, cd, scale)
-    dq, dk, dv = K.sparse_attn_bwd(qd, kd, vd, cd, scale, out, lse, do.to(DEV))
+    dq, dk, dv = K.sparse_attn_bwd(qd, kd, vd, cd, scale, out, lse, do.to(DEV), deterministic=det)
     assert dq.dtype == dtype and dk.dtype == dtype and dv.dtype == dtype
     wq, wk, wv = sparse_attn_bwd_ref(q, k, v, cand, scale, do)
     tol = {torch.float32: 2e-4, torch.bfloat16: 6e-2, torch.float16: 1e-2}[dtype]
@@ -180,6 +182,31 @@ def test_sparse_attn_bwd_matches_oracle(dtype, D, KC):
         err = (got.cpu().float() - want).abs().max().item()
         assert err <= tol * max(1.0, want.abs().max().item()), err
     assert (dq.cpu()[1, 2, 7] == 0).all()
+
+
+@pytest.mark.parametrize('D,KC,T', [(64, 52, 300), (16, 9, 70), (128, 80, 200)])
+def test_sparse_attn_bwd_is_bit_reproducible(D, KC, T):
+    """The fixed-order route: dk and dv (and dq) are the same bits on every run, with and without the causal
+    shortcut (causal candidates: every slot at or before its query), and within float32 rounding of the
+    atomic route."""
+    print('case', D, KC, T, flush=True)
+    B, H = 2, 3
+    q, k, v, do = [rnd(B, H, T, D, seed=s).to(DEV) for s in (50, 51, 52, 53)]
+    g = torch.Generator().manual_seed(54)
+    tq = torch.arange(T).view(1, 1, T, 1)
+    cand = (torch.rand(B, H, T, KC, generator=g) * (tq + 1)).long()      # positions <= t
+    cand[..., 0] = torch.arange(T)
+    cand[..., 1] = 0                                                   # a key every query names
+    cand = torch.where(torch.rand(B, H, T, KC, generator=g) < 0.1, torch.full_like(cand, -1), cand).to(DEV)
+    scale = 1 / math.sqrt(D)
+    out, lse = K.sparse_attn_fwd(q, k, v, cand, scale)
+    runs = [K.sparse_attn_bwd(q, k, v, cand, scale, out, lse, do, causal=c) for c in (False, False, True)]
+    for r in runs[1:]:
+        for a, b in zip(runs[0], r):
+            assert torch.equal(a, b)
+    at = K.sparse_attn_bwd(q, k, v, cand, scale, out, lse, do, deterministic=False)
+    for a, b in zip(runs[0], at):
+        assert (a - b).abs().max().item() <= 1e-5 * max(1.0, b.abs().max().item())
 
 
 def test_fastseg_sparse_attn_is_differentiable():

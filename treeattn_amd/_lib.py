@@ -77,7 +77,8 @@ SIGNATURES = {
                                    c_i64, c_i64, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp,
                                    c_vp, _P(KvPages), c_vp]),
     'ta_sparse_attn_bwd': (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i32] + [c_i64] * 15 + [c_vp, c_vp] + [c_i32] * 6
-                           + [c_f32, c_vp, c_vp, c_vp, c_vp]),
+                           + [c_f32, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp]),
+    'ta_sparse_attn_bwd_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32]),
     'ta_seg_attn_workspace_size': (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     'ta_seg_attn_fwd': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                 c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32,

@@ -70,7 +70,7 @@ class TreeAttention(nn.Module):
             own = torch.arange(B, device=dev).view(1, B).expand(T, B)
             own = torch.where(own <= t.view(T, 1), own, torch.full_like(own, -1))
             cand = own.to(torch.int32).view(1, 1, T, B).expand(b, H, T, B).contiguous()
-            return sparse_attn(q, k, v, cand, scale)
+            return sparse_attn(q, k, v, cand, scale, causal=True)
 
         # (2) the forest of the blocks' keys (the sink left out of every index vector)
         depth = K.forest_depth(B)
@@ -106,7 +106,7 @@ class TreeAttention(nn.Module):
         else:
             cand = cand_full
         # (6) exact attention over own block + static keys + tree keys
-        out = sparse_attn(q, k, v, cand, scale)
+        out = sparse_attn(q, k, v, cand, scale, causal=True)
 
         tvalid = cand[..., B + 3:] >= 0
         tcount = tvalid.sum(-1).float()

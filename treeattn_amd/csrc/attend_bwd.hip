@@ -3,12 +3,16 @@
 // forward's log-sum-exp), Dq = do . o, dp_j = do . v_j and ds_j = p_j (dp_j - Dq):
 //   dq = scale * sum_j ds_j k_j,   dk[cand_j] += scale * ds_j q,   dv[cand_j] += p_j do.
 //
-// One wavefront per query.  Phase A, one lane per candidate slot (64 slots at a time): the two dot
-// products of its key and value rows with q and do (held in LDS and read by every lane at the same address),
-// p and ds, left in LDS.  Phase B, one lane per dimension: dq accumulates the chunk's slots in slot order (so
-// dq is deterministic), and each slot's dk and dv rows receive their contributions with float32 atomic adds
-// -- the reference's scheme: the order of the additions into a key's row depends on scheduling, so dk and dv
-// are reproducible to float32 rounding, not bit for bit.
+// sparse_attn_bwd_kernel, one wavefront per query.  Phase A, one lane per candidate slot (64 slots at a time):
+// the two dot products of its key and value rows with q and do (held in LDS and read by every lane at the same
+// address), p and ds, left in LDS.  Phase B, one lane per dimension: dq accumulates the chunk's slots in slot
+// order (so dq is deterministic).  dk and dv then take one of two routes:
+//  * with a workspace (the default of the Python binding): every slot's ds and p are written there, and
+//    sparse_attn_dkdv_kernel -- one workgroup per block of keys of a (sequence, head) -- scans the queries in
+//    increasing order and their slots in slot order, adding each hit on its keys into LDS accumulators, then
+//    writes the keys' rows once.  The order of the additions is fixed: dk and dv are bit-reproducible.
+//  * without one, each slot's dk and dv rows receive float32 atomic adds (the reference's scheme, whose order
+//    depends on scheduling: reproducible to float32 rounding only).
 #include "common.hpp"
 
 namespace ta {
@@ -19,9 +23,11 @@ struct BwdParams {
   const int32_t* cand;   // (B,H,T,KC) contiguous
   const float* lse;      // (B,H,T) contiguous
   void* dq;              // (B,H,T,D) contiguous, input dtype
-  float *dk, *dv;        // (B,H,Tk,D) contiguous float32, accumulated into
+  float *dk, *dv;        // (B,H,Tk,D) contiguous float32: accumulated into (atomics) or written (workspace)
+  float *ws_ds, *ws_p;   // (B,H,T,KC) per-slot ds and p (the deterministic route), or null
   int B, H, T, Tk, KC, D;
   float scale;
+  int causal;            // every candidate position <= its query's position: key blocks skip earlier queries
 };
 
 constexpr int kBwdMaxD = 256;
@@ -85,6 +91,11 @@ __global__ __launch_bounds__(kWave) void sparse_attn_bwd_kernel(BwdParams p) {
     s_ds[lane] = ds;
     s_pw[lane] = pw;
     s_row[lane] = ok ? j : -1;
+    if (p.ws_ds != nullptr && c < p.KC) {
+      const int64_t o = ((int64_t)bh * p.T + t) * p.KC + c;
+      p.ws_ds[o] = ds;
+      p.ws_p[o] = pw;
+    }
     wave_sync();
     // phase B: lane = dimension (and dimension + 64 m)
     const int nc = p.KC - c0 < kWave ? p.KC - c0 : kWave;
@@ -100,8 +111,10 @@ __global__ __launch_bounds__(kWave) void sparse_attn_bwd_kernel(BwdParams p) {
         const int d = lane + kWave * m;
         if (d < D) {
           dq[m] += dsc * to_f32(kr[d]);
-          atomicAdd(dkr + d, p.scale * dsc * s_q[d]);
-          atomicAdd(dvr + d, pwc * s_do[d]);
+          if (p.ws_ds == nullptr) {
+            atomicAdd(dkr + d, p.scale * dsc * s_q[d]);
+            atomicAdd(dvr + d, pwc * s_do[d]);
+          }
         }
       }
     }
@@ -115,6 +128,68 @@ __global__ __launch_bounds__(kWave) void sparse_attn_bwd_kernel(BwdParams p) {
   }
 }
 
+// dk and dv of the keys [j0, j0 + KB) of one (sequence, head), KB = 4096 / D: one wavefront scans the queries
+// in increasing order (from j0 when causal) and, per query, its candidate slots in slot order; every slot that
+// names one of the block's keys adds scale * ds * q to that key's dk and p * do to its dv (LDS accumulators,
+// lane = dimension).  Each key's rows are written once, after the scan.
+template <typename T>
+__global__ __launch_bounds__(kWave) void sparse_attn_dkdv_kernel(BwdParams p) {
+  __shared__ float s_dk[4096], s_dv[4096];
+  const int lane = lane_id();
+  const int D = p.D, KB = 4096 / D;
+  const int j0 = blockIdx.x * KB, bh = blockIdx.y;
+  const int b = bh / p.H, h = bh - b * p.H;
+  for (int e = lane; e < KB * D; e += kWave) {
+    s_dk[e] = 0.0f;
+    s_dv[e] = 0.0f;
+  }
+  wave_sync();
+  const T* qb = reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh;
+  const T* db = reinterpret_cast<const T*>(p.dout) + b * p.dsb + h * p.dsh;
+  for (int t = p.causal ? j0 : 0; t < p.T; ++t) {
+    const int32_t* cr = p.cand + ((int64_t)bh * p.T + t) * p.KC;
+    bool any = false;
+    float qv[kBwdMaxD / kWave], dov[kBwdMaxD / kWave];
+    for (int c0 = 0; c0 < p.KC; c0 += kWave) {
+      const int c = c0 + lane;
+      const int j = c < p.KC ? cr[c] : -1;
+      uint64_t hits = __ballot(j >= j0 && j < j0 + KB && j < p.Tk);
+      if (hits && !any) {   // the query's q and do rows, once
+        any = true;
+#pragma unroll
+        for (int m = 0; m < kBwdMaxD / kWave; ++m) {
+          const int d = lane + kWave * m;
+          qv[m] = d < D ? to_f32(qb[(int64_t)t * p.qst + d]) : 0.0f;
+          dov[m] = d < D ? to_f32(db[(int64_t)t * p.dst + d]) : 0.0f;
+        }
+      }
+      while (hits) {   // the hits in slot order
+        const int hl = __ffsll((unsigned long long)hits) - 1;
+        hits &= hits - 1;
+        const int key = __shfl(j, hl, kWave) - j0;
+        const int64_t o = ((int64_t)bh * p.T + t) * p.KC + c0 + hl;
+        const float dsv = p.ws_ds[o], pwv = p.ws_p[o];
+#pragma unroll
+        for (int m = 0; m < kBwdMaxD / kWave; ++m) {
+          const int d = lane + kWave * m;
+          if (d < D) {
+            s_dk[key * D + d] += p.scale * dsv * qv[m];
+            s_dv[key * D + d] += pwv * dov[m];
+          }
+        }
+      }
+    }
+  }
+  wave_sync();
+  for (int e = lane; e < KB * D; e += kWave) {
+    const int key = j0 + e / D;
+    if (key < p.Tk) {
+      p.dk[((int64_t)bh * p.Tk + key) * D + e % D] = s_dk[e];
+      p.dv[((int64_t)bh * p.Tk + key) * D + e % D] = s_dv[e];
+    }
+  }
+}
+
 }  // namespace ta
 
 using namespace ta;
@@ -124,7 +199,7 @@ extern "C" int ta_sparse_attn_bwd(const void* q, const void* k, const void* v, c
                                   int64_t kst, int64_t vsb, int64_t vsh, int64_t vst, int64_t osb, int64_t osh,
                                   int64_t ost, int64_t dsb, int64_t dsh, int64_t dst, const int32_t* cand,
                                   const float* lse, int B, int H, int T, int Tk, int KC, int D, float scale,
-                                  void* dq, float* dk, float* dv, void* stream) {
+                                  void* dq, float* dk, float* dv, float* ws, int causal, void* stream) {
   if (B < 0 || H < 0 || T < 0 || Tk <= 0 || KC < 0 || D <= 0 || D > kBwdMaxD || D % 8) {
     set_error("ta_sparse_attn_bwd: bad sizes (D a multiple of 8, at most 256)");
     return TA_ERR_ARG;
@@ -145,8 +220,10 @@ extern "C" int ta_sparse_attn_bwd(const void* q, const void* k, const void* v, c
     set_error("ta_sparse_attn_bwd: B * H above 65535");
     return TA_ERR_UNSUPPORTED;
   }
+  float* ws_ds = ws;
+  float* ws_p = ws != nullptr ? ws + (int64_t)B * H * T * KC : nullptr;
   BwdParams p{q, k, v, o, dout, qsb, qsh, qst, ksb, ksh, kst, vsb, vsh, vst, osb, osh, ost, dsb, dsh, dst,
-              cand, lse, dq, dk, dv, B, H, T, Tk, KC, D, scale};
+              cand, lse, dq, dk, dv, ws_ds, ws_p, B, H, T, Tk, KC, D, scale, causal};
   const dim3 grid((unsigned)T, (unsigned)(B * H));
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
@@ -154,5 +231,20 @@ extern "C" int ta_sparse_attn_bwd(const void* q, const void* k, const void* v, c
     case TA_F16: hipLaunchKernelGGL(sparse_attn_bwd_kernel<f16_t>, grid, dim3(kWave), 0, st, p); break;
     default: hipLaunchKernelGGL(sparse_attn_bwd_kernel<bf16_t>, grid, dim3(kWave), 0, st, p); break;
   }
-  return check_launch("sparse_attn_bwd_kernel");
+  int rc = check_launch("sparse_attn_bwd_kernel");
+  if (rc != TA_OK || ws == nullptr) return rc;
+  const int KB = 4096 / D;
+  const dim3 kgrid((unsigned)((Tk + KB - 1) / KB), (unsigned)(B * H));
+  switch (dtype) {
+    case TA_F32: hipLaunchKernelGGL(sparse_attn_dkdv_kernel<float>, kgrid, dim3(kWave), 0, st, p); break;
+    case TA_F16: hipLaunchKernelGGL(sparse_attn_dkdv_kernel<f16_t>, kgrid, dim3(kWave), 0, st, p); break;
+    default: hipLaunchKernelGGL(sparse_attn_dkdv_kernel<bf16_t>, kgrid, dim3(kWave), 0, st, p); break;
+  }
+  return check_launch("sparse_attn_dkdv_kernel");
+}
+
+// Workspace of the deterministic dk / dv route of ta_sparse_attn_bwd: per-slot ds and p, float32.
+extern "C" int64_t ta_sparse_attn_bwd_workspace_size(int B, int H, int T, int KC) {
+  if (B <= 0 || H <= 0 || T <= 0 || KC <= 0) return 0;
+  return 2 * (int64_t)B * H * T * KC * (int64_t)sizeof(float);
 }

@@ -74,24 +74,27 @@ class _SparseAttnFn(torch.autograd.Function):
     """fastseg.py:144-170: the forward saves (q, k, v, cand, out, lse); the backward returns (dq, dk, dv)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, cand, scale):
+    def forward(ctx, q, k, v, cand, scale, causal=False):
         out, lse = K.sparse_attn_fwd(q, k, v, cand, scale)
         ctx.save_for_backward(q, k, v, cand, out, lse)
         ctx.scale = scale
+        ctx.causal = causal
         return out
 
     @staticmethod
     def backward(ctx, do):
         q, k, v, cand, out, lse = ctx.saved_tensors
-        dq, dk, dv = K.sparse_attn_bwd(q, k, v, cand, ctx.scale, out, lse, do)
-        return dq, dk, dv, None, None
+        dq, dk, dv = K.sparse_attn_bwd(q, k, v, cand, ctx.scale, out, lse, do, causal=ctx.causal)
+        return dq, dk, dv, None, None, None
 
 
-def sparse_attn(q, k, v, cand, scale):
-    """cand: (b,H,T,K) int, -1 = unused slot (fastseg.py:173-177).  Differentiable in q, k, v."""
+def sparse_attn(q, k, v, cand, scale, causal=False):
+    """cand: (b,H,T,K) int, -1 = unused slot (fastseg.py:173-177).  Differentiable in q, k, v; the gradients
+    of k and v are summed in a fixed order (bit-reproducible).  causal (no counterpart in the reference): every
+    candidate position is at most its query's position, which lets the backward skip work."""
     _use_fast(q)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
-        return _SparseAttnFn.apply(q, k, v, cand, scale)
+        return _SparseAttnFn.apply(q, k, v, cand, scale, causal)
     return K.sparse_attn_fwd(q, k, v, cand, scale)[0]
 
 

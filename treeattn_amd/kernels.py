@@ -423,9 +423,11 @@ def sparse_attn_fwd(q, k, v, cand, scale):
     return out, lse
 
 
-def sparse_attn_bwd(q, k, v, cand, scale, out, lse, dout):
+def sparse_attn_bwd(q, k, v, cand, scale, out, lse, dout, deterministic=True, causal=False):
     """Gradients of sparse_attn_fwd: (dq in q's dtype, dk, dv in k's / v's dtype).  dk and dv are summed in
-    float32 with atomic adds (their order depends on scheduling, as in the reference's kernel)."""
+    float32: deterministic, in a fixed order (queries, then slots, ascending) through a per-slot workspace; else
+    with atomic adds whose order depends on scheduling, as in the reference's kernel.  causal: every candidate
+    position is at most its query's position (lets the deterministic route skip earlier queries)."""
     L.require_gpu(q, k, v, cand, out, lse, dout)
     if not (q.dtype == k.dtype == v.dtype == out.dtype):
         raise TypeError('q, k, v and out must share a dtype')
@@ -436,11 +438,17 @@ def sparse_attn_bwd(q, k, v, cand, scale, out, lse, dout):
     cc = cand.to(torch.int32).contiguous()
     ls = lse.float().contiguous()
     dq = torch.empty_like(q)
-    dk = torch.zeros(k.shape, device=q.device, dtype=torch.float32)
-    dv = torch.zeros(v.shape, device=q.device, dtype=torch.float32)
+    ws = None
+    if deterministic and T > 0 and KC > 0:
+        nbytes = L.lib().ta_sparse_attn_bwd_workspace_size(b, H, T, KC)
+        ws = torch.empty(max(1, nbytes // 4), device=q.device, dtype=torch.float32)
+    alloc = torch.empty if ws is not None else torch.zeros   # written whole, or accumulated into
+    dk = alloc(k.shape, device=q.device, dtype=torch.float32)
+    dv = alloc(v.shape, device=q.device, dtype=torch.float32)
     L.call('ta_sparse_attn_bwd', L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(out), L.ptr(dout), L.dtype_code(q),
            *L.rows3(q), *L.rows3(k), *L.rows3(v), *L.rows3(out), *L.rows3(dout), L.ptr(cc), L.ptr(ls), b, H, T, Tk,
-           KC, D, float(scale), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.stream())
+           KC, D, float(scale), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(ws), 1 if (causal and T == Tk) else 0,
+           L.stream())
     return dq, dk.to(k.dtype), dv.to(v.dtype)
 
 

@@ -210,7 +210,7 @@ def attend(q, k, v, lhat, cfg, scale=None):
     cm = torch.where(keep, cand, torch.full_like(cand, -1))
     if grad:
         from . import fastseg as FS
-        out = FS.sparse_attn(q, k, v, cm, scale)
+        out = FS.sparse_attn(q, k, v, cm, scale, causal=True)
     else:
         out, _ = K.sparse_attn_fwd(q, k, v, cm, scale)
     aux = dict(keys_total=keep.sum(-1).float().mean(), keys_tree=keep[..., :leaf * wl].sum(-1).float().mean(),
