@@ -168,7 +168,11 @@ def seg_sparse_attend(q, k, v, cfg, lhat=None, mode='faithful'):
     scale = 1.0 / math.sqrt(dh)
     if lhat is None:
         lhat = torch.full((b, H, T), cfg.beam, dtype=torch.long)
-    sel = select_seg(q.detach(), k.detach(), lhat, cfg, mode)
+    if getattr(cfg, 'attn', 'seg') == 'dyn':   # attention_dyn.py:65: the LaneTree selection
+        from .dyn_ref import select_keys
+        sel = select_keys(q.detach(), k.detach(), lhat, cfg, mode)
+    else:
+        sel = select_seg(q.detach(), k.detach(), lhat, cfg, mode)
     tq = torch.arange(T)
     cand, keep, used = assemble(sel, tq, cfg, b, H)
     out = sparse_attn_ref(q, k, v, torch.where(keep, cand, torch.full_like(cand, -1)), scale)

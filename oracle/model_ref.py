@@ -100,7 +100,7 @@ class Block(nn.Module):
     def __init__(self, cfg, mode):
         super().__init__()
         self.ln1 = LayerNorm(cfg.n_embd)
-        self.attn = SegAttentionRef(cfg, mode) if cfg.attn == 'seg' else TreeAttentionRef(cfg, mode)
+        self.attn = SegAttentionRef(cfg, mode) if cfg.attn in ('seg', 'dyn') else TreeAttentionRef(cfg, mode)
         self.ln2 = LayerNorm(cfg.n_embd)
         self.mlp = MLP(cfg)
 

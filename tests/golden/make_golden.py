@@ -25,6 +25,9 @@ closed form, brute force or invariant pins:
                         (1,2,256,16) keys, and TreeAttention.sparse_attend (attention.py:47-176) on seeded
                         (1,2,128,16) q, k, v: fixed budget, budget head + gate, train mode with the routing
                         loss; the parameter summary of a block-attention GPT under a seed.
+* dyn_lanetree.npz      dyntree.LaneTree (slots, node sums and counts after the build and after 16 insertions),
+                        dyntree.select_keys on seeded (2,2,64,16) q, k (neighbour borrowing on and off), and
+                        DynAttention.sparse_attend with attn='dyn' (fixed budget and budget head).
 * decode_small.npz      engine.Decoder on a 2-layer 64-wide model (vocab 64, Tcap 256) in reference-default
                         mode (neighbour borrowing on) and with the budget head (pred + global_pool): logits of
                         256 teacher-forced steps, plus GPT.forward logits over the same tokens.
@@ -231,6 +234,58 @@ def forest_fixtures(ta):
     np.savez_compressed(os.path.join(HERE, 'forest_block.npz'), **out)
 
 
+def dyn_fixtures(ta):
+    """dyntree.LaneTree (build, then 16 insertions) and dyntree.select_keys, and DynAttention.sparse_attend with
+    attn='dyn' (attention_dyn.py): the tree's slots, node sums and counts, the selection dict for the reference's
+    default neighbour settings and with the budget head's budgets, the module's output and aux."""
+    from treeattn.attention_dyn import DynAttention
+    from treeattn.config import Config
+    from treeattn.dyntree import LaneTree, select_keys
+    out = {}
+    kfull = seeded((4, 64, 8), 401)
+    n = torch.tensor([0, 8, 20, 33])
+    tree = LaneTree(kfull, n, iters=3)
+    for tag in ('built', 'inserted'):
+        if tag == 'inserted':
+            ar = torch.arange(4)
+            for i in range(16):
+                kpos = n + i
+                tree.insert(kfull[ar, kpos], kpos, kpos >= 1)
+        out[tag + '_slot'] = tree.slot.numpy().astype(np.int16)
+        for lvl in range(tree.D + 1):
+            out['%s_sums%d' % (tag, lvl)] = tree.sums[lvl].numpy().copy()   # the insertions update in place
+            out['%s_cnt%d' % (tag, lvl)] = tree.cnt[lvl].numpy().astype(np.int16)
+    out['kfull'] = kfull.numpy()
+    base = dict(vocab_size=64, seq_len=64, n_layer=2, n_head=2, n_embd=32, attn='dyn', chunk=16, wmax=4, beam=2,
+                beam_classes=(2, 3, 4), nb_window=4, nb_store=2, nb_probe=2, nb_cap_min=1)
+    q, k = seeded((2, 2, 64, 16), 411), seeded((2, 2, 64, 16), 412)
+    out.update(q=q.numpy(), k=k.numpy())
+    g = torch.Generator().manual_seed(413)
+    lhat = torch.randint(2, 5, (2, 2, 64), generator=g)
+    out['lhat'] = lhat.numpy().astype(np.int8)
+    for name, kw in (('default', dict()), ('nonb', dict(neighbors=False))):
+        sel = select_keys(q, k, lhat, Config(**base, **kw))
+        for key in ('tree_pos', 'nb_pos'):
+            out[name + '_' + key] = sel[key].numpy().astype(np.int16)
+        out[name + '_leaf_ok'] = sel['leaf_ok'].numpy()
+        out[name + '_n_tree'] = sel['n_tree'].numpy().astype(np.int8)
+        out[name + '_nb_leaves'] = sel['nb_leaves'].numpy().astype(np.int8)
+    v = seeded((2, 2, 64, 16), 414)
+    out['v'] = v.numpy()
+    for name, kw in (('fixed', dict(beam_mode='fixed')), ('pred', dict(beam_mode='pred', global_pool=True))):
+        torch.manual_seed(8)
+        m = DynAttention(Config(**base, **kw)).eval()
+        with torch.no_grad():
+            o = m.sparse_attend(q, k, v)
+        out['mod_' + name + '_out'] = o.numpy()
+        out['mod_' + name + '_aux_keys'] = np.array(sorted(m.aux))
+        out['mod_' + name + '_aux'] = np.array([float(m.aux[a]) for a in sorted(m.aux)])
+        for pn, p in m.state_dict().items():
+            if pn.startswith('pred.'):
+                out['mod_' + name + '_w_' + pn] = p.numpy()
+    np.savez_compressed(os.path.join(HERE, 'dyn_lanetree.npz'), **out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--reference', default='/root/reference')
@@ -239,7 +294,7 @@ def main():
     torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
     ta = load_reference(args.reference)
     jobs = dict(select=select_fixtures, attend=attend_fixtures, init=init_fixtures, config1=decode_config1,
-                small=decode_small, forest=forest_fixtures)
+                small=decode_small, forest=forest_fixtures, dyn=dyn_fixtures)
     for name, fn in jobs.items():
         if args.only and name not in args.only.split(','):
             continue
