@@ -530,6 +530,38 @@ int ta_forest_descend(const void* q, int dtype, int64_t qsb, int64_t qsh, int64_
 /* Leaves per query (wl), candidate-list width (Kc = block + 3 + 2 wl) and widest level of ta_forest_descend. */
 int ta_forest_shape(int T, int block, int wmax, int* wl, int* kc, int* widest);
 
+/*
+ * LaneTree (the reference's attn='dyn' selection), workspace -- bytes of the lane trees of ta_lanetree_build /
+ * ta_lanetree_walk: B * H * (T / chunk) trees of capacity T, each T * (4 D + 8) bytes (node sums float32, counts
+ * and leaf slots int32).  T a power of two in [4, 4096], chunk dividing T, D 16, 32 or 64.
+ */
+int ta_lanetree_workspace_size(int B, int H, int T, int D, int chunk, int64_t* bytes);
+
+/*
+ * LaneTree, step 1 -- replaces dyntree.py:34-82 LaneTree.__init__ with dyntree.py:6-31 masked_two_means_order,
+ * for every lane of dyntree.py:161-166: lane l of every (b, h) gets a tree of capacity T over the keys
+ * [1, l * chunk) of k (B, H, T, D): log2(T) - 1 rounds of masked 2-means splits (kmeans_iters iterations each),
+ * every group's real keys laid out half and half, then the node sums and counts.  ws: the workspace above.
+ */
+int ta_lanetree_build(const void* k, int dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int T, int D,
+                      int chunk, int kmeans_iters, void* ws, int64_t ws_bytes, void* stream);
+
+/*
+ * LaneTree, step 2 -- replaces dyntree.py:148-243 select_keys (with dyntree.py:84-131 insert / search /
+ * leaf_keys) on the trees of ta_lanetree_build, which it updates.  Every lane walks its positions t in order:
+ * the neighbour test over the leaves the lane's last nb_window positions stored (nb_store each; score >=
+ * base - nb_rho |base|, the cap from the match rate of the first nb_probe positions), the leaf budget from
+ * lhat (B, H, T) int32, the beam search (node score q . mean key, wmax wide), then the insertion of key t.
+ * Writes tree_pos (B, H, T, 2 wl) int32 [all first keys | all second keys] of the found leaves (wl =
+ * min(wmax, T / 2)), leaf_ok (B, H, T, wl), nb_pos (B, H, T, 2 nb_window nb_store) int32, n_tree and nb_leaves
+ * (B, H, T) int32, -1 / 0 where unused.  1 <= wmax <= 32, nb_window * nb_store <= 64, nb_store <= wl.
+ */
+int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t qsb, int64_t qsh, int64_t qst, int64_t ksb,
+                     int64_t ksh, int64_t kst, int B, int H, int T, int D, int chunk, const int32_t* lhat, int wmax,
+                     int nb_window, int nb_store, float nb_rho, int nb_probe, int nb_cap_min, int neighbors,
+                     void* ws, int64_t ws_bytes, int32_t* tree_pos, uint8_t* leaf_ok, int32_t* nb_pos,
+                     int32_t* n_tree, int32_t* nb_leaves, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

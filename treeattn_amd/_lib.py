@@ -110,6 +110,12 @@ SIGNATURES = {
                                   _P(c_i64), _P(c_i64), c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32,
                                   c_vp]),
     'ta_forest_shape': (c_i32, [c_i32, c_i32, c_i32, _P(c_i32), _P(c_i32), _P(c_i32)]),
+    'ta_lanetree_workspace_size': (c_i32, [c_i32, c_i32, c_i32, c_i32, c_i32, _P(c_i64)]),
+    'ta_lanetree_build': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp,
+                                  c_i64, c_vp]),
+    'ta_lanetree_walk': (c_i32, [c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32,
+                                 c_i32, c_i32, c_vp, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32, c_i32, c_vp, c_i64,
+                                 c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'ta_level_log_sums': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                   _P(c_vp), _P(c_i64), _P(c_i64), _P(c_i32), c_vp, c_i64, c_vp]),
     'ta_gate_levels': (c_i32, [c_i32, c_i32, c_i32, c_i32, _P(c_vp), _P(c_vp), _P(c_vp), _P(c_i64), _P(c_i64),

@@ -33,6 +33,7 @@ SOURCES = {
     'neighbor.hip': [],
     'gate.hip': [],
     'forest.hip': [],
+    'lanetree.hip': [],
 }
 
 COMMON = ['--offload-arch=gfx950', '-O3', '-fPIC', '-std=c++17', '-Wall', '-Wno-unused-function',

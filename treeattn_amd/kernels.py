@@ -785,3 +785,57 @@ def mfma_peak(wgs=None, iters=20000, reps=5):
             best = ms if best is None else min(best, ms)
     flops = wgs * 4 * 4 * iters * 32768.0
     return flops / (best * 1e-3) / 1e12
+
+
+def lanetree_workspace(B, H, T, D, chunk, device):
+    """Workspace of ta_lanetree_build / ta_lanetree_walk (the lane trees), uint8."""
+    n = ctypes.c_int64()
+    L.call('ta_lanetree_workspace_size', int(B), int(H), int(T), int(D), int(chunk), ctypes.byref(n))
+    return torch.empty(n.value, device=device, dtype=torch.uint8)
+
+
+def lanetree_build(k, chunk, kmeans_iters, ws=None):
+    """The lane trees of dyntree.py:161-166 (LaneTree.__init__ of every lane, dyntree.py:34-82) from keys k
+    (B, H, T, D).  Returns the workspace holding them: per tree (index (b * H + h) * (T / chunk) + lane) the
+    node sums (T, D) float32 (node (l, i) at row 2^l - 1 + i), then all counts (T,) int32, then all leaf slots
+    (T,) int32."""
+    L.require_gpu(k)
+    B, H, T, D = k.shape
+    if ws is None:
+        ws = lanetree_workspace(B, H, T, D, chunk, k.device)
+    L.call('ta_lanetree_build', L.ptr(k), L.dtype_code(k), *L.rows3(k), B, H, T, D, int(chunk), int(kmeans_iters),
+           L.ptr(ws), ws.numel(), L.stream())
+    return ws
+
+
+def lanetree_views(ws, B, H, T, D, chunk):
+    """(sums (P, T, D) float32, counts (P, T) int32, slots (P, T / 2, 2) int32) views of a lane-tree workspace."""
+    P = B * H * (T // chunk)
+    f = ws[:P * T * D * 4].view(torch.float32).view(P, T, D)
+    ints = ws[P * T * D * 4:P * T * (D * 4 + 8)].view(torch.int32)
+    return f, ints[:P * T].view(P, T), ints[P * T:].view(P, T // 2, 2)
+
+
+def lanetree_walk(q, k, lhat, ws, cfg):
+    """The walk of dyntree.py:148-243 over lane trees built by lanetree_build (updated in place).  Returns
+    (tree_pos (B,H,T,2wl) int32, leaf_ok (B,H,T,wl) bool, nb_pos (B,H,T,2 Wn NS) int32, n_tree, nb_leaves
+    (B,H,T) int32)."""
+    L.require_gpu(q, k, lhat, ws)
+    if q.dtype != k.dtype:
+        raise TypeError('q and k must share a dtype')
+    B, H, T, D = q.shape
+    nlev = _ilog2(T) - 1
+    wl = min(cfg.wmax, 1 << nlev)
+    Wn, NS = cfg.nb_window, cfg.nb_store
+    dev = q.device
+    tree_pos = torch.empty(B, H, T, 2 * wl, device=dev, dtype=torch.int32)
+    leaf_ok = torch.empty(B, H, T, wl, device=dev, dtype=torch.bool)
+    nb_pos = torch.empty(B, H, T, 2 * Wn * NS, device=dev, dtype=torch.int32)
+    n_tree = torch.empty(B, H, T, device=dev, dtype=torch.int32)
+    nb_leaves = torch.empty(B, H, T, device=dev, dtype=torch.int32)
+    lh = lhat.to(device=dev, dtype=torch.int32).contiguous()
+    L.call('ta_lanetree_walk', L.ptr(q), L.ptr(k), L.dtype_code(q), *L.rows3(q), *L.rows3(k), B, H, T, D,
+           int(cfg.chunk), L.ptr(lh), int(cfg.wmax), int(Wn), int(NS), float(cfg.nb_rho), int(cfg.nb_probe),
+           int(cfg.nb_cap_min), 1 if cfg.neighbors else 0, L.ptr(ws), ws.numel(), L.ptr(tree_pos), L.ptr(leaf_ok),
+           L.ptr(nb_pos), L.ptr(n_tree), L.ptr(nb_leaves), L.stream())
+    return tree_pos, leaf_ok, nb_pos, n_tree, nb_leaves

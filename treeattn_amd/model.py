@@ -1,7 +1,8 @@
 """GPT-2 style language model around the segment-tree attention (model.py:12-93 of the reference).
 
-Host PyTorch (embeddings, LayerNorm, linears, GELU); attention is SegAttention, DynAttention('seg') or the
-block forest's TreeAttention, whose selection and attention run in the HIP kernels.  Same module names, parameter names, initialisation and
+Host PyTorch (embeddings, LayerNorm, linears, GELU); attention is SegAttention (attn='seg'), DynAttention with
+the LaneTree (attn='dyn') or the block forest's TreeAttention, whose selection and attention run in the HIP
+kernels.  Same module names, parameter names, initialisation and
 forward signature as the reference, so its checkpoints and tests carry over.
 """
 import math
@@ -36,7 +37,7 @@ class MLP(nn.Module):
 
 
 def make_attention(cfg):
-    """model.py:37: 'seg' the segment tree, 'dyn' the dynamic-tree module, anything else the block forest."""
+    """model.py:37: 'seg' the segment tree, 'dyn' the LaneTree module, anything else the block forest."""
     if cfg.attn == 'seg':
         return SegAttention(cfg)
     if cfg.attn == 'dyn':

@@ -187,16 +187,22 @@ def attend(q, k, v, lhat, cfg, scale=None):
     candidate list of the reference is built and attended by the candidate-list kernel."""
     b, H, T, dh = q.shape
     scale = 1.0 / math.sqrt(dh) if scale is None else scale
-    shape = cfg_shape(cfg, T)
-    leaf = shape.leaf
-    sel, ids32, vld8, sct, levels = select(q.detach(), k.detach(), lhat, cfg, shape)
-    wl = ids32.shape[-1]
-    NBK = sel['nb_pos'].shape[-1]
     tq = torch.arange(T, device=q.device)
+    if getattr(cfg, 'attn', 'seg') == 'dyn':   # the LaneTree selection (attention_dyn.py:74-75)
+        from .dyntree import select_keys
+        leaf = 2
+        sel = select_keys(q.detach(), k.detach(), lhat, cfg)
+        wl = sel['leaf_ok'].shape[-1]
+    else:
+        shape = cfg_shape(cfg, T)
+        leaf = shape.leaf
+        sel, ids32, vld8, sct, levels = select(q.detach(), k.detach(), lhat, cfg, shape)
+        wl = ids32.shape[-1]
+    NBK = sel['nb_pos'].shape[-1]
     # gradients wanted (training): the candidate-list kernels, whose backward is built (the structural kernel
     # attends the same key set, forward only)
     grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
-    if not cfg.neighbors and not grad:
+    if not cfg.neighbors and not grad and getattr(cfg, 'attn', 'seg') != 'dyn':
         n_tree = sel['n_tree'].to(torch.int32)
         keys = torch.empty(b, H, T, device=q.device)
         out, _, keys = K.seg_attn(q, k, v, tq, ids32, vld8, n_tree, leaf, cfg.local, scale, keys=keys)
