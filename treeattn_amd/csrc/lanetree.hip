@@ -61,46 +61,126 @@ __device__ __forceinline__ int seg_argmax_idx(float v, int i, int L) {
   return i;
 }
 
-// The group member (index inside the group) with the largest squared distance to ref among the real keys,
-// the first on ties; -1 stands for empty slots (masked_fill(~valid, -1)).
-template <typename T, int D>
-__device__ __forceinline__ int lt_farthest(const T* kb, int64_t kst, const int32_t* s_perm, const uint8_t* s_val,
-                                           int wb, int gb, int lane, int M, int L, bool live,
-                                           const float (&ref)[D], float (&x)[D]) {
-  float bv = -1.0f;
-  int bi = 0;
-  for (int t = 0; t < M; ++t) {
-    const int s = wb + lane + kWave * t;
-    float d2 = -1.0f;
-    if (live) {
-      load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
-      const float dd = lane_dot<D>([&](int i) { return x[i] - ref[i]; }, [&](int i) { return x[i] - ref[i]; });
-      d2 = s_val[s] ? dd : -1.0f;
-    }
-    if (t == 0 || d2 > bv) {
-      bv = d2;
-      bi = s - gb;
+// Integer min / max over an aligned L-lane segment.
+__device__ __forceinline__ int seg_imax(int v, int L) {
+  for (int h = L >> 1; h >= 1; h >>= 1) v = max(v, __shfl_xor(v, h, kWave));
+  return v;
+}
+__device__ __forceinline__ int seg_imin(int v, int L) {
+  for (int h = L >> 1; h >= 1; h >>= 1) v = min(v, __shfl_xor(v, h, kWave));
+  return v;
+}
+
+// Sort key of a projection: ascending float order (-0 taken as +0, as the comparison does) above the member
+// index, so that sorting the 64-bit words is the stable sort of the projections.
+__device__ __forceinline__ uint64_t lt_sort_key(float p, int idx) {
+  const uint32_t u = __float_as_uint(p + 0.0f);
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint32_t)idx;
+}
+
+// Ascending bitonic sort of s[0, n2) (n2 a power of two) by one wavefront.
+__device__ __forceinline__ void wave_bitonic_sort(uint64_t* s, int n2, int lane) {
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = lane; i < (n2 >> 1); i += kWave) {
+        const int a = ((i & ~(j - 1)) << 1) | (i & (j - 1)), b = a + j;
+        const uint64_t x = s[a], y = s[b];
+        if ((x > y) == ((a & k) == 0)) {
+          s[a] = y;
+          s[b] = x;
+        }
+      }
+      wave_sync();
     }
   }
-  return seg_argmax_idx(bv, bi, L);
+}
+
+constexpr int kLtGroups = 16;   // groups side by side in a 64-slot window (the smallest group has 4 slots)
+
+// The outputs of lt_group_reduce for groups of L lanes: every (group, dimension) this lane owns (D / L of them,
+// at most one when L = 64), the halving tree over the group's L partials (LDS rows of stride D + 4), divided by
+// max(count, 1).  All reads are issued before the first store.
+template <int D, int L>
+__device__ __forceinline__ void lt_group_outputs(const float* red, const float* cnt, bool always, float* dst,
+                                                 int lane) {
+  constexpr int RS = D + 4, nout = (kWave / L) * D, NU = nout >= kWave ? nout / kWave : 1;
+  float p[NU][L], c[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int o = lane + kWave * u, g = o / D, d = o - g * D;
+    const bool in = o < nout;
+    const float* col = red + g * L * RS + d;
+#pragma unroll
+    for (int j = 0; j < L; ++j) p[u][j] = in ? col[j * RS] : 0.0f;
+    c[u] = in ? cnt[g] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+#pragma unroll
+    for (int n = L / 2; n >= 1; n >>= 1)
+#pragma unroll
+      for (int i = 0; i < n; ++i) p[u][i] = p[u][i] + p[u][i + n];
+    p[u][0] = p[u][0] / fmaxf(c[u], 1.0f);
+  }
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int o = lane + kWave * u, g = o / D, d = o - g * D;
+    if (o < nout && (always || c[u] > 0.0f)) dst[g * RS + d] = p[u][0];
+  }
+}
+
+// Canonical sums of the groups of L consecutive lanes (64 / L groups, L in {4, ..., 64}), in two steps:
+// lt_group_row puts this lane's partial (v, or zero when !take) into its LDS row; lt_group_reduce then reduces
+// every (group, dimension) by the halving tree over the group's L partials in one lane, divides by
+// max(count, 1) and writes dst (row stride D + 4) when the count is positive or `always`.
+template <int D>
+__device__ __forceinline__ void lt_group_row(const float (&v)[D], bool take, float* red, int lane) {
+  float* row = red + lane * (D + 4);
+#pragma unroll
+  for (int d = 0; d < D; d += 4)
+    *reinterpret_cast<float4*>(row + d) = take ? make_float4(v[d], v[d + 1], v[d + 2], v[d + 3])
+                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+template <int D>
+__device__ __forceinline__ void lt_group_reduce(const float* red, int L, const float* cnt, bool always, float* dst,
+                                                int lane) {
+  wave_sync();
+  switch (L) {
+    case 4: lt_group_outputs<D, 4>(red, cnt, always, dst, lane); break;
+    case 8: lt_group_outputs<D, 8>(red, cnt, always, dst, lane); break;
+    case 16: lt_group_outputs<D, 16>(red, cnt, always, dst, lane); break;
+    case 32: lt_group_outputs<D, 32>(red, cnt, always, dst, lane); break;
+    default: lt_group_outputs<D, 64>(red, cnt, always, dst, lane); break;
+  }
+  wave_sync();
 }
 
 // ---------------------------------------------------------------------------------------------------- build
 // One wavefront per lane tree (dyntree.py:34-82).  Every level splits each group of S = C >> lvl slots by a
 // masked 2-means projection; the group's real keys are then laid out half and half (the larger half first),
-// empty slots after each half's keys.  Groups of S >= 64 slots are done one at a time, lane j holding members
-// j, j + 64, ...; smaller groups side by side, one member per lane.  The permutation, validity and projections
-// live in LDS; key rows are read from k on every pass.
+// empty slots after each half's keys, every empty slot holding the position of the group's last empty slot
+// (the one the stable sort ranks last).  Empty slots add key * 0 to the masked sums; they are skipped, which
+// changes at most the sign of a zero.  A window of max(S, 64) slots is done at a time: lane j holds member j
+// (and j + 64, j + 128, ... when S > 64: partial j of the canonical sums); groups of S < 64 slots sit side by
+// side, L = min(S, 64) lanes each.  Means and centroids live in LDS.  The order: for S >= 64 a bitonic sort of
+// (projection, index) over the span of the real keys, for smaller groups ranks by counting.
+// LDS: permutation (4 C bytes), sort words / projections / reduction rows (max(8 C, 64 (D + 4) 4)),
+// centroids (2 x 16 x (D + 4) floats), counts (2 x 16 floats), validity (C).
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void lanetree_build_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
                                                                int64_t kst, int H, int C, int nlane, int chunk,
                                                                int iters, float* __restrict__ ws, int64_t P) {
+  constexpr int RS = D + 4;
   extern __shared__ __align__(16) unsigned char s_raw[];
   int32_t* s_perm = reinterpret_cast<int32_t*>(s_raw);
-  float* s_proj = reinterpret_cast<float*>(s_perm + C);
-  int32_t* s_np = reinterpret_cast<int32_t*>(s_proj + C);
-  uint8_t* s_val = reinterpret_cast<uint8_t*>(s_np + C);
-  uint8_t* s_nv = s_val + C;
+  uint64_t* s_sort = reinterpret_cast<uint64_t*>(s_perm + C);
+  float* s_key = reinterpret_cast<float*>(s_sort);
+  float* s_red = reinterpret_cast<float*>(s_sort);
+  const int scratch = 8 * C > kWave * RS * 4 ? 8 * C : kWave * RS * 4;
+  float* s_cen = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(s_sort) + scratch);   // [2][16][RS]
+  float* s_cnt = s_cen + 2 * kLtGroups * RS;                                                       // [2][16]
+  uint8_t* s_val = reinterpret_cast<uint8_t*>(s_cnt + 2 * kLtGroups);
   const int lane = lane_id();
   const int64_t pt = blockIdx.x;
   const int ln = (int)(pt % nlane);
@@ -108,142 +188,196 @@ __global__ __launch_bounds__(kWave) void lanetree_build_kernel(const T* __restri
   const T* kb = k + (bh / H) * ksb + (bh % H) * ksh;
   const int n0 = ln * chunk;
   const LaneTree tr = lane_tree(ws, P, C, D, pt);
+  const float kInf = __int_as_float(0x7f800000);
   for (int c = lane; c < C; c += kWave) {
     s_perm[c] = c;
     s_val[c] = (c >= 1 && c < n0) ? 1 : 0;
   }
   wave_sync();
   const int nlev = lt_log2(C) - 1;
-  float x[D], c0[D], c1[D], acc[D];
+  float x[D], acc0[D], acc1[D];
   for (int lvl = 0; lvl < nlev; ++lvl) {
-    const int S = C >> lvl;
-    const int L = S < kWave ? S : kWave;       // partial sums per group
-    const int M = S < kWave ? 1 : S / kWave;   // members per lane
-    const int Wz = S < kWave ? kWave : S;      // slots per window
+    const int S = C >> lvl, half = S >> 1;
+    const int L = S < kWave ? S : kWave, M = S < kWave ? 1 : S / kWave, Wz = S < kWave ? kWave : S;
     const int nwin = C > Wz ? C / Wz : 1;
+    const int g = lane / L, gl = lane & (L - 1);
+    float* c0 = s_cen + g * RS;
+    float* c1 = s_cen + (kLtGroups + g) * RS;
     for (int win = 0; win < nwin; ++win) {
-      const int wb = win * Wz;
-      const int gb = S < kWave ? wb + (lane & ~(S - 1)) : wb;   // this lane's group
-      const bool live = wb + lane < C;                          // C < 64: lanes past the tree sit out
-      // (1) valid count and masked mean
-      float cntp = 0.0f;
-      for (int t = 0; t < M; ++t) {
-        const int s = wb + lane + kWave * t;
-        const float v = live && s_val[s] ? 1.0f : 0.0f;
-        if (live) load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
+      const int gb = win * Wz + g * S;
+      const bool live = win * Wz + lane < C;   // C < 64: lanes past the tree sit out
+      // (1) counts and the masked mean
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-          const float xv = live ? x[d] * v : 0.0f;
-          acc[d] = t == 0 ? xv : acc[d] + xv;
+      for (int d = 0; d < D; ++d) acc0[d] = 0.0f;
+      float cntp = 0.0f;
+      int vlo = S, vhi = -1, lastinv = -1;
+      const bool resident = M == 1;   // one member per lane: its row stays in x for every pass of the window
+      for (int t = 0; t < M; ++t) {
+        const int i = gl + L * t, s = gb + i;
+        if (!live) continue;
+        if (s_val[s]) {
+          load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
+          if (!resident) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) acc0[d] = acc0[d] + x[d];
+          }
+          cntp = cntp + 1.0f;
+          vlo = min(vlo, i);
+          vhi = max(vhi, i);
+        } else {
+          lastinv = i;
         }
-        cntp = t == 0 ? v : cntp + v;
       }
       const float cnt = seg_sum(cntp, L);
       const int ng = (int)cnt;
-      const float den = fmaxf(cnt, 1.0f);
-#pragma unroll
-      for (int d = 0; d < D; ++d) c0[d] = seg_sum(acc[d], L) / den;   // c0 = the mean for now
-      const bool work = __ballot(live && ng > 0) != 0;           // no real key in the window: identity order
+      vlo = seg_imin(vlo, L);
+      vhi = seg_imax(vhi, L);
+      lastinv = seg_imax(lastinv, L);
+      const bool work = __ballot(cntp > 0.0f) != 0;
       if (work) {
-        // (2) a = the member farthest from the mean, b = the member farthest from a
-        const int ia = lt_farthest<T, D>(kb, kst, s_perm, s_val, wb, gb, lane, M, L, live, c0, x);
-        if (live) load_row_g<T, D>(kb + (int64_t)s_perm[gb + ia] * kst, c0);
-        const int ib = lt_farthest<T, D>(kb, kst, s_perm, s_val, wb, gb, lane, M, L, live, c0, x);
-        if (live) load_row_g<T, D>(kb + (int64_t)s_perm[gb + ib] * kst, c1);
-        // (3) Lloyd iterations over the two centroids
-        for (int it = 0; it < iters; ++it) {
-          const float cc0 = lane_dot<D>([&](int i) { return c0[i]; }, [&](int i) { return c0[i]; });
-          const float cc1 = lane_dot<D>([&](int i) { return c1[i]; }, [&](int i) { return c1[i]; });
-          uint64_t lab = 0;   // bit t: member t of this lane is nearer c1
+        if (gl == 0) s_cnt[g] = cnt;
+        if (resident) lt_group_row<D>(x, cntp > 0.0f, s_red, lane);
+        else lt_group_row<D>(acc0, true, s_red, lane);
+        lt_group_reduce<D>(s_red, L, s_cnt, true, c0 - g * RS, lane);   // the means, into c0
+        // a = the real key farthest from the mean, then b = the real key farthest from a
+        for (int pass = 0; pass < 2; ++pass) {
+          float bv = -1.0f;
+          int bi = 0;
           for (int t = 0; t < M; ++t) {
-            const int s = wb + lane + kWave * t;
-            if (!live) continue;
-            load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
-            const float xx = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return x[i]; });
-            const float xc0 = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return c0[i]; });
-            const float xc1 = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return c1[i]; });
-            const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
-            if (dist1 < dist0) lab |= 1ull << t;
+            const int i = gl + L * t, s = gb + i;
+            if (!live || !s_val[s]) continue;
+            if (!resident) load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
+            const float d2 = lane_dot<D>([&](int e) { return x[e] - c0[e]; }, [&](int e) { return x[e] - c0[e]; });
+            if (d2 > bv) {
+              bv = d2;
+              bi = i;
+            }
           }
-          for (int j = 0; j < 2; ++j) {
-            float cp = 0.0f;
-            for (int t = 0; t < M; ++t) {
-              const int s = wb + lane + kWave * t;
-              const bool in = live && s_val[s] && (((lab >> t) & 1ull) == (uint64_t)j);
-              const float m = in ? 1.0f : 0.0f;
-              if (live) load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
+          const int sel = seg_argmax_idx(bv, bi, L);
+          if (live) load_row_g<T, D>(kb + (int64_t)s_perm[gb + sel] * kst, acc1);
+          wave_sync();
+          float* dst = pass == 0 ? c0 : c1;
+          if (live) {
 #pragma unroll
-              for (int d = 0; d < D; ++d) {
-                const float xv = live ? x[d] * m : 0.0f;
-                acc[d] = t == 0 ? xv : acc[d] + xv;
+            for (int d = 0; d < D; d += 4)
+              *reinterpret_cast<float4*>(dst + d) = make_float4(acc1[d], acc1[d + 1], acc1[d + 2], acc1[d + 3]);
+          }
+          wave_sync();
+        }
+        // Lloyd iterations: labels from the current centroids, then both masked sums, in one pass
+        for (int it = 0; it < iters; ++it) {
+          const float cc0 = lane_dot<D>([&](int e) { return c0[e]; }, [&](int e) { return c0[e]; });
+          const float cc1 = lane_dot<D>([&](int e) { return c1[e]; }, [&](int e) { return c1[e]; });
+#pragma unroll
+          for (int d = 0; d < D; ++d) {
+            acc0[d] = 0.0f;
+            acc1[d] = 0.0f;
+          }
+          float cp0 = 0.0f, cp1 = 0.0f;
+          for (int t = 0; t < M; ++t) {
+            const int s = gb + gl + L * t;
+            if (!live || !s_val[s]) continue;
+            if (!resident) load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
+            const float xx = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return x[e]; });
+            const float xc0 = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return c0[e]; });
+            const float xc1 = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return c1[e]; });
+            const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
+            if (dist1 < dist0) {
+              if (!resident) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) acc1[d] = acc1[d] + x[d];
               }
-              cp = t == 0 ? m : cp + m;
-            }
-            const float cj = seg_sum(cp, L);
-            const float dj = fmaxf(cj, 1.0f);
+              cp1 = cp1 + 1.0f;
+            } else {
+              if (!resident) {
 #pragma unroll
-            for (int d = 0; d < D; ++d) {
-              const float nc = seg_sum(acc[d], L) / dj;
-              if (j == 0) c0[d] = cj > 0.0f ? nc : c0[d];
-              else c1[d] = cj > 0.0f ? nc : c1[d];
+                for (int d = 0; d < D; ++d) acc0[d] = acc0[d] + x[d];
+              }
+              cp0 = cp0 + 1.0f;
             }
+          }
+          const float cj0 = seg_sum(cp0, L), cj1 = seg_sum(cp1, L);
+          if (gl == 0) {
+            s_cnt[g] = cj0;
+            s_cnt[kLtGroups + g] = cj1;
+          }
+          if (resident) lt_group_row<D>(x, cp0 > 0.0f, s_red, lane);
+          else lt_group_row<D>(acc0, true, s_red, lane);
+          lt_group_reduce<D>(s_red, L, s_cnt, false, c0 - g * RS, lane);
+          if (resident) lt_group_row<D>(x, cp1 > 0.0f, s_red, lane);
+          else lt_group_row<D>(acc1, true, s_red, lane);
+          lt_group_reduce<D>(s_red, L, s_cnt + kLtGroups, false, c1 - g * RS, lane);
+        }
+      }
+      const int nl = (ng + 1) / 2, nr = ng - nl;
+      if (S >= kWave) {
+        // one group: projections on c0 - c1 over the span of the real keys (empty slots inside it: +inf),
+        // padded to a power of two with entries that sort last; bitonic sort
+        if (ng > 0) {
+          const int n = vhi - vlo + 1;
+          int n2 = 1;
+          while (n2 < n) n2 <<= 1;
+          for (int t = 0; t < M; ++t) {
+            const int i = lane + kWave * t, s = gb + i;
+            if (i < vlo || i > vhi) continue;
+            float pr = kInf;
+            if (s_val[s]) {
+              if (!resident) load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
+              pr = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return c0[e] - c1[e]; });
+            }
+            s_sort[i - vlo] = lt_sort_key(pr, i - vlo);
+          }
+          for (int r = n + lane; r < n2; r += kWave) s_sort[r] = lt_sort_key(kInf, r);
+          wave_sync();
+          wave_bitonic_sort(s_sort, n2, lane);
+        }
+        // layout: sorted ranks [0, nl) to the left half, [nl, ng) to the right half (phase A rewrites each
+        // sort word as (position, key position) before phase B moves the permutation)
+        for (int r = lane; r < ng; r += kWave) {
+          const int m = vlo + (int)(uint32_t)s_sort[r];
+          const int pos = r < nl ? r : half + r - nl;
+          s_sort[r] = ((uint64_t)(uint32_t)pos << 32) | (uint32_t)s_perm[gb + m];
+        }
+        const int fillp = lastinv >= 0 ? s_perm[gb + lastinv] : 0;
+        wave_sync();
+        for (int r = lane; r < ng; r += kWave) {
+          const uint64_t e = s_sort[r];
+          s_perm[gb + (int)(e >> 32)] = (int32_t)(uint32_t)e;
+        }
+        for (int p = lane; p < S; p += kWave) {
+          const bool filled = p < half ? p < nl : (p - half) < nr;
+          if (!filled) s_perm[gb + p] = fillp;
+          s_val[gb + p] = filled ? 1 : 0;
+        }
+        wave_sync();
+      } else {
+        // groups of S < 64 side by side, one member per lane: ranks by counting
+        const int s = gb + gl;
+        const bool v = live && s_val[s];
+        float key = kInf;
+        if (v) {
+          key = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return c0[e] - c1[e]; });
+        }
+        if (live) s_key[s] = key;
+        wave_sync();
+        int rank = 0;
+        if (v) {
+          for (int j = 0; j < S; ++j) {
+            const float kj = s_key[gb + j];
+            rank += (kj < key || (kj == key && j < gl)) ? 1 : 0;
           }
         }
-        // (4) projections on c0 - c1, empty slots last
-        for (int t = 0; t < M; ++t) {
-          const int s = wb + lane + kWave * t;
-          if (!live) continue;
-          load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
-          const float pr = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return c0[i] - c1[i]; });
-          s_proj[s] = s_val[s] ? pr : __int_as_float(0x7f800000);
+        const int pm = live ? s_perm[s] : 0;
+        const int fillp = live && lastinv >= 0 ? s_perm[gb + lastinv] : 0;
+        wave_sync();
+        if (v) s_perm[gb + (rank < nl ? rank : half + rank - nl)] = pm;
+        if (live) {
+          const bool filled = gl < half ? gl < nl : (gl - half) < nr;
+          if (!filled) s_perm[s] = fillp;
+          s_val[s] = filled ? 1 : 0;
         }
         wave_sync();
       }
-      // (5) stable ranks, then the balanced layout: ranks [0, nl) to the left half, [nl, ng) to the right half
-      const int nl = (ng + 1) / 2, nr = ng - nl, half = S / 2;
-      for (int t = 0; t < M; ++t) {
-        const int s = wb + lane + kWave * t;
-        if (!live) continue;
-        const int mi = s - gb;
-        int rank = mi;
-        if (work) {
-          const float pi = s_proj[s];
-          rank = 0;
-          for (int j = 0; j < S; ++j) {
-            const float pj = s_proj[gb + j];
-            rank += (pj < pi || (pj == pi && j < mi)) ? 1 : 0;
-          }
-        }
-        const int pm = s_perm[s];
-        int r = -1;
-        if (rank < nl) r = rank;
-        else if (rank < ng) r = half + rank - nl;
-        if (r >= 0) {
-          s_np[gb + r] = pm;
-          s_nv[gb + r] = 1;
-        } else if (rank == S - 1) {
-          s_np[gb + S - 1] = pm;   // every empty slot of the group takes the last-ranked member's position
-        }
-      }
-      wave_sync();
-      for (int t = 0; t < M; ++t) {
-        const int s = wb + lane + kWave * t;
-        if (!live) continue;
-        const int r = s - gb;
-        const bool filled = r < half ? r < nl : (r - half) < nr;
-        if (!filled) {
-          s_np[s] = s_np[gb + S - 1];
-          s_nv[s] = 0;
-        }
-      }
-      wave_sync();
-      for (int t = 0; t < M; ++t) {
-        const int s = wb + lane + kWave * t;
-        if (!live) continue;
-        s_perm[s] = s_np[s];
-        s_val[s] = s_nv[s];
-      }
-      wave_sync();
     }
   }
   // leaf slots, then the node sums and counts by adjacent pairs from the slots up
@@ -288,12 +422,65 @@ struct LaneWalk {
   float* ws;
   int64_t P;
   int H, T, C, nlev, nlane, chunk, wmax, wl, Wn, NS, probe, cap_min, neighbors;
+  int ntop;   // nodes held in LDS during the walk
   float rho;
   int32_t* tree_pos;   // (B, H, T, 2 wl)
   uint8_t* leaf_ok;    // (B, H, T, wl)
   int32_t* nb_pos;     // (B, H, T, 2 Wn NS)
   int32_t* n_tree;     // (B, H, T)
   int32_t* nb_leaves;  // (B, H, T)
+};
+
+// The nodes of a lane tree during the walk: nodes [0, ntop) (its top levels) live in LDS for the whole walk
+// (rows of stride D + 4 floats, and counts), deeper nodes in the workspace.  Every access below is uniform in
+// which side it takes (one level at a time).
+template <int D>
+struct LaneNodes {
+  LaneTree tr;
+  float* top;
+  int32_t* tcnt;
+  int ntop;
+  __device__ __forceinline__ int cnt(int n) const { return n < ntop ? tcnt[n] : tr.cnt[n]; }
+  __device__ __forceinline__ void set_cnt(int n, int v) const {
+    if (n < ntop) tcnt[n] = v;
+    else tr.cnt[n] = v;
+  }
+  __device__ __forceinline__ float elem(int n, int d) const {
+    return n < ntop ? top[n * (D + 4) + d] : tr.sums[(int64_t)n * D + d];
+  }
+  __device__ __forceinline__ void set_elem(int n, int d, float v) const {
+    if (n < ntop) top[n * (D + 4) + d] = v;
+    else tr.sums[(int64_t)n * D + d] = v;
+  }
+  __device__ __forceinline__ void row(int n, float (&r)[D]) const {
+    if (n < ntop) {
+      const float* src = top + n * (D + 4);
+#pragma unroll
+      for (int d = 0; d < D; d += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(src + d);
+        r[d] = v.x;
+        r[d + 1] = v.y;
+        r[d + 2] = v.z;
+        r[d + 3] = v.w;
+      }
+    } else {
+      load_row_g<float, D>(tr.sums + (int64_t)n * D, r);
+    }
+  }
+  // workspace -> LDS (to_lds) or back
+  __device__ __forceinline__ void copy(bool to_lds, int lane) const {
+    for (int i = lane; i < ntop * (D / 4); i += kWave) {
+      const int n = i / (D / 4), d = (i - n * (D / 4)) * 4;
+      float4* l = reinterpret_cast<float4*>(top + n * (D + 4) + d);
+      float4* g = reinterpret_cast<float4*>(tr.sums + (int64_t)n * D + d);
+      if (to_lds) *l = *g;
+      else *g = *l;
+    }
+    for (int n = lane; n < ntop; n += kWave) {
+      if (to_lds) tcnt[n] = tr.cnt[n];
+      else tr.cnt[n] = tcnt[n];
+    }
+  }
 };
 
 // Canonical dot of two D-vectors held one element per lane (lane d < D holds a[d] * b[d] in `prod`): the
@@ -329,6 +516,14 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
   const T* qb = static_cast<const T*>(p.q) + b * p.qsb + h * p.qsh;
   const T* kb = static_cast<const T*>(p.k) + b * p.ksb + h * p.ksh;
   const LaneTree tr = lane_tree(p.ws, p.P, p.C, D, pt);
+  extern __shared__ __align__(16) unsigned char s_dyn[];
+  LaneNodes<D> nd;
+  nd.tr = tr;
+  nd.top = reinterpret_cast<float*>(s_dyn);
+  nd.tcnt = reinterpret_cast<int32_t*>(nd.top + p.ntop * (D + 4));
+  nd.ntop = p.ntop;
+  nd.copy(true, lane);
+  wave_sync();
   const int WN = p.Wn * p.NS, wl = p.wl, nlev = p.nlev;
   const float kInf = __int_as_float(0x7f800000);
   const int start = ln * p.chunk;
@@ -349,9 +544,9 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
         id = s_stl[rs];
         if (ok0) {
           const int node = (1 << nlev) - 1 + id;
-          const int cn = tr.cnt[node];
+          const int cn = nd.cnt(node);
           float row[D];
-          load_row_g<float, D>(tr.sums + (int64_t)node * D, row);
+          nd.row(node, row);
           const float sc = lane_dot<D>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) /
                            (float)(cn > 1 ? cn : 1);
           const float base = s_sts[rs];
@@ -383,7 +578,7 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
     // ---- beam search from the root
     if (lane == 0) {
       s_cur[0] = 0;
-      s_bok[0] = tr.cnt[0] > 0;
+      s_bok[0] = nd.cnt(0) > 0;
       s_bsc[0] = 0.0f;
     }
     wave_sync();
@@ -398,9 +593,9 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
         cid = 2 * s_cur[par] + (lane < wp ? 0 : 1);
         if (s_bok[par]) {
           const int node = (1 << lv) - 1 + cid;
-          const int cn = tr.cnt[node];
+          const int cn = nd.cnt(node);
           float row[D];
-          load_row_g<float, D>(tr.sums + (int64_t)node * D, row);
+          nd.row(node, row);
           cv = cn > 0;
           if (cv)
             sc = lane_dot<D>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) / (float)(cn > 1 ? cn : 1);
@@ -453,14 +648,14 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
     // ---- insertion of this position's key (dyntree.py:84-106), one dimension per lane
     const int act = t >= 1 ? 1 : 0;
     const float kva = kd * (act ? 1.0f : 0.0f);
-    if (lane < D) tr.sums[lane] = tr.sums[lane] + kva;
-    if (lane == 0) tr.cnt[0] = tr.cnt[0] + act;
+    if (lane < D) nd.set_elem(0, lane, nd.elem(0, lane) + kva);
+    if (lane == 0) nd.set_cnt(0, nd.cnt(0) + act);
     int node = 0;
     for (int lv = 0; lv < nlev; ++lv) {
       const int base = (2 << lv) - 1, lc = 2 * node, cap = p.C >> (lv + 1);
-      const int cL = tr.cnt[base + lc], cR = tr.cnt[base + lc + 1];
-      const float xL = lane < D ? tr.sums[(int64_t)(base + lc) * D + lane] : 0.0f;
-      const float xR = lane < D ? tr.sums[(int64_t)(base + lc + 1) * D + lane] : 0.0f;
+      const int cL = nd.cnt(base + lc), cR = nd.cnt(base + lc + 1);
+      const float xL = lane < D ? nd.elem(base + lc, lane) : 0.0f;
+      const float xR = lane < D ? nd.elem(base + lc + 1, lane) : 0.0f;
       const float dL = dims_dot<D>(kd * xL), dR = dims_dot<D>(kd * xR);
       float sL = cL == 0 ? -1e9f : dL / (float)(cL > 1 ? cL : 1);
       float sR = cR == 0 ? -1e9f : dR / (float)(cR > 1 ? cR : 1);
@@ -468,8 +663,8 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
       if (cR >= cap) sR = -kInf;
       const bool right = sR > sL;
       node = lc + (right ? 1 : 0);
-      if (lane < D) tr.sums[(int64_t)(base + node) * D + lane] = (right ? xR : xL) + kva;
-      if (lane == 0) tr.cnt[base + node] = (right ? cR : cL) + act;
+      if (lane < D) nd.set_elem(base + node, lane, (right ? xR : xL) + kva);
+      if (lane == 0) nd.set_cnt(base + node, (right ? cR : cL) + act);
     }
     if (lane == 0 && act) {
       const int s0 = tr.slot[2 * node];
@@ -478,6 +673,7 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
     __threadfence_block();
     wave_sync();
   }
+  nd.copy(false, lane);
 }
 
 bool lanetree_dim_ok(int D) { return D == 16 || D == 32 || D == 64; }
@@ -519,7 +715,9 @@ extern "C" int ta_lanetree_build(const void* k, int dtype, int64_t ksb, int64_t 
     return TA_ERR_ARG;
   }
   const int64_t P = (int64_t)B * H * (T / chunk);
-  const size_t lds = (size_t)T * 14;
+  const size_t red = (size_t)kWave * (D + 4) * 4;
+  const size_t lds = (size_t)T * 4 + ((size_t)T * 8 > red ? (size_t)T * 8 : red) +
+                     (size_t)2 * kLtGroups * (D + 4) * 4 + (size_t)2 * kLtGroups * 4 + (size_t)T;
   hipStream_t st = (hipStream_t)stream;
 #define TA_LB(TT, DD)                                                                                          \
   hipLaunchKernelGGL((lanetree_build_kernel<TT, DD>), dim3((unsigned)P), dim3(kWave), lds, st, (const TT*)k, \
@@ -576,9 +774,15 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
   p.wmax = wmax; p.wl = wl; p.Wn = nb_window; p.NS = nb_store; p.probe = nb_probe * nb_store;
   p.cap_min = nb_cap_min; p.neighbors = neighbors ? 1 : 0; p.rho = nb_rho;
   p.tree_pos = tree_pos; p.leaf_ok = leaf_ok; p.nb_pos = nb_pos; p.n_tree = n_tree; p.nb_leaves = nb_leaves;
+  // the top levels of every tree stay in LDS during the walk: as many whole levels as fit in 40 KB
+  const int rowb = (D + 4) * 4 + 4;
+  int ntop = 1;
+  while (2 * ntop + 1 <= T - 1 && (2 * ntop + 1) * rowb <= 40960) ntop = 2 * ntop + 1;
+  p.ntop = ntop;
+  const size_t lds = (size_t)ntop * rowb;
   hipStream_t st = (hipStream_t)stream;
 #define TA_LW(TT, DD) \
-  hipLaunchKernelGGL((lanetree_walk_kernel<TT, DD>), dim3((unsigned)p.P), dim3(kWave), 0, st, p)
+  hipLaunchKernelGGL((lanetree_walk_kernel<TT, DD>), dim3((unsigned)p.P), dim3(kWave), lds, st, p)
 #define TA_LW_D(TT)                  \
   switch (D) {                       \
     case 16: TA_LW(TT, 16); break;   \
