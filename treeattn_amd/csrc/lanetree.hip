@@ -432,14 +432,15 @@ struct LaneWalk {
 };
 
 // The nodes of a lane tree during the walk: nodes [0, ntop) (its top levels) live in LDS for the whole walk
-// (rows of stride D + 4 floats, and counts), deeper nodes in the workspace.  Every access below is uniform in
-// which side it takes (one level at a time).
+// (rows of stride D + 4 floats, and counts), deeper nodes in the workspace; the leaf slots (C entries) live in
+// LDS too.  Every access below is uniform in which side it takes (one level at a time).
 template <int D>
 struct LaneNodes {
   LaneTree tr;
   float* top;
   int32_t* tcnt;
-  int ntop;
+  int32_t* slot;   // LDS copy of the leaf slots
+  int ntop, C;
   __device__ __forceinline__ int cnt(int n) const { return n < ntop ? tcnt[n] : tr.cnt[n]; }
   __device__ __forceinline__ void set_cnt(int n, int v) const {
     if (n < ntop) tcnt[n] = v;
@@ -480,17 +481,50 @@ struct LaneNodes {
       if (to_lds) tcnt[n] = tr.cnt[n];
       else tr.cnt[n] = tcnt[n];
     }
+    for (int n = lane; n < C; n += kWave) {
+      if (to_lds) slot[n] = tr.slot[n];
+      else tr.slot[n] = slot[n];
+    }
   }
 };
 
-// Canonical dot of two D-vectors held one element per lane (lane d < D holds a[d] * b[d] in `prod`): the
-// halving tree inside groups of R = D/16 consecutive lanes, then over the 16 groups (lanes R apart).
+// v of the lane at distance h within the butterfly, for the steps dims_dot takes: xor 1 and xor 2 inside a
+// quad (DPP quad_perm), xor 8 inside a 16-lane row (row rotate by 8), xor 4 by a row rotate by 4 (exact there
+// because the xor-8 step before it left every row 8-periodic), xor 16 and 32 across rows (LDS permute).
+template <int H>
+__device__ __forceinline__ float lt_xor(float v) {
+  const int x = __float_as_int(v);
+  if constexpr (H == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  else if constexpr (H == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  else if constexpr (H == 4) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false));
+  else if constexpr (H == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+  else return __shfl_xor(v, H, kWave);
+}
+
+// Canonical dot of two D-vectors held one element per lane (lane d < D holds a[d] * b[d] in `prod`, 0 past D):
+// the halving tree inside groups of R = D/16 consecutive lanes, then over the 16 groups (lanes R apart), as
+// an xor butterfly (every lane ends with the sum).
 template <int D>
 __device__ __forceinline__ float dims_dot(float prod) {
   constexpr int R = D < 16 ? 1 : D / 16;
-  for (int h = R >> 1; h >= 1; h >>= 1) prod = prod + __shfl_xor(prod, h, kWave);
-  for (int h = 8 * R; h >= R; h >>= 1) prod = prod + __shfl_xor(prod, h, kWave);
+  if constexpr (R >= 4) prod = prod + lt_xor<2>(prod);
+  if constexpr (R >= 2) prod = prod + lt_xor<1>(prod);
+  if constexpr (8 * R >= 32) prod = prod + lt_xor<32>(prod);
+  if constexpr (8 * R >= 16 && R <= 16) prod = prod + lt_xor<16>(prod);
+  if constexpr (R <= 8) prod = prod + lt_xor<8>(prod);
+  if constexpr (R <= 4) prod = prod + lt_xor<4>(prod);
+  if constexpr (R <= 2) prod = prod + lt_xor<2>(prod);
+  if constexpr (R <= 1) prod = prod + lt_xor<1>(prod);
   return prod;
+}
+
+// Search ranking word: valid first, then score descending, node id ascending; invalid candidates by slot.
+// Unique per candidate, so a candidate's rank is the number of smaller words.
+__device__ __forceinline__ uint64_t lt_rank_word(bool valid, float sc, int id, int slot) {
+  if (!valid) return (1ull << 63) | (uint32_t)slot;
+  const uint32_t u = __float_as_uint(sc + 0.0f);
+  const uint32_t asc = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)(~asc) << 31) | (uint32_t)id;
 }
 
 // One wavefront per lane tree, built by lanetree_build_kernel, walking the lane's positions in order
@@ -502,9 +536,7 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
   __shared__ float s_sts[kLaneMaxNb];
   __shared__ uint8_t s_sto[kLaneMaxNb];
   __shared__ int32_t s_nid[kWave];
-  __shared__ int32_t s_cid[kWave];   // the level's children
-  __shared__ float s_csc[kWave];
-  __shared__ uint8_t s_ccv[kWave];
+  __shared__ __align__(16) uint64_t s_rw[kWave];   // the level's children's ranking words
   __shared__ int32_t s_cur[kWave];   // the beam
   __shared__ float s_bsc[kWave];
   __shared__ uint8_t s_bok[kWave];
@@ -521,18 +553,28 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
   nd.tr = tr;
   nd.top = reinterpret_cast<float*>(s_dyn);
   nd.tcnt = reinterpret_cast<int32_t*>(nd.top + p.ntop * (D + 4));
+  nd.slot = nd.tcnt + p.ntop;
   nd.ntop = p.ntop;
+  nd.C = p.C;
   nd.copy(true, lane);
   wave_sync();
   const int WN = p.Wn * p.NS, wl = p.wl, nlev = p.nlev;
   const float kInf = __int_as_float(0x7f800000);
   const int start = ln * p.chunk;
+  float qn[D];   // the next position's query and key, requested while the current position runs
+  load_row_g<T, D>(qb + (int64_t)start * p.qst, qn);
+  float kn = lane < D ? to_f32(kb[(int64_t)start * p.kst + lane]) : 0.0f;
   for (int i = 0; i < p.chunk; ++i) {
     const int t = start + i;
     const int64_t orow = bh * p.T + t;
     float qv[D];
-    load_row_g<T, D>(qb + (int64_t)t * p.qst, qv);
-    const float kd = lane < D ? to_f32(kb[(int64_t)t * p.kst + lane]) : 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) qv[d] = qn[d];
+    const float kd = kn;
+    if (i + 1 < p.chunk) {
+      load_row_g<T, D>(qb + (int64_t)(t + 1) * p.qst, qn);
+      kn = lane < D ? to_f32(kb[(int64_t)(t + 1) * p.kst + lane]) : 0.0f;
+    }
     // ---- neighbours: the leaves the last Wn positions of the lane stored, re-scored on the current tree
     int id = 0;
     bool ok0 = false, match = false;
@@ -565,7 +607,7 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
     for (int e = 0; e < lane && first; ++e) first = s_nid[e] != id;
     const int nL = __popcll(__ballot(first));
     if (lane < WN) {
-      const int s0 = tr.slot[2 * id], s1 = tr.slot[2 * id + 1];
+      const int s0 = nd.slot[2 * id], s1 = nd.slot[2 * id + 1];
       int32_t* o = p.nb_pos + orow * 2 * WN;
       o[lane] = match && s0 >= 0 ? s0 : -1;
       o[WN + lane] = match && s1 >= 0 ? s1 : -1;
@@ -600,21 +642,23 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
           if (cv)
             sc = lane_dot<D>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) / (float)(cn > 1 ? cn : 1);
         }
-        s_cid[lane] = cid;
-        s_csc[lane] = sc;
-        s_ccv[lane] = cv;
+        s_rw[lane] = lt_rank_word(cv, sc, cid, lane);
       }
       wave_sync();
       const int w = nch < p.wmax ? nch : p.wmax;
       if (lane < nch) {
+        const uint64_t mine = s_rw[lane];
         int rank = 0;
-        for (int j = 0; j < nch; ++j) {
-          const bool vj = s_ccv[j] != 0;
-          bool before;
-          if (vj != cv) before = vj;
-          else if (cv) before = s_csc[j] > sc || (s_csc[j] == sc && s_cid[j] < cid);
-          else before = j < lane;
-          rank += before ? 1 : 0;
+        for (int j0 = 0; j0 < nch; j0 += 8) {   // words read four pairs at a time
+          uint64_t wv[8];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const uint4 two = *reinterpret_cast<const uint4*>(s_rw + j0 + 2 * h);
+            wv[2 * h] = ((uint64_t)two.y << 32) | two.x;
+            wv[2 * h + 1] = ((uint64_t)two.w << 32) | two.z;
+          }
+#pragma unroll
+          for (int h = 0; h < 8; ++h) rank += (j0 + h < nch && wv[h] < mine) ? 1 : 0;
         }
         if (rank < w) {
           s_cur[rank] = cid;
@@ -629,7 +673,7 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
     if (lane < wl) {
       const int lid = s_cur[lane];
       const bool ok = s_bok[lane] != 0;
-      const int s0 = tr.slot[2 * lid], s1 = tr.slot[2 * lid + 1];
+      const int s0 = nd.slot[2 * lid], s1 = nd.slot[2 * lid + 1];
       int32_t* o = p.tree_pos + orow * 2 * wl;
       o[lane] = ok && s0 >= 0 ? s0 : -1;
       o[wl + lane] = ok && s1 >= 0 ? s1 : -1;
@@ -667,8 +711,8 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
       if (lane == 0) nd.set_cnt(base + node, (right ? cR : cL) + act);
     }
     if (lane == 0 && act) {
-      const int s0 = tr.slot[2 * node];
-      tr.slot[2 * node + (s0 >= 0 ? 1 : 0)] = t;
+      const int s0 = nd.slot[2 * node];
+      nd.slot[2 * node + (s0 >= 0 ? 1 : 0)] = t;
     }
     __threadfence_block();
     wave_sync();
@@ -779,7 +823,7 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
   int ntop = 1;
   while (2 * ntop + 1 <= T - 1 && (2 * ntop + 1) * rowb <= 40960) ntop = 2 * ntop + 1;
   p.ntop = ntop;
-  const size_t lds = (size_t)ntop * rowb;
+  const size_t lds = (size_t)ntop * rowb + (size_t)T * 4;   // + the leaf slots
   hipStream_t st = (hipStream_t)stream;
 #define TA_LW(TT, DD) \
   hipLaunchKernelGGL((lanetree_walk_kernel<TT, DD>), dim3((unsigned)p.P), dim3(kWave), lds, st, p)
