@@ -31,14 +31,55 @@ __device__ __forceinline__ float lane_dot(FA fa, FB fb) {
   return g[0];
 }
 
+// The 32-bit value of lane (this lane ^ H), without the LDS crossbar: xor 1 and 2 by DPP quad permutes, xor 4 by
+// a 16-lane row rotate by 4 or 12 (the one that lands on the partner), xor 8 by a row rotate by 8, xor 16 and 32
+// by the gfx950 lane swaps (v_permlane16_swap / v_permlane32_swap of the value with itself; the swapped copy
+// holds the partner's value in this lane).
+template <int H>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v) {
+  const int x = (int)v;
+  if constexpr (H == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (H == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (H == 4) {
+    const uint32_t r4 = (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false);
+    const uint32_t r12 = (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x12C, 0xF, 0xF, false);
+    return (threadIdx.x & 4) ? r4 : r12;
+  } else if constexpr (H == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);
+  } else if constexpr (H == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? s[0] : s[1];
+  } else {
+    static_assert(H == 32, "xor distance 1..32");
+    const auto s = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? s[0] : s[1];
+  }
+}
+template <int H>
+__device__ __forceinline__ float xor_lane(float v) { return __uint_as_float(xor_lane_u32<H>(__float_as_uint(v))); }
+template <int H>
+__device__ __forceinline__ int xor_lane(int v) { return (int)xor_lane_u32<H>((uint32_t)v); }
+
 // Sum over the aligned S-lane segment holding this lane, by the halving tree over the segment's lanes in order
 // (every lane returns the same value: each step adds the lane at distance h, and float addition commutes).
 __device__ __forceinline__ float seg_sum(float v, int S) {
-  for (int h = S >> 1; h >= 1; h >>= 1) v = v + __shfl_xor(v, h, kWave);
+  if (S > 32) v = v + xor_lane<32>(v);
+  if (S > 16) v = v + xor_lane<16>(v);
+  if (S > 8) v = v + xor_lane<8>(v);
+  if (S > 4) v = v + xor_lane<4>(v);
+  if (S > 2) v = v + xor_lane<2>(v);
+  if (S > 1) v = v + xor_lane<1>(v);
   return v;
 }
 __device__ __forceinline__ float seg_max(float v, int S) {
-  for (int h = S >> 1; h >= 1; h >>= 1) v = fmaxf(v, __shfl_xor(v, h, kWave));
+  if (S > 32) v = fmaxf(v, xor_lane<32>(v));
+  if (S > 16) v = fmaxf(v, xor_lane<16>(v));
+  if (S > 8) v = fmaxf(v, xor_lane<8>(v));
+  if (S > 4) v = fmaxf(v, xor_lane<4>(v));
+  if (S > 2) v = fmaxf(v, xor_lane<2>(v));
+  if (S > 1) v = fmaxf(v, xor_lane<1>(v));
   return v;
 }
 // The first lane of the segment [gb, gb + S) whose v equals the segment's maximum.

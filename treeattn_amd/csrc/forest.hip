@@ -29,6 +29,23 @@ constexpr int kForestMaxW = 64;         // wmax
 
 __device__ __forceinline__ float forest_log(float x) { return (float)log((double)(fabsf(x) + 1e-6f)); }
 
+// seg_sum of every element of v (the same butterfly per element), step-major so the shuffles of all D
+// elements are in flight together.
+template <int H, int D>
+__device__ __forceinline__ void seg_sum_rows_step(float (&v)[D]) {
+#pragma unroll
+  for (int d = 0; d < D; ++d) v[d] = v[d] + xor_lane<H>(v[d]);
+}
+template <int D>
+__device__ __forceinline__ void seg_sum_rows(float (&v)[D], int S) {
+  if (S > 32) seg_sum_rows_step<32>(v);
+  if (S > 16) seg_sum_rows_step<16>(v);
+  if (S > 8) seg_sum_rows_step<8>(v);
+  if (S > 4) seg_sum_rows_step<4>(v);
+  if (S > 2) seg_sum_rows_step<2>(v);
+  if (S > 1) seg_sum_rows_step<1>(v);
+}
+
 struct ForestLevels {
   float* sums[kMaxLevels];   // level l: (B, H, nb << l, D) float32, node rows contiguous
   float* lg[kMaxLevels];     // the gate's log-magnitude sums (null without the gate)
@@ -48,6 +65,7 @@ __global__ __launch_bounds__(kWave) void forest_build_kernel(const T* __restrict
   constexpr int DP = D + 1;   // LDS row stride of the reorder buffer
   __shared__ float s_x[kWave * DP];
   __shared__ int s_p[kWave];
+  __shared__ __align__(16) float s_pr[kWave];   // the level's projections
   const int lane = lane_id();
   const int pb = blockIdx.x, blk = pb % nb, bh = pb / nb, b = bh / H, h = bh % H;
   const bool live = lane < Bk;
@@ -58,12 +76,15 @@ __global__ __launch_bounds__(kWave) void forest_build_kernel(const T* __restrict
   for (int d = 0; d < D; ++d) x[d] = live ? (pos == 0 ? x[d] * 0.0f : x[d]) : 0.0f;   // the sink: k * 0
   int p = lane;
 
-  float c0[D], c1[D];
+  float c0[D], c1[D], t[D];
   for (int lvl = 0; lvl < depth; ++lvl) {
     const int S = Bk >> lvl, gb = lane & ~(S - 1), li = lane - gb;
     // the group mean, then the member farthest from it (a) and the member farthest from a (b)
 #pragma unroll
-    for (int d = 0; d < D; ++d) c0[d] = seg_sum(x[d], S) / (float)S;
+    for (int d = 0; d < D; ++d) c0[d] = x[d];
+    seg_sum_rows<D>(c0, S);
+#pragma unroll
+    for (int d = 0; d < D; ++d) c0[d] = c0[d] / (float)S;
     const float d2 = lane_dot<D>([&](int i) { return x[i] - c0[i]; }, [&](int i) { return x[i] - c0[i]; });
     const int la = seg_argmax_first(d2, gb, S);
 #pragma unroll
@@ -84,22 +105,28 @@ __global__ __launch_bounds__(kWave) void forest_build_kernel(const T* __restrict
       const float cnt0 = seg_sum(m0, S), cnt1 = seg_sum(m1, S);
       const float den0 = fmaxf(cnt0, 1.0f), den1 = fmaxf(cnt1, 1.0f);
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const float n0 = seg_sum(x[d] * m0, S) / den0;
-        c0[d] = cnt0 > 0.0f ? n0 : c0[d];
-      }
+      for (int d = 0; d < D; ++d) t[d] = x[d] * m0;
+      seg_sum_rows<D>(t, S);
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const float n1 = seg_sum(x[d] * m1, S) / den1;
-        c1[d] = cnt1 > 0.0f ? n1 : c1[d];
-      }
+      for (int d = 0; d < D; ++d) c0[d] = cnt0 > 0.0f ? t[d] / den0 : c0[d];
+#pragma unroll
+      for (int d = 0; d < D; ++d) t[d] = x[d] * m1;
+      seg_sum_rows<D>(t, S);
+#pragma unroll
+      for (int d = 0; d < D; ++d) c1[d] = cnt1 > 0.0f ? t[d] / den1 : c1[d];
     }
     const float proj = lane_dot<D>([&](int i) { return x[i]; }, [&](int i) { return c0[i] - c1[i]; });
-    // stable ascending rank of the projection inside the group, then the member moves to that rank
+    // stable ascending rank of the projection inside the group (read from LDS four at a time), then the
+    // member moves to that rank
+    s_pr[lane] = proj;
+    wave_sync();
     int rank = 0;
-    for (int j = 0; j < S; ++j) {
-      const float pj = __shfl(proj, gb + j, kWave);
-      rank += (pj < proj || (pj == proj && j < li)) ? 1 : 0;
+#pragma unroll 4
+    for (int j = 0; j < S; j += 4) {
+      const float4 q4 = *reinterpret_cast<const float4*>(s_pr + gb + j);
+      const float pj[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rank += (pj[e] < proj || (pj[e] == proj && j + e < li)) ? 1 : 0;
     }
     const int slot = gb + rank;
 #pragma unroll
@@ -117,8 +144,14 @@ __global__ __launch_bounds__(kWave) void forest_build_kernel(const T* __restrict
   auto pyramid = [&](float (&y)[D], float* const* out) {
     for (int l = depth; l >= 0; --l) {
       const int sz = Bk >> l;   // keys per node at level l
-#pragma unroll
-      for (int d = 0; d < D; ++d) y[d] = y[d] + __shfl_xor(y[d], sz >> 1, kWave);
+      switch (sz >> 1) {   // adjacent pairs of the level below: partner at distance sz / 2
+        case 1: seg_sum_rows_step<1>(y); break;
+        case 2: seg_sum_rows_step<2>(y); break;
+        case 4: seg_sum_rows_step<4>(y); break;
+        case 8: seg_sum_rows_step<8>(y); break;
+        case 16: seg_sum_rows_step<16>(y); break;
+        default: seg_sum_rows_step<32>(y); break;
+      }
       if (live && (lane & (sz - 1)) == 0) {
         float* row = out[l] + b * lv.sb[l] + h * lv.sh[l] + ((int64_t)blk * (Bk / sz) + lane / sz) * D;
 #pragma unroll

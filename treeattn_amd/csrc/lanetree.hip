@@ -49,27 +49,39 @@ __device__ __forceinline__ LaneTree lane_tree(float* ws, int64_t P, int C, int D
 }
 
 // (value, index) argmax over an aligned L-lane segment: the largest value, the smallest index among equals.
-__device__ __forceinline__ int seg_argmax_idx(float v, int i, int L) {
-  for (int h = L >> 1; h >= 1; h >>= 1) {
-    const float ov = __shfl_xor(v, h, kWave);
-    const int oi = __shfl_xor(i, h, kWave);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
+template <int H>
+__device__ __forceinline__ void argmax_step(float& v, int& i) {
+  const float ov = xor_lane<H>(v);
+  const int oi = xor_lane<H>(i);
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
   }
+}
+__device__ __forceinline__ int seg_argmax_idx(float v, int i, int L) {
+  if (L > 32) argmax_step<32>(v, i);
+  if (L > 16) argmax_step<16>(v, i);
+  if (L > 8) argmax_step<8>(v, i);
+  if (L > 4) argmax_step<4>(v, i);
+  if (L > 2) argmax_step<2>(v, i);
+  if (L > 1) argmax_step<1>(v, i);
   return i;
 }
 
 // Integer min / max over an aligned L-lane segment.
-__device__ __forceinline__ int seg_imax(int v, int L) {
-  for (int h = L >> 1; h >= 1; h >>= 1) v = max(v, __shfl_xor(v, h, kWave));
+template <bool MAX>
+__device__ __forceinline__ int seg_iext(int v, int L) {
+  auto f = [](int a, int b) { return MAX ? max(a, b) : min(a, b); };
+  if (L > 32) v = f(v, xor_lane<32>(v));
+  if (L > 16) v = f(v, xor_lane<16>(v));
+  if (L > 8) v = f(v, xor_lane<8>(v));
+  if (L > 4) v = f(v, xor_lane<4>(v));
+  if (L > 2) v = f(v, xor_lane<2>(v));
+  if (L > 1) v = f(v, xor_lane<1>(v));
   return v;
 }
-__device__ __forceinline__ int seg_imin(int v, int L) {
-  for (int h = L >> 1; h >= 1; h >>= 1) v = min(v, __shfl_xor(v, h, kWave));
-  return v;
-}
+__device__ __forceinline__ int seg_imax(int v, int L) { return seg_iext<true>(v, L); }
+__device__ __forceinline__ int seg_imin(int v, int L) { return seg_iext<false>(v, L); }
 
 // Sort key of a projection: ascending float order (-0 taken as +0, as the comparison does) above the member
 // index, so that sorting the 64-bit words is the stable sort of the projections.
@@ -488,33 +500,20 @@ struct LaneNodes {
   }
 };
 
-// v of the lane at distance h within the butterfly, for the steps dims_dot takes: xor 1 and xor 2 inside a
-// quad (DPP quad_perm), xor 8 inside a 16-lane row (row rotate by 8), xor 4 by a row rotate by 4 (exact there
-// because the xor-8 step before it left every row 8-periodic), xor 16 and 32 across rows (LDS permute).
-template <int H>
-__device__ __forceinline__ float lt_xor(float v) {
-  const int x = __float_as_int(v);
-  if constexpr (H == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
-  else if constexpr (H == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
-  else if constexpr (H == 4) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false));
-  else if constexpr (H == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
-  else return __shfl_xor(v, H, kWave);
-}
-
 // Canonical dot of two D-vectors held one element per lane (lane d < D holds a[d] * b[d] in `prod`, 0 past D):
 // the halving tree inside groups of R = D/16 consecutive lanes, then over the 16 groups (lanes R apart), as
 // an xor butterfly (every lane ends with the sum).
 template <int D>
 __device__ __forceinline__ float dims_dot(float prod) {
   constexpr int R = D < 16 ? 1 : D / 16;
-  if constexpr (R >= 4) prod = prod + lt_xor<2>(prod);
-  if constexpr (R >= 2) prod = prod + lt_xor<1>(prod);
-  if constexpr (8 * R >= 32) prod = prod + lt_xor<32>(prod);
-  if constexpr (8 * R >= 16 && R <= 16) prod = prod + lt_xor<16>(prod);
-  if constexpr (R <= 8) prod = prod + lt_xor<8>(prod);
-  if constexpr (R <= 4) prod = prod + lt_xor<4>(prod);
-  if constexpr (R <= 2) prod = prod + lt_xor<2>(prod);
-  if constexpr (R <= 1) prod = prod + lt_xor<1>(prod);
+  if constexpr (R >= 4) prod = prod + xor_lane<2>(prod);
+  if constexpr (R >= 2) prod = prod + xor_lane<1>(prod);
+  if constexpr (8 * R >= 32) prod = prod + xor_lane<32>(prod);
+  if constexpr (8 * R >= 16 && R <= 16) prod = prod + xor_lane<16>(prod);
+  if constexpr (R <= 8) prod = prod + xor_lane<8>(prod);
+  if constexpr (R <= 4) prod = prod + xor_lane<4>(prod);
+  if constexpr (R <= 2) prod = prod + xor_lane<2>(prod);
+  if constexpr (R <= 1) prod = prod + xor_lane<1>(prod);
   return prod;
 }
 
