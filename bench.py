@@ -193,9 +193,9 @@ def gather_dot_bench(args):
            'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16 in, f32 out',
            'data': 'synthetic (N(0,1) q and k, uniform causally valid block ids, seed 1)',
            'config': {'workload': leg['workload'], 'bytes_per_call': leg['bytes_per_call']},
-           'roofline': {'bound': 'hbm', 'kernel': 'gather_blocks_kernel (matrix-core block gather-dot)',
+           'roofline': {'bound': 'hbm', 'kernel': 'gather_pairs_kernel (matrix-core block-major gather-dot)',
                         'achieved': leg['GB/s'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': leg['frac_of_hbm'],
-                        'traffic': recorded_traffic('gather_blocks_kernel'), 'bytes_per_launch': leg['bytes_per_call'],
+                        'traffic': recorded_traffic('gather_pairs_kernel'), 'bytes_per_launch': leg['bytes_per_call'],
                         'avg_us': leg['avg_us'], 'timing': 'cold caches (1 GiB read before each of 20 launches)'},
            'parity': {'slice': [0, 0], 'max_rel_err_vs_oracle': float('%.3g' % rel), 'bar': 2e-5},
            'cpu_baseline': {'value': round(bytes_slice / slice_s / 1e9, 3), 'unit': 'GB/s', 'cores': ncores,
