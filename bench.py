@@ -206,7 +206,37 @@ def gather_dot_bench(args):
     return res
 
 
-def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64):
+def selection_check(dec, ref, probes, t, cfg, sel):
+    """Sequence 0's selections at position t for every layer and head: the GPU descent (ta_tree_descend over
+    the GPU pyramid) with the oracle's query against the oracle's canonical descent, bit for bit; and the
+    reference's torch order (the oracle step's own faithful selection) against the canonical order, every
+    disagreement classified by oracle.ties.tie_report."""
+    from oracle.engine_ref import descend
+    from oracle.ties import tie_report
+    from treeattn_amd import kernels as K
+    tq = torch.tensor([t], dtype=torch.int32, device='cuda')
+    for i, st in enumerate(ref.states):
+        p = probes[i]
+        q = p['q'].float()                                          # (1, H, 1, dh), bf16 values
+        ci, cv, _ = descend(st, q, t, 'canonical')
+        gs = dec.states[i]
+        gi, gv, _ = K.tree_descend(q.to(gs.dtype).cuda(), [lv[0:1] for lv in gs.score_levels], tq, gs.shape, cfg.wmax)
+        gi, gv = gi.long().cpu(), gv.bool().cpu()
+        same = (gv == cv).all(-1) & (torch.where(cv, ci, -1) == torch.where(gv, gi, -1)).all(-1)   # (1, H, 1)
+        sel['gpu_equals_canonical'] += int(same.sum())
+        fi, fv = p['sel']['ids'], p['sel']['vld']
+        geom = st.geom
+        for h in range(q.shape[1]):
+            r = tie_report(q[0, h], {j: st.raw[l][0, h] for j, l in enumerate(geom.blevels)}, torch.tensor([t]),
+                           geom, cfg.wmax, ci[0, h], cv[0, h], fi[0, h], fv[0, h])
+            sel['queries'] += 1
+            sel['torch_order_diverged'] += r['diverged']
+            sel['ties_within_1ulp'] += r['within_1ulp']
+            sel['ties_within_bound'] += r['within_bound']
+            sel['worst_gap_ulps'] = max(sel['worst_gap_ulps'], float('%.3g' % r['worst_ulps']))
+
+
+def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64, sel_steps=4):
     """The oracle engine (CPU restatement of engine.py) decodes sequence 0 from the GPU's state."""
     from oracle.engine_ref import DecoderRef, linear_f32_round
     from treeattn_amd import kernels as K
@@ -228,6 +258,9 @@ def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64):
     t = int(t_now)
     # GPU: decode the same steps eagerly for the parity check of sequence 0 (both sides fed the oracle's token)
     times, errs, floors, toks_same, flips_near_tie = [], [], [], 0, 0
+    sel = dict(queries=0, gpu_equals_canonical=0, torch_order_diverged=0, ties_within_1ulp=0, ties_within_bound=0,
+               worst_gap_ulps=0.0)
+    block0 = int(t_now) // dec.states[0].shape.leaf
     tg = tok_now.clone()
     n = 0
     t_start = time.perf_counter()
@@ -235,8 +268,13 @@ def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64):
         t0 = time.perf_counter()
         lc, _ = ref.step(tok, t)
         dt = time.perf_counter() - t0
-        la, _ = alt.step(tok, t)
+        probes = {}
+        la, _ = alt.step(tok, t, probe=lambda i, d: probes.__setitem__(i, d))
         lg, _ = dec.step(tg, t)
+        if n < sel_steps and t // dec.states[0].shape.leaf == block0:
+            # the descents at t read only nodes that end before t, and no node holding a decode-appended row is
+            # complete yet, so the GPU's pyramid of sequence 0 equals the oracle's: selection compared bit for bit
+            selection_check(dec, alt, probes, t, cfg, sel)
         lg0 = lg[0].float().cpu()
         errs.append((lc - lg0).abs().max().item())
         floors.append((lc - la.float()).abs().max().item())
@@ -267,6 +305,12 @@ def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64):
                             'bound': round(max(2e-2, 2 * max(floors)), 5),
                             'same_greedy_token': toks_same,
                             'flips_at_top2_gap_within_2x_diff': flips_near_tie,
+                            'selection': dict(sel, note='every (layer, head) query of sequence 0 at the first '
+                                              'decode steps (the oracle\'s q): the GPU descent against the '
+                                              'oracle\'s canonical order bit for bit, and the reference\'s torch '
+                                              'order against the canonical one, each disagreement classified '
+                                              '(score gap in ulps at the first divergent level; within the '
+                                              'float32 rounding bound of the two scores = a tie)'),
                             'note': 'free-running decode from the same cache; the oracle runs the reference op '
                                     'chain (torch order selection); floor = the same oracle with its linear '
                                     'layers accumulated in another order'}}
