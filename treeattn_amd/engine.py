@@ -319,7 +319,10 @@ def _pw_budget(state, pw, q, t):
 
 def _pw_budget_seq(cfg, H, pw, q, k):
     """_pw_budget for every position of a prompt (q, k: (B,H,T,dh)): the same features, the global pool being
-    the mean of the keys before each position (what the decode cache's running sum holds at that step)."""
+    the mean of the keys before each position (what the decode cache's running sum holds at that step).
+    Computed in float32 like the decode step's budget head (engine.py:89-96), not in the model dtype like the
+    forward's SegAttention.budget (fastseg.py:352-362): the prefill seeds the decode cache, so its budgets are
+    the ones decoding the prompt position by position would pick."""
     B, _, T, _ = q.shape
     feats = [q.float(), torch.log(q.float().norm(dim=-1, keepdim=True) + 1e-6),
              torch.eye(H, device=q.device).view(1, H, 1, H).expand(B, H, T, H)]
