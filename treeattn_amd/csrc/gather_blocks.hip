@@ -1,20 +1,24 @@
 // Leaf-block gather-dot on gfx950 MFMA: out[b,h,n, c*block + j] = scale * q[b,h,n] . K[b,h, blk[b,h,n,c]*block + j].
 //
-// Block-major: a workgroup takes kGpQ consecutive queries of one (b, h) and turns their (query, slot) pairs into
+// Block-major: a workgroup takes Q consecutive queries of one (b, h) (512 at D = 64, 128 at D = 128: as many as
+// the LDS copy of their rows allows) and turns their (query, slot) pairs into
 // per-block lists, so every score the matrix cores compute belongs to a pair that selected the block.
 //
-//  * Set-up: the workgroup's query rows are copied into LDS; its pairs (at most kGpQ * 16) are sorted by block
+//  * Set-up: the workgroup's query rows are copied into LDS; its pairs (at most Q * 16) are sorted by block
 //    id with a counting sort in LDS (a count per block, one scan giving each block its list offset and its
 //    number of 32-pair chunks, then each pair placed with an LDS atomic).  A chunk is up to 32 pairs that
 //    selected the same block; an item is a chunk and one 32-key tile of its block.
-//  * The wavefronts take contiguous runs of chunks.  For an item a wavefront reads its pairs' query rows from
-//    LDS as the MFMA B operand and the key tile from global memory (the head's keys stay in the XCD's L2) as the
-//    A operand, and computes S^T = K_tile . Q^T with v_mfma_f32_32x32x16: lane (p, hh) holds keys
-//    8 i + 4 hh + r of pair p.  The 32 x 32 scores pass through the wavefront's own LDS tile so that each store
-//    instruction writes eight pairs' 128-byte runs of consecutive keys (whole lines).
-//  * The next item's key tile is requested before the current item's stores, and the loop runs two items per
-//    pass with the two register sets alternating: the vector-memory counter counts stores too, so a wait for a
-//    key tile then never covers the stores issued after it, and the stores drain while the next item computes.
+//  * The wavefronts take contiguous runs of chunks, in groups of four consecutive chunks: for each key tile of
+//    the group the group's chunks come back to back, so the chunks of one block (neighbours in the sorted list)
+//    request the same tile one item after another and the repeats are served close to the CU.  For an item a
+//    wavefront reads its pairs' query rows from LDS as the MFMA B operand and the key tile from global memory
+//    (the head's keys stay in the XCD's L2) as the A operand, and computes S^T = K_tile . Q^T with
+//    v_mfma_f32_32x32x16: lane (p, hh) holds keys 8 i + 4 hh + r of pair p.  The 32 x 32 scores pass through
+//    the wavefront's own LDS tile so that each store instruction writes eight pairs' 128-byte runs of
+//    consecutive keys (whole lines).
+//  * The key tile of item i + 2 is requested before item i's stores, with three register sets in rotation
+//    (the loop runs three items per pass): the vector-memory counter counts stores too, so a wait for a key tile
+//    then covers only stores issued at least two items earlier, and the stores drain while later items compute.
 //    Stores go through a buffer resource over the workgroup's output rows; lanes past a chunk's count get an
 //    offset past its end, which the hardware drops, so every store is issued unconditionally.
 //
@@ -50,10 +54,14 @@ __device__ __forceinline__ f32x16_g mfma32<f16_t>(const uint4& a, const uint4& b
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, c, 0, 0, 0);
 }
 
-constexpr int kGpQ = 128;                                  // queries per workgroup
 constexpr int kGpWaves = 8;
 constexpr int kGpThreads = kGpWaves * kWave;
-constexpr int kGpMaxPairs = kGpQ * kGdMaxSlots;            // 2048
+// Queries per workgroup: as many as the LDS copy of their rows allows (512 rows of D = 64, 128 of D = 128).
+// More queries per workgroup means more pairs per block, so each key tile read from the L2 serves more chunks.
+template <int D> struct GpShape {
+  static constexpr int Q = D == 64 ? 512 : 128;
+  static constexpr int MaxPairs = Q * kGdMaxSlots;
+};
 constexpr int kGpRow = 36;                                 // staging row stride in floats (32 + 4 of padding)
 constexpr int kGpStage = 32 * kGpRow;                      // floats per wavefront staging tile
 
@@ -62,17 +70,18 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
     const T* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qsn, const T* __restrict__ K, int64_t ksb,
     int64_t ksh, int64_t ksn, const int32_t* __restrict__ blk, int H, int N, int nblocks, int NB, int ntile,
     float scale, float* __restrict__ out) {
+  constexpr int Q = GpShape<D>::Q, MaxPairs = GpShape<D>::MaxPairs;
   constexpr int KS = D / 16;         // MFMA k-steps
   constexpr int KT = BLOCK / 32;     // 32-key tiles per block
   constexpr int kUnion = (kGdMaxBlocks > kGpWaves * kGpStage ? kGdMaxBlocks : kGpWaves * kGpStage);
-  static_assert(kGpMaxPairs % kGpThreads == 0, "pairs per thread");
+  static_assert(MaxPairs % kGpThreads == 0, "pairs per thread");
   // counts / offsets per block during the sort, then the wavefronts' staging tiles
   __shared__ __attribute__((aligned(16))) uint32_t uni[kUnion];
-  __shared__ uint16_t plist[kGpMaxPairs];      // (query << 4 | slot), grouped by block
-  __shared__ uint32_t chunk[kGpMaxPairs];      // block << 17 | start << 5 | (count - 1)
+  __shared__ uint16_t plist[MaxPairs];      // (query << 4 | slot), grouped by block
+  __shared__ uint32_t chunk[MaxPairs];      // block << 18 | start << 5 | (count - 1)
   __shared__ uint32_t wsum[kGpWaves];
   __shared__ uint32_t s_tot;
-  __shared__ __attribute__((aligned(16))) T qs[kGpQ * (D + 8)];   // the workgroup's query rows
+  __shared__ __attribute__((aligned(16))) T qs[Q * (D + 8)];   // the workgroup's query rows
 
   const int tid = threadIdx.x, lane = lane_id();
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
@@ -82,9 +91,9 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   const int base = G / 8, rem = G % 8, xcd = x % 8;
   const int lam = xcd * base + (xcd < rem ? xcd : rem) + x / 8;
   const int bh = lam / ntile;
-  const int n0 = (lam - bh * ntile) * kGpQ;
+  const int n0 = (lam - bh * ntile) * Q;
   const int b = bh / H, h = bh - b * H;
-  const int nq = N - n0 < kGpQ ? N - n0 : kGpQ;
+  const int nq = N - n0 < Q ? N - n0 : Q;
   const int npairs = nq * NB;
 
   {
@@ -98,7 +107,7 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   // 1. counts per block (ids clamped into [0, nblocks - 1])
   for (int i = tid; i < nblocks; i += kGpThreads) uni[i] = 0u;
   __syncthreads();
-  constexpr int PPT = kGpMaxPairs / kGpThreads;
+  constexpr int PPT = MaxPairs / kGpThreads;
   int pid[PPT];
   const int32_t* brow = blk + ((int64_t)bh * N + n0) * NB;
 #pragma unroll
@@ -147,7 +156,7 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
       const uint32_t st = run & 0xffffu, cs = run >> 16;
       for (uint32_t k = 0; 32u * k < c; ++k) {
         const uint32_t cnt = c - 32u * k < 32u ? c - 32u * k : 32u;
-        chunk[cs + k] = ((uint32_t)j << 17) | ((st + 32u * k) << 5) | (cnt - 1u);
+        chunk[cs + k] = ((uint32_t)j << 18) | ((st + 32u * k) << 5) | (cnt - 1u);
       }
       uni[j] = st;    // becomes the running fill position
       run += (((c + 31u) >> 5) << 16) | c;
@@ -177,12 +186,18 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   // offset past the end, which the hardware drops, so every store is issued unconditionally
   const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(obase, 0, nq * NB * BLOCK * 4, 0x00020000);
   const int rP = lane >> 3, rc = lane & 7;
-  const int nit = (c1 - c0) * KT;
+  const int nch2 = ((c1 - c0) + 3) & ~3;   // chunks rounded up to groups of four
+  const int nit = nch2 * KT;
+  // item i -> (chunk, key tile): groups of four consecutive chunks, key tile kt, the group's chunks back to back,
+  // so the chunks of one block (consecutive in the block-sorted list) request the same tile one item apart
+  auto item_chunk = [&](int i) { return c0 + 4 * (i / (4 * KT)) + (i & 3); };
+  auto item_kt = [&](int i) { return (i >> 2) % KT; };
   // item i = (chunk c0 + i / KT, key tile i % KT); its K tile is requested one item ahead, before the
   // current item's stores, so no wait for a K tile covers stores that were issued after it
   auto kload = [&](int i, uint4 (&kk)[KS]) {
-    const int c = c0 + i / KT, kt = i % KT;
-    const int j = (int)(chunk[c] >> 17);
+    const int cc = item_chunk(i), kt = item_kt(i);
+    const int c = cc < c1 ? cc : c1 - 1;
+    const int j = (int)(chunk[c] >> 18);
     const T* kr = kbase + ((int64_t)j * BLOCK + 32 * kt + p) * ksn;
 #pragma unroll
     for (int s = 0; s < KS; ++s) kk[s] = ldg16(kr + 16 * s);
@@ -190,11 +205,14 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   // one item: scores from the K tile in cur, the next item's tile requested into nxt, then the stores; the
   // loop runs two items per pass with the two register sets alternating (an odd count is padded by an item
   // whose stores are all dropped), so no register copy waits for a load issued in the same pass
-  auto item = [&](int i, const uint4 (&cur)[KS], uint4 (&nxt)[KS]) {
+  // item i with its key tile in ck; the key tile of item i + 2 is requested into nk before this item's stores, so
+  // a wait for a tile covers only stores issued at least two items earlier
+  auto item = [&](int i, const uint4 (&ck)[KS], uint4 (&nk)[KS]) {
     const int iv = i < nit ? i : nit - 1;
-    const int c = c0 + iv / KT, kt = iv % KT;
+    const int cc = item_chunk(iv), kt = item_kt(iv);
+    const int c = cc < c1 ? cc : c1 - 1;
     const uint32_t ce = chunk[c];
-    const int st = (int)((ce >> 5) & 0xfffu), cnt = i < nit ? (int)(ce & 31u) + 1 : 0;
+    const int st = (int)((ce >> 5) & 0x1fffu), cnt = (i < nit && cc < c1) ? (int)(ce & 31u) + 1 : 0;
     const int code = plist[st + (p < cnt ? p : 0)];
     const uint4* qr = reinterpret_cast<const uint4*>(qs + (code >> 4) * (D + 8)) + hh;
     uint4 qb[KS];
@@ -204,8 +222,8 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) acc = mfma32<T>(cur[s], qb[s], acc);
-    kload(iv + 1 < nit ? iv + 1 : iv, nxt);
+    for (int s = 0; s < KS; ++s) acc = mfma32<T>(ck[s], qb[s], acc);
+    kload(iv + 2 < nit ? iv + 2 : nit - 1, nk);
     int orow[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -229,14 +247,17 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
     }
     wave_sync();
   };
-  uint4 ka[KS], kb[KS];
+  uint4 k0[KS], k1[KS], k2[KS];
   if (nit > 0) {
-    // the first item is peeled so that both ways into the loop end with a tile request followed by stores
-    kload(0, ka);
-    item(0, ka, kb);
-    for (int i = 1; i < nit; i += 2) {
-      item(i, kb, ka);
-      item(i + 1, ka, kb);
+    // three register sets in rotation; the first item is peeled so that every way into the loop ends with a
+    // tile request followed by stores
+    kload(0, k0);
+    kload(nit > 1 ? 1 : 0, k1);
+    item(0, k0, k2);
+    for (int i = 1; i < nit; i += 3) {
+      item(i, k1, k0);
+      item(i + 1, k2, k1);
+      item(i + 2, k0, k2);
     }
   }
 }
@@ -258,7 +279,8 @@ int ta::gather_blocks_mfma(const void* q, const void* K, int dtype, int64_t qsb,
   if (N == 0) return TA_OK;
   hipStream_t st = (hipStream_t)stream;
   const int nblocks = M / block;
-  const int ntp = (N + kGpQ - 1) / kGpQ;
+  const int qpw = D == 64 ? GpShape<64>::Q : GpShape<128>::Q;
+  const int ntp = (N + qpw - 1) / qpw;
   const int64_t nwp = (int64_t)ntp * B * H;
   if (nwp > 0x7fffffff) return TA_ERR_UNSUPPORTED;
 #define TA_GP(T, DD, BL)                                                                                        \
