@@ -133,8 +133,9 @@ int ta_gather_dot(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t 
 /*
  * Leaf-block gather-dot: the candidates of a query are whole blocks of `block` consecutive rows,
  * out[b,h,n, c*block + j] = scale * q[b,h,n] . K[b,h, blk[b,h,n,c]*block + j] (fastseg.py:118-130 with
- * cand = blk*block + arange(block)).  blk: (B,H,N,NB) int32 contiguous, ids in [0, M/block) (ids outside
- * are clamped to that range).  Same dtype for q and K; out (B,H,N,NB*block) float32 contiguous.
+ * cand = blk*block + arange(block)).  blk: (B,H,N,NB) int32 contiguous, ids in [0, M/block); as in the
+ * reference every key position is clamped into [0, M) (fastseg.py:121), so an id below 0 scores row 0 for all
+ * its keys and an id at or past M/block row M - 1.  Same dtype for q and K; out (B,H,N,NB*block) float32 contiguous.
  * For bf16/f16 with D in {64, 128}, block in {32, 64, 128}, M a multiple of block, NB <= 64 and 16-byte
  * aligned rows, the scores come from matrix-core products of the exact bf16/f16 values with float32
  * accumulation (a few ulps from a sequential float32 sum); other shapes use the canonical order of

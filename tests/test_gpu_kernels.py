@@ -140,6 +140,42 @@ def test_gather_dot_blocks(T, D, NB, blk, dtype, N):
         assert (got - want).abs().max().item() <= 2e-5 * max(1.0, want.abs().max().item())
 
 
+@pytest.mark.parametrize('T,D,NB,blk,dtype,N', [(512, 64, 16, 64, torch.bfloat16, 700), (1024, 128, 8, 32, torch.float16, 130),
+                                               (512, 16, 4, 64, torch.bfloat16, 40)])
+def test_gather_dot_blocks_clamps_key_positions(T, D, NB, blk, dtype, N):
+    """Block ids outside [0, T/blk): every key position is clamped into [0, T) as the reference's
+    cand.clamp(0, M - 1) does (fastseg.py:121) -- a negative id scores row 0 for all of its keys, an id past the
+    end row T - 1 -- on the matrix-core path and the canonical one (D=16) alike."""
+    B, H = 2, 3
+    q = rnd(B, H, N, D, seed=40, dtype=dtype)
+    Km = rnd(B, H, T, D, seed=41, dtype=dtype)
+    g = torch.Generator().manual_seed(42)
+    nblk = T // blk
+    idx = torch.randint(-3, nblk + 3, (B, H, N, NB), generator=g, dtype=torch.int32)
+    idx[0, 0, 0] = -1
+    idx[0, 0, 1] = nblk
+    got = K.gather_dot_blocks(q.to(DEV), Km.to(DEV), idx.to(DEV), blk).cpu()
+    want = o_gather_blocks(q, Km, idx, blk)
+    assert (want[0, 0, 0, :blk] == want[0, 0, 0, 0]).all()   # the oracle's clamp: all keys of id -1 are row 0
+    if D == 16:
+        assert torch.equal(got, want)
+    else:
+        assert (got - want).abs().max().item() <= 2e-5 * max(1.0, want.abs().max().item())
+
+
+def test_gather_dot_blocks_most_blocks():
+    """8192 blocks per (b, h), the most the matrix-core path's counts hold: ids over the whole range."""
+    B, H, T, D, NB, blk, N = 1, 2, 8192 * 32, 64, 16, 32, 600
+    q = rnd(B, H, N, D, seed=43, dtype=torch.bfloat16)
+    Km = rnd(B, H, T, D, seed=44, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(45)
+    idx = torch.randint(0, T // blk, (B, H, N, NB), generator=g, dtype=torch.int32)
+    idx[0, 0, :, 0] = T // blk - 1
+    got = K.gather_dot_blocks(q.to(DEV), Km.to(DEV), idx.to(DEV), blk).cpu()
+    want = o_gather_blocks(q, Km, idx, blk)
+    assert (got - want).abs().max().item() <= 2e-5 * max(1.0, want.abs().max().item())
+
+
 @pytest.mark.parametrize('dtype,D', [(torch.float32, 64), (torch.bfloat16, 64), (torch.bfloat16, 128),
                                      (torch.float32, 16)])
 def test_sparse_attn_matches_oracle(dtype, D):

@@ -34,7 +34,7 @@ typedef _Float16 f16x8_g __attribute__((ext_vector_type(8)));
 typedef float f32x16_g __attribute__((ext_vector_type(16)));
 typedef unsigned int gd_u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kGdMaxBlocks = 8192;      // blocks per (b, h) (M / block): the per-block counts fit the LDS union
+constexpr int kGdMaxBlocks = 8192;      // blocks per (b, h) (M / block): the per-block counts (+2) fit the LDS union
 constexpr int kGdMaxSlots = 16;         // selected blocks per query
 
 template <typename T>
@@ -73,12 +73,12 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   constexpr int Q = GpShape<D>::Q, MaxPairs = GpShape<D>::MaxPairs;
   constexpr int KS = D / 16;         // MFMA k-steps
   constexpr int KT = BLOCK / 32;     // 32-key tiles per block
-  constexpr int kUnion = (kGdMaxBlocks > kGpWaves * kGpStage ? kGdMaxBlocks : kGpWaves * kGpStage);
+  constexpr int kUnion = (kGdMaxBlocks + 2 > kGpWaves * kGpStage ? kGdMaxBlocks + 2 : kGpWaves * kGpStage);
   static_assert(MaxPairs % kGpThreads == 0, "pairs per thread");
   // counts / offsets per block during the sort, then the wavefronts' staging tiles
   __shared__ __attribute__((aligned(16))) uint32_t uni[kUnion];
   __shared__ uint16_t plist[MaxPairs];      // (query << 4 | slot), grouped by block
-  __shared__ uint32_t chunk[MaxPairs];      // block << 18 | start << 5 | (count - 1)
+  __shared__ uint32_t chunk[MaxPairs];      // list << 18 | start << 5 | (count - 1)
   __shared__ uint32_t wsum[kGpWaves];
   __shared__ uint32_t s_tot;
   __shared__ __attribute__((aligned(16))) T qs[Q * (D + 8)];   // the workgroup's query rows
@@ -104,8 +104,11 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
       *reinterpret_cast<uint4*>(qs + r * (D + 8) + 8 * cc) = ldg16(qb0 + (int64_t)r * qsn + 8 * cc);
     }
   }
-  // 1. counts per block (ids clamped into [0, nblocks - 1])
-  for (int i = tid; i < nblocks; i += kGpThreads) uni[i] = 0u;
+  // 1. counts per block.  The reference clamps every key position into [0, M - 1] (cand = blk * block + j,
+  // fastseg.py:121): a negative id's keys are all row 0 and an id past the end all row M - 1, so those pairs go
+  // to two extra lists, nblocks and nblocks + 1
+  const int nlist = nblocks + 2;
+  for (int i = tid; i < nlist; i += kGpThreads) uni[i] = 0u;
   __syncthreads();
   constexpr int PPT = MaxPairs / kGpThreads;
   int pid[PPT];
@@ -116,19 +119,19 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
     int v = -1;
     if (pi < npairs) {
       v = brow[pi];
-      v = v < 0 ? 0 : (v >= nblocks ? nblocks - 1 : v);
+      v = v < 0 ? nblocks : (v >= nblocks ? nblocks + 1 : v);
       atomicAdd(&uni[v], 1u);
     }
     pid[k] = v;
   }
   __syncthreads();
   // 2. one scan over the blocks of (chunks << 16 | count): each thread takes E consecutive blocks
-  const int E = (nblocks + kGpThreads - 1) / kGpThreads;
+  const int E = (nlist + kGpThreads - 1) / kGpThreads;
   const int j0 = tid * E;
   uint32_t loc = 0;
   for (int e = 0; e < E; ++e) {
     const int j = j0 + e;
-    if (j < nblocks) {
+    if (j < nlist) {
       const uint32_t c = uni[j];
       loc += (((c + 31u) >> 5) << 16) | c;
     }
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   uint32_t run = wpre + inc - loc;    // exclusive prefix of this thread's first block
   for (int e = 0; e < E; ++e) {
     const int j = j0 + e;
-    if (j < nblocks) {
+    if (j < nlist) {
       const uint32_t c = uni[j];
       const uint32_t st = run & 0xffffu, cs = run >> 16;
       for (uint32_t k = 0; 32u * k < c; ++k) {
@@ -198,7 +201,8 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
     const int cc = item_chunk(i), kt = item_kt(i);
     const int c = cc < c1 ? cc : c1 - 1;
     const int j = (int)(chunk[c] >> 18);
-    const T* kr = kbase + ((int64_t)j * BLOCK + 32 * kt + p) * ksn;
+    const int64_t row = j < nblocks ? (int64_t)j * BLOCK + 32 * kt + p : (j == nblocks ? 0 : (int64_t)nblocks * BLOCK - 1);
+    const T* kr = kbase + row * ksn;
 #pragma unroll
     for (int s = 0; s < KS; ++s) kk[s] = ldg16(kr + 16 * s);
   };
