@@ -6,20 +6,19 @@
 //
 //  * Set-up: the workgroup's query rows are copied into LDS; its pairs (at most Q * 16) are sorted by block
 //    id with a counting sort in LDS (a count per block, one scan giving each block its list offset and its
-//    number of 32-pair chunks, then each pair placed with an LDS atomic).  A chunk is up to 32 pairs that
-//    selected the same block; an item is a chunk and one 32-key tile of its block.
-//  * The wavefronts take contiguous runs of chunks, in groups of four consecutive chunks: for each key tile of
-//    the group the group's chunks come back to back, so the chunks of one block (neighbours in the sorted list)
-//    request the same tile one item after another and the repeats are served close to the CU.  For an item a
-//    wavefront reads its pairs' query rows from LDS as the MFMA B operand and the key tile from global memory
-//    (the head's keys stay in the XCD's L2) as the A operand, and computes S^T = K_tile . Q^T with
-//    v_mfma_f32_32x32x16: lane (p, hh) holds keys 8 i + 4 hh + r of pair p.  The 32 x 32 scores pass through
-//    the wavefront's own LDS tile so that each store instruction writes eight pairs' 128-byte runs of
-//    consecutive keys (whole lines).
+//    number of chunks, then each pair placed with an LDS atomic).  A chunk is up to 128 pairs that selected the
+//    same block; an item is a chunk and one 32-key tile of its block.
+//  * The wavefronts take contiguous runs of chunks.  For an item a wavefront requests the key tile once (from
+//    global memory; the head's keys stay in the XCD's L2) as the MFMA A operand and runs the chunk's 32-pair
+//    sub-chunks against it: their query rows from LDS as the B operand, S^T = K_tile . Q^T with
+//    v_mfma_f32_32x32x16 (lane (p, hh) holds keys 8 i + 4 hh + r of pair p).  One tile read serving up to 128
+//    pairs is what keeps the L2 traffic of the tiles well below the scores' (a 32-pair chunk read a 4 KB tile
+//    for 4 KB of scores).  The 32 x 32 scores pass through the wavefront's own LDS tile so that each store
+//    instruction writes eight pairs' 128-byte runs of consecutive keys (whole lines).
 //  * The key tile of item i + 2 is requested before item i's stores, with three register sets in rotation
 //    (the loop runs three items per pass): the vector-memory counter counts stores too, so a wait for a key tile
 //    then covers only stores issued at least two items earlier, and the stores drain while later items compute.
-//    Stores go through a buffer resource over the workgroup's output rows; lanes past a chunk's count get an
+//    Stores go through a buffer resource over the workgroup's output rows; lanes past a sub-chunk's count get an
 //    offset past its end, which the hardware drops, so every store is issued unconditionally.
 //
 // The products of bf16 / f16 values are exact in float32 and the sum over D is taken by the MFMA, so scores
@@ -78,7 +77,7 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   // counts / offsets per block during the sort, then the wavefronts' staging tiles
   __shared__ __attribute__((aligned(16))) uint32_t uni[kUnion];
   __shared__ uint16_t plist[MaxPairs];      // (query << 4 | slot), grouped by block
-  __shared__ uint32_t chunk[MaxPairs];      // list << 18 | start << 5 | (count - 1)
+  __shared__ uint32_t chunk[MaxPairs];      // list << 18 | start << 5 (the count: up to the next start)
   __shared__ uint32_t wsum[kGpWaves];
   __shared__ uint32_t s_tot;
   __shared__ __attribute__((aligned(16))) T qs[Q * (D + 8)];   // the workgroup's query rows
@@ -133,7 +132,7 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
     const int j = j0 + e;
     if (j < nlist) {
       const uint32_t c = uni[j];
-      loc += (((c + 31u) >> 5) << 16) | c;
+      loc += (((c + 127u) >> 7) << 16) | c;
     }
   }
   uint32_t inc = loc;
@@ -157,12 +156,9 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
     if (j < nlist) {
       const uint32_t c = uni[j];
       const uint32_t st = run & 0xffffu, cs = run >> 16;
-      for (uint32_t k = 0; 32u * k < c; ++k) {
-        const uint32_t cnt = c - 32u * k < 32u ? c - 32u * k : 32u;
-        chunk[cs + k] = ((uint32_t)j << 18) | ((st + 32u * k) << 5) | (cnt - 1u);
-      }
+      for (uint32_t k = 0; 128u * k < c; ++k) chunk[cs + k] = ((uint32_t)j << 18) | ((st + 128u * k) << 5);
       uni[j] = st;    // becomes the running fill position
-      run += (((c + 31u) >> 5) << 16) | c;
+      run += (((c + 127u) >> 7) << 16) | c;
     }
   }
   if (tid == 0) s_tot = tot;
@@ -189,14 +185,12 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   // offset past the end, which the hardware drops, so every store is issued unconditionally
   const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(obase, 0, nq * NB * BLOCK * 4, 0x00020000);
   const int rP = lane >> 3, rc = lane & 7;
-  const int nch2 = ((c1 - c0) + 3) & ~3;   // chunks rounded up to groups of four
-  const int nit = nch2 * KT;
-  // item i -> (chunk, key tile): groups of four consecutive chunks, key tile kt, the group's chunks back to back,
-  // so the chunks of one block (consecutive in the block-sorted list) request the same tile one item apart
-  auto item_chunk = [&](int i) { return c0 + 4 * (i / (4 * KT)) + (i & 3); };
-  auto item_kt = [&](int i) { return (i >> 2) % KT; };
-  // item i = (chunk c0 + i / KT, key tile i % KT); its K tile is requested one item ahead, before the
-  // current item's stores, so no wait for a K tile covers stores that were issued after it
+  // item i = (chunk c0 + i / KT, key tile i % KT); a chunk's pairs run from its start to the next chunk's (the
+  // chunks partition the block-sorted list in order)
+  const int nit = (c1 - c0) * KT;
+  auto item_chunk = [&](int i) { return c0 + i / KT; };
+  auto item_kt = [&](int i) { return i % KT; };
+  auto cstart = [&](int c) { return c < nchunk ? (int)((chunk[c] >> 5) & 0x1fffu) : npairs; };
   auto kload = [&](int i, uint4 (&kk)[KS]) {
     const int cc = item_chunk(i), kt = item_kt(i);
     const int c = cc < c1 ? cc : c1 - 1;
@@ -211,45 +205,53 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   // whose stores are all dropped), so no register copy waits for a load issued in the same pass
   // item i with its key tile in ck; the key tile of item i + 2 is requested into nk before this item's stores, so
   // a wait for a tile covers only stores issued at least two items earlier
+  // item i from its key tile in ck: the chunk's pairs in 32-pair sub-chunks, each scored, transposed and stored;
+  // the key tile of item i + 2 is requested into nk first
   auto item = [&](int i, const uint4 (&ck)[KS], uint4 (&nk)[KS]) {
     const int iv = i < nit ? i : nit - 1;
     const int cc = item_chunk(iv), kt = item_kt(iv);
     const int c = cc < c1 ? cc : c1 - 1;
-    const uint32_t ce = chunk[c];
-    const int st = (int)((ce >> 5) & 0x1fffu), cnt = (i < nit && cc < c1) ? (int)(ce & 31u) + 1 : 0;
-    const int code = plist[st + (p < cnt ? p : 0)];
-    const uint4* qr = reinterpret_cast<const uint4*>(qs + (code >> 4) * (D + 8)) + hh;
-    uint4 qb[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qb[s] = qr[2 * s];
-    f32x16_g acc;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) acc = mfma32<T>(ck[s], qb[s], acc);
+    const int st = cstart(c);
+    const int cnt = (i < nit && cc < c1) ? cstart(c + 1) - st : 0;
     kload(iv + 2 < nit ? iv + 2 : nit - 1, nk);
-    int orow[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int P = 8 * u + rP;
-      const int cd = plist[st + (P < cnt ? P : 0)];
-      const int o = (((cd >> 4) * NB + (cd & 15)) * BLOCK + 4 * rc + 32 * kt) * 4;
-      orow[u] = P < cnt ? o : 0x7fffff00;
-    }
+    for (int sb = 0; sb < 4; ++sb) {
+      const int sc = cnt - 32 * sb < 0 ? 0 : (cnt - 32 * sb > 32 ? 32 : cnt - 32 * sb);
+      if (sb > 0 && sc == 0) continue;   // past the chunk's pairs
+      const int s0 = sc > 0 ? st + 32 * sb : st;
+      const int code = plist[s0 + (p < sc ? p : 0)];
+      const uint4* qr = reinterpret_cast<const uint4*>(qs + (code >> 4) * (D + 8)) + hh;
+      uint4 qb[KS];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const float4 v = make_float4(acc[4 * a] * scale, acc[4 * a + 1] * scale, acc[4 * a + 2] * scale,
-                                   acc[4 * a + 3] * scale);
-      *reinterpret_cast<float4*>(stg + p * kGpRow + 8 * a + 4 * hh) = v;
-    }
-    wave_sync();
+      for (int s = 0; s < KS; ++s) qb[s] = qr[2 * s];
+      f32x16_g acc;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float4 v = *reinterpret_cast<const float4*>(stg + (8 * u + rP) * kGpRow + 4 * rc);
-      gd_u32x4 vv = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
-      __builtin_amdgcn_raw_buffer_store_b128(vv, orsrc, orow[u], 0, 0);
+      for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) acc = mfma32<T>(ck[s], qb[s], acc);
+      int orow[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int P = 8 * u + rP;
+        const int cd = plist[s0 + (P < sc ? P : 0)];
+        const int o = (((cd >> 4) * NB + (cd & 15)) * BLOCK + 4 * rc + 32 * kt) * 4;
+        orow[u] = P < sc ? o : 0x7fffff00;
+      }
+#pragma unroll
+      for (int a2 = 0; a2 < 4; ++a2) {
+        const float4 v = make_float4(acc[4 * a2] * scale, acc[4 * a2 + 1] * scale, acc[4 * a2 + 2] * scale,
+                                     acc[4 * a2 + 3] * scale);
+        *reinterpret_cast<float4*>(stg + p * kGpRow + 8 * a2 + 4 * hh) = v;
+      }
+      wave_sync();
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 v = *reinterpret_cast<const float4*>(stg + (8 * u + rP) * kGpRow + 4 * rc);
+        gd_u32x4 vv = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+        __builtin_amdgcn_raw_buffer_store_b128(vv, orsrc, orow[u], 0, 0);
+      }
+      wave_sync();
     }
-    wave_sync();
   };
   uint4 k0[KS], k1[KS], k2[KS];
   if (nit > 0) {
