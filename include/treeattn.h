@@ -453,6 +453,17 @@ int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64
                      int32_t* n_tree, void* stream);
 
 /*
+ * The decode step's neighbour store (replaces the assignments of engine.py:103-105): for every (b, h) and slot
+ * r < n, at position t = t_pos[b] (skipped outside [0, Tst)): st_leaf[b,h,t,r] = ids[b,h,0,r] (an invalid slot's
+ * -1 stored as 0), st_score = sct when vld else 0, st_ok = vld.  ids int32 / vld uint8 / sct float32 are the
+ * descent's (B, H, 1, wl) contiguous outputs; st_leaf int32 / st_score float32 / st_ok uint8 (B, H, Tst, nb_store)
+ * share the element strides st_sb, st_sh, st_st; n <= wl.
+ */
+int ta_leaf_store(const int32_t* ids, const uint8_t* vld, const float* sct, int B, int H, int wl, int n,
+                  const int32_t* t_pos, int32_t* st_leaf, float* st_score, uint8_t* st_ok, int64_t st_sb,
+                  int64_t st_sh, int64_t st_st, int Tst, void* stream);
+
+/*
  * Log-magnitude pyramid for the mean-log gate (seg.py:33, 39; engine.py:47, 53-54): ta_level_sums over the
  * values log(|x| + 1e-6) of the index keys x (position 0 counted as 0 when zero_sink) instead of the keys --
  * each log the float32 rounding of the double-precision log of the float32 |x| + 1e-6 -- with the same

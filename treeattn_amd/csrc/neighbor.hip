@@ -122,9 +122,53 @@ __global__ __launch_bounds__(256) void neighbor_kernel(NbParams p) {
   }
 }
 
+// ----------------------------------------------------------------------------------------- leaf store
+// The decode step's store of position t's top n leaves for the next positions' neighbour pass (engine.py:103-105):
+// st_leaf[b, h, t, r] = the leaf id (an invalid slot's -1 as 0), st_score = its score (0 when invalid), st_ok =
+// valid, for r < n.  One thread per (b, h, r); a position outside [0, Tst) is skipped.
+__global__ __launch_bounds__(256) void leaf_store_kernel(const int32_t* __restrict__ ids, const uint8_t* __restrict__ vld,
+                                                         const float* __restrict__ sct, int H, int wl, int n,
+                                                         const int32_t* __restrict__ t_pos, int32_t* __restrict__ st_leaf,
+                                                         float* __restrict__ st_score, uint8_t* __restrict__ st_ok,
+                                                         int64_t st_sb, int64_t st_sh, int64_t st_st, int Tst,
+                                                         int total) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int bh = i / n, r = i - bh * n;
+  const int b = bh / H, h = bh - b * H;
+  const int t = t_pos[b];
+  if (t < 0 || t >= Tst) return;
+  const int64_t src = (int64_t)bh * wl + r;
+  const int64_t dst = b * st_sb + h * st_sh + (int64_t)t * st_st + r;
+  const bool ok = vld[src] != 0;
+  const int id = ids[src];
+  st_leaf[dst] = id < 0 ? 0 : id;
+  st_score[dst] = ok ? sct[src] : 0.0f;
+  st_ok[dst] = ok ? 1 : 0;
+}
+
 }  // namespace ta
 
 using namespace ta;
+
+extern "C" int ta_leaf_store(const int32_t* ids, const uint8_t* vld, const float* sct, int B, int H, int wl, int n,
+                             const int32_t* t_pos, int32_t* st_leaf, float* st_score, uint8_t* st_ok, int64_t st_sb,
+                             int64_t st_sh, int64_t st_st, int Tst, void* stream) {
+  if (B <= 0 || H <= 0 || wl < 0 || n < 0 || n > wl || Tst <= 0 || ids == nullptr || vld == nullptr ||
+      sct == nullptr || t_pos == nullptr || st_leaf == nullptr || st_score == nullptr || st_ok == nullptr) {
+    set_error("ta_leaf_store: bad arguments (0 <= n <= wl)");
+    return TA_ERR_ARG;
+  }
+  const int64_t total = (int64_t)B * H * n;
+  if (total == 0) return TA_OK;
+  if (total > 0x7fffffff) {
+    set_error("ta_leaf_store: too many slots");
+    return TA_ERR_ARG;
+  }
+  hipLaunchKernelGGL(leaf_store_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, ids,
+                     vld, sct, H, wl, n, t_pos, st_leaf, st_score, st_ok, st_sb, st_sh, st_st, Tst, (int)total);
+  return check_launch("leaf_store_kernel");
+}
 
 extern "C" int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const float* S0,
                                 int64_t ssb, int64_t ssh, int M, const int32_t* st_leaf, const float* st_score,

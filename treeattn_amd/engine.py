@@ -257,6 +257,7 @@ class _Scratch:
         self.keys_all = torch.zeros(n_layer, B, H, 1, device=dev)
         self.keys = self.keys_all[0]
         self.n_tree = None
+        self.lhat = None        # the fixed budget of every (sequence, head), when no budget head picks it
         self.nsplit = nsplit
         self.ws = K.seg_attn_workspace(B, H, 1, dh, nsplit, dev)
         self.mm_ws = None
@@ -387,7 +388,9 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     # n_tree tree leaves and the matched neighbour leaves, each block once, with the own block and static keys
     # (engine.py:107-119).
     if lhat is None:
-        lhat = torch.full((B, H, 1), cfg.beam, dtype=torch.long, device=q.device)
+        if scratch.lhat is None:
+            scratch.lhat = torch.full((B, H, 1), cfg.beam, dtype=torch.long, device=q.device)
+        lhat = scratch.lhat
     NS = cfg.nb_store
     if state.shape.n_levels:
         nid, match, nL, n_tree = K.neighbor_pass(q, state.score_levels[0], state.st_leaf, state.st_score, state.st_ok,
@@ -398,19 +401,12 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         match = torch.zeros_like(nid, dtype=torch.bool)
         n_tree = SEL.budget_split(torch.zeros_like(lhat.view(B, H, 1)), lhat.view(B, H, 1), cfg.wmax).to(torch.int32)
     if update:
-        n = min(NS, wl)
-        bidx = torch.arange(B, device=q.device).view(B, 1)
-        hidx = torch.arange(H, device=q.device).view(1, H)
-        tt = tpos.long().view(B, 1)
-        vb = vld.bool()
-        state.st_leaf[bidx, hidx, tt, :n] = ids[:, :, 0, :n].clamp(min=0)
-        state.st_score[bidx, hidx, tt, :n] = torch.where(vb[:, :, 0, :n], sct[:, :, 0, :n],
-                                                         torch.zeros_like(sct[:, :, 0, :n]))
-        state.st_ok[bidx, hidx, tt, :n] = vb[:, :, 0, :n]
+        K.leaf_store(ids, vld, sct, tpos, state.st_leaf, state.st_score, state.st_ok, min(NS, wl))
         if not appendable:
             K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
             state.gate_append(tpos)
-        state.ksum += k[:, :, 0].float()
+        if cfg.global_pool:
+            state.ksum += k[:, :, 0].float()
     out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
     K.seg_attn(q, Kc, Vc, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out, keys=scratch.keys,
                nsplit=scratch.nsplit, ws=scratch.ws, nb=(nid, match))

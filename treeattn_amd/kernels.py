@@ -285,6 +285,26 @@ def gather_dot(q, S, cand, scale):
     return out
 
 
+def leaf_store(ids, vld, sct, t_pos, st_leaf, st_score, st_ok, n):
+    """The decode step's neighbour store (engine.py:103-105): the first n leaves of each (b, h)'s selection
+    (ids int32 / vld uint8 / sct float32, (B,H,1,wl) contiguous) into row t_pos[b] of st_leaf / st_score / st_ok
+    ((B,H,Tst,NS) contiguous int32 / float32 / bool); an invalid slot's id is stored as 0 and its score as 0."""
+    L.require_gpu(ids, vld, sct, t_pos, st_leaf, st_score, st_ok)
+    B, H, _, wl = ids.shape
+    if not (ids.is_contiguous() and vld.is_contiguous() and sct.is_contiguous() and ids.dtype == torch.int32
+            and vld.dtype == torch.uint8 and sct.dtype == torch.float32):
+        raise ValueError('leaf_store: ids int32, vld uint8, sct float32, contiguous')
+    if not (st_leaf.is_contiguous() and st_score.is_contiguous() and st_ok.is_contiguous()
+            and st_leaf.dtype == torch.int32 and st_score.dtype == torch.float32 and st_ok.dtype == torch.bool
+            and st_leaf.shape == st_score.shape == st_ok.shape):
+        raise ValueError('leaf_store: st_leaf int32, st_score float32, st_ok bool, contiguous, one shape')
+    if t_pos.dtype != torch.int32 or not t_pos.is_contiguous() or t_pos.numel() != B:
+        raise ValueError('leaf_store: t_pos contiguous int32 (B,)')
+    Tst = st_leaf.shape[2]
+    L.call('ta_leaf_store', L.ptr(ids), L.ptr(vld), L.ptr(sct), B, H, wl, int(n), L.ptr(t_pos), L.ptr(st_leaf),
+           L.ptr(st_score), L.ptr(st_ok), st_leaf.stride(0), st_leaf.stride(1), st_leaf.stride(2), Tst, L.stream())
+
+
 def neighbor_pass(q, S0, st_leaf, st_score, st_ok, tq, cfg, leaf, lhat=None):
     """Neighbour borrowing (ta_neighbor_pass; seg.py:73-103, with lhat also seg.py:111-117's budget split).
     q (b,H,Nq,D); S0 leaf-level node sums (b,H,M,D) float32; st_leaf int32 / st_score float32 / st_ok bool
