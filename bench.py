@@ -54,6 +54,10 @@ def parse():
     ap.add_argument('--neighbors', action='store_true',
                     help='configs 4/5: decode in the reference-default selection mode (neighbour borrowing on); '
                          'reports the step rate only')
+    ap.add_argument('--production', action='store_true',
+                    help='configs 4/5: decode in the reference author\'s training configuration (long_train.py:86-88: '
+                         'budget head with the global pool, mean-log gate from level 6, neighbour borrowing); '
+                         'reports the step rate only')
     ap.add_argument('--no-gather-dot', action='store_true', help='skip the isolated gather-dot leg')
     ap.add_argument('--kernel-iters', type=int, default=50)
     ap.add_argument('--kv-layout', choices=('paged', 'contiguous'), default='paged',
@@ -339,6 +343,10 @@ def decode_bench(args):
     cfg = Config(vocab_size=args.vocab, seq_len=Tcap, n_layer=args.layers, n_head=H, n_embd=C, attn='seg',
                  wmax=args.topk, beam=args.topk, beam_mode='fixed', neighbors=bool(args.neighbors), leaf=args.leaf,
                  arity=args.arity, local=3)
+    if args.production:
+        args.neighbors = True
+        cfg.neighbors, cfg.beam_mode, cfg.global_pool = True, 'pred', True
+        cfg.gate, cfg.gate_min_level = True, 6
     log('init model (seed 3)')
     W = build_model(cfg, 3, torch.bfloat16)
     g = torch.Generator().manual_seed(args.ids_seed)
@@ -358,7 +366,7 @@ def decode_bench(args):
     t0 = time.perf_counter()
     if args.neighbors:
         # the prompt is filled without neighbour borrowing (its candidate lists at 32k positions would take tens
-        # of GB per sequence); the neighbour store then fills from the decode steps (warm-up >= nb_window)
+        # of GB per sequence); its tree passes still seed the neighbour store the decode steps read
         cfg.neighbors = False
         logits = dec.prefill(idx.cuda(), chunk=args.prefill_chunk)
         cfg.neighbors = True
@@ -383,15 +391,20 @@ def decode_bench(args):
     t_now = T0 + args.warmup + args.steps
     log('%.3f ms/step, %.0f tokens/s' % (ms_step, value))
     if args.neighbors:
-        return {'metric': 'sparse-attn decode tokens/s @bs%dx%d, reference-default selection (neighbour borrowing '
-                          'on)' % (B, T0), 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1,
+        mode = ('the reference author\'s training configuration (budget head with the global pool, mean-log gate '
+                'from level 6, neighbour borrowing)' if args.production else
+                'reference-default selection (neighbour borrowing on)')
+        return {'metric': 'sparse-attn decode tokens/s @bs%dx%d, %s' % (B, T0, mode), 'value': round(value, 1),
+                'unit': 'tokens/s', 'n_gpus': 1,
                 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(ms_step, 4),
                 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16',
                 'data': 'synthetic (random-init weights seed 3, uniform random token ids seed %d)' % args.ids_seed,
                 'config': {'workload': 'config %d model and cache, neighbours on (nb_window %d, nb_store %d), leaf %d, '
-                                       'wmax = beam = %d; prompt filled without borrowing, the store from the %d '
-                                       'warm-up steps' % (args.config, cfg.nb_window, cfg.nb_store, args.leaf,
-                                                          args.topk, args.warmup),
+                                       'wmax %d, %s; prompt filled without borrowing (its tree passes seed the '
+                                       'neighbour store)' % (args.config, cfg.nb_window, cfg.nb_store, args.leaf,
+                                                             args.topk, 'budget classes %s, gate from level %d' % (
+                                                                 list(cfg.beam_classes), cfg.gate_min_level)
+                                                             if args.production else 'beam %d' % cfg.beam),
                            'batch': B, 'context': T0},
                 'roofline': None, 'cpu_baseline': None}
 

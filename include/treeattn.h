@@ -453,6 +453,20 @@ int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64
                      int32_t* n_tree, void* stream);
 
 /*
+ * The decode step's budget head (replaces the feature / linear / argmax sequence of engine.py:89-96) for every
+ * (b, h): features f = [q (D), log(|q| + 1e-6), one-hot(h) (H)] plus, when ksum is given, ksum[b,h] / max(t_pos[b],
+ * 1) (D); lhat[b*H + h] = classes[argmax(W2 relu(W1 f + b1) + b2)], float32 throughout, the first maximum winning.
+ * q (B, H, D) rows of q_dtype at element strides qsb, qsh; ksum float32 (B, H, D) contiguous or null; with k (same
+ * dtype as q, strides ksb, ksh) the key sum then takes this step's key (ksum += k).  w1t is W1 transposed,
+ * float32 (F, hid) row-major with F = D + 1 + H (+ D with ksum); w2 float32 (ncls, hid); hid <= 256,
+ * ncls <= 64, 2 D + 1 + H <= 1024, (F + ncls) * hid <= 24576.
+ */
+int ta_budget_head(const void* q, int q_dtype, int64_t qsb, int64_t qsh, float* ksum, const void* k, int64_t ksb,
+                   int64_t ksh, const int32_t* t_pos, const float* w1t, const float* b1, const float* w2,
+                   const float* b2, const int32_t* classes, int B, int H, int D, int hid, int ncls, int32_t* lhat,
+                   void* stream);
+
+/*
  * The decode step's neighbour store (replaces the assignments of engine.py:103-105): for every (b, h) and slot
  * r < n, at position t = t_pos[b] (skipped outside [0, Tst)): st_leaf[b,h,t,r] = ids[b,h,0,r] (an invalid slot's
  * -1 stored as 0), st_score = sct when vld else 0, st_ok = vld.  ids int32 / vld uint8 / sct float32 are the

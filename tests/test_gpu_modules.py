@@ -171,6 +171,53 @@ def test_engine_matches_forward(kw):
     assert (ref - got).abs().max().item() < 1e-4
 
 
+@pytest.mark.parametrize('dtype,D,H,hid,ncls,pool', [(torch.bfloat16, 64, 12, 64, 5, True),
+                                                       (torch.float32, 32, 3, 128, 7, True),
+                                                       (torch.bfloat16, 128, 4, 30, 3, False)])
+def test_budget_head_kernel_matches_oracle(dtype, D, H, hid, ncls, pool):
+    """ta_budget_head against the oracle decoder's budget head (engine.py:89-96, float32 on the CPU) for every
+    (sequence, head), positions 0 (the pool's max(t, 1)) and beyond; the key sum afterwards holds ksum + k.  A
+    budget may differ only where the two best logits are within 1e-4 (summation order)."""
+    import types
+    from oracle.engine_ref import budget as ref_budget
+    B = 6
+    F_ = D + 1 + H + (D if pool else 0)
+    g = torch.Generator().manual_seed(D + H + hid)
+    w1 = torch.randn(hid, F_, generator=g) / math.sqrt(F_)
+    b1 = torch.randn(hid, generator=g) * 0.1
+    w2 = torch.randn(ncls, hid, generator=g) / math.sqrt(hid)
+    b2 = torch.randn(ncls, generator=g) * 0.1
+    classes = torch.tensor([2 + 3 * c for c in range(ncls)])
+    q = torch.randn(B, H, D, generator=g).to(dtype)
+    k = torch.randn(B, H, D, generator=g).to(dtype)
+    ksum = torch.randn(B, H, D, generator=g) * 20
+    t = torch.tensor([0, 1, 2, 17, 300, 4095], dtype=torch.int32)
+    cfg = types.SimpleNamespace(beam_mode='pred', global_pool=pool)
+    pw = dict(w1=w1, b1=b1, w2=w2, b2=b2, classes=classes)
+    ks_dev = ksum.clone().to(DEV)
+    got = K.budget_head(q.to(DEV), t.to(DEV), w1.t().contiguous().to(DEV), b1.to(DEV), w2.to(DEV), b2.to(DEV),
+                        classes.to(torch.int32).to(DEV), ksum=ks_dev if pool else None,
+                        k=k.to(DEV) if pool else None).cpu()
+    torch.cuda.synchronize()
+    bad = 0
+    for b in range(B):
+        st = types.SimpleNamespace(cfg=cfg, H=H, ksum=ksum[b:b + 1])
+        want = ref_budget(st, pw, q[b:b + 1].float().unsqueeze(2), int(t[b])).view(H)
+        # the logits in float64, to excuse near-ties
+        feats = [q[b].double(), torch.log(q[b].double().norm(dim=-1, keepdim=True) + 1e-6), torch.eye(H).double()]
+        if pool:
+            feats.append(ksum[b].double() / max(int(t[b]), 1))
+        lg = torch.relu(torch.cat(feats, -1) @ w1.double().t() + b1.double()) @ w2.double().t() + b2.double()
+        top = lg.topk(2, -1).values
+        for h in range(H):
+            if int(got[b, h]) != int(want[h]):
+                assert float(top[h, 0] - top[h, 1]) < 1e-4, (b, h, int(got[b, h]), int(want[h]))
+                bad += 1
+    assert bad <= 1
+    if pool:
+        assert torch.equal(ks_dev.cpu(), ksum + k.float())
+
+
 @pytest.mark.parametrize('kw', [dict(), dict(leaf=4, arity=4, wmax=3, beam=2), dict(beam_mode='pred', global_pool=True),
                                 dict(beam_mode='pred', neighbors=False, leaf=8, wmax=4)])
 def test_prefill_with_neighbours_then_decode_matches_decode_from_scratch(kw):

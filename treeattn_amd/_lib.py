@@ -126,6 +126,8 @@ SIGNATURES = {
     'ta_neighbor_pass': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp,
                                  c_i64, c_i64, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                  c_i32, c_i32, c_f32, c_i32, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    'ta_budget_head': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
     'ta_leaf_store': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                               c_i32, c_vp]),
     'ta_logits_workspace_size': (c_i64, [c_i32, c_i32]),

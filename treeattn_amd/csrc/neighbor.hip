@@ -147,6 +147,103 @@ __global__ __launch_bounds__(256) void leaf_store_kernel(const int32_t* __restri
   st_ok[dst] = ok ? 1 : 0;
 }
 
+
+// The budget head of one decode step (engine.py:89-96): per (sequence, head) the features
+//   f = [q (D), log(|q| + 1e-6), one-hot(h) (H), ksum / max(t, 1) (D, with the global pool)],
+// hidden = relu(W1 f + b1), logits = W2 hidden + b2, budget = classes[argmax logits] (the first maximum; a NaN
+// logit counts as the maximum, as torch's argmax takes it).  Everything in float32.  A workgroup of eight
+// wavefronts serves eight (b, h): it first copies the weights (W1 transposed, F x hid; W2; b1; b2) into LDS with
+// all its loads in flight, then each wavefront puts its features in its LDS row, lane j forms hidden units j,
+// j + 64, ... (consecutive LDS words across the lanes, the feature a broadcast), and each logit is a wave sum.
+// The one-hot term adds W1's column D + 1 + h, the product with the other zero features being exact zeros.
+// With `k` the running key sum then takes this step's key (ksum += k), after its read: the sum of keys
+// 0 .. t-1 feeds the head at t.
+constexpr int kBhWaves = 8, kBhMaxF = 1024, kBhMaxHid = 256, kBhMaxCls = 64, kBhMaxW = 24576;
+
+template <typename T>
+__global__ __launch_bounds__(kBhWaves * kWave) void budget_head_kernel(
+    const T* __restrict__ q, int64_t qsb, int64_t qsh, float* __restrict__ ksum, const T* __restrict__ k, int64_t ksb,
+    int64_t ksh, const int32_t* __restrict__ t_pos, const float* __restrict__ w1t, const float* __restrict__ b1,
+    const float* __restrict__ w2, const float* __restrict__ b2, const int32_t* __restrict__ classes, int B, int H,
+    int D, int F, int hid, int ncls, int32_t* __restrict__ lhat) {
+  extern __shared__ float bh_lds[];
+  const int nw = F * hid, n2 = ncls * hid;
+  float* wl = bh_lds;                                   // W1 transposed, F x hid
+  float* w2l = wl + ((nw + 3) & ~3);                    // W2, ncls x hid
+  float* b1l = w2l + n2;                                // b1 (hid), then b2 (ncls)
+  float* b2l = b1l + hid;
+  const int lane = lane_id(), w = wave_id();
+  float* f = bh_lds + ((nw + 3) & ~3) + ((n2 + hid + ncls + 3) & ~3) + w * (F + hid);
+  float* hs = f + F;                                    // this wavefront's features, then its hidden units
+  {
+    // the weights into LDS, every load issued before the first is waited for: W1 in float4 words while the
+    // size allows (hid % 4 == 0 keeps the table 16-byte aligned)
+    const int tid = threadIdx.x;
+    if ((hid & 3) == 0) {
+      const float4* src = reinterpret_cast<const float4*>(w1t);
+      float4* dst = reinterpret_cast<float4*>(wl);
+      const int n4 = nw >> 2;
+#pragma unroll 8
+      for (int i = tid; i < n4; i += kBhWaves * kWave) dst[i] = src[i];
+    } else {
+#pragma unroll 8
+      for (int i = tid; i < nw; i += kBhWaves * kWave) wl[i] = w1t[i];
+    }
+#pragma unroll 4
+    for (int i = tid; i < n2; i += kBhWaves * kWave) w2l[i] = w2[i];
+    if (tid < hid) b1l[tid] = b1[tid];
+    if (tid < ncls) b2l[tid] = b2[tid];
+  }
+  const int bh = blockIdx.x * kBhWaves + w;
+  const bool live = bh < B * H;
+  const int b = live ? bh / H : 0, h = live ? bh - b * H : 0;
+  if (live) {
+    const T* qr = q + b * qsb + h * qsh;
+    float ss = 0.0f;
+    for (int i = lane; i < D; i += kWave) {
+      const float x = to_f32(qr[i]);
+      f[i] = x;
+      ss += x * x;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) f[D] = logf(sqrtf(ss) + 1e-6f);
+    if (ksum != nullptr) {
+      const float tt = (float)max(t_pos[b], 1);
+      float* kr = ksum + (int64_t)bh * D;
+      float* fp = f + D + 1 + H;
+      for (int i = lane; i < D; i += kWave) {
+        const float s = kr[i];
+        fp[i] = s / tt;
+        if (k != nullptr) kr[i] = s + to_f32(k[b * ksb + h * ksh + i]);
+      }
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  for (int j = lane; j < hid; j += kWave) {
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int i = 0; i <= D; ++i) acc += wl[i * hid + j] * f[i];
+    acc += wl[(D + 1 + h) * hid + j];
+#pragma unroll 8
+    for (int i = D + 1 + H; i < F; ++i) acc += wl[i * hid + j] * f[i];
+    hs[j] = fmaxf(acc + b1l[j], 0.0f);
+  }
+  wave_sync();
+  int best = 0;
+  float bv = 0.0f;
+  for (int c = 0; c < ncls; ++c) {
+    float part = 0.0f;
+    for (int j = lane; j < hid; j += kWave) part += w2l[c * hid + j] * hs[j];
+    const float v = wave_sum(part) + b2l[c];
+    if (c == 0 || (!(bv != bv) && (v > bv || v != v))) {
+      best = c;
+      bv = v;
+    }
+  }
+  if (lane == 0) lhat[bh] = classes[best];
+}
+
 }  // namespace ta
 
 using namespace ta;
@@ -168,6 +265,39 @@ extern "C" int ta_leaf_store(const int32_t* ids, const uint8_t* vld, const float
   hipLaunchKernelGGL(leaf_store_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, ids,
                      vld, sct, H, wl, n, t_pos, st_leaf, st_score, st_ok, st_sb, st_sh, st_st, Tst, (int)total);
   return check_launch("leaf_store_kernel");
+}
+
+extern "C" int ta_budget_head(const void* q, int q_dtype, int64_t qsb, int64_t qsh, float* ksum, const void* k,
+                              int64_t ksb, int64_t ksh, const int32_t* t_pos, const float* w1t, const float* b1,
+                              const float* w2, const float* b2, const int32_t* classes, int B, int H, int D, int hid,
+                              int ncls, int32_t* lhat, void* stream) {
+  const int F = D + 1 + H + (ksum != nullptr ? D : 0);
+  if (B <= 0 || H <= 0 || D <= 0 || hid <= 0 || hid > kBhMaxHid || ncls <= 0 || ncls > kBhMaxCls ||
+      2 * D + 1 + H > kBhMaxF || (int64_t)(F + ncls) * hid > kBhMaxW || q == nullptr || t_pos == nullptr ||
+      w1t == nullptr || b1 == nullptr || w2 == nullptr || b2 == nullptr || classes == nullptr || lhat == nullptr ||
+      (k != nullptr && ksum == nullptr) || (int64_t)B * H > 0x7fffffff - kBhWaves ||
+      ((hid & 3) == 0 && ((uintptr_t)w1t & 15))) {
+    set_error("ta_budget_head: bad arguments (hid <= 256, classes <= 64, 2 D + 1 + H <= 1024, (F + classes) * hid <= 24576, "
+              "W1 16-byte aligned)");
+    return TA_ERR_ARG;
+  }
+  const dim3 grid((unsigned)((B * H + kBhWaves - 1) / kBhWaves));
+  const size_t lds = ((size_t)((F * hid + 3) & ~3) + (size_t)((ncls * hid + hid + ncls + 3) & ~3) +
+                      (size_t)kBhWaves * (F + hid)) * sizeof(float);
+  hipStream_t st = (hipStream_t)stream;
+#define TA_BH(TT)                                                                                                  \
+  hipLaunchKernelGGL(budget_head_kernel<TT>, grid, dim3(kBhWaves * kWave), lds, st, (const TT*)q, qsb, qsh, ksum,  \
+                     (const TT*)k, ksb, ksh, t_pos, w1t, b1, w2, b2, classes, B, H, D, F, hid, ncls, lhat)
+  switch (q_dtype) {
+    case TA_F32: TA_BH(float); break;
+    case TA_BF16: TA_BH(bf16_t); break;
+    case TA_F16: TA_BH(f16_t); break;
+    default:
+      set_error("ta_budget_head: q dtype f32, bf16 or f16");
+      return TA_ERR_ARG;
+  }
+#undef TA_BH
+  return check_launch("budget_head_kernel");
 }
 
 extern "C" int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const float* S0,

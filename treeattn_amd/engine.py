@@ -127,6 +127,7 @@ class SegState:
         self.st_score = torch.zeros(batch, H, Tst, NS, device=dev)
         self.st_ok = torch.zeros(batch, H, Tst, NS, dtype=torch.bool, device=dev)
         self.ksum = torch.zeros(batch, H, dh, device=dev)
+        self.pw32 = None    # the budget head's weights as its kernel takes them (prepared on first use)
 
     def kv(self):
         """The cache as the kernels take it: (K, V) tensors, or (PagedCache, None)."""
@@ -304,18 +305,30 @@ def decode_nsplit(B, H, wl, leaf):
     return 4 * g
 
 
-def _pw_budget(state, pw, q, t):
-    cfg, H = state.cfg, state.H
+def _budget_weights(state, pw):
+    """The budget head's weights as ta_budget_head takes them (float32, W1 transposed, classes int32), prepared
+    once per layer state and kept while the same weight dict is passed."""
+    c = state.pw32
+    if c is None or c[0] is not pw:
+        dev = state.ksum.device
+        c = (pw, pw['w1'].to(dev, torch.float32).t().contiguous(), pw['b1'].to(dev, torch.float32).contiguous(),
+             pw['w2'].to(dev, torch.float32).contiguous(), pw['b2'].to(dev, torch.float32).contiguous(),
+             pw['classes'].to(dev, torch.int32).contiguous())
+        state.pw32 = c
+    return c[1:]
+
+
+def _pw_budget(state, pw, q, tpos, k=None):
+    """The budget head of one decode step (engine.py:89-96) for every (sequence, head): (B,H) int32 budgets, or
+    None without the head.  With the global pool the features take the running key sum over positions < t, and
+    with k (B,H,dh) the sum then adds this step's key in the same launch.  tpos: (B,) int32 positions."""
+    cfg = state.cfg
     if cfg.beam_mode != 'pred':
         return None
-    B = q.shape[0]
-    feats = [q.float(), torch.log(q.float().norm(dim=-1, keepdim=True) + 1e-6),
-             torch.eye(H, device=q.device).view(1, H, 1, H).expand(B, H, 1, H)]
-    if cfg.global_pool:
-        tt = state._tpos(t).float().clamp(min=1).view(B, 1, 1)
-        feats.append((state.ksum / tt).unsqueeze(2))
-    h = F.relu(F.linear(torch.cat(feats, -1), pw['w1'].float(), pw['b1'].float()))
-    return pw['classes'].to(q.device)[F.linear(h, pw['w2'].float(), pw['b2'].float()).argmax(-1)]
+    w1t, b1, w2, b2, cls = _budget_weights(state, pw)
+    pool = state.ksum if cfg.global_pool else None
+    return K.budget_head(q[:, :, 0], tpos, w1t, b1, w2, b2, cls, ksum=pool,
+                         k=k if pool is not None else None)
 
 
 def _pw_budget_seq(cfg, H, pw, q, k):
@@ -344,7 +357,8 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     leaf = state.shape.leaf
     tpos = state._tpos(t)
     scale = 1.0 / math.sqrt(dh)
-    lhat = _pw_budget(state, pw, q, t)
+    lhat = _pw_budget(state, pw, q, tpos, k=k[:, :, 0] if update else None)
+    pooled = lhat is not None and cfg.global_pool and update   # the budget head's launch added k to ksum
     wl = state.shape.leaf_width(cfg.wmax)
     if scratch is None:
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
@@ -405,7 +419,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         if not appendable:
             K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
             state.gate_append(tpos)
-        if cfg.global_pool:
+        if cfg.global_pool and not pooled:
             state.ksum += k[:, :, 0].float()
     out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
     K.seg_attn(q, Kc, Vc, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out, keys=scratch.keys,
@@ -495,6 +509,10 @@ class Decoder:
                 self.pool = PagePool(B, H, dh, leaf, self.Tcap, npages, self.nl, self.dtype, self.dev)
             self.states = [SegState(self.cfg, self.Tcap, H, dh, self.dev, B, self.dtype, pages=self.pool, layer=i)
                            for i in range(self.nl)]
+            if self.cfg.beam_mode == 'pred':
+                # the budget heads' kernel-ready weights, before any step is captured
+                for st, L in zip(self.states, self.W['layers']):
+                    _budget_weights(st, L['pw'])
             sh = self.states[0].shape
             wl = sh.leaf_width(self.cfg.wmax)
             self.scratch = _Scratch(B, H, dh, wl, self.dev, self._nsplit(B, wl, sh.leaf), self.nl)
@@ -676,14 +694,13 @@ class Decoder:
                     lv = SEL.build_gated(k, st.shape, lv, cfg, t_end=T0, lg=[t[b0:b1] for t in st.lg],
                                          gl=[t[b0:b1] if t is not None else None for t in st.gl])
                 out = torch.empty(nb, T0, H, dh, device=self.dev, dtype=v.dtype)
-                if cfg.neighbors or cfg.beam_mode == 'pred':
-                    # the forward's selection with neighbour borrowing and/or the budget head's per-query budget
-                    # (fastseg.py:345-389), and the decode store seeded with what decoding positions 0..T0-1
-                    # would have written (engine.py:103-105): each position's top nb_store leaves of its own tree
-                    # pass, which the selection's own neighbour pass reads too
-                    if cfg.beam_mode == 'pred':
-                        lhat = _pw_budget_seq(cfg, H, L['pw'], q, k)
-                    else:
+                lhat = _pw_budget_seq(cfg, H, L['pw'], q, k) if cfg.beam_mode == 'pred' else None
+                if cfg.neighbors:
+                    # the forward's selection with neighbour borrowing (and the budget head's per-query budget
+                    # when on) (fastseg.py:345-389), and the decode store seeded with what decoding positions
+                    # 0..T0-1 would have written (engine.py:103-105): each position's top nb_store leaves of its
+                    # own tree pass, which the selection's own neighbour pass reads too
+                    if lhat is None:
                         lhat = torch.full((nb, H, T0), cfg.beam, dtype=torch.long, device=self.dev)
                     sel, ids, vld, sct, _ = SEL.select(q, k, lhat, cfg, st.shape, lv)
                     n = min(cfg.nb_store, ids.shape[-1])
@@ -696,11 +713,25 @@ class Decoder:
                     out.transpose(1, 2).copy_(o)
                     del sel, ids, vld, sct, cand, keep, o
                 else:
-                    ids, vld, _ = K.tree_descend(q, lv, tq, st.shape, cfg.wmax)
-                    n_tree = torch.full(ids.shape[:3], n_tree_val, dtype=torch.int32, device=self.dev)
+                    # no neighbour borrowing: the tree leaves of each query's budget plus the static and local
+                    # keys, attended by the structural kernel (the same key set as the candidate list, which at
+                    # prompt length would take tens of GB); with the budget head the split is seg.py:111-117's
+                    # with no borrowed leaves
+                    ids, vld, sct = K.tree_descend(q, lv, tq, st.shape, cfg.wmax)
+                    if lhat is None:
+                        n_tree = torch.full(ids.shape[:3], n_tree_val, dtype=torch.int32, device=self.dev)
+                    else:
+                        n_tree = SEL.budget_split(torch.zeros_like(lhat), lhat, cfg.wmax).to(torch.int32)
                     K.seg_attn(q, k, v, tq, ids, vld, n_tree, st.shape.leaf, cfg.local, scale,
                                out=out.transpose(1, 2))
-                    del ids, vld, n_tree
+                    if st.st_leaf.shape[2] > 0:
+                        # the decode store, as above
+                        n = min(cfg.nb_store, ids.shape[-1])
+                        vb = vld[..., :n].bool()
+                        st.st_leaf[b0:b1, :, :T0, :n] = ids[..., :n].clamp(min=0)
+                        st.st_score[b0:b1, :, :T0, :n] = torch.where(vb, sct[..., :n], torch.zeros_like(sct[..., :n]))
+                        st.st_ok[b0:b1, :, :T0, :n] = vb
+                    del ids, vld, sct, n_tree
                 x = x + F.linear(out.view(nb, T0, C), L['c_proj'])
                 x = x + F.linear(F.gelu(F.linear(_ln(x, L['ln2']), L['c_fc'])), L['c_mlp'])
                 if cfg.global_pool:

@@ -285,6 +285,35 @@ def gather_dot(q, S, cand, scale):
     return out
 
 
+def budget_head(q, t_pos, w1t, b1, w2, b2, classes, ksum=None, k=None, out=None):
+    """The decode step's budget head (engine.py:89-96) in one launch: q (B,H,D) rows (unit last stride), t_pos
+    (B,) int32, W1 transposed w1t (F,hid) / b1 / w2 (ncls,hid) / b2 float32 contiguous, classes int32 (ncls,);
+    ksum (B,H,D) float32 contiguous for the global pool, and with k (B,H,D, q's dtype) the pool then adds this
+    step's key.  Returns the budgets (B,H) int32 (into `out` when given)."""
+    L.require_gpu(q, t_pos, w1t, b1, w2, b2, classes)
+    B, H, D = q.shape
+    hid = w1t.shape[1]
+    ncls = w2.shape[0]
+    F = D + 1 + H + (D if ksum is not None else 0)
+    if q.stride(-1) != 1 or (k is not None and (k.stride(-1) != 1 or k.shape != q.shape or k.dtype != q.dtype)):
+        raise ValueError('budget_head: q and k rows (B,H,D) of one dtype, unit last stride')
+    for t, shp in ((w1t, (F, hid)), (b1, (hid,)), (w2, (ncls, hid)), (b2, (ncls,))):
+        if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != shp:
+            raise ValueError('budget_head: weights float32 contiguous, W1 transposed (%d, %d)' % (F, hid))
+    if classes.dtype != torch.int32 or classes.numel() != ncls or t_pos.dtype != torch.int32 or t_pos.numel() != B:
+        raise ValueError('budget_head: classes int32 (ncls,), t_pos int32 (B,)')
+    if ksum is not None and (ksum.dtype != torch.float32 or not ksum.is_contiguous() or ksum.shape != q.shape):
+        raise ValueError('budget_head: ksum float32 contiguous (B,H,D)')
+    if k is not None and ksum is None:
+        raise ValueError('budget_head: k updates ksum, which is missing')
+    if out is None:
+        out = torch.empty(B, H, dtype=torch.int32, device=q.device)
+    L.call('ta_budget_head', L.ptr(q), L.dtype_code(q), q.stride(0), q.stride(1), L.ptr(ksum), L.ptr(k),
+           k.stride(0) if k is not None else 0, k.stride(1) if k is not None else 0, L.ptr(t_pos), L.ptr(w1t),
+           L.ptr(b1), L.ptr(w2), L.ptr(b2), L.ptr(classes), B, H, D, hid, ncls, L.ptr(out), L.stream())
+    return out
+
+
 def leaf_store(ids, vld, sct, t_pos, st_leaf, st_score, st_ok, n):
     """The decode step's neighbour store (engine.py:103-105): the first n leaves of each (b, h)'s selection
     (ids int32 / vld uint8 / sct float32, (B,H,1,wl) contiguous) into row t_pos[b] of st_leaf / st_score / st_ok
