@@ -63,6 +63,21 @@ typedef struct ta_kv_pages {
 } ta_kv_pages;
 
 /*
+ * The neighbour store of the selection (engine.py:103-105) that a descent can write as it writes its outputs:
+ * for a query at position t in [0, Tst) and slot r < n, leaf[b,h,t,r] = the r-th kept leaf id (0 past the kept
+ * ones), score = its score (0 past them), ok = 1 for a kept leaf else 0.  leaf int32 / score float32 / ok uint8
+ * (B, H, Tst, >= n) share the element strides sb, sh, st; n <= wl.
+ */
+typedef struct ta_leaf_store_out {
+  int32_t* leaf;
+  float* score;
+  uint8_t* ok;
+  int64_t sb, sh, st;
+  int Tst;
+  int n;
+} ta_leaf_store_out;
+
+/*
  * Level-sum pyramid of a key tensor (replaces seg.py:26-41 level_sums, fastseg.py:238-251 level_sums_min
  * without the gate, and the index-key preparation seg.py:128-130 / fastseg.py:306-308).
  *
@@ -104,6 +119,14 @@ int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_
                     int T, int leaf_log2, int arity_log2, int wmax, int wl,
                     int32_t* ids, uint8_t* vld, float* sct, void* stream);
 
+/* ta_tree_descend that also writes each query's neighbour store (store non-NULL; engine.py:103-105). */
+int ta_tree_descend_store(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn,
+                          int B, int H, int Nq, int D,
+                          const int32_t* tq, int64_t tq_sb,
+                          int n_levels, const float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh,
+                          int T, int leaf_log2, int arity_log2, int wmax, int wl,
+                          int32_t* ids, uint8_t* vld, float* sct, const ta_leaf_store_out* store, void* stream);
+
 /*
  * One decode position per (sequence, head): ta_tree_descend of q (B,H,1,D) at t = t_pos[b], and, in the same
  * launch, ta_kv_append of k_new / v_new at row t_pos[b] (the selection and cache update of one decode step,
@@ -118,6 +141,15 @@ int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int64_t qsh, i
                            const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
                            int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
                            const ta_kv_pages* pages, void* stream);
+
+/* ta_tree_descend_append that also writes the position's neighbour store (store non-NULL; engine.py:103-105). */
+int ta_tree_descend_append_store(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
+                                 const int32_t* t_pos, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                                 const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl,
+                                 int32_t* ids, uint8_t* vld, float* sct,
+                                 const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
+                                 int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
+                                 const ta_kv_pages* pages, const ta_leaf_store_out* store, void* stream);
 
 /*
  * Scores of queries against gathered rows (replaces fastseg.py:118-130 gather_dot and its kernel

@@ -218,6 +218,54 @@ def test_budget_head_kernel_matches_oracle(dtype, D, H, hid, ncls, pool):
         assert torch.equal(ks_dev.cpu(), ksum + k.float())
 
 
+@pytest.mark.parametrize('leaf,arity,wmax,ns', [(8, 2, 4, 2), (4, 4, 3, 3), (16, 2, 6, 2)])
+def test_descent_writes_neighbour_store(leaf, arity, wmax, ns):
+    """The descent's neighbour store (ta_tree_descend_store, ta_tree_descend_append_store) against the reference's
+    assignments (engine.py:103-105) applied to the descent's own outputs, and against ta_leaf_store: every
+    position of a prompt (one shared position list) and one decode position per sequence (with the append)."""
+    from treeattn_amd import selection as SEL
+    B, H, T, D = 2, 3, 96, 32
+    cfg = tiny(seq_len=128, leaf=leaf, arity=arity, wmax=wmax, beam=wmax, nb_store=ns)
+    shape = SEL.cfg_shape(cfg, 128)
+    wl = shape.leaf_width(wmax)
+    n = min(ns, wl)
+    q = rnd(B, H, T, D, seed=31).to(DEV)
+    k = rnd(B, H, T, D, seed=32).to(DEV)
+    Tcap = 128
+    Kc = torch.zeros(B, H, Tcap, D, device=DEV)
+    Vc = torch.zeros(B, H, Tcap, D, device=DEV)
+    Kc[:, :, :T] = k
+    levels = SEL.build_pyramid(Kc, shape, t_end=T)
+    tq = torch.arange(T, device=DEV, dtype=torch.int32)
+    st = [torch.zeros(B, H, 128, ns, dtype=dt, device=DEV) for dt in (torch.int32, torch.float32, torch.bool)]
+    ids, vld, sct = K.tree_descend(q, levels, tq, shape, wmax, store=(*st, n))
+    want = [torch.zeros_like(x) for x in st]
+    vb = vld[..., :n].bool()
+    want[0][:, :, :T, :n] = ids[..., :n].clamp(min=0)
+    want[1][:, :, :T, :n] = torch.where(vb, sct[..., :n], torch.zeros_like(sct[..., :n]))
+    want[2][:, :, :T, :n] = vb
+    for a, b in zip(st, want):
+        assert torch.equal(a, b)
+    # one decode position per sequence, with the cache append, against the descent + ta_leaf_store
+    lv = [x.clone() for x in levels]
+    lv2 = [x.clone() for x in lv]
+    t_pos = torch.tensor([T, T - 7], dtype=torch.int32, device=DEV)
+    qd = rnd(B, H, 1, D, seed=33).to(DEV)
+    kn, vn = rnd(B, H, D, seed=34).to(DEV), rnd(B, H, D, seed=35).to(DEV)
+    outs = [torch.empty(B, H, 1, wl, dtype=dt, device=DEV) for dt in (torch.int32, torch.uint8, torch.float32)]
+    outs2 = [torch.empty_like(x) for x in outs]
+    sa = [torch.zeros_like(x) for x in st]
+    sb_ = [torch.zeros_like(x) for x in st]
+    K.tree_descend_append(qd, lv, t_pos, shape, wmax, kn, vn, Kc.clone(), Vc.clone(), out=outs, store=(*sa, n))
+    K.tree_descend_append(qd, lv2, t_pos, shape, wmax, kn, vn, Kc.clone(), Vc.clone(), out=outs2)
+    K.leaf_store(outs2[0], outs2[1], outs2[2], t_pos, *sb_, n)
+    for a, b in zip(outs, outs2):
+        assert torch.equal(a, b)
+    for a, b in zip(sa, sb_):
+        assert torch.equal(a, b)
+    assert bool(sa[2][0, :, T].any()) and bool(sa[2][1, :, T - 7].any())
+
+
 @pytest.mark.parametrize('kw', [dict(), dict(leaf=4, arity=4, wmax=3, beam=2), dict(beam_mode='pred', global_pool=True),
                                 dict(beam_mode='pred', neighbors=False, leaf=8, wmax=4)])
 def test_prefill_with_neighbours_then_decode_matches_decode_from_scratch(kw):

@@ -28,6 +28,12 @@ class KvPages(ctypes.Structure):
                 ('block_log2', c_i32)]
 
 
+class LeafStoreOut(ctypes.Structure):
+    """ta_leaf_store_out (include/treeattn.h)."""
+    _fields_ = [('leaf', c_vp), ('score', c_vp), ('ok', c_vp), ('sb', c_i64), ('sh', c_i64), ('st', c_i64),
+                ('Tst', c_i32), ('n', c_i32)]
+
+
 class StepLayer(ctypes.Structure):
     """ta_step_layer"""
     _fields_ = [('ln1', c_vp), ('c_attn', c_vp), ('c_proj', c_vp), ('ln2', c_vp), ('c_fc', c_vp), ('c_mlp', c_vp),
@@ -61,10 +67,17 @@ SIGNATURES = {
     'ta_tree_descend': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64,
                                 c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32,
                                 c_vp, c_vp, c_vp, c_vp]),
+    'ta_tree_descend_store': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64,
+                                      c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32,
+                                      c_vp, c_vp, c_vp, _P(LeafStoreOut), c_vp]),
     'ta_tree_descend_append': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp),
                                        _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp,
                                        c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
                                        c_i32, _P(KvPages), c_vp]),
+    'ta_tree_descend_append_store': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp),
+                                             _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                             c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
+                                             c_i64, c_i32, _P(KvPages), _P(LeafStoreOut), c_vp]),
     'ta_seg_attend': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32,
                               c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32,
                               c_vp, c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_i32, c_f32, c_vp, c_vp, c_vp, c_vp,

@@ -104,7 +104,8 @@ template <typename TQ, int D, int WPQ, bool APPEND>
 __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
     const TQ* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qsn, int H, int Nq, int T,
     const int32_t* __restrict__ tq, int64_t tq_sb, LevelIn lv, int n_levels, int arity_log2, int wmax, int wl,
-    int cmax4, int32_t* __restrict__ ids, uint8_t* __restrict__ vld, float* __restrict__ sct, AppendIn ap) {
+    int cmax4, int32_t* __restrict__ ids, uint8_t* __restrict__ vld, float* __restrict__ sct, AppendIn ap,
+    ta_leaf_store_out so) {
   constexpr int NT = kWave * WPQ;      // threads per query
   extern __shared__ int32_t smem_i[];
   const int lane = lane_id(), w = wave_id();
@@ -147,6 +148,16 @@ __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
       ids[obase + r] = -1;
       vld[obase + r] = 0;
       sct[obase + r] = -INFINITY;
+    }
+  }
+  if (so.leaf != nullptr && t >= 0 && t < so.Tst) {
+    // the neighbour store of position t: kept leaves first, empty slots as id 0, score 0, not ok
+    const int64_t sbase = b * so.sb + h * so.sh + (int64_t)t * so.st;
+    for (int r = tid; r < so.n; r += NT) {
+      const bool ok = r < nk;
+      so.leaf[sbase + r] = ok ? max(kid[r], 0) : 0;
+      so.score[sbase + r] = ok ? ksc[r] : 0.0f;
+      so.ok[sbase + r] = ok ? 1 : 0;
     }
   }
 }
@@ -283,7 +294,8 @@ template <typename T, int D>
 struct DescendRun {
   static int run(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H, int Nq, const int32_t* tq,
                  int64_t tq_sb, const LevelIn& lv, int n_levels, int Tgeo, int arity_log2, int wmax, int wl,
-                 int32_t* ids, uint8_t* vld, float* sct, const AppendIn* ap, hipStream_t st) {
+                 int32_t* ids, uint8_t* vld, float* sct, const AppendIn* ap, const ta_leaf_store_out* so,
+                 hipStream_t st) {
     const int arity = 1 << arity_log2;
     const int cmax4 = (arity * wmax + arity - 1 + 3) & ~3;
     const int wmax4 = (wmax + 3) & ~3;
@@ -307,9 +319,11 @@ struct DescendRun {
     }
     dim3 grid((Nq + qpb - 1) / qpb, B * H);
     const AppendIn none{};
+    const ta_leaf_store_out no_store{};
 #define TA_DESC(WPQ, NTH, APP)                                                                                   \
   hipLaunchKernelGGL((descend_kernel<T, D, WPQ, APP>), grid, dim3(NTH), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq, \
-                     Tgeo, tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct, ap ? *ap : none)
+                     Tgeo, tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct, ap ? *ap : none, \
+                     so ? *so : no_store)
     if (ap) {
       if (wpq == 16) TA_DESC(16, 1024, true);
       else TA_DESC(4, 256, true);
@@ -430,14 +444,19 @@ int level_sums_impl(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_
 }
 }  // namespace
 
-extern "C" int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H,
-                               int Nq, int D, const int32_t* tq, int64_t tq_sb, int n_levels,
-                               const float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh, int T,
-                               int leaf_log2, int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld,
-                               float* sct, void* stream) {
+namespace {
+bool store_ok(const ta_leaf_store_out* so, int wl) {
+  return so == nullptr || (so->leaf != nullptr && so->score != nullptr && so->ok != nullptr && so->Tst >= 0 &&
+                           so->n >= 0 && so->n <= wl);
+}
+
+int tree_descend_impl(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H, int Nq, int D,
+                      const int32_t* tq, int64_t tq_sb, int n_levels, const float* const* lv_ptr,
+                      const int64_t* lv_sb, const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax,
+                      int wl, int32_t* ids, uint8_t* vld, float* sct, const ta_leaf_store_out* so, void* stream) {
   if (B <= 0 || H <= 0 || Nq < 0 || wmax < 1 || wl < 0 || n_levels < 0 || n_levels > kMaxLevels || !pow2(T) ||
-      leaf_log2 < 1 || arity_log2 < 1) {
-    set_error("ta_tree_descend: bad sizes");
+      leaf_log2 < 1 || arity_log2 < 1 || !store_ok(so, wl)) {
+    set_error("ta_tree_descend: bad sizes (or store: arrays missing, n > wl)");
     return TA_ERR_ARG;
   }
   if (Nq == 0) return TA_OK;
@@ -457,19 +476,20 @@ extern "C" int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t 
     }
   }
   return dispatch_dt_d<DescendRun>(q_dtype, D, q, qsb, qsh, qsn, B, H, Nq, tq, tq_sb, lv, n_levels, T, arity_log2,
-                                   wmax, wl, ids, vld, sct, (const AppendIn*)nullptr, (hipStream_t)stream);
+                                   wmax, wl, ids, vld, sct, (const AppendIn*)nullptr, so, (hipStream_t)stream);
 }
 
-extern "C" int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
-                                      const int32_t* t_pos, int n_levels, float* const* lv_ptr,
-                                      const int64_t* lv_sb, const int64_t* lv_sh, int T, int leaf_log2,
-                                      int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld, float* sct,
-                                      const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
-                                      int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst,
-                                      int Tcap, const ta_kv_pages* pages, void* stream) {
+int tree_descend_append_impl(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
+                             const int32_t* t_pos, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                             const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl,
+                             int32_t* ids, uint8_t* vld, float* sct, const void* k_new, const void* v_new,
+                             int64_t nsb, int64_t nsh, int64_t vnsb, int64_t vnsh, void* Kc, void* Vc, int64_t csb,
+                             int64_t csh, int64_t cst, int Tcap, const ta_kv_pages* pages,
+                             const ta_leaf_store_out* so, void* stream) {
   if (B <= 0 || H <= 0 || wmax < 1 || wl < 0 || n_levels < 0 || n_levels > kMaxLevels || !pow2(T) ||
-      leaf_log2 < 1 || leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4 || Tcap <= 0 || D > 256) {
-    set_error("ta_tree_descend_append: bad sizes");
+      leaf_log2 < 1 || leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4 || Tcap <= 0 || D > 256 ||
+      !store_ok(so, wl)) {
+    set_error("ta_tree_descend_append: bad sizes (or store: arrays missing, n > wl)");
     return TA_ERR_ARG;
   }
   if (!rows_aligned(q, dtype, D, {qsb, qsh})) {
@@ -502,7 +522,59 @@ extern "C" int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int
     ap.npages = pages->num_pages;
   }
   return dispatch_dt_d<DescendRun>(dtype, D, q, qsb, qsh, (int64_t)0, B, H, 1, t_pos, (int64_t)1, lv, n_levels, T,
-                                   arity_log2, wmax, wl, ids, vld, sct, (const AppendIn*)&ap, (hipStream_t)stream);
+                                   arity_log2, wmax, wl, ids, vld, sct, (const AppendIn*)&ap, so, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int ta_tree_descend(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H,
+                               int Nq, int D, const int32_t* tq, int64_t tq_sb, int n_levels,
+                               const float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh, int T,
+                               int leaf_log2, int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld,
+                               float* sct, void* stream) {
+  return tree_descend_impl(q, q_dtype, qsb, qsh, qsn, B, H, Nq, D, tq, tq_sb, n_levels, lv_ptr, lv_sb, lv_sh, T,
+                           leaf_log2, arity_log2, wmax, wl, ids, vld, sct, nullptr, stream);
+}
+
+extern "C" int ta_tree_descend_store(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H,
+                                     int Nq, int D, const int32_t* tq, int64_t tq_sb, int n_levels,
+                                     const float* const* lv_ptr, const int64_t* lv_sb, const int64_t* lv_sh, int T,
+                                     int leaf_log2, int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld,
+                                     float* sct, const ta_leaf_store_out* store, void* stream) {
+  if (store == nullptr) {
+    set_error("ta_tree_descend_store: store missing");
+    return TA_ERR_ARG;
+  }
+  return tree_descend_impl(q, q_dtype, qsb, qsh, qsn, B, H, Nq, D, tq, tq_sb, n_levels, lv_ptr, lv_sb, lv_sh, T,
+                           leaf_log2, arity_log2, wmax, wl, ids, vld, sct, store, stream);
+}
+
+extern "C" int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
+                                      const int32_t* t_pos, int n_levels, float* const* lv_ptr,
+                                      const int64_t* lv_sb, const int64_t* lv_sh, int T, int leaf_log2,
+                                      int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld, float* sct,
+                                      const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
+                                      int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst,
+                                      int Tcap, const ta_kv_pages* pages, void* stream) {
+  return tree_descend_append_impl(q, dtype, qsb, qsh, B, H, D, t_pos, n_levels, lv_ptr, lv_sb, lv_sh, T, leaf_log2,
+                                  arity_log2, wmax, wl, ids, vld, sct, k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc,
+                                  csb, csh, cst, Tcap, pages, nullptr, stream);
+}
+
+extern "C" int ta_tree_descend_append_store(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
+                                            const int32_t* t_pos, int n_levels, float* const* lv_ptr,
+                                            const int64_t* lv_sb, const int64_t* lv_sh, int T, int leaf_log2,
+                                            int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld, float* sct,
+                                            const void* k_new, const void* v_new, int64_t nsb, int64_t nsh,
+                                            int64_t vnsb, int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh,
+                                            int64_t cst, int Tcap, const ta_kv_pages* pages,
+                                            const ta_leaf_store_out* store, void* stream) {
+  if (store == nullptr) {
+    set_error("ta_tree_descend_append_store: store missing");
+    return TA_ERR_ARG;
+  }
+  return tree_descend_append_impl(q, dtype, qsb, qsh, B, H, D, t_pos, n_levels, lv_ptr, lv_sb, lv_sh, T, leaf_log2,
+                                  arity_log2, wmax, wl, ids, vld, sct, k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc,
+                                  csb, csh, cst, Tcap, pages, store, stream);
 }
 
 extern "C" int ta_gather_dot(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const void* S,

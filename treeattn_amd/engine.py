@@ -258,7 +258,7 @@ class _Scratch:
         self.keys_all = torch.zeros(n_layer, B, H, 1, device=dev)
         self.keys = self.keys_all[0]
         self.n_tree = None
-        self.lhat = None        # the fixed budget of every (sequence, head), when no budget head picks it
+        self.lhat = None        # the fixed budget of every (sequence, head), int32 as the neighbour pass takes it
         self.nsplit = nsplit
         self.ws = K.seg_attn_workspace(B, H, 1, dh, nsplit, dev)
         self.mm_ws = None
@@ -375,13 +375,16 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         K.seg_attend(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0], Kc, Vc,
                      scratch.n_tree, cfg.local, scale, (scratch.ids, scratch.vld, scratch.sct), out, keys=scratch.keys)
         return out, scratch.keys
+    # the list path stores this position's top nb_store leaves (engine.py:103-105) from the descent's own launch;
+    # the neighbour pass below reads only the rows of earlier positions
+    store = (state.st_leaf, state.st_score, state.st_ok, min(cfg.nb_store, wl)) if update and not structural else None
     if appendable:
         # descent and cache append in one launch (the append touches only row t and the nodes ending at t)
         ids, vld, sct = K.tree_descend_append(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0],
-                                              Kc, Vc, out=(scratch.ids, scratch.vld, scratch.sct))
+                                              Kc, Vc, out=(scratch.ids, scratch.vld, scratch.sct), store=store)
     else:
         ids, vld, sct = K.tree_descend(q, state.score_levels, tpos.view(B, 1), state.shape, cfg.wmax,
-                                       out=(scratch.ids, scratch.vld, scratch.sct))
+                                       out=(scratch.ids, scratch.vld, scratch.sct), store=store)
     if structural:
         if update:
             if not appendable:
@@ -403,7 +406,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     # (engine.py:107-119).
     if lhat is None:
         if scratch.lhat is None:
-            scratch.lhat = torch.full((B, H, 1), cfg.beam, dtype=torch.long, device=q.device)
+            scratch.lhat = torch.full((B, H, 1), cfg.beam, dtype=torch.int32, device=q.device)
         lhat = scratch.lhat
     NS = cfg.nb_store
     if state.shape.n_levels:
@@ -415,7 +418,6 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         match = torch.zeros_like(nid, dtype=torch.bool)
         n_tree = SEL.budget_split(torch.zeros_like(lhat.view(B, H, 1)), lhat.view(B, H, 1), cfg.wmax).to(torch.int32)
     if update:
-        K.leaf_store(ids, vld, sct, tpos, state.st_leaf, state.st_score, state.st_ok, min(NS, wl))
         if not appendable:
             K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
             state.gate_append(tpos)
@@ -717,20 +719,16 @@ class Decoder:
                     # keys, attended by the structural kernel (the same key set as the candidate list, which at
                     # prompt length would take tens of GB); with the budget head the split is seg.py:111-117's
                     # with no borrowed leaves
-                    ids, vld, sct = K.tree_descend(q, lv, tq, st.shape, cfg.wmax)
+                    # the decode store (as above) written by the descent itself
+                    store = ((st.st_leaf[b0:b1], st.st_score[b0:b1], st.st_ok[b0:b1],
+                              min(cfg.nb_store, st.shape.leaf_width(cfg.wmax))) if st.st_leaf.shape[2] > 0 else None)
+                    ids, vld, sct = K.tree_descend(q, lv, tq, st.shape, cfg.wmax, store=store)
                     if lhat is None:
                         n_tree = torch.full(ids.shape[:3], n_tree_val, dtype=torch.int32, device=self.dev)
                     else:
                         n_tree = SEL.budget_split(torch.zeros_like(lhat), lhat, cfg.wmax).to(torch.int32)
                     K.seg_attn(q, k, v, tq, ids, vld, n_tree, st.shape.leaf, cfg.local, scale,
                                out=out.transpose(1, 2))
-                    if st.st_leaf.shape[2] > 0:
-                        # the decode store, as above
-                        n = min(cfg.nb_store, ids.shape[-1])
-                        vb = vld[..., :n].bool()
-                        st.st_leaf[b0:b1, :, :T0, :n] = ids[..., :n].clamp(min=0)
-                        st.st_score[b0:b1, :, :T0, :n] = torch.where(vb, sct[..., :n], torch.zeros_like(sct[..., :n]))
-                        st.st_ok[b0:b1, :, :T0, :n] = vb
                     del ids, vld, sct, n_tree
                 x = x + F.linear(out.view(nb, T0, C), L['c_proj'])
                 x = x + F.linear(F.gelu(F.linear(_ln(x, L['ln2']), L['c_fc'])), L['c_mlp'])

@@ -191,9 +191,25 @@ def gate_append(Kc, t_pos, raw, lg, out, blevels, arity, gate_q):
 
 
 # ----------------------------------------------------------------------------------------------- descent
-def tree_descend(q, levels, tq, shape, wmax, out=None):
+def _store_out(store, wl):
+    """store = (st_leaf int32, st_score float32, st_ok bool, n): the neighbour store arrays (B,H,Tst,NS) sharing
+    strides, and the slots per position to write -> a ta_leaf_store_out."""
+    st_leaf, st_score, st_ok, n = store
+    L.require_gpu(st_leaf, st_score, st_ok)
+    if not (st_leaf.dtype == torch.int32 and st_score.dtype == torch.float32 and st_ok.dtype == torch.bool
+            and st_leaf.stride() == st_score.stride() == st_ok.stride() and st_leaf.stride(-1) == 1
+            and st_leaf.shape == st_score.shape == st_ok.shape and 0 <= int(n) <= min(wl, st_leaf.shape[-1])):
+        raise ValueError('neighbour store: st_leaf int32, st_score float32, st_ok bool of one shape and strides, '
+                         'n <= min(wl, nb_store)')
+    return L.LeafStoreOut(st_leaf.data_ptr(), st_score.data_ptr(), st_ok.data_ptr(), st_leaf.stride(0),
+                          st_leaf.stride(1), st_leaf.stride(2), st_leaf.shape[2], int(n))
+
+
+def tree_descend(q, levels, tq, shape, wmax, out=None, store=None):
     """Beam descent of queries q (B,H,Nq,D) at positions tq ((Nq,) shared or (B,Nq)) over pyramid `levels`
-    (tree levels 0..J of `shape`).  Returns ids int32, vld uint8, sct float32, each (B,H,Nq,wl)."""
+    (tree levels 0..J of `shape`).  Returns ids int32, vld uint8, sct float32, each (B,H,Nq,wl).  With store =
+    (st_leaf, st_score, st_ok, n) the same launch writes each query's neighbour store at its position
+    (engine.py:103-105): the first n kept leaves, an empty slot as id 0, score 0, not ok."""
     L.require_gpu(q, tq)
     B, H, Nq, D = q.shape
     wl = shape.leaf_width(wmax)
@@ -210,17 +226,22 @@ def tree_descend(q, levels, tq, shape, wmax, out=None):
     if wl == 0 or Nq == 0:
         return ids, vld, sct
     sb, sh, sn = L.rows3(q)
-    L.call('ta_tree_descend', L.ptr(q), L.dtype_code(q), sb, sh, sn, B, H, Nq, D, L.ptr(tq), tq_sb,
-           len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
-           L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl,
-           L.ptr(ids), L.ptr(vld), L.ptr(sct), L.stream())
+    args = [L.ptr(q), L.dtype_code(q), sb, sh, sn, B, H, Nq, D, L.ptr(tq), tq_sb,
+            len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
+            L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl,
+            L.ptr(ids), L.ptr(vld), L.ptr(sct)]
+    if store is None:
+        L.call('ta_tree_descend', *args, L.stream())
+    else:
+        so = _store_out(store, wl)
+        L.call('ta_tree_descend_store', *args, ctypes.byref(so), L.stream())
     return ids, vld, sct
 
 
-def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out):
+def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out, store=None):
     """Decode step's descent of q (B,H,1,D) at t_pos (B,) int32 and, in the same launch, the cache append of
     k_new, v_new (B,H,D) at row t_pos[b] of the cache (Kc, Vc (B,H,Tcap,D), or a PagedCache as Kc) with node
-    formation.  out = (ids, vld, sct) buffers (B,H,1,wl)."""
+    formation.  out = (ids, vld, sct) buffers (B,H,1,wl); store as for tree_descend."""
     L.require_gpu(q, t_pos, k_new, v_new, *_cache_tensors(Kc, Vc))
     B, H, Nq, D = q.shape
     if Nq != 1 or t_pos.dtype != torch.int32 or not t_pos.is_contiguous():
@@ -232,11 +253,16 @@ def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out
     kp, vp, csb, csh, cst, tcap, pages = _cache(Kc, Vc)
     ids, vld, sct = out
     wl = shape.leaf_width(wmax)
-    L.call('ta_tree_descend_append', L.ptr(q), L.dtype_code(q), q.stride(0), q.stride(1), B, H, D, L.ptr(t_pos),
-           len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
-           L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, L.ptr(ids),
-           L.ptr(vld), L.ptr(sct), L.ptr(k_new), L.ptr(v_new), k_new.stride(0), k_new.stride(1), v_new.stride(0),
-           v_new.stride(1), kp, vp, csb, csh, cst, tcap, pages, L.stream())
+    args = [L.ptr(q), L.dtype_code(q), q.stride(0), q.stride(1), B, H, D, L.ptr(t_pos),
+            len(levels), L.ptr_array(levels), L.i64_array([t.stride(0) for t in levels]),
+            L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, L.ptr(ids),
+            L.ptr(vld), L.ptr(sct), L.ptr(k_new), L.ptr(v_new), k_new.stride(0), k_new.stride(1), v_new.stride(0),
+            v_new.stride(1), kp, vp, csb, csh, cst, tcap, pages]
+    if store is None:
+        L.call('ta_tree_descend_append', *args, L.stream())
+    else:
+        so = _store_out(store, wl)
+        L.call('ta_tree_descend_append_store', *args, ctypes.byref(so), L.stream())
     return ids, vld, sct
 
 
