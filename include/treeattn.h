@@ -142,14 +142,21 @@ int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int64_t qsh, i
                            int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
                            const ta_kv_pages* pages, void* stream);
 
-/* ta_tree_descend_append that also writes the position's neighbour store (store non-NULL; engine.py:103-105). */
-int ta_tree_descend_append_store(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
-                                 const int32_t* t_pos, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
-                                 const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl,
-                                 int32_t* ids, uint8_t* vld, float* sct,
-                                 const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
-                                 int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
-                                 const ta_kv_pages* pages, const ta_leaf_store_out* store, void* stream);
+/*
+ * ta_tree_descend_append with two options: app_lv_ptr / app_lv_sb / app_lv_sh (n_levels entries, or NULL) name the
+ * levels the append forms its nodes in when they are not the scored ones (the mean-log gate: gated levels are
+ * scored from their gated vectors while the append forms the raw sums; the gate's own node update follows as
+ * ta_gate_append), and store (or NULL) the position's neighbour store (engine.py:103-105), as
+ * ta_tree_descend_store writes it.
+ */
+int ta_tree_descend_append_ex(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
+                              const int32_t* t_pos, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
+                              const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl,
+                              int32_t* ids, uint8_t* vld, float* sct,
+                              const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
+                              int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
+                              const ta_kv_pages* pages, float* const* app_lv_ptr, const int64_t* app_lv_sb,
+                              const int64_t* app_lv_sh, const ta_leaf_store_out* store, void* stream);
 
 /*
  * Scores of queries against gathered rows (replaces fastseg.py:118-130 gather_dot and its kernel

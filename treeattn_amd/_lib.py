@@ -74,10 +74,11 @@ SIGNATURES = {
                                        _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp,
                                        c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64,
                                        c_i32, _P(KvPages), c_vp]),
-    'ta_tree_descend_append_store': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp),
-                                             _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
-                                             c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
-                                             c_i64, c_i32, _P(KvPages), _P(LeafStoreOut), c_vp]),
+    'ta_tree_descend_append_ex': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp),
+                                          _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                          c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
+                                          c_i64, c_i32, _P(KvPages), _P(c_vp), _P(c_i64), _P(c_i64),
+                                          _P(LeafStoreOut), c_vp]),
     'ta_seg_attend': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32,
                               c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32,
                               c_vp, c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_i32, c_f32, c_vp, c_vp, c_vp, c_vp,

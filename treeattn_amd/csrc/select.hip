@@ -105,7 +105,7 @@ __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
     const TQ* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qsn, int H, int Nq, int T,
     const int32_t* __restrict__ tq, int64_t tq_sb, LevelIn lv, int n_levels, int arity_log2, int wmax, int wl,
     int cmax4, int32_t* __restrict__ ids, uint8_t* __restrict__ vld, float* __restrict__ sct, AppendIn ap,
-    ta_leaf_store_out so) {
+    LevelIn alv, ta_leaf_store_out so) {
   constexpr int NT = kWave * WPQ;      // threads per query
   extern __shared__ int32_t smem_i[];
   const int lane = lane_id(), w = wave_id();
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
       append_dim<TQ>(tid, D, t, reinterpret_cast<const TQ*>(ap.kn) + b * ap.nsb + h * ap.nsh,
                      reinterpret_cast<const TQ*>(ap.vn) + b * ap.vnsb + h * ap.vnsh, kbase, vbase, rows, n_levels,
                      lv.blevel[0], arity_log2, stk,
-                     [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
+                     [&](int j) { return const_cast<float*>(alv.ptr[j]) + b * alv.sb[j] + h * alv.sh[j]; });
     }
   }
   const int64_t obase = ((int64_t)bh * Nq + n) * wl;
@@ -294,8 +294,8 @@ template <typename T, int D>
 struct DescendRun {
   static int run(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H, int Nq, const int32_t* tq,
                  int64_t tq_sb, const LevelIn& lv, int n_levels, int Tgeo, int arity_log2, int wmax, int wl,
-                 int32_t* ids, uint8_t* vld, float* sct, const AppendIn* ap, const ta_leaf_store_out* so,
-                 hipStream_t st) {
+                 int32_t* ids, uint8_t* vld, float* sct, const AppendIn* ap, const LevelIn* alv,
+                 const ta_leaf_store_out* so, hipStream_t st) {
     const int arity = 1 << arity_log2;
     const int cmax4 = (arity * wmax + arity - 1 + 3) & ~3;
     const int wmax4 = (wmax + 3) & ~3;
@@ -323,7 +323,7 @@ struct DescendRun {
 #define TA_DESC(WPQ, NTH, APP)                                                                                   \
   hipLaunchKernelGGL((descend_kernel<T, D, WPQ, APP>), grid, dim3(NTH), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq, \
                      Tgeo, tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct, ap ? *ap : none, \
-                     so ? *so : no_store)
+                     alv ? *alv : lv, so ? *so : no_store)
     if (ap) {
       if (wpq == 16) TA_DESC(16, 1024, true);
       else TA_DESC(4, 256, true);
@@ -476,7 +476,8 @@ int tree_descend_impl(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int6
     }
   }
   return dispatch_dt_d<DescendRun>(q_dtype, D, q, qsb, qsh, qsn, B, H, Nq, tq, tq_sb, lv, n_levels, T, arity_log2,
-                                   wmax, wl, ids, vld, sct, (const AppendIn*)nullptr, so, (hipStream_t)stream);
+                                   wmax, wl, ids, vld, sct, (const AppendIn*)nullptr, (const LevelIn*)nullptr, so,
+                                   (hipStream_t)stream);
 }
 
 int tree_descend_append_impl(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
@@ -484,8 +485,9 @@ int tree_descend_append_impl(const void* q, int dtype, int64_t qsb, int64_t qsh,
                              const int64_t* lv_sh, int T, int leaf_log2, int arity_log2, int wmax, int wl,
                              int32_t* ids, uint8_t* vld, float* sct, const void* k_new, const void* v_new,
                              int64_t nsb, int64_t nsh, int64_t vnsb, int64_t vnsh, void* Kc, void* Vc, int64_t csb,
-                             int64_t csh, int64_t cst, int Tcap, const ta_kv_pages* pages,
-                             const ta_leaf_store_out* so, void* stream) {
+                             int64_t csh, int64_t cst, int Tcap, const ta_kv_pages* pages, float* const* app_ptr,
+                             const int64_t* app_sb, const int64_t* app_sh, const ta_leaf_store_out* so,
+                             void* stream) {
   if (B <= 0 || H <= 0 || wmax < 1 || wl < 0 || n_levels < 0 || n_levels > kMaxLevels || !pow2(T) ||
       leaf_log2 < 1 || leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4 || Tcap <= 0 || D > 256 ||
       !store_ok(so, wl)) {
@@ -521,8 +523,23 @@ int tree_descend_append_impl(const void* q, int dtype, int64_t qsb, int64_t qsh,
     ap.pstride = pages->page_stride;
     ap.npages = pages->num_pages;
   }
+  // the levels the append forms nodes in: the scored ones unless given apart (gated levels are scored from
+  // their gated vectors while the append forms the raw sums)
+  LevelIn alv = lv;
+  if (app_ptr != nullptr) {
+    for (int j = 0; j < n_levels; ++j) {
+      alv.ptr[j] = app_ptr[j];
+      alv.sb[j] = app_sb[j];
+      alv.sh[j] = app_sh[j];
+      if (!aligned(app_ptr[j], 16)) {
+        set_error("ta_tree_descend_append: append level pointer not 16-byte aligned");
+        return TA_ERR_ARG;
+      }
+    }
+  }
   return dispatch_dt_d<DescendRun>(dtype, D, q, qsb, qsh, (int64_t)0, B, H, 1, t_pos, (int64_t)1, lv, n_levels, T,
-                                   arity_log2, wmax, wl, ids, vld, sct, (const AppendIn*)&ap, so, (hipStream_t)stream);
+                                   arity_log2, wmax, wl, ids, vld, sct, (const AppendIn*)&ap, (const LevelIn*)&alv,
+                                   so, (hipStream_t)stream);
 }
 }  // namespace
 
@@ -557,24 +574,21 @@ extern "C" int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int
                                       int Tcap, const ta_kv_pages* pages, void* stream) {
   return tree_descend_append_impl(q, dtype, qsb, qsh, B, H, D, t_pos, n_levels, lv_ptr, lv_sb, lv_sh, T, leaf_log2,
                                   arity_log2, wmax, wl, ids, vld, sct, k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc,
-                                  csb, csh, cst, Tcap, pages, nullptr, stream);
+                                  csb, csh, cst, Tcap, pages, nullptr, nullptr, nullptr, nullptr, stream);
 }
 
-extern "C" int ta_tree_descend_append_store(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
-                                            const int32_t* t_pos, int n_levels, float* const* lv_ptr,
-                                            const int64_t* lv_sb, const int64_t* lv_sh, int T, int leaf_log2,
-                                            int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld, float* sct,
-                                            const void* k_new, const void* v_new, int64_t nsb, int64_t nsh,
-                                            int64_t vnsb, int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh,
-                                            int64_t cst, int Tcap, const ta_kv_pages* pages,
-                                            const ta_leaf_store_out* store, void* stream) {
-  if (store == nullptr) {
-    set_error("ta_tree_descend_append_store: store missing");
-    return TA_ERR_ARG;
-  }
+extern "C" int ta_tree_descend_append_ex(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
+                                         const int32_t* t_pos, int n_levels, float* const* lv_ptr,
+                                         const int64_t* lv_sb, const int64_t* lv_sh, int T, int leaf_log2,
+                                         int arity_log2, int wmax, int wl, int32_t* ids, uint8_t* vld, float* sct,
+                                         const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
+                                         int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst,
+                                         int Tcap, const ta_kv_pages* pages, float* const* app_lv_ptr,
+                                         const int64_t* app_lv_sb, const int64_t* app_lv_sh,
+                                         const ta_leaf_store_out* store, void* stream) {
   return tree_descend_append_impl(q, dtype, qsb, qsh, B, H, D, t_pos, n_levels, lv_ptr, lv_sb, lv_sh, T, leaf_log2,
                                   arity_log2, wmax, wl, ids, vld, sct, k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc,
-                                  csb, csh, cst, Tcap, pages, store, stream);
+                                  csb, csh, cst, Tcap, pages, app_lv_ptr, app_lv_sb, app_lv_sh, store, stream);
 }
 
 extern "C" int ta_gather_dot(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const void* S,

@@ -363,9 +363,10 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     if scratch is None:
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
     structural = (not cfg.neighbors) and lhat is None
-    # the fused append writes the levels the descent reads: not with the gate, whose descent reads gated vectors
-    appendable = update and B * H < 4096 and q.dtype == k.dtype == state.dtype and not state.gated
-    fused = structural and appendable
+    # the descent's launch also appends (row t and the nodes ending at t, which the descent does not read); with
+    # the gate it scores the gated vectors while the append forms the raw sums, and the gate's node update follows
+    appendable = update and B * H < 4096 and q.dtype == k.dtype == state.dtype
+    fused = structural and appendable and not state.gated
     Kc, Vc = state.kv()
     if fused and scratch.nsplit == 4 and dh in (64, 128) and wl <= 64 and not cfg.global_pool:
         # append, descent and attention in one launch (one workgroup per (sequence, head))
@@ -380,8 +381,9 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     store = (state.st_leaf, state.st_score, state.st_ok, min(cfg.nb_store, wl)) if update and not structural else None
     if appendable:
         # descent and cache append in one launch (the append touches only row t and the nodes ending at t)
-        ids, vld, sct = K.tree_descend_append(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0],
-                                              Kc, Vc, out=(scratch.ids, scratch.vld, scratch.sct), store=store)
+        ids, vld, sct = K.tree_descend_append(q, state.score_levels, tpos, state.shape, cfg.wmax, k[:, :, 0],
+                                              v[:, :, 0], Kc, Vc, out=(scratch.ids, scratch.vld, scratch.sct),
+                                              store=store, app_levels=state.levels if state.gated else None)
     else:
         ids, vld, sct = K.tree_descend(q, state.score_levels, tpos.view(B, 1), state.shape, cfg.wmax,
                                        out=(scratch.ids, scratch.vld, scratch.sct), store=store)
@@ -389,7 +391,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         if update:
             if not appendable:
                 K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
-                state.gate_append(tpos)
+            state.gate_append(tpos)
             if cfg.global_pool:
                 state.ksum += k[:, :, 0].float()
         out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
@@ -420,7 +422,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     if update:
         if not appendable:
             K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
-            state.gate_append(tpos)
+        state.gate_append(tpos)
         if cfg.global_pool and not pooled:
             state.ksum += k[:, :, 0].float()
     out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)

@@ -238,10 +238,12 @@ def tree_descend(q, levels, tq, shape, wmax, out=None, store=None):
     return ids, vld, sct
 
 
-def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out, store=None):
+def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out, store=None, app_levels=None):
     """Decode step's descent of q (B,H,1,D) at t_pos (B,) int32 and, in the same launch, the cache append of
     k_new, v_new (B,H,D) at row t_pos[b] of the cache (Kc, Vc (B,H,Tcap,D), or a PagedCache as Kc) with node
-    formation.  out = (ids, vld, sct) buffers (B,H,1,wl); store as for tree_descend."""
+    formation.  out = (ids, vld, sct) buffers (B,H,1,wl); store as for tree_descend.  app_levels: the levels the
+    append forms its nodes in when they are not the scored `levels` (with the mean-log gate: the raw sums, the
+    scored levels holding gated vectors where the gate applies)."""
     L.require_gpu(q, t_pos, k_new, v_new, *_cache_tensors(Kc, Vc))
     B, H, Nq, D = q.shape
     if Nq != 1 or t_pos.dtype != torch.int32 or not t_pos.is_contiguous():
@@ -258,11 +260,19 @@ def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out
             L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, L.ptr(ids),
             L.ptr(vld), L.ptr(sct), L.ptr(k_new), L.ptr(v_new), k_new.stride(0), k_new.stride(1), v_new.stride(0),
             v_new.stride(1), kp, vp, csb, csh, cst, tcap, pages]
-    if store is None:
+    if store is None and app_levels is None:
         L.call('ta_tree_descend_append', *args, L.stream())
     else:
-        so = _store_out(store, wl)
-        L.call('ta_tree_descend_append_store', *args, ctypes.byref(so), L.stream())
+        so = ctypes.byref(_store_out(store, wl)) if store is not None else None
+        if app_levels is not None:
+            if len(app_levels) != len(levels) or any(a.shape != l.shape or a.dtype != torch.float32 or
+                                                     a.stride(-1) != 1 for a, l in zip(app_levels, levels)):
+                raise ValueError('tree_descend_append: app_levels must match the scored levels in shape, float32')
+            ap = (L.ptr_array(app_levels), L.i64_array([t.stride(0) for t in app_levels]),
+                  L.i64_array([t.stride(1) for t in app_levels]))
+        else:
+            ap = (None, None, None)
+        L.call('ta_tree_descend_append_ex', *args, *ap, so, L.stream())
     return ids, vld, sct
 
 
