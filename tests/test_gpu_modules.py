@@ -220,7 +220,7 @@ def test_budget_head_kernel_matches_oracle(dtype, D, H, hid, ncls, pool):
 
 @pytest.mark.parametrize('leaf,arity,wmax,ns', [(8, 2, 4, 2), (4, 4, 3, 3), (16, 2, 6, 2)])
 def test_descent_writes_neighbour_store(leaf, arity, wmax, ns):
-    """The descent's neighbour store (ta_tree_descend_store, ta_tree_descend_append_store) against the reference's
+    """The descent's neighbour store (ta_tree_descend_store, ta_tree_descend_append_ex) against the reference's
     assignments (engine.py:103-105) applied to the descent's own outputs, and against ta_leaf_store: every
     position of a prompt (one shared position list) and one decode position per sequence (with the append)."""
     from treeattn_amd import selection as SEL
