@@ -506,6 +506,38 @@ int ta_budget_head(const void* q, int q_dtype, int64_t qsb, int64_t qsh, float* 
                    void* stream);
 
 /*
+ * The budget head of a decode step as ta_neighbor_pass_head takes it (the weights as ta_budget_head takes them:
+ * W1 transposed (F x hid) and W2 (ncls x hid) float32, 16-byte aligned, hid a multiple of 4 and <= 256,
+ * ncls <= 64; ksum (B, H, D) float32 contiguous or NULL without the global pool; k this step's keys (q's dtype,
+ * strides ksb, ksh) added to ksum after its read, or NULL; lhat (B, H) int32 receives the budgets, or NULL).
+ */
+typedef struct ta_budget_head_in {
+  const float* w1t;
+  const float* b1;
+  const float* w2;
+  const float* b2;
+  const int32_t* classes;
+  int hid, ncls;
+  float* ksum;
+  const void* k;
+  int64_t ksb, ksh;
+  int32_t* lhat;
+} ta_budget_head_in;
+
+/*
+ * One decode position per (sequence, head): ta_budget_head and ta_neighbor_pass with its budget split in one
+ * launch (engine.py:89-102).  q (B, H, D) rows at strides qsb, qsh; t_pos (B,) positions; the other arguments as
+ * ta_neighbor_pass's with Nq = 1; n_tree receives the split of the head's budget.  The budgets and the key sum
+ * equal ta_budget_head's, bit for bit.
+ */
+int ta_neighbor_pass_head(const void* q, int q_dtype, int64_t qsb, int64_t qsh, const float* S0, int64_t ssb,
+                          int64_t ssh, int M, const int32_t* st_leaf, const float* st_score, const uint8_t* st_ok,
+                          int64_t st_sb, int64_t st_sh, int64_t st_st, int Tst, const int32_t* t_pos, int B, int H,
+                          int D, int nb_window, int nb_store, int nb_probe, int nb_cap_min, float nb_rho,
+                          int neighbors, float scale, int wmax, const ta_budget_head_in* head, int32_t* nid,
+                          uint8_t* match, int32_t* nL, int32_t* n_tree, void* stream);
+
+/*
  * The decode step's neighbour store (replaces the assignments of engine.py:103-105): for every (b, h) and slot
  * r < n, at position t = t_pos[b] (skipped outside [0, Tst)): st_leaf[b,h,t,r] = ids[b,h,0,r] (an invalid slot's
  * -1 stored as 0), st_score = sct when vld else 0, st_ok = vld.  ids int32 / vld uint8 / sct float32 are the

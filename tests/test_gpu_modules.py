@@ -218,6 +218,48 @@ def test_budget_head_kernel_matches_oracle(dtype, D, H, hid, ncls, pool):
         assert torch.equal(ks_dev.cpu(), ksum + k.float())
 
 
+@pytest.mark.parametrize('dtype,D,H,hid,pool', [(torch.bfloat16, 64, 12, 64, True), (torch.float32, 32, 3, 128, False),
+                                               (torch.bfloat16, 128, 4, 64, True)])
+def test_neighbor_pass_with_budget_head_matches_separate_launches(dtype, D, H, hid, pool):
+    """ta_neighbor_pass_head (budget head + neighbour pass + budget split in one launch) against ta_budget_head
+    followed by ta_neighbor_pass with its budgets: the same budgets, key sums, matches, distinct counts and
+    splits, bit for bit, over stored leaves with invalid slots and positions near 0."""
+    B, M, Tst = 5, 64, 128
+    cfg = tiny(nb_window=4, nb_store=2, nb_probe=2, nb_cap_min=1, wmax=6, beam_classes=(2, 3, 4, 6))
+    ncls = len(cfg.beam_classes)
+    F_ = D + 1 + H + (D if pool else 0)
+    g = torch.Generator().manual_seed(D + hid)
+    w1t = (torch.randn(F_, hid, generator=g) / math.sqrt(F_)).to(DEV)
+    b1 = (torch.randn(hid, generator=g) * 0.1).to(DEV)
+    w2 = (torch.randn(ncls, hid, generator=g) / math.sqrt(hid)).to(DEV)
+    b2 = (torch.randn(ncls, generator=g) * 0.1).to(DEV)
+    cls = torch.tensor(cfg.beam_classes, dtype=torch.int32, device=DEV)
+    q = torch.randn(B, H, 1, D, generator=g).to(dtype).to(DEV)
+    k = torch.randn(B, H, D, generator=g).to(dtype).to(DEV)
+    ksum = (torch.randn(B, H, D, generator=g) * 10).to(DEV)
+    S0 = torch.randn(B, H, M, D, generator=g).to(DEV)
+    st_leaf = torch.randint(-1, M + 2, (B, H, Tst, 2), generator=g, dtype=torch.int32).to(DEV)
+    st_score = torch.randn(B, H, Tst, 2, generator=g).to(DEV)
+    st_ok = (torch.rand(B, H, Tst, 2, generator=g) < 0.8).to(DEV)
+    t_pos = torch.tensor([0, 1, 3, 77, 127], dtype=torch.int32, device=DEV)
+    leaf = 2
+    ks_a, ks_b = ksum.clone(), ksum.clone()
+    lhat_a = torch.empty(B, H, dtype=torch.int32, device=DEV)
+    nid_a, m_a, nL_a, nt_a = K.neighbor_pass_head(q, S0, st_leaf, st_score, st_ok, t_pos, cfg, leaf,
+                                                  (w1t, b1, w2, b2, cls), ksum=ks_a if pool else None,
+                                                  k=k if pool else None, lhat=lhat_a)
+    lhat_b = K.budget_head(q[:, :, 0], t_pos, w1t, b1, w2, b2, cls, ksum=ks_b if pool else None,
+                           k=k if pool else None)
+    nid_b, m_b, nL_b, nt_b = K.neighbor_pass(q, S0, st_leaf, st_score, st_ok, t_pos.view(B, 1), cfg, leaf,
+                                             lhat=lhat_b.view(B, H, 1))
+    torch.cuda.synchronize()
+    assert torch.equal(lhat_a, lhat_b)
+    assert torch.equal(ks_a, ks_b)
+    assert torch.equal(nid_a, nid_b) and torch.equal(m_a, m_b)
+    assert torch.equal(nL_a, nL_b) and torch.equal(nt_a, nt_b)
+    assert len(set(lhat_a.flatten().tolist())) > 1
+
+
 @pytest.mark.parametrize('leaf,arity,wmax,ns', [(8, 2, 4, 2), (4, 4, 3, 3), (16, 2, 6, 2)])
 def test_descent_writes_neighbour_store(leaf, arity, wmax, ns):
     """The descent's neighbour store (ta_tree_descend_store, ta_tree_descend_append_ex) against the reference's

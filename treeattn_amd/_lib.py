@@ -34,6 +34,12 @@ class LeafStoreOut(ctypes.Structure):
                 ('Tst', c_i32), ('n', c_i32)]
 
 
+class BudgetHeadIn(ctypes.Structure):
+    """ta_budget_head_in (include/treeattn.h)."""
+    _fields_ = [('w1t', c_vp), ('b1', c_vp), ('w2', c_vp), ('b2', c_vp), ('classes', c_vp), ('hid', c_i32),
+                ('ncls', c_i32), ('ksum', c_vp), ('k', c_vp), ('ksb', c_i64), ('ksh', c_i64), ('lhat', c_vp)]
+
+
 class StepLayer(ctypes.Structure):
     """ta_step_layer"""
     _fields_ = [('ln1', c_vp), ('c_attn', c_vp), ('c_proj', c_vp), ('ln2', c_vp), ('c_fc', c_vp), ('c_mlp', c_vp),
@@ -142,6 +148,10 @@ SIGNATURES = {
                                  c_i32, c_i32, c_f32, c_i32, c_f32, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'ta_budget_head': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                 c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
+    'ta_neighbor_pass_head': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp, c_i64,
+                                      c_i64, c_i64, c_i32, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                      c_f32, c_i32, c_f32, c_i32, _P(BudgetHeadIn), c_vp, c_vp, c_vp, c_vp,
+                                      c_vp]),
     'ta_leaf_store': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                               c_i32, c_vp]),
     'ta_logits_workspace_size': (c_i64, [c_i32, c_i32]),

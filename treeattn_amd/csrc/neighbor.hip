@@ -40,14 +40,89 @@ struct NbParams {
   uint8_t* match;             // out: matched slots
   int32_t* nL;                // out (B, H, Nq): distinct matched leaves
   int32_t* n_tree;            // out (B, H, Nq): tree leaves to use (with lhat)
+  ta_budget_head_in hd;       // with the budget head in the same launch (one query per (b, h)): its weights
+  int hd_F;                   // the head's feature count
 };
 
-template <typename T, int D>
+// LDS of the budget head's weights (floats): W1 transposed, W2, b1, b2, each rounded up to a copy round of 256
+__host__ __device__ inline int nb_head_words(int F, int hid, int ncls) {
+  return ((F * hid + 255) & ~255) + ((ncls * hid + 255) & ~255) + ((hid + 3) & ~3) + ((ncls + 3) & ~3);
+}
+
+// The budget head's class for one (sequence, head), by one wavefront: f holds its F features in LDS (the
+// one-hot block at D + 1 .. D + H is not read: the head's column D + 1 + h is added instead, the product with the
+// other zero features being exact zeros), hs its hid hidden units; W1 transposed (F x hid), W2 (ncls x hid) and
+// the biases in LDS.  hidden = relu(W1 f + b1) (lane j forms units j, j + 64, ...), logits = W2 hidden + b2 (wave
+// sums), the first maximum wins and a NaN logit counts as the maximum (torch's argmax).
+__device__ __forceinline__ int budget_class(const float* f, float* hs, const float* wl, const float* w2l,
+                                            const float* b1l, const float* b2l, int D, int H, int F, int hid,
+                                            int ncls, int h) {
+  const int lane = lane_id();
+  wave_sync();
+  for (int j = lane; j < hid; j += kWave) {
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int i = 0; i <= D; ++i) acc += wl[i * hid + j] * f[i];
+    acc += wl[(D + 1 + h) * hid + j];
+#pragma unroll 8
+    for (int i = D + 1 + H; i < F; ++i) acc += wl[i * hid + j] * f[i];
+    hs[j] = fmaxf(acc + b1l[j], 0.0f);
+  }
+  wave_sync();
+  int best = 0;
+  float bv = 0.0f;
+  for (int c = 0; c < ncls; ++c) {
+    float part = 0.0f;
+    for (int j = lane; j < hid; j += kWave) part += w2l[c * hid + j] * hs[j];
+    const float v = wave_sum(part) + b2l[c];
+    if (c == 0 || (!(bv != bv) && (v > bv || v != v))) {
+      best = c;
+      bv = v;
+    }
+  }
+  return best;
+}
+
+template <typename T, int D, bool HEAD>
 __global__ __launch_bounds__(256) void neighbor_kernel(NbParams p) {
   constexpr int R = D / 16;
   const int lane = lane_id();
-  const int64_t qi = (int64_t)blockIdx.x * 4 + wave_id();   // flat (b, h, n)
-  if (qi >= (int64_t)p.B * p.H * p.Nq) return;
+  const int64_t nq_all = (int64_t)p.B * p.H * p.Nq;
+  const int64_t q_flat = (int64_t)blockIdx.x * 4 + wave_id();   // flat (b, h, n)
+  const bool live = q_flat < nq_all;
+  if (!HEAD && !live) return;
+  // with the head every wavefront reaches its workgroup barrier: a wavefront past the end works on the last
+  // query and writes nothing
+  const int64_t qi = live ? q_flat : nq_all - 1;
+  extern __shared__ float nb_lds[];
+  float* w1l = nb_lds;
+  float* w2l = w1l + ((p.hd_F * p.hd.hid + 255) & ~255);
+  float* b1l = w2l + ((p.hd.ncls * p.hd.hid + 255) & ~255);
+  float* b2l = b1l + ((p.hd.hid + 3) & ~3);
+  float fq[(D + kWave - 1) / kWave], fs[(D + kWave - 1) / kWave], fk[(D + kWave - 1) / kWave];
+  if constexpr (HEAD) {
+    // the head's own inputs first (a wait for them must not wait for the copies below), then W1 and W2 into
+    // LDS by direct loads, 1 KB per wavefront round, in flight while the neighbour pass runs
+    const int bq = (int)(qi / p.H), hq = (int)(qi % p.H);
+#pragma unroll
+    for (int u = 0; u < (D + kWave - 1) / kWave; ++u) {
+      const int i = lane + u * kWave < D ? lane + u * kWave : D - 1;
+      fq[u] = to_f32(reinterpret_cast<const T*>(p.q)[bq * p.qsb + hq * p.qsh + i]);
+      fs[u] = p.hd.ksum != nullptr ? p.hd.ksum[qi * D + i] : 0.0f;
+      fk[u] = p.hd.k != nullptr ? to_f32(reinterpret_cast<const T*>(p.hd.k)[bq * p.hd.ksb + hq * p.hd.ksh + i])
+                                : 0.0f;
+    }
+    const int n1 = (p.hd_F * p.hd.hid + 255) >> 8, n2 = (p.hd.ncls * p.hd.hid + 255) >> 8;
+    for (int c = wave_id(); c < n1 + n2; c += 4) {
+      const bool first = c < n1;
+      const int cc = first ? c : c - n1;
+      const int nw = first ? p.hd_F * p.hd.hid : p.hd.ncls * p.hd.hid;
+      const int e = cc * 256 + lane * 4 < nw ? cc * 256 + lane * 4 : 0;   // a surplus lane copies word 0 again
+      const float* src = (first ? p.hd.w1t : p.hd.w2) + e;
+      float* dst = (first ? w1l : w2l) + cc * 256;
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)dst, 16, 0, 0);
+    }
+  }
   const int n = (int)(qi % p.Nq);
   const int bh = (int)(qi / p.Nq);
   const int b = bh / p.H, h = bh % p.H;
@@ -105,14 +180,44 @@ __global__ __launch_bounds__(256) void neighbor_kernel(NbParams p) {
   }
   const int nl = __popcll(__ballot(first));
 
+  int L = 0;
+  if constexpr (HEAD) {
+    const int F = p.hd_F, hid = p.hd.hid, ncls = p.hd.ncls;
+    float* f = b2l + ((ncls + 3) & ~3) + wave_id() * (F + hid);
+    float* hs = f + F;
+    if ((int)threadIdx.x < hid) b1l[threadIdx.x] = p.hd.b1[threadIdx.x];
+    if ((int)threadIdx.x < ncls) b2l[threadIdx.x] = p.hd.b2[threadIdx.x];
+    // features [q, log(|q| + 1e-6), one-hot(h), ksum / max(t, 1)]; the key sum then takes this step's key
+    float ss = 0.0f;
+    const float tt = (float)max(t, 1);
+#pragma unroll
+    for (int u = 0; u < (D + kWave - 1) / kWave; ++u) {
+      const int i = lane + u * kWave;
+      if (i < D) {
+        f[i] = fq[u];
+        ss += fq[u] * fq[u];
+        if (p.hd.ksum != nullptr) {
+          f[D + 1 + p.H + i] = fs[u] / tt;
+          if (live && p.hd.k != nullptr) p.hd.ksum[qi * D + i] = fs[u] + fk[u];
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) f[D] = logf(sqrtf(ss) + 1e-6f);
+    wait_vmcnt_n<0>();
+    __syncthreads();
+    if (!live) return;
+    L = p.hd.classes[budget_class(f, hs, w1l, w2l, b1l, b2l, D, p.H, F, hid, ncls, h)];
+    if (lane == 0 && p.hd.lhat != nullptr) p.hd.lhat[qi] = L;
+  }
   if (lane < S) {
     p.nid[qi * S + lane] = id;
     p.match[qi * S + lane] = m ? 1 : 0;
   }
   if (lane == 0) {
     p.nL[qi] = nl;
-    if (p.lhat != nullptr && p.n_tree != nullptr) {
-      const int L = p.lhat[qi];
+    if ((HEAD || p.lhat != nullptr) && p.n_tree != nullptr) {
+      if constexpr (!HEAD) L = p.lhat[qi];
       const int half = (L + 1) / 2;
       const int need = L - nl > 0 ? L - nl : 0;
       const int least = nl < half ? 2 : 1;
@@ -220,27 +325,7 @@ __global__ __launch_bounds__(kBhWaves * kWave) void budget_head_kernel(
   }
   __syncthreads();
   if (!live) return;
-  for (int j = lane; j < hid; j += kWave) {
-    float acc = 0.0f;
-#pragma unroll 8
-    for (int i = 0; i <= D; ++i) acc += wl[i * hid + j] * f[i];
-    acc += wl[(D + 1 + h) * hid + j];
-#pragma unroll 8
-    for (int i = D + 1 + H; i < F; ++i) acc += wl[i * hid + j] * f[i];
-    hs[j] = fmaxf(acc + b1l[j], 0.0f);
-  }
-  wave_sync();
-  int best = 0;
-  float bv = 0.0f;
-  for (int c = 0; c < ncls; ++c) {
-    float part = 0.0f;
-    for (int j = lane; j < hid; j += kWave) part += w2l[c * hid + j] * hs[j];
-    const float v = wave_sum(part) + b2l[c];
-    if (c == 0 || (!(bv != bv) && (v > bv || v != v))) {
-      best = c;
-      bv = v;
-    }
-  }
+  const int best = budget_class(f, hs, wl, w2l, b1l, b2l, D, H, F, hid, ncls, h);
   if (lane == 0) lhat[bh] = classes[best];
 }
 
@@ -300,13 +385,14 @@ extern "C" int ta_budget_head(const void* q, int q_dtype, int64_t qsb, int64_t q
   return check_launch("budget_head_kernel");
 }
 
-extern "C" int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const float* S0,
-                                int64_t ssb, int64_t ssh, int M, const int32_t* st_leaf, const float* st_score,
-                                const uint8_t* st_ok, int64_t st_sb, int64_t st_sh, int64_t st_st, int Tst,
-                                const int32_t* tq, int64_t tq_sb, int B, int H, int Nq, int D, int nb_window,
-                                int nb_store, int nb_probe, int nb_cap_min, float nb_rho, int neighbors, float scale,
-                                const int32_t* lhat, int wmax, int32_t* nid, uint8_t* match, int32_t* nL,
-                                int32_t* n_tree, void* stream) {
+namespace {
+int neighbor_pass_impl(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const float* S0,
+                       int64_t ssb, int64_t ssh, int M, const int32_t* st_leaf, const float* st_score,
+                       const uint8_t* st_ok, int64_t st_sb, int64_t st_sh, int64_t st_st, int Tst,
+                       const int32_t* tq, int64_t tq_sb, int B, int H, int Nq, int D, int nb_window,
+                       int nb_store, int nb_probe, int nb_cap_min, float nb_rho, int neighbors, float scale,
+                       const int32_t* lhat, int wmax, int32_t* nid, uint8_t* match, int32_t* nL,
+                       int32_t* n_tree, const ta_budget_head_in* hd, void* stream) {
   if (B <= 0 || H <= 0 || Nq <= 0 || M <= 0 || nb_window <= 0 || nb_store <= 0 || nb_window * nb_store > 64 ||
       nb_probe < 0 || Tst <= 0 || (D != 16 && D != 32 && D != 64 && D != 128 && D != 256) || q == nullptr || S0 == nullptr || st_leaf == nullptr ||
       st_score == nullptr || st_ok == nullptr || tq == nullptr || nid == nullptr || match == nullptr ||
@@ -322,11 +408,33 @@ extern "C" int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t
   }
   NbParams p{q, qsb, qsh, qsn, S0, ssb, ssh, M, st_leaf, st_score, st_ok, st_sb, st_sh, st_st, Tst, tq, tq_sb,
              B, H, Nq, nb_window, nb_store, nb_probe, nb_cap_min, neighbors, nb_rho, scale, lhat, wmax, nid, match,
-             nL, n_tree};
+             nL, n_tree, ta_budget_head_in{}, 0};
+  size_t lds = 0;
+  if (hd != nullptr) {
+    // the budget head in the same launch: one query per (b, h), W1 / W2 rows whole float4 words
+    const int F = D + 1 + H + (hd->ksum != nullptr ? D : 0);
+    lds = ((size_t)nb_head_words(F, hd->hid, hd->ncls) + (size_t)4 * (F + hd->hid)) * sizeof(float);
+    if (Nq != 1 || lhat != nullptr || n_tree == nullptr || hd->w1t == nullptr || hd->b1 == nullptr ||
+        hd->w2 == nullptr || hd->b2 == nullptr || hd->classes == nullptr || hd->hid <= 0 || hd->hid > 256 ||
+        (hd->hid & 3) || hd->ncls <= 0 || hd->ncls > 64 || ((uintptr_t)hd->w1t & 15) || ((uintptr_t)hd->w2 & 15) ||
+        (hd->k != nullptr && hd->ksum == nullptr) || lds > 160 * 1024) {
+      set_error("ta_neighbor_pass_head: one query per (b, h), no lhat, n_tree given; hid <= 256 and a multiple of "
+                "4, classes <= 64, W1 and W2 16-byte aligned, weights within 160 KB of LDS");
+      return TA_ERR_ARG;
+    }
+    p.hd = *hd;
+    p.hd_F = F;
+  }
   const int64_t nqry = (int64_t)B * H * Nq;
   const dim3 grid((unsigned)((nqry + 3) / 4));
   hipStream_t st = (hipStream_t)stream;
-#define TA_NB(TT, DD) hipLaunchKernelGGL((neighbor_kernel<TT, DD>), grid, dim3(256), 0, st, p)
+#define TA_NB(TT, DD)                                                                          \
+  do {                                                                                         \
+    if (hd != nullptr)                                                                         \
+      hipLaunchKernelGGL((neighbor_kernel<TT, DD, true>), grid, dim3(256), lds, st, p);        \
+    else                                                                                       \
+      hipLaunchKernelGGL((neighbor_kernel<TT, DD, false>), grid, dim3(256), 0, st, p);         \
+  } while (0)
 #define TA_NB_D(TT)                          \
   switch (D) {                               \
     case 16: TA_NB(TT, 16); break;           \
@@ -344,4 +452,33 @@ extern "C" int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t
 #undef TA_NB_D
 #undef TA_NB
   return check_launch("neighbor_kernel");
+}
+}  // namespace
+
+extern "C" int ta_neighbor_pass(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const float* S0,
+                                int64_t ssb, int64_t ssh, int M, const int32_t* st_leaf, const float* st_score,
+                                const uint8_t* st_ok, int64_t st_sb, int64_t st_sh, int64_t st_st, int Tst,
+                                const int32_t* tq, int64_t tq_sb, int B, int H, int Nq, int D, int nb_window,
+                                int nb_store, int nb_probe, int nb_cap_min, float nb_rho, int neighbors, float scale,
+                                const int32_t* lhat, int wmax, int32_t* nid, uint8_t* match, int32_t* nL,
+                                int32_t* n_tree, void* stream) {
+  return neighbor_pass_impl(q, q_dtype, qsb, qsh, qsn, S0, ssb, ssh, M, st_leaf, st_score, st_ok, st_sb, st_sh, st_st,
+                            Tst, tq, tq_sb, B, H, Nq, D, nb_window, nb_store, nb_probe, nb_cap_min, nb_rho, neighbors,
+                            scale, lhat, wmax, nid, match, nL, n_tree, nullptr, stream);
+}
+
+extern "C" int ta_neighbor_pass_head(const void* q, int q_dtype, int64_t qsb, int64_t qsh, const float* S0,
+                                     int64_t ssb, int64_t ssh, int M, const int32_t* st_leaf, const float* st_score,
+                                     const uint8_t* st_ok, int64_t st_sb, int64_t st_sh, int64_t st_st, int Tst,
+                                     const int32_t* t_pos, int B, int H, int D, int nb_window, int nb_store,
+                                     int nb_probe, int nb_cap_min, float nb_rho, int neighbors, float scale, int wmax,
+                                     const ta_budget_head_in* head, int32_t* nid, uint8_t* match, int32_t* nL,
+                                     int32_t* n_tree, void* stream) {
+  if (head == nullptr) {
+    set_error("ta_neighbor_pass_head: head missing");
+    return TA_ERR_ARG;
+  }
+  return neighbor_pass_impl(q, q_dtype, qsb, qsh, 0, S0, ssb, ssh, M, st_leaf, st_score, st_ok, st_sb, st_sh, st_st,
+                            Tst, t_pos, 1, B, H, 1, D, nb_window, nb_store, nb_probe, nb_cap_min, nb_rho, neighbors,
+                            scale, nullptr, wmax, nid, match, nL, n_tree, head, stream);
 }

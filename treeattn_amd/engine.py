@@ -357,12 +357,17 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     leaf = state.shape.leaf
     tpos = state._tpos(t)
     scale = 1.0 / math.sqrt(dh)
-    lhat = _pw_budget(state, pw, q, tpos, k=k[:, :, 0] if update else None)
-    pooled = lhat is not None and cfg.global_pool and update   # the budget head's launch added k to ksum
+    # the budget head runs in the neighbour pass's launch when there is one (its hidden width a multiple of 4),
+    # else in its own
+    head = (_budget_weights(state, pw) if cfg.beam_mode == 'pred' and state.shape.n_levels else None)
+    if head is not None and head[0].shape[1] % 4:
+        head = None
+    lhat = None if head is not None else _pw_budget(state, pw, q, tpos, k=k[:, :, 0] if update else None)
+    pooled = cfg.beam_mode == 'pred' and cfg.global_pool and update   # the head's launch adds k to ksum
     wl = state.shape.leaf_width(cfg.wmax)
     if scratch is None:
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
-    structural = (not cfg.neighbors) and lhat is None
+    structural = (not cfg.neighbors) and cfg.beam_mode != 'pred'
     # the descent's launch also appends (row t and the nodes ending at t, which the descent does not read); with
     # the gate it scores the gated vectors while the append forms the raw sums, and the gate's node update follows
     appendable = update and B * H < 4096 and q.dtype == k.dtype == state.dtype
@@ -406,12 +411,17 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     # leaves of this descent are stored for position t (engine.py:103-105); the attention takes the first
     # n_tree tree leaves and the matched neighbour leaves, each block once, with the own block and static keys
     # (engine.py:107-119).
-    if lhat is None:
+    if lhat is None and head is None:
         if scratch.lhat is None:
             scratch.lhat = torch.full((B, H, 1), cfg.beam, dtype=torch.int32, device=q.device)
         lhat = scratch.lhat
     NS = cfg.nb_store
-    if state.shape.n_levels:
+    if head is not None:
+        pool = state.ksum if cfg.global_pool else None
+        nid, match, nL, n_tree = K.neighbor_pass_head(q, state.score_levels[0], state.st_leaf, state.st_score,
+                                                      state.st_ok, tpos, cfg, leaf, head, ksum=pool,
+                                                      k=k[:, :, 0] if update and pool is not None else None)
+    elif state.shape.n_levels:
         nid, match, nL, n_tree = K.neighbor_pass(q, state.score_levels[0], state.st_leaf, state.st_score, state.st_ok,
                                                  tpos.view(B, 1), cfg, leaf, lhat=lhat.view(B, H, 1))
     else:

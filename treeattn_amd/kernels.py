@@ -404,6 +404,52 @@ def neighbor_pass(q, S0, st_leaf, st_score, st_ok, tq, cfg, leaf, lhat=None):
     return nid, match, nL
 
 
+def neighbor_pass_head(q, S0, st_leaf, st_score, st_ok, t_pos, cfg, leaf, head, ksum=None, k=None, lhat=None):
+    """The budget head and neighbour borrowing of one decode position per (sequence, head) in one launch
+    (ta_neighbor_pass_head; engine.py:89-102, seg.py:73-117): q (B,H,1,D), t_pos (B,) int32, head = (w1t, b1, w2,
+    b2, classes) as budget_head takes them (hid a multiple of 4), ksum / k as for budget_head, lhat (B,H) int32 to
+    receive the budgets or None.  Returns (nid, match, nL, n_tree) as neighbor_pass with lhat does."""
+    L.require_gpu(q, S0, st_leaf, st_score, st_ok, t_pos)
+    B, H, Nq, D = q.shape
+    Wn, NS = int(cfg.nb_window), int(cfg.nb_store)
+    w1t, b1, w2, b2, classes = head
+    hid, ncls = w1t.shape[1], w2.shape[0]
+    F = D + 1 + H + (D if ksum is not None else 0)
+    if Nq != 1 or q.stride(3) != 1 or t_pos.dtype != torch.int32 or not t_pos.is_contiguous() or t_pos.numel() != B:
+        raise ValueError('neighbor_pass_head: one query per (sequence, head), contiguous rows, t_pos int32 (B,)')
+    if st_leaf.dtype != torch.int32 or st_score.dtype != torch.float32 or st_ok.dtype != torch.bool:
+        raise TypeError('neighbor_pass_head: st_leaf int32, st_score float32, st_ok bool')
+    if S0.dtype != torch.float32 or S0.stride(3) != 1 or S0.stride(2) != D:
+        raise ValueError('neighbor_pass_head: S0 float32 with contiguous rows')
+    if not (st_leaf.stride() == st_score.stride() == st_ok.stride()) or st_leaf.stride(3) != 1:
+        raise ValueError('neighbor_pass_head: st_* must share one layout with the entries of a position contiguous')
+    for t, shp in ((w1t, (F, hid)), (b1, (hid,)), (w2, (ncls, hid)), (b2, (ncls,))):
+        if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != shp:
+            raise ValueError('neighbor_pass_head: weights float32 contiguous, W1 transposed (%d, %d)' % (F, hid))
+    if classes.dtype != torch.int32 or classes.numel() != ncls:
+        raise ValueError('neighbor_pass_head: classes int32 (ncls,)')
+    if ksum is not None and (ksum.dtype != torch.float32 or not ksum.is_contiguous() or ksum.shape != (B, H, D)):
+        raise ValueError('neighbor_pass_head: ksum float32 contiguous (B,H,D)')
+    if k is not None and (ksum is None or k.shape != (B, H, D) or k.dtype != q.dtype or k.stride(-1) != 1):
+        raise ValueError('neighbor_pass_head: k (B,H,D) of q\'s dtype with unit last stride, and ksum')
+    if lhat is not None and (lhat.dtype != torch.int32 or not lhat.is_contiguous() or lhat.numel() != B * H):
+        raise ValueError('neighbor_pass_head: lhat int32 contiguous (B,H)')
+    hd = L.BudgetHeadIn(w1t.data_ptr(), b1.data_ptr(), w2.data_ptr(), b2.data_ptr(), classes.data_ptr(), hid, ncls,
+                        ksum.data_ptr() if ksum is not None else None, k.data_ptr() if k is not None else None,
+                        k.stride(0) if k is not None else 0, k.stride(1) if k is not None else 0,
+                        lhat.data_ptr() if lhat is not None else None)
+    nid = torch.empty(B, H, 1, Wn * NS, device=q.device, dtype=torch.int32)
+    match = torch.empty(B, H, 1, Wn * NS, device=q.device, dtype=torch.bool)
+    nL = torch.empty(B, H, 1, device=q.device, dtype=torch.int32)
+    n_tree = torch.empty(B, H, 1, device=q.device, dtype=torch.int32)
+    L.call('ta_neighbor_pass_head', L.ptr(q), L.dtype_code(q), q.stride(0), q.stride(1), L.ptr(S0), S0.stride(0),
+           S0.stride(1), S0.shape[2], L.ptr(st_leaf), L.ptr(st_score), L.ptr(st_ok), st_leaf.stride(0),
+           st_leaf.stride(1), st_leaf.stride(2), st_leaf.shape[2], L.ptr(t_pos), B, H, D, Wn, NS,
+           int(cfg.nb_probe), int(cfg.nb_cap_min), float(cfg.nb_rho), 1 if cfg.neighbors else 0, 1.0 / float(leaf),
+           int(cfg.wmax), ctypes.byref(hd), L.ptr(nid), L.ptr(match), L.ptr(nL), L.ptr(n_tree), L.stream())
+    return nid, match, nL, n_tree
+
+
 def gather_dot_blocks(q, K, blk, block, scale=1.0, out=None):
     """Leaf-block gather-dot: out[..., c*block + j] = scale * q . K[blk[..., c]*block + j]."""
     L.require_gpu(q, K, blk)
