@@ -147,7 +147,9 @@ int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int64_t qsh, i
  * levels the append forms its nodes in when they are not the scored ones (the mean-log gate: gated levels are
  * scored from their gated vectors while the append forms the raw sums; the gate's own node update follows as
  * ta_gate_append), and store (or NULL) the position's neighbour store (engine.py:103-105), as
- * ta_tree_descend_store writes it.
+ * ta_tree_descend_store writes it.  gate_lg (n_levels log-sum levels, or NULL) with gate_out (gated-vector levels,
+ * NULL entries where a level is not gated, or NULL) and gate_q: the same launch then does ta_gate_append's work for
+ * the nodes the append completes (the levels sharing the append levels' strides; D <= 128).
  */
 int ta_tree_descend_append_ex(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
                               const int32_t* t_pos, int n_levels, float* const* lv_ptr, const int64_t* lv_sb,
@@ -156,7 +158,8 @@ int ta_tree_descend_append_ex(const void* q, int dtype, int64_t qsb, int64_t qsh
                               const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
                               int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst, int Tcap,
                               const ta_kv_pages* pages, float* const* app_lv_ptr, const int64_t* app_lv_sb,
-                              const int64_t* app_lv_sh, const ta_leaf_store_out* store, void* stream);
+                              const int64_t* app_lv_sh, float* const* gate_lg, float* const* gate_out,
+                              float gate_q, const ta_leaf_store_out* store, void* stream);
 
 /*
  * Scores of queries against gathered rows (replaces fastseg.py:118-130 gather_dot and its kernel

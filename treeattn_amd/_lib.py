@@ -83,8 +83,8 @@ SIGNATURES = {
     'ta_tree_descend_append_ex': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_i32, _P(c_vp),
                                           _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
                                           c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
-                                          c_i64, c_i32, _P(KvPages), _P(c_vp), _P(c_i64), _P(c_i64),
-                                          _P(LeafStoreOut), c_vp]),
+                                          c_i64, c_i32, _P(KvPages), _P(c_vp), _P(c_i64), _P(c_i64), _P(c_vp),
+                                          _P(c_vp), c_f32, _P(LeafStoreOut), c_vp]),
     'ta_seg_attend': (c_i32, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32,
                               c_i32, c_vp, c_i32, _P(c_vp), _P(c_i64), _P(c_i64), c_i32, c_i32, c_i32, c_i32, c_i32,
                               c_vp, c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_i32, c_f32, c_vp, c_vp, c_vp, c_vp,

@@ -10,6 +10,7 @@
 #include "append.hpp"
 #include "common.hpp"
 #include "descend.hpp"
+#include "gate.hpp"
 
 namespace ta {
 
@@ -98,14 +99,35 @@ __global__ __launch_bounds__(256) void level_pass_kernel(const T* __restrict__ i
 }
 
 // ----------------------------------------------------------------------------------------- descent
+// The mean-log gate's share of a fused decode append: the log-sum and gated-vector levels (same strides as the
+// levels the append forms; out[j] null where the level is not gated) and the quantile's order statistic / weight.
+struct GateAppendIn {
+  float* lg[kMaxLevels];
+  float* out[kMaxLevels];
+  int lo;
+  float w;
+};
+
+// The gate append's view of a fused descent's levels: the raw sums are the append's own targets.
+struct DescentGateView {
+  const LevelIn& raw_lv;
+  const GateAppendIn& ga;
+  __device__ __forceinline__ const float* raw(int j) const { return raw_lv.ptr[j]; }
+  __device__ __forceinline__ float* lg(int j) const { return ga.lg[j]; }
+  __device__ __forceinline__ float* out(int j) const { return ga.out[j]; }
+  __device__ __forceinline__ int64_t sb(int j) const { return raw_lv.sb[j]; }
+  __device__ __forceinline__ int64_t sh(int j) const { return raw_lv.sh[j]; }
+  __device__ __forceinline__ int blevel(int j) const { return raw_lv.blevel[j]; }
+};
+
 // Descent of one query per WPQ wavefronts; with APPEND (one query per (sequence, head)) the decode-cache
 // append of ap (rows of the query's element type) runs in the same launch.
-template <typename TQ, int D, int WPQ, bool APPEND>
+template <typename TQ, int D, int WPQ, bool APPEND, bool GATE>
 __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
     const TQ* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qsn, int H, int Nq, int T,
     const int32_t* __restrict__ tq, int64_t tq_sb, LevelIn lv, int n_levels, int arity_log2, int wmax, int wl,
     int cmax4, int32_t* __restrict__ ids, uint8_t* __restrict__ vld, float* __restrict__ sct, AppendIn ap,
-    LevelIn alv, ta_leaf_store_out so) {
+    LevelIn alv, ta_leaf_store_out so, GateAppendIn ga) {
   constexpr int NT = kWave * WPQ;      // threads per query
   extern __shared__ int32_t smem_i[];
   const int lane = lane_id(), w = wave_id();
@@ -158,6 +180,15 @@ __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
       so.leaf[sbase + r] = ok ? max(kid[r], 0) : 0;
       so.score[sbase + r] = ok ? ksc[r] : 0.0f;
       so.ok[sbase + r] = ok ? 1 : 0;
+    }
+  }
+  if constexpr (APPEND && GATE) {
+    // the gate's share of the append when position t completes a leaf block (one query per workgroup, so the
+    // condition is the workgroup's): the block's keys and the raw nodes the append formed, written by this
+    // workgroup's threads, are read back by its first wavefront after a barrier
+    if (t >= 0 && t < ap.Tcap && n_levels > 0 && ((t + 1) & ((1 << lv.blevel[0]) - 1)) == 0) {
+      __syncthreads();
+      if (w == 0) gate_append_wave<TQ, D>(ap, DescentGateView{alv, ga}, n_levels, arity_log2, b, h, t, ga.lo, ga.w);
     }
   }
 }
@@ -295,7 +326,7 @@ struct DescendRun {
   static int run(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, int B, int H, int Nq, const int32_t* tq,
                  int64_t tq_sb, const LevelIn& lv, int n_levels, int Tgeo, int arity_log2, int wmax, int wl,
                  int32_t* ids, uint8_t* vld, float* sct, const AppendIn* ap, const LevelIn* alv,
-                 const ta_leaf_store_out* so, hipStream_t st) {
+                 const ta_leaf_store_out* so, const GateAppendIn* ga, hipStream_t st) {
     const int arity = 1 << arity_log2;
     const int cmax4 = (arity * wmax + arity - 1 + 3) & ~3;
     const int wmax4 = (wmax + 3) & ~3;
@@ -320,17 +351,21 @@ struct DescendRun {
     dim3 grid((Nq + qpb - 1) / qpb, B * H);
     const AppendIn none{};
     const ta_leaf_store_out no_store{};
-#define TA_DESC(WPQ, NTH, APP)                                                                                   \
-  hipLaunchKernelGGL((descend_kernel<T, D, WPQ, APP>), grid, dim3(NTH), lds, st, (const T*)q, qsb, qsh, qsn, H, Nq, \
-                     Tgeo, tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct, ap ? *ap : none, \
-                     alv ? *alv : lv, so ? *so : no_store)
-    if (ap) {
-      if (wpq == 16) TA_DESC(16, 1024, true);
-      else TA_DESC(4, 256, true);
+    const GateAppendIn no_gate{};
+#define TA_DESC(WPQ, NTH, APP, GT)                                                                                \
+  hipLaunchKernelGGL((descend_kernel<T, D, WPQ, APP, GT>), grid, dim3(NTH), lds, st, (const T*)q, qsb, qsh, qsn, H, \
+                     Nq, Tgeo, tq, tq_sb, lv, n_levels, arity_log2, wmax, wl, cmax4, ids, vld, sct,                  \
+                     ap ? *ap : none, alv ? *alv : lv, so ? *so : no_store, ga ? *ga : no_gate)
+    if (ap && ga) {
+      if (wpq == 16) TA_DESC(16, 1024, true, true);
+      else TA_DESC(4, 256, true, true);
+    } else if (ap) {
+      if (wpq == 16) TA_DESC(16, 1024, true, false);
+      else TA_DESC(4, 256, true, false);
     } else {
-      if (wpq == 16) TA_DESC(16, 1024, false);
-      else if (wide) TA_DESC(4, 256, false);
-      else TA_DESC(1, 256, false);
+      if (wpq == 16) TA_DESC(16, 1024, false, false);
+      else if (wide) TA_DESC(4, 256, false, false);
+      else TA_DESC(1, 256, false, false);
     }
 #undef TA_DESC
     return check_launch("descend_kernel");
@@ -477,7 +512,7 @@ int tree_descend_impl(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int6
   }
   return dispatch_dt_d<DescendRun>(q_dtype, D, q, qsb, qsh, qsn, B, H, Nq, tq, tq_sb, lv, n_levels, T, arity_log2,
                                    wmax, wl, ids, vld, sct, (const AppendIn*)nullptr, (const LevelIn*)nullptr, so,
-                                   (hipStream_t)stream);
+                                   (const GateAppendIn*)nullptr, (hipStream_t)stream);
 }
 
 int tree_descend_append_impl(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
@@ -486,8 +521,8 @@ int tree_descend_append_impl(const void* q, int dtype, int64_t qsb, int64_t qsh,
                              int32_t* ids, uint8_t* vld, float* sct, const void* k_new, const void* v_new,
                              int64_t nsb, int64_t nsh, int64_t vnsb, int64_t vnsh, void* Kc, void* Vc, int64_t csb,
                              int64_t csh, int64_t cst, int Tcap, const ta_kv_pages* pages, float* const* app_ptr,
-                             const int64_t* app_sb, const int64_t* app_sh, const ta_leaf_store_out* so,
-                             void* stream) {
+                             const int64_t* app_sb, const int64_t* app_sh, float* const* gate_lg,
+                             float* const* gate_out, float gate_q, const ta_leaf_store_out* so, void* stream) {
   if (B <= 0 || H <= 0 || wmax < 1 || wl < 0 || n_levels < 0 || n_levels > kMaxLevels || !pow2(T) ||
       leaf_log2 < 1 || leaf_log2 > 14 || arity_log2 < 1 || arity_log2 > 4 || Tcap <= 0 || D > 256 ||
       !store_ok(so, wl)) {
@@ -537,9 +572,27 @@ int tree_descend_append_impl(const void* q, int dtype, int64_t qsb, int64_t qsh,
       }
     }
   }
+  // the gate's log sums and gated vectors of the nodes the append completes (the leaf level log-summed even
+  // when no level is gated)
+  GateAppendIn ga{};
+  if (gate_lg != nullptr) {
+    if (n_levels == 0 || !(gate_q >= 0.0f && gate_q <= 1.0f) || leaf_log2 > 14 || D > 128) {
+      set_error("ta_tree_descend_append_ex: gate needs levels, gate_q in [0, 1], leaf <= 2^14, D <= 128");
+      return TA_ERR_ARG;
+    }
+    for (int j = 0; j < n_levels; ++j) {
+      ga.lg[j] = gate_lg[j];
+      ga.out[j] = gate_out != nullptr ? gate_out[j] : nullptr;
+      if (ga.lg[j] == nullptr) {
+        set_error("ta_tree_descend_append_ex: a log-sum level is missing");
+        return TA_ERR_ARG;
+      }
+    }
+    gate_rank(gate_q, D, ga.lo, ga.w);
+  }
   return dispatch_dt_d<DescendRun>(dtype, D, q, qsb, qsh, (int64_t)0, B, H, 1, t_pos, (int64_t)1, lv, n_levels, T,
                                    arity_log2, wmax, wl, ids, vld, sct, (const AppendIn*)&ap, (const LevelIn*)&alv,
-                                   so, (hipStream_t)stream);
+                                   so, gate_lg != nullptr ? &ga : (const GateAppendIn*)nullptr, (hipStream_t)stream);
 }
 }  // namespace
 
@@ -574,7 +627,8 @@ extern "C" int ta_tree_descend_append(const void* q, int dtype, int64_t qsb, int
                                       int Tcap, const ta_kv_pages* pages, void* stream) {
   return tree_descend_append_impl(q, dtype, qsb, qsh, B, H, D, t_pos, n_levels, lv_ptr, lv_sb, lv_sh, T, leaf_log2,
                                   arity_log2, wmax, wl, ids, vld, sct, k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc,
-                                  csb, csh, cst, Tcap, pages, nullptr, nullptr, nullptr, nullptr, stream);
+                                  csb, csh, cst, Tcap, pages, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f,
+                                  nullptr, stream);
 }
 
 extern "C" int ta_tree_descend_append_ex(const void* q, int dtype, int64_t qsb, int64_t qsh, int B, int H, int D,
@@ -584,11 +638,13 @@ extern "C" int ta_tree_descend_append_ex(const void* q, int dtype, int64_t qsb, 
                                          const void* k_new, const void* v_new, int64_t nsb, int64_t nsh, int64_t vnsb,
                                          int64_t vnsh, void* Kc, void* Vc, int64_t csb, int64_t csh, int64_t cst,
                                          int Tcap, const ta_kv_pages* pages, float* const* app_lv_ptr,
-                                         const int64_t* app_lv_sb, const int64_t* app_lv_sh,
-                                         const ta_leaf_store_out* store, void* stream) {
+                                         const int64_t* app_lv_sb, const int64_t* app_lv_sh, float* const* gate_lg,
+                                         float* const* gate_out, float gate_q, const ta_leaf_store_out* store,
+                                         void* stream) {
   return tree_descend_append_impl(q, dtype, qsb, qsh, B, H, D, t_pos, n_levels, lv_ptr, lv_sb, lv_sh, T, leaf_log2,
                                   arity_log2, wmax, wl, ids, vld, sct, k_new, v_new, nsb, nsh, vnsb, vnsh, Kc, Vc,
-                                  csb, csh, cst, Tcap, pages, app_lv_ptr, app_lv_sb, app_lv_sh, store, stream);
+                                  csb, csh, cst, Tcap, pages, app_lv_ptr, app_lv_sb, app_lv_sh, gate_lg, gate_out,
+                                  gate_q, store, stream);
 }
 
 extern "C" int ta_gather_dot(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qsn, const void* S,

@@ -369,7 +369,8 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         scratch = _Scratch(B, H, dh, wl, q.device, decode_nsplit(B, H, wl, leaf))
     structural = (not cfg.neighbors) and cfg.beam_mode != 'pred'
     # the descent's launch also appends (row t and the nodes ending at t, which the descent does not read); with
-    # the gate it scores the gated vectors while the append forms the raw sums, and the gate's node update follows
+    # the gate it scores the gated vectors while the append forms the raw sums, then the gate's log sums and gated
+    # vectors of those nodes
     appendable = update and B * H < 4096 and q.dtype == k.dtype == state.dtype
     fused = structural and appendable and not state.gated
     Kc, Vc = state.kv()
@@ -388,7 +389,9 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         # descent and cache append in one launch (the append touches only row t and the nodes ending at t)
         ids, vld, sct = K.tree_descend_append(q, state.score_levels, tpos, state.shape, cfg.wmax, k[:, :, 0],
                                               v[:, :, 0], Kc, Vc, out=(scratch.ids, scratch.vld, scratch.sct),
-                                              store=store, app_levels=state.levels if state.gated else None)
+                                              store=store, app_levels=state.levels if state.gated else None,
+                                              gate=(state.lg, state.gl, cfg.gate_q)
+                                              if state.gated and state.shape.n_levels else None)
     else:
         ids, vld, sct = K.tree_descend(q, state.score_levels, tpos.view(B, 1), state.shape, cfg.wmax,
                                        out=(scratch.ids, scratch.vld, scratch.sct), store=store)
@@ -396,7 +399,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         if update:
             if not appendable:
                 K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
-            state.gate_append(tpos)
+                state.gate_append(tpos)
             if cfg.global_pool:
                 state.ksum += k[:, :, 0].float()
         out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
@@ -432,7 +435,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
     if update:
         if not appendable:
             K.kv_append(k[:, :, 0], v[:, :, 0], Kc, Vc, tpos, state.levels, leaf, state.shape.arity)
-        state.gate_append(tpos)
+            state.gate_append(tpos)
         if cfg.global_pool and not pooled:
             state.ksum += k[:, :, 0].float()
     out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)

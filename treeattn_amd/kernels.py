@@ -238,12 +238,15 @@ def tree_descend(q, levels, tq, shape, wmax, out=None, store=None):
     return ids, vld, sct
 
 
-def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out, store=None, app_levels=None):
+def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out, store=None, app_levels=None,
+                        gate=None):
     """Decode step's descent of q (B,H,1,D) at t_pos (B,) int32 and, in the same launch, the cache append of
     k_new, v_new (B,H,D) at row t_pos[b] of the cache (Kc, Vc (B,H,Tcap,D), or a PagedCache as Kc) with node
     formation.  out = (ids, vld, sct) buffers (B,H,1,wl); store as for tree_descend.  app_levels: the levels the
     append forms its nodes in when they are not the scored `levels` (with the mean-log gate: the raw sums, the
-    scored levels holding gated vectors where the gate applies)."""
+    scored levels holding gated vectors where the gate applies).  gate = (lg, gl, gate_q): the same launch then
+    does gate_append's work (log sums, and gated vectors where gl[j] is not None) for the nodes the append
+    completes."""
     L.require_gpu(q, t_pos, k_new, v_new, *_cache_tensors(Kc, Vc))
     B, H, Nq, D = q.shape
     if Nq != 1 or t_pos.dtype != torch.int32 or not t_pos.is_contiguous():
@@ -260,7 +263,7 @@ def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out
             L.i64_array([t.stride(1) for t in levels]), shape.T, shape.l0, shape.s, int(wmax), wl, L.ptr(ids),
             L.ptr(vld), L.ptr(sct), L.ptr(k_new), L.ptr(v_new), k_new.stride(0), k_new.stride(1), v_new.stride(0),
             v_new.stride(1), kp, vp, csb, csh, cst, tcap, pages]
-    if store is None and app_levels is None:
+    if store is None and app_levels is None and gate is None:
         L.call('ta_tree_descend_append', *args, L.stream())
     else:
         so = ctypes.byref(_store_out(store, wl)) if store is not None else None
@@ -272,7 +275,19 @@ def tree_descend_append(q, levels, t_pos, shape, wmax, k_new, v_new, Kc, Vc, out
                   L.i64_array([t.stride(1) for t in app_levels]))
         else:
             ap = (None, None, None)
-        L.call('ta_tree_descend_append_ex', *args, *ap, so, L.stream())
+        if gate is not None:
+            lg, gl, gate_q = gate
+            tgt = app_levels if app_levels is not None else levels
+            if len(lg) != len(tgt) or len(gl) != len(tgt) or any(
+                    a.shape != r.shape or a.stride() != r.stride() or a.dtype != torch.float32
+                    for a, r in zip(list(lg) + [x for x in gl if x is not None],
+                                    list(tgt) + [r for x, r in zip(gl, tgt) if x is not None])):
+                raise ValueError('tree_descend_append: gate levels must match the appended levels in shape and strides')
+            gp = (L.ptr_array(lg), (ctypes.c_void_p * len(gl))(*[x.data_ptr() if x is not None else None for x in gl]),
+                  float(gate_q))
+        else:
+            gp = (None, None, 0.0)
+        L.call('ta_tree_descend_append_ex', *args, *ap, *gp, so, L.stream())
     return ids, vld, sct
 
 
