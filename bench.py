@@ -106,21 +106,55 @@ def descent_nodes(t, shape, wmax):
     return total
 
 
-def recorded_traffic(name):
-    """HBM bytes per launch of a kernel from the committed rocprofv3 counter summary (FETCH_SIZE and
-    WRITE_SIZE passes scaled by a calibration copy), or None when not recorded."""
+def recorded_traffic(name, live_bytes):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter summaries (FETCH_SIZE and
+    WRITE_SIZE passes scaled by a calibration copy), as (traffic, note).  A summary line reads
+    `traffic_bytes_per_launch <name>: <traffic> algorithmic <bytes>`, the algorithmic bytes being those of the
+    launches the counters were read on.  The figure describes this run's launch only when those bytes equal
+    live_bytes within 1 %; otherwise (or when nothing is recorded) the traffic is None and the note says why."""
     pdir = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles')
     try:
         names = sorted(os.listdir(pdir))
     except OSError:
-        return None
+        names = []
     for fn in names:
         if not fn.endswith('.md'):
             continue
         for line in open(os.path.join(pdir, fn)):
-            if line.startswith('traffic_bytes_per_launch ' + name + ':'):
-                return int(line.split(':')[1])
-    return None
+            if not line.startswith('traffic_bytes_per_launch ' + name + ':'):
+                continue
+            parts = line.split(':', 1)[1].split()
+            if len(parts) < 3 or parts[1] != 'algorithmic':
+                return None, 'profiles/%s records no algorithmic bytes beside the traffic' % fn
+            traffic, algo = int(parts[0]), int(parts[2])
+            dev = abs(algo - live_bytes) / max(live_bytes, 1)
+            if dev > 0.01:
+                return None, ('profiles/%s was measured on launches of %d algorithmic bytes, %.1f %% away from '
+                              'this run\'s %d' % (fn, algo, 100 * dev, int(live_bytes)))
+            return traffic, ('profiles/%s (rocprofv3 FETCH_SIZE and WRITE_SIZE passes, calibrated on a copy); '
+                             'traffic / algorithmic bytes = %.4f on the launches measured' % (fn, traffic / algo))
+    return None, 'no counter summary for %s under profiles/' % name
+
+
+def set_traffic(roof, name):
+    """Fill roofline['traffic'] (HBM bytes per launch from the counter summary, or None) and its note."""
+    traffic, note = recorded_traffic(name, roof['bytes_per_launch'])
+    roof['traffic'] = traffic
+    roof['traffic_note'] = note
+    if traffic is not None:
+        roof['traffic_over_algorithmic'] = round(traffic / roof['bytes_per_launch'], 4)
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), for the CPU baseline lines."""
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or 'unknown'
 
 
 def time_launches(fn, iters, flush=None):
@@ -199,14 +233,16 @@ def gather_dot_bench(args):
            'config': {'workload': leg['workload'], 'bytes_per_call': leg['bytes_per_call']},
            'roofline': {'bound': 'hbm', 'kernel': 'gather_pairs_kernel (matrix-core block-major gather-dot)',
                         'achieved': leg['GB/s'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': leg['frac_of_hbm'],
-                        'traffic': recorded_traffic('gather_pairs_kernel'), 'bytes_per_launch': leg['bytes_per_call'],
+                        'bytes_per_launch': leg['bytes_per_call'],
                         'avg_us': leg['avg_us'], 'timing': 'cold caches (1 GiB read before each of 20 launches)'},
            'parity': {'slice': [0, 0], 'max_rel_err_vs_oracle': float('%.3g' % rel), 'bar': 2e-5},
            'cpu_baseline': {'value': round(bytes_slice / slice_s / 1e9, 3), 'unit': 'GB/s', 'cores': ncores,
+                            'cpu_model': cpu_model(),
                             'kind': 'port',
                             'sample': 'oracle gather_dot (the reference op chain, torch CPU) over one of the %d '
                                       '(b, h) slices (4096 queries in 512-query tiles), median of 3; GB/s of that '
                                       'slice\'s compulsory bytes' % (B * H)}}
+    set_traffic(res['roofline'], 'gather_pairs_kernel')
     return res
 
 
@@ -299,7 +335,8 @@ def cpu_baseline_leg(args, cfg, W, dec, t_now, tok_now, budget_s, max_steps=64, 
             break
     times.sort()
     med = times[len(times) // 2]
-    return {'value': round(1.0 / med, 3), 'unit': 'tokens/s', 'cores': ncores, 'kind': 'port',
+    return {'value': round(1.0 / med, 3), 'unit': 'tokens/s', 'cores': ncores, 'cpu_model': cpu_model(),
+            'kind': 'port',
             'sample': '%d greedy decode steps of 1 of the %d sequences from the GPU state at position %d, '
                       'oracle engine on the host (torch CPU, bf16 activations, fp32 selection/attention); '
                       'median s/token; a %d-sequence batch takes %dx as long on the host'
@@ -489,26 +526,26 @@ def decode_bench(args):
                                                'one layer)',
                      'achieved': round(attn_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(attn_gbs / HBM_PEAK_GBS, 4),
-                     'traffic': recorded_traffic('attn_kernel_decode') if headline else None,
                      'bytes_per_launch': int(attn_bytes), 'avg_us': round(attn_us, 2),
                      'timing': 'cold caches (1 GiB read before each of %d launches)' % args.kernel_iters,
                      'avg_us_warm_cache': round(attn_warm_us, 2),
                      'keys_per_query': round(keys_total / (B * H), 1)},
         'kernels': {'attn_kernel_us': round(attn_us, 2), 'attn_kernel_GB/s': round(attn_gbs, 1),
                     'descend_us': round(desc_us, 2), 'descend_GB/s': round(desc_gbs, 1),
-                    'descend_bytes': int(desc_bytes), 'attn_nsplit': sc.nsplit},
+                    'descend_bytes': int(desc_bytes), 'attn_kernel_bytes': int(attn_bytes),
+                    'attn_nsplit': sc.nsplit},
     }
-    if headline:
-        res['roofline']['traffic_source'] = ('profiles/decode_attention_traffic.md (rocprofv3 FETCH_SIZE x2.0 + '
-                                             'WRITE_SIZE x1.0, calibrated on a 256 MiB copy)')
     if fused:
         # the decode step runs the one-launch layer attention: that is the dominant kernel
         res['roofline'].update({
             'kernel': 'seg_attend_kernel<bf16_t, 64> (cache append + beam descent + attention, one layer)',
             'achieved': round(attend_gbs, 1), 'frac': round(attend_gbs / HBM_PEAK_GBS, 4),
-            'traffic': recorded_traffic('seg_attend_kernel_decode') if headline else None,
             'bytes_per_launch': int(attend_bytes), 'avg_us': round(attend_us, 2),
             'avg_us_warm_cache': round(attend_warm_us, 2)})
+    if headline:
+        set_traffic(res['roofline'], 'seg_attend_kernel_decode' if fused else 'attn_kernel_decode')
+    else:
+        res['roofline'].update(traffic=None, traffic_note='no counter passes recorded for this configuration')
     if headline and not args.no_gather_dot:
         log('gather-dot leg')
         res['gather_dot'] = gather_dot_leg(args)
@@ -605,6 +642,7 @@ def small_model_bench(args):
                                    'top-k %d, leaf %d and leaf 2' % (args.topk, args.leaf)},
             'runs': runs,
             'cpu_baseline': {'value': main_run['cpu_tokens_per_s'], 'unit': 'tokens/s', 'cores': ncores,
+                             'cpu_model': cpu_model(),
                              'kind': 'port',
                              'sample': 'the oracle engine decoding the same 256 greedy steps (after the prompt) '
                                        'on the host, median s/token'}}
@@ -720,7 +758,7 @@ def prefill_attention_bench(args):
                          'gathered_GB/s': round(attn_bytes / (a_us * 1e-6) / 1e9, 1)},
             'parity': {'slice': [bb, hh], 'selection_bit_exact': sel_same, 'max_abs_out_diff': float('%.3g' % err)},
             'cpu_baseline': {'value': round(T / cpu_attn_s, 1), 'unit': 'tokens/s (attention only, one (b,h))',
-                             'cores': ncores, 'kind': 'port',
+                             'cores': ncores, 'cpu_model': cpu_model(), 'kind': 'port',
                              'sample': 'oracle sparse_attn_ref over the selected keys of one (b, h) slice '
                                        '(16384 queries); the whole call has 64 such slices'}}
 

@@ -6,11 +6,11 @@
   against the oracle engine.  Bar: identical greedy tokens, logits within 1e-5.
 * config 3 -- one (1, 2, 16384, 128) bf16 slice with the config's low-rank keys, leaf 64, top-32: the
   descent of every query bit-exact against the oracle's canonical order, every disagreement between the
-  canonical and the reference's torch order classified as a tie, and the matrix-core attention of the last
-  2048 queries of each head within 2e-2 of the oracle's.
+  canonical and the reference's torch order a tie within 1 ulp of the float32 node score, and the
+  matrix-core attention of the last 2048 queries of each head within 2e-2 of the oracle's.
 * config 4 -- the 12L/768/12H vocab-50304 bf16 model, leaf 64, top-32, 2 sequences with a 32768-token
   context (Tcap 65536), 8 decode steps; config 5 -- the same model, leaf 128, 4-ary, top-64, 1 sequence with
-  a 65536-token context (Tcap 131072), 6 steps.  Against the oracle engine (engine.py:84-177, bf16
+  its full 131072-token context (Tcap 262144), 6 steps.  Against the oracle engine (engine.py:84-177, bf16
   activations, canonical selection) from the same cache contents:
     - teacher-forced, layer by layer (each GPU op fed the oracle's inputs): leaf ids bit-exact, every
       intermediate (q/k/v, attention output, residual stream, MLP hidden) and the logits within 2e-2;
@@ -153,7 +153,9 @@ def test_config3_selection_and_attention():
                        ci[0, h], cv[0, h], fi[0, h], fv[0, h])
         print('config 3 head %d: %d of %d queries differ from the torch order, %d within 1 ulp, %d within the '
               'rounding bound' % (h, r['diverged'], T, r['within_1ulp'], r['within_bound']), flush=True)
-        assert r['within_bound'] == r['diverged']
+        # the north star's tie rule: a query may differ from the torch order only at a tie within 1 ulp of the
+        # float32 node score; the rounding-bound classification is kept as a diagnostic
+        assert r['within_1ulp'] == r['diverged'], r
     # attention of the last 2048 queries of each head against the oracle over the same kept keys
     lhat = torch.full((1, H, T), 32, dtype=torch.long)
     nid = torch.zeros(1, H, T, cfg.nb_window * cfg.nb_store, dtype=torch.long)
@@ -255,7 +257,7 @@ def _decode_parity(leaf, arity, topk, B, T0, Tcap, steps, ids_seed, sort_dedupe)
     print('teacher-forced (leaf %d, arity %d, top-%d, %d x %d): %s' %
           (leaf, arity, topk, B, T0, ', '.join('%s %.3g' % kv for kv in err.items())), flush=True)
     print('selection vs the torch order: %s' % ties, flush=True)
-    assert ties['within_bound'] == ties['diverged']
+    assert ties['within_1ulp'] == ties['diverged'], ties
     for name, e in err.items():
         assert e <= BF16_BAR, (name, e)
 
@@ -303,4 +305,4 @@ def test_config4_decode_matches_oracle():
 
 
 def test_config5_decode_matches_oracle():
-    _decode_parity(leaf=128, arity=4, topk=64, B=1, T0=65536, Tcap=131072, steps=6, ids_seed=4, sort_dedupe=True)
+    _decode_parity(leaf=128, arity=4, topk=64, B=1, T0=131072, Tcap=262144, steps=6, ids_seed=4, sort_dedupe=True)
