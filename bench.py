@@ -29,6 +29,9 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
+# config 1 bytes per decode step at batch 1: the block weights and the tied head read once (10.7 M fp32 parameters,
+# 42.9 MB) plus the K/V rows and node sums the six layers' attention reads (about 4.7 MB)
+STEP_BYTES_CONFIG1 = 47_600_000
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -64,8 +67,16 @@ def parse():
                     help='decode cache in pages of one leaf block per (sequence, head), or contiguous per sequence')
     ap.add_argument('--groups', type=int, default=None,
                     help='independent sequence groups, each captured and replayed on its own stream')
+    ap.add_argument('--no-sublines', action='store_true',
+                    help='config 4: skip the bounded lines of configs 1, 3 and 5 that follow the headline')
     args = ap.parse_args()
-    # per-config defaults: 4 (the headline) and 5 are decode engines; 1 the small fp32 model; 3 prefill attention
+    args.quick = False
+    return apply_presets(args)
+
+
+def apply_presets(args):
+    """Fill the unset per-config options: 4 (the headline) and 5 are decode engines; 1 the small fp32 model;
+    3 prefill attention; 2 the isolated gather-dot."""
     presets = {4: dict(steps=64, warmup=8, batch=32, context=32768, tcap=65536, leaf=64, arity=2, topk=32,
                        prefill_chunk=8, ids_seed=3),
                5: dict(steps=512, warmup=8, batch=1, context=131072, tcap=262144, leaf=128, arity=4, topk=64,
@@ -80,6 +91,21 @@ def parse():
         if getattr(args, k, None) is None:
             setattr(args, k, v)
     return args
+
+
+def subline_args(base, config):
+    """Options of a bounded line of another configuration run after the headline: that configuration's own
+    presets (not the headline's --steps / --warmup) and a shorter CPU sample."""
+    a = argparse.Namespace(**vars(base))
+    for k in ('steps', 'warmup', 'batch', 'context', 'tcap', 'leaf', 'arity', 'topk', 'prefill_chunk', 'ids_seed'):
+        setattr(a, k, None)
+    a.config = config
+    a.quick = True
+    a.neighbors = a.production = False
+    a.groups = None
+    a.cpu_seconds = 8.0
+    a.no_gather_dot = True
+    return apply_presets(a)
 
 
 def log(msg):
@@ -573,7 +599,7 @@ def small_model_bench(args):
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
     runs = []
-    for leaf in (args.leaf, 2):
+    for leaf in ((args.leaf,) if args.quick else (args.leaf, 2)):
         cfg = Config(vocab_size=256, seq_len=1024, n_layer=6, n_head=6, n_embd=384, attn='seg', wmax=args.topk,
                      beam=args.topk, beam_mode='fixed', neighbors=False, leaf=leaf, arity=2, local=3)
         torch.manual_seed(0)
@@ -639,8 +665,16 @@ def small_model_bench(args):
             'vs_baseline': None, 'dtype': 'f32',
             'data': 'synthetic (random-init weights seed 0, uniform random prompt ids seed 0)',
             'config': {'workload': 'GPT 6L/384/6H vocab 256 fp32, batch 1, 512-token prompt, 256 greedy steps, '
-                                   'top-k %d, leaf %d and leaf 2' % (args.topk, args.leaf)},
+                                   'top-k %d, leaf %d%s' % (args.topk, args.leaf, '' if args.quick else ' and leaf 2')},
             'runs': runs,
+            'roofline': {'bound': 'latency', 'kernel': 'whole decode step (graph of 6 layers at batch 1)',
+                         'achieved': round(STEP_BYTES_CONFIG1 / (main_run['gpu_ms_per_token'] * 1e-3) / 1e9, 1),
+                         'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                         'frac': round(STEP_BYTES_CONFIG1 / (main_run['gpu_ms_per_token'] * 1e-3) / 1e9 /
+                                       HBM_PEAK_GBS, 5),
+                         'traffic': None, 'bytes_per_step': STEP_BYTES_CONFIG1,
+                         'note': 'weights 42.9 MB + KV 4.7 MB per step; a batch-1 fp32 step is bound by its chain of '
+                                 'dependent launches, not by HBM'},
             'cpu_baseline': {'value': main_run['cpu_tokens_per_s'], 'unit': 'tokens/s', 'cores': ncores,
                              'cpu_model': cpu_model(),
                              'kind': 'port',
@@ -715,29 +749,33 @@ def prefill_attention_bench(args):
     attn_bytes = keys_total * D * 2 * 2 + B * H * T * (2 * D * 2 + wl * 5)
     log('config 3: build %.1f us, descent %.1f us, attention %.1f us (%.1f TFLOP/s)' % (b_us, d_us, a_us, tflops))
 
-    # parity on slice (b, h) = (1, 5): selection bit for bit, output within the bf16 tolerance
+    # parity on slice (b, h) = (1, 5): selection bit for bit, output within the bf16 tolerance -- every query, or
+    # in the bounded line the last 2048 (the ones with the most keys)
     bb, hh = 1, 5
+    t_lo = T - 2048 if args.quick else 0
+    Tq = T - t_lo
     geom = S.Geometry(T, cfg.leaf, cfg.arity)
     pyr = S.pyramid(S.index_keys(kc[bb:bb + 1, hh:hh + 1]), geom)
-    t_sel = torch.arange(T)
-    rid, rvld, _ = S.tree_pass_general(qc[bb:bb + 1, hh:hh + 1].float(), pyr, t_sel, geom, cfg.wmax, 'canonical')
-    gid = ids[bb:bb + 1, hh:hh + 1].long().cpu()
-    gv = vld[bb:bb + 1, hh:hh + 1].bool().cpu()
+    t_sel = torch.arange(t_lo, T)
+    rid, rvld, _ = S.tree_pass_general(qc[bb:bb + 1, hh:hh + 1, t_lo:].float(), pyr, t_sel, geom, cfg.wmax,
+                                       'canonical')
+    gid = ids[bb:bb + 1, hh:hh + 1, t_lo:].long().cpu()
+    gv = vld[bb:bb + 1, hh:hh + 1, t_lo:].bool().cpu()
     sel_same = bool(torch.equal(gv, rvld) and torch.equal(torch.where(gv, gid, -1), torch.where(rvld, rid, -1)))
-    lhat = torch.full((1, 1, T), cfg.beam, dtype=torch.long)
-    nid = torch.zeros(1, 1, T, cfg.nb_window * cfg.nb_store, dtype=torch.long)
-    sel = S.finish(rid, rvld, nid, torch.zeros_like(nid, dtype=torch.bool), torch.zeros(1, 1, T, dtype=torch.long),
+    lhat = torch.full((1, 1, Tq), cfg.beam, dtype=torch.long)
+    nid = torch.zeros(1, 1, Tq, cfg.nb_window * cfg.nb_store, dtype=torch.long)
+    sel = S.finish(rid, rvld, nid, torch.zeros_like(nid, dtype=torch.bool), torch.zeros(1, 1, Tq, dtype=torch.long),
                    lhat, cfg, cfg.leaf)
     cand, keep, _ = A.assemble(sel, t_sel, cfg, 1, 1)
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
     cm = torch.where(keep, cand, -1)
-    qs, ks, vs = qc[bb:bb + 1, hh:hh + 1], kc[bb:bb + 1, hh:hh + 1], vc[bb:bb + 1, hh:hh + 1]
+    qs, ks, vs = qc[bb:bb + 1, hh:hh + 1, t_lo:], kc[bb:bb + 1, hh:hh + 1], vc[bb:bb + 1, hh:hh + 1]
     c0 = time.perf_counter()
     want = torch.cat([A.sparse_attn_ref(qs[:, :, t0:t0 + 256], ks, vs, cm[:, :, t0:t0 + 256], scale)
-                      for t0 in range(0, T, 256)], 2)     # chunks of 256 queries bound the gathered rows
+                      for t0 in range(0, Tq, 256)], 2)     # chunks of 256 queries bound the gathered rows
     cpu_attn_s = time.perf_counter() - c0
-    err = (out[bb:bb + 1, hh:hh + 1].float().cpu() - want.float()).abs().max().item()
+    err = (out[bb:bb + 1, hh:hh + 1, t_lo:].float().cpu() - want.float()).abs().max().item()
     log('config 3 parity: selection same %s, max |out - oracle| %.3g' % (sel_same, err))
     return {'metric': 'prefill sparse attention tokens/s (config 3)', 'value': round(B * T / (total_us * 1e-6), 1),
             'unit': 'tokens/s', 'n_gpus': 1, 'steps': it, 'warmup': args.warmup,
@@ -756,11 +794,13 @@ def prefill_attention_bench(args):
                          'flops_per_launch': flops, 'keys_per_query': round(keys_total / (B * H * T), 1),
                          'gathered_bytes_per_launch': int(attn_bytes),
                          'gathered_GB/s': round(attn_bytes / (a_us * 1e-6) / 1e9, 1)},
-            'parity': {'slice': [bb, hh], 'selection_bit_exact': sel_same, 'max_abs_out_diff': float('%.3g' % err)},
-            'cpu_baseline': {'value': round(T / cpu_attn_s, 1), 'unit': 'tokens/s (attention only, one (b,h))',
+            'parity': {'slice': [bb, hh], 'queries': [t_lo, T], 'selection_bit_exact': sel_same,
+                       'max_abs_out_diff': float('%.3g' % err)},
+            'cpu_baseline': {'value': round(Tq / cpu_attn_s, 1), 'unit': 'tokens/s (attention only, one (b,h))',
                              'cores': ncores, 'cpu_model': cpu_model(), 'kind': 'port',
-                             'sample': 'oracle sparse_attn_ref over the selected keys of one (b, h) slice '
-                                       '(16384 queries); the whole call has 64 such slices'}}
+                             'sample': 'oracle sparse_attn_ref over the selected keys of %d queries (positions %d..%d) '
+                                       'of one (b, h) slice; the whole call has 64 slices of 16384 queries'
+                                       % (Tq, t_lo, T - 1)}}
 
 
 def main():
@@ -772,6 +812,18 @@ def main():
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     if args.config in (4, 5):
         res = decode_bench(args)
+        if args.config == 4 and not args.no_sublines:
+            # bounded lines of the other decode and prefill configurations, each with its own roofline and CPU
+            # baseline (the isolated gather-dot, config 2, is the headline's gather_dot leg)
+            res['configs'] = {}
+            for n, fn in ((1, small_model_bench), (3, prefill_attention_bench), (5, decode_bench)):
+                torch.cuda.synchronize()
+                torch.cuda.empty_cache()
+                log('bounded line of config %d' % n)
+                t0 = time.perf_counter()
+                sub = fn(subline_args(args, n))
+                sub['wall_s'] = round(time.perf_counter() - t0, 1)
+                res['configs'][str(n)] = sub
     elif args.config == 1:
         res = small_model_bench(args)
     elif args.config == 2:

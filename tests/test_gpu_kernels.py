@@ -49,6 +49,38 @@ def test_level_sums_partial_and_no_sink():
         assert torch.equal(g.cpu()[:, :, :n], want[l][:, :, :n]), l
 
 
+@pytest.mark.parametrize('case', ['projection_view', 'unaligned_rows', 'long_multipass', 'partial_bf16'])
+def test_level_sums_layouts(case):
+    """The pyramid from a strided view of a (b, T, 3C) projection (the prefill's k), from rows whose 16-byte
+    slices are not aligned (the element-wise pass), over 131072 positions (several passes, config 5's tree) and
+    over a partial prefix: every level bit for bit against the oracle's adjacent-pair sums."""
+    print('case', case, flush=True)
+    if case == 'projection_view':
+        B, H, T, D, dtype, leaf, arity, t_end = 2, 4, 4096, 128, torch.bfloat16, 64, 2, None
+        x = rnd(B, T, 3 * H * D, seed=90, dtype=dtype)
+        k = x[..., H * D:2 * H * D].view(B, T, H, D).transpose(1, 2)
+    elif case == 'unaligned_rows':
+        B, H, T, D, dtype, leaf, arity, t_end = 1, 2, 2048, 64, torch.float32, 8, 2, None
+        k = rnd(B, H, T, D + 1, seed=91, dtype=dtype)[..., 1:]
+    elif case == 'long_multipass':
+        B, H, T, D, dtype, leaf, arity, t_end = 1, 2, 131072, 64, torch.bfloat16, 128, 4, None
+        k = rnd(B, H, T, D, seed=92, dtype=dtype)
+    else:
+        B, H, T, D, dtype, leaf, arity, t_end = 2, 3, 4096, 128, torch.bfloat16, 16, 2, 3001
+        k = rnd(B, H, T, D, seed=93, dtype=dtype)
+    shape = K.TreeShape(T, leaf, arity)
+    kd = k.to(DEV) if case != 'projection_view' else x.to(DEV)[..., H * D:2 * H * D].view(B, T, H, D).transpose(1, 2)
+    got = K.level_sums(kd, shape.blevels, t_end=t_end)
+    kc = k.contiguous()
+    if t_end is not None:
+        kc = kc.clone()
+        kc[:, :, t_end:] = 0
+    want = S.pyramid(S.index_keys(kc), S.Geometry(T, leaf, arity))
+    for j in range(shape.n_levels):
+        n = (T if t_end is None else t_end) >> shape.blevels[j]
+        assert torch.equal(got[j].cpu()[:, :, :n], want[j][:, :, :n]), (case, j)
+
+
 def _descent_case(T, D, leaf, arity, wmax, dtype, B=2, H=2, seed=0, tq=None):
     q = rnd(B, H, T if tq is None else tq.shape[-1], D, seed=seed, dtype=dtype)
     k = rnd(B, H, T, D, seed=seed + 1, dtype=dtype)

@@ -584,3 +584,31 @@ def test_tree_pass_with_a_plain_getU():
     n2 = seg.neighbor_pass(q, lambda c: getU(1, c), *st, tq, cfg, T=256)
     for x, y in zip(n1, n2):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize('kw', [dict(), dict(leaf=8, neighbors=False, wmax=4, beam=4)])
+def test_seg_attend_without_update_matches_oracle(kw):
+    """The reference's one-layer decode benchmark call (bench_decode.py:40-45): SegState.fill with a whole
+    context, then seg_attend(state, None, q, None, None, T - 1, update=False) -- no new key or value -- in the
+    reference's default mode (leaf groups of 2, neighbours on) and in a structural mode: output within 1e-5 of the
+    oracle's seg_attend, the same mean key count, and the state left as it was."""
+    from oracle.engine_ref import SegStateRef, seg_attend_ref
+    from treeattn_amd.engine import SegState, seg_attend
+    H, dh, T = 6, 64, 1024
+    cfg = Config(seq_len=T, n_head=H, n_embd=H * dh, attn='seg', beam=kw.get('beam', 4), beam_mode='fixed', local=3,
+                 **{k: v for k, v in kw.items() if k != 'beam'})
+    g = torch.Generator().manual_seed(21)
+    Kt, Vt, q = torch.randn(1, H, T, dh, generator=g), torch.randn(1, H, T, dh, generator=g), \
+        torch.randn(1, H, 1, dh, generator=g)
+    st = SegState(cfg, T, H, dh, DEV)
+    st.fill(Kt.to(DEV), Vt.to(DEV))
+    levels_before = [x.clone() for x in st.levels]
+    got, keys = seg_attend(st, None, q.to(DEV), None, None, T - 1, update=False)
+    ref = SegStateRef(cfg, T, H, dh, canon=True)
+    ref.fill(Kt, Vt)
+    want, wkeys = seg_attend_ref(ref, None, q, None, None, T - 1, update=False, mode='canonical')
+    err = (got.float().cpu() - want).abs().max().item()
+    print('max |dout| %.2e, keys %.2f vs %.2f' % (err, keys, wkeys))
+    assert err < FP32_BAR, err
+    assert abs(keys - wkeys) < 1e-4
+    assert all(torch.equal(a, b) for a, b in zip(levels_before, st.levels))

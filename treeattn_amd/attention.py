@@ -119,55 +119,80 @@ class TreeAttention(nn.Module):
 
     # ------------------------------------------------------------------------------------------ training
     def _training_signals(self, q, k, v, cand, cand_full, leaf, lv, perm, plog, depth):
-        """attention.py:150-174: the routing loss (route_weight > 0: at every level, cross-entropy of the
-        query's scores against the ancestor of the tree leaf it attends to most) and the budget head's loss
-        (the label: how many of the found leaves hold 90 % of their attention mass)."""
+        """The training-only losses of attention.py:150-174, stated from their definitions.
+
+        Labels come from the attention itself (no gradient): p[s] is the softmax probability of tree-key slot s
+        of the labelling list (the full list when the budget head cuts the attended one).  A query's anchor is
+        its most probable tree key, when that key exists and the query lies past the first block; the anchor's
+        leaf is the tree leaf owning that slot (slot s and s + wl belong to leaf s mod wl).
+          * routing loss (route_weight > 0): at each forest level the query's candidate scores, divided by
+            (node size x sqrt(dh)), against the anchor leaf's ancestor at that level, by cross-entropy over the
+            rows where that ancestor is a candidate; the mean over the levels that have such rows;
+          * budget loss (beam_mode 'pred'): the budget head's logits against the class of the smallest budget
+            whose leading leaves (best first) carry 90 % of the found leaves' probability mass."""
         cfg = self.cfg
-        b, H, T, dh = q.shape
+        T = q.shape[2]
         B = cfg.tree_block
         wl = leaf.shape[-1]
-        dev = q.device
-        scale = 1.0 / math.sqrt(dh)
-        blk = torch.arange(T, device=dev) // B
         pred_mode = cfg.beam_mode == 'pred'
+        past_first = (torch.arange(T, device=q.device) >= B).view(1, 1, T)
         with torch.no_grad():
-            lab_cand = cand_full if pred_mode else cand
-            _, lse = K.sparse_attn_fwd(q.detach(), k.detach(), v.detach(), lab_cand, scale)
-            tkey = lab_cand[..., B + 3:]
-            tv_lab = tkey >= 0
-            kg = gather_nodes(k.detach().float(), tkey.long().clamp(min=0))
-            s = torch.einsum('bhtd,bhtkd->bhtk', q.detach().float(), kg) * scale
-            wt = torch.where(tv_lab, torch.exp(s - lse.unsqueeze(-1)), torch.zeros_like(s))
-            best = wt.argmax(-1)
-            ok = tv_lab.gather(-1, best.unsqueeze(-1)).squeeze(-1) & (wt.max(-1).values > 0) & \
-                (blk >= 1).view(1, 1, T)
-            leafnode = leaf.long().gather(-1, (best % wl).unsqueeze(-1)).squeeze(-1)
-            if pred_mode:
-                leaf_mass = wt[..., :wl] + wt[..., wl:]
-                total = leaf_mass.sum(-1, keepdim=True)
-                need = (leaf_mass.cumsum(-1) < 0.9 * total).sum(-1) + 1
-                label = (need.unsqueeze(-1) > self.classes).sum(-1).clamp(max=len(self.classes) - 1)
+            p, slot_ok = self._tree_slot_probs(q, k, v, cand_full if pred_mode else cand)
+            p_top, s_top = p.max(-1)
+            anchored = slot_ok.gather(-1, s_top.unsqueeze(-1)).squeeze(-1) & (p_top > 0) & past_first
+            anchor_leaf = leaf.long().gather(-1, (s_top % wl).unsqueeze(-1)).squeeze(-1)
+            budget_class = self._budget_class(p, wl) if pred_mode else None
         route = q.new_zeros(()).float()
-        if cfg.route_weight > 0 and bool(ok.any()):
-            sums_t = _torch_forest_sums(k, perm, B, depth, cfg)   # differentiable in k
-            terms = []
-            for lvl in range(depth + 1):
-                cur_l, cv_l = lv[0][lvl], lv[1][lvl]   # slots past the level's width: -1, invalid
-                sc = torch.einsum('bhtd,bhtwd->bhtw', q, gather_nodes(sums_t[lvl], cur_l.long().clamp(min=0)))
-                sc = sc.masked_fill(~cv_l, float('-inf'))
-                anc = leafnode >> (depth - lvl)
-                match = (cur_l.long() == anc.unsqueeze(-1)) & cv_l
-                rows = ok & match.any(-1)
-                if bool(rows.any()):
-                    size = B // (2 ** lvl)
-                    lg = (sc / (size * math.sqrt(dh))).float()
-                    terms.append(F.cross_entropy(lg[rows], match.float().argmax(-1)[rows]))
-            if terms:
-                route = torch.stack(terms).mean()
+        if cfg.route_weight > 0 and bool(anchored.any()):
+            route = self._routing_loss(q, k, perm, lv, depth, anchor_leaf, anchored)
         self.aux['route'] = route
         if pred_mode:
-            prow = (blk >= 1).view(1, 1, T).expand(b, H, T)
-            self.aux['pred'] = F.cross_entropy(plog.float()[prow], label[prow])
+            rows = past_first.expand_as(budget_class)
+            self.aux['pred'] = F.cross_entropy(plog.float()[rows], budget_class[rows])
+
+    def _tree_slot_probs(self, q, k, v, cand):
+        """Softmax probabilities of the tree-key slots of candidate list `cand` (0 where a slot is empty) and the
+        slots' validity: exp(q . k_slot / sqrt(dh) - lse), lse the log-sum-exp of the whole list from the kernel."""
+        B = self.cfg.tree_block
+        dh = q.shape[-1]
+        scale = 1.0 / math.sqrt(dh)
+        _, lse = K.sparse_attn_fwd(q.detach(), k.detach(), v.detach(), cand, scale)
+        slots = cand[..., B + 3:]
+        ok = slots >= 0
+        keys = gather_nodes(k.detach().float(), slots.long().clamp(min=0))           # (b, H, T, S, dh)
+        logits = torch.matmul(keys, q.detach().float().unsqueeze(-1)).squeeze(-1) * scale
+        return torch.exp(logits - lse.unsqueeze(-1)).masked_fill(~ok, 0.0), ok
+
+    def _budget_class(self, p, wl):
+        """Index of the smallest budget class holding the leaves that carry 90 % of the found leaves' mass (the
+        leaves best first; a leaf's mass is its two key slots'), capped at the largest class."""
+        leaf_mass = p[..., :wl] + p[..., wl:]
+        cum = leaf_mass.cumsum(-1)
+        # leaves needed: one more than those whose running mass stays short of 90 % of the total
+        total = leaf_mass.sum(-1, keepdim=True)
+        needed = torch.searchsorted(cum.contiguous(), (0.9 * total).contiguous()).squeeze(-1) + 1
+        return (self.classes < needed.unsqueeze(-1)).sum(-1).clamp(max=len(self.classes) - 1)
+
+    def _routing_loss(self, q, k, perm, lv, depth, anchor_leaf, anchored):
+        """Mean over forest levels of the cross-entropy between a query's scaled candidate scores and the position
+        of its anchor leaf's ancestor among them (rows where the ancestor is a candidate).  The node sums are
+        rebuilt from k in torch (forest.py:65-75) so the loss has a gradient in k as well as in q."""
+        cfg = self.cfg
+        B = cfg.tree_block
+        dh = q.shape[-1]
+        node_sums = _torch_forest_sums(k, perm, B, depth, cfg)
+        losses = []
+        for lvl in range(depth + 1):
+            ids, ok = lv[0][lvl], lv[1][lvl]            # slots past the level's width: -1, not ok
+            nodes = gather_nodes(node_sums[lvl], ids.long().clamp(min=0))          # (b, H, T, W, dh)
+            score = torch.matmul(nodes, q.unsqueeze(-1)).squeeze(-1).masked_fill(~ok, float('-inf'))
+            target = (ids.long() == (anchor_leaf >> (depth - lvl)).unsqueeze(-1)) & ok
+            rows = anchored & target.any(-1)
+            if bool(rows.any()):
+                node_size = B >> lvl
+                logits = (score / (node_size * math.sqrt(dh))).float()
+                losses.append(F.cross_entropy(logits[rows], target.float().argmax(-1)[rows]))
+        return torch.stack(losses).mean() if losses else q.new_zeros(()).float()
 
 
 def _torch_forest_sums(k, perm, B, depth, cfg):

@@ -98,6 +98,131 @@ __global__ __launch_bounds__(256) void level_pass_kernel(const T* __restrict__ i
   }
 }
 
+// The same pass with each thread holding VEC = 16 / sizeof(T) consecutive dimensions of a row, read with one
+// 16-byte load per row: TPR = D / VEC threads cover a row, so a wavefront's load instruction reads whole row
+// slices of 64 / TPR rows (64 rows apart), and each thread keeps 16 rows in flight.  Thread (slice, seg):
+// dimensions [slice VEC, slice VEC + VEC) of a segment of 64 consecutive rows, reduced by adjacent pairs with a
+// carry stack; the workgroup's NSEG = 256 / TPR segment sums are then combined pairwise in LDS, one tree level
+// per step.  Every node is (left + right) of its two children, so the nodes equal level_pass_kernel's bit for
+// bit whatever the thread layout.  Rows, level rows and the strides must keep 16-byte slices aligned.
+// (A thread holds 16 rows' loads: two batches of 8.)
+template <typename T>
+struct VecPass {
+  static constexpr int VEC = 16 / (int)sizeof(T);
+};
+
+template <int VEC>
+__device__ __forceinline__ void store_node_vec(const LevelOut& lo, int blevel, int b, int h, int64_t node, int D,
+                                               int d0, const float (&x)[VEC]) {
+  if (blevel < 64) {
+    const int j = lo.slot_of_blevel[blevel];
+    if (j >= 0) {
+      float* p = lo.ptr[j] + b * lo.sb[j] + h * lo.sh[j] + node * D + d0;
+#pragma unroll
+      for (int c = 0; c < VEC; c += 4) *reinterpret_cast<float4*>(p + c) = make_float4(x[c], x[c + 1], x[c + 2], x[c + 3]);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void level_vec_kernel(const T* __restrict__ in, int64_t isb, int64_t ish,
+                                                        int64_t isr, int H, int n_rows, int base, int zero_first,
+                                                        LevelOut lo, float* __restrict__ tot, int n_chunks) {
+  constexpr int VEC = VecPass<T>::VEC;
+  constexpr int TPR = D / VEC;
+  constexpr int NSEG = 256 / TPR;
+  constexpr int LOG_NSEG = NSEG == 2 ? 1 : NSEG == 4 ? 2 : NSEG == 8 ? 3 : NSEG == 16 ? 4 : NSEG == 32 ? 5 :
+                           NSEG == 64 ? 6 : 7;
+  constexpr int RB = 8;    // rows per load batch; two batches in flight
+  static_assert(TPR >= 1 && (1 << LOG_NSEG) == NSEG, "layout");
+  __shared__ __align__(16) float seg_sum[NSEG][D];
+  const int sl = threadIdx.x % TPR;
+  const int seg = threadIdx.x / TPR;
+  const int d0 = sl * VEC;
+  const int chunk = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / H, h = bh % H;
+  const int64_t crow0 = (int64_t)chunk * 64 * NSEG;
+  const int64_t row0 = crow0 + seg * 64;
+  const T* src = in + b * isb + h * ish + d0;
+  const int64_t last = n_rows - 1;
+
+  float carry[7][VEC];
+  uint4 buf[2][RB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+    const int64_t r = row0 + i < last ? row0 + i : last;
+    buf[0][i] = ldg16(src + r * isr);
+  }
+#pragma unroll
+  for (int bt = 0; bt < 64 / RB; ++bt) {
+    if (bt + 1 < 64 / RB) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int64_t rr = row0 + (bt + 1) * RB + i;
+        const int64_t r = rr < last ? rr : last;
+        buf[(bt + 1) & 1][i] = ldg16(src + r * isr);
+      }
+    }
+#pragma unroll
+    for (int i0 = 0; i0 < RB; ++i0) {
+      const int i = bt * RB + i0;
+      const int64_t r = row0 + i;
+      if (r < n_rows) {
+        float x[VEC];
+        const T* e = reinterpret_cast<const T*>(&buf[bt & 1][i0]);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          x[v] = (zero_first && r == 0) ? 0.0f : to_f32(e[v]);
+        }
+        int lv = 0;
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+          if (((i >> k) & 1) == 0) break;
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) x[v] = __fadd_rn(carry[k][v], x[v]);
+          lv = k + 1;
+          store_node_vec<VEC>(lo, base + lv, b, h, r >> lv, D, d0, x);
+        }
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) carry[lv][v] = x[v];
+      }
+    }
+  }
+  if (row0 + 63 < n_rows) {
+#pragma unroll
+    for (int v = 0; v < VEC; v += 4)
+      *reinterpret_cast<float4*>(&seg_sum[seg][d0 + v]) =
+          make_float4(carry[6][v], carry[6][v + 1], carry[6][v + 2], carry[6][v + 3]);
+  }
+  // pairwise combination of the segment sums: at step k the node of binary level base + 6 + k + 1 with index p
+  // in this chunk is seg_sum[2p << k] + seg_sum[(2p + 1) << k], kept in the left child's slot
+  for (int k = 0; k < LOG_NSEG; ++k) {
+    __syncthreads();
+    const int npairs = NSEG >> (k + 1);
+    for (int e = threadIdx.x; e < npairs * TPR; e += 256) {
+      const int p = e / TPR, s2 = e % TPR;
+      const int64_t node_rows = (int64_t)64 << (k + 1);
+      if (crow0 + (p + 1) * node_rows <= n_rows) {
+        float* lft = &seg_sum[(2 * p) << k][s2 * VEC];
+        const float* rgt = &seg_sum[(2 * p + 1) << k][s2 * VEC];
+        float x[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) x[v] = __fadd_rn(lft[v], rgt[v]);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) lft[v] = x[v];
+        store_node_vec<VEC>(lo, base + 6 + k + 1, b, h, (int64_t)chunk * (NSEG >> (k + 1)) + p, D, s2 * VEC, x);
+      }
+    }
+  }
+  if (tot != nullptr && crow0 + 64 * NSEG <= n_rows) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < D / 4; e += 256)
+      *reinterpret_cast<float4*>(tot + ((int64_t)bh * n_chunks + chunk) * D + 4 * e) =
+          *reinterpret_cast<const float4*>(&seg_sum[0][4 * e]);
+  }
+}
+
 // ----------------------------------------------------------------------------------------- descent
 // The mean-log gate's share of a fused decode append: the log-sum and gated-vector levels (same strides as the
 // levels the append forms; out[j] null where the level is not gated) and the quantile's order statistic / weight.
@@ -275,13 +400,27 @@ int dispatch_dt_d(int dt, int D, A&&... a) {
 
 int chunk_rows(int D) { return 64 * (256 / D); }
 
+// Rows of the pass's input a workgroup reduces: 64 rows per segment, 256 / (threads per row) segments.
+int chunk_rows_vec(int D, int elem) { return 64 * (256 / (D / (16 / elem))); }
+
 template <typename T, int D>
 struct LevelSumsRun {
+  // The 16-byte-slice pass needs a slice of at least 4 floats per thread and aligned rows; the element pass
+  // (level_pass_kernel) covers every other layout.
+  static bool vec_ok(const void* p, int elem, int64_t sb, int64_t sh, int64_t sr, const LevelOut& lo, int n_out) {
+    if (D * elem < 16 || (D * elem) % 16) return false;
+    if ((uintptr_t)p % 16) return false;
+    for (int64_t s : {sb, sh, sr})
+      if ((s * elem) % 16) return false;
+    for (int j = 0; j < n_out; ++j)
+      if ((uintptr_t)lo.ptr[j] % 16 || (lo.sb[j] * 4) % 16 || (lo.sh[j] * 4) % 16) return false;
+    return true;
+  }
+
   static int run(const void* k, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int t_end, int zero_sink,
-                 const LevelOut& lo, int top_blevel, float* ws, hipStream_t st, bool logt = false) {
-    const int CH = chunk_rows(D);
-    const int LCH = log2i(CH);
-    int64_t nA = ((int64_t)t_end / CH + 1) * B * H * D;
+                 const LevelOut& lo, int n_out, int top_blevel, float* ws, hipStream_t st, bool logt = false) {
+    // the workspace holds the chunk totals of the element pass's chunks (the smallest any pass uses)
+    int64_t nA = ((int64_t)t_end / chunk_rows(D) + 1) * B * H * D;
     float* bufs[2] = {ws, ws + nA};
     int base = 0;
     int n_rows = t_end;
@@ -290,22 +429,30 @@ struct LevelSumsRun {
     const void* src = k;
     int64_t sb = ksb, sh = ksh, sr = kst;
     while (true) {
+      const int elem = pass == 0 ? (int)sizeof(T) : 4;
+      // the log-magnitude pass (the gate's statistic) stays on the element pass: its double-precision log is a
+      // call, around which the 16-byte pass's row loop would not stay unrolled
+      const bool vec = !(pass == 0 && logt) && vec_ok(src, elem, sb, sh, sr, lo, n_out);
+      const int CH = vec ? chunk_rows_vec(D, elem) : chunk_rows(D);
+      const int LCH = log2i(CH);
       const int n_chunks = (n_rows + CH - 1) / CH;
       if (n_chunks == 0) break;
       const bool more = top_blevel > base + LCH;
       float* tot = more ? bufs[pass & 1] : nullptr;
       const int tot_chunks = n_rows / CH;
       dim3 grid(n_chunks, B * H);
+#define TA_LEVEL_PASS(KER, TT, ZF)                                                                                 \
+  hipLaunchKernelGGL(KER, grid, dim3(256), 0, st, (const TT*)src, sb, sh, sr, H, n_rows, base, ZF, lo, tot, tot_chunks)
       if (pass == 0 && logt) {
-        hipLaunchKernelGGL((level_pass_kernel<T, D, true>), grid, dim3(256), 0, st, (const T*)src, sb, sh, sr, H,
-                           n_rows, base, zero_sink, lo, tot, tot_chunks);
+        TA_LEVEL_PASS((level_pass_kernel<T, D, true>), T, zero_sink);
       } else if (pass == 0) {
-        hipLaunchKernelGGL((level_pass_kernel<T, D>), grid, dim3(256), 0, st, (const T*)src, sb, sh, sr, H, n_rows,
-                           base, zero_sink, lo, tot, tot_chunks);
+        if (vec) TA_LEVEL_PASS((level_vec_kernel<T, D>), T, zero_sink);
+        else TA_LEVEL_PASS((level_pass_kernel<T, D>), T, zero_sink);
       } else {
-        hipLaunchKernelGGL((level_pass_kernel<float, D>), grid, dim3(256), 0, st, (const float*)src, sb, sh, sr, H,
-                           n_rows, base, 0, lo, tot, tot_chunks);
+        if (vec) TA_LEVEL_PASS((level_vec_kernel<float, D>), float, 0);
+        else TA_LEVEL_PASS((level_pass_kernel<float, D>), float, 0);
       }
+#undef TA_LEVEL_PASS
       int rc = check_launch("level_pass_kernel");
       if (rc) return rc;
       if (!more) break;
@@ -474,7 +621,7 @@ int level_sums_impl(const void* k, int k_dtype, int64_t ksb, int64_t ksh, int64_
     set_error("ta_level_sums: workspace too small");
     return TA_ERR_WORKSPACE;
   }
-  return dispatch_dt_d<LevelSumsRun>(k_dtype, D, k, ksb, ksh, kst, B, H, t_end, zero_sink, lo, prev, ws,
+  return dispatch_dt_d<LevelSumsRun>(k_dtype, D, k, ksb, ksh, kst, B, H, t_end, zero_sink, lo, n_levels, prev, ws,
                                     (hipStream_t)stream, logt);
 }
 }  // namespace

@@ -378,7 +378,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
         # append, descent and attention in one launch (one workgroup per (sequence, head))
         if scratch.n_tree is None:
             scratch.n_tree = torch.full((B, H, 1), SEL.fixed_n_tree(cfg), dtype=torch.int32, device=q.device)
-        out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
+        out = torch.empty(B, H, 1, dh, device=q.device, dtype=state.dtype)
         K.seg_attend(q, state.levels, tpos, state.shape, cfg.wmax, k[:, :, 0], v[:, :, 0], Kc, Vc,
                      scratch.n_tree, cfg.local, scale, (scratch.ids, scratch.vld, scratch.sct), out, keys=scratch.keys)
         return out, scratch.keys
@@ -402,7 +402,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
                 state.gate_append(tpos)
             if cfg.global_pool:
                 state.ksum += k[:, :, 0].float()
-        out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
+        out = torch.empty(B, H, 1, dh, device=q.device, dtype=state.dtype)
         if scratch.n_tree is None:
             scratch.n_tree = torch.full((B, H, 1), SEL.fixed_n_tree(cfg), dtype=torch.int32, device=q.device)
         n_tree = scratch.n_tree
@@ -438,7 +438,7 @@ def seg_attend_(state, pw, q, k, v, t, update=True, scratch=None):
             state.gate_append(tpos)
         if cfg.global_pool and not pooled:
             state.ksum += k[:, :, 0].float()
-    out = torch.empty(B, H, 1, dh, device=q.device, dtype=v.dtype)
+    out = torch.empty(B, H, 1, dh, device=q.device, dtype=state.dtype)
     K.seg_attn(q, Kc, Vc, tpos.view(B, 1), ids, vld, n_tree, leaf, cfg.local, scale, out=out, keys=scratch.keys,
                nsplit=scratch.nsplit, ws=scratch.ws, nb=(nid, match))
     return out, scratch.keys
