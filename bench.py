@@ -570,6 +570,8 @@ def decode_bench(args):
             'avg_us_warm_cache': round(attend_warm_us, 2)})
     if headline:
         set_traffic(res['roofline'], 'seg_attend_kernel_decode' if fused else 'attn_kernel_decode')
+    elif args.config == 5 and not args.neighbors:
+        set_traffic(res['roofline'], 'attn_kernel_decode_config5')
     else:
         res['roofline'].update(traffic=None, traffic_note='no counter passes recorded for this configuration')
     if headline and not args.no_gather_dot:
@@ -747,6 +749,9 @@ def prefill_attention_bench(args):
     mfma_peak = K.mfma_peak()
     log('attention %.1f TFLOP/s useful; matrix-core peak measured %.1f TFLOP/s' % (tflops, mfma_peak))
     attn_bytes = keys_total * D * 2 * 2 + B * H * T * (2 * D * 2 + wl * 5)
+    # the attention launch's compulsory HBM bytes: q, k, v read and the output written once (bf16), the selection
+    # (ids, flags) and the budget read; the gathered K/V rows above are served from the caches
+    compulsory = B * H * T * (4 * D * 2 + wl * 5 + 4)
     log('config 3: build %.1f us, descent %.1f us, attention %.1f us (%.1f TFLOP/s)' % (b_us, d_us, a_us, tflops))
 
     # parity on slice (b, h) = (1, 5): selection bit for bit, output within the bf16 tolerance -- every query, or
@@ -777,7 +782,7 @@ def prefill_attention_bench(args):
     cpu_attn_s = time.perf_counter() - c0
     err = (out[bb:bb + 1, hh:hh + 1, t_lo:].float().cpu() - want.float()).abs().max().item()
     log('config 3 parity: selection same %s, max |out - oracle| %.3g' % (sel_same, err))
-    return {'metric': 'prefill sparse attention tokens/s (config 3)', 'value': round(B * T / (total_us * 1e-6), 1),
+    res = {'metric': 'prefill sparse attention tokens/s (config 3)', 'value': round(B * T / (total_us * 1e-6), 1),
             'unit': 'tokens/s', 'n_gpus': 1, 'steps': it, 'warmup': args.warmup,
             'ms_per_step': round(total_us / 1000, 4), 'higher_is_better': True, 'scaling': 'weak',
             'vs_baseline': None, 'dtype': 'bf16',
@@ -792,6 +797,7 @@ def prefill_attention_bench(args):
                          'peak_measured_how': 'ta_mfma_peak: 4 workgroups per CU, four independent '
                                               'v_mfma_f32_32x32x16_bf16 chains per wavefront on registers',
                          'flops_per_launch': flops, 'keys_per_query': round(keys_total / (B * H * T), 1),
+                         'bytes_per_launch': int(compulsory),
                          'gathered_bytes_per_launch': int(attn_bytes),
                          'gathered_GB/s': round(attn_bytes / (a_us * 1e-6) / 1e9, 1)},
             'parity': {'slice': [bb, hh], 'queries': [t_lo, T], 'selection_bit_exact': sel_same,
@@ -801,6 +807,8 @@ def prefill_attention_bench(args):
                              'sample': 'oracle sparse_attn_ref over the selected keys of %d queries (positions %d..%d) '
                                        'of one (b, h) slice; the whole call has 64 slices of 16384 queries'
                                        % (Tq, t_lo, T - 1)}}
+    set_traffic(res['roofline'], 'prefill_attn_kernel_config3')
+    return res
 
 
 def main():

@@ -85,6 +85,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void seg_attend_kernel(Attn
   float* att = stk + 16 * D;                                 // the attention's LDS
 
   const int t = p.tq[b];
+  TA_DMARK(12);
   // paged caches: the pages of the static keys' blocks are requested now and stored after the descent, so
   // neither they nor the kept leaves' pages (read by the descent with the node rows) cost a round trip later
   const int32_t* ptrow = p.ptab ? p.ptab + b * p.pt_sb + h * p.pt_sh : nullptr;
@@ -108,6 +109,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void seg_attend_kernel(Attn
   const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.qsb + h * p.qsh;
   int nk = descend_query<T, D, kWavesPerBlock>(qrow, t, Tgeo, b, h, lv, n_levels, arity_log2, wmax, tid, ckey, cid,
                                                csc, kid, ksc, ptrow, cpg, kpg);
+  TA_DMARK(13);
   if (appends)
     append_dim_with<T>(tid, D, t, apre, kbase, vbase, rows, n_levels, lv.blevel[0], arity_log2, stk,
                        [&](int j) { return const_cast<float*>(lv.ptr[j]) + b * lv.sb[j] + h * lv.sh[j]; });
@@ -119,7 +121,9 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void seg_attend_kernel(Attn
   __syncthreads();
   const int nt = p.n_tree ? p.n_tree[bh] : p.wl;
   T* orow = reinterpret_cast<T*>(p.out) + b * p.osb + h * p.osh;
+  TA_DMARK(14);
   attn_query<T, D, true, false>(p, 0, 0, b, h, bh, qrow, t, kid, nullptr, nkw, nt, orow, att, kpg, s_pre);
+  TA_DMARK(15);
   const int64_t obase = (int64_t)bh * p.wl;   // kid and ksc are not written by the attention
   for (int r = tid; r < p.wl; r += NT) {
     const bool ok = r < nk;

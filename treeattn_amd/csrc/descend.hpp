@@ -9,6 +9,9 @@
 
 #include "common.hpp"
 
+// TA_DMARK(i): a phase mark (a no-op here; a tracing build of a kernel defines it before including this header).
+// The descent marks 0 (after its set-up), 1 + 2k and 2 + 2k (after level k's scores and ranking); the layer
+// attention kernel marks 12 (start), 13 (descent done), 14 (attention start) and 15 (attention done).
 #ifndef TA_DMARK
 #define TA_DMARK(i) \
   do {              \
