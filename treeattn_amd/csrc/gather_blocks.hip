@@ -4,7 +4,8 @@
 // the LDS copy of their rows allows) and turns their (query, slot) pairs into
 // per-block lists, so every score the matrix cores compute belongs to a pair that selected the block.
 //
-//  * Set-up: the workgroup's query rows are copied into LDS; its pairs (at most Q * 16) are sorted by block
+//  * Set-up: the workgroup's query rows are copied into LDS (every piece requested before the first is stored);
+//    its pairs (at most Q * 16, their block ids all requested before they are counted) are sorted by block
 //    id with a counting sort in LDS (a count per block, one scan giving each block its list offset and its
 //    number of chunks, then each pair placed with an LDS atomic).  A chunk is up to 128 pairs that selected the
 //    same block; an item is a chunk and one 32-key tile of its block.
@@ -96,11 +97,24 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   const int npairs = nq * NB;
 
   {
+    // every 16-byte piece of the workgroup's query rows requested before any is stored (a load-store pair per
+    // piece in a loop would wait for each load in turn)
     constexpr int CPR = D / 8;
+    constexpr int NQL = Q * CPR / kGpThreads;
+    static_assert(Q * CPR % kGpThreads == 0, "query pieces per thread");
     const T* qb0 = q + b * qsb + h * qsh + (int64_t)n0 * qsn;
-    for (int e = tid; e < nq * CPR; e += kGpThreads) {
+    uint4 piece[NQL];
+#pragma unroll
+    for (int k = 0; k < NQL; ++k) {
+      const int e = tid + k * kGpThreads;
       const int r = e / CPR, cc = e - r * CPR;
-      *reinterpret_cast<uint4*>(qs + r * (D + 8) + 8 * cc) = ldg16(qb0 + (int64_t)r * qsn + 8 * cc);
+      piece[k] = ldg16(qb0 + (int64_t)(r < nq ? r : nq - 1) * qsn + 8 * cc);
+    }
+#pragma unroll
+    for (int k = 0; k < NQL; ++k) {
+      const int e = tid + k * kGpThreads;
+      const int r = e / CPR, cc = e - r * CPR;
+      if (r < nq) *reinterpret_cast<uint4*>(qs + r * (D + 8) + 8 * cc) = piece[k];
     }
   }
   // 1. counts per block.  The reference clamps every key position into [0, M - 1] (cand = blk * block + j,
@@ -112,12 +126,19 @@ __global__ __launch_bounds__(kGpThreads) void gather_pairs_kernel(
   constexpr int PPT = MaxPairs / kGpThreads;
   int pid[PPT];
   const int32_t* brow = blk + ((int64_t)bh * N + n0) * NB;
+  // all of this thread's block ids requested first, then counted (a load then an LDS atomic per pair in one loop
+  // would wait for each load in turn)
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int pi = tid + k * kGpThreads;
+    pid[k] = *(const TA_GLOBAL int32_t*)(brow + (pi < npairs ? pi : 0));
+  }
 #pragma unroll
   for (int k = 0; k < PPT; ++k) {
     const int pi = tid + k * kGpThreads;
     int v = -1;
     if (pi < npairs) {
-      v = brow[pi];
+      v = pid[k];
       v = v < 0 ? nblocks : (v >= nblocks ? nblocks + 1 : v);
       atomicAdd(&uni[v], 1u);
     }

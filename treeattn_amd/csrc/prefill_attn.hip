@@ -136,11 +136,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int EB = 4;
   for (int e0 = 0; e0 < ne; e0 += 256 * EB) {
     uint8_t vv[EB];
+    // unconditional loads (clamped index), so the EB requests are in flight together
 #pragma unroll
     for (int j = 0; j < EB; ++j) {
       const int e = e0 + tid + 256 * j;
-      vv[j] = e < ne ? p.vld[ebase + e] : 0;
+      vv[j] = *(const TA_GLOBAL uint8_t*)(p.vld + ebase + (e < ne ? e : ne - 1));
     }
+#pragma unroll
+    for (int j = 0; j < EB; ++j)
+      if (e0 + tid + 256 * j >= ne) vv[j] = 0;
 #pragma unroll
     for (int j = 0; j < EB; ++j)
       if (vv[j]) atomicAdd(&s_nv[(e0 + tid + 256 * j) / p.wl], 1);
@@ -164,11 +168,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int j = 0; j < EB; ++j) {
       const int e = e0 + tid + 256 * j;
-      uu[j] = -1;
+      uu[j] = *(const TA_GLOBAL int32_t*)(p.ids + ebase + (e < ne ? e : ne - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < EB; ++j) {
+      const int e = e0 + tid + 256 * j;
+      bool use = false;
       if (e < ne) {
         const int q = e / p.wl;
-        if (e - q * p.wl < s_nused[q]) uu[j] = p.ids[ebase + e];
+        use = e - q * p.wl < s_nused[q];
       }
+      if (!use) uu[j] = -1;
     }
 #pragma unroll
     for (int j = 0; j < EB; ++j) {
