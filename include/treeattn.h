@@ -633,7 +633,7 @@ int ta_forest_shape(int T, int block, int wmax, int* wl, int* kc, int* widest);
 /*
  * LaneTree (the reference's attn='dyn' selection), workspace -- bytes of the lane trees of ta_lanetree_build /
  * ta_lanetree_walk: B * H * (T / chunk) trees of capacity T, each T * (4 D + 8) bytes (node sums float32, counts
- * and leaf slots int32).  T a power of two in [4, 4096], chunk dividing T, D 16, 32 or 64.
+ * and leaf slots int32).  T a power of two in [4, 16384], chunk dividing T, D 16, 32, 64 or 128.
  */
 int ta_lanetree_workspace_size(int B, int H, int T, int D, int chunk, int64_t* bytes);
 
@@ -654,7 +654,7 @@ int ta_lanetree_build(const void* k, int dtype, int64_t ksb, int64_t ksh, int64_
  * lhat (B, H, T) int32, the beam search (node score q . mean key, wmax wide), then the insertion of key t.
  * Writes tree_pos (B, H, T, 2 wl) int32 [all first keys | all second keys] of the found leaves (wl =
  * min(wmax, T / 2)), leaf_ok (B, H, T, wl), nb_pos (B, H, T, 2 nb_window nb_store) int32, n_tree and nb_leaves
- * (B, H, T) int32, -1 / 0 where unused.  1 <= wmax <= 32, nb_window * nb_store <= 64, nb_store <= wl.
+ * (B, H, T) int32, -1 / 0 where unused.  1 <= wmax <= 64, nb_window * nb_store <= 64, nb_store <= wl.
  */
 int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t qsb, int64_t qsh, int64_t qst, int64_t ksb,
                      int64_t ksh, int64_t kst, int B, int H, int T, int D, int chunk, const int32_t* lhat, int wmax,

@@ -2,7 +2,12 @@
 // positions; lane l owns one balanced binary tree of capacity T over the keys [1, l * chunk) (the tree a
 // sequential decoder would hold when it reaches the lane), then walks through the lane's positions one at a time:
 // neighbour search over the leaves the lane's previous positions stored, beam search over the tree, store,
-// insertion of the position's key.  One wavefront per lane tree; the lane trees run in parallel.
+// insertion of the position's key.  One workgroup per lane tree; the lane trees run in parallel.
+//
+// Inside a workgroup a row of D dimensions is held 16 dimensions per lane by Q = D / 16 consecutive lanes (a
+// "slot"), so the workgroup's Q wavefronts form 64 slots: 64 members of the groups being split (build) or 64
+// candidates being scored (walk) at a time.  A dot product of two rows is finished across the slot's lanes by
+// DPP exchanges; reductions over slots run as xor butterflies inside a wavefront and through LDS across them.
 //
 // Reference functions replaced: dyntree.py:6-31 masked_two_means_order, dyntree.py:34-82 LaneTree.__init__,
 // dyntree.py:84-106 insert, dyntree.py:108-127 search, dyntree.py:129-131 leaf_keys and dyntree.py:148-243
@@ -11,8 +16,8 @@
 //
 // Arithmetic order (the CPU oracle's canonical mode computes the same, bit for bit):
 //  * a mean or centroid over the S members of a group: L = min(S, 64) partial sums, partial j adding members
-//    j, j + L, j + 2L, ... in that order, then the halving tree over the L partials (the xor butterfly over L
-//    lanes); divided by the member count (at least 1);
+//    j, j + L, j + 2L, ... in that order, then the halving tree over the L partials; divided by the member
+//    count (at least 1);
 //  * dot products: per-dimension float32 products in canon_dot's order; node score = dot / max(count, 1);
 //    dist = (|x|^2 - 2 x.c) + |c|^2;
 //  * argmax: the first index; member order: stable ascending sort of the projections, empty slots last;
@@ -25,9 +30,12 @@
 
 namespace ta {
 
-constexpr int kLaneMaxT = 4096;    // tree capacity = sequence length
-constexpr int kLaneMaxW = 32;      // wmax: the 2 * wmax children of a level are scored one per lane
-constexpr int kLaneMaxNb = 64;     // nb_window * nb_store neighbour entries, one per lane
+constexpr int kLaneMaxT = 16384;   // tree capacity = sequence length (the build holds 8 bytes per slot in LDS)
+constexpr int kLaneMaxW = 64;      // wmax: the 2 * wmax children of a level are scored in rounds of 64 slots
+constexpr int kLaneMaxNb = 64;     // nb_window * nb_store neighbour entries, one per slot
+constexpr int kLaneDQ = 16;        // dimensions of a row held by one lane
+constexpr int kLaneSlots = 64;     // slots of a workgroup
+constexpr int kLtGroups = 16;      // groups side by side in a 64-slot window (the smallest group has 4 slots)
 
 __device__ __forceinline__ int lt_log2(int x) { return 31 - __clz(x); }
 
@@ -48,7 +56,53 @@ __device__ __forceinline__ LaneTree lane_tree(float* ws, int64_t P, int C, int D
   return t;
 }
 
-// (value, index) argmax over an aligned L-lane segment: the largest value, the smallest index among equals.
+// canon_dot's value for two D-vectors held by the Q lanes of a slot, 16 dimensions each (fa(i), fb(i) give
+// element i of this lane's dimensions [16 q, 16 q + 16)): each lane reduces its 16 / Q whole groups of D / 16
+// products by the halving tree, then the halving tree over the 16 groups runs as an xor butterfly in which a
+// step pairs groups held by different lanes of the slot.  Every lane of the slot ends with the value.
+template <int N, int GQ>
+__device__ __forceinline__ void lt_groups_step(float (&g)[GQ]) {
+  if constexpr (N >= GQ) {
+#pragma unroll
+    for (int i = 0; i < GQ; ++i) g[i] = g[i] + xor_lane<N / GQ>(g[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) g[i] = g[i] + g[i + N];
+  }
+}
+template <int D, int Q, typename FA, typename FB>
+__device__ __forceinline__ float slice_dot(FA fa, FB fb) {
+  static_assert(D % 16 == 0 && Q * kLaneDQ == D, "16 dimensions per lane");
+  constexpr int R = D / 16, GQ = 16 / Q;
+  float g[GQ];
+#pragma unroll
+  for (int j = 0; j < GQ; ++j) {
+    float p[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) p[i] = fa(R * j + i) * fb(R * j + i);
+#pragma unroll
+    for (int n = R / 2; n >= 1; n /= 2)
+#pragma unroll
+      for (int i = 0; i < n; ++i) p[i] = p[i] + p[i + n];
+    g[j] = p[0];
+  }
+  lt_groups_step<8, GQ>(g);
+  lt_groups_step<4, GQ>(g);
+  lt_groups_step<2, GQ>(g);
+  lt_groups_step<1, GQ>(g);
+  return g[0];
+}
+
+// Integer sum over the Q lanes of a slot.
+template <int Q>
+__device__ __forceinline__ int slot_isum(int v) {
+  if constexpr (Q >= 2) v += xor_lane<1>(v);
+  if constexpr (Q >= 4) v += xor_lane<2>(v);
+  if constexpr (Q >= 8) v += xor_lane<4>(v);
+  return v;
+}
+
+// (value, index) argmax step: the largest value, the smallest index among equals.
 template <int H>
 __device__ __forceinline__ void argmax_step(float& v, int& i) {
   const float ov = xor_lane<H>(v);
@@ -58,69 +112,118 @@ __device__ __forceinline__ void argmax_step(float& v, int& i) {
     i = oi;
   }
 }
-__device__ __forceinline__ int seg_argmax_idx(float v, int i, int L) {
-  if (L > 32) argmax_step<32>(v, i);
-  if (L > 16) argmax_step<16>(v, i);
-  if (L > 8) argmax_step<8>(v, i);
-  if (L > 4) argmax_step<4>(v, i);
-  if (L > 2) argmax_step<2>(v, i);
-  if (L > 1) argmax_step<1>(v, i);
+
+// Reductions over the L slots of an aligned group of slots, every lane of a slot holding the slot's value:
+// xor butterflies over the slot bits inside the wavefront, then, when the group spans several wavefronts (L * Q
+// > 64), one word per wavefront through LDS (xw, one entry per wavefront).  Every thread of the workgroup calls
+// them with the same L (they wait at workgroup barriers).  The operations are exact whatever the order: integer
+// counts held as floats, min / max, and the argmax.
+template <int Q, typename V, typename Op>
+__device__ __forceinline__ V grp_reduce(V v, int L, Op op, V* xw) {
+  const int span = L * Q < kWave ? L * Q : kWave;
+  if constexpr (Q <= 1) {
+    if (1 < span) v = op(v, xor_lane<1>(v));
+  }
+  if constexpr (Q <= 2) {
+    if (2 < span) v = op(v, xor_lane<2>(v));
+  }
+  if constexpr (Q <= 4) {
+    if (4 < span) v = op(v, xor_lane<4>(v));
+  }
+  if constexpr (Q <= 8) {
+    if (8 < span) v = op(v, xor_lane<8>(v));
+  }
+  if (16 < span) v = op(v, xor_lane<16>(v));
+  if (32 < span) v = op(v, xor_lane<32>(v));
+  if (L * Q > kWave) {
+    const int nw = L * Q / kWave, w0 = wave_id() & ~(nw - 1);
+    __syncthreads();
+    if (lane_id() == 0) xw[wave_id()] = v;
+    __syncthreads();
+    v = xw[w0];
+    for (int j = 1; j < nw; ++j) v = op(v, xw[w0 + j]);
+  }
+  return v;
+}
+template <int Q>
+__device__ __forceinline__ int grp_argmax(float v, int i, int L, float* xwf, int* xwi) {
+  const int span = L * Q < kWave ? L * Q : kWave;
+  if constexpr (Q <= 1) {
+    if (1 < span) argmax_step<1>(v, i);
+  }
+  if constexpr (Q <= 2) {
+    if (2 < span) argmax_step<2>(v, i);
+  }
+  if constexpr (Q <= 4) {
+    if (4 < span) argmax_step<4>(v, i);
+  }
+  if constexpr (Q <= 8) {
+    if (8 < span) argmax_step<8>(v, i);
+  }
+  if (16 < span) argmax_step<16>(v, i);
+  if (32 < span) argmax_step<32>(v, i);
+  if (L * Q > kWave) {
+    const int nw = L * Q / kWave, w0 = wave_id() & ~(nw - 1);
+    __syncthreads();
+    if (lane_id() == 0) {
+      xwf[wave_id()] = v;
+      xwi[wave_id()] = i;
+    }
+    __syncthreads();
+    v = xwf[w0];
+    i = xwi[w0];
+    for (int j = 1; j < nw; ++j) {
+      const float ov = xwf[w0 + j];
+      const int oi = xwi[w0 + j];
+      if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+      }
+    }
+  }
   return i;
 }
 
-// Integer min / max over an aligned L-lane segment.
-template <bool MAX>
-__device__ __forceinline__ int seg_iext(int v, int L) {
-  auto f = [](int a, int b) { return MAX ? max(a, b) : min(a, b); };
-  if (L > 32) v = f(v, xor_lane<32>(v));
-  if (L > 16) v = f(v, xor_lane<16>(v));
-  if (L > 8) v = f(v, xor_lane<8>(v));
-  if (L > 4) v = f(v, xor_lane<4>(v));
-  if (L > 2) v = f(v, xor_lane<2>(v));
-  if (L > 1) v = f(v, xor_lane<1>(v));
-  return v;
-}
-__device__ __forceinline__ int seg_imax(int v, int L) { return seg_iext<true>(v, L); }
-__device__ __forceinline__ int seg_imin(int v, int L) { return seg_iext<false>(v, L); }
-
-// Sort key of a projection: ascending float order (-0 taken as +0, as the comparison does) above the member
-// index, so that sorting the 64-bit words is the stable sort of the projections.
-__device__ __forceinline__ uint64_t lt_sort_key(float p, int idx) {
+// Sort key of a projection: ascending float order (-0 taken as +0, as the comparison does).  With the member
+// index as the second key, sorting is the stable sort of the projections.
+__device__ __forceinline__ uint32_t lt_sort_key(float p) {
   const uint32_t u = __float_as_uint(p + 0.0f);
-  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)o << 32) | (uint32_t)idx;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Ascending bitonic sort of s[0, n2) (n2 a power of two) by one wavefront.
-__device__ __forceinline__ void wave_bitonic_sort(uint64_t* s, int n2, int lane) {
+// Ascending bitonic sort of the pairs (key[i], idx[i]), i < n2 (a power of two; the indices unique), by the
+// whole workgroup.
+__device__ __forceinline__ void lt_bitonic_sort(uint32_t* key, uint16_t* idx, int n2, int tid, int nt) {
   for (int k = 2; k <= n2; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = lane; i < (n2 >> 1); i += kWave) {
+      for (int i = tid; i < (n2 >> 1); i += nt) {
         const int a = ((i & ~(j - 1)) << 1) | (i & (j - 1)), b = a + j;
-        const uint64_t x = s[a], y = s[b];
-        if ((x > y) == ((a & k) == 0)) {
-          s[a] = y;
-          s[b] = x;
+        const uint32_t ka = key[a], kb = key[b];
+        const uint16_t ia = idx[a], ib = idx[b];
+        const bool gt = ka > kb || (ka == kb && ia > ib);
+        if (gt == ((a & k) == 0)) {
+          key[a] = kb;
+          key[b] = ka;
+          idx[a] = ib;
+          idx[b] = ia;
         }
       }
-      wave_sync();
+      __syncthreads();
     }
   }
 }
 
-constexpr int kLtGroups = 16;   // groups side by side in a 64-slot window (the smallest group has 4 slots)
-
-// The outputs of lt_group_reduce for groups of L lanes: every (group, dimension) this lane owns (D / L of them,
-// at most one when L = 64), the halving tree over the group's L partials (LDS rows of stride D + 4), divided by
-// max(count, 1).  All reads are issued before the first store.
-template <int D, int L>
+// The outputs of lt_group_reduce for groups of L slots: every (group, dimension) this thread owns, the halving
+// tree over the group's L partials (LDS rows of stride D + 4), divided by max(count, 1).  All reads are issued
+// before the first store.
+template <int D, int L, int NT>
 __device__ __forceinline__ void lt_group_outputs(const float* red, const float* cnt, bool always, float* dst,
-                                                 int lane) {
-  constexpr int RS = D + 4, nout = (kWave / L) * D, NU = nout >= kWave ? nout / kWave : 1;
+                                                 int tid) {
+  constexpr int RS = D + 4, nout = (kLaneSlots / L) * D, NU = (nout + NT - 1) / NT;
   float p[NU][L], c[NU];
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
-    const int o = lane + kWave * u, g = o / D, d = o - g * D;
+    const int o = tid + NT * u, g = o / D, d = o - g * D;
     const bool in = o < nout;
     const float* col = red + g * L * RS + d;
 #pragma unroll
@@ -137,101 +240,113 @@ __device__ __forceinline__ void lt_group_outputs(const float* red, const float* 
   }
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
-    const int o = lane + kWave * u, g = o / D, d = o - g * D;
+    const int o = tid + NT * u, g = o / D, d = o - g * D;
     if (o < nout && (always || c[u] > 0.0f)) dst[g * RS + d] = p[u][0];
   }
 }
 
-// Canonical sums of the groups of L consecutive lanes (64 / L groups, L in {4, ..., 64}), in two steps:
-// lt_group_row puts this lane's partial (v, or zero when !take) into its LDS row; lt_group_reduce then reduces
-// every (group, dimension) by the halving tree over the group's L partials in one lane, divides by
-// max(count, 1) and writes dst (row stride D + 4) when the count is positive or `always`.
-template <int D>
-__device__ __forceinline__ void lt_group_row(const float (&v)[D], bool take, float* red, int lane) {
-  float* row = red + lane * (D + 4);
+// Canonical sums of the groups of L consecutive slots (64 / L groups, L in {4, ..., 64}), in two steps:
+// lt_group_row puts this lane's part of its slot's partial (v, or zero when !take) into the slot's LDS row;
+// lt_group_reduce then reduces every (group, dimension) by the halving tree over the group's L partials in one
+// thread, divides by max(count, 1) and writes dst (row stride D + 4) when the count is positive or `always`.
+__device__ __forceinline__ void lt_group_row(const float (&v)[kLaneDQ], bool take, float* row) {
 #pragma unroll
-  for (int d = 0; d < D; d += 4)
+  for (int d = 0; d < kLaneDQ; d += 4)
     *reinterpret_cast<float4*>(row + d) = take ? make_float4(v[d], v[d + 1], v[d + 2], v[d + 3])
                                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
-template <int D>
+template <int D, int NT>
 __device__ __forceinline__ void lt_group_reduce(const float* red, int L, const float* cnt, bool always, float* dst,
-                                                int lane) {
-  wave_sync();
+                                                int tid) {
+  __syncthreads();
   switch (L) {
-    case 4: lt_group_outputs<D, 4>(red, cnt, always, dst, lane); break;
-    case 8: lt_group_outputs<D, 8>(red, cnt, always, dst, lane); break;
-    case 16: lt_group_outputs<D, 16>(red, cnt, always, dst, lane); break;
-    case 32: lt_group_outputs<D, 32>(red, cnt, always, dst, lane); break;
-    default: lt_group_outputs<D, 64>(red, cnt, always, dst, lane); break;
+    case 4: lt_group_outputs<D, 4, NT>(red, cnt, always, dst, tid); break;
+    case 8: lt_group_outputs<D, 8, NT>(red, cnt, always, dst, tid); break;
+    case 16: lt_group_outputs<D, 16, NT>(red, cnt, always, dst, tid); break;
+    case 32: lt_group_outputs<D, 32, NT>(red, cnt, always, dst, tid); break;
+    default: lt_group_outputs<D, 64, NT>(red, cnt, always, dst, tid); break;
   }
-  wave_sync();
+  __syncthreads();
+}
+
+// Bytes of the build's sort area: sort keys (4 C) and indices (2 C), or the reduction rows, whichever is larger.
+__host__ __device__ constexpr int lt_sort_bytes(int C, int D) {
+  return 6 * C > kLaneSlots * (D + 4) * 4 ? ((6 * C + 15) & ~15) : kLaneSlots * (D + 4) * 4;
+}
+__host__ __device__ constexpr int lt_build_lds_bytes(int C, int D) {
+  return lt_sort_bytes(C, D) + ((2 * C + 15) & ~15) + 2 * kLtGroups * (D + 4) * 4 + 2 * kLtGroups * 4 + 16 * 4;
 }
 
 // ---------------------------------------------------------------------------------------------------- build
-// One wavefront per lane tree (dyntree.py:34-82).  Every level splits each group of S = C >> lvl slots by a
-// masked 2-means projection; the group's real keys are then laid out half and half (the larger half first),
-// empty slots after each half's keys, every empty slot holding the position of the group's last empty slot
-// (the one the stable sort ranks last).  Empty slots add key * 0 to the masked sums; they are skipped, which
-// changes at most the sign of a zero.  A window of max(S, 64) slots is done at a time: lane j holds member j
-// (and j + 64, j + 128, ... when S > 64: partial j of the canonical sums); groups of S < 64 slots sit side by
-// side, L = min(S, 64) lanes each.  Means and centroids live in LDS.  The order: for S >= 64 a bitonic sort of
-// (projection, index) over the span of the real keys, for smaller groups ranks by counting.
-// LDS: permutation (4 C bytes), sort words / projections / reduction rows (max(8 C, 64 (D + 4) 4)),
-// centroids (2 x 16 x (D + 4) floats), counts (2 x 16 floats), validity (C).
-template <typename T, int D>
-__global__ __launch_bounds__(kWave) void lanetree_build_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
-                                                               int64_t kst, int H, int C, int nlane, int chunk,
-                                                               int iters, float* __restrict__ ws, int64_t P) {
-  constexpr int RS = D + 4;
+// One workgroup per lane tree (dyntree.py:34-82).  Every level splits each group of S = C >> lvl slots of the
+// tree by a masked 2-means projection; the group's real keys are then laid out half and half (the larger half
+// first), empty slots after each half's keys, every empty slot holding the position of the group's last empty
+// slot (the one the stable sort ranks last).  Empty slots add key * 0 to the masked sums; they are skipped, which
+// changes at most the sign of a zero.  A window of max(S, 64) members is done at a time: workgroup slot j holds
+// member j (and j + 64, j + 128, ... when S > 64: partial j of the canonical sums); groups of S < 64 members
+// sit side by side, L = min(S, 64) slots each.  Means and centroids live in LDS.  The order: for S >= 64 a
+// bitonic sort of (projection, index) over the span of the real keys, for smaller groups ranks by counting.
+// LDS: the sort area (lt_sort_bytes: sort keys and indices / reduction rows / a window's projections), the tree
+// slots as 16-bit words (key position, bit 15 set when the slot holds a real key), centroids (2 x 16 x (D + 4)
+// floats), counts (2 x 16 floats), cross-wavefront words (16).
+template <typename T, int D, int Q>
+__global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
+                                                                   int64_t kst, int H, int C, int nlane, int chunk,
+                                                                   int iters, float* __restrict__ ws, int64_t P) {
+  constexpr int RS = D + 4, DQ = kLaneDQ, NT = kWave * Q;
   extern __shared__ __align__(16) unsigned char s_raw[];
-  int32_t* s_perm = reinterpret_cast<int32_t*>(s_raw);
-  uint64_t* s_sort = reinterpret_cast<uint64_t*>(s_perm + C);
-  float* s_key = reinterpret_cast<float*>(s_sort);
-  float* s_red = reinterpret_cast<float*>(s_sort);
-  const int scratch = 8 * C > kWave * RS * 4 ? 8 * C : kWave * RS * 4;
-  float* s_cen = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(s_sort) + scratch);   // [2][16][RS]
-  float* s_cnt = s_cen + 2 * kLtGroups * RS;                                                       // [2][16]
-  uint8_t* s_val = reinterpret_cast<uint8_t*>(s_cnt + 2 * kLtGroups);
-  const int lane = lane_id();
+  const int sortb = lt_sort_bytes(C, D);
+  uint32_t* s_sk = reinterpret_cast<uint32_t*>(s_raw);
+  uint16_t* s_si = reinterpret_cast<uint16_t*>(s_raw + 4 * C);
+  float* s_red = reinterpret_cast<float*>(s_raw);
+  float* s_key = reinterpret_cast<float*>(s_raw);
+  uint16_t* s_pv = reinterpret_cast<uint16_t*>(s_raw + sortb);
+  float* s_cen = reinterpret_cast<float*>(s_raw + sortb + ((2 * C + 15) & ~15));   // [2][16][RS]
+  float* s_cnt = s_cen + 2 * kLtGroups * RS;                                          // [2][16]
+  float* s_xf = s_cnt + 2 * kLtGroups;                                                // [8]
+  int* s_xi = reinterpret_cast<int*>(s_xf + 8);                                       // [8]
+  const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ;
   const int64_t pt = blockIdx.x;
   const int ln = (int)(pt % nlane);
   const int64_t bh = pt / nlane;
-  const T* kb = k + (bh / H) * ksb + (bh % H) * ksh;
+  const T* kb = k + (bh / H) * ksb + (bh % H) * ksh + d0;
   const int n0 = ln * chunk;
   const LaneTree tr = lane_tree(ws, P, C, D, pt);
   const float kInf = __int_as_float(0x7f800000);
-  for (int c = lane; c < C; c += kWave) {
-    s_perm[c] = c;
-    s_val[c] = (c >= 1 && c < n0) ? 1 : 0;
-  }
-  wave_sync();
+  auto perm = [&](int s) { return (int)(s_pv[s] & 0x7fff); };
+  auto val = [&](int s) { return (s_pv[s] & 0x8000) != 0; };
+  auto fadd = [](float a, float b) { return a + b; };
+  auto imin = [](int a, int b) { return min(a, b); };
+  auto imax = [](int a, int b) { return max(a, b); };
+  for (int c = tid; c < C; c += NT) s_pv[c] = (uint16_t)(c | ((c >= 1 && c < n0) ? 0x8000 : 0));
+  __syncthreads();
   const int nlev = lt_log2(C) - 1;
-  float x[D], acc0[D], acc1[D];
+  float x[DQ], acc0[DQ], acc1[DQ];
   for (int lvl = 0; lvl < nlev; ++lvl) {
     const int S = C >> lvl, half = S >> 1;
-    const int L = S < kWave ? S : kWave, M = S < kWave ? 1 : S / kWave, Wz = S < kWave ? kWave : S;
+    const int L = S < kLaneSlots ? S : kLaneSlots, M = S < kLaneSlots ? 1 : S / kLaneSlots;
+    const int Wz = S < kLaneSlots ? kLaneSlots : S;
     const int nwin = C > Wz ? C / Wz : 1;
-    const int g = lane / L, gl = lane & (L - 1);
-    float* c0 = s_cen + g * RS;
-    float* c1 = s_cen + (kLtGroups + g) * RS;
+    const int g = m / L, gl = m & (L - 1);
+    float* c0 = s_cen + g * RS + d0;
+    float* c1 = s_cen + (kLtGroups + g) * RS + d0;
     for (int win = 0; win < nwin; ++win) {
       const int gb = win * Wz + g * S;
-      const bool live = win * Wz + lane < C;   // C < 64: lanes past the tree sit out
+      const bool live = win * Wz + m < C;   // C < 64: slots past the tree sit out
       // (1) counts and the masked mean
 #pragma unroll
-      for (int d = 0; d < D; ++d) acc0[d] = 0.0f;
+      for (int d = 0; d < DQ; ++d) acc0[d] = 0.0f;
       float cntp = 0.0f;
       int vlo = S, vhi = -1, lastinv = -1;
-      const bool resident = M == 1;   // one member per lane: its row stays in x for every pass of the window
+      const bool resident = M == 1;   // one member per slot: its row stays in x for every pass of the window
       for (int t = 0; t < M; ++t) {
         const int i = gl + L * t, s = gb + i;
         if (!live) continue;
-        if (s_val[s]) {
-          load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
+        if (val(s)) {
+          load_row_g<T, DQ>(kb + (int64_t)perm(s) * kst, x);
           if (!resident) {
 #pragma unroll
-            for (int d = 0; d < D; ++d) acc0[d] = acc0[d] + x[d];
+            for (int d = 0; d < DQ; ++d) acc0[d] = acc0[d] + x[d];
           }
           cntp = cntp + 1.0f;
           vlo = min(vlo, i);
@@ -240,89 +355,90 @@ __global__ __launch_bounds__(kWave) void lanetree_build_kernel(const T* __restri
           lastinv = i;
         }
       }
-      const float cnt = seg_sum(cntp, L);
+      const float cnt = grp_reduce<Q>(cntp, L, fadd, s_xf);
       const int ng = (int)cnt;
-      vlo = seg_imin(vlo, L);
-      vhi = seg_imax(vhi, L);
-      lastinv = seg_imax(lastinv, L);
-      const bool work = __ballot(cntp > 0.0f) != 0;
+      vlo = grp_reduce<Q>(vlo, L, imin, s_xi);
+      vhi = grp_reduce<Q>(vhi, L, imax, s_xi);
+      lastinv = grp_reduce<Q>(lastinv, L, imax, s_xi);
+      const bool work = __syncthreads_or(cntp > 0.0f) != 0;
       if (work) {
-        if (gl == 0) s_cnt[g] = cnt;
-        if (resident) lt_group_row<D>(x, cntp > 0.0f, s_red, lane);
-        else lt_group_row<D>(acc0, true, s_red, lane);
-        lt_group_reduce<D>(s_red, L, s_cnt, true, c0 - g * RS, lane);   // the means, into c0
+        if (gl == 0 && q == 0) s_cnt[g] = cnt;
+        if (resident) lt_group_row(x, cntp > 0.0f, s_red + m * RS + d0);
+        else lt_group_row(acc0, true, s_red + m * RS + d0);
+        lt_group_reduce<D, NT>(s_red, L, s_cnt, true, s_cen, tid);   // the means, into c0
         // a = the real key farthest from the mean, then b = the real key farthest from a
         for (int pass = 0; pass < 2; ++pass) {
           float bv = -1.0f;
           int bi = 0;
           for (int t = 0; t < M; ++t) {
             const int i = gl + L * t, s = gb + i;
-            if (!live || !s_val[s]) continue;
-            if (!resident) load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
-            const float d2 = lane_dot<D>([&](int e) { return x[e] - c0[e]; }, [&](int e) { return x[e] - c0[e]; });
+            if (!live || !val(s)) continue;
+            if (!resident) load_row_g<T, DQ>(kb + (int64_t)perm(s) * kst, x);
+            const float d2 =
+                slice_dot<D, Q>([&](int e) { return x[e] - c0[e]; }, [&](int e) { return x[e] - c0[e]; });
             if (d2 > bv) {
               bv = d2;
               bi = i;
             }
           }
-          const int sel = seg_argmax_idx(bv, bi, L);
-          if (live) load_row_g<T, D>(kb + (int64_t)s_perm[gb + sel] * kst, acc1);
-          wave_sync();
+          const int sel = grp_argmax<Q>(bv, bi, L, s_xf, s_xi);
+          if (live) load_row_g<T, DQ>(kb + (int64_t)perm(gb + sel) * kst, acc1);
+          __syncthreads();
           float* dst = pass == 0 ? c0 : c1;
           if (live) {
 #pragma unroll
-            for (int d = 0; d < D; d += 4)
+            for (int d = 0; d < DQ; d += 4)
               *reinterpret_cast<float4*>(dst + d) = make_float4(acc1[d], acc1[d + 1], acc1[d + 2], acc1[d + 3]);
           }
-          wave_sync();
+          __syncthreads();
         }
         // Lloyd iterations: labels from the current centroids, then both masked sums, in one pass
         for (int it = 0; it < iters; ++it) {
-          const float cc0 = lane_dot<D>([&](int e) { return c0[e]; }, [&](int e) { return c0[e]; });
-          const float cc1 = lane_dot<D>([&](int e) { return c1[e]; }, [&](int e) { return c1[e]; });
+          const float cc0 = slice_dot<D, Q>([&](int e) { return c0[e]; }, [&](int e) { return c0[e]; });
+          const float cc1 = slice_dot<D, Q>([&](int e) { return c1[e]; }, [&](int e) { return c1[e]; });
 #pragma unroll
-          for (int d = 0; d < D; ++d) {
+          for (int d = 0; d < DQ; ++d) {
             acc0[d] = 0.0f;
             acc1[d] = 0.0f;
           }
           float cp0 = 0.0f, cp1 = 0.0f;
           for (int t = 0; t < M; ++t) {
             const int s = gb + gl + L * t;
-            if (!live || !s_val[s]) continue;
-            if (!resident) load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
-            const float xx = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return x[e]; });
-            const float xc0 = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return c0[e]; });
-            const float xc1 = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return c1[e]; });
+            if (!live || !val(s)) continue;
+            if (!resident) load_row_g<T, DQ>(kb + (int64_t)perm(s) * kst, x);
+            const float xx = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return x[e]; });
+            const float xc0 = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0[e]; });
+            const float xc1 = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c1[e]; });
             const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
             if (dist1 < dist0) {
               if (!resident) {
 #pragma unroll
-                for (int d = 0; d < D; ++d) acc1[d] = acc1[d] + x[d];
+                for (int d = 0; d < DQ; ++d) acc1[d] = acc1[d] + x[d];
               }
               cp1 = cp1 + 1.0f;
             } else {
               if (!resident) {
 #pragma unroll
-                for (int d = 0; d < D; ++d) acc0[d] = acc0[d] + x[d];
+                for (int d = 0; d < DQ; ++d) acc0[d] = acc0[d] + x[d];
               }
               cp0 = cp0 + 1.0f;
             }
           }
-          const float cj0 = seg_sum(cp0, L), cj1 = seg_sum(cp1, L);
-          if (gl == 0) {
+          const float cj0 = grp_reduce<Q>(cp0, L, fadd, s_xf), cj1 = grp_reduce<Q>(cp1, L, fadd, s_xf);
+          if (gl == 0 && q == 0) {
             s_cnt[g] = cj0;
             s_cnt[kLtGroups + g] = cj1;
           }
-          if (resident) lt_group_row<D>(x, cp0 > 0.0f, s_red, lane);
-          else lt_group_row<D>(acc0, true, s_red, lane);
-          lt_group_reduce<D>(s_red, L, s_cnt, false, c0 - g * RS, lane);
-          if (resident) lt_group_row<D>(x, cp1 > 0.0f, s_red, lane);
-          else lt_group_row<D>(acc1, true, s_red, lane);
-          lt_group_reduce<D>(s_red, L, s_cnt + kLtGroups, false, c1 - g * RS, lane);
+          if (resident) lt_group_row(x, cp0 > 0.0f, s_red + m * RS + d0);
+          else lt_group_row(acc0, true, s_red + m * RS + d0);
+          lt_group_reduce<D, NT>(s_red, L, s_cnt, false, s_cen, tid);
+          if (resident) lt_group_row(x, cp1 > 0.0f, s_red + m * RS + d0);
+          else lt_group_row(acc1, true, s_red + m * RS + d0);
+          lt_group_reduce<D, NT>(s_red, L, s_cnt + kLtGroups, false, s_cen + kLtGroups * RS, tid);
         }
       }
       const int nl = (ng + 1) / 2, nr = ng - nl;
-      if (S >= kWave) {
+      if (S >= kLaneSlots) {
         // one group: projections on c0 - c1 over the span of the real keys (empty slots inside it: +inf),
         // padded to a power of two with entries that sort last; bitonic sort
         if (ng > 0) {
@@ -330,98 +446,98 @@ __global__ __launch_bounds__(kWave) void lanetree_build_kernel(const T* __restri
           int n2 = 1;
           while (n2 < n) n2 <<= 1;
           for (int t = 0; t < M; ++t) {
-            const int i = lane + kWave * t, s = gb + i;
+            const int i = m + kLaneSlots * t, s = gb + i;
             if (i < vlo || i > vhi) continue;
             float pr = kInf;
-            if (s_val[s]) {
-              if (!resident) load_row_g<T, D>(kb + (int64_t)s_perm[s] * kst, x);
-              pr = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return c0[e] - c1[e]; });
+            if (val(s)) {
+              if (!resident) load_row_g<T, DQ>(kb + (int64_t)perm(s) * kst, x);
+              pr = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0[e] - c1[e]; });
             }
-            s_sort[i - vlo] = lt_sort_key(pr, i - vlo);
+            if (q == 0) {
+              s_sk[i - vlo] = lt_sort_key(pr);
+              s_si[i - vlo] = (uint16_t)(i - vlo);
+            }
           }
-          for (int r = n + lane; r < n2; r += kWave) s_sort[r] = lt_sort_key(kInf, r);
-          wave_sync();
-          wave_bitonic_sort(s_sort, n2, lane);
+          for (int r = n + tid; r < n2; r += NT) {
+            s_sk[r] = lt_sort_key(kInf);
+            s_si[r] = (uint16_t)r;
+          }
+          __syncthreads();
+          lt_bitonic_sort(s_sk, s_si, n2, tid, NT);
         }
         // layout: sorted ranks [0, nl) to the left half, [nl, ng) to the right half (phase A rewrites each
-        // sort word as (position, key position) before phase B moves the permutation)
-        for (int r = lane; r < ng; r += kWave) {
-          const int m = vlo + (int)(uint32_t)s_sort[r];
+        // sort key as (position, key position) before phase B moves the slots)
+        for (int r = tid; r < ng; r += NT) {
+          const int mm = vlo + (int)s_si[r];
           const int pos = r < nl ? r : half + r - nl;
-          s_sort[r] = ((uint64_t)(uint32_t)pos << 32) | (uint32_t)s_perm[gb + m];
+          s_sk[r] = ((uint32_t)pos << 16) | (uint32_t)perm(gb + mm);
         }
-        const int fillp = lastinv >= 0 ? s_perm[gb + lastinv] : 0;
-        wave_sync();
-        for (int r = lane; r < ng; r += kWave) {
-          const uint64_t e = s_sort[r];
-          s_perm[gb + (int)(e >> 32)] = (int32_t)(uint32_t)e;
+        const int fillp = lastinv >= 0 ? perm(gb + lastinv) : 0;
+        __syncthreads();
+        for (int r = tid; r < ng; r += NT) {
+          const uint32_t e = s_sk[r];
+          s_pv[gb + (int)(e >> 16)] = (uint16_t)((e & 0xffffu) | 0x8000u);
         }
-        for (int p = lane; p < S; p += kWave) {
-          const bool filled = p < half ? p < nl : (p - half) < nr;
-          if (!filled) s_perm[gb + p] = fillp;
-          s_val[gb + p] = filled ? 1 : 0;
+        for (int pp = tid; pp < S; pp += NT) {
+          const bool filled = pp < half ? pp < nl : (pp - half) < nr;
+          if (!filled) s_pv[gb + pp] = (uint16_t)fillp;
         }
-        wave_sync();
+        __syncthreads();
       } else {
-        // groups of S < 64 side by side, one member per lane: ranks by counting
+        // groups of S < 64 side by side, one member per slot: ranks by counting
         const int s = gb + gl;
-        const bool v = live && s_val[s];
+        const bool v = live && val(s);
         float key = kInf;
-        if (v) {
-          key = lane_dot<D>([&](int e) { return x[e]; }, [&](int e) { return c0[e] - c1[e]; });
-        }
-        if (live) s_key[s] = key;
-        wave_sync();
+        if (v) key = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0[e] - c1[e]; });
+        if (live && q == 0) s_key[m] = key;
+        __syncthreads();
         int rank = 0;
         if (v) {
           for (int j = 0; j < S; ++j) {
-            const float kj = s_key[gb + j];
+            const float kj = s_key[g * S + j];
             rank += (kj < key || (kj == key && j < gl)) ? 1 : 0;
           }
         }
-        const int pm = live ? s_perm[s] : 0;
-        const int fillp = live && lastinv >= 0 ? s_perm[gb + lastinv] : 0;
-        wave_sync();
-        if (v) s_perm[gb + (rank < nl ? rank : half + rank - nl)] = pm;
-        if (live) {
+        const int pm = live ? perm(s) : 0;
+        const int fillp = live && lastinv >= 0 ? perm(gb + lastinv) : 0;
+        __syncthreads();
+        if (v && q == 0) s_pv[gb + (rank < nl ? rank : half + rank - nl)] = (uint16_t)(pm | 0x8000);
+        if (live && q == 0) {
           const bool filled = gl < half ? gl < nl : (gl - half) < nr;
-          if (!filled) s_perm[s] = fillp;
-          s_val[s] = filled ? 1 : 0;
+          if (!filled) s_pv[s] = (uint16_t)fillp;
         }
-        wave_sync();
+        __syncthreads();
       }
     }
   }
   // leaf slots, then the node sums and counts by adjacent pairs from the slots up
-  for (int c = lane; c < C; c += kWave) tr.slot[c] = s_val[c] ? s_perm[c] : -1;
+  for (int c = tid; c < C; c += NT) tr.slot[c] = val(c) ? perm(c) : -1;
   const int nleaf = C / 2;
-  for (int i = lane; i < nleaf; i += kWave) {
-    float y[D];
-    load_row_g<T, D>(kb + (int64_t)s_perm[2 * i] * kst, x);
-    load_row_g<T, D>(kb + (int64_t)s_perm[2 * i + 1] * kst, y);
-    const float v0 = s_val[2 * i] ? 1.0f : 0.0f, v1 = s_val[2 * i + 1] ? 1.0f : 0.0f;
-    float* row = tr.sums + (int64_t)(nleaf - 1 + i) * D;
+  for (int i = m; i < nleaf; i += kLaneSlots) {
+    float y[DQ];
+    load_row_g<T, DQ>(kb + (int64_t)perm(2 * i) * kst, x);
+    load_row_g<T, DQ>(kb + (int64_t)perm(2 * i + 1) * kst, y);
+    const float v0 = val(2 * i) ? 1.0f : 0.0f, v1 = val(2 * i + 1) ? 1.0f : 0.0f;
+    float* row = tr.sums + (int64_t)(nleaf - 1 + i) * D + d0;
 #pragma unroll
-    for (int d = 0; d < D; d += 4)
+    for (int d = 0; d < DQ; d += 4)
       *reinterpret_cast<float4*>(row + d) =
           make_float4(x[d] * v0 + y[d] * v1, x[d + 1] * v0 + y[d + 1] * v1, x[d + 2] * v0 + y[d + 2] * v1,
                       x[d + 3] * v0 + y[d + 3] * v1);
-    tr.cnt[nleaf - 1 + i] = (int)s_val[2 * i] + (int)s_val[2 * i + 1];
+    if (q == 0) tr.cnt[nleaf - 1 + i] = (int)val(2 * i) + (int)val(2 * i + 1);
   }
   for (int lv = nlev - 1; lv >= 0; --lv) {
-    __threadfence_block();
+    __syncthreads();
     const int nn = 1 << lv, base = nn - 1, cb = 2 * nn - 1;
-    for (int i = lane; i < nn; i += kWave) {
-      const float* a = tr.sums + (int64_t)(cb + 2 * i) * D;
-      float* row = tr.sums + (int64_t)(base + i) * D;
-#pragma unroll
-      for (int d = 0; d < D; d += 4) {
-        const float4 u = *reinterpret_cast<const float4*>(a + d);
-        const float4 w = *reinterpret_cast<const float4*>(a + D + d);
-        *reinterpret_cast<float4*>(row + d) = make_float4(u.x + w.x, u.y + w.y, u.z + w.z, u.w + w.w);
-      }
-      tr.cnt[base + i] = tr.cnt[cb + 2 * i] + tr.cnt[cb + 2 * i + 1];
+    for (int w = tid; w < nn * (D / 4); w += NT) {
+      const int i = w / (D / 4), d = (w - i * (D / 4)) * 4;
+      const float* a = tr.sums + (int64_t)(cb + 2 * i) * D + d;
+      const float4 u = *reinterpret_cast<const float4*>(a);
+      const float4 z = *reinterpret_cast<const float4*>(a + D);
+      *reinterpret_cast<float4*>(tr.sums + (int64_t)(base + i) * D + d) =
+          make_float4(u.x + z.x, u.y + z.y, u.z + z.z, u.w + z.w);
     }
+    for (int i = tid; i < nn; i += NT) tr.cnt[base + i] = tr.cnt[cb + 2 * i] + tr.cnt[cb + 2 * i + 1];
   }
 }
 
@@ -445,7 +561,7 @@ struct LaneWalk {
 
 // The nodes of a lane tree during the walk: nodes [0, ntop) (its top levels) live in LDS for the whole walk
 // (rows of stride D + 4 floats, and counts), deeper nodes in the workspace; the leaf slots (C entries) live in
-// LDS too.  Every access below is uniform in which side it takes (one level at a time).
+// LDS too.  A lane reads and writes its 16 dimensions of a row.
 template <int D>
 struct LaneNodes {
   LaneTree tr;
@@ -458,18 +574,11 @@ struct LaneNodes {
     if (n < ntop) tcnt[n] = v;
     else tr.cnt[n] = v;
   }
-  __device__ __forceinline__ float elem(int n, int d) const {
-    return n < ntop ? top[n * (D + 4) + d] : tr.sums[(int64_t)n * D + d];
-  }
-  __device__ __forceinline__ void set_elem(int n, int d, float v) const {
-    if (n < ntop) top[n * (D + 4) + d] = v;
-    else tr.sums[(int64_t)n * D + d] = v;
-  }
-  __device__ __forceinline__ void row(int n, float (&r)[D]) const {
+  __device__ __forceinline__ void row(int n, int d0, float (&r)[kLaneDQ]) const {
     if (n < ntop) {
-      const float* src = top + n * (D + 4);
+      const float* src = top + n * (D + 4) + d0;
 #pragma unroll
-      for (int d = 0; d < D; d += 4) {
+      for (int d = 0; d < kLaneDQ; d += 4) {
         const float4 v = *reinterpret_cast<const float4*>(src + d);
         r[d] = v.x;
         r[d + 1] = v.y;
@@ -477,45 +586,41 @@ struct LaneNodes {
         r[d + 3] = v.w;
       }
     } else {
-      load_row_g<float, D>(tr.sums + (int64_t)n * D, r);
+      load_row_g<float, kLaneDQ>(tr.sums + (int64_t)n * D + d0, r);
+    }
+  }
+  __device__ __forceinline__ void set_row(int n, int d0, const float (&r)[kLaneDQ]) const {
+    if (n < ntop) {
+      float* dst = top + n * (D + 4) + d0;
+#pragma unroll
+      for (int d = 0; d < kLaneDQ; d += 4)
+        *reinterpret_cast<float4*>(dst + d) = make_float4(r[d], r[d + 1], r[d + 2], r[d + 3]);
+    } else {
+      float* dst = tr.sums + (int64_t)n * D + d0;
+#pragma unroll
+      for (int d = 0; d < kLaneDQ; d += 4)
+        *reinterpret_cast<float4*>(dst + d) = make_float4(r[d], r[d + 1], r[d + 2], r[d + 3]);
     }
   }
   // workspace -> LDS (to_lds) or back
-  __device__ __forceinline__ void copy(bool to_lds, int lane) const {
-    for (int i = lane; i < ntop * (D / 4); i += kWave) {
+  __device__ __forceinline__ void copy(bool to_lds, int tid, int nt) const {
+    for (int i = tid; i < ntop * (D / 4); i += nt) {
       const int n = i / (D / 4), d = (i - n * (D / 4)) * 4;
       float4* l = reinterpret_cast<float4*>(top + n * (D + 4) + d);
       float4* g = reinterpret_cast<float4*>(tr.sums + (int64_t)n * D + d);
       if (to_lds) *l = *g;
       else *g = *l;
     }
-    for (int n = lane; n < ntop; n += kWave) {
+    for (int n = tid; n < ntop; n += nt) {
       if (to_lds) tcnt[n] = tr.cnt[n];
       else tr.cnt[n] = tcnt[n];
     }
-    for (int n = lane; n < C; n += kWave) {
+    for (int n = tid; n < C; n += nt) {
       if (to_lds) slot[n] = tr.slot[n];
       else tr.slot[n] = slot[n];
     }
   }
 };
-
-// Canonical dot of two D-vectors held one element per lane (lane d < D holds a[d] * b[d] in `prod`, 0 past D):
-// the halving tree inside groups of R = D/16 consecutive lanes, then over the 16 groups (lanes R apart), as
-// an xor butterfly (every lane ends with the sum).
-template <int D>
-__device__ __forceinline__ float dims_dot(float prod) {
-  constexpr int R = D < 16 ? 1 : D / 16;
-  if constexpr (R >= 4) prod = prod + xor_lane<2>(prod);
-  if constexpr (R >= 2) prod = prod + xor_lane<1>(prod);
-  if constexpr (8 * R >= 32) prod = prod + xor_lane<32>(prod);
-  if constexpr (8 * R >= 16 && R <= 16) prod = prod + xor_lane<16>(prod);
-  if constexpr (R <= 8) prod = prod + xor_lane<8>(prod);
-  if constexpr (R <= 4) prod = prod + xor_lane<4>(prod);
-  if constexpr (R <= 2) prod = prod + xor_lane<2>(prod);
-  if constexpr (R <= 1) prod = prod + xor_lane<1>(prod);
-  return prod;
-}
 
 // Search ranking word: valid first, then score descending, node id ascending; invalid candidates by slot.
 // Unique per candidate, so a candidate's rank is the number of smaller words.
@@ -526,26 +631,28 @@ __device__ __forceinline__ uint64_t lt_rank_word(bool valid, float sc, int id, i
   return ((uint64_t)(~asc) << 31) | (uint32_t)id;
 }
 
-// One wavefront per lane tree, built by lanetree_build_kernel, walking the lane's positions in order
-// (dyntree.py:148-243).  The tree state is read back by the same wavefront after its own stores; a
-// workgroup-scope fence ends every position.
-template <typename T, int D>
-__global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
+// One workgroup per lane tree, built by lanetree_build_kernel, walking the lane's positions in order
+// (dyntree.py:148-243).  Slot j scores neighbour entry j and the level's children j and j + 64; the lanes of
+// slot 0 insert the position's key.  A workgroup barrier ends every position (the tree rows the insertion
+// wrote are read by other wavefronts at the next one).
+template <typename T, int D, int Q>
+__global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
+  constexpr int DQ = kLaneDQ, NT = kWave * Q;
   __shared__ int32_t s_stl[kLaneMaxNb];   // stored leaves of the last Wn positions (ring), NS each
   __shared__ float s_sts[kLaneMaxNb];
   __shared__ uint8_t s_sto[kLaneMaxNb];
-  __shared__ int32_t s_nid[kWave];
-  __shared__ __align__(16) uint64_t s_rw[kWave];   // the level's children's ranking words
-  __shared__ int32_t s_cur[kWave];   // the beam
-  __shared__ float s_bsc[kWave];
-  __shared__ uint8_t s_bok[kWave];
-  const int lane = lane_id();
+  __shared__ int32_t s_nid[kLaneSlots];
+  __shared__ __align__(16) uint64_t s_rw[2 * kLaneMaxW];   // the level's children's ranking words
+  __shared__ int32_t s_cur[kLaneMaxW];                      // the beam
+  __shared__ float s_bsc[kLaneMaxW];
+  __shared__ uint8_t s_bok[kLaneMaxW];
+  const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ;
   const int64_t pt = blockIdx.x;
   const int ln = (int)(pt % p.nlane);
   const int64_t bh = pt / p.nlane;
   const int64_t b = bh / p.H, h = bh % p.H;
-  const T* qb = static_cast<const T*>(p.q) + b * p.qsb + h * p.qsh;
-  const T* kb = static_cast<const T*>(p.k) + b * p.ksb + h * p.ksh;
+  const T* qb = static_cast<const T*>(p.q) + b * p.qsb + h * p.qsh + d0;
+  const T* kb = static_cast<const T*>(p.k) + b * p.ksb + h * p.ksh + d0;
   const LaneTree tr = lane_tree(p.ws, p.P, p.C, D, pt);
   extern __shared__ __align__(16) unsigned char s_dyn[];
   LaneNodes<D> nd;
@@ -555,61 +662,67 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
   nd.slot = nd.tcnt + p.ntop;
   nd.ntop = p.ntop;
   nd.C = p.C;
-  nd.copy(true, lane);
-  wave_sync();
+  nd.copy(true, tid, NT);
+  __syncthreads();
   const int WN = p.Wn * p.NS, wl = p.wl, nlev = p.nlev;
   const float kInf = __int_as_float(0x7f800000);
   const int start = ln * p.chunk;
-  float qn[D];   // the next position's query and key, requested while the current position runs
-  load_row_g<T, D>(qb + (int64_t)start * p.qst, qn);
-  float kn = lane < D ? to_f32(kb[(int64_t)start * p.kst + lane]) : 0.0f;
+  const bool ins = tid < Q;   // the lanes of slot 0 insert the keys
+  float qn[DQ], kn[DQ];       // the next position's query and key, requested while the current position runs
+  load_row_g<T, DQ>(qb + (int64_t)start * p.qst, qn);
+#pragma unroll
+  for (int d = 0; d < DQ; ++d) kn[d] = 0.0f;
+  if (ins) load_row_g<T, DQ>(kb + (int64_t)start * p.kst, kn);
   for (int i = 0; i < p.chunk; ++i) {
     const int t = start + i;
     const int64_t orow = bh * p.T + t;
-    float qv[D];
+    float qv[DQ], kd[DQ];
 #pragma unroll
-    for (int d = 0; d < D; ++d) qv[d] = qn[d];
-    const float kd = kn;
+    for (int d = 0; d < DQ; ++d) {
+      qv[d] = qn[d];
+      kd[d] = kn[d];
+    }
     if (i + 1 < p.chunk) {
-      load_row_g<T, D>(qb + (int64_t)(t + 1) * p.qst, qn);
-      kn = lane < D ? to_f32(kb[(int64_t)(t + 1) * p.kst + lane]) : 0.0f;
+      load_row_g<T, DQ>(qb + (int64_t)(t + 1) * p.qst, qn);
+      if (ins) load_row_g<T, DQ>(kb + (int64_t)(t + 1) * p.kst, kn);
     }
     // ---- neighbours: the leaves the last Wn positions of the lane stored, re-scored on the current tree
     int id = 0;
     bool ok0 = false, match = false;
-    if (lane < WN) {
-      const int back = lane / p.NS + 1, j = i - back;
+    if (m < WN) {
+      const int back = m / p.NS + 1, j = i - back;
       if (j >= 0) {
-        const int rs = (j % p.Wn) * p.NS + lane % p.NS;
+        const int rs = (j % p.Wn) * p.NS + m % p.NS;
         ok0 = s_sto[rs] != 0;
         id = s_stl[rs];
         if (ok0) {
           const int node = (1 << nlev) - 1 + id;
           const int cn = nd.cnt(node);
-          float row[D];
-          nd.row(node, row);
-          const float sc = lane_dot<D>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) /
+          float row[DQ];
+          nd.row(node, d0, row);
+          const float sc = slice_dot<D, Q>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) /
                            (float)(cn > 1 ? cn : 1);
           const float base = s_sts[rs];
           match = cn > 0 && sc >= base - p.rho * fabsf(base);
         }
       }
     }
-    const bool inprobe = lane < p.probe;
-    const int pm = __popcll(__ballot(match && inprobe)), po = __popcll(__ballot(ok0 && inprobe));
+    const bool inprobe = m < p.probe;
+    const int pm = __syncthreads_count(match && inprobe && q == 0);
+    const int po = __syncthreads_count(ok0 && inprobe && q == 0);
     const float rate = (float)pm / fmaxf((float)po, 1.0f);
     const int cap = p.cap_min + (int)rintf((float)(p.Wn - p.cap_min) * rate);
-    match = match && (lane / p.NS + 1) <= cap && p.neighbors;
-    s_nid[lane] = match ? id : -1;
-    wave_sync();
+    match = match && (m / p.NS + 1) <= cap && p.neighbors;
+    if (q == 0) s_nid[m] = match ? id : -1;
+    __syncthreads();
     bool first = match;
-    for (int e = 0; e < lane && first; ++e) first = s_nid[e] != id;
-    const int nL = __popcll(__ballot(first));
-    if (lane < WN) {
+    for (int e = 0; e < m && first; ++e) first = s_nid[e] != id;
+    const int nL = __syncthreads_count(first && q == 0);
+    if (m < WN && q == 0) {
       const int s0 = nd.slot[2 * id], s1 = nd.slot[2 * id + 1];
       int32_t* o = p.nb_pos + orow * 2 * WN;
-      o[lane] = match && s0 >= 0 ? s0 : -1;
-      o[WN + lane] = match && s1 >= 0 ? s1 : -1;
+      o[m] = match && s0 >= 0 ? s0 : -1;
+      o[WN + m] = match && s1 >= 0 ? s1 : -1;
     }
     // ---- budget (dyntree.py:218-222)
     const int Lq = p.lhat[orow];
@@ -617,109 +730,124 @@ __global__ __launch_bounds__(kWave) void lanetree_walk_kernel(LaneWalk p) {
     int bt = nL >= Lq ? 0 : (need > floor_b ? need : floor_b);
     bt = bt < p.wmax ? bt : p.wmax;
     // ---- beam search from the root
-    if (lane == 0) {
+    if (tid == 0) {
       s_cur[0] = 0;
       s_bok[0] = nd.cnt(0) > 0;
       s_bsc[0] = 0.0f;
     }
-    wave_sync();
+    __syncthreads();
     int wp = 1;
     for (int lv = 1; lv <= nlev; ++lv) {
       const int nch = 2 * wp;
-      int cid = 0;
-      bool cv = false;
-      float sc = -kInf;
-      if (lane < nch) {
-        const int par = lane < wp ? lane : lane - wp;
-        cid = 2 * s_cur[par] + (lane < wp ? 0 : 1);
-        if (s_bok[par]) {
-          const int node = (1 << lv) - 1 + cid;
-          const int cn = nd.cnt(node);
-          float row[D];
-          nd.row(node, row);
-          cv = cn > 0;
-          if (cv)
-            sc = lane_dot<D>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) / (float)(cn > 1 ? cn : 1);
-        }
-        s_rw[lane] = lt_rank_word(cv, sc, cid, lane);
-      }
-      wave_sync();
-      const int w = nch < p.wmax ? nch : p.wmax;
-      if (lane < nch) {
-        const uint64_t mine = s_rw[lane];
-        int rank = 0;
-        for (int j0 = 0; j0 < nch; j0 += 8) {   // words read four pairs at a time
-          uint64_t wv[8];
+      int cid[2];
+      bool cv[2];
+      float sc[2];
+      uint64_t mine[2];
 #pragma unroll
-          for (int h = 0; h < 4; ++h) {
-            const uint4 two = *reinterpret_cast<const uint4*>(s_rw + j0 + 2 * h);
-            wv[2 * h] = ((uint64_t)two.y << 32) | two.x;
-            wv[2 * h + 1] = ((uint64_t)two.w << 32) | two.z;
+      for (int r = 0; r < 2; ++r) {
+        const int c = m + kLaneSlots * r;
+        cid[r] = 0;
+        cv[r] = false;
+        sc[r] = -kInf;
+        mine[r] = 0;
+        if (c < nch) {
+          const int par = c < wp ? c : c - wp;
+          cid[r] = 2 * s_cur[par] + (c < wp ? 0 : 1);
+          if (s_bok[par]) {
+            const int node = (1 << lv) - 1 + cid[r];
+            const int cn = nd.cnt(node);
+            float row[DQ];
+            nd.row(node, d0, row);
+            cv[r] = cn > 0;
+            if (cv[r])
+              sc[r] = slice_dot<D, Q>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) /
+                      (float)(cn > 1 ? cn : 1);
           }
-#pragma unroll
-          for (int h = 0; h < 8; ++h) rank += (j0 + h < nch && wv[h] < mine) ? 1 : 0;
-        }
-        if (rank < w) {
-          s_cur[rank] = cid;
-          s_bsc[rank] = sc;
-          s_bok[rank] = cv;
+          mine[r] = lt_rank_word(cv[r], sc[r], cid[r], c);
+          if (q == 0) s_rw[c] = mine[r];
         }
       }
-      wave_sync();
+      __syncthreads();
+      const int w = nch < p.wmax ? nch : p.wmax;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int c = m + kLaneSlots * r;
+        if (c < nch) {   // the slot's lanes count the smaller words among every Q-th word, then add up
+          int rank = 0;
+          for (int j = q; j < nch; j += Q) rank += s_rw[j] < mine[r] ? 1 : 0;
+          rank = slot_isum<Q>(rank);
+          if (q == 0 && rank < w) {
+            s_cur[rank] = cid[r];
+            s_bsc[rank] = sc[r];
+            s_bok[rank] = cv[r];
+          }
+        }
+      }
+      __syncthreads();
       wp = w;
     }
     // ---- outputs, and the stored leaves of this position
-    if (lane < wl) {
-      const int lid = s_cur[lane];
-      const bool ok = s_bok[lane] != 0;
+    if (m < wl && q == 0) {
+      const int lid = s_cur[m];
+      const bool ok = s_bok[m] != 0;
       const int s0 = nd.slot[2 * lid], s1 = nd.slot[2 * lid + 1];
       int32_t* o = p.tree_pos + orow * 2 * wl;
-      o[lane] = ok && s0 >= 0 ? s0 : -1;
-      o[wl + lane] = ok && s1 >= 0 ? s1 : -1;
-      p.leaf_ok[orow * wl + lane] = ok ? 1 : 0;
+      o[m] = ok && s0 >= 0 ? s0 : -1;
+      o[wl + m] = ok && s1 >= 0 ? s1 : -1;
+      p.leaf_ok[orow * wl + m] = ok ? 1 : 0;
     }
-    if (lane == 0) {
+    if (tid == 0) {
       p.n_tree[orow] = bt;
       p.nb_leaves[orow] = nL;
     }
-    if (lane < p.NS) {
-      const int rs = (i % p.Wn) * p.NS + lane;
-      s_stl[rs] = s_cur[lane];
-      s_sts[rs] = s_bsc[lane];
-      s_sto[rs] = s_bok[lane];
+    if (m < p.NS && q == 0) {
+      const int rs = (i % p.Wn) * p.NS + m;
+      s_stl[rs] = s_cur[m];
+      s_sts[rs] = s_bsc[m];
+      s_sto[rs] = s_bok[m];
     }
-    // ---- insertion of this position's key (dyntree.py:84-106), one dimension per lane
-    const int act = t >= 1 ? 1 : 0;
-    const float kva = kd * (act ? 1.0f : 0.0f);
-    if (lane < D) nd.set_elem(0, lane, nd.elem(0, lane) + kva);
-    if (lane == 0) nd.set_cnt(0, nd.cnt(0) + act);
-    int node = 0;
-    for (int lv = 0; lv < nlev; ++lv) {
-      const int base = (2 << lv) - 1, lc = 2 * node, cap = p.C >> (lv + 1);
-      const int cL = nd.cnt(base + lc), cR = nd.cnt(base + lc + 1);
-      const float xL = lane < D ? nd.elem(base + lc, lane) : 0.0f;
-      const float xR = lane < D ? nd.elem(base + lc + 1, lane) : 0.0f;
-      const float dL = dims_dot<D>(kd * xL), dR = dims_dot<D>(kd * xR);
-      float sL = cL == 0 ? -1e9f : dL / (float)(cL > 1 ? cL : 1);
-      float sR = cR == 0 ? -1e9f : dR / (float)(cR > 1 ? cR : 1);
-      if (cL >= cap) sL = -kInf;
-      if (cR >= cap) sR = -kInf;
-      const bool right = sR > sL;
-      node = lc + (right ? 1 : 0);
-      if (lane < D) nd.set_elem(base + node, lane, (right ? xR : xL) + kva);
-      if (lane == 0) nd.set_cnt(base + node, (right ? cR : cL) + act);
+    // ---- insertion of this position's key (dyntree.py:84-106) by the lanes of slot 0
+    if (ins) {
+      const int act = t >= 1 ? 1 : 0;
+      float kva[DQ], r0[DQ];
+#pragma unroll
+      for (int d = 0; d < DQ; ++d) kva[d] = kd[d] * (act ? 1.0f : 0.0f);
+      nd.row(0, d0, r0);
+#pragma unroll
+      for (int d = 0; d < DQ; ++d) r0[d] = r0[d] + kva[d];
+      nd.set_row(0, d0, r0);
+      if (q == 0) nd.set_cnt(0, nd.cnt(0) + act);
+      int node = 0;
+      for (int lv = 0; lv < nlev; ++lv) {
+        const int base = (2 << lv) - 1, lc = 2 * node, cap = p.C >> (lv + 1);
+        const int cL = nd.cnt(base + lc), cR = nd.cnt(base + lc + 1);
+        float xL[DQ], xR[DQ];
+        nd.row(base + lc, d0, xL);
+        nd.row(base + lc + 1, d0, xR);
+        const float dL = slice_dot<D, Q>([&](int e) { return kd[e]; }, [&](int e) { return xL[e]; });
+        const float dR = slice_dot<D, Q>([&](int e) { return kd[e]; }, [&](int e) { return xR[e]; });
+        float sL = cL == 0 ? -1e9f : dL / (float)(cL > 1 ? cL : 1);
+        float sR = cR == 0 ? -1e9f : dR / (float)(cR > 1 ? cR : 1);
+        if (cL >= cap) sL = -kInf;
+        if (cR >= cap) sR = -kInf;
+        const bool right = sR > sL;
+        node = lc + (right ? 1 : 0);
+#pragma unroll
+        for (int d = 0; d < DQ; ++d) xL[d] = (right ? xR[d] : xL[d]) + kva[d];
+        nd.set_row(base + node, d0, xL);
+        if (q == 0) nd.set_cnt(base + node, (right ? cR : cL) + act);
+      }
+      if (q == 0 && act) {
+        const int s0 = nd.slot[2 * node];
+        nd.slot[2 * node + (s0 >= 0 ? 1 : 0)] = t;
+      }
     }
-    if (lane == 0 && act) {
-      const int s0 = nd.slot[2 * node];
-      nd.slot[2 * node + (s0 >= 0 ? 1 : 0)] = t;
-    }
-    __threadfence_block();
-    wave_sync();
+    __syncthreads();
   }
-  nd.copy(false, lane);
+  nd.copy(false, tid, NT);
 }
 
-bool lanetree_dim_ok(int D) { return D == 16 || D == 32 || D == 64; }
+bool lanetree_dim_ok(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
 int lanetree_levels(int T) {
   int lg = 0;
@@ -734,8 +862,8 @@ using namespace ta;
 extern "C" int ta_lanetree_workspace_size(int B, int H, int T, int D, int chunk, int64_t* bytes) {
   if (B <= 0 || H <= 0 || T < 4 || T > kLaneMaxT || (T & (T - 1)) || chunk <= 0 || T % chunk ||
       !lanetree_dim_ok(D) || bytes == nullptr) {
-    set_error("ta_lanetree_workspace_size: bad arguments (T a power of two in [4, 4096], chunk dividing T, "
-              "D 16, 32 or 64)");
+    set_error("ta_lanetree_workspace_size: bad arguments (T a power of two in [4, 16384], chunk dividing T, "
+              "D 16, 32, 64 or 128)");
     return TA_ERR_ARG;
   }
   const int64_t P = (int64_t)B * H * (T / chunk);
@@ -758,18 +886,17 @@ extern "C" int ta_lanetree_build(const void* k, int dtype, int64_t ksb, int64_t 
     return TA_ERR_ARG;
   }
   const int64_t P = (int64_t)B * H * (T / chunk);
-  const size_t red = (size_t)kWave * (D + 4) * 4;
-  const size_t lds = (size_t)T * 4 + ((size_t)T * 8 > red ? (size_t)T * 8 : red) +
-                     (size_t)2 * kLtGroups * (D + 4) * 4 + (size_t)2 * kLtGroups * 4 + (size_t)T;
+  const size_t lds = (size_t)lt_build_lds_bytes(T, D);
   hipStream_t st = (hipStream_t)stream;
 #define TA_LB(TT, DD)                                                                                          \
-  hipLaunchKernelGGL((lanetree_build_kernel<TT, DD>), dim3((unsigned)P), dim3(kWave), lds, st, (const TT*)k, \
-                     ksb, ksh, kst, H, T, T / chunk, chunk, kmeans_iters, (float*)ws, P)
+  hipLaunchKernelGGL((lanetree_build_kernel<TT, DD, DD / kLaneDQ>), dim3((unsigned)P), dim3(DD / kLaneDQ * kWave), \
+                     lds, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, chunk, kmeans_iters, (float*)ws, P)
 #define TA_LB_D(TT)                  \
   switch (D) {                       \
     case 16: TA_LB(TT, 16); break;   \
     case 32: TA_LB(TT, 32); break;   \
-    default: TA_LB(TT, 64); break;   \
+    case 64: TA_LB(TT, 64); break;   \
+    default: TA_LB(TT, 128); break;  \
   }
   switch (dtype) {
     case TA_F32: TA_LB_D(float); break;
@@ -798,13 +925,14 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
       leaf_ok == nullptr || nb_pos == nullptr || n_tree == nullptr || nb_leaves == nullptr || wmax < 1 ||
       wmax > kLaneMaxW || nb_window < 1 || nb_store < 1 || nb_window * nb_store > kLaneMaxNb || nb_store > wl ||
       nb_probe < 0 || !(nb_rho == nb_rho)) {
-    set_error("ta_lanetree_walk: bad arguments (1 <= wmax <= 32, nb_window * nb_store <= 64, nb_store at most "
+    set_error("ta_lanetree_walk: bad arguments (1 <= wmax <= 64, nb_window * nb_store <= 64, nb_store at most "
               "the leaves per query, workspace from ta_lanetree_workspace_size)");
     return TA_ERR_ARG;
   }
   const int es = dtype == TA_F32 ? 4 : 2;
-  if (((uintptr_t)q % 16) || (qsb * es) % 16 || (qsh * es) % 16 || (qst * es) % 16) {
-    set_error("ta_lanetree_walk: query rows 16-byte aligned");
+  if (((uintptr_t)q % 16) || (qsb * es) % 16 || (qsh * es) % 16 || (qst * es) % 16 || ((uintptr_t)k % 16) ||
+      (ksb * es) % 16 || (ksh * es) % 16 || (kst * es) % 16) {
+    set_error("ta_lanetree_walk: query and key rows 16-byte aligned");
     return TA_ERR_ARG;
   }
   LaneWalk p{};
@@ -824,13 +952,15 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
   p.ntop = ntop;
   const size_t lds = (size_t)ntop * rowb + (size_t)T * 4;   // + the leaf slots
   hipStream_t st = (hipStream_t)stream;
-#define TA_LW(TT, DD) \
-  hipLaunchKernelGGL((lanetree_walk_kernel<TT, DD>), dim3((unsigned)p.P), dim3(kWave), lds, st, p)
+#define TA_LW(TT, DD)                                                                                          \
+  hipLaunchKernelGGL((lanetree_walk_kernel<TT, DD, DD / kLaneDQ>), dim3((unsigned)p.P), dim3(DD / kLaneDQ * kWave), \
+                     lds, st, p)
 #define TA_LW_D(TT)                  \
   switch (D) {                       \
     case 16: TA_LW(TT, 16); break;   \
     case 32: TA_LW(TT, 32); break;   \
-    default: TA_LW(TT, 64); break;   \
+    case 64: TA_LW(TT, 64); break;   \
+    default: TA_LW(TT, 128); break;  \
   }
   switch (dtype) {
     case TA_F32: TA_LW_D(float); break;
