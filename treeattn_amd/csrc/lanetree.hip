@@ -26,6 +26,8 @@
 //  * search ranking: valid first, score descending, node id ascending (invalid candidates by slot).
 #pragma clang fp contract(off)
 
+#include <type_traits>
+
 #include "canon.hpp"
 
 namespace ta {
@@ -102,25 +104,12 @@ __device__ __forceinline__ int slot_isum(int v) {
   return v;
 }
 
-// (value, index) argmax step: the largest value, the smallest index among equals.
-template <int H>
-__device__ __forceinline__ void argmax_step(float& v, int& i) {
-  const float ov = xor_lane<H>(v);
-  const int oi = xor_lane<H>(i);
-  if (ov > v || (ov == v && oi < i)) {
-    v = ov;
-    i = oi;
-  }
-}
-
-// Reductions over the L slots of an aligned group of slots, every lane of a slot holding the slot's value:
-// xor butterflies over the slot bits inside the wavefront, then, when the group spans several wavefronts (L * Q
-// > 64), one word per wavefront through LDS (xw, one entry per wavefront).  Every thread of the workgroup calls
-// them with the same L (they wait at workgroup barriers).  The operations are exact whatever the order: integer
-// counts held as floats, min / max, and the argmax.
+// In-wavefront part of a reduction over the L slots of an aligned group of slots, every lane of a slot holding
+// the slot's value (span = min(L * Q, 64) lanes): xor butterflies over the slot bits.  The operations used are
+// exact whatever the order: integer counts held as floats, min / max, and the argmax (the largest value, the
+// smallest index among equals).
 template <int Q, typename V, typename Op>
-__device__ __forceinline__ V grp_reduce(V v, int L, Op op, V* xw) {
-  const int span = L * Q < kWave ? L * Q : kWave;
+__device__ __forceinline__ V wave_grp(V v, int span, Op op) {
   if constexpr (Q <= 1) {
     if (1 < span) v = op(v, xor_lane<1>(v));
   }
@@ -135,19 +124,19 @@ __device__ __forceinline__ V grp_reduce(V v, int L, Op op, V* xw) {
   }
   if (16 < span) v = op(v, xor_lane<16>(v));
   if (32 < span) v = op(v, xor_lane<32>(v));
-  if (L * Q > kWave) {
-    const int nw = L * Q / kWave, w0 = wave_id() & ~(nw - 1);
-    __syncthreads();
-    if (lane_id() == 0) xw[wave_id()] = v;
-    __syncthreads();
-    v = xw[w0];
-    for (int j = 1; j < nw; ++j) v = op(v, xw[w0 + j]);
-  }
   return v;
 }
+template <int H>
+__device__ __forceinline__ void argmax_step(float& v, int& i) {
+  const float ov = xor_lane<H>(v);
+  const int oi = xor_lane<H>(i);
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
 template <int Q>
-__device__ __forceinline__ int grp_argmax(float v, int i, int L, float* xwf, int* xwi) {
-  const int span = L * Q < kWave ? L * Q : kWave;
+__device__ __forceinline__ void wave_grp_argmax(float& v, int& i, int span) {
   if constexpr (Q <= 1) {
     if (1 < span) argmax_step<1>(v, i);
   }
@@ -162,27 +151,20 @@ __device__ __forceinline__ int grp_argmax(float v, int i, int L, float* xwf, int
   }
   if (16 < span) argmax_step<16>(v, i);
   if (32 < span) argmax_step<32>(v, i);
-  if (L * Q > kWave) {
-    const int nw = L * Q / kWave, w0 = wave_id() & ~(nw - 1);
-    __syncthreads();
-    if (lane_id() == 0) {
-      xwf[wave_id()] = v;
-      xwi[wave_id()] = i;
-    }
-    __syncthreads();
-    v = xwf[w0];
-    i = xwi[w0];
-    for (int j = 1; j < nw; ++j) {
-      const float ov = xwf[w0 + j];
-      const int oi = xwi[w0 + j];
-      if (ov > v || (ov == v && oi < i)) {
-        v = ov;
-        i = oi;
-      }
-    }
-  }
-  return i;
 }
+
+// Cross-wavefront words (8 per wavefront) in two LDS buffers used in turn: a buffer is written again only after
+// every thread has passed the barrier of the exchange in between, so one workgroup barrier per exchange
+// suffices.  Every thread makes the same sequence of exchanges.
+struct LtXchg {
+  int* buf;   // [2][8 wavefronts][8]
+  int sel;
+  __device__ __forceinline__ int* next() {
+    int* b = buf + sel * 64;
+    sel ^= 1;
+    return b;
+  }
+};
 
 // Sort key of a projection: ascending float order (-0 taken as +0, as the comparison does).  With the member
 // index as the second key, sorting is the stable sort of the projections.
@@ -213,22 +195,34 @@ __device__ __forceinline__ void lt_bitonic_sort(uint32_t* key, uint16_t* idx, in
   }
 }
 
-// The outputs of lt_group_reduce for groups of L slots: every (group, dimension) this thread owns, the halving
-// tree over the group's L partials (LDS rows of stride D + 4), divided by max(count, 1).  All reads are issued
-// before the first store.
-template <int D, int L, int NT>
-__device__ __forceinline__ void lt_group_outputs(const float* red, const float* cnt, bool always, float* dst,
+// Canonical sums of the groups of L consecutive slots (64 / L groups, L in {4, ..., 64}), for NSET sets of slot
+// rows at once.  Each slot writes its partial (lt_group_row: this lane's 16 dimensions) into its row of a set
+// (64 rows of stride D + 4), and the group's member count is left in gc as nseg partial counts per group (set s,
+// group g at gc[16 s + nseg g + j], integers); lt_group_reduce then reduces every (set, group, dimension) in one
+// thread: the halving tree over the group's L partials, divided by max(count, 1).  The value goes to dst + set *
+// 16 (D + 4) + group (D + 4) + dimension when the count is positive or `always`.  All reads are issued before
+// the first store.
+__device__ __forceinline__ void lt_group_row(const float (&v)[kLaneDQ], bool take, float* row) {
+#pragma unroll
+  for (int d = 0; d < kLaneDQ; d += 4)
+    *reinterpret_cast<float4*>(row + d) = take ? make_float4(v[d], v[d + 1], v[d + 2], v[d + 3])
+                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+template <int D, int L, int NT, int NSET>
+__device__ __forceinline__ void lt_group_outputs(const float* red, const float* gc, int nseg, bool always, float* dst,
                                                  int tid) {
-  constexpr int RS = D + 4, nout = (kLaneSlots / L) * D, NU = (nout + NT - 1) / NT;
+  constexpr int RS = D + 4, nout1 = (kLaneSlots / L) * D, nout = NSET * nout1, NU = (nout + NT - 1) / NT;
   float p[NU][L], c[NU];
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
-    const int o = tid + NT * u, g = o / D, d = o - g * D;
+    const int o = tid + NT * u, set = o / nout1, r = o - set * nout1, g = r / D, d = r - g * D;
     const bool in = o < nout;
-    const float* col = red + g * L * RS + d;
+    const float* base = red + (set * kLaneSlots + g * L) * RS;
 #pragma unroll
-    for (int j = 0; j < L; ++j) p[u][j] = in ? col[j * RS] : 0.0f;
-    c[u] = in ? cnt[g] : 0.0f;
+    for (int j = 0; j < L; ++j) p[u][j] = in ? base[j * RS + d] : 0.0f;
+    float cs = 0.0f;
+    for (int j = 0; j < nseg; ++j) cs = cs + (in ? gc[set * kLtGroups + g * nseg + j] : 0.0f);
+    c[u] = cs;
   }
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
@@ -240,41 +234,81 @@ __device__ __forceinline__ void lt_group_outputs(const float* red, const float* 
   }
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
-    const int o = tid + NT * u, g = o / D, d = o - g * D;
-    if (o < nout && (always || c[u] > 0.0f)) dst[g * RS + d] = p[u][0];
+    const int o = tid + NT * u, set = o / nout1, r = o - set * nout1, g = r / D, d = r - g * D;
+    if (o < nout && (always || c[u] > 0.0f)) dst[(set * kLtGroups + g) * RS + d] = p[u][0];
   }
 }
-
-// Canonical sums of the groups of L consecutive slots (64 / L groups, L in {4, ..., 64}), in two steps:
-// lt_group_row puts this lane's part of its slot's partial (v, or zero when !take) into the slot's LDS row;
-// lt_group_reduce then reduces every (group, dimension) by the halving tree over the group's L partials in one
-// thread, divides by max(count, 1) and writes dst (row stride D + 4) when the count is positive or `always`.
-__device__ __forceinline__ void lt_group_row(const float (&v)[kLaneDQ], bool take, float* row) {
-#pragma unroll
-  for (int d = 0; d < kLaneDQ; d += 4)
-    *reinterpret_cast<float4*>(row + d) = take ? make_float4(v[d], v[d + 1], v[d + 2], v[d + 3])
-                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-}
-template <int D, int NT>
-__device__ __forceinline__ void lt_group_reduce(const float* red, int L, const float* cnt, bool always, float* dst,
-                                                int tid) {
+template <int D, int NT, int NSET>
+__device__ __forceinline__ void lt_group_reduce(const float* red, const float* gc, int nseg, int L, bool always,
+                                                float* dst, int tid) {
   __syncthreads();
   switch (L) {
-    case 4: lt_group_outputs<D, 4, NT>(red, cnt, always, dst, tid); break;
-    case 8: lt_group_outputs<D, 8, NT>(red, cnt, always, dst, tid); break;
-    case 16: lt_group_outputs<D, 16, NT>(red, cnt, always, dst, tid); break;
-    case 32: lt_group_outputs<D, 32, NT>(red, cnt, always, dst, tid); break;
-    default: lt_group_outputs<D, 64, NT>(red, cnt, always, dst, tid); break;
+    case 4: lt_group_outputs<D, 4, NT, NSET>(red, gc, nseg, always, dst, tid); break;
+    case 8: lt_group_outputs<D, 8, NT, NSET>(red, gc, nseg, always, dst, tid); break;
+    case 16: lt_group_outputs<D, 16, NT, NSET>(red, gc, nseg, always, dst, tid); break;
+    case 32: lt_group_outputs<D, 32, NT, NSET>(red, gc, nseg, always, dst, tid); break;
+    default: lt_group_outputs<D, 64, NT, NSET>(red, gc, nseg, always, dst, tid); break;
   }
   __syncthreads();
 }
 
-// Bytes of the build's sort area: sort keys (4 C) and indices (2 C), or the reduction rows, whichever is larger.
-__host__ __device__ constexpr int lt_sort_bytes(int C, int D) {
-  return 6 * C > kLaneSlots * (D + 4) * 4 ? ((6 * C + 15) & ~15) : kLaneSlots * (D + 4) * 4;
+// lt_group_reduce for groups that lie inside one wavefront (L * Q <= 64): the wavefront reduces the outputs of
+// its own groups (64 / (Q L) of them, from group wave * 64 / (Q L) on), between wavefront barriers.
+template <int D, int Q, int L, int NSET>
+__device__ __forceinline__ void lt_group_outputs_w(const float* red, const float* gc, bool always, float* dst, int lane,
+                                                   int wv) {
+  if constexpr (L * Q <= kWave) {
+    constexpr int RS = D + 4, gpw = kWave / (Q * L), nout1 = gpw * D, nout = NSET * nout1;
+    constexpr int NU = (nout + kWave - 1) / kWave;
+    float p[NU][L], c[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int o = lane + kWave * u, set = o / nout1, r = o - set * nout1, gg = wv * gpw + r / D, d = r % D;
+      const bool in = o < nout;
+      const float* base = red + (set * kLaneSlots + gg * L) * RS;
+#pragma unroll
+      for (int j = 0; j < L; ++j) p[u][j] = in ? base[j * RS + d] : 0.0f;
+      c[u] = in ? gc[set * kLtGroups + gg] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+#pragma unroll
+      for (int n = L / 2; n >= 1; n >>= 1)
+#pragma unroll
+        for (int i = 0; i < n; ++i) p[u][i] = p[u][i] + p[u][i + n];
+      p[u][0] = p[u][0] / fmaxf(c[u], 1.0f);
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int o = lane + kWave * u, set = o / nout1, r = o - set * nout1, gg = wv * gpw + r / D, d = r % D;
+      if (o < nout && (always || c[u] > 0.0f)) dst[(set * kLtGroups + gg) * RS + d] = p[u][0];
+    }
+  }
+}
+template <int D, int Q, int NSET>
+__device__ __forceinline__ void lt_group_reduce_w(const float* red, const float* gc, int L, bool always, float* dst,
+                                                  int lane, int wv) {
+  wave_sync();
+  switch (L) {
+    case 4: lt_group_outputs_w<D, Q, 4, NSET>(red, gc, always, dst, lane, wv); break;
+    case 8: lt_group_outputs_w<D, Q, 8, NSET>(red, gc, always, dst, lane, wv); break;
+    case 16: lt_group_outputs_w<D, Q, 16, NSET>(red, gc, always, dst, lane, wv); break;
+    case 32: lt_group_outputs_w<D, Q, 32, NSET>(red, gc, always, dst, lane, wv); break;
+    default: lt_group_outputs_w<D, Q, 64, NSET>(red, gc, always, dst, lane, wv); break;
+  }
+  wave_sync();
+}
+
+// The build's LDS: the row area (three sets of 64 slot rows: A the mean's partials, B and C the two Lloyd
+// partials; or a level's sort keys and indices, 6 bytes per slot), the tree slots as 16-bit words (key
+// position, bit 15 set when the slot holds a real key), three centroid banks of 16 groups (the mean, c0, c1),
+// the rank keys of two windows and the cross-wavefront words.
+__host__ __device__ constexpr int lt_rows_bytes(int C, int D) {
+  return 6 * C > 3 * kLaneSlots * (D + 4) * 4 ? ((6 * C + 15) & ~15) : 3 * kLaneSlots * (D + 4) * 4;
 }
 __host__ __device__ constexpr int lt_build_lds_bytes(int C, int D) {
-  return lt_sort_bytes(C, D) + ((2 * C + 15) & ~15) + 2 * kLtGroups * (D + 4) * 4 + 2 * kLtGroups * 4 + 16 * 4;
+  return lt_rows_bytes(C, D) + ((2 * C + 15) & ~15) + 3 * kLtGroups * (D + 4) * 4 + 2 * kLaneSlots * 4 +
+         2 * 64 * 4 + 3 * kLtGroups * 4;
 }
 
 // ---------------------------------------------------------------------------------------------------- build
@@ -283,29 +317,27 @@ __host__ __device__ constexpr int lt_build_lds_bytes(int C, int D) {
 // first), empty slots after each half's keys, every empty slot holding the position of the group's last empty
 // slot (the one the stable sort ranks last).  Empty slots add key * 0 to the masked sums; they are skipped, which
 // changes at most the sign of a zero.  A window of max(S, 64) members is done at a time: workgroup slot j holds
-// member j (and j + 64, j + 128, ... when S > 64: partial j of the canonical sums); groups of S < 64 members
-// sit side by side, L = min(S, 64) slots each.  Means and centroids live in LDS.  The order: for S >= 64 a
-// bitonic sort of (projection, index) over the span of the real keys, for smaller groups ranks by counting.
-// LDS: the sort area (lt_sort_bytes: sort keys and indices / reduction rows / a window's projections), the tree
-// slots as 16-bit words (key position, bit 15 set when the slot holds a real key), centroids (2 x 16 x (D + 4)
-// floats), counts (2 x 16 floats), cross-wavefront words (16).
+// member j (and j + 64, j + 128, ... when S > 64: partial j of the canonical sums, their rows requested four at
+// a time); groups of S < 64 members sit side by side, L = min(S, 64) slots each, and then a slot's member row
+// stays in registers for the whole window (the next window's row is requested while this one runs) and the
+// two farthest members are read from the mean's slot rows in LDS.  The order: for S >= 64 a bitonic sort of
+// (projection, index) over the span of the real keys, for smaller groups ranks by counting.
 template <typename T, int D, int Q>
 __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
                                                                    int64_t kst, int H, int C, int nlane, int chunk,
                                                                    int iters, float* __restrict__ ws, int64_t P) {
-  constexpr int RS = D + 4, DQ = kLaneDQ, NT = kWave * Q;
+  constexpr int RS = D + 4, DQ = kLaneDQ, NT = kWave * Q, U = Q >= 8 ? 2 : 4;   // U: member rows requested at a time
   extern __shared__ __align__(16) unsigned char s_raw[];
-  const int sortb = lt_sort_bytes(C, D);
-  uint32_t* s_sk = reinterpret_cast<uint32_t*>(s_raw);
-  uint16_t* s_si = reinterpret_cast<uint16_t*>(s_raw + 4 * C);
-  float* s_red = reinterpret_cast<float*>(s_raw);
-  float* s_key = reinterpret_cast<float*>(s_raw);
-  uint16_t* s_pv = reinterpret_cast<uint16_t*>(s_raw + sortb);
-  float* s_cen = reinterpret_cast<float*>(s_raw + sortb + ((2 * C + 15) & ~15));   // [2][16][RS]
-  float* s_cnt = s_cen + 2 * kLtGroups * RS;                                          // [2][16]
-  float* s_xf = s_cnt + 2 * kLtGroups;                                                // [8]
-  int* s_xi = reinterpret_cast<int*>(s_xf + 8);                                       // [8]
-  const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ;
+  const int rowsb = lt_rows_bytes(C, D);
+  float* s_rows = reinterpret_cast<float*>(s_raw);                                    // [3][64][RS]
+  uint32_t* s_sk = reinterpret_cast<uint32_t*>(s_raw);                                // [C]
+  uint16_t* s_si = reinterpret_cast<uint16_t*>(s_raw + 4 * C);                        // [C]
+  uint16_t* s_pv = reinterpret_cast<uint16_t*>(s_raw + rowsb);                        // [C]
+  float* s_cen = reinterpret_cast<float*>(s_raw + rowsb + ((2 * C + 15) & ~15));   // [3][16][RS]
+  float* s_key = s_cen + 3 * kLtGroups * RS;                                          // [2][64]
+  LtXchg xw{reinterpret_cast<int*>(s_key + 2 * kLaneSlots), 0};
+  float* s_gc = s_key + 2 * kLaneSlots + 2 * 64;   // [3][16] group counts: the mean's, then the two clusters'
+  const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ, wv = wave_id();
   const int64_t pt = blockIdx.x;
   const int ln = (int)(pt % nlane);
   const int64_t bh = pt / nlane;
@@ -321,200 +353,345 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
   for (int c = tid; c < C; c += NT) s_pv[c] = (uint16_t)(c | ((c >= 1 && c < n0) ? 0x8000 : 0));
   __syncthreads();
   const int nlev = lt_log2(C) - 1;
-  float x[DQ], acc0[DQ], acc1[DQ];
-  for (int lvl = 0; lvl < nlev; ++lvl) {
-    const int S = C >> lvl, half = S >> 1;
-    const int L = S < kLaneSlots ? S : kLaneSlots, M = S < kLaneSlots ? 1 : S / kLaneSlots;
-    const int Wz = S < kLaneSlots ? kLaneSlots : S;
-    const int nwin = C > Wz ? C / Wz : 1;
-    const int g = m / L, gl = m & (L - 1);
-    float* c0 = s_cen + g * RS + d0;
-    float* c1 = s_cen + (kLtGroups + g) * RS + d0;
-    for (int win = 0; win < nwin; ++win) {
-      const int gb = win * Wz + g * S;
-      const bool live = win * Wz + m < C;   // C < 64: slots past the tree sit out
-      // (1) counts and the masked mean
+  // the level's geometry (set_level)
+  int S = 0, half = 0, L = 0, M = 0, Wz = 0, nwin = 0, g = 0, gl = 0, span = 0;
+  float *meanp = nullptr, *c0b = nullptr, *c1b = nullptr;   // the group's mean, c0 and c1 (this lane's part)
+  float* rowA = s_rows + m * RS;                              // this slot's rows of the sets A, B, C
+  float* rowB = rowA + kLaneSlots * RS;
+  float* rowC = rowB + kLaneSlots * RS;
+  auto set_level = [&](int lvl) {
+    S = C >> lvl;
+    half = S >> 1;
+    L = S < kLaneSlots ? S : kLaneSlots;
+    M = S < kLaneSlots ? 1 : S / kLaneSlots;
+    Wz = S < kLaneSlots ? kLaneSlots : S;
+    nwin = C > Wz ? C / Wz : 1;
+    g = m / L;
+    gl = m & (L - 1);
+    span = L * Q < kWave ? L * Q : kWave;
+    meanp = s_cen + g * RS + d0;
+    c0b = s_cen + (kLtGroups + g) * RS + d0;
+    c1b = s_cen + (2 * kLtGroups + g) * RS + d0;
+  };
+  // One window of a level.  RES: one member per slot (S <= 64), its row in x for the whole window; otherwise
+  // the slot's members are scanned in order, rows requested U at a time, partial sums in acc0 / acc1.
+  auto window = [&](auto res, auto loc, int win, float(&x)[DQ], float(&acc0)[DQ], float(&acc1)[DQ])
+                    __attribute__((always_inline)) {
+    constexpr bool resident = decltype(res)::value;
+    constexpr bool local = decltype(loc)::value;   // every group inside one wavefront: wavefront barriers
+    auto sync = [&]() {
+      if constexpr (local) wave_sync();
+      else __syncthreads();
+    };
+    const int gb = win * Wz + g * S;
+    const bool live = win * Wz + m < C;   // C < 64: slots past the tree sit out
+    auto scan = [&](auto&& f) __attribute__((always_inline)) {
+      for (int t0 = 0; t0 < M; t0 += U) {
+        float xb[U][DQ];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int t = t0 + u < M ? t0 + u : M - 1;
+          load_row_g<T, DQ>(kb + (int64_t)perm(gb + gl + L * t) * kst, xb[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (t0 + u < M) f(gl + L * (t0 + u), xb[u]);
+      }
+    };
+    // (1) counts and the masked mean
+    float cntp = 0.0f;
+    int vlo = S, vhi = -1, lastinv = -1;
+    if constexpr (resident) {
+      if (live) {
+        if (val(gb + gl)) {
+          cntp = 1.0f;
+          vlo = vhi = gl;
+        } else {
+          lastinv = gl;
+        }
+      }
+    } else {
 #pragma unroll
       for (int d = 0; d < DQ; ++d) acc0[d] = 0.0f;
-      float cntp = 0.0f;
-      int vlo = S, vhi = -1, lastinv = -1;
-      const bool resident = M == 1;   // one member per slot: its row stays in x for every pass of the window
-      for (int t = 0; t < M; ++t) {
-        const int i = gl + L * t, s = gb + i;
-        if (!live) continue;
-        if (val(s)) {
-          load_row_g<T, DQ>(kb + (int64_t)perm(s) * kst, x);
-          if (!resident) {
+      scan([&](int i, const float(&r)[DQ]) {
+        if (val(gb + i)) {
 #pragma unroll
-            for (int d = 0; d < DQ; ++d) acc0[d] = acc0[d] + x[d];
-          }
+          for (int d = 0; d < DQ; ++d) acc0[d] = acc0[d] + r[d];
           cntp = cntp + 1.0f;
           vlo = min(vlo, i);
           vhi = max(vhi, i);
         } else {
           lastinv = i;
         }
+      });
+    }
+    float cnt = wave_grp<Q>(cntp, span, fadd);
+    vlo = wave_grp<Q>(vlo, span, imin);
+    vhi = wave_grp<Q>(vhi, span, imax);
+    lastinv = wave_grp<Q>(lastinv, span, imax);
+    bool work = __ballot(cntp > 0.0f) != 0;
+    if constexpr (Q > 1 && !local) {   // the group's statistics across wavefronts, and whether any group has keys
+      int* xb = xw.next();
+      if (lane_id() == 0) {
+        int* e = xb + wv * 8;
+        e[0] = __float_as_int(cnt);
+        e[1] = vlo;
+        e[2] = vhi;
+        e[3] = lastinv;
+        e[4] = work ? 1 : 0;
       }
-      const float cnt = grp_reduce<Q>(cntp, L, fadd, s_xf);
-      const int ng = (int)cnt;
-      vlo = grp_reduce<Q>(vlo, L, imin, s_xi);
-      vhi = grp_reduce<Q>(vhi, L, imax, s_xi);
-      lastinv = grp_reduce<Q>(lastinv, L, imax, s_xi);
-      const bool work = __syncthreads_or(cntp > 0.0f) != 0;
-      if (work) {
-        if (gl == 0 && q == 0) s_cnt[g] = cnt;
-        if (resident) lt_group_row(x, cntp > 0.0f, s_red + m * RS + d0);
-        else lt_group_row(acc0, true, s_red + m * RS + d0);
-        lt_group_reduce<D, NT>(s_red, L, s_cnt, true, s_cen, tid);   // the means, into c0
-        // a = the real key farthest from the mean, then b = the real key farthest from a
-        for (int pass = 0; pass < 2; ++pass) {
-          float bv = -1.0f;
-          int bi = 0;
-          for (int t = 0; t < M; ++t) {
-            const int i = gl + L * t, s = gb + i;
-            if (!live || !val(s)) continue;
-            if (!resident) load_row_g<T, DQ>(kb + (int64_t)perm(s) * kst, x);
+      __syncthreads();
+      if (L * Q > kWave) {
+        const int nw = L * Q / kWave, w0 = wv & ~(nw - 1);
+        cnt = 0.0f;
+        vlo = S;
+        vhi = -1;
+        lastinv = -1;
+        for (int j = 0; j < nw; ++j) {
+          const int* e = xb + (w0 + j) * 8;
+          cnt = cnt + __int_as_float(e[0]);
+          vlo = min(vlo, e[1]);
+          vhi = max(vhi, e[2]);
+          lastinv = max(lastinv, e[3]);
+        }
+      }
+      work = false;
+      for (int j = 0; j < Q; ++j) work = work || xb[j * 8 + 4] != 0;
+    }
+    const int ng = (int)cnt;
+    // the group argmax of (value, member index)
+    auto argmax_grp = [&](float v, int i) {
+      wave_grp_argmax<Q>(v, i, span);
+      if (L * Q > kWave) {
+        int* xb = xw.next();
+        if (lane_id() == 0) {
+          xb[wv * 8] = __float_as_int(v);
+          xb[wv * 8 + 1] = i;
+        }
+        __syncthreads();
+        const int nw = L * Q / kWave, w0 = wv & ~(nw - 1);
+        v = __int_as_float(xb[w0 * 8]);
+        i = xb[w0 * 8 + 1];
+        for (int j = 1; j < nw; ++j) {
+          const float ov = __int_as_float(xb[(w0 + j) * 8]);
+          const int oi = xb[(w0 + j) * 8 + 1];
+          if (ov > v || (ov == v && oi < i)) {
+            v = ov;
+            i = oi;
+          }
+        }
+      }
+      return i;
+    };
+    if (work) {
+      if constexpr (resident) lt_group_row(x, cntp > 0.0f, rowA + d0);
+      else lt_group_row(acc0, true, rowA + d0);
+      if (gl == 0 && q == 0) s_gc[g] = cnt;
+      if constexpr (local) lt_group_reduce_w<D, Q, 1>(s_rows, s_gc, L, true, s_cen, lane_id(), wv);   // the means
+      else lt_group_reduce<D, NT, 1>(s_rows, s_gc, 1, L, true, s_cen, tid);
+      // a = the real key farthest from the mean, then b = the real key farthest from a
+      const float* pa = c0b;
+      const float* pb = c1b;
+      for (int pass = 0; pass < 2; ++pass) {
+        const float* ref = pass == 0 ? meanp : pa;
+        float bv = -1.0f;
+        int bi = 0;
+        if constexpr (resident) {
+          if (live && cntp > 0.0f) {
+            bv = slice_dot<D, Q>([&](int e) { return x[e] - ref[e]; }, [&](int e) { return x[e] - ref[e]; });
+            bi = gl;
+          }
+        } else {
+          scan([&](int i, const float(&r)[DQ]) {
+            if (!val(gb + i)) return;
             const float d2 =
-                slice_dot<D, Q>([&](int e) { return x[e] - c0[e]; }, [&](int e) { return x[e] - c0[e]; });
+                slice_dot<D, Q>([&](int e) { return r[e] - ref[e]; }, [&](int e) { return r[e] - ref[e]; });
             if (d2 > bv) {
               bv = d2;
               bi = i;
             }
-          }
-          const int sel = grp_argmax<Q>(bv, bi, L, s_xf, s_xi);
-          if (live) load_row_g<T, DQ>(kb + (int64_t)perm(gb + sel) * kst, acc1);
-          __syncthreads();
-          float* dst = pass == 0 ? c0 : c1;
+          });
+        }
+        const int sel = argmax_grp(bv, bi);
+        float* bank = pass == 0 ? c0b : c1b;
+        if constexpr (resident) {
+          // the selected member's row is its slot's row of set A; copied into the centroid bank, which the
+          // Lloyd outputs keep for an empty cluster and the projection reads
+          const float* src = s_rows + (g * L + sel) * RS + d0;
+          if (pass == 0) pa = src;
+          else pb = src;
           if (live) {
 #pragma unroll
             for (int d = 0; d < DQ; d += 4)
-              *reinterpret_cast<float4*>(dst + d) = make_float4(acc1[d], acc1[d + 1], acc1[d + 2], acc1[d + 3]);
+              *reinterpret_cast<float4*>(bank + d) = *reinterpret_cast<const float4*>(src + d);
           }
+        } else {
+          load_row_g<T, DQ>(kb + (int64_t)perm(gb + sel) * kst, acc1);
+#pragma unroll
+          for (int d = 0; d < DQ; d += 4)
+            *reinterpret_cast<float4*>(bank + d) = make_float4(acc1[d], acc1[d + 1], acc1[d + 2], acc1[d + 3]);
           __syncthreads();
         }
-        // Lloyd iterations: labels from the current centroids, then both masked sums, in one pass
-        for (int it = 0; it < iters; ++it) {
-          const float cc0 = slice_dot<D, Q>([&](int e) { return c0[e]; }, [&](int e) { return c0[e]; });
-          const float cc1 = slice_dot<D, Q>([&](int e) { return c1[e]; }, [&](int e) { return c1[e]; });
+      }
+      // Lloyd iterations: labels from the current centroids, then both masked sums, in one pass and one
+      // reduction (sets B and C into the banks c0 and c1; an empty cluster keeps its centroid)
+      for (int it = 0; it < iters; ++it) {
+        const float* r0 = it == 0 ? pa : c0b;
+        const float* r1 = it == 0 ? pb : c1b;
+        const float cc0 = slice_dot<D, Q>([&](int e) { return r0[e]; }, [&](int e) { return r0[e]; });
+        const float cc1 = slice_dot<D, Q>([&](int e) { return r1[e]; }, [&](int e) { return r1[e]; });
+        float cp0 = 0.0f, cp1 = 0.0f;
+        auto label = [&](const float(&r)[DQ]) {
+          const float xx = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return r[e]; });
+          const float xc0 = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return r0[e]; });
+          const float xc1 = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return r1[e]; });
+          const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
+          return dist1 < dist0;
+        };
+        if constexpr (resident) {
+          if (live && cntp > 0.0f) {
+            if (label(x)) cp1 = 1.0f;
+            else cp0 = 1.0f;
+          }
+          lt_group_row(x, cp0 > 0.0f, rowB + d0);
+          lt_group_row(x, cp1 > 0.0f, rowC + d0);
+        } else {
 #pragma unroll
           for (int d = 0; d < DQ; ++d) {
             acc0[d] = 0.0f;
             acc1[d] = 0.0f;
           }
-          float cp0 = 0.0f, cp1 = 0.0f;
-          for (int t = 0; t < M; ++t) {
-            const int s = gb + gl + L * t;
-            if (!live || !val(s)) continue;
-            if (!resident) load_row_g<T, DQ>(kb + (int64_t)perm(s) * kst, x);
-            const float xx = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return x[e]; });
-            const float xc0 = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0[e]; });
-            const float xc1 = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c1[e]; });
-            const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
-            if (dist1 < dist0) {
-              if (!resident) {
+          scan([&](int i, const float(&r)[DQ]) {
+            if (!val(gb + i)) return;
+            if (label(r)) {
 #pragma unroll
-                for (int d = 0; d < DQ; ++d) acc1[d] = acc1[d] + x[d];
-              }
+              for (int d = 0; d < DQ; ++d) acc1[d] = acc1[d] + r[d];
               cp1 = cp1 + 1.0f;
             } else {
-              if (!resident) {
 #pragma unroll
-                for (int d = 0; d < DQ; ++d) acc0[d] = acc0[d] + x[d];
-              }
+              for (int d = 0; d < DQ; ++d) acc0[d] = acc0[d] + r[d];
               cp0 = cp0 + 1.0f;
             }
+          });
+          lt_group_row(acc0, true, rowB + d0);
+          lt_group_row(acc1, true, rowC + d0);
+        }
+        // the clusters' counts: a partial per aligned segment of `span` lanes (a group inside a wavefront, or
+        // a group's part in one wavefront)
+        const float w0 = wave_grp<Q>(cp0, span, fadd), w1 = wave_grp<Q>(cp1, span, fadd);
+        if ((tid & (span - 1)) == 0) {
+          s_gc[kLtGroups + tid / span] = w0;
+          s_gc[2 * kLtGroups + tid / span] = w1;
+        }
+        if constexpr (local)
+          lt_group_reduce_w<D, Q, 2>(s_rows + kLaneSlots * RS, s_gc + kLtGroups, L, false, s_cen + kLtGroups * RS,
+                                     lane_id(), wv);
+        else
+          lt_group_reduce<D, NT, 2>(s_rows + kLaneSlots * RS, s_gc + kLtGroups, L * Q / span, L, false,
+                                    s_cen + kLtGroups * RS, tid);
+      }
+      if (resident && iters == 0) sync();   // the banks' copies of a and b, for the projection
+    }
+    const int nl = (ng + 1) / 2, nr = ng - nl;
+    if constexpr (!resident) {
+      // one group: projections on c0 - c1 over the span of the real keys (empty slots inside it: +inf),
+      // padded to a power of two with entries that sort last; bitonic sort
+      if (ng > 0) {
+        const int n = vhi - vlo + 1;
+        int n2 = 1;
+        while (n2 < n) n2 <<= 1;
+        auto proj = [&](int i, const float(&r)[DQ]) {
+          if (i < vlo || i > vhi) return;
+          float pr = kInf;
+          if (val(gb + i))
+            pr = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return c0b[e] - c1b[e]; });
+          if (q == 0) {
+            s_sk[i - vlo] = lt_sort_key(pr);
+            s_si[i - vlo] = (uint16_t)(i - vlo);
           }
-          const float cj0 = grp_reduce<Q>(cp0, L, fadd, s_xf), cj1 = grp_reduce<Q>(cp1, L, fadd, s_xf);
-          if (gl == 0 && q == 0) {
-            s_cnt[g] = cj0;
-            s_cnt[kLtGroups + g] = cj1;
-          }
-          if (resident) lt_group_row(x, cp0 > 0.0f, s_red + m * RS + d0);
-          else lt_group_row(acc0, true, s_red + m * RS + d0);
-          lt_group_reduce<D, NT>(s_red, L, s_cnt, false, s_cen, tid);
-          if (resident) lt_group_row(x, cp1 > 0.0f, s_red + m * RS + d0);
-          else lt_group_row(acc1, true, s_red + m * RS + d0);
-          lt_group_reduce<D, NT>(s_red, L, s_cnt + kLtGroups, false, s_cen + kLtGroups * RS, tid);
+        };
+        scan(proj);
+        for (int r = n + tid; r < n2; r += NT) {
+          s_sk[r] = lt_sort_key(kInf);
+          s_si[r] = (uint16_t)r;
+        }
+        __syncthreads();
+        lt_bitonic_sort(s_sk, s_si, n2, tid, NT);
+      }
+      // layout: sorted ranks [0, nl) to the left half, [nl, ng) to the right half (phase A rewrites each
+      // sort key as (position, key position) before phase B moves the slots)
+      for (int r = tid; r < ng; r += NT) {
+        const int mm = vlo + (int)s_si[r];
+        const int pos = r < nl ? r : half + r - nl;
+        s_sk[r] = ((uint32_t)pos << 16) | (uint32_t)perm(gb + mm);
+      }
+      const int fillp = lastinv >= 0 ? perm(gb + lastinv) : 0;
+      __syncthreads();
+      for (int r = tid; r < ng; r += NT) {
+        const uint32_t e = s_sk[r];
+        s_pv[gb + (int)(e >> 16)] = (uint16_t)((e & 0xffffu) | 0x8000u);
+      }
+      for (int pp = tid; pp < S; pp += NT) {
+        const bool filled = pp < half ? pp < nl : (pp - half) < nr;
+        if (!filled) s_pv[gb + pp] = (uint16_t)fillp;
+      }
+      __syncthreads();
+    } else {
+      // one member per slot (groups of S <= 64, side by side when S < 64): ranks by counting, the stable
+      // order of the projections (the rank keys alternate between two windows' areas; a window's slot words
+      // are read by no other window)
+      const int s = gb + gl;
+      const bool v = live && val(s);
+      float key = kInf;
+      if (v) key = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0b[e] - c1b[e]; });
+      const int pm = live ? perm(s) : 0;
+      const int fillp = live && lastinv >= 0 ? perm(gb + lastinv) : 0;
+      float* keys = s_key + (win & 1) * kLaneSlots;
+      if (live && q == 0) keys[m] = key;
+      sync();
+      int rank = 0;
+      if (v) {
+        for (int j = 0; j < S; ++j) {
+          const float kj = keys[g * S + j];
+          rank += (kj < key || (kj == key && j < gl)) ? 1 : 0;
         }
       }
-      const int nl = (ng + 1) / 2, nr = ng - nl;
-      if (S >= kLaneSlots) {
-        // one group: projections on c0 - c1 over the span of the real keys (empty slots inside it: +inf),
-        // padded to a power of two with entries that sort last; bitonic sort
-        if (ng > 0) {
-          const int n = vhi - vlo + 1;
-          int n2 = 1;
-          while (n2 < n) n2 <<= 1;
-          for (int t = 0; t < M; ++t) {
-            const int i = m + kLaneSlots * t, s = gb + i;
-            if (i < vlo || i > vhi) continue;
-            float pr = kInf;
-            if (val(s)) {
-              if (!resident) load_row_g<T, DQ>(kb + (int64_t)perm(s) * kst, x);
-              pr = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0[e] - c1[e]; });
-            }
-            if (q == 0) {
-              s_sk[i - vlo] = lt_sort_key(pr);
-              s_si[i - vlo] = (uint16_t)(i - vlo);
-            }
-          }
-          for (int r = n + tid; r < n2; r += NT) {
-            s_sk[r] = lt_sort_key(kInf);
-            s_si[r] = (uint16_t)r;
-          }
-          __syncthreads();
-          lt_bitonic_sort(s_sk, s_si, n2, tid, NT);
-        }
-        // layout: sorted ranks [0, nl) to the left half, [nl, ng) to the right half (phase A rewrites each
-        // sort key as (position, key position) before phase B moves the slots)
-        for (int r = tid; r < ng; r += NT) {
-          const int mm = vlo + (int)s_si[r];
-          const int pos = r < nl ? r : half + r - nl;
-          s_sk[r] = ((uint32_t)pos << 16) | (uint32_t)perm(gb + mm);
-        }
-        const int fillp = lastinv >= 0 ? perm(gb + lastinv) : 0;
-        __syncthreads();
-        for (int r = tid; r < ng; r += NT) {
-          const uint32_t e = s_sk[r];
-          s_pv[gb + (int)(e >> 16)] = (uint16_t)((e & 0xffffu) | 0x8000u);
-        }
-        for (int pp = tid; pp < S; pp += NT) {
-          const bool filled = pp < half ? pp < nl : (pp - half) < nr;
-          if (!filled) s_pv[gb + pp] = (uint16_t)fillp;
-        }
-        __syncthreads();
-      } else {
-        // groups of S < 64 side by side, one member per slot: ranks by counting
-        const int s = gb + gl;
-        const bool v = live && val(s);
-        float key = kInf;
-        if (v) key = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0[e] - c1[e]; });
-        if (live && q == 0) s_key[m] = key;
-        __syncthreads();
-        int rank = 0;
-        if (v) {
-          for (int j = 0; j < S; ++j) {
-            const float kj = s_key[g * S + j];
-            rank += (kj < key || (kj == key && j < gl)) ? 1 : 0;
-          }
-        }
-        const int pm = live ? perm(s) : 0;
-        const int fillp = live && lastinv >= 0 ? perm(gb + lastinv) : 0;
-        __syncthreads();
-        if (v && q == 0) s_pv[gb + (rank < nl ? rank : half + rank - nl)] = (uint16_t)(pm | 0x8000);
-        if (live && q == 0) {
-          const bool filled = gl < half ? gl < nl : (gl - half) < nr;
-          if (!filled) s_pv[s] = (uint16_t)fillp;
-        }
-        __syncthreads();
+      if (v && q == 0) s_pv[gb + (rank < nl ? rank : half + rank - nl)] = (uint16_t)(pm | 0x8000);
+      if (live && q == 0) {
+        const bool filled = gl < half ? gl < nl : (gl - half) < nr;
+        if (!filled) s_pv[s] = (uint16_t)fillp;
       }
+    }
+  };
+  int lvl = 0;
+  {   // levels with S > 64: several members per slot
+    float acc0[DQ], acc1[DQ], xd[DQ];
+    for (; lvl < nlev && (C >> lvl) > kLaneSlots; ++lvl) {
+      set_level(lvl);
+      for (int win = 0; win < nwin; ++win) window(std::false_type{}, std::false_type{}, win, xd, acc0, acc1);
+      __syncthreads();
+    }
+  }
+  {   // levels with S <= 64: the next window's member row is requested while a window runs
+    float x[DQ], xn[DQ], ad[DQ];
+    for (; lvl < nlev; ++lvl) {
+      set_level(lvl);
+      if (m < C) load_row_g<T, DQ>(kb + (int64_t)perm(g * S + gl) * kst, xn);
+      for (int win = 0; win < nwin; ++win) {
+#pragma unroll
+        for (int d = 0; d < DQ; ++d) x[d] = xn[d];
+        if (win + 1 < nwin) load_row_g<T, DQ>(kb + (int64_t)perm((win + 1) * Wz + g * S + gl) * kst, xn);
+        if (L * Q <= kWave) window(std::true_type{}, std::true_type{}, win, x, ad, ad);
+        else window(std::true_type{}, std::false_type{}, win, x, ad, ad);
+      }
+      __syncthreads();
     }
   }
   // leaf slots, then the node sums and counts by adjacent pairs from the slots up
   for (int c = tid; c < C; c += NT) tr.slot[c] = val(c) ? perm(c) : -1;
   const int nleaf = C / 2;
   for (int i = m; i < nleaf; i += kLaneSlots) {
-    float y[DQ];
+    float x[DQ], y[DQ];
     load_row_g<T, DQ>(kb + (int64_t)perm(2 * i) * kst, x);
     load_row_g<T, DQ>(kb + (int64_t)perm(2 * i + 1) * kst, y);
     const float v0 = val(2 * i) ? 1.0f : 0.0f, v1 = val(2 * i + 1) ? 1.0f : 0.0f;
