@@ -174,7 +174,85 @@ def test_config3_selection_and_attention():
     _free()
 
 
+def test_config3_selection_more_slices():
+    """Config 3's selection on eight more (b, h) slices (four heads of two more sequences, every one of the 16,384
+    queries of each): the descent kernel equals the canonical oracle bit for bit, and the kept-key counts of the
+    attention's candidate lists equal the oracle's."""
+    H, T, D = 4, 16384, 128
+    cfg = Config(n_head=H, n_embd=H * D, seq_len=T, attn='seg', wmax=32, beam=32, beam_mode='fixed',
+                 neighbors=False, leaf=64, arity=2, local=3)
+    shape = K.TreeShape(T, 64, 2)
+    geom = S.Geometry(T, 64, 2)
+    t_all = torch.arange(T)
+    for seed in (5, 7):
+        qc, kc, vc = config3_slice(H, T, D, seed)
+        q, k, v = qc.to(DEV), kc.to(DEV), vc.to(DEV)
+        levels = K.level_sums(k, shape.blevels)
+        tq = torch.arange(T, dtype=torch.int32, device=DEV)
+        ids, vld, _ = K.tree_descend(q, levels, tq, shape, cfg.wmax)
+        n_tree = torch.full((1, H, T), 32, dtype=torch.int32, device=DEV)
+        _, _, keys = K.seg_attn(q, k, v, tq, ids, vld, n_tree, 64, cfg.local, 1.0 / math.sqrt(D),
+                                keys=torch.empty(1, H, T, device=DEV))
+        gi, gv, keys = ids.long().cpu(), vld.bool().cpu(), keys.cpu()
+        ci, cv, _ = S.tree_pass_general(qc.float(), S.pyramid(S.index_keys(kc), geom), t_all, geom, cfg.wmax,
+                                        'canonical')
+        print('config 3 sequence seed %d: %d heads x %d queries, kept leaves %d' % (seed, H, T, int(cv.sum())),
+              flush=True)
+        assert torch.equal(gv, cv)
+        assert torch.equal(torch.where(gv, gi, -1), torch.where(cv, ci, -1))
+        lhat = torch.full((1, H, T), 32, dtype=torch.long)
+        nid = torch.zeros(1, H, T, cfg.nb_window * cfg.nb_store, dtype=torch.long)
+        sel = S.finish(ci, cv, nid, torch.zeros_like(nid, dtype=torch.bool), torch.zeros(1, H, T, dtype=torch.long),
+                       lhat, cfg, 64)
+        _, keep, _ = A.assemble(sel, t_all, cfg, 1, H)
+        assert torch.equal(keys, keep.sum(-1).float())
+        del levels, ids, vld, q, k, v
+    _free()
+
+
 # ------------------------------------------------------------------------------------------------ configs 4, 5
+def test_config4_full_batch_selection():
+    """Config 4 at its full batch: 32 sequences x 12 heads, a 32,768-token prompt prefilled into the paged cache,
+    then the decode step's layer attention kernel (seg_attend_kernel: cache append, descent and attention in one
+    launch) at position 32,768 in layers 0 and 11: every (sequence, head)'s kept leaves equal the canonical
+    oracle descent over that sequence's own cache, bit for bit, and every output row is finite."""
+    n_layer, H, C, V = 12, 12, 768, 50304
+    B, T0, Tcap, dh, topk = 32, 32768, 65536, 64, 32
+    cfg = Config(vocab_size=V, seq_len=Tcap, n_layer=n_layer, n_head=H, n_embd=C, attn='seg', wmax=topk,
+                 beam=topk, beam_mode='fixed', neighbors=False, leaf=64, arity=2, local=3)
+    torch.manual_seed(3)
+    model = GPT(cfg)
+    W = weights_from_ours({k: v.detach().to(torch.bfloat16).to(DEV) for k, v in model.state_dict().items()}, cfg)
+    del model
+    idx = torch.randint(0, V, (B, T0), generator=torch.Generator().manual_seed(3))
+    dec = Decoder(W, n_layer, H, C, Tcap, 'seg', cfg, DEV, batch=B, dtype=torch.bfloat16)
+    dec.prefill(idx.to(DEV), chunk=8)
+    sc = dec.groups[0]['scratch']
+    geom = S.Geometry(Tcap, 64, 2)
+    tpos = torch.full((B,), T0, dtype=torch.int32, device=DEV)
+    g = torch.Generator().manual_seed(9)
+    for i in (0, n_layer - 1):
+        q, k_, v_ = (torch.randn(B, H, 1, dh, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3))
+        sc.keys = sc.keys_all[i]
+        out, _ = E.seg_attend_(dec.states[i], None, q, k_, v_, tpos, scratch=sc)
+        ids, vld = sc.ids.long().cpu(), sc.vld.bool().cpu()
+        assert bool(torch.isfinite(out.float()).all())
+        kept = 0
+        for b in range(B):
+            kb, _ = dec.states[i].dense_kv(b)
+            kc = kb.float().cpu()
+            del kb
+            ci, cv, _ = S.tree_pass_general(q[b:b + 1].float().cpu(), S.pyramid(S.index_keys(kc), geom),
+                                            torch.tensor([T0]), geom, topk, 'canonical')
+            assert torch.equal(vld[b:b + 1], cv), (i, b)
+            assert torch.equal(torch.where(cv, ids[b:b + 1], -1), torch.where(cv, ci, -1)), (i, b)
+            kept += int(cv.sum())
+        print('config 4 layer %d: %d sequences x %d heads, %d kept leaves, all equal to the oracle' % (i, B, H, kept),
+              flush=True)
+    del dec
+    _free()
+
+
 def _decode_parity(leaf, arity, topk, B, T0, Tcap, steps, ids_seed, sort_dedupe):
     n_layer, H, C, V = 12, 12, 768, 50304
     dh = C // H
