@@ -598,8 +598,8 @@ int ta_mfma_peak(int wgs, int iters, float* out, void* stream);
 
 /*
  * Block forest (the reference's attn='block' attention), step 1 -- replaces forest.py:47-75 build_forest with
- * forest.py:12-33 two_means_order and forest.py:36-44 soft_gate.  Keys k (B, H, T, D) (row 0, the sink, counted
- * as zero), cut into blocks of `block` keys (a power of two in [4, 64] dividing T; depth = log2(block / 2)):
+ * forest.py:12-33 two_means_order and forest.py:36-44 soft_gate.  Keys k (B, H, T, D), D 16, 32, 64 or 128 (row 0,
+ * the sink, counted as zero), cut into blocks of `block` keys (a power of two in [4, 64] dividing T; depth = log2(block / 2)):
  * every block's keys are ordered by depth rounds of 2-means splits of its groups (kmeans_iters iterations each),
  * perm (B, H, T) int32 gets rank -> position inside the block, and sums[l] (B, H, (T / block) << l, D) float32
  * (l = 0..depth; strides sb[l], sh[l], node rows contiguous) the node sums of every level (level 0 = the block,

@@ -35,10 +35,13 @@ def rnd(*shape, seed):
 
 @pytest.mark.parametrize('D,block,T,dtype,gate', [(16, 32, 256, torch.float32, False), (64, 64, 512, torch.float32, False),
                                                   (32, 8, 128, torch.bfloat16, False), (16, 32, 256, torch.float32, True),
-                                                  (64, 16, 256, torch.bfloat16, True), (16, 4, 64, torch.float32, False)])
+                                                  (64, 16, 256, torch.bfloat16, True), (16, 4, 64, torch.float32, False),
+                                                  (128, 64, 512, torch.float32, False), (128, 64, 1024, torch.bfloat16, True),
+                                                  (128, 8, 128, torch.float32, True), (128, 32, 256, torch.float16, False),
+                                                  (128, 4, 64, torch.bfloat16, True)])
 def test_forest_build_is_bit_exact(D, block, T, dtype, gate):
     """ta_forest_build: the permutation and every level's node sums (soft-gated where on) equal the oracle's
-    canonical build_forest bit for bit."""
+    canonical build_forest bit for bit (head size 128 on the kernel that holds a key 16 dimensions per lane)."""
     print('case', D, block, T, dtype, gate, flush=True)
     k = rnd(2, 3, T, D, seed=D + T).to(dtype)
     k_idx = k.float().clone()
@@ -52,14 +55,17 @@ def test_forest_build_is_bit_exact(D, block, T, dtype, gate):
 
 
 @pytest.mark.parametrize('kw', [dict(), dict(wmax=8, beam=8), dict(tree_block=8, wmax=6, beam=3),
-                                dict(beam_mode='pred', wmax=4), dict(gate=True)])
+                                dict(beam_mode='pred', wmax=4), dict(gate=True), dict(D=128, wmax=8, beam=8),
+                                dict(D=128, gate=True, tree_block=16)])
 def test_forest_descend_is_bit_exact(kw):
     """ta_forest_descend: the leaves, their validity, every level's candidates and the candidate list equal the
-    oracle's canonical descent and forest_candidates."""
+    oracle's canonical descent and forest_candidates (head sizes 16 and 128)."""
     print('case', kw, flush=True)
+    kw = dict(kw)
+    D = kw.pop('D', 16)
     cfg = tiny(seq_len=256, **kw)
     B = cfg.tree_block
-    q, k = rnd(2, 2, 256, 16, seed=5), rnd(2, 2, 256, 16, seed=6)
+    q, k = rnd(2, 2, 256, D, seed=5), rnd(2, 2, 256, D, seed=6)
     k_idx = k.clone()
     k_idx[:, :, 0] = 0
     depth = K.forest_depth(B)
@@ -87,7 +93,7 @@ def test_forest_descend_is_bit_exact(kw):
 
 
 CFGS = [dict(), dict(gate=True), dict(beam_mode='pred', global_pool=True), dict(beam_mode='pred', global_pool=True,
-        gate=True), dict(tree_block=16, wmax=6, beam=3)]
+        gate=True), dict(tree_block=16, wmax=6, beam=3), dict(n_embd=256, beam_mode='pred', global_pool=True, gate=True)]
 
 
 @pytest.mark.parametrize('kw', CFGS)
@@ -102,7 +108,8 @@ def test_sparse_attend_matches_oracle(kw):
     if cfg.beam_mode == 'pred':
         sd = mod.state_dict()
         pw = dict(w1=sd['pred.0.weight'], b1=sd['pred.0.bias'], w2=sd['pred.2.weight'], b2=sd['pred.2.bias'])
-    q, k, v = (rnd(2, 2, 256, 16, seed=s) for s in (11, 12, 13))
+    dh = cfg.n_embd // cfg.n_head
+    q, k, v = (rnd(2, 2, 256, dh, seed=s) for s in (11, 12, 13))
     want, aux, wcand, _ = FR.tree_sparse_attend(q, k, v, cfg, pw=pw, mode='canonical')
     mod = mod.to(DEV)
     with torch.no_grad():

@@ -170,6 +170,228 @@ __global__ __launch_bounds__(kWave) void forest_build_kernel(const T* __restrict
   }
 }
 
+// The same build for a head size of 128 (forest_build_kernel holds five D-vectors per lane): a workgroup of
+// Q = D / 16 wavefronts per block, key i held 16 dimensions per lane by lanes [Q i, Q i + Q).  The member sums
+// are the same halving trees (member i + member i + S/2 first, ...) and the node sums the same adjacent pairs:
+// a step whose partner lies in another wavefront goes through LDS, the others are xor exchanges; dot products
+// are canon_dot's value finished across the Q lanes of a key.  The results equal the one-wavefront kernel's
+// arithmetic, so the canonical oracle's, bit for bit.
+template <int Q>
+__device__ __forceinline__ void fw_step(float (&v)[16], int lh, float* xb, int tid) {
+  if (lh >= kWave) {   // the partner in another wavefront: every lane's 16 values through LDS
+    __syncthreads();
+#pragma unroll
+    for (int d = 0; d < 16; d += 4)
+      *reinterpret_cast<float4*>(xb + tid * 16 + d) = make_float4(v[d], v[d + 1], v[d + 2], v[d + 3]);
+    __syncthreads();
+    const float* o = xb + (tid ^ lh) * 16;
+#pragma unroll
+    for (int d = 0; d < 16; d += 4) {
+      const float4 u = *reinterpret_cast<const float4*>(o + d);
+      v[d] = v[d] + u.x;
+      v[d + 1] = v[d + 1] + u.y;
+      v[d + 2] = v[d + 2] + u.z;
+      v[d + 3] = v[d + 3] + u.w;
+    }
+    return;
+  }
+  switch (lh) {
+    case 32: seg_sum_rows_step<32>(v); break;
+    case 16: seg_sum_rows_step<16>(v); break;
+    case 8: seg_sum_rows_step<8>(v); break;
+    case 4: seg_sum_rows_step<4>(v); break;
+    case 2: seg_sum_rows_step<2>(v); break;
+    default: seg_sum_rows_step<1>(v); break;
+  }
+}
+// A scalar of every member summed over the group by the same halving tree (the counts: integers, any order).
+template <int Q>
+__device__ __forceinline__ float fw_sum(float v, int S, float* xs, int tid) {
+  for (int h = S / 2; h >= 1; h >>= 1) {
+    const int lh = h * Q;
+    if (lh >= kWave) {
+      __syncthreads();
+      xs[tid] = v;
+      __syncthreads();
+      v = v + xs[tid ^ lh];
+    } else {
+      v = v + __shfl_xor(v, lh, kWave);
+    }
+  }
+  return v;
+}
+// The first member (smallest index) of the group whose value is the group's largest.
+template <int Q>
+__device__ __forceinline__ int fw_argmax_first(float v, int m, int S, float* xs, int* xi, int tid) {
+  int i = m;
+  for (int h = S / 2; h >= 1; h >>= 1) {
+    const int lh = h * Q;
+    float ov;
+    int oi;
+    if (lh >= kWave) {
+      __syncthreads();
+      xs[tid] = v;
+      xi[tid] = i;
+      __syncthreads();
+      ov = xs[tid ^ lh];
+      oi = xi[tid ^ lh];
+    } else {
+      ov = __shfl_xor(v, lh, kWave);
+      oi = __shfl_xor(i, lh, kWave);
+    }
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  return i;
+}
+// canon_dot's value for two D-vectors held 16 dimensions per lane by the Q lanes of a key (lane q: dimensions
+// [16 q, 16 q + 16)): each lane reduces its 16 / Q whole groups of D / 16, then the halving tree over the 16
+// groups crosses lanes where a step pairs groups held by different lanes.
+template <int D, int Q, typename FA, typename FB>
+__device__ __forceinline__ float fw_dot(FA fa, FB fb) {
+  constexpr int R = D / 16, GQ = 16 / Q;
+  float g[GQ];
+#pragma unroll
+  for (int j = 0; j < GQ; ++j) {
+    float p[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) p[i] = fa(R * j + i) * fb(R * j + i);
+#pragma unroll
+    for (int n = R / 2; n >= 1; n /= 2)
+#pragma unroll
+      for (int i = 0; i < n; ++i) p[i] = p[i] + p[i + n];
+    g[j] = p[0];
+  }
+#pragma unroll
+  for (int n = 8; n >= 1; n /= 2) {
+    if (n >= GQ) {
+#pragma unroll
+      for (int i = 0; i < GQ; ++i) g[i] = g[i] + __shfl_xor(g[i], n / GQ, kWave);
+    } else {
+#pragma unroll
+      for (int i = 0; i < n; ++i) g[i] = g[i] + g[i + n];
+    }
+  }
+  return g[0];
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kWave * (D / 16)) void forest_build_wide_kernel(const T* __restrict__ k, int64_t ksb,
+                                                                            int64_t ksh, int64_t kst, int H, int nb,
+                                                                            int Bk, int depth, int iters, int gate,
+                                                                            int32_t* __restrict__ perm,
+                                                                            ForestLevels lv) {
+  constexpr int Q = D / 16, DQ = 16, NT = kWave * Q, RS = D + 4;
+  __shared__ __align__(16) float s_x[kWave * RS];   // the members' rows (the reorder buffer too)
+  __shared__ __align__(16) float s_xb[NT * DQ];     // cross-wavefront exchange of 16 values per lane
+  __shared__ float s_xs[NT];
+  __shared__ int s_xi[NT];
+  __shared__ int s_p[kWave];
+  __shared__ __align__(16) float s_pr[kWave];       // the level's projections
+  const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ;
+  const int pb = blockIdx.x, blk = pb % nb, bh = pb / nb, b = bh / H, h = bh % H;
+  const bool live = m < Bk;
+  const int64_t pos = (int64_t)blk * Bk + (live ? m : 0);
+  float x[DQ];
+  load_row_g<T, DQ>(k + b * ksb + h * ksh + pos * kst + d0, x);
+#pragma unroll
+  for (int d = 0; d < DQ; ++d) x[d] = live ? (pos == 0 ? x[d] * 0.0f : x[d]) : 0.0f;   // the sink: k * 0
+  int p = m;
+  float c0[DQ], c1[DQ], t[DQ];
+  auto bfly = [&](float (&v)[DQ], int S) {
+    for (int hh = S / 2; hh >= 1; hh >>= 1) fw_step<Q>(v, hh * Q, s_xb, tid);
+  };
+  for (int lvl = 0; lvl < depth; ++lvl) {
+    const int S = Bk >> lvl, gb = m & ~(S - 1), li = m - gb;
+    // the members' rows in LDS, for the two farthest members' rows
+#pragma unroll
+    for (int d = 0; d < DQ; d += 4)
+      *reinterpret_cast<float4*>(s_x + m * RS + d0 + d) = make_float4(x[d], x[d + 1], x[d + 2], x[d + 3]);
+    // the group mean, then the member farthest from it (a) and the member farthest from a (b)
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) c0[d] = x[d];
+    bfly(c0, S);
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) c0[d] = c0[d] / (float)S;
+    const float d2 = fw_dot<D, Q>([&](int i) { return x[i] - c0[i]; }, [&](int i) { return x[i] - c0[i]; });
+    const int la = fw_argmax_first<Q>(d2, m, S, s_xs, s_xi, tid);
+    __syncthreads();   // the rows in s_x
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) c0[d] = s_x[la * RS + d0 + d];
+    const float d2b = fw_dot<D, Q>([&](int i) { return x[i] - c0[i]; }, [&](int i) { return x[i] - c0[i]; });
+    const int lb = fw_argmax_first<Q>(d2b, m, S, s_xs, s_xi, tid);
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) c1[d] = s_x[lb * RS + d0 + d];
+    const float xx = fw_dot<D, Q>([&](int i) { return x[i]; }, [&](int i) { return x[i]; });
+    for (int it = 0; it < iters; ++it) {
+      const float cc0 = fw_dot<D, Q>([&](int i) { return c0[i]; }, [&](int i) { return c0[i]; });
+      const float cc1 = fw_dot<D, Q>([&](int i) { return c1[i]; }, [&](int i) { return c1[i]; });
+      const float xc0 = fw_dot<D, Q>([&](int i) { return x[i]; }, [&](int i) { return c0[i]; });
+      const float xc1 = fw_dot<D, Q>([&](int i) { return x[i]; }, [&](int i) { return c1[i]; });
+      const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
+      const bool lab1 = dist1 < dist0;   // argmin over the two centroids, the first on ties
+      const float m0 = lab1 ? 0.0f : 1.0f, m1 = lab1 ? 1.0f : 0.0f;
+      const float cnt0 = fw_sum<Q>(m0, S, s_xs, tid), cnt1 = fw_sum<Q>(m1, S, s_xs, tid);
+      const float den0 = fmaxf(cnt0, 1.0f), den1 = fmaxf(cnt1, 1.0f);
+#pragma unroll
+      for (int d = 0; d < DQ; ++d) t[d] = x[d] * m0;
+      bfly(t, S);
+#pragma unroll
+      for (int d = 0; d < DQ; ++d) c0[d] = cnt0 > 0.0f ? t[d] / den0 : c0[d];
+#pragma unroll
+      for (int d = 0; d < DQ; ++d) t[d] = x[d] * m1;
+      bfly(t, S);
+#pragma unroll
+      for (int d = 0; d < DQ; ++d) c1[d] = cnt1 > 0.0f ? t[d] / den1 : c1[d];
+    }
+    const float proj = fw_dot<D, Q>([&](int i) { return x[i]; }, [&](int i) { return c0[i] - c1[i]; });
+    // stable ascending rank of the projection inside the group, then the member moves to that rank
+    __syncthreads();   // every read of s_x above is done
+    if (q == 0) s_pr[m] = proj;
+    __syncthreads();
+    int rank = 0;
+    for (int j = 0; j < S; ++j) {
+      const float pj = s_pr[gb + j];
+      rank += (pj < proj || (pj == proj && j < li)) ? 1 : 0;
+    }
+    const int slot = gb + rank;
+#pragma unroll
+    for (int d = 0; d < DQ; d += 4)
+      *reinterpret_cast<float4*>(s_x + slot * RS + d0 + d) = make_float4(x[d], x[d + 1], x[d + 2], x[d + 3]);
+    if (q == 0) s_p[slot] = p;
+    __syncthreads();
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) x[d] = s_x[m * RS + d0 + d];
+    p = s_p[m];
+    __syncthreads();
+  }
+  if (live && q == 0) perm[(int64_t)bh * nb * Bk + (int64_t)blk * Bk + m] = p;
+
+  // node sums by adjacent pairs: level depth holds pairs of ranks, level 0 the whole block
+  auto pyramid = [&](float (&y)[DQ], float* const* out) {
+    for (int l = depth; l >= 0; --l) {
+      const int sz = Bk >> l;   // keys per node at level l
+      fw_step<Q>(y, (sz >> 1) * Q, s_xb, tid);
+      if (live && (m & (sz - 1)) == 0) {
+        float* row = out[l] + b * lv.sb[l] + h * lv.sh[l] + ((int64_t)blk * (Bk / sz) + m / sz) * D + d0;
+#pragma unroll
+        for (int d = 0; d < DQ; d += 4) *reinterpret_cast<float4*>(row + d) = make_float4(y[d], y[d + 1], y[d + 2], y[d + 3]);
+      }
+    }
+  };
+  float y[DQ];
+#pragma unroll
+  for (int d = 0; d < DQ; ++d) y[d] = x[d];
+  pyramid(y, lv.sums);
+  if (gate) {
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) y[d] = forest_log(x[d]);
+    pyramid(y, lv.lg);
+  }
+}
+
 // The soft gate of every node (forest.py:36-44), one wavefront per node, lane = dimension: mean log-magnitude
 // ml = lg / keys, thr = the gate_q quantile of ml over the dimensions, g = logistic((ml - thr) / temp), the node
 // sum becomes (sum * g) * (D / max(sum of g, 1)).  In place.
@@ -209,6 +431,72 @@ __global__ __launch_bounds__(256) void forest_gate_kernel(ForestLevels lv, int H
   const float kept = fmaxf(seg_sum(g, D), 1.0f);
   const float scale = (float)D / kept;
   if (in) row[lane] = (raw * g) * scale;
+}
+
+// forest_gate_kernel for a head size above 64: lane i holds dimensions i + 64 e (e < D / 64).  The rank of a
+// mean log-magnitude among the D is the same stable count, the quantile the same interpolation, and the kept mass
+// the same halving tree over dimensions (dimension d + dimension d + D/2 first: the lane's own values when
+// D = 128, then the butterfly over the 64 lanes).
+template <int D>
+__global__ __launch_bounds__(256) void forest_gate_wide_kernel(ForestLevels lv, int H, int nb, int Bk, int depth,
+                                                               int lo, float w, float temp) {
+  static_assert(D == 128, "two dimensions per lane");
+  constexpr int DL = D / kWave;
+  const int lane = lane_id();
+  const int64_t idx = (int64_t)blockIdx.x * 4 + wave_id();
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  int l = 0;
+  int64_t n = idx, cnt = nb;
+  while (l <= depth && n >= cnt) {
+    n -= cnt;
+    cnt <<= 1;
+    ++l;
+  }
+  if (l > depth) return;
+  float* row = lv.sums[l] + b * lv.sb[l] + h * lv.sh[l] + n * D;
+  const float* lrow = lv.lg[l] + b * lv.sb[l] + h * lv.sh[l] + n * D;
+  float raw[DL], ml[DL];
+#pragma unroll
+  for (int e = 0; e < DL; ++e) {
+    raw[e] = row[lane + kWave * e];
+    ml[e] = lrow[lane + kWave * e] / (float)(Bk >> l);
+  }
+  int rank[DL];
+#pragma unroll
+  for (int e = 0; e < DL; ++e) rank[e] = 0;
+#pragma unroll
+  for (int e2 = 0; e2 < DL; ++e2) {
+    for (int src = 0; src < kWave; ++src) {
+      const float o = __shfl(ml[e2], src, kWave);
+      const int d2 = src + kWave * e2;
+#pragma unroll
+      for (int e = 0; e < DL; ++e) {
+        const int d = lane + kWave * e;
+        rank[e] += (o < ml[e] || (o == ml[e] && d2 < d)) ? 1 : 0;
+      }
+    }
+  }
+  const int hi = w > 0.0f ? lo + 1 : lo;
+  // the values at ranks lo and hi (each rank held by exactly one dimension)
+  float vlo = 0.0f, vhi = 0.0f;
+#pragma unroll
+  for (int e = 0; e < DL; ++e) {
+    const uint64_t blo = __ballot(rank[e] == lo), bhi = __ballot(rank[e] == hi);
+    if (blo) vlo = __shfl(ml[e], __ffsll((unsigned long long)blo) - 1, kWave);
+    if (bhi) vhi = __shfl(ml[e], __ffsll((unsigned long long)bhi) - 1, kWave);
+  }
+  const float dd = vhi - vlo;
+  const float thr = w < 0.5f ? vlo + w * dd : vhi - dd * (1.0f - w);
+  float g[DL];
+#pragma unroll
+  for (int e = 0; e < DL; ++e) {
+    const float z = (ml[e] - thr) / temp;
+    g[e] = (float)(1.0 / (1.0 + exp(-(double)z)));
+  }
+  const float kept = fmaxf(seg_sum(g[0] + g[1], kWave), 1.0f);
+  const float scale = (float)D / kept;
+#pragma unroll
+  for (int e = 0; e < DL; ++e) row[lane + kWave * e] = (raw[e] * g[e]) * scale;
 }
 
 struct ForestDesc {
@@ -342,7 +630,7 @@ __global__ __launch_bounds__(256) void forest_descend_kernel(ForestDesc p) {
 using namespace ta;
 
 namespace {
-bool forest_dim_ok(int D) { return D == 16 || D == 32 || D == 64; }
+bool forest_dim_ok(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 }  // namespace
 
 extern "C" int ta_forest_build(const void* k, int dtype, int64_t ksb, int64_t ksh, int64_t kst, int B, int H, int T,
@@ -352,7 +640,7 @@ extern "C" int ta_forest_build(const void* k, int dtype, int64_t ksb, int64_t ks
   if (B <= 0 || H <= 0 || T <= 0 || block < 4 || block > kWave || (block & (block - 1)) || T % block ||
       !forest_dim_ok(D) || kmeans_iters < 0 || perm == nullptr || sums == nullptr || sb == nullptr ||
       sh == nullptr || (gate && (lg == nullptr || !(gate_q >= 0.0f && gate_q <= 1.0f) || !(gate_temp > 0.0f)))) {
-    set_error("ta_forest_build: bad arguments (block a power of two in [4, 64] dividing T; D 16, 32 or 64)");
+    set_error("ta_forest_build: bad arguments (block a power of two in [4, 64] dividing T; D 16, 32, 64 or 128)");
     return TA_ERR_ARG;
   }
   const int es = dtype == TA_F32 ? 4 : 2;
@@ -379,11 +667,15 @@ extern "C" int ta_forest_build(const void* k, int dtype, int64_t ksb, int64_t ks
 #define TA_FB(TT, DD)                                                                                           \
   hipLaunchKernelGGL((forest_build_kernel<TT, DD>), grid, dim3(kWave), 0, st, (const TT*)k, ksb, ksh, kst, H, \
                      nb, block, depth, kmeans_iters, gate, perm, lv)
-#define TA_FB_D(TT)                  \
-  switch (D) {                       \
-    case 16: TA_FB(TT, 16); break;   \
-    case 32: TA_FB(TT, 32); break;   \
-    default: TA_FB(TT, 64); break;   \
+#define TA_FB_D(TT)                                                                                          \
+  switch (D) {                                                                                               \
+    case 16: TA_FB(TT, 16); break;                                                                           \
+    case 32: TA_FB(TT, 32); break;                                                                           \
+    case 64: TA_FB(TT, 64); break;                                                                           \
+    default:                                                                                                 \
+      hipLaunchKernelGGL((forest_build_wide_kernel<TT, 128>), grid, dim3(8 * kWave), 0, st, (const TT*)k, ksb, \
+                         ksh, kst, H, nb, block, depth, kmeans_iters, gate, perm, lv);                       \
+      break;                                                                                                 \
   }
   switch (dtype) {
     case TA_F32: TA_FB_D(float); break;
@@ -403,7 +695,8 @@ extern "C" int ta_forest_build(const void* k, int dtype, int64_t ksb, int64_t ks
   switch (D) {
     case 16: hipLaunchKernelGGL((forest_gate_kernel<16>), ggrid, dim3(256), 0, st, lv, H, nb, block, depth, lo, w, gate_temp); break;
     case 32: hipLaunchKernelGGL((forest_gate_kernel<32>), ggrid, dim3(256), 0, st, lv, H, nb, block, depth, lo, w, gate_temp); break;
-    default: hipLaunchKernelGGL((forest_gate_kernel<64>), ggrid, dim3(256), 0, st, lv, H, nb, block, depth, lo, w, gate_temp); break;
+    case 64: hipLaunchKernelGGL((forest_gate_kernel<64>), ggrid, dim3(256), 0, st, lv, H, nb, block, depth, lo, w, gate_temp); break;
+    default: hipLaunchKernelGGL((forest_gate_wide_kernel<128>), ggrid, dim3(256), 0, st, lv, H, nb, block, depth, lo, w, gate_temp); break;
   }
   return check_launch("forest_gate_kernel");
 }
@@ -418,7 +711,7 @@ extern "C" int ta_forest_descend(const void* q, int dtype, int64_t qsb, int64_t 
       sums == nullptr || perm == nullptr || leaf == nullptr || leafv == nullptr || cand == nullptr ||
       (lv_cur != nullptr && lv_cv == nullptr)) {
     set_error("ta_forest_descend: bad arguments (block a power of two in [4, 64] dividing T, at most 1024 blocks; "
-              "D 16, 32 or 64; 1 <= wmax <= 64)");
+              "D 16, 32, 64 or 128; 1 <= wmax <= 64)");
     return TA_ERR_ARG;
   }
   const int R = D / 16, es = dtype == TA_F32 ? 4 : 2;
@@ -463,7 +756,8 @@ extern "C" int ta_forest_descend(const void* q, int dtype, int64_t qsb, int64_t 
   switch (D) {                       \
     case 16: TA_FD(TT, 16); break;   \
     case 32: TA_FD(TT, 32); break;   \
-    default: TA_FD(TT, 64); break;   \
+    case 64: TA_FD(TT, 64); break;   \
+    default: TA_FD(TT, 128); break;  \
   }
   switch (dtype) {
     case TA_F32: TA_FD_D(float); break;
