@@ -56,3 +56,15 @@ def test_product_refuses_cpu_tensors():
     q = torch.zeros(1, 1, 4, 64)
     with pytest.raises(RuntimeError, match='GPU'):
         kernels.gather_dot(q, q, torch.zeros(1, 1, 4, 2, dtype=torch.long), 1.0)
+
+
+def test_backward_route_choice():
+    """The default dk/dv route: the fixed-order (bit-reproducible) scan while its candidate-row reads stay within
+    DKDV_SCAN_LIMIT, the atomic adds beyond (the scan is quadratic in T).  Causal scans skip the queries before a
+    key block: sum over blocks of (T - block start) rows."""
+    from treeattn_amd import kernels as K
+    # T = 512, D = 64 (blocks of 64 keys), KC = 100: 8 blocks x 512 rows, or 512 + 448 + ... + 64 causally
+    assert K.dkdv_scan_ints(1, 1, 512, 512, 100, 64, False) == 8 * 512 * 100
+    assert K.dkdv_scan_ints(1, 1, 512, 512, 100, 64, True) == sum(512 - 64 * j for j in range(8)) * 100
+    assert K.dkdv_scan_ints(2, 6, 512, 512, 100, 64, True) <= K.DKDV_SCAN_LIMIT          # the reference's size
+    assert K.dkdv_scan_ints(1, 16, 16384, 16384, 2100, 128, True) > K.DKDV_SCAN_LIMIT    # config 3's shape

@@ -7,7 +7,8 @@
 // the two dot products of its key and value rows with q and do (held in LDS and read by every lane at the same
 // address), p and ds, left in LDS.  Phase B, one lane per dimension: dq accumulates the chunk's slots in slot
 // order (so dq is deterministic).  dk and dv then take one of two routes:
-//  * with a workspace (the default of the Python binding): every slot's ds and p are written there, and
+//  * with a workspace (the Python binding's default while this route's scan, quadratic in T, stays bounded):
+//    every slot's ds and p are written there, and
 //    sparse_attn_dkdv_kernel -- one workgroup per block of keys of a (sequence, head) -- scans the queries in
 //    increasing order and their slots in slot order, adding each hit on its keys into LDS accumulators, then
 //    writes the keys' rows once.  The order of the additions is fixed: dk and dv are bit-reproducible.

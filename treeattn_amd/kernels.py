@@ -569,11 +569,27 @@ def sparse_attn_fwd(q, k, v, cand, scale):
     return out, lse
 
 
-def sparse_attn_bwd(q, k, v, cand, scale, out, lse, dout, deterministic=True, causal=False):
+# The deterministic dk/dv route reads, for every block of 4096 / D keys, the candidate row of every query at or
+# after the block (causal) or of every query: (T / block) * T * KC int32 per (sequence, head), quadratic in T.
+# Above this many int32 reads in all (8 GiB, about 1.7 ms of HBM time) the default is the atomic route.
+DKDV_SCAN_LIMIT = 2 ** 31
+
+
+def dkdv_scan_ints(B, H, T, Tk, KC, D, causal):
+    """int32 reads of the deterministic dk/dv route's scan: per key block, the candidate rows it scans."""
+    KB = max(1, 4096 // max(D, 1))
+    nblk = (Tk + KB - 1) // KB
+    rows = sum(T - min(j * KB, T) for j in range(nblk)) if causal else nblk * T
+    return B * H * rows * KC
+
+
+def sparse_attn_bwd(q, k, v, cand, scale, out, lse, dout, deterministic=None, causal=False):
     """Gradients of sparse_attn_fwd: (dq in q's dtype, dk, dv in k's / v's dtype).  dk and dv are summed in
     float32: deterministic, in a fixed order (queries, then slots, ascending) through a per-slot workspace; else
-    with atomic adds whose order depends on scheduling, as in the reference's kernel.  causal: every candidate
-    position is at most its query's position (lets the deterministic route skip earlier queries)."""
+    with atomic adds whose order depends on scheduling, as in the reference's kernel.  deterministic=None (the
+    default) takes the fixed order while its scan (dkdv_scan_ints) stays within DKDV_SCAN_LIMIT, the atomic adds
+    above it (long training contexts: the scan grows as T^2).  causal: every candidate position is at most its
+    query's position (lets the deterministic route skip earlier queries)."""
     L.require_gpu(q, k, v, cand, out, lse, dout)
     if not (q.dtype == k.dtype == v.dtype == out.dtype):
         raise TypeError('q, k, v and out must share a dtype')
@@ -585,6 +601,8 @@ def sparse_attn_bwd(q, k, v, cand, scale, out, lse, dout, deterministic=True, ca
     ls = lse.float().contiguous()
     dq = torch.empty_like(q)
     ws = None
+    if deterministic is None:
+        deterministic = dkdv_scan_ints(b, H, T, Tk, KC, D, causal and T == Tk) <= DKDV_SCAN_LIMIT
     if deterministic and T > 0 and KC > 0:
         nbytes = L.lib().ta_sparse_attn_bwd_workspace_size(b, H, T, KC)
         ws = torch.empty(max(1, nbytes // 4), device=q.device, dtype=torch.float32)
