@@ -68,3 +68,13 @@ def test_backward_route_choice():
     assert K.dkdv_scan_ints(1, 1, 512, 512, 100, 64, True) == sum(512 - 64 * j for j in range(8)) * 100
     assert K.dkdv_scan_ints(2, 6, 512, 512, 100, 64, True) <= K.DKDV_SCAN_LIMIT          # the reference's size
     assert K.dkdv_scan_ints(1, 16, 16384, 16384, 2100, 128, True) > K.DKDV_SCAN_LIMIT    # config 3's shape
+
+
+def test_tracing_builds_are_separate():
+    """The phase marks are nothing in the library build: it exports no trace buffer accessor, and a tracing build
+    of one source lives in its own library beside it."""
+    from treeattn_amd import _lib, build, phase_trace  # noqa: F401
+    L = _lib.lib()
+    assert not hasattr(L, 'ta_trace_read')
+    assert build.trace_lib_path('attend.hip') != _lib.LIB_PATH
+    assert build.trace_lib_path('attend.hip').endswith('libtreeattn_trace_attend.so')

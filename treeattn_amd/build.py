@@ -1,6 +1,7 @@
 """Build libtreeattn.so (gfx950) in-tree with hipcc.
 
     python -m treeattn_amd.build            # compile every source, link the library
+    python -m treeattn_amd.build --trace attend.hip   # a tracing build of one source (treeattn_amd.phase_trace)
 
 Every HIP source is compiled for gfx950 only, with packed-fp32 instruction generation disabled.  The
 selection kernels (select.hip) are compiled with floating-point contraction off so their scores follow
@@ -66,6 +67,42 @@ def build(verbose=True):
     return LIB
 
 
+def trace_lib_path(name):
+    """Path of the tracing build of source `name` (see build_trace)."""
+    return os.path.join(HERE, 'libtreeattn_trace_%s.so' % name.replace('.hip', ''))
+
+
+def build_trace(name, verbose=True):
+    """A tracing build: source `name` (one of SOURCES) compiled with -DTA_TRACE, so that its phase marks store
+    time stamps (csrc/trace.hpp), and linked with the library's other objects (from a previous build()) into
+    libtreeattn_trace_<name>.so beside the library.  treeattn_amd.phase_trace loads it."""
+    if name not in SOURCES:
+        raise ValueError('unknown source %s' % name)
+    os.makedirs(OBJ, exist_ok=True)
+    src = os.path.join(CSRC, name)
+    obj = os.path.join(OBJ, 'trace_' + name.replace('.hip', '.o'))
+    cmd = [HIPCC, '-c', src, '-o', obj] + COMMON + SOURCES[name] + ['-DTA_TRACE']
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError('hipcc failed for %s (tracing):\n%s' % (name, r.stderr[-6000:]))
+    objs = [os.path.join(OBJ, n.replace('.hip', '.o')) for n in sorted(SOURCES) if n != name]
+    missing = [o for o in objs if not os.path.exists(o)]
+    if missing:
+        raise RuntimeError('run python -m treeattn_amd.build first (missing %s)' % ', '.join(missing))
+    lib = trace_lib_path(name)
+    r = subprocess.run([HIPCC, '-shared', '-fPIC', '--offload-arch=gfx950', '-o', lib + '.tmp'] + objs + [obj],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError('link failed:\n%s' % r.stderr[-4000:])
+    os.replace(lib + '.tmp', lib)
+    if verbose:
+        print('built', lib)
+    return lib
+
+
 if __name__ == '__main__':
-    build()
+    if len(sys.argv) > 2 and sys.argv[1] == '--trace':
+        build_trace(sys.argv[2])
+    else:
+        build()
     sys.exit(0)

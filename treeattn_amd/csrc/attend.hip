@@ -508,3 +508,5 @@ extern "C" int ta_kv_append(const void* k_new, const void* v_new, int dtype, int
   }
   return check_launch("kv_append_kernel");
 }
+
+TA_TRACE_EXPORTS

@@ -8,15 +8,11 @@
 #pragma once
 
 #include "common.hpp"
+#include "trace.hpp"
 
-// TA_DMARK(i): a phase mark (a no-op here; a tracing build of a kernel defines it before including this header).
-// The descent marks 0 (after its set-up), 1 + 2k and 2 + 2k (after level k's scores and ranking); the layer
-// attention kernel marks 12 (start), 13 (descent done), 14 (attention start) and 15 (attention done).
-#ifndef TA_DMARK
-#define TA_DMARK(i) \
-  do {              \
-  } while (0)
-#endif
+// Phase marks (trace.hpp): the descent marks 0 (after its set-up), 1 + 2k and 2 + 2k (after level k's scores and
+// ranking); the layer attention kernel marks 12 (start), 13 (descent done), 14 (attention start) and 15
+// (attention done); the descent kernel marks 12 (start), 13 (its cache append done) and 14 (descent done).
 
 namespace ta {
 

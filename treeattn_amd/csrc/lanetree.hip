@@ -29,6 +29,7 @@
 #include <type_traits>
 
 #include "canon.hpp"
+#include "trace.hpp"
 
 namespace ta {
 
@@ -350,6 +351,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
   auto fadd = [](float a, float b) { return a + b; };
   auto imin = [](int a, int b) { return min(a, b); };
   auto imax = [](int a, int b) { return max(a, b); };
+  TA_DMARK(14);   // phase marks (trace.hpp): 14 start, l = level l done, 13 node sums done
   for (int c = tid; c < C; c += NT) s_pv[c] = (uint16_t)(c | ((c >= 1 && c < n0) ? 0x8000 : 0));
   __syncthreads();
   const int nlev = lt_log2(C) - 1;
@@ -670,6 +672,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
       set_level(lvl);
       for (int win = 0; win < nwin; ++win) window(std::false_type{}, std::false_type{}, win, xd, acc0, acc1);
       __syncthreads();
+      TA_DMARK(lvl);
     }
   }
   {   // levels with S <= 64: the next window's member row is requested while a window runs
@@ -685,6 +688,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
         else window(std::true_type{}, std::false_type{}, win, x, ad, ad);
       }
       __syncthreads();
+      TA_DMARK(lvl);
     }
   }
   // leaf slots, then the node sums and counts by adjacent pairs from the slots up
@@ -716,6 +720,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
     }
     for (int i = tid; i < nn; i += NT) tr.cnt[base + i] = tr.cnt[cb + 2 * i] + tr.cnt[cb + 2 * i + 1];
   }
+  TA_DMARK(13);
 }
 
 // ----------------------------------------------------------------------------------------------------- walk
@@ -1151,3 +1156,5 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
 #undef TA_LW
   return check_launch("ta_lanetree_walk");
 }
+
+TA_TRACE_EXPORTS

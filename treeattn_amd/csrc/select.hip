@@ -271,6 +271,7 @@ __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
   float* ksc = reinterpret_cast<float*>(kid + wmax4);
 
   const int t = tq[b * tq_sb + n];
+  TA_DMARK(12);
   if constexpr (APPEND) {
     // row t and the nodes ending at t; the descent below reads only nodes that end before t
     if (tid < D && t >= 0 && t < ap.Tcap) {
@@ -283,9 +284,11 @@ __global__ __launch_bounds__(WPQ == 16 ? 1024 : 256) void descend_kernel(
                      [&](int j) { return const_cast<float*>(alv.ptr[j]) + b * alv.sb[j] + h * alv.sh[j]; });
     }
   }
+  TA_DMARK(13);
   const int64_t obase = ((int64_t)bh * Nq + n) * wl;
   const int nk = descend_query<TQ, D, WPQ>(q + b * qsb + h * qsh + n * qsn, t, T, b, h, lv, n_levels, arity_log2,
                                            wmax, tid, ckey, cid, csc, kid, ksc);
+  TA_DMARK(14);
   for (int r = tid; r < wl; r += NT) {
     if (r < nk) {
       ids[obase + r] = kid[r];
@@ -828,3 +831,5 @@ extern "C" int ta_gather_dot_blocks(const void* q, const void* K, int dtype, int
   return dispatch_dt_d<GatherDotRun>(dtype, D, dtype, q, qsb, qsh, qsn, K, ksb, ksh, ksn, (const int32_t*)nullptr, blk,
                                      log2i(block), NB, B, H, N, M, NB * block, scale, out, (hipStream_t)stream);
 }
+
+TA_TRACE_EXPORTS
