@@ -172,15 +172,24 @@ def set_traffic(roof, name):
 
 
 def cpu_model():
-    """The host CPU's model name (from /proc/cpuinfo), for the CPU baseline lines."""
+    """The host CPU's model name (from /proc/cpuinfo) with its family / model / stepping numbers (a virtualised
+    host may report only the brand), for the CPU baseline lines."""
+    info = {}
     try:
         for line in open('/proc/cpuinfo'):
-            if line.startswith('model name'):
-                return line.split(':', 1)[1].strip()
+            if ':' in line:
+                k, v = (x.strip() for x in line.split(':', 1))
+                if k in ('model name', 'cpu family', 'model', 'stepping') and k not in info:
+                    info[k] = v
+            elif info:
+                break
     except OSError:
         pass
-    import platform
-    return platform.processor() or 'unknown'
+    if 'model name' not in info:
+        import platform
+        return platform.processor() or 'unknown'
+    nums = ', '.join('%s %s' % (k, info[k]) for k in ('cpu family', 'model', 'stepping') if k in info)
+    return info['model name'] + (' (%s)' % nums if nums else '')
 
 
 def time_launches(fn, iters, flush=None):
