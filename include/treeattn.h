@@ -633,7 +633,9 @@ int ta_forest_shape(int T, int block, int wmax, int* wl, int* kc, int* widest);
 /*
  * LaneTree (the reference's attn='dyn' selection), workspace -- bytes of the lane trees of ta_lanetree_build /
  * ta_lanetree_walk: B * H * (T / chunk) trees of capacity T, each T * (4 D + 8) bytes (node sums float32, counts
- * and leaf slots int32).  T a power of two in [4, 16384], chunk dividing T, D 16, 32, 64 or 128.
+ * and leaf slots int32).  T a power of two in [4, 262144], chunk dividing T, D 16, 32, 64 or 128.  Above
+ * T = 16384 the build and the walk keep the leaf slots in this workspace rather than in LDS, and the build's sort
+ * entries in a tree's node-sum area until it writes the node sums (the results are the same).
  */
 int ta_lanetree_workspace_size(int B, int H, int T, int D, int chunk, int64_t* bytes);
 

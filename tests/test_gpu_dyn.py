@@ -40,11 +40,14 @@ def rnd(*shape, seed):
     (16, 128, 32, torch.float32, 3, 2, 2), (64, 256, 64, torch.bfloat16, 3, 2, 2), (32, 32, 8, torch.float32, 2, 2, 2),
     (16, 1024, 64, torch.float32, 3, 2, 2), (32, 128, 16, torch.bfloat16, 0, 2, 2),
     (128, 256, 64, torch.float32, 3, 2, 2), (128, 16384, 4096, torch.bfloat16, 3, 1, 1),
-    (64, 8192, 1024, torch.float32, 1, 1, 1), (16, 16384, 2048, torch.float16, 2, 1, 1)])
+    (64, 8192, 1024, torch.float32, 1, 1, 1), (16, 16384, 2048, torch.float16, 2, 1, 1),
+    (16, 32768, 8192, torch.float32, 2, 1, 2), (64, 131072, 32768, torch.bfloat16, 3, 1, 1),
+    (16, 262144, 131072, torch.float16, 1, 1, 1)])
 def test_lanetree_build_is_bit_exact(D, T, chunk, dtype, iters, B, H):
     """ta_lanetree_build: every lane's leaf slots, node counts and node sums equal LaneTree.__init__ of the
-    oracle's canonical mode (dyntree.py:34-82) on the same keys, up to the largest tree (T = 16384) and head
-    size (D = 128) the kernel takes."""
+    oracle's canonical mode (dyntree.py:34-82) on the same keys, up to the largest head size (D = 128) and tree
+    (T = 262144) the kernel takes; above T = 16384 the build keeps its slot state in the workspace, and config 5's
+    131072-token context is one of those."""
     print('case', D, T, chunk, dtype, iters, B, H, flush=True)
     nl = T // chunk
     k = rnd(B, H, T, D, seed=T + D).to(dtype)
@@ -71,6 +74,7 @@ SEL_CASES = [
          dtype=torch.bfloat16, lhat='random'),
     dict(seq_len=2048, chunk=256, wmax=48, nb_window=6, nb_store=5, nb_probe=3, nb_cap_min=1, D=128, lhat='random'),
     dict(seq_len=16384, chunk=512, wmax=40, nb_window=4, nb_store=4, D=16, lhat='random', B=1, H=1),
+    dict(seq_len=32768, chunk=1024, wmax=24, nb_window=4, nb_store=4, D=16, lhat='random', B=1, H=1),
 ]
 
 
@@ -165,12 +169,13 @@ def test_all_keys_matches_dense():
 
 @pytest.mark.parametrize('T,D,B,H,kw', [
     (2048, 64, 1, 4, dict(chunk=64, wmax=8, beam=4, nb_window=8, nb_store=2, nb_probe=3, nb_cap_min=2)),
-    (16384, 128, 1, 1, dict(chunk=256, wmax=64, beam=16, nb_window=8, nb_store=8, nb_probe=3, nb_cap_min=2))])
+    (16384, 128, 1, 1, dict(chunk=256, wmax=64, beam=16, nb_window=8, nb_store=8, nb_probe=3, nb_cap_min=2)),
+    (131072, 64, 1, 1, dict(chunk=16384, wmax=64, beam=16, nb_window=8, nb_store=8, nb_probe=3, nb_cap_min=2))])
 def test_walk_properties_at_size(T, D, B, H, kw):
-    """bf16 keys at T = 2048 (D = 64) and at the largest tree, T = 16384 with D = 128 and wmax 64: every selected
-    key lies before its query; after the walk, lane l's tree holds every position 1 .. (l + 1) * chunk - 1
-    exactly once, and every node's count and sum are those of the keys in its slots (sums within float32
-    accumulation error)."""
+    """bf16 keys at T = 2048 (D = 64), at T = 16384 with D = 128 and wmax 64, and at config 5's context
+    (T = 131072, D = 64, slots in the workspace): every selected key lies before its query; after the walk, lane
+    l's tree holds every position 1 .. (l + 1) * chunk - 1 exactly once, and every node's count and sum are those
+    of the keys in its slots (sums within float32 accumulation error)."""
     print('case', T, D, B, H, kw, flush=True)
     cfg = cfg_of(seq_len=T, **kw)
     q, k = (rnd(B, H, T, D, seed=s).to(torch.bfloat16).to(DEV) for s in (61, 62))

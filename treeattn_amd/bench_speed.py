@@ -2,9 +2,10 @@
 fp16, batch 1, T = 512 .. 4096; dense = torch's scaled_dot_product_attention, block = the block forest
 (TreeAttention, tree_block 64, beam 4), dyn = the LaneTree (DynAttention, chunk 64, beam 4, fixed budget).
 --head-dim 128 and lengths up to 16384 time the LaneTree at the sizes beyond the reference's table (--only
-dense,dyn there: the block forest takes head sizes up to 64).
+dense,dyn there: the block forest takes head sizes up to 64); --chunk takes it to long contexts (its workspace
+holds T / chunk trees of T slots per head, so T = 131072 needs lanes of thousands of positions).
 Run: python -m treeattn_amd.bench_speed [--lengths 512,1024,2048,4096] [--iters 10] [--head-dim 64]
-[--only dense,block,dyn] [--wmax 8]."""
+[--only dense,block,dyn] [--wmax 8] [--chunk 64]."""
 import argparse
 import json
 
@@ -35,6 +36,7 @@ def main():
     ap.add_argument('--heads', type=int, default=6)
     ap.add_argument('--head-dim', type=int, default=64)
     ap.add_argument('--wmax', type=int, default=8, help="the LaneTree's wmax (the reference's Config: 8)")
+    ap.add_argument('--chunk', type=int, default=64, help="the LaneTree's lane length (the reference's: 64)")
     ap.add_argument('--only', default='dense,block,dyn', help='the columns to time')
     ap.add_argument('--json', action='store_true', help='one JSON line per length instead of the table')
     args = ap.parse_args()
@@ -56,7 +58,7 @@ def main():
                 blk = TreeAttention(Config(seq_len=T, n_head=H, n_embd=H * dh, tree_block=64, beam=4)).to(dev).eval()
                 res['block'] = timeit(lambda: blk.sparse_attend(q, k, v), args.iters)
             if 'dyn' in cols:
-                dyn = DynAttention(Config(seq_len=T, n_head=H, n_embd=H * dh, attn='dyn', chunk=64, beam=4,
+                dyn = DynAttention(Config(seq_len=T, n_head=H, n_embd=H * dh, attn='dyn', chunk=args.chunk, beam=4,
                                           wmax=args.wmax, beam_mode='fixed', local=3)).to(dev).eval()
                 res['dyn'] = timeit(lambda: dyn.sparse_attend(q, k, v), args.iters)
         rows.append(res)

@@ -33,7 +33,8 @@
 
 namespace ta {
 
-constexpr int kLaneMaxT = 16384;   // tree capacity = sequence length (the build holds 8 bytes per slot in LDS)
+constexpr int kLaneMaxT = 262144;      // tree capacity = sequence length
+constexpr int kLaneLdsMaxT = 16384;    // up to here the build keeps its 8 bytes per slot in LDS, above in HBM
 constexpr int kLaneMaxW = 64;      // wmax: the 2 * wmax children of a level are scored in rounds of 64 slots
 constexpr int kLaneMaxNb = 64;     // nb_window * nb_store neighbour entries, one per slot
 constexpr int kLaneDQ = 16;        // dimensions of a row held by one lane
@@ -176,13 +177,14 @@ __device__ __forceinline__ uint32_t lt_sort_key(float p) {
 
 // Ascending bitonic sort of the pairs (key[i], idx[i]), i < n2 (a power of two; the indices unique), by the
 // whole workgroup.
-__device__ __forceinline__ void lt_bitonic_sort(uint32_t* key, uint16_t* idx, int n2, int tid, int nt) {
+template <typename IW>
+__device__ __forceinline__ void lt_bitonic_sort(uint32_t* key, IW* idx, int n2, int tid, int nt) {
   for (int k = 2; k <= n2; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = tid; i < (n2 >> 1); i += nt) {
         const int a = ((i & ~(j - 1)) << 1) | (i & (j - 1)), b = a + j;
         const uint32_t ka = key[a], kb = key[b];
-        const uint16_t ia = idx[a], ib = idx[b];
+        const IW ia = idx[a], ib = idx[b];
         const bool gt = ka > kb || (ka == kb && ia > ib);
         if (gt == ((a & k) == 0)) {
           key[a] = kb;
@@ -303,13 +305,16 @@ __device__ __forceinline__ void lt_group_reduce_w(const float* red, const float*
 // The build's LDS: the row area (three sets of 64 slot rows: A the mean's partials, B and C the two Lloyd
 // partials; or a level's sort keys and indices, 6 bytes per slot), the tree slots as 16-bit words (key
 // position, bit 15 set when the slot holds a real key), three centroid banks of 16 groups (the mean, c0, c1),
-// the rank keys of two windows and the cross-wavefront words.
-__host__ __device__ constexpr int lt_rows_bytes(int C, int D) {
-  return 6 * C > 3 * kLaneSlots * (D + 4) * 4 ? ((6 * C + 15) & ~15) : 3 * kLaneSlots * (D + 4) * 4;
+// the rank keys of two windows and the cross-wavefront words.  Above kLaneLdsMaxT slots (BIG) the slot words
+// (32-bit: bit 31 the real-key bit) live in the tree's slot array and the sort keys and indices (4 + 4 bytes per
+// slot) in its node-sum area, both in HBM and private to the workgroup until the node sums are written; the LDS
+// then holds the rest only.
+__host__ __device__ constexpr int lt_rows_bytes(int C, int D, bool big) {
+  return !big && 6 * C > 3 * kLaneSlots * (D + 4) * 4 ? ((6 * C + 15) & ~15) : 3 * kLaneSlots * (D + 4) * 4;
 }
-__host__ __device__ constexpr int lt_build_lds_bytes(int C, int D) {
-  return lt_rows_bytes(C, D) + ((2 * C + 15) & ~15) + 3 * kLtGroups * (D + 4) * 4 + 2 * kLaneSlots * 4 +
-         2 * 64 * 4 + 3 * kLtGroups * 4;
+__host__ __device__ constexpr int lt_build_lds_bytes(int C, int D, bool big) {
+  return lt_rows_bytes(C, D, big) + (big ? 0 : ((2 * C + 15) & ~15)) + 3 * kLtGroups * (D + 4) * 4 +
+         2 * kLaneSlots * 4 + 2 * 64 * 4 + 3 * kLtGroups * 4;
 }
 
 // ---------------------------------------------------------------------------------------------------- build
@@ -321,38 +326,40 @@ __host__ __device__ constexpr int lt_build_lds_bytes(int C, int D) {
 // member j (and j + 64, j + 128, ... when S > 64: partial j of the canonical sums, their rows requested four at
 // a time); groups of S < 64 members sit side by side, L = min(S, 64) slots each, and then a slot's member row
 // stays in registers for the whole window (the next window's row is requested while this one runs) and the
-// two farthest members are read from the mean's slot rows in LDS.  The order: for S >= 64 a bitonic sort of
-// (projection, index) over the span of the real keys, for smaller groups ranks by counting.
-template <typename T, int D, int Q>
+// two farthest members are read from the mean's slot rows in LDS.  The order: for S > 64 a bitonic sort of
+// (projection, index) over the span of the real keys, for groups of S <= 64 ranks by counting.
+template <typename T, int D, int Q, bool BIG>
 __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
                                                                    int64_t kst, int H, int C, int nlane, int chunk,
                                                                    int iters, float* __restrict__ ws, int64_t P) {
   constexpr int RS = D + 4, DQ = kLaneDQ, NT = kWave * Q, U = Q >= 8 ? 2 : 4;   // U: member rows requested at a time
+  using SW = std::conditional_t<BIG, uint32_t, uint16_t>;   // slot words and sort indices
+  constexpr uint32_t VBIT = BIG ? 0x80000000u : 0x8000u;     // the slot holds a real key
   extern __shared__ __align__(16) unsigned char s_raw[];
-  const int rowsb = lt_rows_bytes(C, D);
+  const int64_t pt = blockIdx.x;
+  const LaneTree tr = lane_tree(ws, P, C, D, pt);
+  const int rowsb = lt_rows_bytes(C, D, BIG);
   float* s_rows = reinterpret_cast<float*>(s_raw);                                    // [3][64][RS]
-  uint32_t* s_sk = reinterpret_cast<uint32_t*>(s_raw);                                // [C]
-  uint16_t* s_si = reinterpret_cast<uint16_t*>(s_raw + 4 * C);                        // [C]
-  uint16_t* s_pv = reinterpret_cast<uint16_t*>(s_raw + rowsb);                        // [C]
-  float* s_cen = reinterpret_cast<float*>(s_raw + rowsb + ((2 * C + 15) & ~15));   // [3][16][RS]
+  uint32_t* s_sk = BIG ? reinterpret_cast<uint32_t*>(tr.sums) : reinterpret_cast<uint32_t*>(s_raw);   // [C]
+  SW* s_si = BIG ? reinterpret_cast<SW*>(tr.sums + C) : reinterpret_cast<SW*>(s_raw + 4 * C);          // [C]
+  SW* s_pv = BIG ? reinterpret_cast<SW*>(tr.slot) : reinterpret_cast<SW*>(s_raw + rowsb);              // [C]
+  float* s_cen = reinterpret_cast<float*>(s_raw + rowsb + (BIG ? 0 : ((2 * C + 15) & ~15)));   // [3][16][RS]
   float* s_key = s_cen + 3 * kLtGroups * RS;                                          // [2][64]
   LtXchg xw{reinterpret_cast<int*>(s_key + 2 * kLaneSlots), 0};
   float* s_gc = s_key + 2 * kLaneSlots + 2 * 64;   // [3][16] group counts: the mean's, then the two clusters'
   const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ, wv = wave_id();
-  const int64_t pt = blockIdx.x;
   const int ln = (int)(pt % nlane);
   const int64_t bh = pt / nlane;
   const T* kb = k + (bh / H) * ksb + (bh % H) * ksh + d0;
   const int n0 = ln * chunk;
-  const LaneTree tr = lane_tree(ws, P, C, D, pt);
   const float kInf = __int_as_float(0x7f800000);
-  auto perm = [&](int s) { return (int)(s_pv[s] & 0x7fff); };
-  auto val = [&](int s) { return (s_pv[s] & 0x8000) != 0; };
+  auto perm = [&](int s) { return (int)(s_pv[s] & (VBIT - 1)); };
+  auto val = [&](int s) { return (s_pv[s] & VBIT) != 0; };
   auto fadd = [](float a, float b) { return a + b; };
   auto imin = [](int a, int b) { return min(a, b); };
   auto imax = [](int a, int b) { return max(a, b); };
   TA_DMARK(14);   // phase marks (trace.hpp): 14 start, l = level l done, 13 node sums done
-  for (int c = tid; c < C; c += NT) s_pv[c] = (uint16_t)(c | ((c >= 1 && c < n0) ? 0x8000 : 0));
+  for (int c = tid; c < C; c += NT) s_pv[c] = (SW)((uint32_t)c | ((c >= 1 && c < n0) ? VBIT : 0u));
   __syncthreads();
   const int nlev = lt_log2(C) - 1;
   // the level's geometry (set_level)
@@ -609,33 +616,40 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
             pr = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return c0b[e] - c1b[e]; });
           if (q == 0) {
             s_sk[i - vlo] = lt_sort_key(pr);
-            s_si[i - vlo] = (uint16_t)(i - vlo);
+            s_si[i - vlo] = (SW)(i - vlo);
           }
         };
         scan(proj);
         for (int r = n + tid; r < n2; r += NT) {
           s_sk[r] = lt_sort_key(kInf);
-          s_si[r] = (uint16_t)r;
+          s_si[r] = (SW)r;
         }
         __syncthreads();
         lt_bitonic_sort(s_sk, s_si, n2, tid, NT);
       }
       // layout: sorted ranks [0, nl) to the left half, [nl, ng) to the right half (phase A rewrites each
-      // sort key as (position, key position) before phase B moves the slots)
+      // entry as (position, key position) -- one 32-bit word, or the index and key words when BIG -- before phase
+      // B moves the slots)
       for (int r = tid; r < ng; r += NT) {
         const int mm = vlo + (int)s_si[r];
         const int pos = r < nl ? r : half + r - nl;
-        s_sk[r] = ((uint32_t)pos << 16) | (uint32_t)perm(gb + mm);
+        if constexpr (BIG) {
+          s_si[r] = (SW)pos;
+          s_sk[r] = (uint32_t)perm(gb + mm);
+        } else {
+          s_sk[r] = ((uint32_t)pos << 16) | (uint32_t)perm(gb + mm);
+        }
       }
       const int fillp = lastinv >= 0 ? perm(gb + lastinv) : 0;
       __syncthreads();
       for (int r = tid; r < ng; r += NT) {
         const uint32_t e = s_sk[r];
-        s_pv[gb + (int)(e >> 16)] = (uint16_t)((e & 0xffffu) | 0x8000u);
+        if constexpr (BIG) s_pv[gb + (int)s_si[r]] = (SW)(e | VBIT);
+        else s_pv[gb + (int)(e >> 16)] = (SW)((e & 0xffffu) | VBIT);
       }
       for (int pp = tid; pp < S; pp += NT) {
         const bool filled = pp < half ? pp < nl : (pp - half) < nr;
-        if (!filled) s_pv[gb + pp] = (uint16_t)fillp;
+        if (!filled) s_pv[gb + pp] = (SW)fillp;
       }
       __syncthreads();
     } else {
@@ -658,10 +672,10 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
           rank += (kj < key || (kj == key && j < gl)) ? 1 : 0;
         }
       }
-      if (v && q == 0) s_pv[gb + (rank < nl ? rank : half + rank - nl)] = (uint16_t)(pm | 0x8000);
+      if (v && q == 0) s_pv[gb + (rank < nl ? rank : half + rank - nl)] = (SW)((uint32_t)pm | VBIT);
       if (live && q == 0) {
         const bool filled = gl < half ? gl < nl : (gl - half) < nr;
-        if (!filled) s_pv[s] = (uint16_t)fillp;
+        if (!filled) s_pv[s] = (SW)fillp;
       }
     }
   };
@@ -691,8 +705,8 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
       TA_DMARK(lvl);
     }
   }
-  // leaf slots, then the node sums and counts by adjacent pairs from the slots up
-  for (int c = tid; c < C; c += NT) tr.slot[c] = val(c) ? perm(c) : -1;
+  // the leaves' node sums and counts (from the slot words), the leaf slots (in place when BIG), then the node
+  // sums and counts by adjacent pairs from the leaves up
   const int nleaf = C / 2;
   for (int i = m; i < nleaf; i += kLaneSlots) {
     float x[DQ], y[DQ];
@@ -706,6 +720,11 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
           make_float4(x[d] * v0 + y[d] * v1, x[d + 1] * v0 + y[d + 1] * v1, x[d + 2] * v0 + y[d + 2] * v1,
                       x[d + 3] * v0 + y[d + 3] * v1);
     if (q == 0) tr.cnt[nleaf - 1 + i] = (int)val(2 * i) + (int)val(2 * i + 1);
+  }
+  __syncthreads();
+  for (int c = tid; c < C; c += NT) {
+    const int32_t sl = val(c) ? perm(c) : -1;
+    tr.slot[c] = sl;
   }
   for (int lv = nlev - 1; lv >= 0; --lv) {
     __syncthreads();
@@ -743,13 +762,14 @@ struct LaneWalk {
 
 // The nodes of a lane tree during the walk: nodes [0, ntop) (its top levels) live in LDS for the whole walk
 // (rows of stride D + 4 floats, and counts), deeper nodes in the workspace; the leaf slots (C entries) live in
-// LDS too.  A lane reads and writes its 16 dimensions of a row.
-template <int D>
+// LDS too up to kLaneLdsMaxT slots, above that (BIG) in the workspace.  A lane reads and writes its 16 dimensions
+// of a row.
+template <int D, bool BIG>
 struct LaneNodes {
   LaneTree tr;
   float* top;
   int32_t* tcnt;
-  int32_t* slot;   // LDS copy of the leaf slots
+  int32_t* slot;   // the leaf slots: an LDS copy, or the workspace's when BIG
   int ntop, C;
   __device__ __forceinline__ int cnt(int n) const { return n < ntop ? tcnt[n] : tr.cnt[n]; }
   __device__ __forceinline__ void set_cnt(int n, int v) const {
@@ -797,9 +817,11 @@ struct LaneNodes {
       if (to_lds) tcnt[n] = tr.cnt[n];
       else tr.cnt[n] = tcnt[n];
     }
-    for (int n = tid; n < C; n += nt) {
-      if (to_lds) slot[n] = tr.slot[n];
-      else tr.slot[n] = slot[n];
+    if constexpr (!BIG) {
+      for (int n = tid; n < C; n += nt) {
+        if (to_lds) slot[n] = tr.slot[n];
+        else tr.slot[n] = slot[n];
+      }
     }
   }
 };
@@ -817,7 +839,7 @@ __device__ __forceinline__ uint64_t lt_rank_word(bool valid, float sc, int id, i
 // (dyntree.py:148-243).  Slot j scores neighbour entry j and the level's children j and j + 64; the lanes of
 // slot 0 insert the position's key.  A workgroup barrier ends every position (the tree rows the insertion
 // wrote are read by other wavefronts at the next one).
-template <typename T, int D, int Q>
+template <typename T, int D, int Q, bool BIG>
 __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
   constexpr int DQ = kLaneDQ, NT = kWave * Q;
   __shared__ int32_t s_stl[kLaneMaxNb];   // stored leaves of the last Wn positions (ring), NS each
@@ -837,11 +859,11 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
   const T* kb = static_cast<const T*>(p.k) + b * p.ksb + h * p.ksh + d0;
   const LaneTree tr = lane_tree(p.ws, p.P, p.C, D, pt);
   extern __shared__ __align__(16) unsigned char s_dyn[];
-  LaneNodes<D> nd;
+  LaneNodes<D, BIG> nd;
   nd.tr = tr;
   nd.top = reinterpret_cast<float*>(s_dyn);
   nd.tcnt = reinterpret_cast<int32_t*>(nd.top + p.ntop * (D + 4));
-  nd.slot = nd.tcnt + p.ntop;
+  nd.slot = BIG ? tr.slot : nd.tcnt + p.ntop;
   nd.ntop = p.ntop;
   nd.C = p.C;
   nd.copy(true, tid, NT);
@@ -1044,7 +1066,7 @@ using namespace ta;
 extern "C" int ta_lanetree_workspace_size(int B, int H, int T, int D, int chunk, int64_t* bytes) {
   if (B <= 0 || H <= 0 || T < 4 || T > kLaneMaxT || (T & (T - 1)) || chunk <= 0 || T % chunk ||
       !lanetree_dim_ok(D) || bytes == nullptr) {
-    set_error("ta_lanetree_workspace_size: bad arguments (T a power of two in [4, 16384], chunk dividing T, "
+    set_error("ta_lanetree_workspace_size: bad arguments (T a power of two in [4, 262144], chunk dividing T, "
               "D 16, 32, 64 or 128)");
     return TA_ERR_ARG;
   }
@@ -1068,11 +1090,18 @@ extern "C" int ta_lanetree_build(const void* k, int dtype, int64_t ksb, int64_t 
     return TA_ERR_ARG;
   }
   const int64_t P = (int64_t)B * H * (T / chunk);
-  const size_t lds = (size_t)lt_build_lds_bytes(T, D);
+  const bool big = T > kLaneLdsMaxT;
+  const size_t lds = (size_t)lt_build_lds_bytes(T, D, big);
   hipStream_t st = (hipStream_t)stream;
-#define TA_LB(TT, DD)                                                                                          \
-  hipLaunchKernelGGL((lanetree_build_kernel<TT, DD, DD / kLaneDQ>), dim3((unsigned)P), dim3(DD / kLaneDQ * kWave), \
-                     lds, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, chunk, kmeans_iters, (float*)ws, P)
+#define TA_LB(TT, DD)                                                                                                 \
+  if (big)                                                                                                            \
+    hipLaunchKernelGGL((lanetree_build_kernel<TT, DD, DD / kLaneDQ, true>), dim3((unsigned)P),                        \
+                       dim3(DD / kLaneDQ * kWave), lds, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, chunk,      \
+                       kmeans_iters, (float*)ws, P);                                                                  \
+  else                                                                                                                \
+    hipLaunchKernelGGL((lanetree_build_kernel<TT, DD, DD / kLaneDQ, false>), dim3((unsigned)P),                       \
+                       dim3(DD / kLaneDQ * kWave), lds, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, chunk,      \
+                       kmeans_iters, (float*)ws, P)
 #define TA_LB_D(TT)                  \
   switch (D) {                       \
     case 16: TA_LB(TT, 16); break;   \
@@ -1132,11 +1161,16 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
   int ntop = 1;
   while (2 * ntop + 1 <= T - 1 && (2 * ntop + 1) * rowb <= 40960) ntop = 2 * ntop + 1;
   p.ntop = ntop;
-  const size_t lds = (size_t)ntop * rowb + (size_t)T * 4;   // + the leaf slots
+  const bool big = T > kLaneLdsMaxT;
+  const size_t lds = (size_t)ntop * rowb + (big ? 0 : (size_t)T * 4);   // + the leaf slots
   hipStream_t st = (hipStream_t)stream;
-#define TA_LW(TT, DD)                                                                                          \
-  hipLaunchKernelGGL((lanetree_walk_kernel<TT, DD, DD / kLaneDQ>), dim3((unsigned)p.P), dim3(DD / kLaneDQ * kWave), \
-                     lds, st, p)
+#define TA_LW(TT, DD)                                                                                                 \
+  if (big)                                                                                                            \
+    hipLaunchKernelGGL((lanetree_walk_kernel<TT, DD, DD / kLaneDQ, true>), dim3((unsigned)p.P),                       \
+                       dim3(DD / kLaneDQ * kWave), lds, st, p);                                                       \
+  else                                                                                                                \
+    hipLaunchKernelGGL((lanetree_walk_kernel<TT, DD, DD / kLaneDQ, false>), dim3((unsigned)p.P),                      \
+                       dim3(DD / kLaneDQ * kWave), lds, st, p)
 #define TA_LW_D(TT)                  \
   switch (D) {                       \
     case 16: TA_LW(TT, 16); break;   \
