@@ -29,7 +29,6 @@
 #include <type_traits>
 
 #include "canon.hpp"
-#include "trace.hpp"
 
 namespace ta {
 
@@ -204,25 +203,37 @@ __device__ __forceinline__ void lt_bitonic_sort(uint32_t* key, IW* idx, int n2, 
 // group g at gc[16 s + nseg g + j], integers); lt_group_reduce then reduces every (set, group, dimension) in one
 // thread: the halving tree over the group's L partials, divided by max(count, 1).  The value goes to dst + set *
 // 16 (D + 4) + group (D + 4) + dimension when the count is positive or `always`.  All reads are issued before
-// the first store.
+// the first store.  MASK: the sets share one set of rows (zero where the slot holds no key), set s taking a slot's
+// row where its label byte (lab, 64 of them) is s + 1 and zero elsewhere -- the values the separate rows held.
 __device__ __forceinline__ void lt_group_row(const float (&v)[kLaneDQ], bool take, float* row) {
 #pragma unroll
   for (int d = 0; d < kLaneDQ; d += 4)
     *reinterpret_cast<float4*>(row + d) = take ? make_float4(v[d], v[d + 1], v[d + 2], v[d + 3])
                                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
-template <int D, int L, int NT, int NSET>
+template <int L>
+__device__ __forceinline__ void lt_label_mask(float (&p)[L], const uint8_t* lab, int g, int set) {
+#pragma unroll
+  for (int j4 = 0; j4 < L; j4 += 4) {
+    const uint32_t w = reinterpret_cast<const uint32_t*>(lab)[(g * L + j4) >> 2];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if (((w >> (8 * b)) & 0xffu) != (uint32_t)(set + 1)) p[j4 + b] = 0.0f;
+  }
+}
+template <int D, int L, int NT, int NSET, bool MASK = false>
 __device__ __forceinline__ void lt_group_outputs(const float* red, const float* gc, int nseg, bool always, float* dst,
-                                                 int tid) {
+                                                 int tid, const uint8_t* lab = nullptr) {
   constexpr int RS = D + 4, nout1 = (kLaneSlots / L) * D, nout = NSET * nout1, NU = (nout + NT - 1) / NT;
   float p[NU][L], c[NU];
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
     const int o = tid + NT * u, set = o / nout1, r = o - set * nout1, g = r / D, d = r - g * D;
     const bool in = o < nout;
-    const float* base = red + (set * kLaneSlots + g * L) * RS;
+    const float* base = red + ((MASK ? 0 : set * kLaneSlots) + g * L) * RS;
 #pragma unroll
     for (int j = 0; j < L; ++j) p[u][j] = in ? base[j * RS + d] : 0.0f;
+    if constexpr (MASK) lt_label_mask<L>(p[u], lab, g, set);
     float cs = 0.0f;
     for (int j = 0; j < nseg; ++j) cs = cs + (in ? gc[set * kLtGroups + g * nseg + j] : 0.0f);
     c[u] = cs;
@@ -241,25 +252,30 @@ __device__ __forceinline__ void lt_group_outputs(const float* red, const float* 
     if (o < nout && (always || c[u] > 0.0f)) dst[(set * kLtGroups + g) * RS + d] = p[u][0];
   }
 }
-template <int D, int NT, int NSET>
+// LMIN: the smallest group width L the caller passes (narrower widths are not compiled in).
+template <int D, int NT, int NSET, bool MASK = false, int LMIN = 4>
 __device__ __forceinline__ void lt_group_reduce(const float* red, const float* gc, int nseg, int L, bool always,
-                                                float* dst, int tid) {
+                                                float* dst, int tid, const uint8_t* lab = nullptr) {
   __syncthreads();
   switch (L) {
-    case 4: lt_group_outputs<D, 4, NT, NSET>(red, gc, nseg, always, dst, tid); break;
-    case 8: lt_group_outputs<D, 8, NT, NSET>(red, gc, nseg, always, dst, tid); break;
-    case 16: lt_group_outputs<D, 16, NT, NSET>(red, gc, nseg, always, dst, tid); break;
-    case 32: lt_group_outputs<D, 32, NT, NSET>(red, gc, nseg, always, dst, tid); break;
-    default: lt_group_outputs<D, 64, NT, NSET>(red, gc, nseg, always, dst, tid); break;
+    case 4: if constexpr (LMIN <= 4) lt_group_outputs<D, 4, NT, NSET, MASK>(red, gc, nseg, always, dst, tid, lab); break;
+    case 8: if constexpr (LMIN <= 8) lt_group_outputs<D, 8, NT, NSET, MASK>(red, gc, nseg, always, dst, tid, lab); break;
+    case 16:
+      if constexpr (LMIN <= 16) lt_group_outputs<D, 16, NT, NSET, MASK>(red, gc, nseg, always, dst, tid, lab);
+      break;
+    case 32:
+      if constexpr (LMIN <= 32) lt_group_outputs<D, 32, NT, NSET, MASK>(red, gc, nseg, always, dst, tid, lab);
+      break;
+    default: lt_group_outputs<D, 64, NT, NSET, MASK>(red, gc, nseg, always, dst, tid, lab); break;
   }
   __syncthreads();
 }
 
 // lt_group_reduce for groups that lie inside one wavefront (L * Q <= 64): the wavefront reduces the outputs of
 // its own groups (64 / (Q L) of them, from group wave * 64 / (Q L) on), between wavefront barriers.
-template <int D, int Q, int L, int NSET>
+template <int D, int Q, int L, int NSET, bool MASK = false>
 __device__ __forceinline__ void lt_group_outputs_w(const float* red, const float* gc, bool always, float* dst, int lane,
-                                                   int wv) {
+                                                   int wv, const uint8_t* lab) {
   if constexpr (L * Q <= kWave) {
     constexpr int RS = D + 4, gpw = kWave / (Q * L), nout1 = gpw * D, nout = NSET * nout1;
     constexpr int NU = (nout + kWave - 1) / kWave;
@@ -268,9 +284,10 @@ __device__ __forceinline__ void lt_group_outputs_w(const float* red, const float
     for (int u = 0; u < NU; ++u) {
       const int o = lane + kWave * u, set = o / nout1, r = o - set * nout1, gg = wv * gpw + r / D, d = r % D;
       const bool in = o < nout;
-      const float* base = red + (set * kLaneSlots + gg * L) * RS;
+      const float* base = red + ((MASK ? 0 : set * kLaneSlots) + gg * L) * RS;
 #pragma unroll
       for (int j = 0; j < L; ++j) p[u][j] = in ? base[j * RS + d] : 0.0f;
+      if constexpr (MASK) lt_label_mask<L>(p[u], lab, gg, set);
       c[u] = in ? gc[set * kLtGroups + gg] : 0.0f;
     }
 #pragma unroll
@@ -288,65 +305,68 @@ __device__ __forceinline__ void lt_group_outputs_w(const float* red, const float
     }
   }
 }
-template <int D, int Q, int NSET>
+template <int D, int Q, int NSET, bool MASK = false>
 __device__ __forceinline__ void lt_group_reduce_w(const float* red, const float* gc, int L, bool always, float* dst,
-                                                  int lane, int wv) {
+                                                  int lane, int wv, const uint8_t* lab = nullptr) {
   wave_sync();
   switch (L) {
-    case 4: lt_group_outputs_w<D, Q, 4, NSET>(red, gc, always, dst, lane, wv); break;
-    case 8: lt_group_outputs_w<D, Q, 8, NSET>(red, gc, always, dst, lane, wv); break;
-    case 16: lt_group_outputs_w<D, Q, 16, NSET>(red, gc, always, dst, lane, wv); break;
-    case 32: lt_group_outputs_w<D, Q, 32, NSET>(red, gc, always, dst, lane, wv); break;
-    default: lt_group_outputs_w<D, Q, 64, NSET>(red, gc, always, dst, lane, wv); break;
+    case 4: lt_group_outputs_w<D, Q, 4, NSET, MASK>(red, gc, always, dst, lane, wv, lab); break;
+    case 8: lt_group_outputs_w<D, Q, 8, NSET, MASK>(red, gc, always, dst, lane, wv, lab); break;
+    case 16: lt_group_outputs_w<D, Q, 16, NSET, MASK>(red, gc, always, dst, lane, wv, lab); break;
+    case 32: lt_group_outputs_w<D, Q, 32, NSET, MASK>(red, gc, always, dst, lane, wv, lab); break;
+    default: lt_group_outputs_w<D, Q, 64, NSET, MASK>(red, gc, always, dst, lane, wv, lab); break;
   }
   wave_sync();
 }
 
-// The build's LDS: the row area (three sets of 64 slot rows: A the mean's partials, B and C the two Lloyd
-// partials; or a level's sort keys and indices, 6 bytes per slot), the tree slots as 16-bit words (key
-// position, bit 15 set when the slot holds a real key), three centroid banks of 16 groups (the mean, c0, c1),
-// the rank keys of two windows and the cross-wavefront words.  Above kLaneLdsMaxT slots (BIG) the slot words
-// (32-bit: bit 31 the real-key bit) live in the tree's slot array and the sort keys and indices (4 + 4 bytes per
-// slot) in its node-sum area, both in HBM and private to the workgroup until the node sums are written; the LDS
-// then holds the rest only.
+// The split launch's LDS (one group of S slots): the row area (three sets of 64 slot rows: A the mean's partials,
+// B and C the two Lloyd partials; or the group's sort keys and indices, 6 bytes per slot), the group's slots as
+// 16-bit words (key position, bit 15 set when the slot holds a real key), three centroid banks (the mean, c0,
+// c1), the cross-wavefront words and the group counts.  Above kLaneLdsMaxT slots (BIG) the slot words (32-bit:
+// bit 31 the real-key bit) stay in the tree's slot array and the sort keys and indices (4 + 4 bytes per slot) go
+// to the group's part of the node-sum area ([2 g S, 2 g S + 2 S) for group g), both in HBM and unused until the
+// tail writes the node sums; the LDS then holds the rest only.
 __host__ __device__ constexpr int lt_rows_bytes(int C, int D, bool big) {
   return !big && 6 * C > 3 * kLaneSlots * (D + 4) * 4 ? ((6 * C + 15) & ~15) : 3 * kLaneSlots * (D + 4) * 4;
 }
 __host__ __device__ constexpr int lt_build_lds_bytes(int C, int D, bool big) {
-  return lt_rows_bytes(C, D, big) + (big ? 0 : ((2 * C + 15) & ~15)) + 3 * kLtGroups * (D + 4) * 4 +
-         2 * kLaneSlots * 4 + 2 * 64 * 4 + 3 * kLtGroups * 4;
+  return lt_rows_bytes(C, D, big) + (big ? 0 : ((2 * C + 15) & ~15)) + 3 * kLtGroups * (D + 4) * 4 + 2 * 64 * 4 +
+         3 * kLtGroups * 4;
 }
 
 // ---------------------------------------------------------------------------------------------------- build
-// One workgroup per lane tree (dyntree.py:34-82).  Every level splits each group of S = C >> lvl slots of the
+// The lane trees (dyntree.py:34-82) in three launches.  Every level splits each group of S = C >> lvl slots of a
 // tree by a masked 2-means projection; the group's real keys are then laid out half and half (the larger half
 // first), empty slots after each half's keys, every empty slot holding the position of the group's last empty
 // slot (the one the stable sort ranks last).  Empty slots add key * 0 to the masked sums; they are skipped, which
-// changes at most the sign of a zero.  A window of max(S, 64) members is done at a time: workgroup slot j holds
-// member j (and j + 64, j + 128, ... when S > 64: partial j of the canonical sums, their rows requested four at
-// a time); groups of S < 64 members sit side by side, L = min(S, 64) slots each, and then a slot's member row
-// stays in registers for the whole window (the next window's row is requested while this one runs) and the
-// two farthest members are read from the mean's slot rows in LDS.  The order: for S > 64 a bitonic sort of
-// (projection, index) over the span of the real keys, for groups of S <= 64 ranks by counting.
+// changes at most the sign of a zero.
+//
+// lanetree_split_kernel, one launch per level whose groups hold more than 64 slots and one workgroup per group
+// (the groups of a level touch disjoint slots): workgroup slot j holds members j, j + 64, j + 128, ... (partial j
+// of the canonical sums, their rows requested U at a time); the order by a bitonic sort of (projection, index)
+// over the span of the group's real keys.  The slot words (key position, bit 31 set for a real key) go from the
+// tree's slot array into LDS and back; level 0 starts them (key j in slot j, real for 1 <= j < the lane's start).
 template <typename T, int D, int Q, bool BIG>
-__global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
+__global__ __launch_bounds__(kWave * Q) void lanetree_split_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
                                                                    int64_t kst, int H, int C, int nlane, int chunk,
-                                                                   int iters, float* __restrict__ ws, int64_t P) {
+                                                                   int iters, float* __restrict__ ws, int64_t P,
+                                                                   int lvl) {
   constexpr int RS = D + 4, DQ = kLaneDQ, NT = kWave * Q, U = Q >= 8 ? 2 : 4;   // U: member rows requested at a time
   using SW = std::conditional_t<BIG, uint32_t, uint16_t>;   // slot words and sort indices
   constexpr uint32_t VBIT = BIG ? 0x80000000u : 0x8000u;     // the slot holds a real key
   extern __shared__ __align__(16) unsigned char s_raw[];
-  const int64_t pt = blockIdx.x;
+  const int S = C >> lvl, half = S >> 1, M = S / kLaneSlots;
+  const int64_t pt = blockIdx.x >> lvl;
+  const int gb0 = (int)(blockIdx.x - (pt << lvl)) * S;   // the group's first slot
   const LaneTree tr = lane_tree(ws, P, C, D, pt);
-  const int rowsb = lt_rows_bytes(C, D, BIG);
+  const int rowsb = lt_rows_bytes(S, D, BIG);
   float* s_rows = reinterpret_cast<float*>(s_raw);                                    // [3][64][RS]
-  uint32_t* s_sk = BIG ? reinterpret_cast<uint32_t*>(tr.sums) : reinterpret_cast<uint32_t*>(s_raw);   // [C]
-  SW* s_si = BIG ? reinterpret_cast<SW*>(tr.sums + C) : reinterpret_cast<SW*>(s_raw + 4 * C);          // [C]
-  SW* s_pv = BIG ? reinterpret_cast<SW*>(tr.slot) : reinterpret_cast<SW*>(s_raw + rowsb);              // [C]
-  float* s_cen = reinterpret_cast<float*>(s_raw + rowsb + (BIG ? 0 : ((2 * C + 15) & ~15)));   // [3][16][RS]
-  float* s_key = s_cen + 3 * kLtGroups * RS;                                          // [2][64]
-  LtXchg xw{reinterpret_cast<int*>(s_key + 2 * kLaneSlots), 0};
-  float* s_gc = s_key + 2 * kLaneSlots + 2 * 64;   // [3][16] group counts: the mean's, then the two clusters'
+  uint32_t* s_sk = BIG ? reinterpret_cast<uint32_t*>(tr.sums + 2 * gb0) : reinterpret_cast<uint32_t*>(s_raw);   // [S]
+  SW* s_si = BIG ? reinterpret_cast<SW*>(tr.sums + 2 * gb0 + S) : reinterpret_cast<SW*>(s_raw + 4 * S);         // [S]
+  SW* s_pv = BIG ? reinterpret_cast<SW*>(tr.slot + gb0) : reinterpret_cast<SW*>(s_raw + rowsb);                 // [S]
+  float* s_cen = reinterpret_cast<float*>(s_raw + rowsb + (BIG ? 0 : ((2 * S + 15) & ~15)));   // [3][16][RS]
+  LtXchg xw{reinterpret_cast<int*>(s_cen + 3 * kLtGroups * RS), 0};
+  float* s_gc = s_cen + 3 * kLtGroups * RS + 2 * 64;   // [3][16] group counts: the mean's, then the two clusters'
   const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ, wv = wave_id();
   const int ln = (int)(pt % nlane);
   const int64_t bh = pt / nlane;
@@ -358,68 +378,41 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
   auto fadd = [](float a, float b) { return a + b; };
   auto imin = [](int a, int b) { return min(a, b); };
   auto imax = [](int a, int b) { return max(a, b); };
-  TA_DMARK(14);   // phase marks (trace.hpp): 14 start, l = level l done, 13 node sums done
-  for (int c = tid; c < C; c += NT) s_pv[c] = (SW)((uint32_t)c | ((c >= 1 && c < n0) ? VBIT : 0u));
+  if (lvl == 0) {
+    for (int c = tid; c < C; c += NT) s_pv[c] = (SW)((uint32_t)c | ((c >= 1 && c < n0) ? VBIT : 0u));
+  } else if constexpr (!BIG) {
+    for (int c = tid; c < S; c += NT) {
+      const uint32_t w = (uint32_t)tr.slot[gb0 + c];
+      s_pv[c] = (SW)((w & 0x7fffffffu) | ((w & 0x80000000u) ? VBIT : 0u));
+    }
+  }
   __syncthreads();
-  const int nlev = lt_log2(C) - 1;
-  // the level's geometry (set_level)
-  int S = 0, half = 0, L = 0, M = 0, Wz = 0, nwin = 0, g = 0, gl = 0, span = 0;
-  float *meanp = nullptr, *c0b = nullptr, *c1b = nullptr;   // the group's mean, c0 and c1 (this lane's part)
-  float* rowA = s_rows + m * RS;                              // this slot's rows of the sets A, B, C
+  float* meanp = s_cen + d0;   // the group's mean, c0 and c1 (this lane's part)
+  float* c0b = s_cen + kLtGroups * RS + d0;
+  float* c1b = s_cen + 2 * kLtGroups * RS + d0;
+  float* rowA = s_rows + m * RS;   // this slot's rows of the sets A, B, C
   float* rowB = rowA + kLaneSlots * RS;
   float* rowC = rowB + kLaneSlots * RS;
-  auto set_level = [&](int lvl) {
-    S = C >> lvl;
-    half = S >> 1;
-    L = S < kLaneSlots ? S : kLaneSlots;
-    M = S < kLaneSlots ? 1 : S / kLaneSlots;
-    Wz = S < kLaneSlots ? kLaneSlots : S;
-    nwin = C > Wz ? C / Wz : 1;
-    g = m / L;
-    gl = m & (L - 1);
-    span = L * Q < kWave ? L * Q : kWave;
-    meanp = s_cen + g * RS + d0;
-    c0b = s_cen + (kLtGroups + g) * RS + d0;
-    c1b = s_cen + (2 * kLtGroups + g) * RS + d0;
-  };
-  // One window of a level.  RES: one member per slot (S <= 64), its row in x for the whole window; otherwise
-  // the slot's members are scanned in order, rows requested U at a time, partial sums in acc0 / acc1.
-  auto window = [&](auto res, auto loc, int win, float(&x)[DQ], float(&acc0)[DQ], float(&acc1)[DQ])
-                    __attribute__((always_inline)) {
-    constexpr bool resident = decltype(res)::value;
-    constexpr bool local = decltype(loc)::value;   // every group inside one wavefront: wavefront barriers
-    auto sync = [&]() {
-      if constexpr (local) wave_sync();
-      else __syncthreads();
-    };
-    const int gb = win * Wz + g * S;
-    const bool live = win * Wz + m < C;   // C < 64: slots past the tree sit out
-    auto scan = [&](auto&& f) __attribute__((always_inline)) {
-      for (int t0 = 0; t0 < M; t0 += U) {
-        float xb[U][DQ];
+  float acc0[DQ], acc1[DQ];
+  if (S > kLaneSlots) {   // (a tree of at most 64 slots only has its slot words started here)
+    {
+      constexpr int gb = 0;   // slot indices below are the group's
+      auto scan = [&](auto&& f) __attribute__((always_inline)) {
+        for (int t0 = 0; t0 < M; t0 += U) {
+          float xb[U][DQ];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int t = t0 + u < M ? t0 + u : M - 1;
-          load_row_g<T, DQ>(kb + (int64_t)perm(gb + gl + L * t) * kst, xb[u]);
-        }
+          for (int u = 0; u < U; ++u) {
+            const int t = t0 + u < M ? t0 + u : M - 1;
+            load_row_g<T, DQ>(kb + (int64_t)perm(gb + m + kLaneSlots * t) * kst, xb[u]);
+          }
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-          if (t0 + u < M) f(gl + L * (t0 + u), xb[u]);
-      }
-    };
-    // (1) counts and the masked mean
-    float cntp = 0.0f;
-    int vlo = S, vhi = -1, lastinv = -1;
-    if constexpr (resident) {
-      if (live) {
-        if (val(gb + gl)) {
-          cntp = 1.0f;
-          vlo = vhi = gl;
-        } else {
-          lastinv = gl;
+          for (int u = 0; u < U; ++u)
+            if (t0 + u < M) f(m + kLaneSlots * (t0 + u), xb[u]);
         }
-      }
-    } else {
+      };
+      // (1) counts and the masked mean
+      float cntp = 0.0f;
+      int vlo = S, vhi = -1, lastinv = -1;
 #pragma unroll
       for (int d = 0; d < DQ; ++d) acc0[d] = 0.0f;
       scan([&](int i, const float(&r)[DQ]) {
@@ -433,84 +426,69 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
           lastinv = i;
         }
       });
-    }
-    float cnt = wave_grp<Q>(cntp, span, fadd);
-    vlo = wave_grp<Q>(vlo, span, imin);
-    vhi = wave_grp<Q>(vhi, span, imax);
-    lastinv = wave_grp<Q>(lastinv, span, imax);
-    bool work = __ballot(cntp > 0.0f) != 0;
-    if constexpr (Q > 1 && !local) {   // the group's statistics across wavefronts, and whether any group has keys
-      int* xb = xw.next();
-      if (lane_id() == 0) {
-        int* e = xb + wv * 8;
-        e[0] = __float_as_int(cnt);
-        e[1] = vlo;
-        e[2] = vhi;
-        e[3] = lastinv;
-        e[4] = work ? 1 : 0;
-      }
-      __syncthreads();
-      if (L * Q > kWave) {
-        const int nw = L * Q / kWave, w0 = wv & ~(nw - 1);
+      float cnt = wave_grp<Q>(cntp, kWave, fadd);
+      vlo = wave_grp<Q>(vlo, kWave, imin);
+      vhi = wave_grp<Q>(vhi, kWave, imax);
+      lastinv = wave_grp<Q>(lastinv, kWave, imax);
+      bool work = __ballot(cntp > 0.0f) != 0;
+      if constexpr (Q > 1) {   // the group's statistics across the wavefronts
+        int* xb = xw.next();
+        if (lane_id() == 0) {
+          int* e = xb + wv * 8;
+          e[0] = __float_as_int(cnt);
+          e[1] = vlo;
+          e[2] = vhi;
+          e[3] = lastinv;
+          e[4] = work ? 1 : 0;
+        }
+        __syncthreads();
         cnt = 0.0f;
         vlo = S;
         vhi = -1;
         lastinv = -1;
-        for (int j = 0; j < nw; ++j) {
-          const int* e = xb + (w0 + j) * 8;
+        work = false;
+        for (int j = 0; j < Q; ++j) {
+          const int* e = xb + j * 8;
           cnt = cnt + __int_as_float(e[0]);
           vlo = min(vlo, e[1]);
           vhi = max(vhi, e[2]);
           lastinv = max(lastinv, e[3]);
+          work = work || e[4] != 0;
         }
       }
-      work = false;
-      for (int j = 0; j < Q; ++j) work = work || xb[j * 8 + 4] != 0;
-    }
-    const int ng = (int)cnt;
-    // the group argmax of (value, member index)
-    auto argmax_grp = [&](float v, int i) {
-      wave_grp_argmax<Q>(v, i, span);
-      if (L * Q > kWave) {
-        int* xb = xw.next();
-        if (lane_id() == 0) {
-          xb[wv * 8] = __float_as_int(v);
-          xb[wv * 8 + 1] = i;
-        }
-        __syncthreads();
-        const int nw = L * Q / kWave, w0 = wv & ~(nw - 1);
-        v = __int_as_float(xb[w0 * 8]);
-        i = xb[w0 * 8 + 1];
-        for (int j = 1; j < nw; ++j) {
-          const float ov = __int_as_float(xb[(w0 + j) * 8]);
-          const int oi = xb[(w0 + j) * 8 + 1];
-          if (ov > v || (ov == v && oi < i)) {
-            v = ov;
-            i = oi;
+      const int ng = (int)cnt;
+      // the group argmax of (value, member index)
+      auto argmax_grp = [&](float v, int i) {
+        wave_grp_argmax<Q>(v, i, kWave);
+        if constexpr (Q > 1) {
+          int* xb = xw.next();
+          if (lane_id() == 0) {
+            xb[wv * 8] = __float_as_int(v);
+            xb[wv * 8 + 1] = i;
+          }
+          __syncthreads();
+          v = __int_as_float(xb[0]);
+          i = xb[1];
+          for (int j = 1; j < Q; ++j) {
+            const float ov = __int_as_float(xb[j * 8]);
+            const int oi = xb[j * 8 + 1];
+            if (ov > v || (ov == v && oi < i)) {
+              v = ov;
+              i = oi;
+            }
           }
         }
-      }
-      return i;
-    };
-    if (work) {
-      if constexpr (resident) lt_group_row(x, cntp > 0.0f, rowA + d0);
-      else lt_group_row(acc0, true, rowA + d0);
-      if (gl == 0 && q == 0) s_gc[g] = cnt;
-      if constexpr (local) lt_group_reduce_w<D, Q, 1>(s_rows, s_gc, L, true, s_cen, lane_id(), wv);   // the means
-      else lt_group_reduce<D, NT, 1>(s_rows, s_gc, 1, L, true, s_cen, tid);
-      // a = the real key farthest from the mean, then b = the real key farthest from a
-      const float* pa = c0b;
-      const float* pb = c1b;
-      for (int pass = 0; pass < 2; ++pass) {
-        const float* ref = pass == 0 ? meanp : pa;
-        float bv = -1.0f;
-        int bi = 0;
-        if constexpr (resident) {
-          if (live && cntp > 0.0f) {
-            bv = slice_dot<D, Q>([&](int e) { return x[e] - ref[e]; }, [&](int e) { return x[e] - ref[e]; });
-            bi = gl;
-          }
-        } else {
+        return i;
+      };
+      if (work) {
+        lt_group_row(acc0, true, rowA + d0);
+        if (m == 0 && q == 0) s_gc[0] = cnt;
+        lt_group_reduce<D, NT, 1, false, kLaneSlots>(s_rows, s_gc, 1, kLaneSlots, true, s_cen, tid);   // the mean
+        // a = the real key farthest from the mean, then b = the real key farthest from a (into the banks)
+        for (int pass = 0; pass < 2; ++pass) {
+          const float* ref = pass == 0 ? meanp : c0b;
+          float bv = -1.0f;
+          int bi = 0;
           scan([&](int i, const float(&r)[DQ]) {
             if (!val(gb + i)) return;
             const float d2 =
@@ -520,51 +498,20 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
               bi = i;
             }
           });
-        }
-        const int sel = argmax_grp(bv, bi);
-        float* bank = pass == 0 ? c0b : c1b;
-        if constexpr (resident) {
-          // the selected member's row is its slot's row of set A; copied into the centroid bank, which the
-          // Lloyd outputs keep for an empty cluster and the projection reads
-          const float* src = s_rows + (g * L + sel) * RS + d0;
-          if (pass == 0) pa = src;
-          else pb = src;
-          if (live) {
-#pragma unroll
-            for (int d = 0; d < DQ; d += 4)
-              *reinterpret_cast<float4*>(bank + d) = *reinterpret_cast<const float4*>(src + d);
-          }
-        } else {
+          const int sel = argmax_grp(bv, bi);
+          float* bank = pass == 0 ? c0b : c1b;
           load_row_g<T, DQ>(kb + (int64_t)perm(gb + sel) * kst, acc1);
 #pragma unroll
           for (int d = 0; d < DQ; d += 4)
             *reinterpret_cast<float4*>(bank + d) = make_float4(acc1[d], acc1[d + 1], acc1[d + 2], acc1[d + 3]);
           __syncthreads();
         }
-      }
-      // Lloyd iterations: labels from the current centroids, then both masked sums, in one pass and one
-      // reduction (sets B and C into the banks c0 and c1; an empty cluster keeps its centroid)
-      for (int it = 0; it < iters; ++it) {
-        const float* r0 = it == 0 ? pa : c0b;
-        const float* r1 = it == 0 ? pb : c1b;
-        const float cc0 = slice_dot<D, Q>([&](int e) { return r0[e]; }, [&](int e) { return r0[e]; });
-        const float cc1 = slice_dot<D, Q>([&](int e) { return r1[e]; }, [&](int e) { return r1[e]; });
-        float cp0 = 0.0f, cp1 = 0.0f;
-        auto label = [&](const float(&r)[DQ]) {
-          const float xx = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return r[e]; });
-          const float xc0 = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return r0[e]; });
-          const float xc1 = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return r1[e]; });
-          const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
-          return dist1 < dist0;
-        };
-        if constexpr (resident) {
-          if (live && cntp > 0.0f) {
-            if (label(x)) cp1 = 1.0f;
-            else cp0 = 1.0f;
-          }
-          lt_group_row(x, cp0 > 0.0f, rowB + d0);
-          lt_group_row(x, cp1 > 0.0f, rowC + d0);
-        } else {
+        // Lloyd iterations: labels from the current centroids, then both masked sums, in one pass and one
+        // reduction (sets B and C into the banks c0 and c1; an empty cluster keeps its centroid)
+        for (int it = 0; it < iters; ++it) {
+          const float cc0 = slice_dot<D, Q>([&](int e) { return c0b[e]; }, [&](int e) { return c0b[e]; });
+          const float cc1 = slice_dot<D, Q>([&](int e) { return c1b[e]; }, [&](int e) { return c1b[e]; });
+          float cp0 = 0.0f, cp1 = 0.0f;
 #pragma unroll
           for (int d = 0; d < DQ; ++d) {
             acc0[d] = 0.0f;
@@ -572,7 +519,11 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
           }
           scan([&](int i, const float(&r)[DQ]) {
             if (!val(gb + i)) return;
-            if (label(r)) {
+            const float xx = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return r[e]; });
+            const float xc0 = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return c0b[e]; });
+            const float xc1 = slice_dot<D, Q>([&](int e) { return r[e]; }, [&](int e) { return c1b[e]; });
+            const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
+            if (dist1 < dist0) {
 #pragma unroll
               for (int d = 0; d < DQ; ++d) acc1[d] = acc1[d] + r[d];
               cp1 = cp1 + 1.0f;
@@ -584,32 +535,24 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
           });
           lt_group_row(acc0, true, rowB + d0);
           lt_group_row(acc1, true, rowC + d0);
+          // the clusters' counts: a partial per wavefront
+          const float w0 = wave_grp<Q>(cp0, kWave, fadd), w1 = wave_grp<Q>(cp1, kWave, fadd);
+          if (lane_id() == 0) {
+            s_gc[kLtGroups + wv] = w0;
+            s_gc[2 * kLtGroups + wv] = w1;
+          }
+          lt_group_reduce<D, NT, 2, false, kLaneSlots>(s_rows + kLaneSlots * RS, s_gc + kLtGroups, Q, kLaneSlots,
+                                                       false, s_cen + kLtGroups * RS, tid);
         }
-        // the clusters' counts: a partial per aligned segment of `span` lanes (a group inside a wavefront, or
-        // a group's part in one wavefront)
-        const float w0 = wave_grp<Q>(cp0, span, fadd), w1 = wave_grp<Q>(cp1, span, fadd);
-        if ((tid & (span - 1)) == 0) {
-          s_gc[kLtGroups + tid / span] = w0;
-          s_gc[2 * kLtGroups + tid / span] = w1;
-        }
-        if constexpr (local)
-          lt_group_reduce_w<D, Q, 2>(s_rows + kLaneSlots * RS, s_gc + kLtGroups, L, false, s_cen + kLtGroups * RS,
-                                     lane_id(), wv);
-        else
-          lt_group_reduce<D, NT, 2>(s_rows + kLaneSlots * RS, s_gc + kLtGroups, L * Q / span, L, false,
-                                    s_cen + kLtGroups * RS, tid);
       }
-      if (resident && iters == 0) sync();   // the banks' copies of a and b, for the projection
-    }
-    const int nl = (ng + 1) / 2, nr = ng - nl;
-    if constexpr (!resident) {
-      // one group: projections on c0 - c1 over the span of the real keys (empty slots inside it: +inf),
-      // padded to a power of two with entries that sort last; bitonic sort
+      const int nl = (ng + 1) / 2, nr = ng - nl;
+      // projections on c0 - c1 over the span of the real keys (empty slots inside it: +inf), padded to a power
+      // of two with entries that sort last; bitonic sort
       if (ng > 0) {
         const int n = vhi - vlo + 1;
         int n2 = 1;
         while (n2 < n) n2 <<= 1;
-        auto proj = [&](int i, const float(&r)[DQ]) {
+        scan([&](int i, const float(&r)[DQ]) {
           if (i < vlo || i > vhi) return;
           float pr = kInf;
           if (val(gb + i))
@@ -618,8 +561,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
             s_sk[i - vlo] = lt_sort_key(pr);
             s_si[i - vlo] = (SW)(i - vlo);
           }
-        };
-        scan(proj);
+        });
         for (int r = n + tid; r < n2; r += NT) {
           s_sk[r] = lt_sort_key(kInf);
           s_si[r] = (SW)r;
@@ -627,9 +569,9 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
         __syncthreads();
         lt_bitonic_sort(s_sk, s_si, n2, tid, NT);
       }
-      // layout: sorted ranks [0, nl) to the left half, [nl, ng) to the right half (phase A rewrites each
-      // entry as (position, key position) -- one 32-bit word, or the index and key words when BIG -- before phase
-      // B moves the slots)
+      // layout: sorted ranks [0, nl) to the left half, [nl, ng) to the right half (phase A rewrites each entry as
+      // (position, key position) -- one 32-bit word, or the index and key words when BIG -- before phase B moves
+      // the slots)
       for (int r = tid; r < ng; r += NT) {
         const int mm = vlo + (int)s_si[r];
         const int pos = r < nl ? r : half + r - nl;
@@ -652,82 +594,289 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
         if (!filled) s_pv[gb + pp] = (SW)fillp;
       }
       __syncthreads();
-    } else {
-      // one member per slot (groups of S <= 64, side by side when S < 64): ranks by counting, the stable
-      // order of the projections (the rank keys alternate between two windows' areas; a window's slot words
-      // are read by no other window)
-      const int s = gb + gl;
-      const bool v = live && val(s);
-      float key = kInf;
-      if (v) key = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0b[e] - c1b[e]; });
-      const int pm = live ? perm(s) : 0;
-      const int fillp = live && lastinv >= 0 ? perm(gb + lastinv) : 0;
-      float* keys = s_key + (win & 1) * kLaneSlots;
-      if (live && q == 0) keys[m] = key;
-      sync();
-      int rank = 0;
-      if (v) {
-        for (int j = 0; j < S; ++j) {
-          const float kj = keys[g * S + j];
-          rank += (kj < key || (kj == key && j < gl)) ? 1 : 0;
+    }
+  }
+  if constexpr (!BIG) {
+    for (int c = tid; c < S; c += NT)
+      tr.slot[gb0 + c] = (int32_t)((uint32_t)perm(c) | (val(c) ? 0x80000000u : 0u));
+  }
+}
+
+// lanetree_tail_kernel, one workgroup per (tree, window of 64 slots): the levels whose groups hold at most 64
+// slots.  From the first of them on a window's keys stay inside it, so windows are independent and the launch
+// has C / 64 workgroups per tree.  Slot j holds one member, its key row in registers and (zero where the slot
+// holds no key) in LDS, the Lloyd clusters marked by a label byte per slot; groups of S < 64 slots sit side by
+// side, the two farthest members are read from the slot rows, and the order comes from ranks by counting.
+// Then the window's node sums and counts (its leaves and the nodes above them up to the window's root) and its
+// final slots (key position, or -1).
+// (Three wavefronts per SIMD requested for D >= 64: more windows resident per CU, which the window's chain of LDS
+// round trips needs; narrower rows would spill at that register budget.)
+template <typename T, int D, int Q>
+__global__ __launch_bounds__(kWave * Q) __attribute__((amdgpu_waves_per_eu(Q >= 4 ? 3 : 1, 8))) void lanetree_tail_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
+                                                                  int64_t kst, int H, int C, int nlane, int iters,
+                                                                  float* __restrict__ ws, int64_t P) {
+  constexpr int RS = D + 4, DQ = kLaneDQ, NT = kWave * Q;
+  constexpr uint32_t VB = 0x80000000u;
+  __shared__ __align__(16) float s_x[kLaneSlots * RS];          // slot rows; the window's node rows at the end
+  __shared__ __align__(16) float s_cen[3 * kLtGroups * RS];     // banks: the groups' means, c0, c1
+  __shared__ float s_key[kLaneSlots];                           // rank keys
+  __shared__ uint32_t s_pv[kLaneSlots];                         // slot words
+  __shared__ __align__(4) uint8_t s_lab[kLaneSlots];            // cluster labels (1: c0, 2: c1, 0: no key)
+  __shared__ int s_xwb[2 * 64];
+  __shared__ float s_gc[3 * kLtGroups];
+  __shared__ int s_nc[kLaneSlots];                              // the window's node counts
+  const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ, wv = wave_id();
+  const int nw = C > kLaneSlots ? C / kLaneSlots : 1;
+  const int64_t pt = blockIdx.x / nw;
+  const int win = (int)(blockIdx.x - pt * nw);
+  const int W = C < kLaneSlots ? C : kLaneSlots, base = win * kLaneSlots;
+  const int64_t bh = pt / nlane;
+  const T* kb = k + (bh / H) * ksb + (bh % H) * ksh + d0;
+  const LaneTree tr = lane_tree(ws, P, C, D, pt);
+  const bool live = m < W;   // C < 64: slots past the tree sit out
+  const float kInf = __int_as_float(0x7f800000);
+  if (tid < W) s_pv[tid] = (uint32_t)tr.slot[base + tid];
+  LtXchg xw{s_xwb, 0};
+  auto perm = [&](int s) { return (int)(s_pv[s] & (VB - 1)); };
+  auto val = [&](int s) { return (s_pv[s] & VB) != 0; };
+  auto fadd = [](float a, float b) { return a + b; };
+  auto imin = [](int a, int b) { return min(a, b); };
+  auto imax = [](int a, int b) { return max(a, b); };
+  const int nlev = lt_log2(C) - 1;
+  float* rowx = s_x + m * RS + d0;
+  auto level = [&](auto loc, int S, const float(&x)[DQ]) __attribute__((always_inline)) {
+    constexpr bool local = decltype(loc)::value;   // every group inside one wavefront: wavefront barriers
+    auto sync = [&]() {
+      if constexpr (local) wave_sync();
+      else __syncthreads();
+    };
+    const int half = S >> 1, L = S, g = m / L, gl = m & (L - 1), span = L * Q < kWave ? L * Q : kWave;
+    float* meanp = s_cen + g * RS + d0;
+    float* c0b = s_cen + (kLtGroups + g) * RS + d0;
+    float* c1b = s_cen + (2 * kLtGroups + g) * RS + d0;
+    // (1) counts
+    float cntp = 0.0f;
+    int vlo = S, vhi = -1, lastinv = -1;
+    if (live) {
+      if (val(m)) {
+        cntp = 1.0f;
+        vlo = vhi = gl;
+      } else {
+        lastinv = gl;
+      }
+    }
+    float cnt = wave_grp<Q>(cntp, span, fadd);
+    vlo = wave_grp<Q>(vlo, span, imin);
+    vhi = wave_grp<Q>(vhi, span, imax);
+    lastinv = wave_grp<Q>(lastinv, span, imax);
+    bool work = __ballot(cntp > 0.0f) != 0;
+    if constexpr (Q > 1 && !local) {   // the group's statistics across wavefronts, and whether any group has keys
+      int* xb = xw.next();
+      if (lane_id() == 0) {
+        int* e = xb + wv * 8;
+        e[0] = __float_as_int(cnt);
+        e[1] = vlo;
+        e[2] = vhi;
+        e[3] = lastinv;
+        e[4] = work ? 1 : 0;
+      }
+      __syncthreads();
+      if (L * Q > kWave) {
+        const int nwv = L * Q / kWave, w0 = wv & ~(nwv - 1);
+        cnt = 0.0f;
+        vlo = S;
+        vhi = -1;
+        lastinv = -1;
+        for (int j = 0; j < nwv; ++j) {
+          const int* e = xb + (w0 + j) * 8;
+          cnt = cnt + __int_as_float(e[0]);
+          vlo = min(vlo, e[1]);
+          vhi = max(vhi, e[2]);
+          lastinv = max(lastinv, e[3]);
         }
       }
-      if (v && q == 0) s_pv[gb + (rank < nl ? rank : half + rank - nl)] = (SW)((uint32_t)pm | VBIT);
-      if (live && q == 0) {
-        const bool filled = gl < half ? gl < nl : (gl - half) < nr;
-        if (!filled) s_pv[s] = (SW)fillp;
+      work = false;
+      for (int j = 0; j < Q; ++j) work = work || xb[j * 8 + 4] != 0;
+    }
+    const int ng = (int)cnt;
+    // the group argmax of (value, member index)
+    auto argmax_grp = [&](float v, int i) {
+      wave_grp_argmax<Q>(v, i, span);
+      if (L * Q > kWave) {
+        int* xb = xw.next();
+        if (lane_id() == 0) {
+          xb[wv * 8] = __float_as_int(v);
+          xb[wv * 8 + 1] = i;
+        }
+        __syncthreads();
+        const int nwv = L * Q / kWave, w0 = wv & ~(nwv - 1);
+        v = __int_as_float(xb[w0 * 8]);
+        i = xb[w0 * 8 + 1];
+        for (int j = 1; j < nwv; ++j) {
+          const float ov = __int_as_float(xb[(w0 + j) * 8]);
+          const int oi = xb[(w0 + j) * 8 + 1];
+          if (ov > v || (ov == v && oi < i)) {
+            v = ov;
+            i = oi;
+          }
+        }
       }
+      return i;
+    };
+    if (work) {
+      lt_group_row(x, cntp > 0.0f, rowx);
+      if (gl == 0 && q == 0) s_gc[g] = cnt;
+      if constexpr (local) lt_group_reduce_w<D, Q, 1>(s_x, s_gc, L, true, s_cen, lane_id(), wv);   // the means
+      else lt_group_reduce<D, NT, 1, false, 2 * kWave / Q>(s_x, s_gc, 1, L, true, s_cen, tid);
+      // a = the real key farthest from the mean, then b = the real key farthest from a: their slot rows, copied
+      // into the centroid banks, which the Lloyd outputs keep for an empty cluster and the projection reads
+      const float* pa = c0b;
+      const float* pb = c1b;
+      for (int pass = 0; pass < 2; ++pass) {
+        const float* ref = pass == 0 ? meanp : pa;
+        float bv = -1.0f;
+        int bi = 0;
+        if (live && cntp > 0.0f) {
+          bv = slice_dot<D, Q>([&](int e) { return x[e] - ref[e]; }, [&](int e) { return x[e] - ref[e]; });
+          bi = gl;
+        }
+        const int sel = argmax_grp(bv, bi);
+        float* bank = pass == 0 ? c0b : c1b;
+        const float* src = s_x + (g * L + sel) * RS + d0;
+        if (pass == 0) pa = src;
+        else pb = src;
+        if (live) {
+#pragma unroll
+          for (int d = 0; d < DQ; d += 4)
+            *reinterpret_cast<float4*>(bank + d) = *reinterpret_cast<const float4*>(src + d);
+        }
+      }
+      // Lloyd iterations: labels from the current centroids, then both clusters' sums in one reduction (into the
+      // banks c0 and c1; an empty cluster keeps its centroid)
+      for (int it = 0; it < iters; ++it) {
+        const float* r0 = it == 0 ? pa : c0b;
+        const float* r1 = it == 0 ? pb : c1b;
+        const float cc0 = slice_dot<D, Q>([&](int e) { return r0[e]; }, [&](int e) { return r0[e]; });
+        const float cc1 = slice_dot<D, Q>([&](int e) { return r1[e]; }, [&](int e) { return r1[e]; });
+        float cp0 = 0.0f, cp1 = 0.0f;
+        if (live && cntp > 0.0f) {
+          const float xx = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return x[e]; });
+          const float xc0 = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return r0[e]; });
+          const float xc1 = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return r1[e]; });
+          const float dist0 = (xx - 2.0f * xc0) + cc0, dist1 = (xx - 2.0f * xc1) + cc1;
+          if (dist1 < dist0) cp1 = 1.0f;
+          else cp0 = 1.0f;
+        }
+        if (q == 0) s_lab[m] = cp1 > 0.0f ? 2 : (cp0 > 0.0f ? 1 : 0);
+        // the clusters' counts: a partial per aligned segment of `span` lanes (a group inside a wavefront, or a
+        // group's part in one wavefront)
+        const float w0 = wave_grp<Q>(cp0, span, fadd), w1 = wave_grp<Q>(cp1, span, fadd);
+        if ((tid & (span - 1)) == 0) {
+          s_gc[kLtGroups + tid / span] = w0;
+          s_gc[2 * kLtGroups + tid / span] = w1;
+        }
+        if constexpr (local)
+          lt_group_reduce_w<D, Q, 2, true>(s_x, s_gc + kLtGroups, L, false, s_cen + kLtGroups * RS, lane_id(), wv,
+                                           s_lab);
+        else
+          lt_group_reduce<D, NT, 2, true, 2 * kWave / Q>(s_x, s_gc + kLtGroups, L * Q / span, L, false,
+                                                         s_cen + kLtGroups * RS, tid, s_lab);
+      }
+      if (iters == 0) sync();   // the banks' copies of a and b, for the projection
+    }
+    // ranks by counting, the stable order of the projections on c0 - c1
+    const int nl = (ng + 1) / 2, nr = ng - nl;
+    const bool v = live && val(m);
+    float key = kInf;
+    if (v) key = slice_dot<D, Q>([&](int e) { return x[e]; }, [&](int e) { return c0b[e] - c1b[e]; });
+    const int pm = live ? perm(m) : 0;
+    const int fillp = live && lastinv >= 0 ? perm(g * S + lastinv) : 0;
+    if (live && q == 0) s_key[m] = key;
+    sync();
+    int rank = 0;
+    if (v) {
+      for (int j = 0; j < S; ++j) {
+        const float kj = s_key[g * S + j];
+        rank += (kj < key || (kj == key && j < gl)) ? 1 : 0;
+      }
+    }
+    if (v && q == 0) s_pv[g * S + (rank < nl ? rank : half + rank - nl)] = (uint32_t)pm | VB;
+    if (live && q == 0) {
+      const bool filled = gl < half ? gl < nl : (gl - half) < nr;
+      if (!filled) s_pv[m] = (uint32_t)fillp;
     }
   };
-  int lvl = 0;
-  {   // levels with S > 64: several members per slot
-    float acc0[DQ], acc1[DQ], xd[DQ];
-    for (; lvl < nlev && (C >> lvl) > kLaneSlots; ++lvl) {
-      set_level(lvl);
-      for (int win = 0; win < nwin; ++win) window(std::false_type{}, std::false_type{}, win, xd, acc0, acc1);
-      __syncthreads();
-      TA_DMARK(lvl);
-    }
-  }
-  {   // levels with S <= 64: the next window's member row is requested while a window runs
-    float x[DQ], xn[DQ], ad[DQ];
-    for (; lvl < nlev; ++lvl) {
-      set_level(lvl);
-      if (m < C) load_row_g<T, DQ>(kb + (int64_t)perm(g * S + gl) * kst, xn);
-      for (int win = 0; win < nwin; ++win) {
-#pragma unroll
-        for (int d = 0; d < DQ; ++d) x[d] = xn[d];
-        if (win + 1 < nwin) load_row_g<T, DQ>(kb + (int64_t)perm((win + 1) * Wz + g * S + gl) * kst, xn);
-        if (L * Q <= kWave) window(std::true_type{}, std::true_type{}, win, x, ad, ad);
-        else window(std::true_type{}, std::false_type{}, win, x, ad, ad);
-      }
-      __syncthreads();
-      TA_DMARK(lvl);
-    }
-  }
-  // the leaves' node sums and counts (from the slot words), the leaf slots (in place when BIG), then the node
-  // sums and counts by adjacent pairs from the leaves up
-  const int nleaf = C / 2;
-  for (int i = m; i < nleaf; i += kLaneSlots) {
-    float x[DQ], y[DQ];
-    load_row_g<T, DQ>(kb + (int64_t)perm(2 * i) * kst, x);
-    load_row_g<T, DQ>(kb + (int64_t)perm(2 * i + 1) * kst, y);
-    const float v0 = val(2 * i) ? 1.0f : 0.0f, v1 = val(2 * i + 1) ? 1.0f : 0.0f;
-    float* row = tr.sums + (int64_t)(nleaf - 1 + i) * D + d0;
-#pragma unroll
-    for (int d = 0; d < DQ; d += 4)
-      *reinterpret_cast<float4*>(row + d) =
-          make_float4(x[d] * v0 + y[d] * v1, x[d + 1] * v0 + y[d + 1] * v1, x[d + 2] * v0 + y[d + 2] * v1,
-                      x[d + 3] * v0 + y[d + 3] * v1);
-    if (q == 0) tr.cnt[nleaf - 1 + i] = (int)val(2 * i) + (int)val(2 * i + 1);
-  }
   __syncthreads();
-  for (int c = tid; c < C; c += NT) {
-    const int32_t sl = val(c) ? perm(c) : -1;
-    tr.slot[c] = sl;
-  }
-  for (int lv = nlev - 1; lv >= 0; --lv) {
+  for (int lvl = lt_log2(C / W); lvl < nlev; ++lvl) {
+    const int S = C >> lvl;
+    float x[DQ];
+    if (live) {
+      load_row_g<T, DQ>(kb + (int64_t)perm(m) * kst, x);
+    } else {
+#pragma unroll
+      for (int d = 0; d < DQ; ++d) x[d] = 0.0f;
+    }
+    if (S * Q <= kWave) level(std::true_type{}, S, x);
+    else level(std::false_type{}, S, x);
     __syncthreads();
+  }
+  // the window's leaves (slots 2i, 2i + 1): node sums and counts, kept in LDS rows [0, W / 2) and stored
+  const int wl = W / 2, nleaf = C / 2;
+  if (m < wl) {
+    float x[DQ], y[DQ];
+    load_row_g<T, DQ>(kb + (int64_t)perm(2 * m) * kst, x);
+    load_row_g<T, DQ>(kb + (int64_t)perm(2 * m + 1) * kst, y);
+    const float v0 = val(2 * m) ? 1.0f : 0.0f, v1 = val(2 * m + 1) ? 1.0f : 0.0f;
+    float* row = tr.sums + (int64_t)(nleaf - 1 + win * wl + m) * D + d0;
+#pragma unroll
+    for (int d = 0; d < DQ; d += 4) {
+      const float4 s4 = make_float4(x[d] * v0 + y[d] * v1, x[d + 1] * v0 + y[d + 1] * v1,
+                                    x[d + 2] * v0 + y[d + 2] * v1, x[d + 3] * v0 + y[d + 3] * v1);
+      *reinterpret_cast<float4*>(row + d) = s4;
+      *reinterpret_cast<float4*>(rowx + d) = s4;
+    }
+    if (q == 0) {
+      const int c2 = (int)val(2 * m) + (int)val(2 * m + 1);
+      tr.cnt[nleaf - 1 + win * wl + m] = c2;
+      s_nc[m] = c2;
+    }
+  }
+  if (tid < W) {
+    const int32_t sl = val(tid) ? perm(tid) : -1;
+    tr.slot[base + tid] = sl;
+  }
+  // the nodes above the leaves up to the window's root, by adjacent pairs (LDS rows after the leaves' rows)
+  int cofs = 0, pofs = wl;
+  for (int lv = nlev - 1, nn = wl / 2; nn >= 1; --lv, nn >>= 1) {
+    __syncthreads();
+    const int64_t nb = ((int64_t)1 << lv) - 1 + (int64_t)win * nn;
+    for (int w = tid; w < nn * (D / 4); w += NT) {
+      const int i = w / (D / 4), d = (w - i * (D / 4)) * 4;
+      const float* a = s_x + (cofs + 2 * i) * RS + d;
+      const float4 u = *reinterpret_cast<const float4*>(a);
+      const float4 z = *reinterpret_cast<const float4*>(a + RS);
+      const float4 s4 = make_float4(u.x + z.x, u.y + z.y, u.z + z.z, u.w + z.w);
+      *reinterpret_cast<float4*>(s_x + (pofs + i) * RS + d) = s4;
+      *reinterpret_cast<float4*>(tr.sums + (nb + i) * D + d) = s4;
+    }
+    if (tid < nn) {
+      const int c2 = s_nc[cofs + 2 * tid] + s_nc[cofs + 2 * tid + 1];
+      s_nc[pofs + tid] = c2;
+      tr.cnt[nb + tid] = c2;
+    }
+    cofs = pofs;
+    pofs += nn;
+  }
+}
+
+// lanetree_top_kernel, one workgroup per tree of more than 64 slots: the node sums and counts above the windows'
+// roots, by adjacent pairs.
+template <int D, int Q>
+__global__ __launch_bounds__(kWave * Q) void lanetree_top_kernel(float* __restrict__ ws, int64_t P, int C) {
+  constexpr int NT = kWave * Q;
+  const int tid = threadIdx.x;
+  const LaneTree tr = lane_tree(ws, P, C, D, blockIdx.x);
+  for (int lv = lt_log2(C / kLaneSlots) - 1; lv >= 0; --lv) {
     const int nn = 1 << lv, base = nn - 1, cb = 2 * nn - 1;
     for (int w = tid; w < nn * (D / 4); w += NT) {
       const int i = w / (D / 4), d = (w - i * (D / 4)) * 4;
@@ -738,8 +887,8 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_build_kernel(const T* __re
           make_float4(u.x + z.x, u.y + z.y, u.z + z.z, u.w + z.w);
     }
     for (int i = tid; i < nn; i += NT) tr.cnt[base + i] = tr.cnt[cb + 2 * i] + tr.cnt[cb + 2 * i + 1];
+    __syncthreads();
   }
-  TA_DMARK(13);
 }
 
 // ----------------------------------------------------------------------------------------------------- walk
@@ -1091,17 +1240,36 @@ extern "C" int ta_lanetree_build(const void* k, int dtype, int64_t ksb, int64_t 
   }
   const int64_t P = (int64_t)B * H * (T / chunk);
   const bool big = T > kLaneLdsMaxT;
-  const size_t lds = (size_t)lt_build_lds_bytes(T, D, big);
+  const int64_t nwin = T > kLaneSlots ? T / kLaneSlots : 1;
   hipStream_t st = (hipStream_t)stream;
+  if (P * nwin * (D / kLaneDQ * kWave) > (int64_t)0xffffffff) {   // the tail launch's threads
+    set_error("ta_lanetree_build: too many lane trees for one launch (B * H * (T / chunk) * T / 64 workgroups)");
+    return TA_ERR_ARG;
+  }
+  // the levels of groups above 64 slots (a launch per level, a workgroup per group), the rest (a workgroup per
+  // window of 64 slots), then the node sums above the windows
 #define TA_LB(TT, DD)                                                                                                 \
-  if (big)                                                                                                            \
-    hipLaunchKernelGGL((lanetree_build_kernel<TT, DD, DD / kLaneDQ, true>), dim3((unsigned)P),                        \
-                       dim3(DD / kLaneDQ * kWave), lds, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, chunk,      \
-                       kmeans_iters, (float*)ws, P);                                                                  \
-  else                                                                                                                \
-    hipLaunchKernelGGL((lanetree_build_kernel<TT, DD, DD / kLaneDQ, false>), dim3((unsigned)P),                       \
-                       dim3(DD / kLaneDQ * kWave), lds, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, chunk,      \
-                       kmeans_iters, (float*)ws, P)
+  for (int lvl = 0; (T >> lvl) > kLaneSlots; ++lvl) {                                                                 \
+    const size_t lds = (size_t)lt_build_lds_bytes(T >> lvl, DD, big);                                                 \
+    if (big)                                                                                                          \
+      hipLaunchKernelGGL((lanetree_split_kernel<TT, DD, DD / kLaneDQ, true>), dim3((unsigned)(P << lvl)),             \
+                         dim3(DD / kLaneDQ * kWave), lds, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, chunk,    \
+                         kmeans_iters, (float*)ws, P, lvl);                                                           \
+    else                                                                                                              \
+      hipLaunchKernelGGL((lanetree_split_kernel<TT, DD, DD / kLaneDQ, false>), dim3((unsigned)(P << lvl)),            \
+                         dim3(DD / kLaneDQ * kWave), lds, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, chunk,    \
+                         kmeans_iters, (float*)ws, P, lvl);                                                           \
+  }                                                                                                                   \
+  if (T <= kLaneSlots)                                                                                                \
+    hipLaunchKernelGGL((lanetree_split_kernel<TT, DD, DD / kLaneDQ, false>), dim3((unsigned)P),                       \
+                       dim3(DD / kLaneDQ * kWave), (size_t)lt_build_lds_bytes(T, DD, false), st, (const TT*)k, ksb,   \
+                       ksh, kst, H, T, T / chunk, chunk, kmeans_iters, (float*)ws, P, 0);                             \
+  hipLaunchKernelGGL((lanetree_tail_kernel<TT, DD, DD / kLaneDQ>), dim3((unsigned)(P * nwin)),                        \
+                     dim3(DD / kLaneDQ * kWave), 0, st, (const TT*)k, ksb, ksh, kst, H, T, T / chunk, kmeans_iters,   \
+                     (float*)ws, P);                                                                                  \
+  if (T > kLaneSlots)                                                                                                 \
+    hipLaunchKernelGGL((lanetree_top_kernel<DD, DD / kLaneDQ>), dim3((unsigned)P), dim3(DD / kLaneDQ * kWave), 0, st, \
+                       (float*)ws, P, T)
 #define TA_LB_D(TT)                  \
   switch (D) {                       \
     case 16: TA_LB(TT, 16); break;   \
@@ -1191,4 +1359,3 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
   return check_launch("ta_lanetree_walk");
 }
 
-TA_TRACE_EXPORTS

@@ -7,13 +7,10 @@ launch follows a 1 GiB read, so its caches are as cold as inside a decode step.
     python -m treeattn_amd.phase_trace layer-attention  # config 4: seg_attend_kernel, one layer after a 32 x 32768 prefill
     python -m treeattn_amd.build --trace select.hip
     python -m treeattn_amd.phase_trace descent-append   # config 5: descend_kernel with the cache append (batch 1, 131072)
-    python -m treeattn_amd.build --trace lanetree.hip
-    python -m treeattn_amd.phase_trace lanetree-build   # the LaneTree build of bench_speed's T=4096 layer, per level
 
 Marks: the descent's 0 (set-up: position, query row, first level's node rows), 1 + 2k / 2 + 2k (level k scored /
 ranked); the layer attention's 12 (start), 13 (descent done), 14 (attention start), 15 (done); the descent
-kernel's 12 (start), 13 (cache append done), 14 (descent done); the LaneTree build's 14 (start), l (level l of
-the 2-means splits done) and 13 (the first thread done with the node sums).
+kernel's 12 (start), 13 (cache append done), 14 (descent done).
 """
 import argparse
 import ctypes
@@ -137,44 +134,14 @@ def descent_append(reps):
     _run(lib, call, B * H, reps, [12, 13, 0] + list(range(1, 11)) + [14], names)
 
 
-def lanetree_build(reps, T=4096, D=64, H=6, chunk=64):
-    """The LaneTree build of bench_speed's layer (fp16 keys, 6 heads, chunk 64, 3 Lloyd iterations): per level, the
-    time the lane trees with the most keys (the last lane of each head) spend on it, median over the heads."""
-    lib = _load('lanetree.hip')
-    from . import kernels as K
-    nl = T // chunk
-    nlev = T.bit_length() - 2
-    k = torch.randn(1, H, T, D, device='cuda', dtype=torch.float16, generator=torch.Generator(device='cuda').manual_seed(T))
-    ws = K.lanetree_build(k, chunk, 3)
-    buf = (ctypes.c_ulonglong * (4096 * 16))()
-    flush = torch.ones(1 << 28, dtype=torch.float32, device='cuda')
-    for rep in range(reps):
-        flush.sum()
-        torch.cuda.synchronize()
-        lib.ta_trace_clear()
-        K.lanetree_build(k, chunk, 3, ws)
-        torch.cuda.synchronize()
-        lib.ta_trace_read(buf)
-        tr = torch.tensor(list(buf), dtype=torch.float64).view(4096, 16)[:H * nl]
-        last = tr[[h * nl + nl - 1 for h in range(H)]]
-        marks = [14] + list(range(nlev)) + [13]
-        d = (last[:, marks[1:]] - last[:, marks[:-1]]) / 100.0   # us per level, then the node sums
-        med = d.median(0).values
-        tot = float(((last[:, 13] - last[:, 14]) / 100.0).median())
-        print('launch %d, T=%d D=%d, the last lane (%d keys): %s | node sums %.0f | total %.0f us' % (
-            rep, T, D, (nl - 1) * chunk, ' '.join('S=%d:%.0f' % (T >> l, float(med[l])) for l in range(nlev)),
-            float(med[nlev]), tot), flush=True)
-
-
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument('workload', choices=('layer-attention', 'descent-append', 'lanetree-build'))
+    ap.add_argument('workload', choices=('layer-attention', 'descent-append'))
     ap.add_argument('--reps', type=int, default=5)
     args = ap.parse_args()
     if not torch.cuda.is_available():
         raise SystemExit('phase_trace needs a GPU')
-    {'layer-attention': layer_attention, 'descent-append': descent_append,
-     'lanetree-build': lanetree_build}[args.workload](args.reps)
+    {'layer-attention': layer_attention, 'descent-append': descent_append}[args.workload](args.reps)
 
 
 if __name__ == '__main__':
