@@ -221,7 +221,7 @@ __device__ __forceinline__ void lt_label_mask(float (&p)[L], const uint8_t* lab,
       if (((w >> (8 * b)) & 0xffu) != (uint32_t)(set + 1)) p[j4 + b] = 0.0f;
   }
 }
-template <int D, int L, int NT, int NSET, bool MASK = false>
+template <int D, int L, int NT, int NSET, bool MASK = false, int GC = kLtGroups, int GB = kLtGroups>
 __device__ __forceinline__ void lt_group_outputs(const float* red, const float* gc, int nseg, bool always, float* dst,
                                                  int tid, const uint8_t* lab = nullptr) {
   constexpr int RS = D + 4, nout1 = (kLaneSlots / L) * D, nout = NSET * nout1, NU = (nout + NT - 1) / NT;
@@ -235,7 +235,7 @@ __device__ __forceinline__ void lt_group_outputs(const float* red, const float* 
     for (int j = 0; j < L; ++j) p[u][j] = in ? base[j * RS + d] : 0.0f;
     if constexpr (MASK) lt_label_mask<L>(p[u], lab, g, set);
     float cs = 0.0f;
-    for (int j = 0; j < nseg; ++j) cs = cs + (in ? gc[set * kLtGroups + g * nseg + j] : 0.0f);
+    for (int j = 0; j < nseg; ++j) cs = cs + (in ? gc[set * GC + g * nseg + j] : 0.0f);
     c[u] = cs;
   }
 #pragma unroll
@@ -249,11 +249,12 @@ __device__ __forceinline__ void lt_group_outputs(const float* red, const float* 
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
     const int o = tid + NT * u, set = o / nout1, r = o - set * nout1, g = r / D, d = r - g * D;
-    if (o < nout && (always || c[u] > 0.0f)) dst[(set * kLtGroups + g) * RS + d] = p[u][0];
+    if (o < nout && (always || c[u] > 0.0f)) dst[(set * GB + g) * RS + d] = p[u][0];
   }
 }
-// LMIN: the smallest group width L the caller passes (narrower widths are not compiled in).
-template <int D, int NT, int NSET, bool MASK = false, int LMIN = 4>
+// LMIN: the smallest group width L the caller passes (narrower widths are not compiled in); GC and GB: the strides
+// between the sets' counts (in counts) and between their banks (in rows).
+template <int D, int NT, int NSET, bool MASK = false, int LMIN = 4, int GC = kLtGroups, int GB = kLtGroups>
 __device__ __forceinline__ void lt_group_reduce(const float* red, const float* gc, int nseg, int L, bool always,
                                                 float* dst, int tid, const uint8_t* lab = nullptr) {
   __syncthreads();
@@ -266,7 +267,7 @@ __device__ __forceinline__ void lt_group_reduce(const float* red, const float* g
     case 32:
       if constexpr (LMIN <= 32) lt_group_outputs<D, 32, NT, NSET, MASK>(red, gc, nseg, always, dst, tid, lab);
       break;
-    default: lt_group_outputs<D, 64, NT, NSET, MASK>(red, gc, nseg, always, dst, tid, lab); break;
+    default: lt_group_outputs<D, 64, NT, NSET, MASK, GC, GB>(red, gc, nseg, always, dst, tid, lab); break;
   }
   __syncthreads();
 }
@@ -319,19 +320,19 @@ __device__ __forceinline__ void lt_group_reduce_w(const float* red, const float*
   wave_sync();
 }
 
-// The split launch's LDS (one group of S slots): the row area (three sets of 64 slot rows: A the mean's partials,
-// B and C the two Lloyd partials; or the group's sort keys and indices, 6 bytes per slot), the group's slots as
-// 16-bit words (key position, bit 15 set when the slot holds a real key), three centroid banks (the mean, c0,
-// c1), the cross-wavefront words and the group counts.  Above kLaneLdsMaxT slots (BIG) the slot words (32-bit:
+// The split launch's LDS (one group of S slots): the row area (two sets of 64 slot rows: the mean's partials, then
+// the two Lloyd clusters' partials, the first in the mean's set once the mean is reduced; or the group's sort keys
+// and indices, 6 bytes per slot), the group's slots as 16-bit words (key position, bit 15 set when the slot holds
+// a real key), the group's three centroids (the mean, c0, c1), the cross-wavefront words and the counts (the
+// mean's, then a partial per wavefront for each cluster).  Above kLaneLdsMaxT slots (BIG) the slot words (32-bit:
 // bit 31 the real-key bit) stay in the tree's slot array and the sort keys and indices (4 + 4 bytes per slot) go
 // to the group's part of the node-sum area ([2 g S, 2 g S + 2 S) for group g), both in HBM and unused until the
 // tail writes the node sums; the LDS then holds the rest only.
 __host__ __device__ constexpr int lt_rows_bytes(int C, int D, bool big) {
-  return !big && 6 * C > 3 * kLaneSlots * (D + 4) * 4 ? ((6 * C + 15) & ~15) : 3 * kLaneSlots * (D + 4) * 4;
+  return !big && 6 * C > 2 * kLaneSlots * (D + 4) * 4 ? ((6 * C + 15) & ~15) : 2 * kLaneSlots * (D + 4) * 4;
 }
 __host__ __device__ constexpr int lt_build_lds_bytes(int C, int D, bool big) {
-  return lt_rows_bytes(C, D, big) + (big ? 0 : ((2 * C + 15) & ~15)) + 3 * kLtGroups * (D + 4) * 4 + 2 * 64 * 4 +
-         3 * kLtGroups * 4;
+  return lt_rows_bytes(C, D, big) + (big ? 0 : ((2 * C + 15) & ~15)) + 3 * (D + 4) * 4 + 2 * 64 * 4 + 3 * 8 * 4;
 }
 
 // ---------------------------------------------------------------------------------------------------- build
@@ -346,8 +347,11 @@ __host__ __device__ constexpr int lt_build_lds_bytes(int C, int D, bool big) {
 // of the canonical sums, their rows requested U at a time); the order by a bitonic sort of (projection, index)
 // over the span of the group's real keys.  The slot words (key position, bit 31 set for a real key) go from the
 // tree's slot array into LDS and back; level 0 starts them (key j in slot j, real for 1 <= j < the lane's start).
+// (Four wavefronts per SIMD requested at D = 128 and for large trees at D = 64, for a few spilled registers: two
+// groups per CU at D = 128; measured faster there, slightly slower for D = 64 below kLaneLdsMaxT.)
 template <typename T, int D, int Q, bool BIG>
-__global__ __launch_bounds__(kWave * Q) void lanetree_split_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
+__global__ __launch_bounds__(kWave * Q) __attribute__((amdgpu_waves_per_eu(Q >= 8 || (BIG && Q >= 4) ? 4 : 1, 8)))
+void lanetree_split_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
                                                                    int64_t kst, int H, int C, int nlane, int chunk,
                                                                    int iters, float* __restrict__ ws, int64_t P,
                                                                    int lvl) {
@@ -360,13 +364,13 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_split_kernel(const T* __re
   const int gb0 = (int)(blockIdx.x - (pt << lvl)) * S;   // the group's first slot
   const LaneTree tr = lane_tree(ws, P, C, D, pt);
   const int rowsb = lt_rows_bytes(S, D, BIG);
-  float* s_rows = reinterpret_cast<float*>(s_raw);                                    // [3][64][RS]
+  float* s_rows = reinterpret_cast<float*>(s_raw);                                    // [2][64][RS]
   uint32_t* s_sk = BIG ? reinterpret_cast<uint32_t*>(tr.sums + 2 * gb0) : reinterpret_cast<uint32_t*>(s_raw);   // [S]
   SW* s_si = BIG ? reinterpret_cast<SW*>(tr.sums + 2 * gb0 + S) : reinterpret_cast<SW*>(s_raw + 4 * S);         // [S]
   SW* s_pv = BIG ? reinterpret_cast<SW*>(tr.slot + gb0) : reinterpret_cast<SW*>(s_raw + rowsb);                 // [S]
-  float* s_cen = reinterpret_cast<float*>(s_raw + rowsb + (BIG ? 0 : ((2 * S + 15) & ~15)));   // [3][16][RS]
-  LtXchg xw{reinterpret_cast<int*>(s_cen + 3 * kLtGroups * RS), 0};
-  float* s_gc = s_cen + 3 * kLtGroups * RS + 2 * 64;   // [3][16] group counts: the mean's, then the two clusters'
+  float* s_cen = reinterpret_cast<float*>(s_raw + rowsb + (BIG ? 0 : ((2 * S + 15) & ~15)));   // [3][RS]
+  LtXchg xw{reinterpret_cast<int*>(s_cen + 3 * RS), 0};
+  float* s_gc = s_cen + 3 * RS + 2 * 64;   // [3][8] counts: the mean's, then the two clusters' partials
   const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ, wv = wave_id();
   const int ln = (int)(pt % nlane);
   const int64_t bh = pt / nlane;
@@ -388,11 +392,10 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_split_kernel(const T* __re
   }
   __syncthreads();
   float* meanp = s_cen + d0;   // the group's mean, c0 and c1 (this lane's part)
-  float* c0b = s_cen + kLtGroups * RS + d0;
-  float* c1b = s_cen + 2 * kLtGroups * RS + d0;
-  float* rowA = s_rows + m * RS;   // this slot's rows of the sets A, B, C
+  float* c0b = s_cen + RS + d0;
+  float* c1b = s_cen + 2 * RS + d0;
+  float* rowA = s_rows + m * RS;   // this slot's rows: the mean's or the first cluster's (A), the second's (B)
   float* rowB = rowA + kLaneSlots * RS;
-  float* rowC = rowB + kLaneSlots * RS;
   float acc0[DQ], acc1[DQ];
   if (S > kLaneSlots) {   // (a tree of at most 64 slots only has its slot words started here)
     {
@@ -483,7 +486,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_split_kernel(const T* __re
       if (work) {
         lt_group_row(acc0, true, rowA + d0);
         if (m == 0 && q == 0) s_gc[0] = cnt;
-        lt_group_reduce<D, NT, 1, false, kLaneSlots>(s_rows, s_gc, 1, kLaneSlots, true, s_cen, tid);   // the mean
+        lt_group_reduce<D, NT, 1, false, kLaneSlots, 8, 1>(s_rows, s_gc, 1, kLaneSlots, true, s_cen, tid);   // the mean
         // a = the real key farthest from the mean, then b = the real key farthest from a (into the banks)
         for (int pass = 0; pass < 2; ++pass) {
           const float* ref = pass == 0 ? meanp : c0b;
@@ -533,16 +536,16 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_split_kernel(const T* __re
               cp0 = cp0 + 1.0f;
             }
           });
-          lt_group_row(acc0, true, rowB + d0);
-          lt_group_row(acc1, true, rowC + d0);
+          lt_group_row(acc0, true, rowA + d0);
+          lt_group_row(acc1, true, rowB + d0);
           // the clusters' counts: a partial per wavefront
           const float w0 = wave_grp<Q>(cp0, kWave, fadd), w1 = wave_grp<Q>(cp1, kWave, fadd);
           if (lane_id() == 0) {
-            s_gc[kLtGroups + wv] = w0;
-            s_gc[2 * kLtGroups + wv] = w1;
+            s_gc[8 + wv] = w0;
+            s_gc[16 + wv] = w1;
           }
-          lt_group_reduce<D, NT, 2, false, kLaneSlots>(s_rows + kLaneSlots * RS, s_gc + kLtGroups, Q, kLaneSlots,
-                                                       false, s_cen + kLtGroups * RS, tid);
+          lt_group_reduce<D, NT, 2, false, kLaneSlots, 8, 1>(s_rows, s_gc + 8, Q, kLaneSlots, false, s_cen + RS,
+                                                              tid);
         }
       }
       const int nl = (ng + 1) / 2, nr = ng - nl;
@@ -609,10 +612,11 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_split_kernel(const T* __re
 // side, the two farthest members are read from the slot rows, and the order comes from ranks by counting.
 // Then the window's node sums and counts (its leaves and the nodes above them up to the window's root) and its
 // final slots (key position, or -1).
-// (Three wavefronts per SIMD requested for D >= 64: more windows resident per CU, which the window's chain of LDS
-// round trips needs; narrower rows would spill at that register budget.)
+// (Four wavefronts per SIMD requested for D >= 64: more windows resident per CU, which the window's chain of LDS
+// round trips needs, for a few spilled registers; measured faster than three at D = 128 and at T >= 2048 for
+// D = 64.)
 template <typename T, int D, int Q>
-__global__ __launch_bounds__(kWave * Q) __attribute__((amdgpu_waves_per_eu(Q >= 4 ? 3 : 1, 8))) void lanetree_tail_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
+__global__ __launch_bounds__(kWave * Q) __attribute__((amdgpu_waves_per_eu(Q >= 4 ? 4 : 1, 8))) void lanetree_tail_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
                                                                   int64_t kst, int H, int C, int nlane, int iters,
                                                                   float* __restrict__ ws, int64_t P) {
   constexpr int RS = D + 4, DQ = kLaneDQ, NT = kWave * Q;
