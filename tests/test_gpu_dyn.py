@@ -42,6 +42,7 @@ def rnd(*shape, seed):
     (128, 256, 64, torch.float32, 3, 2, 2), (128, 16384, 4096, torch.bfloat16, 3, 1, 1),
     (64, 8192, 1024, torch.float32, 1, 1, 1), (16, 16384, 2048, torch.float16, 2, 1, 1),
     (16, 32768, 8192, torch.float32, 2, 1, 2), (64, 131072, 32768, torch.bfloat16, 3, 1, 1),
+    (16, 4, 2, torch.float32, 3, 1, 2), (32, 8, 4, torch.float32, 3, 2, 1), (64, 64, 16, torch.bfloat16, 3, 2, 2),
     (16, 262144, 131072, torch.float16, 1, 1, 1)])
 def test_lanetree_build_is_bit_exact(D, T, chunk, dtype, iters, B, H):
     """ta_lanetree_build: every lane's leaf slots, node counts and node sums equal LaneTree.__init__ of the

@@ -2,11 +2,13 @@
 // positions; lane l owns one balanced binary tree of capacity T over the keys [1, l * chunk) (the tree a
 // sequential decoder would hold when it reaches the lane), then walks through the lane's positions one at a time:
 // neighbour search over the leaves the lane's previous positions stored, beam search over the tree, store,
-// insertion of the position's key.  One workgroup per lane tree; the lane trees run in parallel.
+// insertion of the position's key.  The build runs a launch per level of groups above 64 slots (a workgroup per
+// group), then one with a workgroup per window of 64 slots for the levels below, then the node sums above the
+// windows; the walk runs a workgroup per lane tree.  The lane trees run in parallel.
 //
 // Inside a workgroup a row of D dimensions is held 16 dimensions per lane by Q = D / 16 consecutive lanes (a
-// "slot"), so the workgroup's Q wavefronts form 64 slots: 64 members of the groups being split (build) or 64
-// candidates being scored (walk) at a time.  A dot product of two rows is finished across the slot's lanes by
+// "slot"), so the workgroup's Q wavefronts form 64 slots: 64 members of the group or window being split (build)
+// or 64 candidates being scored (walk) at a time.  A dot product of two rows is finished across the slot's lanes by
 // DPP exchanges; reductions over slots run as xor butterflies inside a wavefront and through LDS across them.
 //
 // Reference functions replaced: dyntree.py:6-31 masked_two_means_order, dyntree.py:34-82 LaneTree.__init__,
@@ -988,7 +990,7 @@ __device__ __forceinline__ uint64_t lt_rank_word(bool valid, float sc, int id, i
   return ((uint64_t)(~asc) << 31) | (uint32_t)id;
 }
 
-// One workgroup per lane tree, built by lanetree_build_kernel, walking the lane's positions in order
+// One workgroup per lane tree (built by the three build launches), walking the lane's positions in order
 // (dyntree.py:148-243).  Slot j scores neighbour entry j and the level's children j and j + 64; the lanes of
 // slot 0 insert the position's key.  A workgroup barrier ends every position (the tree rows the insertion
 // wrote are read by other wavefronts at the next one).
@@ -1206,6 +1208,30 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
 
 bool lanetree_dim_ok(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
+// The current device's CU count and LDS per CU (queried once per device; 256 CUs and 64 KB if the query fails).
+int lanetree_cus() {
+  static int v[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (v[dev] == 0) {
+    int n = 0;
+    v[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return v[dev];
+}
+int64_t lanetree_lds_per_cu() {
+  static int v[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+  if (v[dev] == 0) {
+    int n = 0;
+    v[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess && n > 0
+                 ? n
+                 : 65536;
+  }
+  return v[dev];
+}
+
 int lanetree_levels(int T) {
   int lg = 0;
   while ((1 << lg) < T) ++lg;
@@ -1328,13 +1354,19 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
   p.wmax = wmax; p.wl = wl; p.Wn = nb_window; p.NS = nb_store; p.probe = nb_probe * nb_store;
   p.cap_min = nb_cap_min; p.neighbors = neighbors ? 1 : 0; p.rho = nb_rho;
   p.tree_pos = tree_pos; p.leaf_ok = leaf_ok; p.nb_pos = nb_pos; p.n_tree = n_tree; p.nb_leaves = nb_leaves;
-  // the top levels of every tree stay in LDS during the walk: as many whole levels as fit in 40 KB
-  const int rowb = (D + 4) * 4 + 4;
-  int ntop = 1;
-  while (2 * ntop + 1 <= T - 1 && (2 * ntop + 1) * rowb <= 40960) ntop = 2 * ntop + 1;
-  p.ntop = ntop;
+  // the top levels of every tree stay in LDS during the walk: as many whole levels as fit in the CU's LDS shared
+  // by the workgroups each CU holds (the trees over the CUs; 4 KB left for the kernel's own arrays), beside the
+  // leaf slots, and at least 40 KB of them (the deeper levels are the walk's slowest dependent reads)
   const bool big = T > kLaneLdsMaxT;
-  const size_t lds = (size_t)ntop * rowb + (big ? 0 : (size_t)T * 4);   // + the leaf slots
+  const int rowb = (D + 4) * 4 + 4;
+  const int64_t slots_b = big ? 0 : (int64_t)T * 4;
+  const int64_t per_cu = (p.P + lanetree_cus() - 1) / lanetree_cus();
+  int64_t budget = lanetree_lds_per_cu() / (per_cu < 1 ? 1 : per_cu) - 4096 - slots_b;
+  if (budget < 40960) budget = 40960;
+  int ntop = 1;
+  while (2 * ntop + 1 <= T - 1 && (int64_t)(2 * ntop + 1) * rowb <= budget) ntop = 2 * ntop + 1;
+  p.ntop = ntop;
+  const size_t lds = (size_t)ntop * rowb + (size_t)slots_b;   // + the leaf slots
   hipStream_t st = (hipStream_t)stream;
 #define TA_LW(TT, DD)                                                                                                 \
   if (big)                                                                                                            \

@@ -1,7 +1,8 @@
 """The LaneTree key selection of the reference's 'dyn' attention (dyntree.py of the reference) on the GPU.
 
-* LaneTree (dyntree.py:34-131): the lane trees are built by ta_lanetree_build, one workgroup per lane, with the
-  masked 2-means ordering (dyntree.py:6-31) inside it;
+* LaneTree (dyntree.py:34-131): the lane trees are built by ta_lanetree_build (a launch per level of groups above
+  64 slots with a workgroup per group, then a workgroup per 64-slot window for the levels below), with the masked
+  2-means ordering (dyntree.py:6-31) inside it;
 * select_keys (dyntree.py:148-243): ta_lanetree_walk walks every lane's positions (neighbour test, budget, beam
   search, store, insertion) on those trees.
 
