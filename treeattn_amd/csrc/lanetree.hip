@@ -992,8 +992,11 @@ __device__ __forceinline__ uint64_t lt_rank_word(bool valid, float sc, int id, i
 
 // One workgroup per lane tree (built by the three build launches), walking the lane's positions in order
 // (dyntree.py:148-243).  Slot j scores neighbour entry j and the level's children j and j + 64; the lanes of
-// slot 0 insert the position's key.  A workgroup barrier ends every position (the tree rows the insertion
-// wrote are read by other wavefronts at the next one).
+// slot 0 insert the position's key.  The barriers order LDS traffic only (lds_barrier), so the next position's
+// query and key rows, requested at a position's start, and the output stores stay in flight across them; counts
+// over the workgroup go through one LDS word per wavefront.  A position ends with wavefront 0 (the inserting
+// lanes) waiting for its stores, then a barrier: the tree rows, counts and slots the insertion wrote to the
+// workspace are read by other wavefronts at the next position.
 template <typename T, int D, int Q, bool BIG>
 __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
   constexpr int DQ = kLaneDQ, NT = kWave * Q;
@@ -1005,7 +1008,8 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
   __shared__ int32_t s_cur[kLaneMaxW];                      // the beam
   __shared__ float s_bsc[kLaneMaxW];
   __shared__ uint8_t s_bok[kLaneMaxW];
-  const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ;
+  __shared__ int s_wc[3][8];   // per-wavefront counts: matches and stored entries in the probe, first occurrences
+  const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ, wv = wave_id();
   const int64_t pt = blockIdx.x;
   const int ln = (int)(pt % p.nlane);
   const int64_t bh = pt / p.nlane;
@@ -1067,16 +1071,33 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
       }
     }
     const bool inprobe = m < p.probe;
-    const int pm = __syncthreads_count(match && inprobe && q == 0);
-    const int po = __syncthreads_count(ok0 && inprobe && q == 0);
+    {
+      const uint64_t bm = __ballot(match && inprobe && q == 0), bo = __ballot(ok0 && inprobe && q == 0);
+      if (lane_id() == 0) {
+        s_wc[0][wv] = __popcll(bm);
+        s_wc[1][wv] = __popcll(bo);
+      }
+    }
+    lds_barrier();
+    int pm = 0, po = 0;
+    for (int w = 0; w < Q; ++w) {
+      pm += s_wc[0][w];
+      po += s_wc[1][w];
+    }
     const float rate = (float)pm / fmaxf((float)po, 1.0f);
     const int cap = p.cap_min + (int)rintf((float)(p.Wn - p.cap_min) * rate);
     match = match && (m / p.NS + 1) <= cap && p.neighbors;
     if (q == 0) s_nid[m] = match ? id : -1;
-    __syncthreads();
+    lds_barrier();
     bool first = match;
     for (int e = 0; e < m && first; ++e) first = s_nid[e] != id;
-    const int nL = __syncthreads_count(first && q == 0);
+    {
+      const uint64_t bf = __ballot(first && q == 0);
+      if (lane_id() == 0) s_wc[2][wv] = __popcll(bf);
+    }
+    lds_barrier();
+    int nL = 0;
+    for (int w = 0; w < Q; ++w) nL += s_wc[2][w];
     if (m < WN && q == 0) {
       const int s0 = nd.slot[2 * id], s1 = nd.slot[2 * id + 1];
       int32_t* o = p.nb_pos + orow * 2 * WN;
@@ -1094,7 +1115,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
       s_bok[0] = nd.cnt(0) > 0;
       s_bsc[0] = 0.0f;
     }
-    __syncthreads();
+    lds_barrier();
     int wp = 1;
     for (int lv = 1; lv <= nlev; ++lv) {
       const int nch = 2 * wp;
@@ -1126,7 +1147,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
           if (q == 0) s_rw[c] = mine[r];
         }
       }
-      __syncthreads();
+      lds_barrier();
       const int w = nch < p.wmax ? nch : p.wmax;
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
@@ -1142,7 +1163,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
           }
         }
       }
-      __syncthreads();
+      lds_barrier();
       wp = w;
     }
     // ---- outputs, and the stored leaves of this position
@@ -1165,7 +1186,10 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
       s_sts[rs] = s_bsc[m];
       s_sto[rs] = s_bok[m];
     }
-    // ---- insertion of this position's key (dyntree.py:84-106) by the lanes of slot 0
+    // ---- insertion of this position's key (dyntree.py:84-106) by the lanes of slot 0, once every wavefront has
+    // read the leaf slots of its outputs (their loads returned: the output stores use them), since the key may go
+    // into one of those leaves (dyntree.py:224-241 reads the leaves' keys before the insertion)
+    lds_barrier();
     if (ins) {
       const int act = t >= 1 ? 1 : 0;
       float kva[DQ], r0[DQ];
@@ -1201,7 +1225,8 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
         nd.slot[2 * node + (s0 >= 0 ? 1 : 0)] = t;
       }
     }
-    __syncthreads();
+    if (wv == 0) wait_vmcnt_n<0>();   // the insertion's stores to the workspace are done
+    lds_barrier();
   }
   nd.copy(false, tid, NT);
 }
