@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "canon.hpp"
+#include "trace.hpp"
 
 namespace ta {
 
@@ -915,10 +916,10 @@ struct LaneWalk {
   int32_t* nb_leaves;  // (B, H, T)
 };
 
-// The nodes of a lane tree during the walk: nodes [0, ntop) (its top levels) live in LDS for the whole walk
-// (rows of stride D + 4 floats, and counts), deeper nodes in the workspace; the leaf slots (C entries) live in
-// LDS too up to kLaneLdsMaxT slots, above that (BIG) in the workspace.  A lane reads and writes its 16 dimensions
-// of a row.
+// The nodes of a lane tree during the walk: nodes [0, ntop) (its top levels, ntop = 2^ltop - 1) live in LDS for
+// the whole walk (rows of stride D + 4 floats, and counts), deeper nodes in the workspace; the leaf slots (C
+// entries) live in LDS too up to kLaneLdsMaxT slots, above that (BIG) in the workspace.  A lane reads and writes
+// its 16 dimensions of a row.
 template <int D, bool BIG>
 struct LaneNodes {
   LaneTree tr;
@@ -926,13 +927,22 @@ struct LaneNodes {
   int32_t* tcnt;
   int32_t* slot;   // the leaf slots: an LDS copy, or the workspace's when BIG
   int ntop, C;
-  __device__ __forceinline__ int cnt(int n) const { return n < ntop ? tcnt[n] : tr.cnt[n]; }
+  // Node n's count and row (this lane's 16 dimensions): L = the node is one of the LDS-held ones (n < ntop), a
+  // compile-time choice, so that every access has a known address space (an address chosen between LDS and the
+  // workspace at run time is a flat access, whose wait covers every outstanding memory operation).
+  template <bool L>
+  __device__ __forceinline__ int cnt(int n) const {
+    if constexpr (L) return tcnt[n];
+    else return tr.cnt[n];
+  }
+  template <bool L>
   __device__ __forceinline__ void set_cnt(int n, int v) const {
-    if (n < ntop) tcnt[n] = v;
+    if constexpr (L) tcnt[n] = v;
     else tr.cnt[n] = v;
   }
+  template <bool L>
   __device__ __forceinline__ void row(int n, int d0, float (&r)[kLaneDQ]) const {
-    if (n < ntop) {
+    if constexpr (L) {
       const float* src = top + n * (D + 4) + d0;
 #pragma unroll
       for (int d = 0; d < kLaneDQ; d += 4) {
@@ -946,18 +956,12 @@ struct LaneNodes {
       load_row_g<float, kLaneDQ>(tr.sums + (int64_t)n * D + d0, r);
     }
   }
+  template <bool L>
   __device__ __forceinline__ void set_row(int n, int d0, const float (&r)[kLaneDQ]) const {
-    if (n < ntop) {
-      float* dst = top + n * (D + 4) + d0;
+    float* dst = L ? top + n * (D + 4) + d0 : tr.sums + (int64_t)n * D + d0;
 #pragma unroll
-      for (int d = 0; d < kLaneDQ; d += 4)
-        *reinterpret_cast<float4*>(dst + d) = make_float4(r[d], r[d + 1], r[d + 2], r[d + 3]);
-    } else {
-      float* dst = tr.sums + (int64_t)n * D + d0;
-#pragma unroll
-      for (int d = 0; d < kLaneDQ; d += 4)
-        *reinterpret_cast<float4*>(dst + d) = make_float4(r[d], r[d + 1], r[d + 2], r[d + 3]);
-    }
+    for (int d = 0; d < kLaneDQ; d += 4)
+      *reinterpret_cast<float4*>(dst + d) = make_float4(r[d], r[d + 1], r[d + 2], r[d + 3]);
   }
   // workspace -> LDS (to_lds) or back
   __device__ __forceinline__ void copy(bool to_lds, int tid, int nt) const {
@@ -1009,6 +1013,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
   __shared__ float s_bsc[kLaneMaxW];
   __shared__ uint8_t s_bok[kLaneMaxW];
   __shared__ int s_wc[3][8];   // per-wavefront counts: matches and stored entries in the probe, first occurrences
+  __shared__ float s_isc[kLaneSlots];   // the insertion's candidate scores
   const int tid = threadIdx.x, m = tid / Q, q = tid % Q, d0 = q * DQ, wv = wave_id();
   const int64_t pt = blockIdx.x;
   const int ln = (int)(pt % p.nlane);
@@ -1028,17 +1033,24 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
   nd.copy(true, tid, NT);
   __syncthreads();
   const int WN = p.Wn * p.NS, wl = p.wl, nlev = p.nlev;
+  const int ltop = lt_log2(p.ntop + 1);   // levels 0 .. ltop - 1 are held in LDS
   const float kInf = __int_as_float(0x7f800000);
   const int start = ln * p.chunk;
-  const bool ins = tid < Q;   // the lanes of slot 0 insert the keys
-  float qn[DQ], kn[DQ];       // the next position's query and key, requested while the current position runs
+  const bool ins = tid < Q;    // the lanes of slot 0 (the root's update, the leaf slot)
+  const bool insw = wv == 0;   // wavefront 0 inserts the keys
+  float qn[DQ], kn[DQ];        // the next position's query and key, requested while the current position runs
   load_row_g<T, DQ>(qb + (int64_t)start * p.qst, qn);
 #pragma unroll
   for (int d = 0; d < DQ; ++d) kn[d] = 0.0f;
-  if (ins) load_row_g<T, DQ>(kb + (int64_t)start * p.kst, kn);
+  if (insw) load_row_g<T, DQ>(kb + (int64_t)start * p.kst, kn);
   for (int i = 0; i < p.chunk; ++i) {
     const int t = start + i;
     const int64_t orow = bh * p.T + t;
+    // phase marks (trace.hpp) of the lane's last position: 0 start, 1 neighbours scored and counted, 2 first
+    // occurrences counted, 3 search started, 4 + l level l + 1 ranked (l < 8), 12 outputs, 13 insertion started,
+    // 14 insertion done (wavefront 0), 15 position done
+    const bool mk = i == p.chunk - 1;
+    if (mk) TA_DMARK(0);
     float qv[DQ], kd[DQ];
 #pragma unroll
     for (int d = 0; d < DQ; ++d) {
@@ -1047,7 +1059,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
     }
     if (i + 1 < p.chunk) {
       load_row_g<T, DQ>(qb + (int64_t)(t + 1) * p.qst, qn);
-      if (ins) load_row_g<T, DQ>(kb + (int64_t)(t + 1) * p.kst, kn);
+      if (insw) load_row_g<T, DQ>(kb + (int64_t)(t + 1) * p.kst, kn);
     }
     // ---- neighbours: the leaves the last Wn positions of the lane stored, re-scored on the current tree
     int id = 0;
@@ -1060,13 +1072,17 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
         id = s_stl[rs];
         if (ok0) {
           const int node = (1 << nlev) - 1 + id;
-          const int cn = nd.cnt(node);
-          float row[DQ];
-          nd.row(node, d0, row);
-          const float sc = slice_dot<D, Q>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) /
-                           (float)(cn > 1 ? cn : 1);
-          const float base = s_sts[rs];
-          match = cn > 0 && sc >= base - p.rho * fabsf(base);
+          auto score = [&](auto lds) {
+            constexpr bool L = decltype(lds)::value;
+            const int cn = nd.template cnt<L>(node);
+            float row[DQ];
+            nd.template row<L>(node, d0, row);
+            const float sc = slice_dot<D, Q>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) /
+                             (float)(cn > 1 ? cn : 1);
+            const float base = s_sts[rs];
+            return cn > 0 && sc >= base - p.rho * fabsf(base);
+          };
+          match = nlev < ltop ? score(std::true_type{}) : score(std::false_type{});
         }
       }
     }
@@ -1084,6 +1100,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
       pm += s_wc[0][w];
       po += s_wc[1][w];
     }
+    if (mk) TA_DMARK(1);
     const float rate = (float)pm / fmaxf((float)po, 1.0f);
     const int cap = p.cap_min + (int)rintf((float)(p.Wn - p.cap_min) * rate);
     match = match && (m / p.NS + 1) <= cap && p.neighbors;
@@ -1098,6 +1115,7 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
     lds_barrier();
     int nL = 0;
     for (int w = 0; w < Q; ++w) nL += s_wc[2][w];
+    if (mk) TA_DMARK(2);
     if (m < WN && q == 0) {
       const int s0 = nd.slot[2 * id], s1 = nd.slot[2 * id + 1];
       int32_t* o = p.nb_pos + orow * 2 * WN;
@@ -1112,12 +1130,14 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
     // ---- beam search from the root
     if (tid == 0) {
       s_cur[0] = 0;
-      s_bok[0] = nd.cnt(0) > 0;
+      s_bok[0] = nd.template cnt<true>(0) > 0;
       s_bsc[0] = 0.0f;
     }
     lds_barrier();
+    if (mk) TA_DMARK(3);
     int wp = 1;
-    for (int lv = 1; lv <= nlev; ++lv) {
+    auto search_level = [&](auto lds, int lv) __attribute__((always_inline)) {
+      constexpr bool L = decltype(lds)::value;
       const int nch = 2 * wp;
       int cid[2];
       bool cv[2];
@@ -1135,9 +1155,9 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
           cid[r] = 2 * s_cur[par] + (c < wp ? 0 : 1);
           if (s_bok[par]) {
             const int node = (1 << lv) - 1 + cid[r];
-            const int cn = nd.cnt(node);
+            const int cn = nd.template cnt<L>(node);
             float row[DQ];
-            nd.row(node, d0, row);
+            nd.template row<L>(node, d0, row);
             cv[r] = cn > 0;
             if (cv[r])
               sc[r] = slice_dot<D, Q>([&](int e) { return qv[e]; }, [&](int e) { return row[e]; }) /
@@ -1164,8 +1184,12 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
         }
       }
       lds_barrier();
+      if (mk && lv <= 8) TA_DMARK(3 + lv);
       wp = w;
-    }
+    };
+    int lv = 1;
+    for (; lv <= nlev && lv < ltop; ++lv) search_level(std::true_type{}, lv);
+    for (; lv <= nlev; ++lv) search_level(std::false_type{}, lv);
     // ---- outputs, and the stored leaves of this position
     if (m < wl && q == 0) {
       const int lid = s_cur[m];
@@ -1186,47 +1210,85 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
       s_sts[rs] = s_bsc[m];
       s_sto[rs] = s_bok[m];
     }
-    // ---- insertion of this position's key (dyntree.py:84-106) by the lanes of slot 0, once every wavefront has
-    // read the leaf slots of its outputs (their loads returned: the output stores use them), since the key may go
-    // into one of those leaves (dyntree.py:224-241 reads the leaves' keys before the insertion)
+    if (mk) TA_DMARK(12);
+    // ---- insertion of this position's key (dyntree.py:84-106) by wavefront 0, once every wavefront has read the
+    // leaf slots of its outputs (their loads returned: the output stores use them), since the key may go into one of
+    // those leaves (dyntree.py:224-241 reads the leaves' keys before the insertion).  Each step scores, one slot
+    // each, all 2 + 4 + ... + 2^kk nodes of the next kk levels below the current node (kk <= KI: as many as the
+    // wavefront's 64 / Q slots hold), then follows the path through them: at each level the right child when its
+    // score is greater (dyntree.py:94-101; the scores use the rows and counts before the insertion, which
+    // changes only the path's nodes), and the path's slots add the key to their node.
     lds_barrier();
-    if (ins) {
+    if (mk) TA_DMARK(13);
+    if (wv == 0) {
+      constexpr int KI = Q == 1 ? 5 : Q == 2 ? 4 : Q == 4 ? 3 : 2;   // 2^(KI + 1) - 2 <= 64 / Q
       const int act = t >= 1 ? 1 : 0;
-      float kva[DQ], r0[DQ];
+      float kva[DQ];
 #pragma unroll
       for (int d = 0; d < DQ; ++d) kva[d] = kd[d] * (act ? 1.0f : 0.0f);
-      nd.row(0, d0, r0);
+      if (ins) {
+        float r0[DQ];
+        nd.template row<true>(0, d0, r0);
 #pragma unroll
-      for (int d = 0; d < DQ; ++d) r0[d] = r0[d] + kva[d];
-      nd.set_row(0, d0, r0);
-      if (q == 0) nd.set_cnt(0, nd.cnt(0) + act);
-      int node = 0;
-      for (int lv = 0; lv < nlev; ++lv) {
-        const int base = (2 << lv) - 1, lc = 2 * node, cap = p.C >> (lv + 1);
-        const int cL = nd.cnt(base + lc), cR = nd.cnt(base + lc + 1);
-        float xL[DQ], xR[DQ];
-        nd.row(base + lc, d0, xL);
-        nd.row(base + lc + 1, d0, xR);
-        const float dL = slice_dot<D, Q>([&](int e) { return kd[e]; }, [&](int e) { return xL[e]; });
-        const float dR = slice_dot<D, Q>([&](int e) { return kd[e]; }, [&](int e) { return xR[e]; });
-        float sL = cL == 0 ? -1e9f : dL / (float)(cL > 1 ? cL : 1);
-        float sR = cR == 0 ? -1e9f : dR / (float)(cR > 1 ? cR : 1);
-        if (cL >= cap) sL = -kInf;
-        if (cR >= cap) sR = -kInf;
-        const bool right = sR > sL;
-        node = lc + (right ? 1 : 0);
-#pragma unroll
-        for (int d = 0; d < DQ; ++d) xL[d] = (right ? xR[d] : xL[d]) + kva[d];
-        nd.set_row(base + node, d0, xL);
-        if (q == 0) nd.set_cnt(base + node, (right ? cR : cL) + act);
+        for (int d = 0; d < DQ; ++d) r0[d] = r0[d] + kva[d];
+        nd.template set_row<true>(0, d0, r0);
+        if (q == 0) nd.template set_cnt<true>(0, nd.template cnt<true>(0) + act);
       }
-      if (q == 0 && act) {
+      int node = 0;   // index within its level of the path's node at level lv
+      auto ins_step = [&](auto lds, int lv, int kk) __attribute__((always_inline)) {
+        constexpr bool L = decltype(lds)::value;
+        const bool on = m < (2 << kk) - 2;
+        const int dep = 31 - __clz(m + 2), ci = m + 2 - (1 << dep);   // this slot's node: depth dep, index ci
+        const int lvc = lv + dep, id = (1 << lvc) - 1 + (node << dep) + ci;
+        int cn = 0;
+        float row[DQ];
+#pragma unroll
+        for (int d = 0; d < DQ; ++d) row[d] = 0.0f;
+        if (on) {
+          cn = nd.template cnt<L>(id);
+          nd.template row<L>(id, d0, row);
+        }
+        const float dt = slice_dot<D, Q>([&](int e) { return kd[e]; }, [&](int e) { return row[e]; });
+        float sc = cn == 0 ? -1e9f : dt / (float)(cn > 1 ? cn : 1);
+        if (cn >= (p.C >> lvc)) sc = -kInf;
+        if (on && q == 0) s_isc[m] = sc;
+        wave_sync();
+        int pi = 0;   // the path's index at depth dd
+        bool onpath = false;
+        for (int dd = 1; dd <= kk; ++dd) {
+          const int l = (1 << dd) - 2 + 2 * pi;
+          pi = 2 * pi + (s_isc[l + 1] > s_isc[l] ? 1 : 0);
+          onpath = onpath || (on && dep == dd && ci == pi);
+        }
+        if (onpath) {
+#pragma unroll
+          for (int d = 0; d < DQ; ++d) row[d] = row[d] + kva[d];
+          nd.template set_row<L>(id, d0, row);
+          if (q == 0) nd.template set_cnt<L>(id, cn + act);
+        }
+        node = (node << kk) + pi;
+        wave_sync();   // the scores are read before the next step writes them
+      };
+      int il = 0;   // the path's level; steps never span the last LDS level and the first workspace one
+      while (il < nlev && il + 1 < ltop) {
+        const int kk = min(KI, min(nlev, ltop - 1) - il);
+        ins_step(std::true_type{}, il, kk);
+        il += kk;
+      }
+      while (il < nlev) {
+        const int kk = min(KI, nlev - il);
+        ins_step(std::false_type{}, il, kk);
+        il += kk;
+      }
+      if (tid == 0 && act) {
         const int s0 = nd.slot[2 * node];
         nd.slot[2 * node + (s0 >= 0 ? 1 : 0)] = t;
       }
     }
+    if (mk) TA_DMARK(14);
     if (wv == 0) wait_vmcnt_n<0>();   // the insertion's stores to the workspace are done
     lds_barrier();
+    if (mk) TA_DMARK(15);
   }
   nd.copy(false, tid, NT);
 }
@@ -1420,3 +1482,4 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
   return check_launch("ta_lanetree_walk");
 }
 
+TA_TRACE_EXPORTS

@@ -7,10 +7,14 @@ launch follows a 1 GiB read, so its caches are as cold as inside a decode step.
     python -m treeattn_amd.phase_trace layer-attention  # config 4: seg_attend_kernel, one layer after a 32 x 32768 prefill
     python -m treeattn_amd.build --trace select.hip
     python -m treeattn_amd.phase_trace descent-append   # config 5: descend_kernel with the cache append (batch 1, 131072)
+    python -m treeattn_amd.build --trace lanetree.hip
+    python -m treeattn_amd.phase_trace lanetree-walk    # the LaneTree walk of bench_speed's layer (T=512), one position
 
 Marks: the descent's 0 (set-up: position, query row, first level's node rows), 1 + 2k / 2 + 2k (level k scored /
 ranked); the layer attention's 12 (start), 13 (descent done), 14 (attention start), 15 (done); the descent
-kernel's 12 (start), 13 (cache append done), 14 (descent done).
+kernel's 12 (start), 13 (cache append done), 14 (descent done); the LaneTree walk's, for each lane's last position,
+0 (start), 1 (neighbours scored and counted), 2 (first occurrences counted), 3 (search started), 4 + l (level l + 1
+ranked), 12 (outputs written), 13 (insertion started), 14 (insertion done), 15 (position done).
 """
 import argparse
 import ctypes
@@ -134,14 +138,47 @@ def descent_append(reps):
     _run(lib, call, B * H, reps, [12, 13, 0] + list(range(1, 11)) + [14], names)
 
 
+def lanetree_walk(reps, T=512, D=64, H=6, chunk=64):
+    """The LaneTree walk of bench_speed's layer (fp16, 6 heads, chunk 64, wmax 8, beam 4, neighbours 8 x 2): the
+    phases of each lane's last position, relative to its start (us; min/median/max over the lanes)."""
+    lib = _load('lanetree.hip')
+    from . import kernels as K
+    from .config import Config
+    cfg = Config(seq_len=T, n_head=H, n_embd=H * D, attn='dyn', chunk=chunk, wmax=8, beam=4, beam_mode='fixed')
+    g = torch.Generator(device='cuda').manual_seed(T)
+    q, k = (torch.randn(1, H, T, D, device='cuda', dtype=torch.float16, generator=g) for _ in range(2))
+    lhat = torch.full((1, H, T), 4, dtype=torch.long, device='cuda')
+    ws0 = K.lanetree_build(k, chunk, 3)
+    ws = ws0.clone()
+    buf = (ctypes.c_ulonglong * (4096 * 16))()
+    nwg = H * (T // chunk)
+    nlev = T.bit_length() - 2
+    marks = [0, 1, 2, 3] + [4 + l for l in range(min(nlev, 8))] + [12, 13, 14, 15]
+    names = {0: 'start', 1: 'neighbours', 2: 'counted', 3: 'search'}
+    names.update({4 + l: 'L%d' % (l + 1) for l in range(8)})
+    names.update({12: 'outputs', 13: 'ins start', 14: 'ins done', 15: 'end'})
+    for rep in range(reps):
+        ws.copy_(ws0)
+        torch.cuda.synchronize()
+        lib.ta_trace_clear()
+        K.lanetree_walk(q, k, lhat, ws, cfg)
+        torch.cuda.synchronize()
+        lib.ta_trace_read(buf)
+        tr = torch.tensor(list(buf), dtype=torch.float64).view(4096, 16)[:nwg]
+        rel = (tr - tr[:, :1]) / 100.0
+        print('launch %d: ' % rep + ' | '.join('%s %.2f/%.2f/%.2f' % (names[m], rel[:, m].min(), rel[:, m].median(),
+                                                                     rel[:, m].max()) for m in marks), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument('workload', choices=('layer-attention', 'descent-append'))
+    ap.add_argument('workload', choices=('layer-attention', 'descent-append', 'lanetree-walk'))
     ap.add_argument('--reps', type=int, default=5)
     args = ap.parse_args()
     if not torch.cuda.is_available():
         raise SystemExit('phase_trace needs a GPU')
-    {'layer-attention': layer_attention, 'descent-append': descent_append}[args.workload](args.reps)
+    {'layer-attention': layer_attention, 'descent-append': descent_append,
+     'lanetree-walk': lanetree_walk}[args.workload](args.reps)
 
 
 if __name__ == '__main__':
