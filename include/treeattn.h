@@ -189,6 +189,21 @@ int ta_gather_dot_blocks(const void* q, const void* K, int dtype,
                          float scale, float* out, void* stream);
 
 /*
+ * Candidate list of the module forward, masked (replaces fastseg.py:367-381 and attention_dyn.py:74-86: the
+ * concatenation of tree, neighbour and static keys, their validity, and dedupe_fast / attention_dyn.py:12-17,
+ * the first valid copy of each position).  Per query row (B,H,N): tree_pos (leaf * wl positions, entry r * wl
+ * + j = position r of found leaf j, -1 = none), leaf_ok (wl bytes), n_tree (leaves to use), nb_pos (nbk
+ * positions), all int64 / uint8 and contiguous; tq: the rows' positions, (N) or (B,N) when tq_batched, int64.
+ * The candidates are tree_pos, nb_pos, then 0, t, t-1, ..., t-Lw+1 (Lw = max(local, 3); negatives -1) and, for
+ * leaf > 2, the query's own leaf group up to t; KC = leaf * wl + nbk + 1 + Lw (+ leaf), at most 320.  cm:
+ * (B,H,N,KC) int32, the position where kept, else -1 (what ta_sparse_attn_fwd takes); counts: (B,H,N,4) int32:
+ * kept entries, kept tree entries, kept neighbour entries, leaves used (found and within n_tree).
+ */
+int ta_assemble_candidates(const int64_t* tree_pos, const uint8_t* leaf_ok, const int64_t* n_tree,
+                           const int64_t* nb_pos, const int64_t* tq, int tq_batched, int B, int H, int N, int wl,
+                           int leaf, int nbk, int local, int32_t* cm, int32_t* counts, void* stream);
+
+/*
  * Softmax attention of each query over an explicit candidate list (replaces fastseg.py:173-177
  * sparse_attn forward, its kernel fastseg.py:50-78 and the fallback fastseg.py:134-141).
  * q: (B,H,T,D), k, v: (B,H,Tk,D), same dtype; cand: (B,H,T,KC) int32 contiguous, -1 = unused, duplicates

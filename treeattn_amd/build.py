@@ -20,6 +20,7 @@ HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
 
 SOURCES = {
     'abi.hip': [],
+    'cand.hip': [],
     'select.hip': ['-ffp-contract=off'],
     'attend.hip': [],
     'attend_static.hip': [],

@@ -551,6 +551,37 @@ def forest_descend(q, sums, perm, block, wmax, bq_desc, bq_use=None, levels=Fals
     return leaf, leafv, cand, lv
 
 
+CAND_MAX = 320   # candidates per row that ta_assemble_candidates takes
+
+
+def candidate_width(wl, leaf, nbk, local):
+    """Candidates per row of the module forward: tree leaves' keys, neighbour keys, static keys, own leaf group."""
+    return leaf * wl + nbk + 1 + max(local, 3) + (leaf if leaf > 2 else 0)
+
+
+def assemble_candidates(sel, tq, local, leaf, b, H):
+    """The module forward's masked candidate list in one launch (fastseg.py:367-381 with dedupe_fast,
+    attention_dyn.py:12-17 and 74-86): sel the selection dict (tree_pos (b,H,N,leaf wl), leaf_ok (b,H,N,wl),
+    n_tree, nb_pos (b,H,N,nbk)), tq (N,) or (b,N) the rows' positions.  Returns cm (b,H,N,KC) int32, the position
+    where the entry is the first valid copy of it, else -1, and counts (b,H,N,4) int32: kept entries, kept tree
+    entries, kept neighbour entries, leaves used."""
+    tree_pos = sel['tree_pos'].to(torch.int64).contiguous()
+    leaf_ok = sel['leaf_ok'].to(torch.bool).contiguous()
+    n_tree = sel['n_tree'].to(torch.int64).contiguous()
+    nb_pos = sel['nb_pos'].to(torch.int64).contiguous()
+    tq = tq.to(torch.int64).contiguous()
+    L.require_gpu(tree_pos, leaf_ok, n_tree, nb_pos, tq)
+    N, wl, nbk = tree_pos.shape[2], leaf_ok.shape[-1], nb_pos.shape[-1]
+    if tree_pos.shape[-1] != leaf * wl or tuple(tree_pos.shape[:3]) != (b, H, N):
+        raise ValueError('assemble_candidates: tree_pos must be (b, H, N, leaf * wl)')
+    KC = candidate_width(wl, leaf, nbk, local)
+    cm = torch.empty(b, H, N, KC, dtype=torch.int32, device=tree_pos.device)
+    counts = torch.empty(b, H, N, 4, dtype=torch.int32, device=tree_pos.device)
+    L.call('ta_assemble_candidates', L.ptr(tree_pos), L.ptr(leaf_ok), L.ptr(n_tree), L.ptr(nb_pos), L.ptr(tq),
+           1 if tq.dim() == 2 else 0, b, H, N, wl, leaf, nbk, int(local), L.ptr(cm), L.ptr(counts), L.stream())
+    return cm, counts
+
+
 def sparse_attn_fwd(q, k, v, cand, scale):
     """Softmax attention over candidate positions (-1 unused) into k, v (b,H,Tk,dh) or a PagedCache (as k).
     Returns (out (b,H,T,dh) in the values' dtype, lse (b,H,T))."""

@@ -212,6 +212,18 @@ def attend(q, k, v, lhat, cfg, scale=None):
                    keys_nb=torch.zeros((), device=q.device), nb_leaves=sel['nb_leaves'].float().mean(),
                    leaves_used=nused.mean())
         return out, aux, sel, None
+    if K.candidate_width(wl, leaf, NBK, cfg.local) <= K.CAND_MAX:
+        # the masked candidate list and its counts in one launch (the same list and statistics as below)
+        cm, counts = K.assemble_candidates(sel, tq, cfg.local, leaf, b, H)
+        if grad:
+            from . import fastseg as FS
+            out = FS.sparse_attn(q, k, v, cm, scale, causal=True)
+        else:
+            out, _ = K.sparse_attn_fwd(q, k, v, cm, scale)
+        c = counts.float().mean((0, 1, 2))
+        aux = dict(keys_total=c[0], keys_tree=c[1], keys_nb=c[2], nb_leaves=sel['nb_leaves'].float().mean(),
+                   leaves_used=c[3])
+        return out, aux, sel, None
     cand, keep, used = assemble(sel, tq, cfg, b, H)
     cm = torch.where(keep, cand, torch.full_like(cand, -1))
     if grad:
