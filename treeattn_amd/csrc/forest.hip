@@ -170,8 +170,10 @@ __global__ __launch_bounds__(kWave) void forest_build_kernel(const T* __restrict
   }
 }
 
-// The same build for a head size of 128 (forest_build_kernel holds five D-vectors per lane): a workgroup of
-// Q = D / 16 wavefronts per block, key i held 16 dimensions per lane by lanes [Q i, Q i + Q).  The member sums
+// The same build with a workgroup of Q = D / 16 wavefronts per block, key i held 16 dimensions per lane by lanes
+// [Q i, Q i + Q): the build for head sizes 32, 64 and 128 (forest_build_kernel, one wavefront per block with a
+// whole key per lane, would hold five D-vectors per lane at 128, and at 64 and 32 its 64 or 32 sequential
+// per-dimension sums per group are a longer chain than Q lanes' 16: 0.161 -> 0.111 ms for bench_speed's layer).  The member sums
 // are the same halving trees (member i + member i + S/2 first, ...) and the node sums the same adjacent pairs:
 // a step whose partner lies in another wavefront goes through LDS, the others are xor exchanges; dot products
 // are canon_dot's value finished across the Q lanes of a key.  The results equal the one-wavefront kernel's
@@ -670,8 +672,14 @@ extern "C" int ta_forest_build(const void* k, int dtype, int64_t ksb, int64_t ks
 #define TA_FB_D(TT)                                                                                          \
   switch (D) {                                                                                               \
     case 16: TA_FB(TT, 16); break;                                                                           \
-    case 32: TA_FB(TT, 32); break;                                                                           \
-    case 64: TA_FB(TT, 64); break;                                                                           \
+    case 32:                                                                                                 \
+      hipLaunchKernelGGL((forest_build_wide_kernel<TT, 32>), grid, dim3(2 * kWave), 0, st, (const TT*)k, ksb,  \
+                         ksh, kst, H, nb, block, depth, kmeans_iters, gate, perm, lv);                       \
+      break;                                                                                                 \
+    case 64:                                                                                                 \
+      hipLaunchKernelGGL((forest_build_wide_kernel<TT, 64>), grid, dim3(4 * kWave), 0, st, (const TT*)k, ksb,  \
+                         ksh, kst, H, nb, block, depth, kmeans_iters, gate, perm, lv);                       \
+      break;                                                                                                 \
     default:                                                                                                 \
       hipLaunchKernelGGL((forest_build_wide_kernel<TT, 128>), grid, dim3(8 * kWave), 0, st, (const TT*)k, ksb, \
                          ksh, kst, H, nb, block, depth, kmeans_iters, gate, perm, lv);                       \
