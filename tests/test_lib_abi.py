@@ -48,6 +48,12 @@ def test_library_rejects_bad_arguments_without_gpu():
                            64, 200, 0.1, None, 0, 0, 0, None, None, 1, None, 0, None, None)
     assert rc == 2
     assert b'local window' in L.ta_last_error()
+    # candidate rows wider than 320 entries (leaf 4 x 64 leaves + 128 neighbour keys + 4 static keys + 4 own keys)
+    import ctypes
+    one = ctypes.c_void_p(8)   # never dereferenced: the sizes are refused first
+    rc = L.ta_assemble_candidates(one, one, one, one, one, 0, 1, 1, 8, 64, 4, 128, 3, one, one, None)
+    assert rc == 1
+    assert b'at most 320 candidates' in L.ta_last_error()
 
 
 def test_product_refuses_cpu_tensors():
