@@ -18,6 +18,27 @@ int check_launch(const char* what) {
   return TA_OK;
 }
 
+static int device_attribute(hipDeviceAttribute_t attr, int (&cache)[64]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, attr, dev) != hipSuccess || n <= 0) return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+int device_cus() {
+  static int cache[64] = {0};
+  return device_attribute(hipDeviceAttributeMultiprocessorCount, cache);
+}
+
+int device_lds_per_cu() {
+  static int cache[64] = {0};
+  return device_attribute(hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, cache);
+}
+
 }  // namespace ta
 
 extern "C" int ta_abi_version(void) { return TA_ABI_VERSION; }

@@ -203,6 +203,10 @@ __device__ __forceinline__ float wave_sum(float x) {
 // ----------------------------------------------------------------------------------------- host helpers
 void set_error(const std::string& msg);
 int check_launch(const char* what);
+// The current device's compute-unit count and LDS bytes per compute unit (queried once per device; 0 if the
+// query fails).
+int device_cus();
+int device_lds_per_cu();
 int gather_blocks_mfma(const void* q, const void* K, int dtype, int64_t qsb, int64_t qsh, int64_t qsn, int64_t ksb,
                        int64_t ksh, int64_t ksn, const int32_t* blk, int B, int H, int N, int M, int NB, int block, int D,
                        float scale, float* out, void* stream);

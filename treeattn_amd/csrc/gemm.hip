@@ -267,7 +267,6 @@ int rowmm_narrow(MmArgs a, int nc, bool ln, int epilogue, hipStream_t st);
 }
 
 namespace {
-int device_cus();
 
 // Columns per output tile of the narrow-tile kernel: the narrowest tile (of 4, 8, 16, 32 columns) whose
 // workgroups all fit on the compute units at once (one per unit: a workgroup of the LayerNorm variant takes
@@ -398,22 +397,6 @@ extern "C" int ta_rowmm_ex(const void* X, int64_t ldx, const void* W, int64_t ld
 #undef TA_LAUNCH
   return check_launch("rowmm_kernel");
 }
-
-namespace {
-
-int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
-}  // namespace
 
 // workspace: [counter | 252 B | keys: one per workgroup and row (at most one workgroup per column tile)]
 extern "C" int64_t ta_logits_workspace_size(int M, int N) {

@@ -1295,30 +1295,6 @@ __global__ __launch_bounds__(kWave * Q) void lanetree_walk_kernel(LaneWalk p) {
 
 bool lanetree_dim_ok(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
-// The current device's CU count and LDS per CU (queried once per device; 256 CUs and 64 KB if the query fails).
-int lanetree_cus() {
-  static int v[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (v[dev] == 0) {
-    int n = 0;
-    v[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
-  }
-  return v[dev];
-}
-int64_t lanetree_lds_per_cu() {
-  static int v[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
-  if (v[dev] == 0) {
-    int n = 0;
-    v[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess && n > 0
-                 ? n
-                 : 65536;
-  }
-  return v[dev];
-}
-
 int lanetree_levels(int T) {
   int lg = 0;
   while ((1 << lg) < T) ++lg;
@@ -1447,8 +1423,9 @@ extern "C" int ta_lanetree_walk(const void* q, const void* k, int dtype, int64_t
   const bool big = T > kLaneLdsMaxT;
   const int rowb = (D + 4) * 4 + 4;
   const int64_t slots_b = big ? 0 : (int64_t)T * 4;
-  const int64_t per_cu = (p.P + lanetree_cus() - 1) / lanetree_cus();
-  int64_t budget = lanetree_lds_per_cu() / (per_cu < 1 ? 1 : per_cu) - 4096 - slots_b;
+  const int cus = device_cus() > 0 ? device_cus() : 256, lds_cu = device_lds_per_cu() > 0 ? device_lds_per_cu() : 65536;
+  const int64_t per_cu = (p.P + cus - 1) / cus;
+  int64_t budget = lds_cu / (per_cu < 1 ? 1 : per_cu) - 4096 - slots_b;
   if (budget < 40960) budget = 40960;
   int ntop = 1;
   while (2 * ntop + 1 <= T - 1 && (int64_t)(2 * ntop + 1) * rowb <= budget) ntop = 2 * ntop + 1;
