@@ -523,9 +523,9 @@ struct ForestDesc {
 template <typename T, int D>
 __global__ __launch_bounds__(256) void forest_descend_kernel(ForestDesc p) {
   constexpr int R = D / 16;
-  __shared__ float s_sc[4][kForestMaxRoots];
-  __shared__ int32_t s_id[4][kForestMaxRoots];
-  __shared__ uint8_t s_v[4][kForestMaxRoots];
+  __shared__ __align__(16) float s_sc[4][kForestMaxRoots];
+  __shared__ __align__(16) int32_t s_id[4][kForestMaxRoots];
+  __shared__ __align__(16) uint8_t s_v[4][kForestMaxRoots];
   __shared__ int32_t s_kid[4][kForestMaxW];
   __shared__ uint8_t s_kv[4][kForestMaxW];
   const int wv = wave_id(), lane = lane_id();
@@ -550,13 +550,22 @@ __global__ __launch_bounds__(256) void forest_descend_kernel(ForestDesc p) {
   int w = 0;
   for (int l = 0; l <= p.depth; ++l) {
     const float* base = p.sums[l] + b * p.sb[l] + h * p.sh[l] + R * j16;
-    for (int c0 = 0; c0 < C; c0 += 4) {
-      const int c = c0 + g;
-      const int cid = id[c < C ? c : 0];
-      float rows[R];
-      load_row_g<float, R>(base + (int64_t)cid * D, rows);
-      const float s = canon_dot<R>(qr, rows);
-      if (c < C && j16 == 0) sc[c] = vv[c] ? s : -INFINITY;
+    // four candidates at a time (a 16-lane group each), the rows of eight such steps requested before the
+    // first is scored
+    constexpr int U = 8;
+    for (int c0 = 0; c0 < C; c0 += 4 * U) {
+      float rows[U][R];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + 4 * u + g;
+        load_row_g<float, R>(base + (int64_t)id[c < C ? c : 0] * D, rows[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + 4 * u + g;
+        const float s = canon_dot<R>(qr, rows[u]);
+        if (c < C && j16 == 0) sc[c] = vv[c] ? s : -INFINITY;
+      }
     }
     if (p.lv_cur != nullptr) {
       const int64_t o = ((int64_t)l * gridDim.y * p.T + qflat) * p.lv_stride;
@@ -572,13 +581,22 @@ __global__ __launch_bounds__(256) void forest_descend_kernel(ForestDesc p) {
       const int ii = id[c];
       const bool vi = vv[c] != 0;
       int rank = 0;
-      for (int e = 0; e < C; ++e) {
-        const bool ve = vv[e] != 0;
-        bool better;
-        if (ve != vi) better = ve;
-        else if (vi) better = sc[e] > si || (sc[e] == si && id[e] < ii);
-        else better = e < c;
-        rank += better ? 1 : 0;
+      for (int e0 = 0; e0 < C; e0 += 4) {   // four entries per LDS read (the arrays hold kForestMaxRoots)
+        const float4 s4 = *reinterpret_cast<const float4*>(sc + e0);
+        const int4 i4 = *reinterpret_cast<const int4*>(id + e0);
+        const uint32_t v4 = *reinterpret_cast<const uint32_t*>(vv + e0);
+        const float se[4] = {s4.x, s4.y, s4.z, s4.w};
+        const int ie[4] = {i4.x, i4.y, i4.z, i4.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int e = e0 + k;
+          const bool ve = ((v4 >> (8 * k)) & 0xffu) != 0;
+          bool better;
+          if (ve != vi) better = ve;
+          else if (vi) better = se[k] > si || (se[k] == si && ie[k] < ii);
+          else better = e < c;
+          rank += (better && e < C) ? 1 : 0;
+        }
       }
       if (rank < w) {
         s_kid[wv][rank] = ii;
