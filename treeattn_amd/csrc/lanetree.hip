@@ -642,8 +642,11 @@ __global__ __launch_bounds__(kWave * Q) __attribute__((amdgpu_waves_per_eu(Q >= 
   const LaneTree tr = lane_tree(ws, P, C, D, pt);
   const bool live = m < W;   // C < 64: slots past the tree sit out
   const float kInf = __int_as_float(0x7f800000);
+  TA_DMARK(0);   // phase marks (trace.hpp): 0 start; level k (from the first): 1 + 3k statistics exchanged,
+                 // 2 + 3k Lloyd iterations done, 3 + 3k laid out
   if (tid < W) s_pv[tid] = (uint32_t)tr.slot[base + tid];
   LtXchg xw{s_xwb, 0};
+  [[maybe_unused]] int mk = 0;   // the level's first mark
   auto perm = [&](int s) { return (int)(s_pv[s] & (VB - 1)); };
   auto val = [&](int s) { return (s_pv[s] & VB) != 0; };
   auto fadd = [](float a, float b) { return a + b; };
@@ -705,6 +708,7 @@ __global__ __launch_bounds__(kWave * Q) __attribute__((amdgpu_waves_per_eu(Q >= 
       work = false;
       for (int j = 0; j < Q; ++j) work = work || xb[j * 8 + 4] != 0;
     }
+    if (mk < 16) TA_DMARK(mk);
     const int ng = (int)cnt;
     // the group argmax of (value, member index)
     auto argmax_grp = [&](float v, int i) {
@@ -791,6 +795,7 @@ __global__ __launch_bounds__(kWave * Q) __attribute__((amdgpu_waves_per_eu(Q >= 
       }
       if (iters == 0) sync();   // the banks' copies of a and b, for the projection
     }
+    if (mk + 1 < 16) TA_DMARK(mk + 1);
     // ranks by counting, the stable order of the projections on c0 - c1
     const int nl = (ng + 1) / 2, nr = ng - nl;
     const bool v = live && val(m);
@@ -823,9 +828,11 @@ __global__ __launch_bounds__(kWave * Q) __attribute__((amdgpu_waves_per_eu(Q >= 
 #pragma unroll
       for (int d = 0; d < DQ; ++d) x[d] = 0.0f;
     }
+    mk = 1 + 3 * (lvl - lt_log2(C / W));
     if (S * Q <= kWave) level(std::true_type{}, S, x);
     else level(std::false_type{}, S, x);
     __syncthreads();
+    if (mk + 2 < 16) TA_DMARK(mk + 2);
   }
   // the window's leaves (slots 2i, 2i + 1): node sums and counts, kept in LDS rows [0, W / 2) and stored
   const int wl = W / 2, nleaf = C / 2;

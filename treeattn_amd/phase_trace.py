@@ -9,12 +9,15 @@ launch follows a 1 GiB read, so its caches are as cold as inside a decode step.
     python -m treeattn_amd.phase_trace descent-append   # config 5: descend_kernel with the cache append (batch 1, 131072)
     python -m treeattn_amd.build --trace lanetree.hip
     python -m treeattn_amd.phase_trace lanetree-walk    # the LaneTree walk of bench_speed's layer (T=512), one position
+    python -m treeattn_amd.phase_trace lanetree-tail    # the LaneTree build's window launch (T=4096), per level
 
 Marks: the descent's 0 (set-up: position, query row, first level's node rows), 1 + 2k / 2 + 2k (level k scored /
 ranked); the layer attention's 12 (start), 13 (descent done), 14 (attention start), 15 (done); the descent
 kernel's 12 (start), 13 (cache append done), 14 (descent done); the LaneTree walk's, for each lane's last position,
 0 (start), 1 (neighbours scored and counted), 2 (first occurrences counted), 3 (search started), 4 + l (level l + 1
-ranked), 12 (outputs written), 13 (insertion started), 14 (insertion done), 15 (position done).
+ranked), 12 (outputs written), 13 (insertion started), 14 (insertion done), 15 (position done); the LaneTree
+build's window launch (lanetree_tail_kernel), 0 (start) and for its k-th level 1 + 3k (statistics exchanged), 2 + 3k
+(Lloyd iterations done), 3 + 3k (laid out).
 """
 import argparse
 import ctypes
@@ -170,15 +173,43 @@ def lanetree_walk(reps, T=512, D=64, H=6, chunk=64):
                                                                      rel[:, m].max()) for m in marks), flush=True)
 
 
+def lanetree_tail(reps, T=4096, D=64, H=6, chunk=64):
+    """The LaneTree build's window launch of bench_speed's layer (fp16, 6 heads, chunk 64, 3 Lloyd iterations): for
+    the first 4096 windows (head 0, every lane), when each level's phases end (us from the window's start;
+    min/median/max over the windows with keys)."""
+    lib = _load('lanetree.hip')
+    from . import kernels as K
+    k = torch.randn(1, H, T, D, device='cuda', dtype=torch.float16, generator=torch.Generator(device='cuda').manual_seed(T))
+    ws = K.lanetree_build(k, chunk, 3)
+    buf = (ctypes.c_ulonglong * (4096 * 16))()
+    flush = torch.ones(1 << 28, dtype=torch.float32, device='cuda')
+    names = {0: 'start'}
+    for lv in range(5):
+        names.update({1 + 3 * lv: 'L%d stats' % lv, 2 + 3 * lv: 'L%d lloyd' % lv, 3 + 3 * lv: 'L%d done' % lv})
+    for rep in range(reps):
+        flush.sum()
+        torch.cuda.synchronize()
+        lib.ta_trace_clear()
+        K.lanetree_build(k, chunk, 3, ws)
+        torch.cuda.synchronize()
+        lib.ta_trace_read(buf)
+        tr = torch.tensor(list(buf), dtype=torch.float64).view(4096, 16)
+        tr = tr[tr[:, 15] > 0]
+        rel = (tr - tr[:, :1]) / 100.0
+        print('launch %d (%d windows): ' % (rep, tr.shape[0]) + ' | '.join(
+            '%s %.2f/%.2f/%.2f' % (names[m], rel[:, m].min(), rel[:, m].median(), rel[:, m].max()) for m in range(16)),
+            flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument('workload', choices=('layer-attention', 'descent-append', 'lanetree-walk'))
+    ap.add_argument('workload', choices=('layer-attention', 'descent-append', 'lanetree-walk', 'lanetree-tail'))
     ap.add_argument('--reps', type=int, default=5)
     args = ap.parse_args()
     if not torch.cuda.is_available():
         raise SystemExit('phase_trace needs a GPU')
     {'layer-attention': layer_attention, 'descent-append': descent_append,
-     'lanetree-walk': lanetree_walk}[args.workload](args.reps)
+     'lanetree-walk': lanetree_walk, 'lanetree-tail': lanetree_tail}[args.workload](args.reps)
 
 
 if __name__ == '__main__':
