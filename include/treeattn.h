@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TA_ABI_VERSION 2
+#define TA_ABI_VERSION 3
 
 enum ta_dtype { TA_F32 = 0, TA_F16 = 1, TA_BF16 = 2 };
 
@@ -634,13 +634,15 @@ int ta_forest_build(const void* k, int dtype, int64_t ksb, int64_t ksh, int64_t 
  * earlier blocks) | the two keys of every used leaf, all first keys then all second keys], -1 where unused; a
  * leaf is used when valid and its rank is below bq_use[b, h, t] (bq_use NULL: every valid leaf); a key equal to
  * a valid static key is dropped.  lv_cur / lv_cv (NULL or (depth + 1, B, H, T, lv_stride)): every level's
- * candidates and their validity (-1 / 0 past the level's count), for the routing loss.  wl, Kc and the widest
- * level: ta_forest_shape.
+ * candidates and their validity (-1 / 0 past the level's count), for the routing loss.  counts (NULL or
+ * (B, H, T, 2) int32): each row's valid static keys and tree keys (the counts behind attention.py:135-137's
+ * statistics, from the kernel that writes the row).  wl, Kc and the widest level: ta_forest_shape.
  */
 int ta_forest_descend(const void* q, int dtype, int64_t qsb, int64_t qsh, int64_t qst, int B, int H, int T, int D,
                       int block, const float* const* sums, const int64_t* sb, const int64_t* sh,
                       const int32_t* perm, int wmax, int bq_desc, const int32_t* bq_use, int32_t* leaf,
-                      uint8_t* leafv, int32_t* cand, int32_t* lv_cur, uint8_t* lv_cv, int lv_stride, void* stream);
+                      uint8_t* leafv, int32_t* cand, int32_t* lv_cur, uint8_t* lv_cv, int lv_stride,
+                      int32_t* counts, void* stream);
 
 /* Leaves per query (wl), candidate-list width (Kc = block + 3 + 2 wl) and widest level of ta_forest_descend. */
 int ta_forest_shape(int T, int block, int wmax, int* wl, int* kc, int* widest);

@@ -85,11 +85,15 @@ def test_forest_descend_is_bit_exact(kw):
         assert (lv[0][lvl][..., W:] == -1).all()
     # a budget cut per query: the tree keys of leaves ranked at or past it are dropped
     use = torch.randint(0, 5, (2, 2, 256), generator=torch.Generator().manual_seed(7))
+    counts = torch.full((2, 2, 256, 2), -7, dtype=torch.int32, device=DEV)
     _, _, cand_u, _ = K.forest_descend(q.to(DEV), [s.to(DEV) for s in sums], perm.to(DEV).to(torch.int32), B, cfg.wmax,
-                                       bq, bq_use=use.to(DEV))
+                                       bq, bq_use=use.to(DEV), counts=counts)
     wl = wleaf.shape[-1]
     wcand_u, _, _, _ = FR.forest_candidates(wleaf, wleafv & (torch.arange(wl) < use.unsqueeze(-1)), perm, B, 256)
     assert torch.equal(cand_u.cpu().long(), wcand_u)
+    # the row counts behind the module's statistics: valid static keys, valid tree keys
+    assert torch.equal(counts[..., 0].cpu().long(), (wcand_u[..., B:B + 3] >= 0).sum(-1))
+    assert torch.equal(counts[..., 1].cpu().long(), (wcand_u[..., B + 3:] >= 0).sum(-1))
 
 
 CFGS = [dict(), dict(gate=True), dict(beam_mode='pred', global_pool=True), dict(beam_mode='pred', global_pool=True,

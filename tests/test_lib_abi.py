@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for n in declared_functions():
         assert hasattr(L, n), n
     assert set(_lib.SIGNATURES) == set(declared_functions())
-    assert L.ta_abi_version() == 2
+    assert L.ta_abi_version() == 3
 
 
 def test_library_rejects_bad_arguments_without_gpu():

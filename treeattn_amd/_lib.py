@@ -130,7 +130,7 @@ SIGNATURES = {
                                 c_f32, c_f32, c_vp, _P(c_vp), _P(c_vp), _P(c_i64), _P(c_i64), c_vp]),
     'ta_forest_descend': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, _P(c_vp),
                                   _P(c_i64), _P(c_i64), c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32,
-                                  c_vp]),
+                                  c_vp, c_vp]),
     'ta_forest_shape': (c_i32, [c_i32, c_i32, c_i32, _P(c_i32), _P(c_i32), _P(c_i32)]),
     'ta_lanetree_workspace_size': (c_i32, [c_i32, c_i32, c_i32, c_i32, c_i32, _P(c_i64)]),
     'ta_lanetree_build': (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp,

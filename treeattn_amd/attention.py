@@ -92,9 +92,11 @@ class TreeAttention(nn.Module):
         # (3) + (5) the descent and the candidate list with every found leaf; the budget cuts the tree keys
         want_levels = self.training and cfg.route_weight > 0
         bq_desc = cfg.wmax if pred_mode else cfg.beam
+        # fixed budget: the attended list is the full one, so the kernel counts its keys for the statistics
+        counts = None if pred_mode else torch.empty(b, H, T, 2, device=dev, dtype=torch.int32)
         with torch.no_grad():
             leaf, leafv, cand_full, lv = K.forest_descend(q.detach(), sums, perm, B, cfg.wmax, bq_desc,
-                                                          levels=want_levels)
+                                                          levels=want_levels, counts=counts)
         wl = leaf.shape[-1]
         tree_full = cand_full[..., B + 3:]
         if pred_mode:
@@ -108,11 +110,15 @@ class TreeAttention(nn.Module):
         # (6) exact attention over own block + static keys + tree keys
         out = sparse_attn(q, k, v, cand, scale, causal=True)
 
-        tvalid = cand[..., B + 3:] >= 0
-        tcount = tvalid.sum(-1).float()
-        sv = cand[..., B:B + 3] >= 0
+        # attention.py:135-137: tree keys per query past the first block, and all keys (own block, static, tree)
+        if counts is not None:
+            cf = counts.float()
+            tcount, svsum = cf[..., 1], cf[..., 0]
+        else:
+            tcount = (cand[..., B + 3:] >= 0).sum(-1).float()
+            svsum = (cand[..., B:B + 3] >= 0).float().sum(-1)
         self.aux['keys_tree'] = tcount[:, :, B:].mean().detach()
-        self.aux['keys_total'] = ((t % B + 1).float().mean() + sv.float().sum(-1).mean() + tcount.mean()).detach()
+        self.aux['keys_total'] = ((B + 1) / 2.0 + svsum.mean() + tcount.mean()).detach()
         if self.training:
             self._training_signals(q, k, v, cand, cand_full, leaf, lv, perm, plog, depth)
         return out

@@ -515,6 +515,7 @@ struct ForestDesc {
   int32_t* lv_cur;          // (depth + 1, B, H, T, lv_stride) candidates of every level, or null
   uint8_t* lv_cv;
   int lv_stride;
+  int32_t* counts;          // (B, H, T, 2): the row's valid static keys and tree keys, or null
 };
 
 // One wavefront per query (attention.py:93-148): score the roots of all blocks (valid: the blocks before the
@@ -632,6 +633,7 @@ __global__ __launch_bounds__(256) void forest_descend_kernel(ForestDesc p) {
   }
   const int use = p.bq_use != nullptr ? p.bq_use[qflat] : wl;
   const int32_t* pr = p.perm + (int64_t)bh * p.nb * p.Bk;
+  int ntree = 0;
   for (int c = lane; c < 2 * wl; c += kWave) {
     const int i = c < wl ? c : c - wl;
     int key = -1;
@@ -642,6 +644,14 @@ __global__ __launch_bounds__(256) void forest_descend_kernel(ForestDesc p) {
       key = dup ? -1 : kk;
     }
     cr[p.Bk + 3 + c] = key;
+    ntree += key >= 0 ? 1 : 0;
+  }
+  if (p.counts != nullptr) {
+    for (int o = 32; o >= 1; o >>= 1) ntree += __shfl_xor(ntree, o, kWave);
+    if (lane == 0) {
+      p.counts[qflat * 2] = (int)v0 + (int)v1 + (int)v2;
+      p.counts[qflat * 2 + 1] = ntree;
+    }
   }
 }
 
@@ -731,7 +741,7 @@ extern "C" int ta_forest_descend(const void* q, int dtype, int64_t qsb, int64_t 
                                  int D, int block, const float* const* sums, const int64_t* sb, const int64_t* sh,
                                  const int32_t* perm, int wmax, int bq_desc, const int32_t* bq_use, int32_t* leaf,
                                  uint8_t* leafv, int32_t* cand, int32_t* lv_cur, uint8_t* lv_cv, int lv_stride,
-                                 void* stream) {
+                                 int32_t* counts, void* stream) {
   if (B <= 0 || H <= 0 || T <= 0 || block < 4 || block > kWave || (block & (block - 1)) || T % block ||
       !forest_dim_ok(D) || wmax < 1 || wmax > kForestMaxW || T / block > kForestMaxRoots || q == nullptr ||
       sums == nullptr || perm == nullptr || leaf == nullptr || leafv == nullptr || cand == nullptr ||
@@ -774,7 +784,7 @@ extern "C" int ta_forest_descend(const void* q, int dtype, int64_t qsb, int64_t 
     p.sh[l] = sh[l];
   }
   p.perm = perm; p.bq_use = bq_use; p.leaf = leaf; p.leafv = leafv; p.cand = cand;
-  p.lv_cur = lv_cur; p.lv_cv = lv_cv; p.lv_stride = lv_stride;
+  p.lv_cur = lv_cur; p.lv_cv = lv_cv; p.lv_stride = lv_stride; p.counts = counts;
   const dim3 grid((unsigned)((T + 3) / 4), B * H);
   hipStream_t st = (hipStream_t)stream;
 #define TA_FD(TT, DD) hipLaunchKernelGGL((forest_descend_kernel<TT, DD>), grid, dim3(256), 0, st, p)

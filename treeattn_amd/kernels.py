@@ -520,10 +520,11 @@ def forest_build(k, block, kmeans_iters, gate=False, gate_q=0.25, gate_temp=0.3)
     return perm, sums
 
 
-def forest_descend(q, sums, perm, block, wmax, bq_desc, bq_use=None, levels=False):
+def forest_descend(q, sums, perm, block, wmax, bq_desc, bq_use=None, levels=False, counts=None):
     """Beam descent over the block trees and the attention's candidate list (attention.py:88-148).  q (B,H,T,D);
     sums / perm from forest_build; bq_desc: leaves kept valid per level (an int); bq_use (B,H,T) the leaves used
-    per query, or None.  Returns (leaf (B,H,T,wl) int32, leafv bool, cand (B,H,T,Kc) int32, per-level
+    per query, or None; counts: None, or a (B,H,T,2) int32 tensor the kernel fills with each row's valid static
+    keys and tree keys.  Returns (leaf (B,H,T,wl) int32, leafv bool, cand (B,H,T,Kc) int32, per-level
     (candidates, validity) or None)."""
     L.require_gpu(q, perm, *sums)
     B, H, T, D = q.shape
@@ -547,7 +548,7 @@ def forest_descend(q, sums, perm, block, wmax, bq_desc, bq_use=None, levels=Fals
            L.i64_array([t.stride(0) for t in sums]), L.i64_array([t.stride(1) for t in sums]),
            L.ptr(perm.contiguous()), int(wmax), int(bq_desc), L.ptr(use), L.ptr(leaf), L.ptr(leafv), L.ptr(cand),
            L.ptr(lv[0]) if lv else ctypes.c_void_p(0), L.ptr(lv[1]) if lv else ctypes.c_void_p(0),
-           wide if lv else 0, L.stream())
+           wide if lv else 0, L.ptr(counts), L.stream())
     return leaf, leafv, cand, lv
 
 
