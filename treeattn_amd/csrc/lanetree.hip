@@ -200,6 +200,76 @@ __device__ __forceinline__ void lt_bitonic_sort(uint32_t* key, IW* idx, int n2, 
   }
 }
 
+// The same sort with the pairs in registers: n2 = E * (workgroup size), thread t holding entries [t E, t E + E) as
+// (key << 32 | index).  Each step of the network exchanges within a thread (distance below E), between lanes of
+// a wavefront (below 64 E) or through the LDS arrays (the rest, a few steps); the arrays hold the sorted pairs
+// at the end.
+template <int J, int E>
+__device__ __forceinline__ void lt_reg_step(uint64_t (&v)[E], int k, int i0) {
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    if ((e & J) == 0) {
+      const bool asc = ((i0 + e) & k) == 0;
+      const uint64_t a = v[e], b = v[e | J];
+      const bool sw = (a > b) == asc;
+      v[e] = sw ? b : a;
+      v[e | J] = sw ? a : b;
+    }
+  }
+}
+template <int E, typename IW>
+__device__ __forceinline__ void lt_bitonic_sort_reg(uint32_t* key, IW* idx, int tid, int nt) {
+  static_assert(E >= 2 && E <= 16 && (E & (E - 1)) == 0, "2 to 16 pairs per thread");
+  const int n2 = E * nt, i0 = tid * E;
+  uint64_t v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = ((uint64_t)key[i0 + e] << 32) | (uint32_t)idx[i0 + e];
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < E) {
+        switch (j) {
+          case 1: lt_reg_step<1, E>(v, k, i0); break;
+          case 2: if constexpr (E > 2) lt_reg_step<2, E>(v, k, i0); break;
+          case 4: if constexpr (E > 4) lt_reg_step<4, E>(v, k, i0); break;
+          default: if constexpr (E > 8) lt_reg_step<8, E>(v, k, i0); break;
+        }
+      } else if (j < E * kWave) {
+        const int m = j / E;
+        const bool lower = (tid & m) == 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int hi = __shfl_xor((int)(v[e] >> 32), m, kWave), lo = __shfl_xor((int)(uint32_t)v[e], m, kWave);
+          const uint64_t o = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+          const bool keepmin = lower == (((i0 + e) & k) == 0);
+          v[e] = keepmin ? (o < v[e] ? o : v[e]) : (o > v[e] ? o : v[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          key[i0 + e] = (uint32_t)(v[e] >> 32);
+          idx[i0 + e] = (IW)(uint32_t)v[e];
+        }
+        __syncthreads();
+        const bool lower = (i0 & j) == 0;   // j >= 64 E: the same for the thread's E entries
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int pi = (i0 + e) ^ j;
+          const uint64_t o = ((uint64_t)key[pi] << 32) | (uint32_t)idx[pi];
+          const bool keepmin = lower == (((i0 + e) & k) == 0);
+          v[e] = keepmin ? (o < v[e] ? o : v[e]) : (o > v[e] ? o : v[e]);
+        }
+        __syncthreads();
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    key[i0 + e] = (uint32_t)(v[e] >> 32);
+    idx[i0 + e] = (IW)(uint32_t)v[e];
+  }
+  __syncthreads();
+}
+
 // Canonical sums of the groups of L consecutive slots (64 / L groups, L in {4, ..., 64}), for NSET sets of slot
 // rows at once.  Each slot writes its partial (lt_group_row: this lane's 16 dimensions) into its row of a set
 // (64 rows of stride D + 4), and the group's member count is left in gc as nseg partial counts per group (set s,
@@ -348,8 +418,9 @@ __host__ __device__ constexpr int lt_build_lds_bytes(int C, int D, bool big) {
 // lanetree_split_kernel, one launch per level whose groups hold more than 64 slots and one workgroup per group
 // (the groups of a level touch disjoint slots): workgroup slot j holds members j, j + 64, j + 128, ... (partial j
 // of the canonical sums, their rows requested U at a time); the order by a bitonic sort of (projection, index)
-// over the span of the group's real keys.  The slot words (key position, bit 31 set for a real key) go from the
-// tree's slot array into LDS and back; level 0 starts them (key j in slot j, real for 1 <= j < the lane's start).
+// over the span of the group's real keys (its pairs in registers, 2 to 16 per thread, when the span fits).  The
+// slot words (key position, bit 31 set for a real key) go from the tree's slot array into LDS and back; level 0
+// starts them (key j in slot j, real for 1 <= j < the lane's start).
 // (Four wavefronts per SIMD requested at D = 128 and for large trees at D = 64, for a few spilled registers: two
 // groups per CU at D = 128; measured faster there, slightly slower for D = 64 below kLaneLdsMaxT.)
 template <typename T, int D, int Q, bool BIG>
@@ -573,7 +644,17 @@ void lanetree_split_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
           s_si[r] = (SW)r;
         }
         __syncthreads();
-        lt_bitonic_sort(s_sk, s_si, n2, tid, NT);
+        if constexpr (!BIG) {   // the pairs in registers, 2 to 16 per thread
+          switch (n2 / NT) {
+            case 2: lt_bitonic_sort_reg<2>(s_sk, s_si, tid, NT); break;
+            case 4: lt_bitonic_sort_reg<4>(s_sk, s_si, tid, NT); break;
+            case 8: lt_bitonic_sort_reg<8>(s_sk, s_si, tid, NT); break;
+            case 16: lt_bitonic_sort_reg<16>(s_sk, s_si, tid, NT); break;
+            default: lt_bitonic_sort(s_sk, s_si, n2, tid, NT); break;
+          }
+        } else {
+          lt_bitonic_sort(s_sk, s_si, n2, tid, NT);
+        }
       }
       // layout: sorted ranks [0, nl) to the left half, [nl, ng) to the right half (phase A rewrites each entry as
       // (position, key position) -- one 32-bit word, or the index and key words when BIG -- before phase B moves
