@@ -43,12 +43,15 @@ def rnd(*shape, seed):
     (64, 8192, 1024, torch.float32, 1, 1, 1), (16, 16384, 2048, torch.float16, 2, 1, 1),
     (16, 32768, 8192, torch.float32, 2, 1, 2), (64, 131072, 32768, torch.bfloat16, 3, 1, 1),
     (16, 4, 2, torch.float32, 3, 1, 2), (32, 8, 4, torch.float32, 3, 2, 1), (64, 64, 16, torch.bfloat16, 3, 2, 2),
-    (16, 262144, 131072, torch.float16, 1, 1, 1)])
+    (16, 262144, 131072, torch.float16, 1, 1, 1), (32, 2048, 256, torch.float16, 3, 1, 2),
+    (64, 4096, 512, torch.float16, 3, 1, 1)])
 def test_lanetree_build_is_bit_exact(D, T, chunk, dtype, iters, B, H):
     """ta_lanetree_build: every lane's leaf slots, node counts and node sums equal LaneTree.__init__ of the
     oracle's canonical mode (dyntree.py:34-82) on the same keys, up to the largest head size (D = 128) and tree
     (T = 262144) the kernel takes; above T = 16384 the build keeps its slot state in the workspace, and config 5's
-    131072-token context is one of those."""
+    131072-token context is one of those.  Groups whose key span sorts with 2 to 16 pairs per thread take the
+    register sort (every such width at head sizes 16, 32, 64 and 128 among these shapes), wider ones the LDS
+    sort."""
     print('case', D, T, chunk, dtype, iters, B, H, flush=True)
     nl = T // chunk
     k = rnd(B, H, T, D, seed=T + D).to(dtype)
