@@ -36,15 +36,18 @@ def random_sel(b, H, N, wl, leaf, Wn, NS, seed, T=None):
 
 @pytest.mark.parametrize('b,H,N,wl,leaf,Wn,NS,local,batched', [
     (2, 3, 64, 8, 2, 8, 2, 3, False), (1, 2, 128, 4, 2, 4, 2, 1, False), (2, 2, 96, 6, 4, 3, 2, 5, True),
-    (1, 1, 200, 64, 2, 8, 8, 3, False), (1, 2, 80, 3, 8, 2, 1, 3, True), (3, 1, 17, 2, 2, 1, 1, 0, False)])
+    (1, 1, 200, 64, 2, 8, 8, 3, False), (1, 2, 80, 3, 8, 2, 1, 3, True), (3, 1, 17, 2, 2, 1, 1, 0, False),
+    (2, 2, 40, 4, 4, 0, 1, 3, False), (1, 1, 1, 2, 2, 1, 1, 3, True)])
 def test_candidates_equal_torch_assembly(b, H, N, wl, leaf, Wn, NS, local, batched):
+    """Element for element and count for count, including rows without neighbour entries (Wn = 0) and a single
+    query."""
     print('case', b, H, N, wl, leaf, Wn, NS, local, batched, flush=True)
     sel = random_sel(b, H, N, wl, leaf, Wn, NS, seed=N + wl)
     if batched:
         tq = torch.arange(N).view(1, N).repeat(b, 1) + torch.arange(b).view(b, 1) * 3
     else:
         tq = torch.arange(N)
-    cfg = Config(leaf=leaf, local=local, nb_window=Wn, nb_store=NS, wmax=max(wl, 2), beam=2)
+    cfg = Config(leaf=leaf, local=local, nb_window=max(Wn, 1), nb_store=NS, wmax=max(wl, 2), beam=2)
     seld = {n: x.to(DEV) for n, x in sel.items()}
     cand, keep, used = SEL.assemble(seld, tq.to(DEV), cfg, b, H)
     want = torch.where(keep, cand, torch.full_like(cand, -1)).to(torch.int32)
