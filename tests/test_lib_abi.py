@@ -54,6 +54,16 @@ def test_library_rejects_bad_arguments_without_gpu():
     rc = L.ta_assemble_candidates(one, one, one, one, one, 0, 1, 1, 8, 64, 4, 128, 3, one, one, None)
     assert rc == 1
     assert b'at most 320 candidates' in L.ta_last_error()
+    # LaneTree workspace: T a power of two in [4, 262144], chunk dividing T, head size 16 / 32 / 64 / 128
+    nb = ctypes.c_int64(0)
+    assert L.ta_lanetree_workspace_size(1, 6, 131072, 64, 4096, ctypes.byref(nb)) == 0
+    assert nb.value == 6 * 32 * 131072 * (64 * 4 + 8)
+    assert L.ta_lanetree_workspace_size(2, 3, 4096, 128, 64, ctypes.byref(nb)) == 0
+    assert nb.value == 2 * 3 * 64 * 4096 * (128 * 4 + 8)
+    for bad in [(1, 1, 100, 64, 4), (1, 1, 524288, 64, 4096), (1, 1, 4096, 48, 64), (1, 1, 4096, 64, 48),
+                (1, 1, 2, 16, 1), (0, 1, 4096, 64, 64)]:
+        assert L.ta_lanetree_workspace_size(*bad, ctypes.byref(nb)) == 1, bad
+        assert b'ta_lanetree_workspace_size' in L.ta_last_error()
 
 
 def test_product_refuses_cpu_tensors():
