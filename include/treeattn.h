@@ -399,6 +399,18 @@ int ta_logits(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, i
               float ln_eps, int M, int N, int K, int64_t* tok_out, void* ws, int64_t ws_bytes, void* stream);
 
 /*
+ * The float32 decode step's row products for a few rows (replaces engine.py:168-177 at float32: F.linear(ln_1(x),
+ * c_attn), x + F.linear(y, c_proj), F.gelu(F.linear(ln_2(x), c_fc)), x + F.linear(h, c_mlp), F.linear(ln_f(x),
+ * wte)), one launch each:
+ *   Y[M,N] = epilogue(LN(X)[M,K] . W[N,K]^T), LN applied when ln_w != NULL (eps ln_eps, no bias), epilogue 0
+ *   none, 1 exact GELU, 2 + R[M,N] (R may be Y).
+ * 1 <= M <= 8, K <= 2048, float32, rows contiguous with strides ldx, ldw, ldy, ldr (elements); X must not
+ * overlap Y.  Float32 sums in the kernel's order (within float32 rounding of the framework's products).
+ */
+int ta_rowvec_f32(const float* X, int64_t ldx, const float* W, int64_t ldw, float* Y, int64_t ldy, const float* R,
+                  int64_t ldr, const float* ln_w, float ln_eps, int M, int N, int K, int epilogue, void* stream);
+
+/*
  * Row-wise argmax for greedy decoding (replaces logits.argmax(-1) of the reference's greedy loop,
  * phase2.py:51-66): out[r] = the first index of the largest value of x[r, 0:n].  x: rows of n elements of
  * dtype with row stride `stride`; out: int64.

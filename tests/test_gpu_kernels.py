@@ -735,6 +735,52 @@ def test_rowmm_split_needs_workspace():
         K.rowmm(x, w, splits=4, ws=None)
 
 
+@pytest.mark.parametrize('M,N,KD,ln,epi', [(1, 1152, 384, True, None), (1, 384, 384, False, 'residual'),
+                                           (1, 1536, 384, True, 'gelu'), (1, 384, 1536, False, 'residual'),
+                                           (3, 256, 384, True, None), (8, 77, 2000, True, 'gelu'),
+                                           (5, 130, 64, False, None), (2, 33, 1, True, 'residual')])
+def test_rowvec_f32_matches_float64(M, N, KD, ln, epi):
+    """ta_rowvec_f32 (the float32 step's LN + product + epilogue in one launch) against the same op chain in
+    float64 on the CPU: within 1e-5 (float32 sums in another order), as close as torch's float32 chain."""
+    import torch.nn.functional as F
+    print('case', M, N, KD, ln, epi, flush=True)
+    g = torch.Generator().manual_seed(M * 1000 + N + KD)
+    x = torch.randn(M, KD, generator=g) * 1.5 + 0.3
+    w = torch.randn(N, KD, generator=g) * 0.02
+    lw = (1.0 + 0.1 * torch.randn(KD, generator=g)) if ln else None
+    r = torch.randn(M, N, generator=g)
+
+    def chain(xx, ww, lww, rr):
+        h = F.layer_norm(xx, (KD,), lww, None, 1e-5) if lww is not None else xx
+        y = h @ ww.t()
+        if epi == 'gelu':
+            y = F.gelu(y)
+        if epi == 'residual':
+            y = rr + y
+        return y
+    want = chain(x.double(), w.double(), lw.double() if ln else None, r.double())
+    torch32 = chain(*(t.to(DEV) if t is not None else None for t in (x, w, lw, r))).cpu().double()
+    res = r.to(DEV)
+    got = K.rowvec_f32(x.to(DEV), w.to(DEV), ln_w=lw.to(DEV) if ln else None, epilogue=epi, residual=res,
+                       out=res if epi == 'residual' else None).cpu().double()
+    err, err_t = (got - want).abs().max().item(), (torch32 - want).abs().max().item()
+    print('max err %.3g (torch float32 %.3g)' % (err, err_t), flush=True)
+    assert err < 1e-5
+    assert err <= 4 * err_t + 1e-6
+
+
+def test_rowvec_f32_rejects_bad_shapes():
+    x = torch.zeros(9, 384, device=DEV)
+    w = torch.zeros(384, 384, device=DEV)
+    with pytest.raises(ValueError):
+        K.rowvec_f32(x, w)
+    with pytest.raises(ValueError):
+        K.rowvec_f32(torch.zeros(1, 4096, device=DEV), torch.zeros(8, 4096, device=DEV))
+    x1 = torch.zeros(1, 384, device=DEV)
+    with pytest.raises(RuntimeError, match='overlap'):
+        K.rowvec_f32(x1, torch.zeros(384, 384, device=DEV), out=x1)
+
+
 @pytest.mark.parametrize('leaf,arity,B,H,dtype', [(8, 2, 2, 3, torch.float32), (16, 4, 1, 2, torch.bfloat16),
                                                   (64, 2, 32, 12, torch.bfloat16)])
 def test_descend_append_equals_two_calls(leaf, arity, B, H, dtype):

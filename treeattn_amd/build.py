@@ -28,6 +28,7 @@ SOURCES = {
     'sample.hip': [],
     'gemm.hip': [],
     'rowmm_nt.hip': [],
+    'rowvec.hip': [],
     'gather_blocks.hip': [],
     'prefill_attn.hip': [],
     'step.hip': [],

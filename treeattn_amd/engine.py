@@ -573,6 +573,8 @@ class Decoder:
         W, H, C, dh, B = self.W, self.H, self.C, self.dh, self.B
         if self.fused:
             return self._forward_step_fused(tok, tpos)
+        if self.mode == 'seg' and self._rowvec_ok():
+            return self._forward_step_rowvec(tok, tpos)
         x = (W['wte'][tok] + W['wpe'][tpos]).view(B, 1, C)
         tpos32 = tpos.to(torch.int32)
         for i, L in enumerate(W['layers']):
@@ -591,6 +593,35 @@ class Decoder:
             x = x + F.linear(out.transpose(1, 2).reshape(B, 1, C), L['c_proj'])
             x = x + F.linear(F.gelu(F.linear(_ln(x, L['ln2']), L['c_fc'])), L['c_mlp'])
         return F.linear(_ln(x, W['ln_f']), W['wte'])[:, 0]
+
+    def _rowvec_ok(self):
+        """Whether the float32 row products of ta_rowvec_f32 serve this decoder (float32 weights, at most 8
+        sequences, widths up to 2048)."""
+        W = self.W
+        lay = W['layers'][0]
+        return (W['wte'].dtype == torch.float32 and W['wte'].is_cuda and 1 <= self.B <= 8 and self.C <= 2048
+                and lay['c_fc'].shape[0] <= 2048 and all(
+                    t.stride(-1) == 1 for t in (W['wte'], lay['c_attn'], lay['c_proj'], lay['c_fc'], lay['c_mlp'])))
+
+    def _forward_step_rowvec(self, tok, tpos):
+        """The float32 step with one launch per row product (LN1 + c_attn, c_proj + residual, LN2 + c_fc + GELU,
+        c_mlp + residual, LN_f + logits: ta_rowvec_f32) and the embedding by ta_embed, the attention as in
+        _forward_step."""
+        W, H, C, dh, B = self.W, self.H, self.C, self.dh, self.B
+        x = torch.empty(B, C, device=self.dev, dtype=torch.float32)
+        tpos32 = torch.empty(B, device=self.dev, dtype=torch.int32)
+        K.embed(tok.contiguous(), tpos.contiguous(), W['wte'], W['wpe'], out=x, pos32=tpos32)
+        for i, L in enumerate(W['layers']):
+            qkv = K.rowvec_f32(x, L['c_attn'], ln_w=L['ln1'])
+            q, k, v = [a.view(B, 1, H, dh).transpose(1, 2) for a in qkv.view(B, 1, 3 * C).split(C, -1)]
+            self.scratch.keys = self.scratch.keys_all[i]
+            out, kr = seg_attend_(self.states[i], L.get('pw'), q, k, v, tpos32, scratch=self.scratch)
+            if kr.data_ptr() != self.scratch.keys_all[i].data_ptr():
+                self.scratch.keys_all[i].copy_(kr.view(B, H, 1))
+            K.rowvec_f32(out.transpose(1, 2).reshape(B, C), L['c_proj'], epilogue='residual', residual=x, out=x)
+            h = K.rowvec_f32(x, L['c_fc'], ln_w=L['ln2'], epilogue='gelu')
+            K.rowvec_f32(h, L['c_mlp'], epilogue='residual', residual=x, out=x)
+        return K.rowvec_f32(x, W['wte'], ln_w=W['ln_f'])
 
     def _group_step(self, grp, tok, tpos, logits, advance=False, tok_out=None):
         """One decode step for the sequences of one group (rows b0..b1-1), logits into `logits` rows.  With

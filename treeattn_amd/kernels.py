@@ -775,6 +775,28 @@ def rowmm(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None, spl
     return (out, out_ln) if ln_next is not None else out
 
 
+def rowvec_supported(x, w):
+    """Whether ta_rowvec_f32 serves these rows and weights (float32, 1 to 8 rows, K at most 2048)."""
+    return (x.dtype == torch.float32 and w.dtype == torch.float32 and x.dim() == 2 and 1 <= x.shape[0] <= 8
+            and 1 <= x.shape[1] <= 2048 and x.stride(1) == 1 and w.stride(1) == 1)
+
+
+def rowvec_f32(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None):
+    """epilogue(LN(x) @ w.T) for a few float32 rows: x (M,K), w (N,K) -> (M,N), M <= 8, K <= 2048; epilogue None |
+    'gelu' | 'residual' (adds `residual`, (M,N)); `out` may be `residual` (not x)."""
+    L.require_gpu(x, w)
+    M, K = x.shape
+    N = w.shape[0]
+    if not rowvec_supported(x, w) or w.shape[1] != K:
+        raise ValueError('rowvec_f32: float32 rows (1 to 8, K <= 2048, contiguous rows) and w (N, K)')
+    if out is None:
+        out = torch.empty(M, N, device=x.device, dtype=torch.float32)
+    r = residual if epilogue == 'residual' else None
+    L.call('ta_rowvec_f32', L.ptr(x), x.stride(0), L.ptr(w), w.stride(0), L.ptr(out), out.stride(0), L.ptr(r),
+           r.stride(0) if r is not None else 0, L.ptr(ln_w), float(eps), M, N, K, _EPI[epilogue], L.stream())
+    return out
+
+
 def logits_supported(x, w):
     """Whether ta_logits serves these rows and weights (bf16, at most 32 rows, K a multiple of 64 up to 1024)."""
     return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and 1 <= x.shape[0] <= 32
