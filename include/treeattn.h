@@ -411,6 +411,19 @@ int ta_rowvec_f32(const float* X, int64_t ldx, const float* W, int64_t ldw, floa
                   int64_t ldr, const float* ln_w, float ln_eps, int M, int N, int K, int epilogue, void* stream);
 
 /*
+ * ta_rowmm's row product (LayerNorm prologue, product, epilogue; replaces the same engine.py:168-177 products at
+ * bf16) for one to eight rows without matrix cores: one wavefront per output column, the same arithmetic at
+ * every rounding point (float32 LayerNorm statistics from the sums of x and x^2, the normalised row rounded to
+ * bf16, float32 products summed in float32, the sum rounded to bf16 before GELU or the residual); only the
+ * order of the float32 sums differs, so outputs agree with ta_rowmm's within one bf16 unit.  What the bf16
+ * decoder runs for one or two rows, where a matrix-core tile computes mostly idle rows.
+ * 1 <= M <= 8, K a multiple of 8 up to 4096; X, W, ln_w 16-byte aligned, row strides multiples of 8 elements;
+ * X must not overlap Y (R may be Y).
+ */
+int ta_rowvec_bf16(const void* X, int64_t ldx, const void* W, int64_t ldw, void* Y, int64_t ldy, const void* R,
+                   int64_t ldr, const void* ln_w, float ln_eps, int M, int N, int K, int epilogue, void* stream);
+
+/*
  * Row-wise argmax for greedy decoding (replaces logits.argmax(-1) of the reference's greedy loop,
  * phase2.py:51-66): out[r] = the first index of the largest value of x[r, 0:n].  x: rows of n elements of
  * dtype with row stride `stride`; out: int64.

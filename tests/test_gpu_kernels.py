@@ -769,6 +769,32 @@ def test_rowvec_f32_matches_float64(M, N, KD, ln, epi):
     assert err <= 4 * err_t + 1e-6
 
 
+@pytest.mark.parametrize('M,N,KD,ln,epi', [(1, 2304, 768, True, None), (1, 768, 768, False, 'residual'),
+                                           (1, 3072, 768, True, 'gelu'), (1, 768, 3072, False, 'residual'),
+                                           (2, 1000, 768, True, None), (5, 96, 4096, True, 'gelu'),
+                                           (1, 40, 64, False, None)])
+def test_rowvec_bf16_agrees_with_rowmm(M, N, KD, ln, epi):
+    """ta_rowvec_bf16 against ta_rowmm on the same bf16 rows: the same rounding points, float32 sums in another
+    order, so every output within one bf16 unit of rowmm's product before the epilogue (GELU's slope is at most
+    1.13) plus one unit of the output, and most outputs the same bits."""
+    print('case', M, N, KD, ln, epi, flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N + KD)
+    x = (torch.randn(M, KD, generator=g) * 1.5 + 0.3).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, KD, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    lw = (1.0 + 0.1 * torch.randn(KD, generator=g)).to(torch.bfloat16).to(DEV) if ln else None
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    lnk = dict(ln_w=lw) if ln else {}
+    want = K.rowmm(x, w, epilogue=epi, residual=r, **lnk).float()
+    pre = K.rowmm(x, w, **lnk).float()   # the product rounded to bf16, before the epilogue
+    got = K.rowvec_bf16(x, w, epilogue=epi, residual=r, **lnk).float()
+    d = (got - want).abs()
+    bound = 1.13 * _bf16_ulp(pre) + _bf16_ulp(torch.maximum(got.abs(), want.abs()))
+    same = (got == want).float().mean().item()
+    print('max |diff| %.3g, same bits %.4f' % (d.max().item(), same), flush=True)
+    assert bool((d <= bound).all())
+    assert same > 0.9
+
+
 def test_rowvec_f32_rejects_bad_shapes():
     x = torch.zeros(9, 384, device=DEV)
     w = torch.zeros(384, 384, device=DEV)
@@ -779,6 +805,9 @@ def test_rowvec_f32_rejects_bad_shapes():
     x1 = torch.zeros(1, 384, device=DEV)
     with pytest.raises(RuntimeError, match='overlap'):
         K.rowvec_f32(x1, torch.zeros(384, 384, device=DEV), out=x1)
+    xb = torch.zeros(1, 100, device=DEV, dtype=torch.bfloat16)   # K not a multiple of 8
+    with pytest.raises(ValueError):
+        K.rowvec_bf16(xb, torch.zeros(8, 100, device=DEV, dtype=torch.bfloat16))
 
 
 @pytest.mark.parametrize('leaf,arity,B,H,dtype', [(8, 2, 2, 3, torch.float32), (16, 4, 1, 2, torch.bfloat16),

@@ -162,6 +162,8 @@ SIGNATURES = {
     'ta_bf16_from_f32': (c_i32, [c_vp, c_vp, c_i64, c_vp]),
     'ta_rowvec_f32': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32,
                                c_i32, c_vp]),
+    'ta_rowvec_bf16': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_f32, c_i32, c_i32, c_i32,
+                                c_i32, c_vp]),
     'ta_decode_step_workspace_size': (c_i64, [_P(StepModel)]),
     'ta_decode_step_prepare': (c_i32, [_P(StepModel), c_vp, c_i64, _P(StepLaunch), c_vp]),
     'ta_decode_step': (c_i32, [_P(StepLaunch), c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp]),

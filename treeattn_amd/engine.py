@@ -263,12 +263,19 @@ class _Scratch:
         self.ws = K.seg_attn_workspace(B, H, 1, dh, nsplit, dev)
         self.mm_ws = None
         self.lg_ws = None
+        self.rowvec = False     # the decoder's choice of ta_rowvec_bf16 for its products (a batch of at most
+                                # ROWVEC_MAX_ROWS sequences, whatever its grouping)
 
     def mm(self, x, w, **kw):
         """ta_rowmm with the split count of K.rowmm_splits; the workspace (split partials, tail counter, argmax
         keys) is allocated (zero-filled) on first use and shared by the group's products, which run one after
-        another on its stream."""
+        another on its stream.  In a decoder of at most ROWVEC_MAX_ROWS sequences (self.rowvec), products
+        without a tail run ta_rowvec_bf16 instead: rowmm's arithmetic without matrix cores, whose 32-row tiles
+        would compute 30 or more idle rows; results within one bf16 unit of rowmm's."""
         M, Kd = x.shape
+        if (self.rowvec and M <= ROWVEC_MAX_ROWS and not {'ln_next', 'tok_out', 'cols', 'splits'} & kw.keys()
+                and K.rowvec_bf16_supported(x, w)):
+            return K.rowvec_bf16(x, w, **kw)
         S = K.rowmm_splits(M, w.shape[0], Kd)
         if S > 1 or kw.get('ln_next') is not None or kw.get('tok_out') is not None:
             need = K.L.lib().ta_rowmm_workspace_size(M, w.shape[0], Kd, S)
@@ -292,6 +299,11 @@ class _Scratch:
                 raise RuntimeError('logits workspace must be allocated before graph capture')
             self.lg_ws = K.logits_workspace(x.shape[0], w.shape[0], x.device)
         K.logits(x, w, ln_w=ln_w, out=out, tok_out=tok_out, ws=self.lg_ws)
+
+
+# Rows up to which the bf16 decoder's products run without matrix cores (ta_rowvec_bf16): config 5's single
+# sequence; at 32 rows (config 4) the matrix-core tiles are the faster.
+ROWVEC_MAX_ROWS = 2
 
 
 def decode_nsplit(B, H, wl, leaf):
@@ -548,6 +560,7 @@ class Decoder:
                     stream=torch.cuda.Stream(device=self.dev) if G > 1 else None,
                     x=torch.empty(n, self.C, device=self.dev, dtype=self.dtype),
                     pos32=torch.empty(n, device=self.dev, dtype=torch.int32)))
+                self.groups[-1]['scratch'].rowvec = B <= ROWVEC_MAX_ROWS
         else:
             self.states = [DenseState(self.Tcap, H, dh, self.dev, B, self.dtype) for _ in range(self.nl)]
         self.graph = None

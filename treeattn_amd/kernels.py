@@ -797,6 +797,31 @@ def rowvec_f32(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None
     return out
 
 
+def rowvec_bf16_supported(x, w):
+    """Whether ta_rowvec_bf16 serves these rows and weights (bf16, 1 to 8 rows, K a multiple of 8 up to 4096,
+    16-byte aligned rows)."""
+    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.dim() == 2 and 1 <= x.shape[0] <= 8
+            and 8 <= x.shape[1] <= 4096 and x.shape[1] % 8 == 0 and x.stride(1) == 1 and w.stride(1) == 1
+            and x.stride(0) % 8 == 0 and w.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+
+
+def rowvec_bf16(x, w, ln_w=None, eps=1e-5, epilogue=None, residual=None, out=None):
+    """rowmm's arithmetic (LN statistics, bf16 rounding points, epilogues) for one to eight bf16 rows, one
+    wavefront per output column: x (M,K), w (N,K) -> (M,N); `out` may be `residual` (not x).  The float32 sums run
+    in another order than rowmm's MFMA chains, so results agree with rowmm's within one bf16 unit."""
+    L.require_gpu(x, w)
+    M, K = x.shape
+    N = w.shape[0]
+    if not rowvec_bf16_supported(x, w) or w.shape[1] != K:
+        raise ValueError('rowvec_bf16: bf16 rows (1 to 8, K a multiple of 8 up to 4096, 16-byte aligned) and w (N, K)')
+    if out is None:
+        out = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    r = residual if epilogue == 'residual' else None
+    L.call('ta_rowvec_bf16', L.ptr(x), x.stride(0), L.ptr(w), w.stride(0), L.ptr(out), out.stride(0), L.ptr(r),
+           r.stride(0) if r is not None else 0, L.ptr(ln_w), float(eps), M, N, K, _EPI[epilogue], L.stream())
+    return out
+
+
 def logits_supported(x, w):
     """Whether ta_logits serves these rows and weights (bf16, at most 32 rows, K a multiple of 64 up to 1024)."""
     return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and 1 <= x.shape[0] <= 32
