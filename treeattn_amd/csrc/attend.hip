@@ -25,7 +25,8 @@ namespace ta {
 
 
 
-template <typename T, int D, bool SPLIT, bool CAND>
+// PIPE: the copy-free chunk loop of attn_query, for several workgroups per query (p.gsplit > 1).
+template <typename T, int D, bool SPLIT, bool CAND, bool PIPE = false>
 __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
   extern __shared__ float smem_f[];
   const int w = wave_id();
@@ -51,7 +52,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
     vr = p.vld + qi * p.wl;
     nt = p.n_tree ? p.n_tree[qi] : p.wl;
   }
-  attn_query<T, D, SPLIT, CAND>(p, n, g, b, h, qi, qrow, t, idr, vr, -1, nt, orow, smem_f);
+  attn_query<T, D, SPLIT, CAND, PIPE>(p, n, g, b, h, qi, qrow, t, idr, vr, -1, nt, orow, smem_f);
 }
 
 // ----------------------------------------------------------------------------------------- decode attend
@@ -182,8 +183,13 @@ int launch_attn(const AttnParams& p, int B, bool split, hipStream_t st) {
   if (split) {
     lds += (size_t)kWavesPerBlock * (D + 2) * sizeof(float);
     dim3 grid((unsigned)((int64_t)p.Nq * p.gsplit), B * p.H);
-    if (p.cand) hipLaunchKernelGGL((attn_kernel<T, D, true, true>), grid, blk, lds, st, p);
-    else hipLaunchKernelGGL((attn_kernel<T, D, true, false>), grid, blk, lds, st, p);
+    if (p.gsplit > 1) {
+      if (p.cand) hipLaunchKernelGGL((attn_kernel<T, D, true, true, true>), grid, blk, lds, st, p);
+      else hipLaunchKernelGGL((attn_kernel<T, D, true, false, true>), grid, blk, lds, st, p);
+    } else {
+      if (p.cand) hipLaunchKernelGGL((attn_kernel<T, D, true, true>), grid, blk, lds, st, p);
+      else hipLaunchKernelGGL((attn_kernel<T, D, true, false>), grid, blk, lds, st, p);
+    }
     return check_launch("attn_kernel");
   }
   dim3 grid((unsigned)((p.Nq + kWavesPerBlock - 1) / kWavesPerBlock), B * p.H);

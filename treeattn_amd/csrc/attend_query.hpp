@@ -58,7 +58,7 @@ template <> struct Raw16<f16_t> {
 // Paged caches: pre_leaf_pg (LDS, may be null) holds the pages of the leaf blocks idr lists and pre_static_pg
 // (LDS, may be null) the page of static slot i's block (slot 0: position 0, slot i >= 1: position t - i + 1),
 // read earlier by the caller; when null they are looked up in the page table here.
-template <typename T, int D, bool SPLIT, bool CAND>
+template <typename T, int D, bool SPLIT, bool CAND, bool PIPE = false>
 __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, int b, int h, int64_t qi, const T* qrow,
                                            int t, const int32_t* idr, const uint8_t* vr, int nv_given, int nt,
                                            T* orow_base, float* smem_f, const int32_t* pre_leaf_pg = nullptr,
@@ -252,30 +252,53 @@ __device__ __forceinline__ void attn_query(const AttnParams& p, int n, int g, in
   };
 
   {
-    constexpr int PF = 4;   // measured with cold caches at config 4: 46.9 us (8 loads x 1 ahead: 49.9 us)
+    constexpr int PF = 4;   // chunks in flight per wavefront
     uint4 kq[PF][NL], vq[PF][NL];
     bool okq[PF][NL];
+    if constexpr (PIPE) {
+      // Several workgroups per query (few queries, each wavefront's chain of round trips is the time): slot j is
+      // consumed, then refilled with the chunk PF steps later, the loop unrolled over the slots so that no
+      // register set is copied (a copy of registers whose loads are in flight waits for those loads, which
+      // makes every chunk a full round trip).  Every fetch is issued, past the last chunk too (its keys are
+      // invalid: row 0 is read and nothing is used), so every path has the same loads in flight and the wait
+      // before a slot's use covers that slot only.  Measured at config 5: 0.690 against 0.711-0.718 ms/step.
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-      if (first + j * stride < nchunks) fetch(first + j * stride, kq[j], vq[j], okq[j]);
-    int c = first;
-    while (c < nchunks) {
-      const int cn = c + PF * stride;
-      uint4 kn[NL], vn[NL];
-      bool okn[NL];
-      if (cn < nchunks) fetch(cn, kn, vn, okn);
-      consume(kq[0], vq[0], okq[0]);
+      for (int j = 0; j < PF; ++j) fetch(first + j * stride, kq[j], vq[j], okq[j]);
+      for (int c0 = first; c0 < nchunks; c0 += PF * stride) {
 #pragma unroll
-      for (int j = 0; j + 1 < PF; ++j)
+        for (int j = 0; j < PF; ++j) {
+          const int c = c0 + j * stride;
+          if (c < nchunks) consume(kq[j], vq[j], okq[j]);
+          fetch(c + PF * stride, kq[j], vq[j], okq[j]);
+        }
+      }
+    } else {
+      // Otherwise (one workgroup per query: many queries streaming together, HBM the limit): the next chunk
+      // requested before each one is consumed and the register sets shifted, which waits for the requests in
+      // flight at the end of every step; measured faster here than the copy-free loop above (config 4's layer
+      // attention 61-63 against 65.5 us with cold caches) and than 8 loads one chunk ahead (49.9 against 46.9 us).
+#pragma unroll
+      for (int j = 0; j < PF; ++j)
+        if (first + j * stride < nchunks) fetch(first + j * stride, kq[j], vq[j], okq[j]);
+      int c = first;
+      while (c < nchunks) {
+        const int cn = c + PF * stride;
+        uint4 kn[NL], vn[NL];
+        bool okn[NL];
+        if (cn < nchunks) fetch(cn, kn, vn, okn);
+        consume(kq[0], vq[0], okq[0]);
+#pragma unroll
+        for (int j = 0; j + 1 < PF; ++j)
+#pragma unroll
+          for (int i = 0; i < NL; ++i) {
+            kq[j][i] = kq[j + 1][i]; vq[j][i] = vq[j + 1][i]; okq[j][i] = okq[j + 1][i];
+          }
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-          kq[j][i] = kq[j + 1][i]; vq[j][i] = vq[j + 1][i]; okq[j][i] = okq[j + 1][i];
+          kq[PF - 1][i] = kn[i]; vq[PF - 1][i] = vn[i]; okq[PF - 1][i] = okn[i];
         }
-#pragma unroll
-      for (int i = 0; i < NL; ++i) {
-        kq[PF - 1][i] = kn[i]; vq[PF - 1][i] = vn[i]; okq[PF - 1][i] = okn[i];
+        c += stride;
       }
-      c += stride;
     }
   }
 
