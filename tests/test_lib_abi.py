@@ -35,6 +35,20 @@ def test_library_exports_every_declared_symbol():
     assert L.ta_abi_version() == 3
 
 
+def test_build_entry_checks_the_declared_abi_version():
+    """__graft_entry__.build() compares the library's ABI version with the one include/treeattn.h declares (no
+    number of its own to fall behind the header); the built library matches it."""
+    import re
+    import torch  # noqa: F401
+    from treeattn_amd import _lib
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = open(os.path.join(root, '__graft_entry__.py')).read()
+    assert 'TA_ABI_VERSION' in src and 'ta_abi_version() == ' not in src
+    declared = int(re.search(r'#define TA_ABI_VERSION (\d+)', open(os.path.join(root, 'include', 'treeattn.h')).read())
+                   .group(1))
+    assert _lib.lib().ta_abi_version() == declared
+
+
 def test_library_rejects_bad_arguments_without_gpu():
     """Argument validation runs on the host: a bad size returns an error code and a message."""
     import torch  # noqa: F401
