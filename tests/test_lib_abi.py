@@ -38,14 +38,11 @@ def test_library_exports_every_declared_symbol():
 def test_build_entry_checks_the_declared_abi_version():
     """__graft_entry__.build() compares the library's ABI version with the one include/treeattn.h declares (no
     number of its own to fall behind the header); the built library matches it."""
-    import re
     import torch  # noqa: F401
     from treeattn_amd import _lib
-    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    src = open(os.path.join(root, '__graft_entry__.py')).read()
+    src = open(os.path.join(ROOT, '__graft_entry__.py')).read()
     assert 'TA_ABI_VERSION' in src and 'ta_abi_version() == ' not in src
-    declared = int(re.search(r'#define TA_ABI_VERSION (\d+)', open(os.path.join(root, 'include', 'treeattn.h')).read())
-                   .group(1))
+    declared = int(re.search(r'#define TA_ABI_VERSION (\d+)', open(HEADER).read()).group(1))
     assert _lib.lib().ta_abi_version() == declared
 
 
